@@ -1,0 +1,39 @@
+"""MI355X-native copy-on-write Sparse Delta Memory decode step.
+
+Drop-in for the decode-state path of p0rc314in/copy-on-write-sdm
+(copy_on_write_sdm/allocator.py and the SDM half of inference.py): the same
+class and function names, arguments and errors, backed by hand-written HIP
+kernels for gfx950 in libcowsdm.so (C ABI: include/cowsdm.h).
+"""
+
+from .allocator import (
+    PackedSDMCopyOnWriteState,
+    SDMCopyOnWriteStep,
+    dense_sdm_sparse_step,
+    dense_sdm_sparse_step_layers,
+    mark_written,
+    packed_sdm_cow_step,
+    packed_sdm_cow_step_layers,
+)
+from .inference import (
+    FaithfulSDMDecodeState,
+    SDMStepInputs,
+    decode_sdm_layer,
+    decode_sdm_layer_dense,
+    pack_prefill_layer,
+)
+
+__all__ = [
+    "FaithfulSDMDecodeState",
+    "PackedSDMCopyOnWriteState",
+    "SDMCopyOnWriteStep",
+    "SDMStepInputs",
+    "decode_sdm_layer",
+    "decode_sdm_layer_dense",
+    "dense_sdm_sparse_step",
+    "dense_sdm_sparse_step_layers",
+    "mark_written",
+    "pack_prefill_layer",
+    "packed_sdm_cow_step",
+    "packed_sdm_cow_step_layers",
+]

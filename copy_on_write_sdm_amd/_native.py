@@ -1,0 +1,210 @@
+"""ctypes binding of libcowsdm.so (include/cowsdm.h) and its build recipe.
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already loaded (both carry the soname libamdhip64.so.7); device pointers and
+the hipStream_t handles torch hands out are then valid in the library.
+
+There is no fallback: if the library is missing, ``lib()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+import threading
+from pathlib import Path
+
+import torch
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_DIR = PACKAGE_DIR.parent
+SOURCE = PACKAGE_DIR / "csrc" / "cowsdm.hip"
+INCLUDE_DIR = REPO_DIR / "include"
+LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
+
+INDEX_INT32 = 0
+INDEX_INT64 = 1
+
+ERR_WRITE_INDEX = 0x1
+ERR_READ_INDEX = 0x2
+ERR_DUP_WRITE = 0x4
+ERR_EXHAUSTED = 0x8
+ERR_TEMPLATE = 0x10
+ERR_CORRUPT = 0x20
+ERR_LOOKBACK = 0x40
+
+SCRATCH_EPOCH = 0
+SCRATCH_TICKET = 1
+SCRATCH_SERVED = 2
+SCRATCH_ERRORS = 3
+SCRATCH_PRECHECK = 4
+SCRATCH_SLOTS = 8
+
+HIPCC_FLAGS = (
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # every product and sum is rounded on its own, as in the reference's
+    # elementwise torch ops
+    "-ffp-contract=off",
+    # never emit packed FP32 VALU ops
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+)
+
+
+def build_library(output: Path | None = None, *, verbose: bool = False) -> Path:
+    """Compile csrc/cowsdm.hip for gfx950 into lib/libcowsdm.so."""
+
+    output = Path(output) if output is not None else LIBRARY
+    output.parent.mkdir(parents=True, exist_ok=True)
+    tmp = output.with_name(output.name + f".tmp{os.getpid()}")
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", str(tmp), str(SOURCE)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            "hipcc failed building libcowsdm.so:\n" + " ".join(cmd) + "\n" + proc.stderr
+        )
+    if verbose and proc.stderr:
+        print(proc.stderr)
+    os.replace(tmp, output)
+    return output
+
+
+class Shape(ctypes.Structure):
+    """cowsdm_shape_t."""
+
+    _fields_ = [
+        ("banks", ctypes.c_int64),
+        ("slots", ctypes.c_int64),
+        ("width", ctypes.c_int64),
+        ("writes", ctypes.c_int64),
+        ("reads", ctypes.c_int64),
+        ("templates", ctypes.c_int64),
+        ("index_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class Layer(ctypes.Structure):
+    """cowsdm_layer_t."""
+
+    _fields_ = [
+        ("shared_initial_memory", ctypes.c_void_p),
+        ("template_indices", ctypes.c_void_p),
+        ("values", ctypes.c_void_p),
+        ("logical_to_physical", ctypes.c_void_p),
+        ("free_rows", ctypes.c_void_p),
+        ("free_count", ctypes.c_void_p),
+        ("overflow_flag", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("capacity_rows", ctypes.c_int64),
+        ("write_indices", ctypes.c_void_p),
+        ("write_weights", ctypes.c_void_p),
+        ("step_values", ctypes.c_void_p),
+        ("input_gate", ctypes.c_void_p),
+        ("erase_gate", ctypes.c_void_p),
+        ("forget_log_gate", ctypes.c_void_p),
+        ("read_indices", ctypes.c_void_p),
+        ("read_weights", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+        ("first_touches_out", ctypes.c_void_p),
+        ("repeated_writes_out", ctypes.c_void_p),
+        ("allocated_rows_out", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+
+# name -> (restype, argtypes); the C declarations live in include/cowsdm.h
+SIGNATURES: dict[str, tuple] = {
+    "cowsdm_abi_version": (_I32, []),
+    "cowsdm_last_error_string": (ctypes.c_char_p, []),
+    "cowsdm_step_scratch_words": (_I64, [_I64]),
+    "cowsdm_workspace_bytes": (_I64, [_I64, _I64]),
+    "cowsdm_packed_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
+    "cowsdm_packed_step_layers": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),
+    "cowsdm_dense_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
+    "cowsdm_dense_step_layers": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),
+    "cowsdm_step_precheck": (
+        _I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _I32, _I32, _I32, _P, _P]),
+    "cowsdm_init_state": (
+        _I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P]),
+    "cowsdm_grow": (_I32, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "cowsdm_count_active": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_pack_overlay": (
+        _I32, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P]),
+    "cowsdm_trim_repack": (
+        _I32, [_P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_append_banks": (
+        _I32,
+        [_P, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P,
+         _P, _P]),
+    "cowsdm_check_banks": (_I32, [_P, _I64, _I64, _P, _I64, _I32, _P, _P, _P]),
+    "cowsdm_release": (_I32, [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_retain_banks": (_I32, [_P, _P, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "cowsdm_materialize_dense": (
+        _I32, [_P, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P]),
+    "cowsdm_check_invariants": (
+        _I32, [_P, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P]),
+    "cowsdm_mark_written": (_I32, [_P, _I64, _I64, _P, _I64, _I32, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("COWSDM_LIBRARY")
+    return Path(override) if override else LIBRARY
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded HIP library; raises if it has not been built."""
+
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = library_path()
+            if not path.exists():
+                raise RuntimeError(
+                    f"libcowsdm.so not found at {path}: build it with "
+                    "`python -c 'import __graft_entry__ as g; g.build()'`; the "
+                    "copy-on-write SDM kernels have no CPU fallback"
+                )
+            handle = ctypes.CDLL(str(path), mode=ctypes.RTLD_LOCAL)
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            if handle.cowsdm_abi_version() != 1:
+                raise RuntimeError("libcowsdm.so ABI version mismatch")
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise RuntimeError on a nonzero C-ABI return code."""
+
+    if rc != 0:
+        message = lib().cowsdm_last_error_string().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {message}")
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()

@@ -1,0 +1,1074 @@
+"""Packed copy-on-write SDM state and its fused decode step on MI355X.
+
+Drop-in for ``copy_on_write_sdm.allocator`` (p0rc314in/copy-on-write-sdm):
+the same ``PackedSDMCopyOnWriteState`` fields, methods and error messages,
+and the same ``packed_sdm_cow_step`` / ``dense_sdm_sparse_step`` signatures.
+All state arithmetic runs in the HIP kernels of libcowsdm.so (include/
+cowsdm.h); torch only allocates device memory, supplies the current stream
+and reads back the few scalars the reference also synchronises on.
+
+Differences from the reference, all deliberate:
+
+* Physical rows for first touches are popped in bank-major order on every
+  backend, so the map, slab and free stack match the reference's torch path
+  (allocator.py:1471-1481) exactly instead of up to a permutation.
+* ``backend`` accepts "auto" and "hip".  "triton" raises the reference's
+  unavailable-backend error; "torch" raises too: no CPU path ships.
+* Value state, route weights, values and gates are float32.
+* The state carries one more tensor, ``scratch`` (int64 [8 + B]), holding the
+  bank-order scan slots, a ticket counter and a sticky error word.
+* Route validation (``validate_routes=True``) and steps on a state without a
+  capacity proof synchronise once and raise ValueError, like the reference's
+  CPU path, where the reference's GPU path would device-assert.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+import torch
+
+from . import _native as nat
+
+
+def _tensor_bytes(tensor: torch.Tensor) -> int:
+    return tensor.numel() * tensor.element_size()
+
+
+def _ceil_to(value: int, quantum: int) -> int:
+    return ((value + quantum - 1) // quantum) * quantum
+
+
+def handoff_capacity(
+    active_count: int,
+    banks: int,
+    slots: int,
+    capacity_rows: int | None,
+    growth_quantum_rows: int,
+    maximum_future_allocations: int | None,
+) -> tuple[int, int]:
+    """Slab size and proven future allocations of a prefill handoff
+    (allocator.py:629-655).  Returns (capacity, proven future rows)."""
+
+    if growth_quantum_rows < 0:
+        raise ValueError("SDM growth quantum cannot be negative")
+    if capacity_rows is None and growth_quantum_rows:
+        selected = max(growth_quantum_rows, _ceil_to(active_count, growth_quantum_rows))
+    else:
+        selected = banks * slots if capacity_rows is None else capacity_rows
+    if selected < active_count:
+        raise ValueError("SDM physical capacity is smaller than the prefill working set")
+    if maximum_future_allocations is None:
+        return selected, 0
+    if maximum_future_allocations < 0:
+        raise ValueError("maximum future allocations cannot be negative")
+    possible = min(maximum_future_allocations, banks * slots - active_count)
+    if selected - active_count < possible:
+        raise ValueError("SDM physical capacity cannot cover the declared decode trace")
+    return selected, possible
+
+
+def growth_target(minimum_capacity_rows: int, quantum: int) -> int:
+    """Capacity after growth: the minimum rounded up to the quantum
+    (allocator.py:706-708)."""
+
+    return _ceil_to(minimum_capacity_rows, quantum)
+
+
+def trim_target(active_count: int, headroom_rows: int, quantum: int) -> int:
+    """Capacity after a trim (allocator.py:792-795)."""
+
+    return max(quantum, _ceil_to(active_count + headroom_rows, quantum))
+
+
+def _require_device(tensor: torch.Tensor, what: str) -> None:
+    if tensor.device.type != "cuda":
+        raise RuntimeError(
+            f"{what} must live on a HIP device: the copy-on-write SDM kernels "
+            "have no CPU path"
+        )
+
+
+def _workspace(entries: int, rows: int, device: torch.device) -> torch.Tensor:
+    size = int(nat.lib().cowsdm_workspace_bytes(entries, rows))
+    return torch.empty(max(size, 256), dtype=torch.uint8, device=device)
+
+
+def _scratch(banks: int, device: torch.device) -> torch.Tensor:
+    words = int(nat.lib().cowsdm_step_scratch_words(banks))
+    return torch.zeros(words, dtype=torch.int64, device=device)
+
+
+@dataclass(frozen=True)
+class SDMCopyOnWriteStep:
+    """Diagnostics for one packed SDM decode step (allocator.py:467-473)."""
+
+    first_touches_by_sequence: torch.Tensor
+    repeated_writes_by_sequence: torch.Tensor
+    allocated_rows_after_step: torch.Tensor
+
+
+@dataclass
+class PackedSDMCopyOnWriteState:
+    """One shared slab backing several independent logical SDM tables.
+
+    Fields as in allocator.py:476-504: ``shared_initial_memory`` [T,N,D]
+    (model-shared M0), ``template_indices`` [B] int64, ``values`` [C,D] slab,
+    ``logical_to_physical`` [B,N] int32 (-1 = shared M0), ``free_rows`` [C]
+    int32 stack with ``free_count`` entries, ``overflow_flag``; plus
+    ``scratch``, the device words of the bank-order scan.
+    """
+
+    shared_initial_memory: torch.Tensor
+    template_indices: torch.Tensor
+    values: torch.Tensor
+    logical_to_physical: torch.Tensor
+    free_rows: torch.Tensor
+    free_count: torch.Tensor
+    overflow_flag: torch.Tensor
+    capacity_is_proven: bool = False
+    proven_maximum_additional_allocations: int = 0
+    growth_quantum_rows: int = 0
+    growth_events: int = 0
+    growth_rows_added: int = 0
+    growth_rows_copied: int = 0
+    scratch: torch.Tensor | None = None
+
+    # --------------------------------------------------------- creation
+
+    @classmethod
+    def allocate(
+        cls,
+        shared_initial_memory: torch.Tensor,
+        *,
+        banks: int,
+        capacity_rows: int,
+        template_indices: torch.Tensor | None = None,
+        state_dtype: torch.dtype = torch.float32,
+        growth_quantum_rows: int = 0,
+    ) -> "PackedSDMCopyOnWriteState":
+        """Allocate an empty shared slab (allocator.py:506-585)."""
+
+        if shared_initial_memory.ndim == 2:
+            shared_initial_memory = shared_initial_memory.unsqueeze(0)
+        if shared_initial_memory.ndim != 3:
+            raise ValueError("shared initial memory must be [H,N,D] or [N,D]")
+        templates, slots, width = shared_initial_memory.shape
+        if banks <= 0 or capacity_rows <= 0:
+            raise ValueError("banks and physical capacity must be positive")
+        if growth_quantum_rows < 0:
+            raise ValueError("SDM growth quantum cannot be negative")
+        if state_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+            raise ValueError("SDM COW state must use float16, bfloat16, or float32")
+        if state_dtype != torch.float32:
+            raise ValueError("this build keeps SDM COW state in float32")
+        _require_device(shared_initial_memory, "shared initial memory")
+        if shared_initial_memory.dtype != torch.float32:
+            raise ValueError("shared initial memory must be float32")
+        shared_initial_memory = shared_initial_memory.contiguous()
+        device = shared_initial_memory.device
+        if template_indices is None:
+            if templates != 1:
+                raise ValueError("multiple initial-memory templates require explicit mapping")
+            template_indices = torch.zeros(banks, device=device, dtype=torch.int64)
+        elif (
+            template_indices.shape != (banks,)
+            or template_indices.dtype not in (torch.int32, torch.int64)
+            or template_indices.device != device
+        ):
+            raise ValueError("template indices must be integer [B] on the state device")
+        else:
+            template_indices = template_indices.to(torch.int64).contiguous()
+        if capacity_rows >= 2**31 or banks * slots >= 2**31:
+            raise ValueError("SDM COW state sizes must stay below 2^31 rows and entries")
+        state = cls(
+            shared_initial_memory=shared_initial_memory,
+            template_indices=template_indices,
+            values=torch.empty(capacity_rows, width, device=device, dtype=torch.float32),
+            logical_to_physical=torch.empty(banks, slots, device=device, dtype=torch.int32),
+            free_rows=torch.empty(capacity_rows, device=device, dtype=torch.int32),
+            free_count=torch.empty((), device=device, dtype=torch.int32),
+            overflow_flag=torch.empty((), device=device, dtype=torch.int32),
+            growth_quantum_rows=growth_quantum_rows,
+            scratch=torch.empty(
+                int(nat.lib().cowsdm_step_scratch_words(banks)), device=device,
+                dtype=torch.int64),
+        )
+        result = torch.empty(1, device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_init_state(
+                state.logical_to_physical.data_ptr(), banks, slots,
+                state.free_rows.data_ptr(), capacity_rows, state.free_count.data_ptr(),
+                state.overflow_flag.data_ptr(), state.scratch.data_ptr(),
+                state.scratch.numel(), template_indices.data_ptr(), templates,
+                result.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_init_state",
+        )
+        if int(result.item()) & nat.ERR_TEMPLATE:
+            raise ValueError("template index lies outside shared initial memory")
+        return state
+
+    @classmethod
+    @torch.no_grad()
+    def from_dense_overlay(
+        cls,
+        shared_initial_memory: torch.Tensor,
+        dense_memory: torch.Tensor,
+        active_slots: torch.Tensor,
+        *,
+        template_indices: torch.Tensor,
+        capacity_rows: int | None = None,
+        state_dtype: torch.dtype = torch.float32,
+        maximum_future_allocations: int | None = None,
+        growth_quantum_rows: int = 0,
+    ) -> "PackedSDMCopyOnWriteState":
+        """Pack an exact full-prefix state into a first-write overlay
+        (allocator.py:587-689)."""
+
+        if shared_initial_memory.ndim == 2:
+            shared_initial_memory = shared_initial_memory.unsqueeze(0)
+        if shared_initial_memory.ndim != 3 or dense_memory.ndim != 3:
+            raise ValueError("SDM handoff memory must be [H,N,D] and [B,N,D]")
+        banks, slots, width = dense_memory.shape
+        if (
+            active_slots.shape != (banks, slots)
+            or active_slots.dtype != torch.bool
+            or active_slots.device != dense_memory.device
+            or shared_initial_memory.device != dense_memory.device
+            or shared_initial_memory.shape[1:] != (slots, width)
+        ):
+            raise ValueError("SDM handoff state and active-slot mask do not align")
+        if (
+            template_indices.shape != (banks,)
+            or template_indices.device != dense_memory.device
+        ):
+            raise ValueError("SDM handoff template indices must be [B] on device")
+        _require_device(dense_memory, "SDM handoff memory")
+        device = dense_memory.device
+        dense = dense_memory.to(torch.float32).contiguous()
+        mask = active_slots.contiguous()
+        workspace = _workspace(banks * slots, 0, device)
+        total = torch.empty(1, device=device, dtype=torch.int64)
+        stream = nat.stream_handle(device)
+        nat.check(
+            nat.lib().cowsdm_count_active(
+                None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
+                total.data_ptr(), stream),
+            "cowsdm_count_active",
+        )
+        active_count = int(total.item())
+        selected, possible = handoff_capacity(
+            active_count, banks, slots, capacity_rows, growth_quantum_rows,
+            maximum_future_allocations)
+        state = cls.allocate(
+            shared_initial_memory,
+            banks=banks,
+            capacity_rows=selected,
+            template_indices=template_indices,
+            state_dtype=state_dtype,
+            growth_quantum_rows=growth_quantum_rows,
+        )
+        workspace = _workspace(banks * slots, selected, device)
+        nat.check(
+            nat.lib().cowsdm_count_active(
+                None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
+                total.data_ptr(), stream),
+            "cowsdm_count_active",
+        )
+        nat.check(
+            nat.lib().cowsdm_pack_overlay(
+                dense.data_ptr(), mask.data_ptr(), banks, slots, width,
+                state.logical_to_physical.data_ptr(), state.values.data_ptr(),
+                state.free_rows.data_ptr(), selected, state.free_count.data_ptr(),
+                workspace.data_ptr(), stream),
+            "cowsdm_pack_overlay",
+        )
+        state.capacity_is_proven = maximum_future_allocations is not None
+        state.proven_maximum_additional_allocations = possible
+        state.validate_invariants()
+        return state
+
+    # ------------------------------------------------------------ growth
+
+    @torch.no_grad()
+    def grow_capacity(self, minimum_capacity_rows: int) -> int:
+        """Grow the shared value slab without changing logical state
+        (allocator.py:691-743).  Row ids stay stable; new ids join the top of
+        the free stack; every old row is counted as copied."""
+
+        if minimum_capacity_rows <= self.capacity_rows:
+            return 0
+        quantum = self.growth_quantum_rows
+        if quantum <= 0:
+            raise ValueError("SDM COW slab growth is disabled")
+        selected = growth_target(minimum_capacity_rows, quantum)
+        if selected >= 2**31:
+            raise ValueError("SDM COW slab cannot grow past 2^31 rows")
+        old_capacity = self.capacity_rows
+        added = selected - old_capacity
+        device = self.values.device
+        values = torch.empty(selected, self.width, device=device, dtype=self.values.dtype)
+        free_rows = torch.empty(selected, device=device, dtype=self.free_rows.dtype)
+        nat.check(
+            nat.lib().cowsdm_grow(
+                self.values.data_ptr(), old_capacity, values.data_ptr(), selected,
+                self.width, self.free_rows.data_ptr(), free_rows.data_ptr(),
+                self.free_count.data_ptr(), self.overflow_flag.data_ptr(),
+                nat.stream_handle(device)),
+            "cowsdm_grow",
+        )
+        self.values = values
+        self.free_rows = free_rows
+        self.proven_maximum_additional_allocations += added
+        self.growth_events += 1
+        self.growth_rows_added += added
+        self.growth_rows_copied += old_capacity
+        return added
+
+    @torch.no_grad()
+    def prepare_step_capacity(self, maximum_new_rows: int) -> int:
+        """Prove one fused decode step, growing pooled headroom if short
+        (allocator.py:745-773).  Host bookkeeping; reads free_count only
+        when the running proof is exhausted."""
+
+        if maximum_new_rows < 0:
+            raise ValueError("maximum new SDM rows cannot be negative")
+        if self.growth_quantum_rows <= 0:
+            if not self.capacity_is_proven:
+                raise ValueError("SDM COW capacity has no decode proof")
+            return 0
+        if self.proven_maximum_additional_allocations < maximum_new_rows:
+            free_rows = int(self.free_count.item())
+            if free_rows < maximum_new_rows:
+                self.grow_capacity(self.capacity_rows + maximum_new_rows - free_rows)
+                free_rows = int(self.free_count.item())
+            self.proven_maximum_additional_allocations = free_rows
+        self.proven_maximum_additional_allocations -= maximum_new_rows
+        self.capacity_is_proven = True
+        return self.capacity_rows
+
+    # -------------------------------------------------------- lifecycle
+
+    def _count_live(self, mapping: torch.Tensor, workspace: torch.Tensor,
+                    bank_list: torch.Tensor | None = None) -> torch.Tensor:
+        total = torch.empty(1, device=mapping.device, dtype=torch.int64)
+        nsel = mapping.shape[0] if bank_list is None else bank_list.numel()
+        nat.check(
+            nat.lib().cowsdm_count_active(
+                mapping.data_ptr(), mapping.shape[0], mapping.shape[1], nat.ptr(bank_list),
+                nsel, None,
+                workspace.data_ptr(), total.data_ptr(), nat.stream_handle(mapping.device)),
+            "cowsdm_count_active",
+        )
+        return total
+
+    @torch.no_grad()
+    def trim_capacity(self, *, headroom_rows: int = 0) -> int:
+        """Repack live rows and return unused slab rows (allocator.py:775-839)."""
+
+        if headroom_rows < 0:
+            raise ValueError("SDM trim headroom cannot be negative")
+        quantum = self.growth_quantum_rows
+        if quantum <= 0:
+            raise ValueError("SDM COW slab trimming requires copy-on-write capacity")
+        device = self.values.device
+        entries = self.banks * self.slots
+        workspace = _workspace(entries, self.capacity_rows, device)
+        active_count = int(self._count_live(self.logical_to_physical, workspace).item())
+        selected = trim_target(active_count, headroom_rows, quantum)
+        if selected >= self.capacity_rows:
+            return 0
+        values = torch.empty(selected, self.width, device=device, dtype=self.values.dtype)
+        mapping = torch.empty_like(self.logical_to_physical)
+        free_rows = torch.empty(selected, device=device, dtype=self.free_rows.dtype)
+        nat.check(
+            nat.lib().cowsdm_trim_repack(
+                self.logical_to_physical.data_ptr(), self.values.data_ptr(),
+                self.capacity_rows, self.banks,
+                self.slots, self.width, mapping.data_ptr(), values.data_ptr(),
+                free_rows.data_ptr(), selected, self.free_count.data_ptr(),
+                self.overflow_flag.data_ptr(), workspace.data_ptr(),
+                nat.stream_handle(device)),
+            "cowsdm_trim_repack",
+        )
+        removed = self.capacity_rows - selected
+        self.values = values
+        self.logical_to_physical = mapping
+        self.free_rows = free_rows
+        self.capacity_is_proven = False
+        self.proven_maximum_additional_allocations = selected - active_count
+        return removed
+
+    @torch.no_grad()
+    def append_banks_from(self, other: "PackedSDMCopyOnWriteState") -> int:
+        """Move another cohort's banks into this pool (allocator.py:841-914).
+        Only live rows are copied, into rows popped from the top of this free
+        stack in the other map's row-major order."""
+
+        if (
+            other.slots != self.slots
+            or other.width != self.width
+            or other.values.device != self.values.device
+            or other.values.dtype != self.values.dtype
+            or other.shared_initial_memory.shape != self.shared_initial_memory.shape
+        ):
+            raise ValueError("admitted SDM banks do not match the destination pool")
+        if (
+            other.shared_initial_memory.data_ptr() != self.shared_initial_memory.data_ptr()
+            and not torch.equal(other.shared_initial_memory, self.shared_initial_memory)
+        ):
+            raise ValueError("admitted SDM banks use different learned initial memory")
+        device = self.values.device
+        other_entries = other.banks * other.slots
+        workspace = _workspace(other_entries, other.capacity_rows, device)
+        active_count = int(self._count_live(other.logical_to_physical, workspace).item())
+        free_count = int(self.free_count.item())
+        if free_count < active_count:
+            self.grow_capacity(self.capacity_rows + active_count - free_count)
+        banks = self.banks + other.banks
+        mapping = torch.empty(banks, self.slots, device=device, dtype=torch.int32)
+        templates = torch.empty(banks, device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_append_banks(
+                self.logical_to_physical.data_ptr(), self.template_indices.data_ptr(),
+                self.banks, self.values.data_ptr(), self.capacity_rows,
+                self.free_rows.data_ptr(), self.free_count.data_ptr(),
+                other.logical_to_physical.data_ptr(), other.template_indices.data_ptr(),
+                other.values.data_ptr(), other.banks, other.capacity_rows, self.slots,
+                self.width, mapping.data_ptr(), templates.data_ptr(),
+                workspace.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_append_banks",
+        )
+        self.logical_to_physical = mapping
+        self.template_indices = templates
+        self.scratch = _scratch(banks, device)
+        if self.growth_quantum_rows:
+            self.proven_maximum_additional_allocations = min(
+                self.proven_maximum_additional_allocations, int(self.free_count.item()))
+        else:
+            self.capacity_is_proven = False
+            self.proven_maximum_additional_allocations = 0
+        return active_count
+
+    def _bank_list(self, bank_indices: torch.Tensor, what: str) -> torch.Tensor:
+        if (
+            bank_indices.ndim != 1
+            or bank_indices.dtype not in (torch.int32, torch.int64)
+            or bank_indices.device != self.values.device
+        ):
+            raise ValueError(f"{what} bank indices must be integer [S] on device")
+        return bank_indices.to(torch.int64).contiguous()
+
+    def _check_banks(self, bank_list: torch.Tensor, discarded_active: bool) -> int:
+        device = self.values.device
+        workspace = _workspace(self.banks * self.slots, self.banks, device)
+        result = torch.empty(1, device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_check_banks(
+                self.logical_to_physical.data_ptr(), self.banks, self.slots,
+                bank_list.data_ptr(), bank_list.numel(), int(discarded_active),
+                workspace.data_ptr(), result.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_check_banks",
+        )
+        return int(result.item())
+
+    @torch.no_grad()
+    def retain_banks(self, bank_indices: torch.Tensor) -> None:
+        """Compact already-released banks; values never move
+        (allocator.py:916-942)."""
+
+        bank_list = self._bank_list(bank_indices, "retained")
+        flags = self._check_banks(bank_list, discarded_active=True)
+        if flags & 1:
+            raise ValueError("retained bank index is invalid or duplicated")
+        if flags & 2:
+            raise ValueError("discarded SDM banks must be released before compaction")
+        device = self.values.device
+        nsel = bank_list.numel()
+        mapping = torch.empty(nsel, self.slots, device=device, dtype=torch.int32)
+        templates = torch.empty(nsel, device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_retain_banks(
+                self.logical_to_physical.data_ptr(), self.template_indices.data_ptr(),
+                self.banks, self.slots, bank_list.data_ptr(), nsel, mapping.data_ptr(),
+                templates.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_retain_banks",
+        )
+        self.logical_to_physical = mapping
+        self.template_indices = templates
+        self.scratch = _scratch(nsel, device)
+
+    @torch.no_grad()
+    def release(self, bank_indices: torch.Tensor) -> torch.Tensor:
+        """Release whole banks and push their rows on the free stack
+        (allocator.py:1018-1067).  Returns the released row count (0-d)."""
+
+        bank_list = self._bank_list(bank_indices, "released")
+        if bank_list.numel() == 0:
+            return self.free_count.new_zeros(())
+        if self._check_banks(bank_list, discarded_active=False) & 1:
+            raise ValueError("released bank index is invalid or duplicated")
+        device = self.values.device
+        nsel = bank_list.numel()
+        workspace = _workspace(nsel * self.slots, 0, device)
+        self._count_live(self.logical_to_physical, workspace, bank_list)
+        released = torch.empty((), device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_release(
+                self.logical_to_physical.data_ptr(), self.banks, self.slots,
+                bank_list.data_ptr(), nsel,
+                self.free_rows.data_ptr(), self.capacity_rows, self.free_count.data_ptr(),
+                workspace.data_ptr(), released.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_release",
+        )
+        return released
+
+    # ------------------------------------------------------ properties
+
+    @property
+    def banks(self) -> int:
+        return self.logical_to_physical.shape[0]
+
+    @property
+    def slots(self) -> int:
+        return self.logical_to_physical.shape[1]
+
+    @property
+    def width(self) -> int:
+        return self.values.shape[1]
+
+    @property
+    def capacity_rows(self) -> int:
+        return self.values.shape[0]
+
+    def allocated_rows_tensor(self) -> torch.Tensor:
+        """Device-resident number of live physical rows (allocator.py:960-963)."""
+
+        return self.free_count.new_tensor(self.capacity_rows) - self.free_count
+
+    def storage_bytes(self) -> dict[str, int]:
+        """Retained tensor storage, shared model state separate
+        (allocator.py:965-982); ``step_scratch`` is this build's extra
+        allocator metadata."""
+
+        private = {
+            "value_slab_reserved": _tensor_bytes(self.values),
+            "logical_to_physical": _tensor_bytes(self.logical_to_physical),
+            "free_row_stack": _tensor_bytes(self.free_rows),
+            "free_count": _tensor_bytes(self.free_count),
+            "overflow_flag": _tensor_bytes(self.overflow_flag),
+            "template_indices": _tensor_bytes(self.template_indices),
+            "step_scratch": 0 if self.scratch is None else _tensor_bytes(self.scratch),
+        }
+        private["private_allocator_reserved_total"] = sum(private.values())
+        private["shared_initial_memory"] = _tensor_bytes(self.shared_initial_memory)
+        private["including_shared_initial_memory"] = (
+            private["private_allocator_reserved_total"] + private["shared_initial_memory"]
+        )
+        return private
+
+    def used_bytes(self) -> dict[str, int]:
+        """Live-row bytes plus resident metadata (allocator.py:984-1001)."""
+
+        allocated = int(self.allocated_rows_tensor().item())
+        live_values = allocated * self.width * self.values.element_size()
+        metadata = (
+            _tensor_bytes(self.logical_to_physical)
+            + _tensor_bytes(self.free_rows)
+            + _tensor_bytes(self.free_count)
+            + _tensor_bytes(self.overflow_flag)
+            + _tensor_bytes(self.template_indices)
+            + (0 if self.scratch is None else _tensor_bytes(self.scratch))
+        )
+        return {
+            "allocated_rows": allocated,
+            "live_value_bytes": live_values,
+            "allocator_metadata_bytes": metadata,
+            "private_live_total": live_values + metadata,
+        }
+
+    @torch.no_grad()
+    def materialize_dense(self) -> torch.Tensor:
+        """Effective [B,N,D] table for validation (allocator.py:1003-1016)."""
+
+        device = self.values.device
+        dense = torch.empty(self.banks, self.slots, self.width, device=device,
+                            dtype=self.values.dtype)
+        nat.check(
+            nat.lib().cowsdm_materialize_dense(
+                self.shared_initial_memory.data_ptr(), self.shared_initial_memory.shape[0],
+                self.template_indices.data_ptr(),
+                self.values.data_ptr(), self.logical_to_physical.data_ptr(), self.banks,
+                self.slots, self.width, self.capacity_rows, dense.data_ptr(),
+                nat.stream_handle(device)),
+            "cowsdm_materialize_dense",
+        )
+        return dense
+
+    @torch.no_grad()
+    def validate_invariants(self) -> dict[str, Any]:
+        """Synchronously validate row ownership and the free-list partition
+        (allocator.py:1069-1095); also surfaces the kernels' sticky error
+        word."""
+
+        device = self.values.device
+        workspace = _workspace(self.banks * self.slots, self.capacity_rows, device)
+        stats = torch.empty(8, device=device, dtype=torch.int64)
+        nat.check(
+            nat.lib().cowsdm_check_invariants(
+                self.logical_to_physical.data_ptr(), self.banks, self.slots,
+                self.free_rows.data_ptr(), self.free_count.data_ptr(),
+                self.overflow_flag.data_ptr(), nat.ptr(self.scratch), self.capacity_rows,
+                workspace.data_ptr(), stats.data_ptr(), nat.stream_handle(device)),
+            "cowsdm_check_invariants",
+        )
+        (live, free, dup_live, dup_free, not_once, outside, overflow, errors) = (
+            int(x) for x in stats.tolist())
+        if overflow != 0:
+            raise AssertionError("SDM COW allocator recorded a slab overflow")
+        if errors != 0:
+            raise AssertionError(f"SDM COW kernels recorded errors (flags {errors:#x})")
+        if dup_live:
+            raise AssertionError("one physical SDM row has multiple logical owners")
+        if dup_free:
+            raise AssertionError("free SDM row stack contains duplicates")
+        if live + free != self.capacity_rows:
+            raise AssertionError("active and free SDM rows do not cover capacity")
+        if not_once or outside:
+            raise AssertionError("active and free SDM rows do not partition the slab")
+        return {
+            "capacity_rows": self.capacity_rows,
+            "allocated_rows": live,
+            "free_rows": free,
+            "exact_partition": True,
+        }
+
+    def ensure_scratch(self) -> torch.Tensor:
+        if self.scratch is None or self.scratch.numel() != int(
+                nat.lib().cowsdm_step_scratch_words(self.banks)):
+            self.scratch = _scratch(self.banks, self.values.device)
+        return self.scratch
+
+
+# ------------------------------------------------------------- validation
+
+
+def _validate_indices(indices: torch.Tensor, *, name: str, banks: int,
+                      device: torch.device) -> None:
+    """Host half of _validate_indices (allocator.py:1107-1126); bounds are
+    checked on the device."""
+
+    if (
+        indices.ndim != 2
+        or indices.shape[0] != banks
+        or indices.shape[1] <= 0
+        or indices.dtype not in (torch.int32, torch.int64)
+        or indices.device != device
+    ):
+        raise ValueError(f"{name} indices must be integer [B,K] on device")
+
+
+def _validate_gates(input_gate, erase_gate, forget_log_gate, *, banks: int) -> None:
+    """allocator.py:1143-1155."""
+
+    if input_gate.shape != (banks,):
+        raise ValueError("native SDM input gate must be [B]")
+    if erase_gate.shape != input_gate.shape or forget_log_gate.shape != input_gate.shape:
+        raise ValueError("SDM input, erase, and forget gates must align")
+
+
+def _select_backend(backend: str, *, tensor: torch.Tensor, writes: int, reads: int) -> None:
+    """Backend dispatch (allocator.py:1158-1176): only the HIP kernels ship."""
+
+    if backend not in ("auto", "torch", "triton", "hip"):
+        raise ValueError("allocator backend must be auto, hip, torch, or triton")
+    if backend == "triton":
+        raise RuntimeError("the requested Triton SDM COW backend is unavailable")
+    if backend == "torch":
+        raise RuntimeError(
+            "the torch SDM COW backend is not shipped: the HIP kernels are the "
+            "only implementation")
+    _require_device(tensor, "SDM COW step tensors")
+    if writes > 64 or reads > 256:
+        raise ValueError("HIP SDM COW step supports at most 64 writes and 256 reads")
+
+
+def _check_float_tensors(tensors: Sequence[torch.Tensor]) -> None:
+    for tensor in tensors:
+        if tensor.dtype != torch.float32:
+            raise ValueError("HIP SDM COW step takes float32 weights, values and gates")
+        if not tensor.is_contiguous():
+            raise ValueError("HIP SDM COW step tensors must be contiguous")
+
+
+def _index_code(write_indices: torch.Tensor, read_indices: torch.Tensor) -> int:
+    if write_indices.dtype != read_indices.dtype:
+        raise ValueError("write and read indices must share one integer dtype")
+    if not (write_indices.is_contiguous() and read_indices.is_contiguous()):
+        raise ValueError("HIP SDM COW step tensors must be contiguous")
+    return nat.INDEX_INT64 if write_indices.dtype == torch.int64 else nat.INDEX_INT32
+
+
+def _raise_precheck(flags: int, *, packed: bool) -> None:
+    """Reference messages, in the reference's check order."""
+
+    if flags & nat.ERR_WRITE_INDEX:
+        raise ValueError("write index lies outside the logical table")
+    if flags & nat.ERR_READ_INDEX:
+        raise ValueError("read index lies outside the logical table")
+    if flags & nat.ERR_DUP_WRITE:
+        raise ValueError("one SDM step cannot write one logical slot twice")
+    if flags & nat.ERR_CORRUPT:
+        raise AssertionError("SDM COW logical map holds a row outside the slab")
+    if packed and flags & nat.ERR_EXHAUSTED:
+        raise ValueError("SDM COW physical slab is exhausted")
+
+
+_precheck_buffers: dict[torch.device, torch.Tensor] = {}
+
+
+def _precheck_result(device: torch.device) -> torch.Tensor:
+    buf = _precheck_buffers.get(device)
+    if buf is None:
+        buf = torch.zeros(1, device=device, dtype=torch.int64)
+        _precheck_buffers[device] = buf
+    return buf
+
+
+def _run_precheck(layer: nat.Layer, shape: nat.Shape, *, dense: bool, unique: bool,
+                  capacity: bool, device: torch.device) -> None:
+    result = _precheck_result(device)
+    nat.check(
+        nat.lib().cowsdm_step_precheck(
+            layer, shape, int(dense), int(unique), int(capacity), result.data_ptr(),
+            nat.stream_handle(device)),
+        "cowsdm_step_precheck",
+    )
+    _raise_precheck(int(result.item()), packed=not dense)
+
+
+# ------------------------------------------------------------------ steps
+
+
+def _step_layer(
+    state: PackedSDMCopyOnWriteState | None,
+    memory: torch.Tensor | None,
+    write_indices, write_weights, values, input_gate, erase_gate, forget_log_gate,
+    read_indices, read_weights, output, first, repeated, allocated,
+) -> nat.Layer:
+    layer = nat.Layer()
+    if state is not None:
+        layer.shared_initial_memory = state.shared_initial_memory.data_ptr()
+        layer.template_indices = state.template_indices.data_ptr()
+        layer.values = state.values.data_ptr()
+        layer.logical_to_physical = state.logical_to_physical.data_ptr()
+        layer.free_rows = state.free_rows.data_ptr()
+        layer.free_count = state.free_count.data_ptr()
+        layer.overflow_flag = state.overflow_flag.data_ptr()
+        layer.scratch = state.ensure_scratch().data_ptr()
+        layer.capacity_rows = state.capacity_rows
+    else:
+        layer.values = memory.data_ptr()
+        layer.capacity_rows = 0
+    layer.write_indices = write_indices.data_ptr()
+    layer.write_weights = write_weights.data_ptr()
+    layer.step_values = values.data_ptr()
+    layer.input_gate = input_gate.data_ptr()
+    layer.erase_gate = erase_gate.data_ptr()
+    layer.forget_log_gate = forget_log_gate.data_ptr()
+    layer.read_indices = read_indices.data_ptr()
+    layer.read_weights = read_weights.data_ptr()
+    layer.output = output.data_ptr()
+    layer.first_touches_out = nat.ptr(first)
+    layer.repeated_writes_out = nat.ptr(repeated)
+    layer.allocated_rows_out = nat.ptr(allocated)
+    return layer
+
+
+def _check_step_inputs(banks, slots, width, device, write_indices, write_weights, values,
+                       input_gate, forget_log_gate, read_indices, read_weights, erase_gate,
+                       *, dense: bool):
+    _validate_indices(write_indices, name="write", banks=banks, device=device)
+    _validate_indices(read_indices, name="read", banks=banks, device=device)
+    if (
+        write_weights.shape != write_indices.shape
+        or read_weights.shape != read_indices.shape
+        or values.shape != (banks, width)
+    ):
+        raise ValueError(
+            "dense SDM route weights and values do not align" if dense
+            else "SDM route weights and values do not align")
+    tensors = (write_weights, values, input_gate, forget_log_gate, read_weights) + (
+        () if erase_gate is None else (erase_gate,))
+    if any(tensor.device != device for tensor in tensors):
+        raise ValueError(
+            "dense SDM step tensors must share one device" if dense
+            else "SDM COW step tensors must share one device")
+    effective_erase = input_gate if erase_gate is None else erase_gate
+    _validate_gates(input_gate, effective_erase, forget_log_gate, banks=banks)
+    return effective_erase
+
+
+def _shape(banks, slots, width, writes, reads, templates, index_code) -> nat.Shape:
+    shape = nat.Shape()
+    shape.banks = banks
+    shape.slots = slots
+    shape.width = width
+    shape.writes = writes
+    shape.reads = reads
+    shape.templates = templates
+    shape.index_dtype = index_code
+    return shape
+
+
+@torch.no_grad()
+def packed_sdm_cow_step(
+    state: PackedSDMCopyOnWriteState,
+    write_indices: torch.Tensor,
+    write_weights: torch.Tensor,
+    values: torch.Tensor,
+    input_gate: torch.Tensor,
+    forget_log_gate: torch.Tensor,
+    read_indices: torch.Tensor,
+    read_weights: torch.Tensor,
+    *,
+    erase_gate: torch.Tensor | None = None,
+    backend: str = "auto",
+    validate_routes: bool = True,
+    collect_diagnostics: bool = True,
+) -> tuple[torch.Tensor, SDMCopyOnWriteStep | None]:
+    """One exact sparse SDM write and read through the packed overlay
+    (allocator.py:1381-1525), as one fused HIP launch.
+
+    Per bank: resolve the W write routes through the map, pop free rows for
+    first touches (bank-major), copy M0 rows, apply the gated-delta update in
+    FP32, then the weighted read of R rows after the write.
+    """
+
+    banks, slots, width = state.banks, state.slots, state.width
+    device = state.values.device
+    effective_erase = _check_step_inputs(
+        banks, slots, width, device, write_indices, write_weights, values, input_gate,
+        forget_log_gate, read_indices, read_weights, erase_gate, dense=False)
+    _select_backend(backend, tensor=state.values, writes=write_indices.shape[1],
+                    reads=read_indices.shape[1])
+    _check_float_tensors((write_weights, values, input_gate, effective_erase,
+                          forget_log_gate, read_weights))
+    index_code = _index_code(write_indices, read_indices)
+    output = torch.empty_like(values)
+    first = repeated = allocated = None
+    if collect_diagnostics:
+        first = torch.empty(banks, device=device, dtype=torch.int64)
+        repeated = torch.empty(banks, device=device, dtype=torch.int64)
+        allocated = torch.empty((), device=device, dtype=torch.int32)
+    layer = _step_layer(state, None, write_indices, write_weights, values, input_gate,
+                        effective_erase, forget_log_gate, read_indices, read_weights, output,
+                        first, repeated, allocated)
+    shape = _shape(banks, slots, width, write_indices.shape[1], read_indices.shape[1],
+                   state.shared_initial_memory.shape[0], index_code)
+    if banks and (validate_routes or not state.capacity_is_proven):
+        _run_precheck(layer, shape, dense=False, unique=validate_routes,
+                      capacity=not state.capacity_is_proven, device=device)
+    if banks:
+        nat.check(nat.lib().cowsdm_packed_step(layer, shape, nat.stream_handle(device)),
+                  "cowsdm_packed_step")
+    elif allocated is not None:
+        allocated = state.allocated_rows_tensor()
+    if not collect_diagnostics:
+        return output, None
+    return output, SDMCopyOnWriteStep(
+        first_touches_by_sequence=first,
+        repeated_writes_by_sequence=repeated,
+        allocated_rows_after_step=allocated,
+    )
+
+
+@torch.no_grad()
+def dense_sdm_sparse_step(
+    memory: torch.Tensor,
+    write_indices: torch.Tensor,
+    write_weights: torch.Tensor,
+    values: torch.Tensor,
+    input_gate: torch.Tensor,
+    forget_log_gate: torch.Tensor,
+    read_indices: torch.Tensor,
+    read_weights: torch.Tensor,
+    *,
+    erase_gate: torch.Tensor | None = None,
+    backend: str = "auto",
+    validate_routes: bool = True,
+) -> torch.Tensor:
+    """Dense-table control: the same sparse update and read on
+    ``memory`` [B,N,D] (allocator.py:1528-1633).  Shares the packed step's
+    row math, so both produce bit-identical state and readings."""
+
+    if memory.ndim != 3:
+        raise ValueError("dense SDM memory must be [B,N,D]")
+    banks, slots, width = memory.shape
+    device = memory.device
+    effective_erase = _check_step_inputs(
+        banks, slots, width, device, write_indices, write_weights, values, input_gate,
+        forget_log_gate, read_indices, read_weights, erase_gate, dense=True)
+    _select_backend(backend, tensor=memory, writes=write_indices.shape[1],
+                    reads=read_indices.shape[1])
+    _check_float_tensors((memory, write_weights, values, input_gate, effective_erase,
+                          forget_log_gate, read_weights))
+    index_code = _index_code(write_indices, read_indices)
+    output = torch.empty_like(values)
+    layer = _step_layer(None, memory, write_indices, write_weights, values, input_gate,
+                        effective_erase, forget_log_gate, read_indices, read_weights, output,
+                        None, None, None)
+    shape = _shape(banks, slots, width, write_indices.shape[1], read_indices.shape[1], 1,
+                   index_code)
+    if banks and validate_routes:
+        _run_precheck(layer, shape, dense=True, unique=True, capacity=False, device=device)
+    if banks:
+        nat.check(nat.lib().cowsdm_dense_step(layer, shape, nat.stream_handle(device)),
+                  "cowsdm_dense_step")
+    return output
+
+
+def _layer_arrays(count: int, *args):
+    out = []
+    for arg in args:
+        if arg is None:
+            out.append([None] * count)
+        else:
+            items = list(arg)
+            if len(items) != count:
+                raise ValueError("per-layer inputs must provide one entry per layer")
+            out.append(items)
+    return out
+
+
+@torch.no_grad()
+def packed_sdm_cow_step_layers(
+    states: Sequence[PackedSDMCopyOnWriteState],
+    write_indices, write_weights, values, input_gate, forget_log_gate,
+    read_indices, read_weights,
+    *,
+    erase_gate=None,
+    outputs: Sequence[torch.Tensor] | None = None,
+    validate_routes: bool = False,
+) -> list[torch.Tensor]:
+    """``packed_sdm_cow_step`` for several independent layers in one launch.
+
+    Every argument after ``states`` is a per-layer sequence (a stacked
+    [L, ...] tensor works).  All layers share B, N, D, W, R and index dtype.
+    Results equal L separate ``packed_sdm_cow_step`` calls.  No counterpart
+    in the reference; meant for callers that hold all layers' routes, such as
+    synthetic-route serving benchmarks.
+    """
+
+    count = len(states)
+    if count == 0:
+        return []
+    (wi, ww, vv, ig, fg, ri, rw, eg, outs) = _layer_arrays(
+        count, write_indices, write_weights, values, input_gate, forget_log_gate,
+        read_indices, read_weights, erase_gate, outputs)
+    first = states[0]
+    device = first.values.device
+    layers = (nat.Layer * count)()
+    shape = None
+    results = []
+    for i, state in enumerate(states):
+        if (state.banks, state.slots, state.width) != (first.banks, first.slots, first.width):
+            raise ValueError("all layers of one launch must share banks, slots and width")
+        effective_erase = _check_step_inputs(
+            state.banks, state.slots, state.width, device, wi[i], ww[i], vv[i], ig[i], fg[i],
+            ri[i], rw[i], eg[i], dense=False)
+        _select_backend("auto", tensor=state.values, writes=wi[i].shape[1],
+                        reads=ri[i].shape[1])
+        _check_float_tensors((ww[i], vv[i], ig[i], effective_erase, fg[i], rw[i]))
+        code = _index_code(wi[i], ri[i])
+        out = outs[i] if outs[i] is not None else torch.empty_like(vv[i])
+        results.append(out)
+        layers[i] = _step_layer(state, None, wi[i], ww[i], vv[i], ig[i], effective_erase,
+                                fg[i], ri[i], rw[i], out, None, None, None)
+        this_shape = _shape(state.banks, state.slots, state.width, wi[i].shape[1],
+                            ri[i].shape[1], state.shared_initial_memory.shape[0], code)
+        if shape is None:
+            shape = this_shape
+        elif (shape.writes, shape.reads, shape.index_dtype, shape.templates) != (
+                this_shape.writes, this_shape.reads, this_shape.index_dtype,
+                this_shape.templates):
+            raise ValueError("all layers of one launch must share W, R and index dtype")
+        if state.banks and (validate_routes or not state.capacity_is_proven):
+            _run_precheck(layers[i], this_shape, dense=False, unique=validate_routes,
+                          capacity=not state.capacity_is_proven, device=device)
+    if first.banks:
+        nat.check(nat.lib().cowsdm_packed_step_layers(
+            layers, count, shape, nat.stream_handle(device)), "cowsdm_packed_step_layers")
+    return results
+
+
+@torch.no_grad()
+def dense_sdm_sparse_step_layers(
+    memories: Sequence[torch.Tensor],
+    write_indices, write_weights, values, input_gate, forget_log_gate,
+    read_indices, read_weights,
+    *,
+    erase_gate=None,
+    outputs: Sequence[torch.Tensor] | None = None,
+) -> list[torch.Tensor]:
+    """``dense_sdm_sparse_step`` for several independent layers in one launch
+    (the dense-table control of ``packed_sdm_cow_step_layers``)."""
+
+    count = len(memories)
+    if count == 0:
+        return []
+    (wi, ww, vv, ig, fg, ri, rw, eg, outs) = _layer_arrays(
+        count, write_indices, write_weights, values, input_gate, forget_log_gate,
+        read_indices, read_weights, erase_gate, outputs)
+    device = memories[0].device
+    layers = (nat.Layer * count)()
+    shape = None
+    results = []
+    for i, memory in enumerate(memories):
+        if memory.ndim != 3 or memory.shape != memories[0].shape:
+            raise ValueError("all layers of one launch must share one [B,N,D] shape")
+        banks, slots, width = memory.shape
+        effective_erase = _check_step_inputs(
+            banks, slots, width, device, wi[i], ww[i], vv[i], ig[i], fg[i], ri[i], rw[i],
+            eg[i], dense=True)
+        _select_backend("auto", tensor=memory, writes=wi[i].shape[1], reads=ri[i].shape[1])
+        _check_float_tensors((memory, ww[i], vv[i], ig[i], effective_erase, fg[i], rw[i]))
+        code = _index_code(wi[i], ri[i])
+        out = outs[i] if outs[i] is not None else torch.empty_like(vv[i])
+        results.append(out)
+        layers[i] = _step_layer(None, memory, wi[i], ww[i], vv[i], ig[i], effective_erase,
+                                fg[i], ri[i], rw[i], out, None, None, None)
+        this_shape = _shape(banks, slots, width, wi[i].shape[1], ri[i].shape[1], 1, code)
+        if shape is None:
+            shape = this_shape
+        elif (shape.writes, shape.reads, shape.index_dtype) != (
+                this_shape.writes, this_shape.reads, this_shape.index_dtype):
+            raise ValueError("all layers of one launch must share W, R and index dtype")
+    if memories[0].shape[0]:
+        nat.check(nat.lib().cowsdm_dense_step_layers(
+            layers, count, shape, nat.stream_handle(device)), "cowsdm_dense_step_layers")
+    return results
+
+
+@torch.no_grad()
+def mark_written(active: torch.Tensor, indices: torch.Tensor) -> None:
+    """active[b, indices[b, k]] = True for every k (inference.py:332-347's
+    union of written rows).  ``indices`` is [B, K] int32/int64."""
+
+    if active.dtype != torch.bool or active.ndim != 2 or not active.is_contiguous():
+        raise ValueError("active mask must be a contiguous bool [B,N] tensor")
+    _require_device(active, "active mask")
+    if indices.ndim != 2 or indices.shape[0] != active.shape[0] or indices.dtype not in (
+            torch.int32, torch.int64) or indices.device != active.device:
+        raise ValueError("written indices must be integer [B,K] on the mask device")
+    indices = indices.contiguous()
+    result = _precheck_result(active.device)
+    nat.check(
+        nat.lib().cowsdm_mark_written(
+            active.data_ptr(), active.shape[0], active.shape[1], indices.data_ptr(),
+            indices.shape[1],
+            nat.INDEX_INT64 if indices.dtype == torch.int64 else nat.INDEX_INT32,
+            result.data_ptr(), nat.stream_handle(active.device)),
+        "cowsdm_mark_written",
+    )

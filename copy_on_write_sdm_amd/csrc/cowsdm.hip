@@ -1,0 +1,1641 @@
+// libcowsdm: copy-on-write Sparse Delta Memory decode step for MI355X
+// (gfx950), plus the slab lifecycle (growth, pack handoff, release, bank
+// retention, trim, admission, invariant checks).  Exposed through the C ABI
+// declared in include/cowsdm.h.
+//
+// Semantics follow the reference's torch path, copy_on_write_sdm/
+// allocator.py:1466-1525 (packed step) and 1612-1633 (dense step), with
+// first-touch rows popped from the free stack in bank-major order exactly as
+// allocator.py:1471-1481 orders them.
+//
+// Design (one wavefront per bank):
+//  * lane l < W holds write route l, lane l holds read routes l, l+64, ...;
+//    route metadata is broadcast with readlane so every row address is a
+//    wave-uniform base plus a lane offset: each D=128 row is one coalesced
+//    512-byte access (two floats per lane).
+//  * every write row and every read row that is not also written this step
+//    is loaded before any cross-bank wait, so the HBM latency of the row
+//    loads overlaps the free-stack resolution;
+//  * a read of a slot written in the same step takes the updated row from
+//    registers (read-after-write without a barrier or a reload);
+//  * first touches pop rows at free_count-1-(bank prefix + rank).  The bank
+//    prefix is an exclusive scan over banks computed with a decoupled
+//    look-back over per-bank slots in the layer's scratch; every wave only
+//    waits on lower-numbered banks of its own layer, and every wait is
+//    bounded (a timed-out scan poisons the banks after it instead of
+//    hanging);
+//  * the last bank to finish (ticket counter) publishes the new free_count
+//    and advances the scratch epoch, which retires this launch's slots.
+//  * float math is the reference's operation order with every product and
+//    sum rounded separately (the file is built with -ffp-contract=off);
+//    exp(forget_log_gate) is evaluated in double and rounded once.
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "cowsdm.h"
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kBanksPerBlock = 4;           // waves (banks) per workgroup
+constexpr int kStepThreads = kWave * kBanksPerBlock;
+constexpr int kMaxLayers = 8;               // layers per step launch
+constexpr int kReadBatch = 16;              // read rows in flight per batch
+constexpr int kMaxReadSlots = 4;            // R <= 256 = 4 * 64
+constexpr int kSpinLimit = 1 << 16;         // bounded look-back wait
+constexpr int kTile = 2048;                 // ranking tile (entries)
+constexpr int kTileThreads = 256;
+constexpr int kPerThread = kTile / kTileThreads;
+
+constexpr uint32_t kStatusEmpty = 0;
+constexpr uint32_t kStatusAggregate = 1;
+constexpr uint32_t kStatusInclusive = 2;
+constexpr uint32_t kStatusPoison = 3;
+constexpr uint64_t kValueMask = (1ull << 30) - 1;
+
+thread_local char g_error[512] = "";
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, args);
+  va_end(args);
+  return code;
+}
+
+int32_t launch_status(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "%s: %s", where, hipGetErrorString(e));
+  }
+  return 0;
+}
+
+struct StepParams {
+  cowsdm_layer_t layer[kMaxLayers];
+  int32_t nlayers;
+  int32_t banks;
+  int32_t slots;
+  int32_t width;
+  int32_t writes;
+  int32_t reads;
+  int32_t templates;
+  int32_t blocks_per_layer;
+};
+
+// ------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ int rl(int x, int lane) {
+  return __builtin_amdgcn_readlane(x, lane);
+}
+
+__device__ __forceinline__ float rlf(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, kWave);
+  return v;
+}
+
+template <typename IDX>
+__device__ __forceinline__ int64_t load_index(const void* base, int64_t i) {
+  return static_cast<int64_t>(static_cast<const IDX*>(base)[i]);
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_row(const float* p, float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+  } else if constexpr (VEC == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    x[0] = t.x; x[1] = t.y;
+  } else {
+    x[0] = *p;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_row(float* p, const float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  } else if constexpr (VEC == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+  } else {
+    *p = x[0];
+  }
+}
+
+__device__ __forceinline__ uint64_t atomic_load_u64(const int64_t* p) {
+  return static_cast<uint64_t>(__hip_atomic_load(
+      const_cast<int64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ void atomic_store_u64(int64_t* p, uint64_t v) {
+  __hip_atomic_store(p, static_cast<int64_t>(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
+                                              uint64_t value) {
+  return (static_cast<uint64_t>(epoch) << 32) |
+         (static_cast<uint64_t>(status) << 30) | (value & kValueMask);
+}
+
+// Exclusive prefix over banks [0, bank) of the per-bank first-touch counts,
+// by decoupled look-back.  Publishes this bank's aggregate first, then its
+// inclusive prefix.  Waits only on lower banks; each wait is bounded.
+__device__ int64_t bank_prefix(int64_t* slots, int bank, uint32_t epoch,
+                               int count, int lane, bool* poisoned) {
+  if (lane == 0) {
+    atomic_store_u64(&slots[bank], slot_word(epoch, kStatusAggregate, count));
+  }
+  int64_t exclusive = 0;
+  bool bad = false;
+  int end = bank;
+  while (end > 0) {
+    const int j = end - 1 - lane;
+    uint32_t status = kStatusInclusive;
+    int64_t value = 0;
+    if (j >= 0) {
+      uint64_t w = atomic_load_u64(&slots[j]);
+      int spins = 0;
+      while ((static_cast<uint32_t>(w >> 32) != epoch ||
+              ((w >> 30) & 3u) == kStatusEmpty) &&
+             spins < kSpinLimit) {
+        __builtin_amdgcn_s_sleep(1);
+        w = atomic_load_u64(&slots[j]);
+        ++spins;
+      }
+      if (static_cast<uint32_t>(w >> 32) != epoch ||
+          ((w >> 30) & 3u) == kStatusEmpty) {
+        status = kStatusPoison;
+      } else {
+        status = static_cast<uint32_t>((w >> 30) & 3u);
+        value = static_cast<int64_t>(w & kValueMask);
+      }
+    }
+    const uint64_t inclusive = __ballot(status == kStatusInclusive);
+    const uint64_t poison = __ballot(status == kStatusPoison);
+    if (inclusive != 0) {
+      const int k = __ffsll(static_cast<long long>(inclusive)) - 1;
+      const uint64_t upto = (k == 63) ? ~0ull : ((2ull << k) - 1);
+      if (poison & upto) bad = true;
+      exclusive += wave_sum64(lane <= k ? value : 0);
+      break;
+    }
+    if (poison != 0) bad = true;
+    exclusive += wave_sum64(value);
+    end -= kWave;
+  }
+  if (lane == 0) {
+    atomic_store_u64(&slots[bank],
+                     slot_word(epoch, bad ? kStatusPoison : kStatusInclusive,
+                               static_cast<uint64_t>(exclusive + count)));
+  }
+  *poisoned = bad;
+  return exclusive;
+}
+
+// --------------------------------------------------------- the fused step
+
+// One wave = one bank of one layer.  DENSE selects the dense-table control
+// (allocator.py:1612-1633): rows live at values[bank, slot] and there is no
+// map, free stack or scan; the row math is shared, so packed and dense
+// results are bit-identical.
+template <typename IDX, int MAXW, int VEC, bool DENSE>
+__global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
+  const int layer_id = blockIdx.x / P.blocks_per_layer;
+  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock +
+                   static_cast<int>(threadIdx.x) / kWave;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  if (layer_id >= P.nlayers || bank >= P.banks) return;
+  const cowsdm_layer_t& L = P.layer[layer_id];
+
+  const int N = P.slots;
+  const int D = P.width;
+  const int W = P.writes;
+  const int R = P.reads;
+  const int64_t C = L.capacity_rows;
+  const int64_t b = bank;
+
+  int lane_err = 0;
+
+  // ---- per-bank scalars
+  int64_t tmpl = 0;
+  if constexpr (!DENSE) {
+    tmpl = L.template_indices[b];
+    if (tmpl < 0 || tmpl >= P.templates) lane_err |= COWSDM_ERR_TEMPLATE;
+  }
+  const float forget = L.forget_log_gate[b];
+  const float in_gate = L.input_gate[b];
+  const float er_gate = L.erase_gate[b];
+  int64_t old_free = 0;
+  uint32_t epoch = 0;
+  if constexpr (!DENSE) {
+    old_free = *L.free_count;
+    epoch = static_cast<uint32_t>(L.scratch[COWSDM_SCRATCH_EPOCH]);
+    if (old_free < 0 || old_free > C) lane_err |= COWSDM_ERR_CORRUPT;
+  }
+
+  // ---- write routes: lane w < W
+  int widx = 0;
+  float wweight = 0.0f;
+  int wphys = -1;
+  if (lane < W) {
+    const int64_t x = load_index<IDX>(L.write_indices, b * W + lane);
+    wweight = L.write_weights[b * W + lane];
+    if (x < 0 || x >= N) {
+      lane_err |= COWSDM_ERR_WRITE_INDEX;
+    } else {
+      widx = static_cast<int>(x);
+    }
+  }
+  // ---- read routes: lane l holds r = l + 64 k
+  int ridx[kMaxReadSlots];
+  float rweight[kMaxReadSlots];
+  int rphys[kMaxReadSlots];
+  int rsrc[kMaxReadSlots];
+#pragma unroll
+  for (int k = 0; k < kMaxReadSlots; ++k) {
+    ridx[k] = 0;
+    rweight[k] = 0.0f;
+    rphys[k] = -1;
+    rsrc[k] = -1;
+    const int r = k * kWave + lane;
+    if (r < R) {
+      const int64_t x = load_index<IDX>(L.read_indices, b * R + r);
+      rweight[k] = L.read_weights[b * R + r];
+      if (x < 0 || x >= N) {
+        lane_err |= COWSDM_ERR_READ_INDEX;
+      } else {
+        ridx[k] = static_cast<int>(x);
+      }
+    }
+  }
+
+  // ---- map lookups (packed) for writes and reads
+  if constexpr (!DENSE) {
+    if (lane < W && !(lane_err & COWSDM_ERR_WRITE_INDEX)) {
+      wphys = L.logical_to_physical[b * N + widx];
+      if (wphys >= C) lane_err |= COWSDM_ERR_CORRUPT;
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxReadSlots; ++k) {
+      const int r = k * kWave + lane;
+      if (r < R) {
+        rphys[k] = L.logical_to_physical[b * N + ridx[k]];
+        if (rphys[k] >= C) lane_err |= COWSDM_ERR_CORRUPT;
+      }
+    }
+  }
+
+  // ---- duplicate writes and read-after-write sources
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+    if (j < W) {
+      const int other = rl(widx, j);
+      if (lane < W && j < lane && other == widx) lane_err |= COWSDM_ERR_DUP_WRITE;
+#pragma unroll
+      for (int k = 0; k < kMaxReadSlots; ++k) {
+        if (k * kWave + lane < R && ridx[k] == other) rsrc[k] = j;
+      }
+    }
+  }
+
+  const int err = wave_or(lane_err);
+  const bool ok = (err == 0);
+  const bool first = !DENSE && lane < W && wphys < 0;
+  const uint64_t first_mask = __ballot(first);
+  const int count = ok ? __popcll(first_mask) : 0;
+  const int rank = __popcll(first_mask & ((1ull << lane) - 1));
+
+  // ---- chunk 0 row loads, issued before the cross-bank wait
+  const float alpha = static_cast<float>(exp(static_cast<double>(forget)));
+  const float* const m0_bank =
+      DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
+  float* const table_bank = DENSE ? L.values + b * N * D : nullptr;
+  const int chunk_cols = kWave * VEC;
+  const int nchunks = (D + chunk_cols - 1) / chunk_cols;
+
+  float cur[MAXW][VEC];
+  float rv[kReadBatch][VEC];
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kReadBatch; ++i) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) rv[i][v] = 0.0f;
+  }
+
+  auto write_row_src = [&](int j) -> const float* {
+    const int slot = rl(widx, j);
+    if constexpr (DENSE) {
+      return table_bank + static_cast<int64_t>(slot) * D;
+    } else {
+      const int p = rl(wphys, j);
+      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
+                   : L.values + static_cast<int64_t>(p) * D;
+    }
+  };
+  auto read_meta = [&](const int (&arr)[kMaxReadSlots], int r) -> int {
+    const int k = r / kWave;
+    const int v = k == 0 ? arr[0] : k == 1 ? arr[1] : k == 2 ? arr[2] : arr[3];
+    return rl(v, r % kWave);
+  };
+  auto read_weight = [&](int r) -> float {
+    const int k = r / kWave;
+    const float v = k == 0 ? rweight[0] : k == 1 ? rweight[1]
+                  : k == 2 ? rweight[2] : rweight[3];
+    return rlf(v, r % kWave);
+  };
+  auto read_row_src = [&](int r) -> const float* {
+    const int slot = read_meta(ridx, r);
+    if constexpr (DENSE) {
+      return table_bank + static_cast<int64_t>(slot) * D;
+    } else {
+      const int p = read_meta(rphys, r);
+      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
+                   : L.values + static_cast<int64_t>(p) * D;
+    }
+  };
+  auto load_writes = [&](int chunk) {
+    const int col = chunk * chunk_cols + lane * VEC;
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) {
+      if (j < W && ok) {
+        const float* src = write_row_src(j);
+        if (col < D) load_row<VEC>(src + col, cur[j]);
+      }
+    }
+  };
+  auto load_read_batch = [&](int chunk, int r0) {
+    const int col = chunk * chunk_cols + lane * VEC;
+#pragma unroll
+    for (int i = 0; i < kReadBatch; ++i) {
+      const int r = r0 + i;
+      if (r < R && ok && read_meta(rsrc, r) < 0) {
+        const float* src = read_row_src(r);
+        if (col < D) load_row<VEC>(src + col, rv[i]);
+      }
+    }
+  };
+
+  load_writes(0);
+  load_read_batch(0, 0);
+
+  // ---- free-stack resolution (packed): bank-major pop positions
+  bool fits = true;
+  int new_row = -1;
+  if constexpr (!DENSE) {
+    bool poisoned = false;
+    int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
+    const int64_t prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
+    fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
+    int bad_row = 0;
+    if (fits && first) {
+      const int64_t pos = old_free - 1 - (prefix + rank);
+      new_row = L.free_rows[pos];
+      if (new_row < 0 || new_row >= C) bad_row = 1;
+    }
+    if (__ballot(bad_row) != 0) {
+      fits = false;
+      if (lane == 0) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_CORRUPT),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (lane == 0) {
+      if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
+      if (poisoned) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  const bool commit = ok && fits;
+  const int dest = DENSE ? widx : (first ? new_row : wphys);
+
+  // ---- gated-delta update and sparse read, chunk by chunk
+  for (int chunk = 0; chunk < nchunks; ++chunk) {
+    if (chunk > 0) {
+      load_writes(chunk);
+      load_read_batch(chunk, 0);
+    }
+    const int col = chunk * chunk_cols + lane * VEC;
+    const bool col_ok = col < D;
+    float vin[VEC];
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) { vin[v] = 0.0f; acc[v] = 0.0f; }
+    if (col_ok) load_row<VEC>(L.step_values + b * D + col, vin);
+
+    if (ok) {
+      // decayed = current * exp(forget); retrieved = sum_w weight_w * decayed_w
+      float ret[VEC];
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const float wj = rlf(wweight, j);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            cur[j][v] = cur[j][v] * alpha;
+            const float term = wj * cur[j][v];
+            ret[v] = (j == 0) ? term : ret[v] + term;
+          }
+        }
+      }
+      // delta = in_gate * value - erase_gate * retrieved
+      // updated_w = decayed_w + weight_w * delta
+      float delta[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float a = in_gate * vin[v];
+        const float e = er_gate * ret[v];
+        delta[v] = a - e;
+      }
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const float wj = rlf(wweight, j);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float t = wj * delta[v];
+            cur[j][v] = cur[j][v] + t;
+          }
+        }
+      }
+      // reading = sum_r weight_r * visible_r, reads after this step's writes
+      for (int r0 = 0; r0 < R; r0 += kReadBatch) {
+        if (r0 > 0) load_read_batch(chunk, r0);
+#pragma unroll
+        for (int i = 0; i < kReadBatch; ++i) {
+          const int r = r0 + i;
+          if (r < R) {
+            const int src = read_meta(rsrc, r);
+            float x[VEC];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) x[v] = rv[i][v];
+            if (src >= 0) {
+#pragma unroll
+              for (int j = 0; j < MAXW; ++j) {
+                if (j == src) {
+#pragma unroll
+                  for (int v = 0; v < VEC; ++v) x[v] = cur[j][v];
+                }
+              }
+            }
+            const float wr = read_weight(r);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+              const float term = wr * x[v];
+              acc[v] = (r == 0) ? term : acc[v] + term;
+            }
+          }
+        }
+      }
+    }
+    if (col_ok) store_row<VEC>(L.output + b * D + col, acc);
+    if (commit) {
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const int row = rl(dest, j);
+          float* dst = DENSE ? table_bank + static_cast<int64_t>(row) * D
+                             : L.values + static_cast<int64_t>(row) * D;
+          if (col_ok) store_row<VEC>(dst + col, cur[j]);
+        }
+      }
+    }
+  }
+
+  if constexpr (!DENSE) {
+    if (commit && first) L.logical_to_physical[b * N + widx] = new_row;
+    if (lane == 0) {
+      if (L.first_touches_out) L.first_touches_out[b] = commit ? count : 0;
+      if (L.repeated_writes_out) L.repeated_writes_out[b] = commit ? W - count : W;
+      if (err) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(err), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (commit && count > 0) {
+        __hip_atomic_fetch_add(&L.scratch[COWSDM_SCRATCH_SERVED],
+                               static_cast<int64_t>(count), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const int64_t ticket = __hip_atomic_fetch_add(
+          &L.scratch[COWSDM_SCRATCH_TICKET], int64_t{1}, __ATOMIC_ACQ_REL,
+          __HIP_MEMORY_SCOPE_AGENT);
+      if (ticket == P.banks - 1) {
+        const int64_t served = __hip_atomic_load(
+            &L.scratch[COWSDM_SCRATCH_SERVED], __ATOMIC_ACQUIRE,
+            __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t now_free = old_free - served;
+        *L.free_count = static_cast<int32_t>(now_free);
+        if (L.allocated_rows_out) {
+          *L.allocated_rows_out = static_cast<int32_t>(C - now_free);
+        }
+        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_SERVED], 0);
+        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_TICKET], 0);
+        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_EPOCH],
+                         static_cast<uint64_t>(epoch + 1u));
+      }
+    }
+  } else {
+    if (lane == 0 && err && L.scratch) {
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(err), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Validation before a step (validate_routes=True, or a packed state whose
+// capacity has no proof): bounds, duplicate writes, first touches vs the
+// free stack.  One workgroup; writes its result word once.
+template <typename IDX>
+__global__ __launch_bounds__(1024) void precheck_kernel(
+    cowsdm_layer_t L, int32_t banks, int32_t slots, int32_t writes,
+    int32_t reads, int32_t dense, int32_t check_unique, int32_t check_capacity,
+    int64_t* result) {
+  __shared__ int s_flags;
+  __shared__ unsigned long long s_first;
+  if (threadIdx.x == 0) { s_flags = 0; s_first = 0; }
+  __syncthreads();
+  int flags = 0;
+  unsigned long long first = 0;
+  const int64_t nw = static_cast<int64_t>(banks) * writes;
+  const int64_t C = L.capacity_rows;
+  for (int64_t e = threadIdx.x; e < nw; e += blockDim.x) {
+    const int64_t b = e / writes;
+    const int64_t w = e % writes;
+    const int64_t x = load_index<IDX>(L.write_indices, e);
+    if (x < 0 || x >= slots) { flags |= COWSDM_ERR_WRITE_INDEX; continue; }
+    if (check_unique) {
+      for (int64_t w2 = 0; w2 < w; ++w2) {
+        if (load_index<IDX>(L.write_indices, b * writes + w2) == x) {
+          flags |= COWSDM_ERR_DUP_WRITE;
+        }
+      }
+    }
+    if (check_capacity && !dense) {
+      const int p = L.logical_to_physical[b * slots + x];
+      if (p < 0) ++first;
+      else if (p >= C) flags |= COWSDM_ERR_CORRUPT;
+    }
+  }
+  const int64_t nr = static_cast<int64_t>(banks) * reads;
+  for (int64_t e = threadIdx.x; e < nr; e += blockDim.x) {
+    const int64_t x = load_index<IDX>(L.read_indices, e);
+    if (x < 0 || x >= slots) flags |= COWSDM_ERR_READ_INDEX;
+  }
+  if (flags) atomicOr(&s_flags, flags);
+  if (first) atomicAdd(&s_first, first);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int out = s_flags;
+    if (check_capacity && !dense) {
+      const int64_t f = *L.free_count;
+      if (static_cast<int64_t>(s_first) > f) out |= COWSDM_ERR_EXHAUSTED;
+    }
+    *result = out;
+  }
+}
+
+// ------------------------------------------------------------ lifecycle
+
+__global__ void init_state_kernel(int32_t* map, int64_t map_entries,
+                                  int32_t* free_rows, int64_t capacity,
+                                  int32_t* free_count, int32_t* overflow,
+                                  int64_t* scratch, int64_t scratch_words) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = t0; i < map_entries; i += stride) map[i] = -1;
+  for (int64_t i = t0; i < capacity; i += stride) free_rows[i] = static_cast<int32_t>(i);
+  for (int64_t i = t0; i < scratch_words; i += stride) scratch[i] = 0;
+  if (t0 == 0) {
+    *free_count = static_cast<int32_t>(capacity);
+    *overflow = 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void check_templates_kernel(
+    const int64_t* tmpl, int64_t banks, int64_t templates, int64_t* result) {
+  __shared__ int s_bad;
+  if (threadIdx.x == 0) s_bad = 0;
+  __syncthreads();
+  int bad = 0;
+  for (int64_t i = threadIdx.x; i < banks; i += blockDim.x) {
+    if (tmpl[i] < 0 || tmpl[i] >= templates) bad = 1;
+  }
+  if (bad) atomicOr(&s_bad, 1);
+  __syncthreads();
+  if (threadIdx.x == 0) *result = s_bad ? COWSDM_ERR_TEMPLATE : 0;
+}
+
+// Row copy dst[dst_rows[i]] = src[src_rows[i]] for i < *count (null row
+// lists mean identity); float4 when the width allows it.
+__global__ void copy_rows_kernel(float* dst, const int32_t* dst_rows,
+                                 const float* src, const int32_t* src_rows,
+                                 const int64_t* count_ptr, int64_t count_max,
+                                 int64_t width) {
+  int64_t count = count_ptr ? *count_ptr : count_max;
+  if (count > count_max) count = count_max;
+  const bool v4 = (width % 4) == 0;
+  const int64_t per_row = v4 ? width / 4 : width;
+  const int64_t total = count * per_row;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < total; i += stride) {
+    const int64_t row = i / per_row;
+    const int64_t c = i % per_row;
+    const int64_t s = src_rows ? src_rows[row] : row;
+    const int64_t d = dst_rows ? dst_rows[row] : row;
+    if (s < 0 || d < 0) continue;
+    if (v4) {
+      reinterpret_cast<float4*>(dst + d * width)[c] =
+          reinterpret_cast<const float4*>(src + s * width)[c];
+    } else {
+      dst[d * width + c] = src[s * width + c];
+    }
+  }
+}
+
+__global__ void copy_i64_kernel(int64_t* dst, const int64_t* src, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n; i += stride) {
+    dst[i] = src[i];
+  }
+}
+
+__global__ void grow_free_kernel(const int32_t* old_free_rows,
+                                 int32_t* new_free_rows,
+                                 const int32_t* free_count,
+                                 int64_t old_capacity, int64_t new_capacity) {
+  const int64_t f = *free_count;
+  const int64_t added = new_capacity - old_capacity;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (f < 0 || f > old_capacity) return;
+  for (int64_t i = t0; i < f; i += stride) new_free_rows[i] = old_free_rows[i];
+  for (int64_t j = t0; j < added; j += stride) {
+    new_free_rows[f + j] = static_cast<int32_t>(old_capacity + j);
+  }
+}
+
+__global__ void add_counter_kernel(int32_t* counter, int64_t delta,
+                                   const int64_t* delta_ptr, int32_t sign,
+                                   int32_t* clear) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int64_t d = delta_ptr ? *delta_ptr : delta;
+    *counter = static_cast<int32_t>(*counter + sign * d);
+    if (clear) *clear = 0;
+  }
+}
+
+// Workspace for ranking passes.
+struct Workspace {
+  int64_t* total;       // [1]
+  int64_t* aux;         // [7] scratch words
+  int32_t* tile_count;  // [ntiles]
+  int32_t* tile_offset; // [ntiles]
+  int32_t* list_a;      // [rows]
+  int32_t* list_b;      // [rows]
+};
+
+int64_t num_tiles(int64_t entries) { return (entries + kTile - 1) / kTile; }
+
+int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+Workspace carve(void* base, int64_t entries, int64_t rows) {
+  char* p = static_cast<char*>(base);
+  Workspace w;
+  w.total = reinterpret_cast<int64_t*>(p);
+  w.aux = reinterpret_cast<int64_t*>(p) + 1;
+  p += 256;
+  const int64_t nt = num_tiles(entries);
+  w.tile_count = reinterpret_cast<int32_t*>(p);
+  p += align_up(nt * 4, 256);
+  w.tile_offset = reinterpret_cast<int32_t*>(p);
+  p += align_up(nt * 4, 256);
+  w.list_a = reinterpret_cast<int32_t*>(p);
+  p += align_up(rows * 4, 256);
+  w.list_b = reinterpret_cast<int32_t*>(p);
+  return w;
+}
+
+// Predicate source of a ranking: row `i` of the ranked order is map row
+// bank_list[i] (or i), or the mask row i.
+struct RankSource {
+  const int32_t* map;
+  const int64_t* bank_list;
+  const uint8_t* mask;
+  int64_t slots;
+  int64_t entries;
+  int64_t banks;  // rows of `map`; listed rows outside [0, banks) are empty
+};
+
+__device__ __forceinline__ int64_t rank_row(const RankSource& s, int64_t e) {
+  const int64_t i = e / s.slots;
+  const int64_t row = s.bank_list ? s.bank_list[i] : i;
+  return (row >= 0 && row < s.banks) ? row : -1;
+}
+
+__device__ __forceinline__ bool rank_active(const RankSource& s, int64_t e) {
+  if (s.mask) return s.mask[e] != 0;
+  const int64_t row = rank_row(s, e);
+  return row >= 0 && s.map[row * s.slots + e % s.slots] >= 0;
+}
+
+__global__ __launch_bounds__(kTileThreads) void rank_count_kernel(
+    RankSource s, int32_t* tile_count) {
+  __shared__ int s_sum;
+  if (threadIdx.x == 0) s_sum = 0;
+  __syncthreads();
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile + threadIdx.x * kPerThread;
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int64_t e = base + k;
+    if (e < s.entries && rank_active(s, e)) ++c;
+  }
+  if (c) atomicAdd(&s_sum, c);
+  __syncthreads();
+  if (threadIdx.x == 0) tile_count[blockIdx.x] = s_sum;
+}
+
+// Exclusive scan of tile counts by one workgroup; writes the total.
+__global__ __launch_bounds__(1024) void rank_scan_kernel(
+    const int32_t* tile_count, int32_t* tile_offset, int64_t ntiles,
+    int64_t* total) {
+  __shared__ int64_t s_part[1024];
+  const int64_t per = (ntiles + blockDim.x - 1) / blockDim.x;
+  const int64_t lo = threadIdx.x * per;
+  const int64_t hi = lo + per < ntiles ? lo + per : ntiles;
+  int64_t sum = 0;
+  for (int64_t i = lo; i < hi; ++i) sum += tile_count[i];
+  s_part[threadIdx.x] = sum;
+  __syncthreads();
+  for (int o = 1; o < static_cast<int>(blockDim.x); o <<= 1) {
+    const int64_t v = threadIdx.x >= static_cast<unsigned>(o) ? s_part[threadIdx.x - o] : 0;
+    __syncthreads();
+    s_part[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int64_t run = s_part[threadIdx.x] - sum;
+  for (int64_t i = lo; i < hi; ++i) {
+    tile_offset[i] = static_cast<int32_t>(run);
+    run += tile_count[i];
+  }
+  if (threadIdx.x == blockDim.x - 1) *total = s_part[threadIdx.x];
+}
+
+enum RankOp : int32_t {
+  kOpPack = 0,     // from_dense_overlay
+  kOpTrim = 1,     // trim_capacity
+  kOpAppend = 2,   // append_banks_from
+  kOpRelease = 3,  // release
+};
+
+struct RankApply {
+  int32_t op;
+  int32_t* map_out;          // pack: state map; trim/append: new map
+  const int32_t* free_rows;  // append: pop source
+  int32_t* free_rows_out;    // release: push target
+  const int32_t* counter;    // append/release: free_count before the op
+  int64_t capacity;          // rows of the slab that receives rows
+  int64_t map_row_offset;    // append: first admitted bank in new map
+  int32_t* list_a;           // gather source rows
+  int32_t* list_b;           // scatter destination rows (append)
+  int64_t list_rows;         // entries list_a / list_b can hold
+  int64_t src_capacity;      // trim/append: rows of the slab read from
+  int32_t* map_clear;        // release: map whose listed rows become -1
+};
+
+// Rank each active entry in ranked order and apply the operation.
+__global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
+    RankSource s, const int32_t* tile_offset, RankApply a) {
+  __shared__ int s_scan[kTileThreads];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile + threadIdx.x * kPerThread;
+  bool act[kPerThread];
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int64_t e = base + k;
+    act[k] = e < s.entries && rank_active(s, e);
+    c += act[k] ? 1 : 0;
+  }
+  s_scan[threadIdx.x] = c;
+  __syncthreads();
+  for (int o = 1; o < kTileThreads; o <<= 1) {
+    const int v = threadIdx.x >= static_cast<unsigned>(o) ? s_scan[threadIdx.x - o] : 0;
+    __syncthreads();
+    s_scan[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int64_t rank = static_cast<int64_t>(tile_offset[blockIdx.x]) + s_scan[threadIdx.x] - c;
+  const int64_t counter = a.counter ? *a.counter : 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int64_t e = base + k;
+    if (e >= s.entries) break;
+    const int64_t slot = e % s.slots;
+    const int64_t row = s.mask ? e / s.slots : rank_row(s, e);
+    const int64_t at = row * s.slots + slot;
+    // live source row of a map entry, -1 when outside the source slab
+    int32_t src = -1;
+    if (act[k] && !s.mask) {
+      src = s.map[at];
+      if (src >= a.src_capacity) src = -1;
+    }
+    switch (a.op) {
+      case kOpPack:
+        a.map_out[e] = act[k] ? static_cast<int32_t>(rank) : -1;
+        if (act[k] && rank < a.list_rows) a.list_a[rank] = static_cast<int32_t>(e);
+        break;
+      case kOpTrim:
+        if (act[k]) {
+          if (rank < a.list_rows) a.list_a[rank] = src;
+          a.map_out[e] = static_cast<int32_t>(rank);
+        } else {
+          a.map_out[e] = -1;
+        }
+        break;
+      case kOpAppend: {
+        int32_t dst = -1;
+        if (act[k]) {
+          const int64_t pos = counter - 1 - rank;
+          if (pos >= 0 && pos < a.capacity) {
+            dst = a.free_rows[pos];
+            if (dst < 0 || dst >= a.capacity) dst = -1;
+          }
+          if (rank < a.list_rows) {
+            a.list_a[rank] = src;
+            a.list_b[rank] = dst;
+          }
+        }
+        a.map_out[a.map_row_offset * s.slots + e] = dst;
+        break;
+      }
+      case kOpRelease:
+        if (row < 0) break;
+        if (act[k]) {
+          const int64_t pos = counter + rank;
+          if (pos >= 0 && pos < a.capacity) a.free_rows_out[pos] = s.map[at];
+        }
+        a.map_clear[at] = -1;
+        break;
+      default:
+        break;
+    }
+    if (act[k]) ++rank;
+  }
+}
+
+// free_rows[i] = A + i for i < capacity - A; free_count = capacity - A.
+__global__ void fill_free_tail_kernel(int32_t* free_rows, int64_t capacity,
+                                      const int64_t* live, int32_t* free_count,
+                                      int32_t* overflow) {
+  const int64_t a = *live;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = t0; i < capacity - a; i += stride) {
+    free_rows[i] = static_cast<int32_t>(a + i);
+  }
+  if (t0 == 0) {
+    *free_count = static_cast<int32_t>(capacity - a);
+    if (overflow) *overflow = 0;
+  }
+}
+
+__global__ void copy_i32_kernel(int32_t* dst, const int32_t* src, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n; i += stride) {
+    dst[i] = src[i];
+  }
+}
+
+__global__ void gather_banks_kernel(const int32_t* map, const int64_t* tmpl,
+                                    int64_t banks, int64_t slots, const int64_t* bank_list,
+                                    int64_t nsel, int32_t* new_map,
+                                    int64_t* new_tmpl, const int64_t* tmpl_b,
+                                    int64_t nb) {
+  // new rows 0..nsel-1 gather map rows bank_list[i]; when tmpl_b is set,
+  // new_tmpl = [tmpl[list] ; tmpl_b[0..nb)].
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (map) {
+    for (int64_t e = t0; e < nsel * slots; e += stride) {
+      const int64_t i = e / slots;
+      const int64_t src = bank_list ? bank_list[i] : i;
+      new_map[e] = (src >= 0 && src < banks) ? map[src * slots + e % slots] : -1;
+    }
+  }
+  for (int64_t i = t0; i < nsel; i += stride) {
+    const int64_t src = bank_list ? bank_list[i] : i;
+    new_tmpl[i] = (src >= 0 && src < banks) ? tmpl[src] : 0;
+  }
+  if (tmpl_b) {
+    for (int64_t i = t0; i < nb; i += stride) new_tmpl[nsel + i] = tmpl_b[i];
+  }
+}
+
+__global__ void zero_i64_kernel(int64_t* p, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n; i += stride) {
+    p[i] = 0;
+  }
+}
+
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n; i += stride) {
+    p[i] = 0;
+  }
+}
+
+__global__ void mark_banks_kernel(const int64_t* bank_list, int64_t nsel,
+                                  int64_t banks, int32_t* marks,
+                                  int64_t* result) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < nsel; i += stride) {
+    const int64_t b = bank_list[i];
+    if (b < 0 || b >= banks) {
+      atomicOr(reinterpret_cast<unsigned long long*>(result), 1ull);
+    } else if (atomicAdd(&marks[b], 1) != 0) {
+      atomicOr(reinterpret_cast<unsigned long long*>(result), 1ull);
+    }
+  }
+}
+
+__global__ void discarded_live_kernel(const int32_t* map, int64_t banks,
+                                      int64_t slots, const int32_t* marks,
+                                      int64_t* result) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  int found = 0;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       e < banks * slots; e += stride) {
+    if (marks[e / slots] == 0 && map[e] >= 0) found = 1;
+  }
+  if (found) atomicOr(reinterpret_cast<unsigned long long*>(result), 2ull);
+}
+
+__global__ void materialize_kernel(const float* m0, int64_t templates, const int64_t* tmpl,
+                                   const float* values, const int32_t* map,
+                                   int64_t banks, int64_t slots, int64_t width,
+                                   int64_t capacity, float* dense) {
+  const bool v4 = (width % 4) == 0;
+  const int64_t per_row = v4 ? width / 4 : width;
+  const int64_t total = banks * slots * per_row;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < total; i += stride) {
+    const int64_t row = i / per_row;  // b * slots + n
+    const int64_t c = i % per_row;
+    const int64_t b = row / slots;
+    const int64_t n = row % slots;
+    const int32_t p = map[row];
+    int64_t t = tmpl[b];
+    if (t < 0 || t >= templates) t = 0;
+    const float* src = (p >= 0 && p < capacity)
+                           ? values + static_cast<int64_t>(p) * width
+                           : m0 + (t * slots + n) * width;
+    if (v4) {
+      reinterpret_cast<float4*>(dense + row * width)[c] =
+          reinterpret_cast<const float4*>(src)[c];
+    } else {
+      dense[row * width + c] = src[c];
+    }
+  }
+}
+
+// Partition check: counts[row] += 1 per live owner and += 1<<16 per free
+// stack entry; stats as documented in cowsdm.h.
+__global__ void own_map_kernel(const int32_t* map, int64_t entries,
+                               int64_t capacity, int32_t* counts,
+                               int64_t* stats) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  unsigned long long live = 0, outside = 0;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       e < entries; e += stride) {
+    const int32_t p = map[e];
+    if (p < 0) continue;
+    ++live;
+    if (p >= capacity) { ++outside; continue; }
+    atomicAdd(&counts[p], 1);
+  }
+  if (live) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[0]), live);
+  if (outside) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), outside);
+}
+
+__global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_count,
+                                int64_t capacity, int32_t* counts, int64_t* stats) {
+  int64_t f = *free_count;
+  if (f < 0) f = 0;
+  if (f > capacity) f = capacity;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  unsigned long long outside = 0;
+  for (int64_t i = t0; i < f; i += stride) {
+    const int32_t p = free_rows[i];
+    if (p < 0 || p >= capacity) { ++outside; continue; }
+    atomicAdd(&counts[p], 1 << 16);
+  }
+  if (outside) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), outside);
+  if (t0 == 0) stats[1] = f;
+}
+
+__global__ void own_eval_kernel(const int32_t* counts, int64_t capacity,
+                                const int32_t* overflow, const int64_t* scratch,
+                                int64_t* stats) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  unsigned long long dup_live = 0, dup_free = 0, not_once = 0;
+  for (int64_t i = t0; i < capacity; i += stride) {
+    const int32_t c = counts[i];
+    const int32_t owners = c & 0xffff;
+    const int32_t frees = c >> 16;
+    if (owners > 1) ++dup_live;
+    if (frees > 1) ++dup_free;
+    if (owners + frees != 1) ++not_once;
+  }
+  if (dup_live) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[2]), dup_live);
+  if (dup_free) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[3]), dup_free);
+  if (not_once) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), not_once);
+  if (t0 == 0) {
+    stats[6] = *overflow;
+    stats[7] = scratch ? scratch[COWSDM_SCRATCH_ERRORS] : 0;
+  }
+}
+
+template <typename IDX>
+__global__ void mark_written_kernel(uint8_t* mask, int64_t banks, int64_t slots,
+                                    const void* idx, int64_t per_bank,
+                                    int64_t* result) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  int bad = 0;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       e < banks * per_bank; e += stride) {
+    const int64_t x = load_index<IDX>(idx, e);
+    if (x < 0 || x >= slots) { bad = 1; continue; }
+    mask[(e / per_bank) * slots + x] = 1;
+  }
+  if (bad && result) atomicOr(reinterpret_cast<unsigned long long*>(result), 2ull);
+}
+
+// ------------------------------------------------------------ host helpers
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int grid_for(int64_t work, int threads, int cap = 8192) {
+  int64_t g = (work + threads - 1) / threads;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<int>(g);
+}
+
+int32_t check_shape(const cowsdm_shape_t* s) {
+  if (!s) return fail(COWSDM_EARG, "shape is null");
+  if (s->banks < 0 || s->slots <= 0 || s->width <= 0 || s->writes <= 0 ||
+      s->reads <= 0) {
+    return fail(COWSDM_EARG, "invalid step shape (B=%lld N=%lld D=%lld W=%lld R=%lld)",
+                (long long)s->banks, (long long)s->slots, (long long)s->width,
+                (long long)s->writes, (long long)s->reads);
+  }
+  if (s->writes > 64 || s->reads > kMaxReadSlots * kWave) {
+    return fail(COWSDM_ELIMIT, "step supports W <= 64 and R <= 256 (got W=%lld R=%lld)",
+                (long long)s->writes, (long long)s->reads);
+  }
+  if (s->slots >= (1ll << 31) || s->banks >= (1ll << 31) ||
+      s->banks * s->writes >= (1ll << 30)) {
+    return fail(COWSDM_ELIMIT, "step sizes exceed 32-bit index ranges");
+  }
+  if (s->index_dtype != COWSDM_INDEX_INT32 && s->index_dtype != COWSDM_INDEX_INT64) {
+    return fail(COWSDM_EARG, "index_dtype must be COWSDM_INDEX_INT32 or _INT64");
+  }
+  return 0;
+}
+
+int32_t check_layer(const cowsdm_layer_t& L, bool dense) {
+  if (!L.values || !L.write_indices || !L.write_weights || !L.step_values ||
+      !L.input_gate || !L.erase_gate || !L.forget_log_gate ||
+      !L.read_indices || !L.read_weights || !L.output) {
+    return fail(COWSDM_EARG, "null tensor pointer in step layer");
+  }
+  if (!dense) {
+    if (!L.shared_initial_memory || !L.template_indices ||
+        !L.logical_to_physical || !L.free_rows || !L.free_count ||
+        !L.overflow_flag || !L.scratch) {
+      return fail(COWSDM_EARG, "null state pointer in packed step layer");
+    }
+    if (L.capacity_rows <= 0 || L.capacity_rows >= (1ll << 31)) {
+      return fail(COWSDM_EARG, "capacity_rows must be in [1, 2^31)");
+    }
+  }
+  return 0;
+}
+
+template <typename IDX, int MAXW, int VEC, bool DENSE>
+void launch_step(const StepParams& P, int blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((sdm_step_kernel<IDX, MAXW, VEC, DENSE>), dim3(blocks),
+                     dim3(kStepThreads), 0, stream, P);
+}
+
+template <typename IDX, int MAXW, bool DENSE>
+void launch_step_vec(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+  if (vec == 4) launch_step<IDX, MAXW, 4, DENSE>(P, blocks, stream);
+  else if (vec == 2) launch_step<IDX, MAXW, 2, DENSE>(P, blocks, stream);
+  else launch_step<IDX, MAXW, 1, DENSE>(P, blocks, stream);
+}
+
+template <typename IDX, bool DENSE>
+void launch_step_w(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+  if (P.writes <= 4) launch_step_vec<IDX, 4, DENSE>(P, blocks, vec, stream);
+  else if (P.writes <= 16) launch_step_vec<IDX, 16, DENSE>(P, blocks, vec, stream);
+  else launch_step_vec<IDX, 64, DENSE>(P, blocks, vec, stream);
+}
+
+int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
+                 const cowsdm_shape_t* shape, bool dense, hipStream_t stream) {
+  if (int32_t e = check_shape(shape)) return e;
+  if (!layers || nlayers <= 0) return fail(COWSDM_EARG, "no layers given");
+  for (int32_t i = 0; i < nlayers; ++i) {
+    if (int32_t e = check_layer(layers[i], dense)) return e;
+  }
+  if (shape->banks == 0) return 0;
+  if (!dense && (shape->templates <= 0 || shape->templates >= (1ll << 31))) {
+    return fail(COWSDM_EARG, "templates must be positive");
+  }
+  const int64_t D = shape->width;
+  int vec = (D % 4 == 0 && D >= 4 * kWave) ? 4 : (D % 2 == 0 ? 2 : 1);
+  // float2/float4 lanes need every row pointer aligned to the vector size
+  for (int32_t i = 0; i < nlayers; ++i) {
+    const cowsdm_layer_t& L = layers[i];
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(L.values) |
+                           reinterpret_cast<uintptr_t>(L.step_values) |
+                           reinterpret_cast<uintptr_t>(L.output) |
+                           (dense ? 0 : reinterpret_cast<uintptr_t>(L.shared_initial_memory));
+    while (vec > 1 && (bits % (4u * vec)) != 0) vec /= 2;
+  }
+  StepParams P;
+  P.banks = static_cast<int32_t>(shape->banks);
+  P.slots = static_cast<int32_t>(shape->slots);
+  P.width = static_cast<int32_t>(shape->width);
+  P.writes = static_cast<int32_t>(shape->writes);
+  P.reads = static_cast<int32_t>(shape->reads);
+  P.templates = static_cast<int32_t>(dense ? 1 : shape->templates);
+  P.blocks_per_layer = static_cast<int32_t>((shape->banks + kBanksPerBlock - 1) / kBanksPerBlock);
+  for (int32_t start = 0; start < nlayers; start += kMaxLayers) {
+    const int32_t n = (nlayers - start) < kMaxLayers ? (nlayers - start) : kMaxLayers;
+    P.nlayers = n;
+    for (int32_t i = 0; i < kMaxLayers; ++i) P.layer[i] = layers[start + (i < n ? i : 0)];
+    const int blocks = P.blocks_per_layer * n;
+    const bool i64 = shape->index_dtype == COWSDM_INDEX_INT64;
+    if (dense) {
+      if (i64) launch_step_w<int64_t, true>(P, blocks, vec, stream);
+      else launch_step_w<int32_t, true>(P, blocks, vec, stream);
+    } else {
+      if (i64) launch_step_w<int64_t, false>(P, blocks, vec, stream);
+      else launch_step_w<int32_t, false>(P, blocks, vec, stream);
+    }
+    if (int32_t e = launch_status(dense ? "dense step" : "packed step")) return e;
+  }
+  return 0;
+}
+
+int32_t rank_count(const RankSource& src, const Workspace& ws, hipStream_t stream) {
+  const int64_t nt = num_tiles(src.entries);
+  if (nt == 0) {
+    hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, stream, ws.total, int64_t{1});
+    return launch_status("count (empty)");
+  }
+  hipLaunchKernelGGL(rank_count_kernel, dim3(static_cast<unsigned>(nt)), dim3(kTileThreads),
+                     0, stream, src, ws.tile_count);
+  if (int32_t e = launch_status("rank count")) return e;
+  hipLaunchKernelGGL(rank_scan_kernel, dim3(1), dim3(1024), 0, stream, ws.tile_count,
+                     ws.tile_offset, nt, ws.total);
+  return launch_status("rank scan");
+}
+
+int32_t rank_apply(const RankSource& src, const Workspace& ws, const RankApply& a,
+                   hipStream_t stream) {
+  const int64_t nt = num_tiles(src.entries);
+  if (nt == 0) return 0;
+  hipLaunchKernelGGL(rank_apply_kernel, dim3(static_cast<unsigned>(nt)), dim3(kTileThreads),
+                     0, stream, src, ws.tile_offset, a);
+  return launch_status("rank apply");
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" {
+
+int32_t cowsdm_abi_version(void) { return COWSDM_ABI_VERSION; }
+
+const char* cowsdm_last_error_string(void) { return g_error; }
+
+int64_t cowsdm_step_scratch_words(int64_t banks) {
+  return banks < 0 ? -1 : COWSDM_SCRATCH_SLOTS + banks;
+}
+
+int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows) {
+  if (entries < 0 || capacity_rows < 0) return -1;
+  const int64_t nt = num_tiles(entries);
+  return 256 + 2 * align_up(nt * 4, 256) + 2 * align_up(capacity_rows * 4, 256);
+}
+
+int32_t cowsdm_packed_step(const cowsdm_layer_t* layer, const cowsdm_shape_t* shape,
+                           void* stream) {
+  return run_step(layer, 1, shape, false, as_stream(stream));
+}
+
+int32_t cowsdm_packed_step_layers(const cowsdm_layer_t* layers, int32_t nlayers,
+                                  const cowsdm_shape_t* shape, void* stream) {
+  return run_step(layers, nlayers, shape, false, as_stream(stream));
+}
+
+int32_t cowsdm_dense_step(const cowsdm_layer_t* layer, const cowsdm_shape_t* shape,
+                          void* stream) {
+  return run_step(layer, 1, shape, true, as_stream(stream));
+}
+
+int32_t cowsdm_dense_step_layers(const cowsdm_layer_t* layers, int32_t nlayers,
+                                 const cowsdm_shape_t* shape, void* stream) {
+  return run_step(layers, nlayers, shape, true, as_stream(stream));
+}
+
+int32_t cowsdm_step_precheck(const cowsdm_layer_t* layer, const cowsdm_shape_t* shape,
+                             int32_t dense, int32_t check_unique,
+                             int32_t check_capacity, int64_t* result, void* stream) {
+  if (int32_t e = check_shape(shape)) return e;
+  if (!layer || !result) return fail(COWSDM_EARG, "precheck: null argument");
+  if (!layer->write_indices || !layer->read_indices) {
+    return fail(COWSDM_EARG, "precheck: null route indices");
+  }
+  if (check_capacity && !dense &&
+      (!layer->logical_to_physical || !layer->free_count)) {
+    return fail(COWSDM_EARG, "precheck: capacity check needs map and free_count");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int32_t B = static_cast<int32_t>(shape->banks);
+  const int32_t N = static_cast<int32_t>(shape->slots);
+  const int32_t W = static_cast<int32_t>(shape->writes);
+  const int32_t R = static_cast<int32_t>(shape->reads);
+  if (shape->index_dtype == COWSDM_INDEX_INT64) {
+    hipLaunchKernelGGL(precheck_kernel<int64_t>, dim3(1), dim3(1024), 0, s, *layer, B, N,
+                       W, R, dense, check_unique, check_capacity, result);
+  } else {
+    hipLaunchKernelGGL(precheck_kernel<int32_t>, dim3(1), dim3(1024), 0, s, *layer, B, N,
+                       W, R, dense, check_unique, check_capacity, result);
+  }
+  return launch_status("step precheck");
+}
+
+int32_t cowsdm_init_state(int32_t* map, int64_t banks, int64_t slots, int32_t* free_rows,
+                          int64_t capacity_rows, int32_t* free_count, int32_t* overflow_flag,
+                          int64_t* scratch, int64_t scratch_words,
+                          const int64_t* template_indices, int64_t templates,
+                          int64_t* result, void* stream) {
+  if (banks < 0 || slots <= 0 || capacity_rows <= 0 || scratch_words < 0) {
+    return fail(COWSDM_EARG, "init_state: invalid sizes");
+  }
+  if ((banks > 0 && !map) || !free_rows || !free_count || !overflow_flag ||
+      (scratch_words > 0 && !scratch)) {
+    return fail(COWSDM_EARG, "init_state: null pointer");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t work = banks * slots > capacity_rows ? banks * slots : capacity_rows;
+  hipLaunchKernelGGL(init_state_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, map,
+                     banks * slots, free_rows, capacity_rows, free_count, overflow_flag,
+                     scratch, scratch_words);
+  if (int32_t e = launch_status("init_state")) return e;
+  if (result) {
+    if (banks > 0 && !template_indices) return fail(COWSDM_EARG, "init_state: null templates");
+    hipLaunchKernelGGL(check_templates_kernel, dim3(1), dim3(256), 0, s, template_indices,
+                       banks, templates, result);
+    return launch_status("check templates");
+  }
+  return 0;
+}
+
+int32_t cowsdm_grow(const float* old_values, int64_t old_capacity, float* new_values,
+                    int64_t new_capacity, int64_t width, const int32_t* old_free_rows,
+                    int32_t* new_free_rows, int32_t* free_count, int32_t* overflow_flag,
+                    void* stream) {
+  if (!old_values || !new_values || !old_free_rows || !new_free_rows || !free_count ||
+      !overflow_flag || old_capacity <= 0 || new_capacity < old_capacity || width <= 0) {
+    return fail(COWSDM_EARG, "grow: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t vecs = old_capacity * (width % 4 == 0 ? width / 4 : width);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s,
+                     new_values, static_cast<const int32_t*>(nullptr), old_values,
+                     static_cast<const int32_t*>(nullptr), static_cast<const int64_t*>(nullptr),
+                     old_capacity, width);
+  if (int32_t e = launch_status("grow copy")) return e;
+  hipLaunchKernelGGL(grow_free_kernel, dim3(grid_for(new_capacity, 256)), dim3(256), 0, s,
+                     old_free_rows, new_free_rows, free_count, old_capacity, new_capacity);
+  if (int32_t e = launch_status("grow free")) return e;
+  hipLaunchKernelGGL(add_counter_kernel, dim3(1), dim3(64), 0, s, free_count,
+                     new_capacity - old_capacity, static_cast<const int64_t*>(nullptr), 1,
+                     overflow_flag);
+  return launch_status("grow counter");
+}
+
+int32_t cowsdm_count_active(const int32_t* map, int64_t banks, int64_t slots,
+                            const int64_t* bank_list, int64_t nsel,
+                            const uint8_t* active_mask, void* workspace, int64_t* total,
+                            void* stream) {
+  if (!workspace || !total || slots <= 0 || nsel < 0 || banks < 0 ||
+      (!map && !active_mask)) {
+    return fail(COWSDM_EARG, "count_active: invalid arguments");
+  }
+  const int64_t entries = nsel * slots;
+  if (entries >= (1ll << 31)) return fail(COWSDM_ELIMIT, "count_active: too many entries");
+  const hipStream_t s = as_stream(stream);
+  Workspace ws = carve(workspace, entries, 0);
+  RankSource src{map, bank_list, active_mask, slots, entries, banks};
+  if (int32_t e = rank_count(src, ws, s)) return e;
+  hipLaunchKernelGGL(copy_i64_kernel, dim3(1), dim3(64), 0, s, total,
+                     static_cast<const int64_t*>(ws.total), int64_t{1});
+  return launch_status("count copy");
+}
+
+int32_t cowsdm_pack_overlay(const float* dense_memory, const uint8_t* active_mask,
+                            int64_t banks, int64_t slots, int64_t width, int32_t* map,
+                            float* values, int32_t* free_rows, int64_t capacity_rows,
+                            int32_t* free_count, void* workspace, void* stream) {
+  if (!dense_memory || !active_mask || !map || !values || !free_rows || !free_count ||
+      !workspace || banks < 0 || slots <= 0 || width <= 0 || capacity_rows <= 0) {
+    return fail(COWSDM_EARG, "pack_overlay: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t entries = banks * slots;
+  Workspace ws = carve(workspace, entries, capacity_rows);
+  RankSource src{nullptr, nullptr, active_mask, slots, entries, banks};
+  RankApply a{};
+  a.op = kOpPack;
+  a.map_out = map;
+  a.list_a = ws.list_a;
+  a.list_rows = capacity_rows;
+  a.capacity = capacity_rows;
+  if (int32_t e = rank_apply(src, ws, a, s)) return e;
+  const int64_t vecs = capacity_rows * (width % 4 == 0 ? width / 4 : width);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s, values,
+                     static_cast<const int32_t*>(nullptr), dense_memory, ws.list_a,
+                     static_cast<const int64_t*>(ws.total), capacity_rows, width);
+  if (int32_t e = launch_status("pack copy")) return e;
+  hipLaunchKernelGGL(fill_free_tail_kernel, dim3(grid_for(capacity_rows, 256)), dim3(256), 0,
+                     s, free_rows, capacity_rows, static_cast<const int64_t*>(ws.total),
+                     free_count, static_cast<int32_t*>(nullptr));
+  return launch_status("pack free");
+}
+
+int32_t cowsdm_trim_repack(const int32_t* map, const float* values, int64_t capacity_rows,
+                           int64_t banks, int64_t slots, int64_t width, int32_t* new_map,
+                           float* new_values,
+                           int32_t* new_free_rows, int64_t new_capacity, int32_t* free_count,
+                           int32_t* overflow_flag, void* workspace, void* stream) {
+  if (!map || !values || !new_map || !new_values || !new_free_rows || !free_count ||
+      !overflow_flag || !workspace || banks < 0 || slots <= 0 || width <= 0 ||
+      new_capacity <= 0 || capacity_rows <= 0) {
+    return fail(COWSDM_EARG, "trim_repack: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t entries = banks * slots;
+  Workspace ws = carve(workspace, entries, new_capacity);
+  RankSource src{map, nullptr, nullptr, slots, entries, banks};
+  RankApply a{};
+  a.op = kOpTrim;
+  a.map_out = new_map;
+  a.list_a = ws.list_a;
+  a.list_rows = new_capacity;
+  a.capacity = new_capacity;
+  a.src_capacity = capacity_rows;
+  if (int32_t e = rank_apply(src, ws, a, s)) return e;
+  const int64_t vecs = new_capacity * (width % 4 == 0 ? width / 4 : width);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s,
+                     new_values, static_cast<const int32_t*>(nullptr), values, ws.list_a,
+                     static_cast<const int64_t*>(ws.total), new_capacity, width);
+  if (int32_t e = launch_status("trim copy")) return e;
+  hipLaunchKernelGGL(fill_free_tail_kernel, dim3(grid_for(new_capacity, 256)), dim3(256), 0,
+                     s, new_free_rows, new_capacity, static_cast<const int64_t*>(ws.total),
+                     free_count, overflow_flag);
+  return launch_status("trim free");
+}
+
+int32_t cowsdm_append_banks(const int32_t* map, const int64_t* tmpl, int64_t banks,
+                            float* values, int64_t capacity_rows, const int32_t* free_rows,
+                            int32_t* free_count, const int32_t* other_map,
+                            const int64_t* other_tmpl, const float* other_values,
+                            int64_t other_banks, int64_t other_capacity_rows, int64_t slots,
+                            int64_t width, int32_t* new_map, int64_t* new_tmpl,
+                            void* workspace, void* stream) {
+  if ((banks > 0 && (!map || !tmpl)) || (other_banks > 0 && (!other_map || !other_tmpl)) ||
+      !other_values || !values || !free_rows || !free_count || !new_map || !new_tmpl ||
+      !workspace || banks < 0 || other_banks < 0 || slots <= 0 || width <= 0 ||
+      capacity_rows <= 0 || other_capacity_rows < 0) {
+    return fail(COWSDM_EARG, "append_banks: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t entries = other_banks * slots;
+  Workspace ws = carve(workspace, entries, other_capacity_rows);
+  if (banks > 0) {
+    hipLaunchKernelGGL(copy_i32_kernel, dim3(grid_for(banks * slots, 256)), dim3(256), 0, s,
+                       new_map, map, banks * slots);
+    if (int32_t e = launch_status("append copy map")) return e;
+  }
+  hipLaunchKernelGGL(gather_banks_kernel, dim3(grid_for(banks + other_banks, 256)),
+                     dim3(256), 0, s, static_cast<const int32_t*>(nullptr), tmpl, banks, slots,
+                     static_cast<const int64_t*>(nullptr), banks,
+                     static_cast<int32_t*>(nullptr), new_tmpl, other_tmpl, other_banks);
+  if (int32_t e = launch_status("append templates")) return e;
+  if (entries == 0) return 0;
+  RankSource src{other_map, nullptr, nullptr, slots, entries, other_banks};
+  RankApply a{};
+  a.op = kOpAppend;
+  a.map_out = new_map;
+  a.free_rows = free_rows;
+  a.counter = free_count;
+  a.capacity = capacity_rows;
+  a.map_row_offset = banks;
+  a.list_a = ws.list_a;
+  a.list_b = ws.list_b;
+  a.list_rows = other_capacity_rows;
+  a.src_capacity = other_capacity_rows;
+  if (int32_t e = rank_apply(src, ws, a, s)) return e;
+  const int64_t vecs = other_capacity_rows * (width % 4 == 0 ? width / 4 : width);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s, values,
+                     ws.list_b, other_values, ws.list_a, static_cast<const int64_t*>(ws.total),
+                     other_capacity_rows, width);
+  if (int32_t e = launch_status("append copy")) return e;
+  hipLaunchKernelGGL(add_counter_kernel, dim3(1), dim3(64), 0, s, free_count, int64_t{0},
+                     static_cast<const int64_t*>(ws.total), -1, static_cast<int32_t*>(nullptr));
+  return launch_status("append counter");
+}
+
+int32_t cowsdm_check_banks(const int32_t* map, int64_t banks, int64_t slots,
+                           const int64_t* bank_list, int64_t nsel, int32_t discarded_active,
+                           void* workspace, int64_t* result, void* stream) {
+  if (!workspace || !result || banks < 0 || slots <= 0 || nsel < 0 ||
+      (nsel > 0 && !bank_list) || (discarded_active && banks > 0 && !map)) {
+    return fail(COWSDM_EARG, "check_banks: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  Workspace ws = carve(workspace, banks * slots, banks);
+  hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, result, int64_t{1});
+  if (int32_t e = launch_status("check_banks zero")) return e;
+  if (banks > 0) {
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(banks, 256)), dim3(256), 0, s,
+                       ws.list_a, banks);
+    if (int32_t e = launch_status("check_banks marks")) return e;
+  }
+  if (nsel > 0) {
+    hipLaunchKernelGGL(mark_banks_kernel, dim3(grid_for(nsel, 256)), dim3(256), 0, s,
+                       bank_list, nsel, banks, ws.list_a, result);
+    if (int32_t e = launch_status("check_banks mark")) return e;
+  }
+  if (discarded_active && banks > 0) {
+    hipLaunchKernelGGL(discarded_live_kernel, dim3(grid_for(banks * slots, 256)), dim3(256),
+                       0, s, map, banks, slots, static_cast<const int32_t*>(ws.list_a),
+                       result);
+    return launch_status("check_banks discarded");
+  }
+  return 0;
+}
+
+int32_t cowsdm_release(int32_t* map, int64_t banks, int64_t slots, const int64_t* bank_list,
+                       int64_t nsel, int32_t* free_rows, int64_t capacity_rows,
+                       int32_t* free_count, void* workspace, int64_t* released,
+                       void* stream) {
+  if (!map || !bank_list || !free_rows || !free_count || !workspace || !released ||
+      slots <= 0 || nsel < 0 || banks < 0 || capacity_rows <= 0) {
+    return fail(COWSDM_EARG, "release: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t entries = nsel * slots;
+  Workspace ws = carve(workspace, entries, 0);
+  RankSource src{map, bank_list, nullptr, slots, entries, banks};
+  RankApply a{};
+  a.op = kOpRelease;
+  a.free_rows_out = free_rows;
+  a.counter = free_count;
+  a.capacity = capacity_rows;
+  a.map_clear = map;
+  if (int32_t e = rank_apply(src, ws, a, s)) return e;
+  hipLaunchKernelGGL(add_counter_kernel, dim3(1), dim3(64), 0, s, free_count, int64_t{0},
+                     static_cast<const int64_t*>(ws.total), 1, static_cast<int32_t*>(nullptr));
+  if (int32_t e = launch_status("release counter")) return e;
+  hipLaunchKernelGGL(copy_i64_kernel, dim3(1), dim3(64), 0, s, released,
+                     static_cast<const int64_t*>(ws.total), int64_t{1});
+  return launch_status("release count");
+}
+
+int32_t cowsdm_retain_banks(const int32_t* map, const int64_t* tmpl, int64_t banks,
+                            int64_t slots, const int64_t* bank_list, int64_t nsel,
+                            int32_t* new_map, int64_t* new_tmpl, void* stream) {
+  if (slots <= 0 || nsel < 0 || banks < 0 ||
+      (nsel > 0 && (!map || !tmpl || !bank_list || !new_map || !new_tmpl))) {
+    return fail(COWSDM_EARG, "retain_banks: invalid arguments");
+  }
+  if (nsel == 0) return 0;
+  const hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(gather_banks_kernel, dim3(grid_for(nsel * slots, 256)), dim3(256), 0, s,
+                     map, tmpl, banks, slots, bank_list, nsel, new_map, new_tmpl,
+                     static_cast<const int64_t*>(nullptr), int64_t{0});
+  return launch_status("retain_banks");
+}
+
+int32_t cowsdm_materialize_dense(const float* m0, int64_t templates, const int64_t* tmpl,
+                                 const float* values, const int32_t* map, int64_t banks,
+                                 int64_t slots, int64_t width, int64_t capacity_rows,
+                                 float* dense, void* stream) {
+  if (banks < 0 || slots <= 0 || width <= 0 || templates <= 0 ||
+      (banks > 0 && (!m0 || !tmpl || !values || !map || !dense))) {
+    return fail(COWSDM_EARG, "materialize_dense: invalid arguments");
+  }
+  if (banks == 0) return 0;
+  const hipStream_t s = as_stream(stream);
+  const int64_t vecs = banks * slots * (width % 4 == 0 ? width / 4 : width);
+  hipLaunchKernelGGL(materialize_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s, m0,
+                     templates, tmpl, values, map, banks, slots, width, capacity_rows, dense);
+  return launch_status("materialize_dense");
+}
+
+int32_t cowsdm_check_invariants(const int32_t* map, int64_t banks, int64_t slots,
+                                const int32_t* free_rows, const int32_t* free_count,
+                                const int32_t* overflow_flag, const int64_t* scratch,
+                                int64_t capacity_rows, void* workspace, int64_t* stats,
+                                void* stream) {
+  if (!free_rows || !free_count || !overflow_flag || !workspace || !stats || banks < 0 ||
+      slots <= 0 || capacity_rows <= 0 || (banks > 0 && !map)) {
+    return fail(COWSDM_EARG, "check_invariants: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  Workspace ws = carve(workspace, banks * slots, capacity_rows);
+  hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, stats, int64_t{8});
+  if (int32_t e = launch_status("invariants zero stats")) return e;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(capacity_rows, 256)), dim3(256), 0, s,
+                     ws.list_a, capacity_rows);
+  if (int32_t e = launch_status("invariants zero counts")) return e;
+  if (banks > 0) {
+    hipLaunchKernelGGL(own_map_kernel, dim3(grid_for(banks * slots, 256)), dim3(256), 0, s,
+                       map, banks * slots, capacity_rows, ws.list_a, stats);
+    if (int32_t e = launch_status("invariants map")) return e;
+  }
+  hipLaunchKernelGGL(own_free_kernel, dim3(grid_for(capacity_rows, 256)), dim3(256), 0, s,
+                     free_rows, free_count, capacity_rows, ws.list_a, stats);
+  if (int32_t e = launch_status("invariants free")) return e;
+  hipLaunchKernelGGL(own_eval_kernel, dim3(grid_for(capacity_rows, 256)), dim3(256), 0, s,
+                     static_cast<const int32_t*>(ws.list_a), capacity_rows, overflow_flag,
+                     scratch, stats);
+  return launch_status("invariants eval");
+}
+
+int32_t cowsdm_mark_written(uint8_t* active_mask, int64_t banks, int64_t slots,
+                            const void* indices, int64_t per_bank, int32_t index_dtype,
+                            int64_t* result, void* stream) {
+  if (!active_mask || banks < 0 || slots <= 0 || per_bank < 0 ||
+      (banks * per_bank > 0 && !indices) ||
+      (index_dtype != COWSDM_INDEX_INT32 && index_dtype != COWSDM_INDEX_INT64)) {
+    return fail(COWSDM_EARG, "mark_written: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  if (result) {
+    hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, result, int64_t{1});
+    if (int32_t e = launch_status("mark_written zero")) return e;
+  }
+  if (banks * per_bank == 0) return 0;
+  if (index_dtype == COWSDM_INDEX_INT64) {
+    hipLaunchKernelGGL(mark_written_kernel<int64_t>, dim3(grid_for(banks * per_bank, 256)),
+                       dim3(256), 0, s, active_mask, banks, slots, indices, per_bank, result);
+  } else {
+    hipLaunchKernelGGL(mark_written_kernel<int32_t>, dim3(grid_for(banks * per_bank, 256)),
+                       dim3(256), 0, s, active_mask, banks, slots, indices, per_bank, result);
+  }
+  return launch_status("mark_written");
+}
+
+}  // extern "C"

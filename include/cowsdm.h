@@ -1,0 +1,297 @@
+/*
+ * cowsdm.h -- C ABI of libcowsdm.so, the MI355X (gfx950) copy-on-write
+ * Sparse Delta Memory (SDM) decode step and its state lifecycle.
+ *
+ * Every entry point takes device pointers, 64-bit sizes and a hipStream_t
+ * (passed as void*), enqueues its kernels on that stream and returns 0 on
+ * success.  A nonzero return is either a hipError_t or one of the negative
+ * COWSDM_E* codes below; cowsdm_last_error_string() then describes it.
+ * Nothing here allocates or frees device memory: callers own every buffer,
+ * including the scratch and workspace arguments, whose sizes are given by
+ * the *_words / *_bytes helpers.  Entry points never synchronise the stream.
+ *
+ * Layout of one SDM layer's packed state (the same tensors the reference's
+ * PackedSDMCopyOnWriteState holds, copy_on_write_sdm/allocator.py:476-504):
+ *   shared_initial_memory  float  [T, N, D]  model-shared M0, read only
+ *   template_indices       int64  [B]        bank -> template row of M0
+ *   values                 float  [C, D]     physical slab shared by banks
+ *   logical_to_physical    int32  [B, N]     -1 = still shared with M0
+ *   free_rows              int32  [C]        free stack, top = free_count-1
+ *   free_count             int32  scalar
+ *   overflow_flag          int32  scalar
+ *   scratch                int64  [cowsdm_step_scratch_words(B)]  zeroed
+ *                          once at creation; the step kernels keep it valid
+ *
+ * Index tensors (write/read routes) are int32 or int64, row-major [B, K].
+ * Weights, values and gates are float32.  A bank is one (request, memory
+ * head) pair.
+ */
+#ifndef COWSDM_H
+#define COWSDM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define COWSDM_ABI_VERSION 1
+
+/* Index dtype codes. */
+#define COWSDM_INDEX_INT32 0
+#define COWSDM_INDEX_INT64 1
+
+/* Negative return codes (hipError_t values are positive). */
+#define COWSDM_EARG (-1)      /* invalid argument (null pointer, bad size) */
+#define COWSDM_ELIMIT (-2)    /* shape outside what the kernels support   */
+
+/* Bits of the device error word (scratch word COWSDM_SCRATCH_ERRORS) and
+ * of the precheck result word. */
+#define COWSDM_ERR_WRITE_INDEX 0x1   /* write index outside [0, N)        */
+#define COWSDM_ERR_READ_INDEX 0x2    /* read index outside [0, N)         */
+#define COWSDM_ERR_DUP_WRITE 0x4     /* one step writes one slot twice    */
+#define COWSDM_ERR_EXHAUSTED 0x8     /* free stack cannot cover the step  */
+#define COWSDM_ERR_TEMPLATE 0x10     /* template index outside [0, T)     */
+#define COWSDM_ERR_CORRUPT 0x20      /* map/free entry outside [0, C)     */
+#define COWSDM_ERR_LOOKBACK 0x40     /* bank-order scan did not complete  */
+
+/* Word offsets inside the per-layer step scratch (int64 words). */
+#define COWSDM_SCRATCH_EPOCH 0
+#define COWSDM_SCRATCH_TICKET 1
+#define COWSDM_SCRATCH_SERVED 2
+#define COWSDM_SCRATCH_ERRORS 3
+#define COWSDM_SCRATCH_PRECHECK 4
+#define COWSDM_SCRATCH_SLOTS 8
+
+/* Shape shared by every layer of one step launch. */
+typedef struct cowsdm_shape {
+  int64_t banks;        /* B: live banks                          */
+  int64_t slots;        /* N: logical rows per bank               */
+  int64_t width;        /* D: row width (floats)                  */
+  int64_t writes;       /* W: write routes per bank, 1..64        */
+  int64_t reads;        /* R: read routes per bank, 1..256        */
+  int64_t templates;    /* T: rows of shared_initial_memory       */
+  int32_t index_dtype;  /* COWSDM_INDEX_INT32 / COWSDM_INDEX_INT64 */
+  int32_t reserved;
+} cowsdm_shape_t;
+
+/* One layer's tensors for a packed (or dense) step.  For the dense step,
+ * `values` is the dense table [B, N, D] and the allocator fields
+ * (logical_to_physical, free_rows, free_count, overflow_flag, scratch,
+ * shared_initial_memory, template_indices, first/repeated/allocated) are
+ * ignored and may be null. */
+typedef struct cowsdm_layer {
+  const float* shared_initial_memory;
+  const int64_t* template_indices;
+  float* values;
+  int32_t* logical_to_physical;
+  const int32_t* free_rows;
+  int32_t* free_count;
+  int32_t* overflow_flag;
+  int64_t* scratch;
+  int64_t capacity_rows;
+  const void* write_indices;
+  const float* write_weights;
+  const float* step_values;
+  const float* input_gate;
+  const float* erase_gate;      /* may equal input_gate */
+  const float* forget_log_gate;
+  const void* read_indices;
+  const float* read_weights;
+  float* output;                /* [B, D] */
+  int64_t* first_touches_out;   /* [B] or null */
+  int64_t* repeated_writes_out; /* [B] or null */
+  int32_t* allocated_rows_out;  /* scalar or null */
+} cowsdm_layer_t;
+
+/* ---------------------------------------------------------------- info */
+
+int32_t cowsdm_abi_version(void);
+const char* cowsdm_last_error_string(void);
+/* int64 words of step scratch one layer with `banks` banks needs. */
+int64_t cowsdm_step_scratch_words(int64_t banks);
+/* Bytes of lifecycle workspace for a ranking over `entries` map entries
+ * (release / trim / append / pack handoff / invariant checks). */
+int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows);
+
+/* ---------------------------------------------------------- decode step */
+
+/* One fused copy-on-write step for one layer: resolve the W write routes
+ * through the map, pop free rows for first touches in bank-major order,
+ * copy M0 rows, apply the FP32 gated-delta update, then the weighted read
+ * of R rows (which observes this step's writes).
+ * Replaces _packed_sdm_cow_step_triton, copy_on_write_sdm/allocator.py:
+ * 1179-1319 (kernel 74-229), with the torch semantics of 1466-1525. */
+int32_t cowsdm_packed_step(const cowsdm_layer_t* layer,
+                           const cowsdm_shape_t* shape, void* stream);
+
+/* The same step for `nlayers` independent layers in one launch (all layers
+ * share one shape).  No counterpart in the reference: a batched form of
+ * cowsdm_packed_step for callers that already hold every layer's routes. */
+int32_t cowsdm_packed_step_layers(const cowsdm_layer_t* layers,
+                                  int32_t nlayers,
+                                  const cowsdm_shape_t* shape, void* stream);
+
+/* Dense-table control step on values = memory [B, N, D].
+ * Replaces _dense_sdm_sparse_step_triton, allocator.py:1322-1378 (kernel
+ * 367-460), with the torch semantics of 1612-1633. */
+int32_t cowsdm_dense_step(const cowsdm_layer_t* layer,
+                          const cowsdm_shape_t* shape, void* stream);
+int32_t cowsdm_dense_step_layers(const cowsdm_layer_t* layers, int32_t nlayers,
+                                 const cowsdm_shape_t* shape, void* stream);
+
+/* Route and capacity validation before a step; writes the COWSDM_ERR_*
+ * bits it finds to *result (int64, device).  check_capacity counts the
+ * step's first touches against free_count (packed state only).
+ * Replaces _validate_indices / _validate_unique_writes (allocator.py:
+ * 1107-1134) and the exhaustion assert of allocator.py:1279-1282, 1475. */
+int32_t cowsdm_step_precheck(const cowsdm_layer_t* layer,
+                             const cowsdm_shape_t* shape, int32_t dense,
+                             int32_t check_unique, int32_t check_capacity,
+                             int64_t* result, void* stream);
+
+/* ------------------------------------------------------------ lifecycle */
+
+/* Fresh state: map = -1, free_rows = 0..C-1, free_count = C, overflow = 0,
+ * scratch = 0; template indices outside [0, T) set COWSDM_ERR_TEMPLATE in
+ * *result.  Replaces PackedSDMCopyOnWriteState.allocate, allocator.py:
+ * 506-585. */
+int32_t cowsdm_init_state(int32_t* logical_to_physical, int64_t banks,
+                          int64_t slots, int32_t* free_rows,
+                          int64_t capacity_rows, int32_t* free_count,
+                          int32_t* overflow_flag, int64_t* scratch,
+                          int64_t scratch_words,
+                          const int64_t* template_indices, int64_t templates,
+                          int64_t* result, void* stream);
+
+/* Slab growth: new_values[:old_C] = old_values; new_free_rows =
+ * old free entries ++ (old_C .. new_C-1); free_count += new_C - old_C;
+ * overflow = 0.  Replaces grow_capacity, allocator.py:691-743. */
+int32_t cowsdm_grow(const float* old_values, int64_t old_capacity,
+                    float* new_values, int64_t new_capacity, int64_t width,
+                    const int32_t* old_free_rows, int32_t* new_free_rows,
+                    int32_t* free_count, int32_t* overflow_flag, void* stream);
+
+/* Count entries >= 0 of map [banks, slots] rows bank_list[0..nsel) (rows
+ * 0..nsel-1 when bank_list is null; listed rows outside [0, banks) count as
+ * empty), row-major, or of active_mask [nsel, slots] when it is not null; writes the int64 total to *total and
+ * keeps per-tile offsets in `workspace` for a following apply call on the
+ * same map.  Replaces the `active.sum().item()` counts of allocator.py:628,
+ * 791, 870 and the cumsum of 1057. */
+int32_t cowsdm_count_active(const int32_t* logical_to_physical, int64_t banks,
+                            int64_t slots, const int64_t* bank_list, int64_t nsel,
+                            const uint8_t* active_mask, void* workspace,
+                            int64_t* total, void* stream);
+
+/* Pack a dense prefill terminal state: active (bank, slot) pairs of
+ * active_mask [B, N] in row-major order get physical rows 0..A-1,
+ * values[:A] = dense[bank, slot], free_rows[:C-A] = A..C-1,
+ * free_count = C-A.  Needs cowsdm_count_active(mask) first.
+ * Replaces the body of from_dense_overlay, allocator.py:664-685. */
+int32_t cowsdm_pack_overlay(const float* dense_memory, const uint8_t* active_mask,
+                            int64_t banks, int64_t slots, int64_t width,
+                            int32_t* logical_to_physical, float* values,
+                            int32_t* free_rows, int64_t capacity_rows,
+                            int32_t* free_count, void* workspace, void* stream);
+
+/* Repack live rows into a smaller slab in row-major map order:
+ * new_values[:A] = values[live rows], new_map = ranks, new_free_rows =
+ * A..new_C-1, free_count = new_C - A, overflow = 0.  Needs
+ * cowsdm_count_active(map) first.  Replaces trim_capacity,
+ * allocator.py:775-839. */
+int32_t cowsdm_trim_repack(const int32_t* logical_to_physical,
+                           const float* values, int64_t capacity_rows,
+                           int64_t banks, int64_t slots,
+                           int64_t width, int32_t* new_logical_to_physical,
+                           float* new_values, int32_t* new_free_rows,
+                           int64_t new_capacity, int32_t* free_count,
+                           int32_t* overflow_flag, void* workspace,
+                           void* stream);
+
+/* Admit another pool's banks: pop destination rows from the top of this
+ * free stack in the other map's row-major live order, copy their values,
+ * build new_map = [map ; admitted map] and new_templates = [templates ;
+ * other templates], free_count -= A.  Needs cowsdm_count_active(other map)
+ * first; the workspace holds cowsdm_workspace_bytes(other_banks * N,
+ * other_capacity_rows).  Replaces append_banks_from, allocator.py:841-914. */
+int32_t cowsdm_append_banks(const int32_t* logical_to_physical,
+                            const int64_t* template_indices, int64_t banks,
+                            float* values, int64_t capacity_rows,
+                            const int32_t* free_rows, int32_t* free_count,
+                            const int32_t* other_logical_to_physical,
+                            const int64_t* other_template_indices,
+                            const float* other_values, int64_t other_banks,
+                            int64_t other_capacity_rows, int64_t slots,
+                            int64_t width, int32_t* new_logical_to_physical,
+                            int64_t* new_template_indices, void* workspace,
+                            void* stream);
+
+/* Validate bank indices for release / retain: bounds, duplicates, and (for
+ * retain, when discarded_active != 0) whether any bank not listed still
+ * owns rows.  Writes bits 1 (invalid or duplicated) and 2 (discarded bank
+ * live) to *result.  Replaces the checks of allocator.py:1032-1051 and
+ * 926-940. */
+int32_t cowsdm_check_banks(const int32_t* logical_to_physical, int64_t banks,
+                           int64_t slots, const int64_t* bank_list,
+                           int64_t nsel, int32_t discarded_active,
+                           void* workspace, int64_t* result, void* stream);
+
+/* Release banks bank_list[0..nsel): push their live rows on the free stack
+ * in (listed bank, slot) order, free_count += released, map rows = -1,
+ * *released = count.  Needs cowsdm_count_active(map, bank_list) first.
+ * Replaces release, allocator.py:1018-1067. */
+int32_t cowsdm_release(int32_t* logical_to_physical, int64_t banks, int64_t slots,
+                       const int64_t* bank_list, int64_t nsel,
+                       int32_t* free_rows, int64_t capacity_rows,
+                       int32_t* free_count, void* workspace, int64_t* released,
+                       void* stream);
+
+/* Keep banks bank_list[0..nsel) in that order: new_map[i] = map[list[i]],
+ * new_templates[i] = templates[list[i]].  Values never move.
+ * Replaces retain_banks, allocator.py:916-942. */
+int32_t cowsdm_retain_banks(const int32_t* logical_to_physical,
+                            const int64_t* template_indices, int64_t banks,
+                            int64_t slots,
+                            const int64_t* bank_list, int64_t nsel,
+                            int32_t* new_logical_to_physical,
+                            int64_t* new_template_indices, void* stream);
+
+/* dense[b, n] = map[b, n] >= 0 ? values[map[b, n]] : M0[template[b], n].
+ * Replaces materialize_dense, allocator.py:1003-1016. */
+int32_t cowsdm_materialize_dense(const float* shared_initial_memory,
+                                 int64_t templates,
+                                 const int64_t* template_indices,
+                                 const float* values,
+                                 const int32_t* logical_to_physical,
+                                 int64_t banks, int64_t slots, int64_t width,
+                                 int64_t capacity_rows, float* dense,
+                                 void* stream);
+
+/* Partition check of live and free rows.  Writes 8 int64 words to stats:
+ * [0] live rows, [1] free rows, [2] rows with two or more live owners,
+ * [3] rows listed twice on the free stack, [4] rows neither live nor free
+ * exactly once, [5] entries outside [0, C), [6] overflow flag,
+ * [7] step error word.  Replaces validate_invariants, allocator.py:
+ * 1069-1095. */
+int32_t cowsdm_check_invariants(const int32_t* logical_to_physical,
+                                int64_t banks, int64_t slots,
+                                const int32_t* free_rows,
+                                const int32_t* free_count,
+                                const int32_t* overflow_flag,
+                                const int64_t* scratch,
+                                int64_t capacity_rows, void* workspace,
+                                int64_t* stats, void* stream);
+
+/* active_mask[b, idx[b, k]] = 1 for k < K (indices outside [0, N) are
+ * ignored and reported as 0x2 in *result when result is not null).  The prefill handoff's union of
+ * written rows, inference.py:332-347. */
+int32_t cowsdm_mark_written(uint8_t* active_mask, int64_t banks, int64_t slots,
+                            const void* indices, int64_t per_bank,
+                            int32_t index_dtype, int64_t* result,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COWSDM_H */

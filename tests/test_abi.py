@@ -1,0 +1,76 @@
+"""The C-ABI library loads and exports every symbol include/cowsdm.h
+declares (CPU only: no kernel is launched)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from copy_on_write_sdm_amd import _native as nat
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "cowsdm.h"
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|int64_t|const char\*)\s+(cowsdm_\w+)\s*\(",
+                                 text, flags=re.M)))
+
+
+def test_library_is_built():
+    assert nat.LIBRARY.exists(), "run __graft_entry__.build() first"
+
+
+def test_exports_every_header_symbol():
+    lib = ctypes.CDLL(str(nat.LIBRARY))
+    names = header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_bindings_cover_header():
+    assert sorted(nat.SIGNATURES) == header_functions()
+
+
+def test_info_entry_points():
+    lib = nat.lib()
+    assert lib.cowsdm_abi_version() == 1
+    assert lib.cowsdm_step_scratch_words(64) == 8 + 64
+    assert lib.cowsdm_step_scratch_words(-1) == -1
+    assert lib.cowsdm_workspace_bytes(0, 0) == 256
+    assert lib.cowsdm_workspace_bytes(4096, 100) > 256 + 2 * 4 + 2 * 400
+    assert lib.cowsdm_workspace_bytes(-1, 0) == -1
+
+
+def test_argument_errors_return_codes_without_launching():
+    lib = nat.lib()
+    assert lib.cowsdm_packed_step(None, None, None) == -1
+    assert b"shape" in lib.cowsdm_last_error_string()
+    shape = nat.Shape(banks=4, slots=16, width=8, writes=65, reads=4, templates=1,
+                      index_dtype=0)
+    layer = nat.Layer()
+    assert lib.cowsdm_packed_step(ctypes.byref(layer), ctypes.byref(shape), None) == -2
+    assert b"W <= 64" in lib.cowsdm_last_error_string()
+    shape.writes = 4
+    assert lib.cowsdm_packed_step(ctypes.byref(layer), ctypes.byref(shape), None) == -1
+    assert b"null" in lib.cowsdm_last_error_string()
+    assert lib.cowsdm_grow(None, 0, None, 0, 0, None, None, None, None, None) == -1
+
+
+def test_structure_layout_matches_header():
+    # 21 pointer-sized fields and one int64 in cowsdm_layer_t
+    assert ctypes.sizeof(nat.Layer) == 21 * 8
+    assert ctypes.sizeof(nat.Shape) == 7 * 8
+
+
+@pytest.mark.parametrize("name", ["cowsdm_packed_step", "cowsdm_dense_step",
+                                  "cowsdm_release", "cowsdm_append_banks"])
+def test_header_cites_reference(name):
+    text = HEADER.read_text()
+    block = text[:text.index(name + "(")]
+    comment = block[block.rfind("/*"):]
+    assert "allocator.py:" in comment
