@@ -1,0 +1,336 @@
+#!/usr/bin/env python3
+"""Decode throughput of the packed copy-on-write SDM step on one MI355X.
+
+Workload (BASELINE config 2 at batch 64): L=7 SDM layers, H=1 memory head,
+N=256 slots, D=128, top-4 writes / top-16 reads drawn uniformly, FP32 state.
+A 256-token prefix runs through the dense-table kernel, each layer's union of
+written slots is packed into a copy-on-write slab with a growth quantum of
+four decode steps (max(16, B*4*4) rows), then decode runs on the packed
+state.  One bench "step" is one decode token for all 7 layers and all B
+requests: one fused launch covering every (layer, bank).
+
+Timing: W untimed warmup steps, then exactly K timed steps between
+synchronisations.  Steps run in groups of G (the growth quantum, 4): before a
+group every layer proves capacity for the group's worst case
+(prepare_step_capacity(B*W*G), growing the slab by the quantum when short),
+then one captured hipGraph replays the group's G launches; a graph is
+recaptured only when a slab grew.  The dense-table control runs the same
+routes the same way from the same packed state; both end states must be
+equal.  The CPU baseline is the torch restatement of the reference's
+dense-table step on the host cores, on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "decode tokens/s at batch 64 (L=7,N=256,D=128); achieved HBM GB/s % of peak"
+PEAK_HBM_GBPS = 8000.0
+LAYERS, HEADS, SLOTS, WIDTH, WRITES, READS = 7, 1, 256, 128, 4, 16
+PREFIX = 256
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=448)
+    p.add_argument("--warmup", type=int, default=64)
+    p.add_argument("--batch", type=int, default=64)
+    p.add_argument("--group", type=int, default=4, help="decode steps per graph replay")
+    p.add_argument("--seed", type=int, default=1234)
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--eager-steps", type=int, default=32,
+                   help="steps of the per-layer Python drop-in path to time (0: skip)")
+    return p.parse_args()
+
+
+def algorithmic_bytes(banks: int, layers: int) -> int:
+    """Bytes one step of one (bank, layer) must move: 2W+R rows of D floats,
+    the value vector and the reading, route indices/weights/map entries
+    (int32/fp32) and three gates."""
+
+    rows = (2 * WRITES + READS) * WIDTH * 4
+    vectors = 2 * WIDTH * 4
+    metadata = (WRITES + READS) * (4 + 4 + 4) + 3 * 4
+    return banks * layers * (rows + vectors + metadata)
+
+
+def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
+    """Time the torch restatement of the reference's dense-table CPU step
+    (allocator.py:1612-1633) at the benchmark's shape on the host cores."""
+
+    import torch
+
+    from copy_on_write_sdm_amd import synthetic
+    from oracle import torch_port
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    steps = 48
+    m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=seed)
+    batch_inputs = synthetic.make_steps(steps=steps, layers=LAYERS, banks=batch, slots=SLOTS,
+                                        width=WIDTH, writes=WRITES, reads=READS, seed=seed + 1)
+    tables = [m0[l, 0].expand(batch, -1, -1).contiguous() for l in range(LAYERS)]
+    for s in range(2):
+        for l in range(LAYERS):
+            torch_port.dense_step(tables[l], **batch_inputs.step(s, l))
+    done = 0
+    t0 = time.perf_counter()
+    while True:
+        s = done % steps
+        for l in range(LAYERS):
+            torch_port.dense_step(tables[l], **batch_inputs.step(s, l))
+        done += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": round(batch * done / elapsed, 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{done} decode steps of the torch dense-table restatement "
+                   f"(oracle/torch_port.py) at L={LAYERS} B={batch} N={SLOTS} D={WIDTH} "
+                   f"W={WRITES} R={READS}, {elapsed:.1f} s on {threads} threads "
+                   f"({platform.processor() or platform.machine()})"),
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(the packed SDM step has no multi-GPU path in this build)", file=sys.stderr)
+        return 2
+    import torch
+
+    import copy_on_write_sdm_amd as cow
+    from copy_on_write_sdm_amd import synthetic
+
+    dev = torch.device("cuda:0")
+    B, K, Wm, G = args.batch, args.steps, args.warmup, args.group
+    total_steps = Wm + K
+    quantum = max(16, B * WRITES * 4)
+
+    # ---- prefill (dense kernel) and copy-on-write handoff, untimed
+    m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=args.seed, device=dev)
+    prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=B, slots=SLOTS, width=WIDTH,
+                                  writes=WRITES, reads=READS, seed=args.seed + 1, device=dev)
+    tables = [m0[l, 0].expand(B, -1, -1).contiguous() for l in range(LAYERS)]
+    prefill = cow.DecodeTrace(memories=tables, write_indices=prefix.write_indices,
+                              write_weights=prefix.write_weights, values=prefix.values,
+                              input_gate=prefix.input_gate,
+                              forget_log_gate=prefix.forget_log_gate,
+                              read_indices=prefix.read_indices, read_weights=prefix.read_weights)
+    for s0 in range(0, PREFIX, 64):
+        prefill.launch(min(64, PREFIX - s0), start=s0)
+    states = []
+    for l in range(LAYERS):
+        active = torch.zeros(B, SLOTS, dtype=torch.bool, device=dev)
+        cow.mark_written(active, prefix.write_indices[:, l].permute(1, 0, 2).reshape(B, -1))
+        states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
+            m0[l], tables[l], active, template_indices=torch.zeros(B, dtype=torch.int64,
+                                                                  device=dev),
+            growth_quantum_rows=quantum))
+    del prefill, prefix
+    handoff_rows = [int(st.allocated_rows_tensor()) for st in states]
+    handoff_capacity = [st.capacity_rows for st in states]
+
+    # ---- decode routes
+    routes = synthetic.make_steps(steps=total_steps, layers=LAYERS, banks=B, slots=SLOTS,
+                                  width=WIDTH, writes=WRITES, reads=READS, seed=args.seed + 2,
+                                  device=dev)
+    inputs = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+                  values=routes.values, input_gate=routes.input_gate,
+                  forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+                  read_weights=routes.read_weights)
+    dense_tables = [st.materialize_dense() for st in states]
+    eager_states = None
+    if args.eager_steps:
+        eager_states = [cow.PackedSDMCopyOnWriteState.from_dense_overlay(
+            m0[l], dense_tables[l], (states[l].logical_to_physical >= 0),
+            template_indices=torch.zeros(B, dtype=torch.int64, device=dev),
+            growth_quantum_rows=quantum) for l in range(LAYERS)]
+    packed = cow.DecodeTrace(states=states, **inputs)
+    dense = cow.DecodeTrace(memories=dense_tables, **inputs)
+    capture_stream = torch.cuda.Stream()
+
+    class Runner:
+        """Replays groups of G steps; recaptures when slab pointers move."""
+
+        def __init__(self, trace, proof):
+            self.trace, self.proof = trace, proof
+            self.graphs, self.key = {}, None
+            self.launch_ms, self.launches, self.recaptures = 0.0, 0, 0
+            self.events = []
+
+        def pointers(self):
+            if self.trace.dense:
+                return tuple(t.data_ptr() for t in self.trace.tables)
+            return tuple((st.values.data_ptr(), st.free_rows.data_ptr())
+                         for st in self.trace.tables)
+
+        def group(self, n, timed):
+            if self.proof:
+                cow.PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
+                    self.trace.tables, B * WRITES * n)
+            key = self.pointers()
+            if key != self.key:
+                self.graphs, self.key = {}, key
+                self.recaptures += 1
+            if n not in self.graphs:
+                layers = self.trace.layer_array()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=capture_stream):
+                    self.trace.launch(n, layers)
+                self.graphs[n] = graph
+            if timed:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                self.graphs[n].replay()
+                e1.record()
+                self.events.append((e0, e1))
+                self.launches += n
+            else:
+                self.graphs[n].replay()
+
+        def run(self, steps, timed):
+            done = 0
+            while done < steps:
+                n = min(G, steps - done)
+                self.group(n, timed)
+                done += n
+
+        def kernel_ms(self):
+            return sum(a.elapsed_time(b) for a, b in self.events)
+
+    def measure(runner, label):
+        runner.trace.set_step(0)
+        runner.run(Wm, timed=False)
+        torch.cuda.synchronize()
+        alloc0 = (sum(int(st.allocated_rows_tensor()) for st in runner.trace.tables)
+                  if not runner.trace.dense else 0)
+        grow0 = (sum(st.growth_events for st in runner.trace.tables)
+                 if not runner.trace.dense else 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        runner.run(K, timed=True)
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - t0
+        new_rows = ((sum(int(st.allocated_rows_tensor()) for st in runner.trace.tables) - alloc0)
+                    if not runner.trace.dense else 0)
+        grows = ((sum(st.growth_events for st in runner.trace.tables) - grow0)
+                 if not runner.trace.dense else 0)
+        return seconds, new_rows, grows
+
+    p_runner = Runner(packed, proof=True)
+    d_runner = Runner(dense, proof=False)
+    p_seconds, new_rows, timed_growths = measure(p_runner, "packed")
+    d_seconds, _, _ = measure(d_runner, "dense")
+
+    # both paths ran identical routes from identical logical state
+    state_diff = max(float((st.materialize_dense() - t).abs().max())
+                     for st, t in zip(states, dense_tables))
+    for st in states:
+        st.validate_invariants()
+    if int(packed.step_index.item()) != total_steps:
+        raise AssertionError("packed decode did not consume the trace")
+
+    # ---- per-layer Python drop-in path (exact reference call pattern)
+    eager = None
+    if eager_states is not None:
+        n = min(args.eager_steps, total_steps)
+        for s in range(2):
+            for l in range(LAYERS):
+                eager_states[l].prepare_step_capacity(B * WRITES)
+                cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
+                                        validate_routes=False, collect_diagnostics=False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(2, n):
+            for l in range(LAYERS):
+                eager_states[l].prepare_step_capacity(B * WRITES)
+                cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
+                                        validate_routes=False, collect_diagnostics=False)
+        torch.cuda.synchronize()
+        eager = B * (n - 2) / (time.perf_counter() - t0)
+
+    launches = p_runner.launches
+    kernel_ms = p_runner.kernel_ms()
+    launch_us = 1000.0 * kernel_ms / launches
+    bytes_per_launch = algorithmic_bytes(B, LAYERS) + 8 * new_rows / max(1, launches)
+    achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
+    dense_launch_us = 1000.0 * d_runner.kernel_ms() / d_runner.launches
+
+    result = {
+        "metric": METRIC,
+        "value": round(B * K / p_seconds, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": round(1000.0 * p_seconds / K, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"config 2: packed copy-on-write SDM decode, L={LAYERS} H={HEADS} "
+                         f"N={SLOTS} D={WIDTH} top-{WRITES} write / top-{READS} read, "
+                         f"batch {B}, prefix {PREFIX}, growth quantum 4 steps"),
+            "batch": B, "layers": LAYERS, "slots": SLOTS, "width": WIDTH,
+            "writes": WRITES, "reads": READS, "prefix": PREFIX,
+            "growth_quantum_rows": quantum, "steps_per_graph": G,
+            "launch": "one fused launch per step for all layers; hipGraph of G steps",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+            "kernel": "sdm_step_kernel<int, 4, 2, false> (packed, 7 layers x 64 banks)",
+            "launch_us": round(launch_us, 3),
+            "algorithmic_bytes_per_launch": int(bytes_per_launch),
+        },
+        "dense_control": {
+            "tokens_per_s": round(B * K / d_seconds, 1),
+            "launch_us": round(dense_launch_us, 3),
+            "packed_over_dense_latency": round(p_seconds / d_seconds, 4),
+            "state_max_abs_diff": state_diff,
+        },
+        "allocator": {
+            "handoff_live_rows": sum(handoff_rows),
+            "handoff_capacity_rows": sum(handoff_capacity),
+            "live_rows_after": sum(int(st.allocated_rows_tensor()) for st in states),
+            "capacity_rows_after": sum(st.capacity_rows for st in states),
+            "growth_events": sum(st.growth_events for st in states),
+            "growth_rows_copied": sum(st.growth_rows_copied for st in states),
+            "timed_growth_events": timed_growths,
+            "graph_recaptures": p_runner.recaptures,
+        },
+        "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

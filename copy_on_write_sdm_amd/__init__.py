@@ -7,6 +7,7 @@ kernels for gfx950 in libcowsdm.so (C ABI: include/cowsdm.h).
 """
 
 from .allocator import (
+    DecodeTrace,
     PackedSDMCopyOnWriteState,
     SDMCopyOnWriteStep,
     dense_sdm_sparse_step,
@@ -24,6 +25,7 @@ from .inference import (
 )
 
 __all__ = [
+    "DecodeTrace",
     "FaithfulSDMDecodeState",
     "PackedSDMCopyOnWriteState",
     "SDMCopyOnWriteStep",

@@ -19,9 +19,13 @@ import torch
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
-SOURCE = PACKAGE_DIR / "csrc" / "cowsdm.hip"
+SOURCE_DIR = PACKAGE_DIR / "csrc"
+# one translation unit per step-kernel family so hipcc can run in parallel
+SOURCES = ("cowsdm.hip", "step_i32_packed.hip", "step_i32_dense.hip", "step_i64_packed.hip",
+           "step_i64_dense.hip")
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
+BUILD_DIR = PACKAGE_DIR / "_build"
 
 INDEX_INT32 = 0
 INDEX_INT64 = 1
@@ -36,9 +40,7 @@ ERR_LOOKBACK = 0x40
 
 SCRATCH_EPOCH = 0
 SCRATCH_TICKET = 1
-SCRATCH_SERVED = 2
 SCRATCH_ERRORS = 3
-SCRATCH_PRECHECK = 4
 SCRATCH_SLOTS = 8
 
 HIPCC_FLAGS = (
@@ -46,7 +48,6 @@ HIPCC_FLAGS = (
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # every product and sum is rounded on its own, as in the reference's
     # elementwise torch ops
     "-ffp-contract=off",
@@ -55,21 +56,37 @@ HIPCC_FLAGS = (
 )
 
 
-def build_library(output: Path | None = None, *, verbose: bool = False) -> Path:
-    """Compile csrc/cowsdm.hip for gfx950 into lib/libcowsdm.so."""
+def build_library(output: Path | None = None, *, jobs: int | None = None) -> Path:
+    """Compile csrc/*.hip for gfx950 and link lib/libcowsdm.so."""
 
     output = Path(output) if output is not None else LIBRARY
     output.parent.mkdir(parents=True, exist_ok=True)
-    tmp = output.with_name(output.name + f".tmp{os.getpid()}")
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", str(tmp), str(SOURCE)]
+    include = [f"-I{INCLUDE_DIR}", f"-I{SOURCE_DIR}"]
+    objects, procs = [], []
+    jobs = jobs or min(len(SOURCES), max(1, os.cpu_count() or 1))
+    pending = list(SOURCES)
+    while pending or procs:
+        while pending and len(procs) < jobs:
+            name = pending.pop(0)
+            obj = BUILD_DIR / (name.rsplit(".", 1)[0] + ".o")
+            cmd = [hipcc, *HIPCC_FLAGS, *include, "-c", "-o", str(obj), str(SOURCE_DIR / name)]
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                                stderr=subprocess.PIPE, text=True)))
+            objects.append(obj)
+        cmd, proc = procs.pop(0)
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            for _, other in procs:
+                other.kill()
+            raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + err)
+    tmp = output.with_name(output.name + f".tmp{os.getpid()}")
+    cmd = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp),
+           *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(
-            "hipcc failed building libcowsdm.so:\n" + " ".join(cmd) + "\n" + proc.stderr
-        )
-    if verbose and proc.stderr:
-        print(proc.stderr)
+        raise RuntimeError("hipcc link failed:\n" + " ".join(cmd) + "\n" + proc.stderr)
     os.replace(tmp, output)
     return output
 
@@ -117,6 +134,17 @@ class Layer(ctypes.Structure):
     ]
 
 
+class Trace(ctypes.Structure):
+    """cowsdm_trace_t."""
+
+    _fields_ = [
+        ("step_index", ctypes.c_void_p),
+        ("ticket", ctypes.c_void_p),
+        ("first_step", ctypes.c_int64),
+        ("stride_bytes", ctypes.c_int64 * 9),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -130,7 +158,13 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_packed_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
     "cowsdm_packed_step_layers": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),
+    "cowsdm_packed_step_trace": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32,
+               _P]),
     "cowsdm_dense_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
+    "cowsdm_dense_step_trace": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32,
+               _P]),
     "cowsdm_dense_step_layers": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),
     "cowsdm_step_precheck": (

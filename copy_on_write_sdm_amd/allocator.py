@@ -348,6 +348,42 @@ class PackedSDMCopyOnWriteState:
         self.capacity_is_proven = True
         return self.capacity_rows
 
+    @staticmethod
+    @torch.no_grad()
+    def prepare_step_capacity_layers(states: Sequence["PackedSDMCopyOnWriteState"],
+                                     maximum_new_rows: int) -> list[int]:
+        """``prepare_step_capacity(maximum_new_rows)`` on every state, with
+        the free counts the proofs need read in one device-to-host transfer.
+
+        Decisions equal separate calls made at the same point of the stream:
+        each state still reads its free count only when its running proof is
+        exhausted, and a grown slab's free count is known on the host (old
+        free count plus the rows added)."""
+
+        if maximum_new_rows < 0:
+            raise ValueError("maximum new SDM rows cannot be negative")
+        short = [st for st in states
+                 if st.growth_quantum_rows > 0
+                 and st.proven_maximum_additional_allocations < maximum_new_rows]
+        if short:
+            frees = torch.stack([st.free_count for st in short]).tolist()
+            for st, free_rows in zip(short, frees):
+                if free_rows < maximum_new_rows:
+                    free_rows += st.grow_capacity(
+                        st.capacity_rows + maximum_new_rows - free_rows)
+                st.proven_maximum_additional_allocations = free_rows
+        capacities = []
+        for st in states:
+            if st.growth_quantum_rows <= 0:
+                if not st.capacity_is_proven:
+                    raise ValueError("SDM COW capacity has no decode proof")
+                capacities.append(0)
+                continue
+            st.proven_maximum_additional_allocations -= maximum_new_rows
+            st.capacity_is_proven = True
+            capacities.append(st.capacity_rows)
+        return capacities
+
     # -------------------------------------------------------- lifecycle
 
     def _count_live(self, mapping: torch.Tensor, workspace: torch.Tensor,
@@ -1072,3 +1108,111 @@ def mark_written(active: torch.Tensor, indices: torch.Tensor) -> None:
             result.data_ptr(), nat.stream_handle(active.device)),
         "cowsdm_mark_written",
     )
+
+
+class DecodeTrace:
+    """Routes of many decode steps for several independent layers, resident
+    on the device, launched ``steps`` at a time.
+
+    Inputs are stacked [S, L, B, ...] (``values`` [S, L, B, D], gates
+    [S, L, B]).  Each launch runs all layers for one step, as
+    ``packed_sdm_cow_step_layers`` would.  ``launch(k, start=s)`` enqueues
+    steps s..s+k-1 from the host; ``launch(k)`` without ``start`` runs the
+    steps named by the device counter ``step_index``, which the kernels
+    advance themselves, so a captured hipGraph of ``launch(k)`` replays k
+    consecutive steps per replay without host work.  ``outputs`` is [S, L, B, D] (one reading per step) or
+    [L, B, D] (every step overwrites the same buffer).  ``memories`` given
+    instead of ``states`` runs the dense-table control.  No counterpart in
+    the reference.
+    """
+
+    _INPUTS = ("write_indices", "write_weights", "values", "input_gate", "erase_gate",
+               "forget_log_gate", "read_indices", "read_weights")
+
+    def __init__(self, *, states=None, memories=None, write_indices, write_weights, values,
+                 input_gate, forget_log_gate, read_indices, read_weights, erase_gate=None,
+                 outputs=None):
+        if (states is None) == (memories is None):
+            raise ValueError("give exactly one of states or memories")
+        self.dense = memories is not None
+        self.tables = list(memories if self.dense else states)
+        layers = len(self.tables)
+        if not 1 <= layers <= 8:
+            raise ValueError("a decode trace drives 1 to 8 layers")
+        erase_gate = input_gate if erase_gate is None else erase_gate
+        self.inputs = dict(write_indices=write_indices, write_weights=write_weights,
+                           values=values, input_gate=input_gate, erase_gate=erase_gate,
+                           forget_log_gate=forget_log_gate, read_indices=read_indices,
+                           read_weights=read_weights)
+        steps = write_indices.shape[0]
+        first = self.tables[0]
+        banks = first.shape[0] if self.dense else first.banks
+        width = first.shape[2] if self.dense else first.width
+        device = first.device if self.dense else first.values.device
+        for name, tensor in self.inputs.items():
+            if tensor.shape[:3] != (steps, layers, banks) or not tensor.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous [S, L, B, ...] tensor")
+            if tensor.device != device:
+                raise ValueError("decode trace tensors must share one device")
+        if outputs is None:
+            outputs = torch.empty(layers, banks, width, device=device)
+        if outputs.shape not in ((steps, layers, banks, width), (layers, banks, width)):
+            raise ValueError("outputs must be [S, L, B, D] or [L, B, D]")
+        self.outputs = outputs
+        self.steps = steps
+        self.device = device
+        self.step_index = torch.zeros(1, dtype=torch.int64, device=device)
+        self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
+        self.trace = nat.Trace()
+        self.trace.step_index = self.step_index.data_ptr()
+        self.trace.ticket = self.ticket.data_ptr()
+        for k, name in enumerate(self._INPUTS):
+            tensor = self.inputs[name]
+            self.trace.stride_bytes[k] = tensor.stride(0) * tensor.element_size()
+        self.trace.stride_bytes[8] = (outputs.stride(0) * outputs.element_size()
+                                      if outputs.ndim == 4 else 0)
+        self.shape = _shape(banks, first.shape[1] if self.dense else first.slots, width,
+                            write_indices.shape[3], read_indices.shape[3],
+                            1 if self.dense else first.shared_initial_memory.shape[0],
+                            _index_code(write_indices, read_indices))
+
+    def set_step(self, step: int) -> None:
+        """Make the next launch run step ``step``."""
+
+        if not 0 <= step <= self.steps:
+            raise ValueError("trace step outside the trace")
+        self.step_index.fill_(step)
+
+    def layer_array(self):
+        """The per-layer C structs for the current state pointers (they
+        change when a slab grows or is trimmed)."""
+
+        count = len(self.tables)
+        layers = (nat.Layer * count)()
+        for l, table in enumerate(self.tables):
+            x = {name: tensor[0, l] for name, tensor in self.inputs.items()}
+            out = self.outputs[0, l] if self.outputs.ndim == 4 else self.outputs[l]
+            layers[l] = _step_layer(
+                None if self.dense else table, table if self.dense else None,
+                x["write_indices"], x["write_weights"], x["values"], x["input_gate"],
+                x["erase_gate"], x["forget_log_gate"], x["read_indices"], x["read_weights"],
+                out, None, None, None)
+        return layers
+
+    def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
+        """Enqueue ``steps`` consecutive step launches on the current stream:
+        steps start..start+steps-1, or, without ``start``, the steps the
+        device counter names."""
+
+        layers = self.layer_array() if layers is None else layers
+        if start is not None:
+            if start < 0 or start + steps > self.steps:
+                raise ValueError("trace launch runs past the recorded steps")
+            self.trace.step_index = None
+            self.trace.first_step = start
+        else:
+            self.trace.step_index = self.step_index.data_ptr()
+            self.trace.first_step = 0
+        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
+        nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps,
+                     nat.stream_handle(self.device)), "decode trace launch")

@@ -1,0 +1,120 @@
+// Shared declarations of libcowsdm's translation units: constants,
+// launch parameters and wave-level device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "cowsdm.h"
+
+namespace cowsdm_impl {
+
+constexpr int kWave = 64;
+constexpr int kBanksPerBlock = 4;           // waves (banks) per workgroup
+constexpr int kStepThreads = kWave * kBanksPerBlock;
+constexpr int kMaxLayers = 8;               // layers per step launch
+constexpr int kReadBatch = 16;              // read rows in flight per batch
+constexpr int kMaxReadSlots = 4;            // R <= 256 = 4 * 64
+constexpr int kSpinLimit = 1 << 16;         // bounded look-back wait
+constexpr int kFreeWindow = 256;            // prefetched free-stack entries
+constexpr int kTile = 2048;                 // ranking tile (entries)
+constexpr int kTileThreads = 256;
+constexpr int kPerThread = kTile / kTileThreads;
+
+constexpr uint32_t kStatusEmpty = 0;
+constexpr uint32_t kStatusAggregate = 1;
+constexpr uint32_t kStatusInclusive = 2;
+constexpr uint32_t kStatusPoison = 3;
+constexpr uint64_t kValueMask = (1ull << 30) - 1;
+
+// Record a message for cowsdm_last_error_string() and return `code`.
+int32_t fail(int32_t code, const char* fmt, ...);
+// 0, or the pending hipError_t of the last launch (recorded by fail()).
+int32_t launch_status(const char* where);
+const char* last_error();
+
+struct StepParams {
+  cowsdm_layer_t layer[kMaxLayers];
+  const int64_t* trace_step;     // device step counter, or null
+  int64_t* trace_ticket;         // [0] launch, [1 + layer] dense per-layer
+  int64_t trace_first;           // step of this launch when trace_step is null
+  int64_t trace_stride[9];
+  int32_t nlayers;
+  int32_t banks;
+  int32_t slots;
+  int32_t width;
+  int32_t writes;
+  int32_t reads;
+  int32_t templates;
+  int32_t blocks_per_layer;
+};
+
+// ------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ int rl(int x, int lane) {
+  return __builtin_amdgcn_readlane(x, lane);
+}
+
+__device__ __forceinline__ float rlf(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, kWave);
+  return v;
+}
+
+template <typename IDX>
+__device__ __forceinline__ int64_t load_index(const void* base, int64_t i) {
+  return static_cast<int64_t>(static_cast<const IDX*>(base)[i]);
+}
+
+template <int VEC>
+__device__ __forceinline__ void load_row(const float* p, float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+  } else if constexpr (VEC == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    x[0] = t.x; x[1] = t.y;
+  } else {
+    x[0] = *p;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_row(float* p, const float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  } else if constexpr (VEC == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+  } else {
+    *p = x[0];
+  }
+}
+
+__device__ __forceinline__ uint64_t atomic_load_u64(const int64_t* p) {
+  return static_cast<uint64_t>(__hip_atomic_load(
+      const_cast<int64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ void atomic_store_u64(int64_t* p, uint64_t v) {
+  __hip_atomic_store(p, static_cast<int64_t>(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
+                                              uint64_t value) {
+  return (static_cast<uint64_t>(epoch) << 32) |
+         (static_cast<uint64_t>(status) << 30) | (value & kValueMask);
+}
+
+
+}  // namespace cowsdm_impl

@@ -35,28 +35,21 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include "common.h"
 #include "cowsdm.h"
 
+namespace cowsdm_impl {
+
+template <typename IDX, bool DENSE>
+void launch_step_w(const StepParams& P, int blocks, int vec, hipStream_t stream);
+extern template void launch_step_w<int32_t, false>(const StepParams&, int, int, hipStream_t);
+extern template void launch_step_w<int32_t, true>(const StepParams&, int, int, hipStream_t);
+extern template void launch_step_w<int64_t, false>(const StepParams&, int, int, hipStream_t);
+extern template void launch_step_w<int64_t, true>(const StepParams&, int, int, hipStream_t);
+
 namespace {
-
-constexpr int kWave = 64;
-constexpr int kBanksPerBlock = 4;           // waves (banks) per workgroup
-constexpr int kStepThreads = kWave * kBanksPerBlock;
-constexpr int kMaxLayers = 8;               // layers per step launch
-constexpr int kReadBatch = 16;              // read rows in flight per batch
-constexpr int kMaxReadSlots = 4;            // R <= 256 = 4 * 64
-constexpr int kSpinLimit = 1 << 16;         // bounded look-back wait
-constexpr int kTile = 2048;                 // ranking tile (entries)
-constexpr int kTileThreads = 256;
-constexpr int kPerThread = kTile / kTileThreads;
-
-constexpr uint32_t kStatusEmpty = 0;
-constexpr uint32_t kStatusAggregate = 1;
-constexpr uint32_t kStatusInclusive = 2;
-constexpr uint32_t kStatusPoison = 3;
-constexpr uint64_t kValueMask = (1ull << 30) - 1;
-
 thread_local char g_error[512] = "";
+}  // namespace
 
 int32_t fail(int32_t code, const char* fmt, ...) {
   va_list args;
@@ -74,496 +67,7 @@ int32_t launch_status(const char* where) {
   return 0;
 }
 
-struct StepParams {
-  cowsdm_layer_t layer[kMaxLayers];
-  int32_t nlayers;
-  int32_t banks;
-  int32_t slots;
-  int32_t width;
-  int32_t writes;
-  int32_t reads;
-  int32_t templates;
-  int32_t blocks_per_layer;
-};
-
-// ------------------------------------------------------------ wave helpers
-
-__device__ __forceinline__ int rl(int x, int lane) {
-  return __builtin_amdgcn_readlane(x, lane);
-}
-
-__device__ __forceinline__ float rlf(float x, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
-
-__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
-__device__ __forceinline__ int wave_or(int v) {
-  for (int o = kWave / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, kWave);
-  return v;
-}
-
-template <typename IDX>
-__device__ __forceinline__ int64_t load_index(const void* base, int64_t i) {
-  return static_cast<int64_t>(static_cast<const IDX*>(base)[i]);
-}
-
-template <int VEC>
-__device__ __forceinline__ void load_row(const float* p, float (&x)[VEC]) {
-  if constexpr (VEC == 4) {
-    const float4 t = *reinterpret_cast<const float4*>(p);
-    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
-  } else if constexpr (VEC == 2) {
-    const float2 t = *reinterpret_cast<const float2*>(p);
-    x[0] = t.x; x[1] = t.y;
-  } else {
-    x[0] = *p;
-  }
-}
-
-template <int VEC>
-__device__ __forceinline__ void store_row(float* p, const float (&x)[VEC]) {
-  if constexpr (VEC == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
-  } else if constexpr (VEC == 2) {
-    *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
-  } else {
-    *p = x[0];
-  }
-}
-
-__device__ __forceinline__ uint64_t atomic_load_u64(const int64_t* p) {
-  return static_cast<uint64_t>(__hip_atomic_load(
-      const_cast<int64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-
-__device__ __forceinline__ void atomic_store_u64(int64_t* p, uint64_t v) {
-  __hip_atomic_store(p, static_cast<int64_t>(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
-                                              uint64_t value) {
-  return (static_cast<uint64_t>(epoch) << 32) |
-         (static_cast<uint64_t>(status) << 30) | (value & kValueMask);
-}
-
-// Exclusive prefix over banks [0, bank) of the per-bank first-touch counts,
-// by decoupled look-back.  Publishes this bank's aggregate first, then its
-// inclusive prefix.  Waits only on lower banks; each wait is bounded.
-__device__ int64_t bank_prefix(int64_t* slots, int bank, uint32_t epoch,
-                               int count, int lane, bool* poisoned) {
-  if (lane == 0) {
-    atomic_store_u64(&slots[bank], slot_word(epoch, kStatusAggregate, count));
-  }
-  int64_t exclusive = 0;
-  bool bad = false;
-  int end = bank;
-  while (end > 0) {
-    const int j = end - 1 - lane;
-    uint32_t status = kStatusInclusive;
-    int64_t value = 0;
-    if (j >= 0) {
-      uint64_t w = atomic_load_u64(&slots[j]);
-      int spins = 0;
-      while ((static_cast<uint32_t>(w >> 32) != epoch ||
-              ((w >> 30) & 3u) == kStatusEmpty) &&
-             spins < kSpinLimit) {
-        __builtin_amdgcn_s_sleep(1);
-        w = atomic_load_u64(&slots[j]);
-        ++spins;
-      }
-      if (static_cast<uint32_t>(w >> 32) != epoch ||
-          ((w >> 30) & 3u) == kStatusEmpty) {
-        status = kStatusPoison;
-      } else {
-        status = static_cast<uint32_t>((w >> 30) & 3u);
-        value = static_cast<int64_t>(w & kValueMask);
-      }
-    }
-    const uint64_t inclusive = __ballot(status == kStatusInclusive);
-    const uint64_t poison = __ballot(status == kStatusPoison);
-    if (inclusive != 0) {
-      const int k = __ffsll(static_cast<long long>(inclusive)) - 1;
-      const uint64_t upto = (k == 63) ? ~0ull : ((2ull << k) - 1);
-      if (poison & upto) bad = true;
-      exclusive += wave_sum64(lane <= k ? value : 0);
-      break;
-    }
-    if (poison != 0) bad = true;
-    exclusive += wave_sum64(value);
-    end -= kWave;
-  }
-  if (lane == 0) {
-    atomic_store_u64(&slots[bank],
-                     slot_word(epoch, bad ? kStatusPoison : kStatusInclusive,
-                               static_cast<uint64_t>(exclusive + count)));
-  }
-  *poisoned = bad;
-  return exclusive;
-}
-
-// --------------------------------------------------------- the fused step
-
-// One wave = one bank of one layer.  DENSE selects the dense-table control
-// (allocator.py:1612-1633): rows live at values[bank, slot] and there is no
-// map, free stack or scan; the row math is shared, so packed and dense
-// results are bit-identical.
-template <typename IDX, int MAXW, int VEC, bool DENSE>
-__global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
-  const int layer_id = blockIdx.x / P.blocks_per_layer;
-  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock +
-                   static_cast<int>(threadIdx.x) / kWave;
-  const int lane = static_cast<int>(threadIdx.x) % kWave;
-  if (layer_id >= P.nlayers || bank >= P.banks) return;
-  const cowsdm_layer_t& L = P.layer[layer_id];
-
-  const int N = P.slots;
-  const int D = P.width;
-  const int W = P.writes;
-  const int R = P.reads;
-  const int64_t C = L.capacity_rows;
-  const int64_t b = bank;
-
-  int lane_err = 0;
-
-  // ---- per-bank scalars
-  int64_t tmpl = 0;
-  if constexpr (!DENSE) {
-    tmpl = L.template_indices[b];
-    if (tmpl < 0 || tmpl >= P.templates) lane_err |= COWSDM_ERR_TEMPLATE;
-  }
-  const float forget = L.forget_log_gate[b];
-  const float in_gate = L.input_gate[b];
-  const float er_gate = L.erase_gate[b];
-  int64_t old_free = 0;
-  uint32_t epoch = 0;
-  if constexpr (!DENSE) {
-    old_free = *L.free_count;
-    epoch = static_cast<uint32_t>(L.scratch[COWSDM_SCRATCH_EPOCH]);
-    if (old_free < 0 || old_free > C) lane_err |= COWSDM_ERR_CORRUPT;
-  }
-
-  // ---- write routes: lane w < W
-  int widx = 0;
-  float wweight = 0.0f;
-  int wphys = -1;
-  if (lane < W) {
-    const int64_t x = load_index<IDX>(L.write_indices, b * W + lane);
-    wweight = L.write_weights[b * W + lane];
-    if (x < 0 || x >= N) {
-      lane_err |= COWSDM_ERR_WRITE_INDEX;
-    } else {
-      widx = static_cast<int>(x);
-    }
-  }
-  // ---- read routes: lane l holds r = l + 64 k
-  int ridx[kMaxReadSlots];
-  float rweight[kMaxReadSlots];
-  int rphys[kMaxReadSlots];
-  int rsrc[kMaxReadSlots];
-#pragma unroll
-  for (int k = 0; k < kMaxReadSlots; ++k) {
-    ridx[k] = 0;
-    rweight[k] = 0.0f;
-    rphys[k] = -1;
-    rsrc[k] = -1;
-    const int r = k * kWave + lane;
-    if (r < R) {
-      const int64_t x = load_index<IDX>(L.read_indices, b * R + r);
-      rweight[k] = L.read_weights[b * R + r];
-      if (x < 0 || x >= N) {
-        lane_err |= COWSDM_ERR_READ_INDEX;
-      } else {
-        ridx[k] = static_cast<int>(x);
-      }
-    }
-  }
-
-  // ---- map lookups (packed) for writes and reads
-  if constexpr (!DENSE) {
-    if (lane < W && !(lane_err & COWSDM_ERR_WRITE_INDEX)) {
-      wphys = L.logical_to_physical[b * N + widx];
-      if (wphys >= C) lane_err |= COWSDM_ERR_CORRUPT;
-    }
-#pragma unroll
-    for (int k = 0; k < kMaxReadSlots; ++k) {
-      const int r = k * kWave + lane;
-      if (r < R) {
-        rphys[k] = L.logical_to_physical[b * N + ridx[k]];
-        if (rphys[k] >= C) lane_err |= COWSDM_ERR_CORRUPT;
-      }
-    }
-  }
-
-  // ---- duplicate writes and read-after-write sources
-#pragma unroll
-  for (int j = 0; j < MAXW; ++j) {
-    if (j < W) {
-      const int other = rl(widx, j);
-      if (lane < W && j < lane && other == widx) lane_err |= COWSDM_ERR_DUP_WRITE;
-#pragma unroll
-      for (int k = 0; k < kMaxReadSlots; ++k) {
-        if (k * kWave + lane < R && ridx[k] == other) rsrc[k] = j;
-      }
-    }
-  }
-
-  const int err = wave_or(lane_err);
-  const bool ok = (err == 0);
-  const bool first = !DENSE && lane < W && wphys < 0;
-  const uint64_t first_mask = __ballot(first);
-  const int count = ok ? __popcll(first_mask) : 0;
-  const int rank = __popcll(first_mask & ((1ull << lane) - 1));
-
-  // ---- chunk 0 row loads, issued before the cross-bank wait
-  const float alpha = static_cast<float>(exp(static_cast<double>(forget)));
-  const float* const m0_bank =
-      DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
-  float* const table_bank = DENSE ? L.values + b * N * D : nullptr;
-  const int chunk_cols = kWave * VEC;
-  const int nchunks = (D + chunk_cols - 1) / chunk_cols;
-
-  float cur[MAXW][VEC];
-  float rv[kReadBatch][VEC];
-#pragma unroll
-  for (int j = 0; j < MAXW; ++j) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
-  }
-#pragma unroll
-  for (int i = 0; i < kReadBatch; ++i) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) rv[i][v] = 0.0f;
-  }
-
-  auto write_row_src = [&](int j) -> const float* {
-    const int slot = rl(widx, j);
-    if constexpr (DENSE) {
-      return table_bank + static_cast<int64_t>(slot) * D;
-    } else {
-      const int p = rl(wphys, j);
-      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
-                   : L.values + static_cast<int64_t>(p) * D;
-    }
-  };
-  auto read_meta = [&](const int (&arr)[kMaxReadSlots], int r) -> int {
-    const int k = r / kWave;
-    const int v = k == 0 ? arr[0] : k == 1 ? arr[1] : k == 2 ? arr[2] : arr[3];
-    return rl(v, r % kWave);
-  };
-  auto read_weight = [&](int r) -> float {
-    const int k = r / kWave;
-    const float v = k == 0 ? rweight[0] : k == 1 ? rweight[1]
-                  : k == 2 ? rweight[2] : rweight[3];
-    return rlf(v, r % kWave);
-  };
-  auto read_row_src = [&](int r) -> const float* {
-    const int slot = read_meta(ridx, r);
-    if constexpr (DENSE) {
-      return table_bank + static_cast<int64_t>(slot) * D;
-    } else {
-      const int p = read_meta(rphys, r);
-      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
-                   : L.values + static_cast<int64_t>(p) * D;
-    }
-  };
-  auto load_writes = [&](int chunk) {
-    const int col = chunk * chunk_cols + lane * VEC;
-#pragma unroll
-    for (int j = 0; j < MAXW; ++j) {
-      if (j < W && ok) {
-        const float* src = write_row_src(j);
-        if (col < D) load_row<VEC>(src + col, cur[j]);
-      }
-    }
-  };
-  auto load_read_batch = [&](int chunk, int r0) {
-    const int col = chunk * chunk_cols + lane * VEC;
-#pragma unroll
-    for (int i = 0; i < kReadBatch; ++i) {
-      const int r = r0 + i;
-      if (r < R && ok && read_meta(rsrc, r) < 0) {
-        const float* src = read_row_src(r);
-        if (col < D) load_row<VEC>(src + col, rv[i]);
-      }
-    }
-  };
-
-  load_writes(0);
-  load_read_batch(0, 0);
-
-  // ---- free-stack resolution (packed): bank-major pop positions
-  bool fits = true;
-  int new_row = -1;
-  if constexpr (!DENSE) {
-    bool poisoned = false;
-    int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
-    const int64_t prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
-    fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
-    int bad_row = 0;
-    if (fits && first) {
-      const int64_t pos = old_free - 1 - (prefix + rank);
-      new_row = L.free_rows[pos];
-      if (new_row < 0 || new_row >= C) bad_row = 1;
-    }
-    if (__ballot(bad_row) != 0) {
-      fits = false;
-      if (lane == 0) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_CORRUPT),
-                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    if (lane == 0) {
-      if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
-      if (poisoned) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  const bool commit = ok && fits;
-  const int dest = DENSE ? widx : (first ? new_row : wphys);
-
-  // ---- gated-delta update and sparse read, chunk by chunk
-  for (int chunk = 0; chunk < nchunks; ++chunk) {
-    if (chunk > 0) {
-      load_writes(chunk);
-      load_read_batch(chunk, 0);
-    }
-    const int col = chunk * chunk_cols + lane * VEC;
-    const bool col_ok = col < D;
-    float vin[VEC];
-    float acc[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) { vin[v] = 0.0f; acc[v] = 0.0f; }
-    if (col_ok) load_row<VEC>(L.step_values + b * D + col, vin);
-
-    if (ok) {
-      // decayed = current * exp(forget); retrieved = sum_w weight_w * decayed_w
-      float ret[VEC];
-#pragma unroll
-      for (int j = 0; j < MAXW; ++j) {
-        if (j < W) {
-          const float wj = rlf(wweight, j);
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            cur[j][v] = cur[j][v] * alpha;
-            const float term = wj * cur[j][v];
-            ret[v] = (j == 0) ? term : ret[v] + term;
-          }
-        }
-      }
-      // delta = in_gate * value - erase_gate * retrieved
-      // updated_w = decayed_w + weight_w * delta
-      float delta[VEC];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const float a = in_gate * vin[v];
-        const float e = er_gate * ret[v];
-        delta[v] = a - e;
-      }
-#pragma unroll
-      for (int j = 0; j < MAXW; ++j) {
-        if (j < W) {
-          const float wj = rlf(wweight, j);
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            const float t = wj * delta[v];
-            cur[j][v] = cur[j][v] + t;
-          }
-        }
-      }
-      // reading = sum_r weight_r * visible_r, reads after this step's writes
-      for (int r0 = 0; r0 < R; r0 += kReadBatch) {
-        if (r0 > 0) load_read_batch(chunk, r0);
-#pragma unroll
-        for (int i = 0; i < kReadBatch; ++i) {
-          const int r = r0 + i;
-          if (r < R) {
-            const int src = read_meta(rsrc, r);
-            float x[VEC];
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) x[v] = rv[i][v];
-            if (src >= 0) {
-#pragma unroll
-              for (int j = 0; j < MAXW; ++j) {
-                if (j == src) {
-#pragma unroll
-                  for (int v = 0; v < VEC; ++v) x[v] = cur[j][v];
-                }
-              }
-            }
-            const float wr = read_weight(r);
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) {
-              const float term = wr * x[v];
-              acc[v] = (r == 0) ? term : acc[v] + term;
-            }
-          }
-        }
-      }
-    }
-    if (col_ok) store_row<VEC>(L.output + b * D + col, acc);
-    if (commit) {
-#pragma unroll
-      for (int j = 0; j < MAXW; ++j) {
-        if (j < W) {
-          const int row = rl(dest, j);
-          float* dst = DENSE ? table_bank + static_cast<int64_t>(row) * D
-                             : L.values + static_cast<int64_t>(row) * D;
-          if (col_ok) store_row<VEC>(dst + col, cur[j]);
-        }
-      }
-    }
-  }
-
-  if constexpr (!DENSE) {
-    if (commit && first) L.logical_to_physical[b * N + widx] = new_row;
-    if (lane == 0) {
-      if (L.first_touches_out) L.first_touches_out[b] = commit ? count : 0;
-      if (L.repeated_writes_out) L.repeated_writes_out[b] = commit ? W - count : W;
-      if (err) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(err), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (commit && count > 0) {
-        __hip_atomic_fetch_add(&L.scratch[COWSDM_SCRATCH_SERVED],
-                               static_cast<int64_t>(count), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      }
-      const int64_t ticket = __hip_atomic_fetch_add(
-          &L.scratch[COWSDM_SCRATCH_TICKET], int64_t{1}, __ATOMIC_ACQ_REL,
-          __HIP_MEMORY_SCOPE_AGENT);
-      if (ticket == P.banks - 1) {
-        const int64_t served = __hip_atomic_load(
-            &L.scratch[COWSDM_SCRATCH_SERVED], __ATOMIC_ACQUIRE,
-            __HIP_MEMORY_SCOPE_AGENT);
-        const int64_t now_free = old_free - served;
-        *L.free_count = static_cast<int32_t>(now_free);
-        if (L.allocated_rows_out) {
-          *L.allocated_rows_out = static_cast<int32_t>(C - now_free);
-        }
-        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_SERVED], 0);
-        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_TICKET], 0);
-        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_EPOCH],
-                         static_cast<uint64_t>(epoch + 1u));
-      }
-    }
-  } else {
-    if (lane == 0 && err && L.scratch) {
-      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                            static_cast<int64_t>(err), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
+const char* last_error() { return g_error; }
 
 // Validation before a step (validate_routes=True, or a packed state whose
 // capacity has no proof): bounds, duplicate writes, first touches vs the
@@ -1155,28 +659,9 @@ int32_t check_layer(const cowsdm_layer_t& L, bool dense) {
   return 0;
 }
 
-template <typename IDX, int MAXW, int VEC, bool DENSE>
-void launch_step(const StepParams& P, int blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((sdm_step_kernel<IDX, MAXW, VEC, DENSE>), dim3(blocks),
-                     dim3(kStepThreads), 0, stream, P);
-}
-
-template <typename IDX, int MAXW, bool DENSE>
-void launch_step_vec(const StepParams& P, int blocks, int vec, hipStream_t stream) {
-  if (vec == 4) launch_step<IDX, MAXW, 4, DENSE>(P, blocks, stream);
-  else if (vec == 2) launch_step<IDX, MAXW, 2, DENSE>(P, blocks, stream);
-  else launch_step<IDX, MAXW, 1, DENSE>(P, blocks, stream);
-}
-
-template <typename IDX, bool DENSE>
-void launch_step_w(const StepParams& P, int blocks, int vec, hipStream_t stream) {
-  if (P.writes <= 4) launch_step_vec<IDX, 4, DENSE>(P, blocks, vec, stream);
-  else if (P.writes <= 16) launch_step_vec<IDX, 16, DENSE>(P, blocks, vec, stream);
-  else launch_step_vec<IDX, 64, DENSE>(P, blocks, vec, stream);
-}
-
 int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
-                 const cowsdm_shape_t* shape, bool dense, hipStream_t stream) {
+                 const cowsdm_shape_t* shape, bool dense, hipStream_t stream,
+                 const cowsdm_trace_t* trace = nullptr, int32_t steps = 1) {
   if (int32_t e = check_shape(shape)) return e;
   if (!layers || nlayers <= 0) return fail(COWSDM_EARG, "no layers given");
   for (int32_t i = 0; i < nlayers; ++i) {
@@ -1197,7 +682,24 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
                            (dense ? 0 : reinterpret_cast<uintptr_t>(L.shared_initial_memory));
     while (vec > 1 && (bits % (4u * vec)) != 0) vec /= 2;
   }
+  if (trace) {
+    if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
+    if (trace->first_step < 0) return fail(COWSDM_EARG, "trace: negative first step");
+    if (nlayers > kMaxLayers) {
+      return fail(COWSDM_ELIMIT, "trace launches take at most %d layers", kMaxLayers);
+    }
+    for (int k = 0; k < 9; ++k) {
+      if (trace->stride_bytes[k] % 4 != 0) return fail(COWSDM_EARG, "trace: stride not float aligned");
+      // every step's rows must keep the vector alignment of step 0
+      while (vec > 1 && (trace->stride_bytes[k] % (4 * vec)) != 0) vec /= 2;
+    }
+  }
+  if (steps < 0) return fail(COWSDM_EARG, "steps must be non-negative");
   StepParams P;
+  P.trace_step = trace ? trace->step_index : nullptr;
+  P.trace_ticket = trace ? trace->ticket : nullptr;
+  P.trace_first = trace ? trace->first_step : 0;
+  for (int k = 0; k < 9; ++k) P.trace_stride[k] = trace ? trace->stride_bytes[k] : 0;
   P.banks = static_cast<int32_t>(shape->banks);
   P.slots = static_cast<int32_t>(shape->slots);
   P.width = static_cast<int32_t>(shape->width);
@@ -1211,14 +713,17 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     for (int32_t i = 0; i < kMaxLayers; ++i) P.layer[i] = layers[start + (i < n ? i : 0)];
     const int blocks = P.blocks_per_layer * n;
     const bool i64 = shape->index_dtype == COWSDM_INDEX_INT64;
-    if (dense) {
-      if (i64) launch_step_w<int64_t, true>(P, blocks, vec, stream);
-      else launch_step_w<int32_t, true>(P, blocks, vec, stream);
-    } else {
-      if (i64) launch_step_w<int64_t, false>(P, blocks, vec, stream);
-      else launch_step_w<int32_t, false>(P, blocks, vec, stream);
+    for (int32_t it = 0; it < steps; ++it) {
+      if (trace && !trace->step_index) P.trace_first = trace->first_step + it;
+      if (dense) {
+        if (i64) launch_step_w<int64_t, true>(P, blocks, vec, stream);
+        else launch_step_w<int32_t, true>(P, blocks, vec, stream);
+      } else {
+        if (i64) launch_step_w<int64_t, false>(P, blocks, vec, stream);
+        else launch_step_w<int32_t, false>(P, blocks, vec, stream);
+      }
+      if (int32_t e = launch_status(dense ? "dense step" : "packed step")) return e;
     }
-    if (int32_t e = launch_status(dense ? "dense step" : "packed step")) return e;
   }
   return 0;
 }
@@ -1246,7 +751,9 @@ int32_t rank_apply(const RankSource& src, const Workspace& ws, const RankApply& 
   return launch_status("rank apply");
 }
 
-}  // namespace
+}  // namespace cowsdm_impl
+
+using namespace cowsdm_impl;
 
 // ================================================================ C ABI
 
@@ -1254,7 +761,7 @@ extern "C" {
 
 int32_t cowsdm_abi_version(void) { return COWSDM_ABI_VERSION; }
 
-const char* cowsdm_last_error_string(void) { return g_error; }
+const char* cowsdm_last_error_string(void) { return last_error(); }
 
 int64_t cowsdm_step_scratch_words(int64_t banks) {
   return banks < 0 ? -1 : COWSDM_SCRATCH_SLOTS + banks;
@@ -1284,6 +791,20 @@ int32_t cowsdm_dense_step(const cowsdm_layer_t* layer, const cowsdm_shape_t* sha
 int32_t cowsdm_dense_step_layers(const cowsdm_layer_t* layers, int32_t nlayers,
                                  const cowsdm_shape_t* shape, void* stream) {
   return run_step(layers, nlayers, shape, true, as_stream(stream));
+}
+
+int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
+                                 const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                                 int32_t steps, void* stream) {
+  if (!trace) return fail(COWSDM_EARG, "trace is null");
+  return run_step(layers, nlayers, shape, false, as_stream(stream), trace, steps);
+}
+
+int32_t cowsdm_dense_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
+                                const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                                int32_t steps, void* stream) {
+  if (!trace) return fail(COWSDM_EARG, "trace is null");
+  return run_step(layers, nlayers, shape, true, as_stream(stream), trace, steps);
 }
 
 int32_t cowsdm_step_precheck(const cowsdm_layer_t* layer, const cowsdm_shape_t* shape,

@@ -1,0 +1,494 @@
+// The fused copy-on-write SDM step kernel (packed and dense-table forms)
+// and its launchers; each step_*.hip file instantiates one index type
+// and one form.
+#pragma once
+
+#include "common.h"
+
+namespace cowsdm_impl {
+
+// Exclusive prefix over banks [0, bank) of the per-bank first-touch counts,
+// by decoupled look-back.  Publishes this bank's aggregate first, then its
+// inclusive prefix.  Waits only on lower banks; each wait is bounded.
+__device__ inline int64_t bank_prefix(int64_t* slots, int bank, uint32_t epoch,
+                               int count, int lane, bool* poisoned) {
+  if (lane == 0) {
+    atomic_store_u64(&slots[bank], slot_word(epoch, kStatusAggregate, count));
+  }
+  int64_t exclusive = 0;
+  bool bad = false;
+  int end = bank;
+  while (end > 0) {
+    const int j = end - 1 - lane;
+    uint32_t status = kStatusInclusive;
+    int64_t value = 0;
+    if (j >= 0) {
+      uint64_t w = atomic_load_u64(&slots[j]);
+      int spins = 0;
+      while ((static_cast<uint32_t>(w >> 32) != epoch ||
+              ((w >> 30) & 3u) == kStatusEmpty) &&
+             spins < kSpinLimit) {
+        __builtin_amdgcn_s_sleep(1);
+        w = atomic_load_u64(&slots[j]);
+        ++spins;
+      }
+      if (static_cast<uint32_t>(w >> 32) != epoch ||
+          ((w >> 30) & 3u) == kStatusEmpty) {
+        status = kStatusPoison;
+      } else {
+        status = static_cast<uint32_t>((w >> 30) & 3u);
+        value = static_cast<int64_t>(w & kValueMask);
+      }
+    }
+    const uint64_t inclusive = __ballot(status == kStatusInclusive);
+    const uint64_t poison = __ballot(status == kStatusPoison);
+    if (inclusive != 0) {
+      const int k = __ffsll(static_cast<long long>(inclusive)) - 1;
+      const uint64_t upto = (k == 63) ? ~0ull : ((2ull << k) - 1);
+      if (poison & upto) bad = true;
+      exclusive += wave_sum64(lane <= k ? value : 0);
+      break;
+    }
+    if (poison != 0) bad = true;
+    exclusive += wave_sum64(value);
+    end -= kWave;
+  }
+  if (lane == 0) {
+    atomic_store_u64(&slots[bank],
+                     slot_word(epoch, bad ? kStatusPoison : kStatusInclusive,
+                               static_cast<uint64_t>(exclusive + count)));
+  }
+  *poisoned = bad;
+  return exclusive;
+}
+
+// --------------------------------------------------------- the fused step
+
+// One wave = one bank of one layer.  DENSE selects the dense-table control
+// (allocator.py:1612-1633): rows live at values[bank, slot] and there is no
+// map, free stack or scan; the row math is shared, so packed and dense
+// results are bit-identical.
+template <typename IDX, int MAXW, int VEC, bool DENSE>
+__global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
+  const int layer_id = blockIdx.x / P.blocks_per_layer;
+  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock +
+                   static_cast<int>(threadIdx.x) / kWave;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  if (layer_id >= P.nlayers || bank >= P.banks) return;
+  const cowsdm_layer_t& L = P.layer[layer_id];
+  const int64_t trace_s = P.trace_step ? *P.trace_step : P.trace_first;
+  auto step_ptr = [&](const void* base, int k) -> const char* {
+    return static_cast<const char*>(base) + trace_s * P.trace_stride[k];
+  };
+  const void* const write_indices = step_ptr(L.write_indices, 0);
+  const float* const write_weights = reinterpret_cast<const float*>(step_ptr(L.write_weights, 1));
+  const float* const step_values = reinterpret_cast<const float*>(step_ptr(L.step_values, 2));
+  const float* const input_gate = reinterpret_cast<const float*>(step_ptr(L.input_gate, 3));
+  const float* const erase_gate = reinterpret_cast<const float*>(step_ptr(L.erase_gate, 4));
+  const float* const forget_gate = reinterpret_cast<const float*>(step_ptr(L.forget_log_gate, 5));
+  const void* const read_indices = step_ptr(L.read_indices, 6);
+  const float* const read_weights = reinterpret_cast<const float*>(step_ptr(L.read_weights, 7));
+  float* const output = const_cast<float*>(reinterpret_cast<const float*>(step_ptr(L.output, 8)));
+
+  const int N = P.slots;
+  const int D = P.width;
+  const int W = P.writes;
+  const int R = P.reads;
+  const int64_t C = L.capacity_rows;
+  const int64_t b = bank;
+
+  int lane_err = 0;
+
+  // ---- per-bank scalars
+  int64_t tmpl = 0;
+  if constexpr (!DENSE) {
+    tmpl = L.template_indices[b];
+    if (tmpl < 0 || tmpl >= P.templates) lane_err |= COWSDM_ERR_TEMPLATE;
+  }
+  const float forget = forget_gate[b];
+  const float in_gate = input_gate[b];
+  const float er_gate = erase_gate[b];
+  int64_t old_free = 0;
+  uint32_t epoch = 0;
+  // top kFreeWindow entries of the free stack, entry t (t-th from the top)
+  // held by lane t % 64 in register t / 64: pops rarely reach deeper, so the
+  // pop needs no dependent load after the bank-order scan
+  int free_top[kFreeWindow / kWave];
+  if constexpr (!DENSE) {
+    old_free = *L.free_count;
+    epoch = static_cast<uint32_t>(L.scratch[COWSDM_SCRATCH_EPOCH]);
+    if (old_free < 0 || old_free > C) lane_err |= COWSDM_ERR_CORRUPT;
+#pragma unroll
+    for (int k = 0; k < kFreeWindow / kWave; ++k) {
+      const int64_t pos = old_free - 1 - (k * kWave + lane);
+      free_top[k] = (pos >= 0 && pos < C) ? L.free_rows[pos] : -1;
+    }
+  }
+
+  // ---- write routes: lane w < W
+  int widx = 0;
+  float wweight = 0.0f;
+  int wphys = -1;
+  if (lane < W) {
+    const int64_t x = load_index<IDX>(write_indices, b * W + lane);
+    wweight = write_weights[b * W + lane];
+    if (x < 0 || x >= N) {
+      lane_err |= COWSDM_ERR_WRITE_INDEX;
+    } else {
+      widx = static_cast<int>(x);
+    }
+  }
+  // ---- read routes: lane l holds r = l + 64 k
+  int ridx[kMaxReadSlots];
+  float rweight[kMaxReadSlots];
+  int rphys[kMaxReadSlots];
+  int rsrc[kMaxReadSlots];
+#pragma unroll
+  for (int k = 0; k < kMaxReadSlots; ++k) {
+    ridx[k] = 0;
+    rweight[k] = 0.0f;
+    rphys[k] = -1;
+    rsrc[k] = -1;
+    const int r = k * kWave + lane;
+    if (r < R) {
+      const int64_t x = load_index<IDX>(read_indices, b * R + r);
+      rweight[k] = read_weights[b * R + r];
+      if (x < 0 || x >= N) {
+        lane_err |= COWSDM_ERR_READ_INDEX;
+      } else {
+        ridx[k] = static_cast<int>(x);
+      }
+    }
+  }
+
+  // ---- map lookups (packed) for writes and reads
+  if constexpr (!DENSE) {
+    if (lane < W && !(lane_err & COWSDM_ERR_WRITE_INDEX)) {
+      wphys = L.logical_to_physical[b * N + widx];
+      if (wphys >= C) lane_err |= COWSDM_ERR_CORRUPT;
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxReadSlots; ++k) {
+      const int r = k * kWave + lane;
+      if (r < R) {
+        rphys[k] = L.logical_to_physical[b * N + ridx[k]];
+        if (rphys[k] >= C) lane_err |= COWSDM_ERR_CORRUPT;
+      }
+    }
+  }
+
+  // ---- duplicate writes and read-after-write sources
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+    if (j < W) {
+      const int other = rl(widx, j);
+      if (lane < W && j < lane && other == widx) lane_err |= COWSDM_ERR_DUP_WRITE;
+#pragma unroll
+      for (int k = 0; k < kMaxReadSlots; ++k) {
+        if (k * kWave + lane < R && ridx[k] == other) rsrc[k] = j;
+      }
+    }
+  }
+
+  const int err = wave_or(lane_err);
+  const bool ok = (err == 0);
+  const bool first = !DENSE && lane < W && wphys < 0;
+  const uint64_t first_mask = __ballot(first);
+  const int count = ok ? __popcll(first_mask) : 0;
+  const int rank = __popcll(first_mask & ((1ull << lane) - 1));
+
+  // ---- chunk 0 row loads, issued before the cross-bank wait
+  const float alpha = static_cast<float>(exp(static_cast<double>(forget)));
+  const float* const m0_bank =
+      DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
+  float* const table_bank = DENSE ? L.values + b * N * D : nullptr;
+  const int chunk_cols = kWave * VEC;
+  const int nchunks = (D + chunk_cols - 1) / chunk_cols;
+
+  float cur[MAXW][VEC];
+  float rv[kReadBatch][VEC];
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kReadBatch; ++i) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) rv[i][v] = 0.0f;
+  }
+
+  auto write_row_src = [&](int j) -> const float* {
+    const int slot = rl(widx, j);
+    if constexpr (DENSE) {
+      return table_bank + static_cast<int64_t>(slot) * D;
+    } else {
+      const int p = rl(wphys, j);
+      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
+                   : L.values + static_cast<int64_t>(p) * D;
+    }
+  };
+  auto read_meta = [&](const int (&arr)[kMaxReadSlots], int r) -> int {
+    const int k = r / kWave;
+    const int v = k == 0 ? arr[0] : k == 1 ? arr[1] : k == 2 ? arr[2] : arr[3];
+    return rl(v, r % kWave);
+  };
+  auto read_weight = [&](int r) -> float {
+    const int k = r / kWave;
+    const float v = k == 0 ? rweight[0] : k == 1 ? rweight[1]
+                  : k == 2 ? rweight[2] : rweight[3];
+    return rlf(v, r % kWave);
+  };
+  auto read_row_src = [&](int r) -> const float* {
+    const int slot = read_meta(ridx, r);
+    if constexpr (DENSE) {
+      return table_bank + static_cast<int64_t>(slot) * D;
+    } else {
+      const int p = read_meta(rphys, r);
+      return p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
+                   : L.values + static_cast<int64_t>(p) * D;
+    }
+  };
+  auto load_writes = [&](int chunk) {
+    const int col = chunk * chunk_cols + lane * VEC;
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) {
+      if (j < W && ok) {
+        const float* src = write_row_src(j);
+        if (col < D) load_row<VEC>(src + col, cur[j]);
+      }
+    }
+  };
+  auto load_read_batch = [&](int chunk, int r0) {
+    const int col = chunk * chunk_cols + lane * VEC;
+#pragma unroll
+    for (int i = 0; i < kReadBatch; ++i) {
+      const int r = r0 + i;
+      if (r < R && ok && read_meta(rsrc, r) < 0) {
+        const float* src = read_row_src(r);
+        if (col < D) load_row<VEC>(src + col, rv[i]);
+      }
+    }
+  };
+
+  load_writes(0);
+  load_read_batch(0, 0);
+
+  // ---- free-stack resolution (packed): bank-major pop positions
+  bool fits = true;
+  int new_row = -1;
+  if constexpr (!DENSE) {
+    bool poisoned = false;
+    int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
+    const int64_t prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
+    fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
+    int bad_row = 0;
+    const int64_t from_top = prefix + rank;  // pop position counted from the top
+    const int src_lane = static_cast<int>(from_top % kWave);
+    int window_row = -1;
+#pragma unroll
+    for (int k = 0; k < kFreeWindow / kWave; ++k) {
+      const int v = __shfl(free_top[k], src_lane, kWave);
+      if (from_top / kWave == k) window_row = v;
+    }
+    if (fits && first) {
+      new_row = from_top < kFreeWindow ? window_row : L.free_rows[old_free - 1 - from_top];
+      if (new_row < 0 || new_row >= C) bad_row = 1;
+    }
+    if (__ballot(bad_row) != 0) {
+      fits = false;
+      if (lane == 0) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_CORRUPT),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (lane == 0) {
+      if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
+      if (poisoned) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  const bool commit = ok && fits;
+  const int dest = DENSE ? widx : (first ? new_row : wphys);
+
+  // ---- gated-delta update and sparse read, chunk by chunk
+  for (int chunk = 0; chunk < nchunks; ++chunk) {
+    if (chunk > 0) {
+      load_writes(chunk);
+      load_read_batch(chunk, 0);
+    }
+    const int col = chunk * chunk_cols + lane * VEC;
+    const bool col_ok = col < D;
+    float vin[VEC];
+    float acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) { vin[v] = 0.0f; acc[v] = 0.0f; }
+    if (col_ok) load_row<VEC>(step_values + b * D + col, vin);
+
+    if (ok) {
+      // decayed = current * exp(forget); retrieved = sum_w weight_w * decayed_w
+      float ret[VEC];
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const float wj = rlf(wweight, j);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            cur[j][v] = cur[j][v] * alpha;
+            const float term = wj * cur[j][v];
+            ret[v] = (j == 0) ? term : ret[v] + term;
+          }
+        }
+      }
+      // delta = in_gate * value - erase_gate * retrieved
+      // updated_w = decayed_w + weight_w * delta
+      float delta[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float a = in_gate * vin[v];
+        const float e = er_gate * ret[v];
+        delta[v] = a - e;
+      }
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const float wj = rlf(wweight, j);
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float t = wj * delta[v];
+            cur[j][v] = cur[j][v] + t;
+          }
+        }
+      }
+      // reading = sum_r weight_r * visible_r, reads after this step's writes
+      for (int r0 = 0; r0 < R; r0 += kReadBatch) {
+        if (r0 > 0) load_read_batch(chunk, r0);
+#pragma unroll
+        for (int i = 0; i < kReadBatch; ++i) {
+          const int r = r0 + i;
+          if (r < R) {
+            const int src = read_meta(rsrc, r);
+            float x[VEC];
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) x[v] = rv[i][v];
+            if (src >= 0) {
+#pragma unroll
+              for (int j = 0; j < MAXW; ++j) {
+                if (j == src) {
+#pragma unroll
+                  for (int v = 0; v < VEC; ++v) x[v] = cur[j][v];
+                }
+              }
+            }
+            const float wr = read_weight(r);
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) {
+              const float term = wr * x[v];
+              acc[v] = (r == 0) ? term : acc[v] + term;
+            }
+          }
+        }
+      }
+    }
+    if (col_ok) store_row<VEC>(output + b * D + col, acc);
+    if (commit) {
+#pragma unroll
+      for (int j = 0; j < MAXW; ++j) {
+        if (j < W) {
+          const int row = rl(dest, j);
+          float* dst = DENSE ? table_bank + static_cast<int64_t>(row) * D
+                             : L.values + static_cast<int64_t>(row) * D;
+          if (col_ok) store_row<VEC>(dst + col, cur[j]);
+        }
+      }
+    }
+  }
+
+  bool closed_layer = false;
+  if constexpr (!DENSE) {
+    if (commit && first) L.logical_to_physical[b * N + widx] = new_row;
+    if (lane == 0) {
+      if (L.first_touches_out) L.first_touches_out[b] = commit ? count : 0;
+      if (L.repeated_writes_out) L.repeated_writes_out[b] = commit ? W - count : W;
+      if (err) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(err), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // one relaxed atomic carries both the finished-bank count (high word)
+      // and the rows this bank popped (low word): the last bank to arrive
+      // gets the layer's total from its own return value, so no fence and
+      // no second atomic are needed
+      const int64_t mine = commit ? count : 0;
+      const uint64_t before = static_cast<uint64_t>(__hip_atomic_fetch_add(
+          &L.scratch[COWSDM_SCRATCH_TICKET], static_cast<int64_t>((1ull << 32) | mine),
+          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      if (static_cast<int64_t>(before >> 32) == P.banks - 1) {
+        closed_layer = true;
+        const int64_t served = static_cast<int64_t>(before & 0xffffffffull) + mine;
+        const int64_t now_free = old_free - served;
+        *L.free_count = static_cast<int32_t>(now_free);
+        if (L.allocated_rows_out) {
+          *L.allocated_rows_out = static_cast<int32_t>(C - now_free);
+        }
+        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_TICKET], 0);
+        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_EPOCH],
+                         static_cast<uint64_t>(epoch + 1u));
+      }
+    }
+  } else {
+    if (lane == 0 && err && L.scratch) {
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(err), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // device-counted trace launches: the bank that closes the last layer moves
+  // the trace to the next step (every bank read *trace_step before its
+  // ticket); tickets are per layer, then per launch, to spread the atomics
+  if (P.trace_step && lane == 0) {
+    if constexpr (DENSE) {
+      int64_t* layer_ticket = P.trace_ticket + 1 + layer_id;
+      const int64_t done = __hip_atomic_fetch_add(layer_ticket, int64_t{1}, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      closed_layer = (done == P.banks - 1);
+      if (closed_layer) atomic_store_u64(layer_ticket, 0);
+    }
+    if (closed_layer) {
+      const int64_t layers_done = __hip_atomic_fetch_add(
+          P.trace_ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (layers_done == P.nlayers - 1) {
+        atomic_store_u64(P.trace_ticket, 0);
+        atomic_store_u64(const_cast<int64_t*>(P.trace_step),
+                         static_cast<uint64_t>(trace_s + 1));
+      }
+    }
+  }
+}
+
+template <typename IDX, int MAXW, int VEC, bool DENSE>
+void launch_step(const StepParams& P, int blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((sdm_step_kernel<IDX, MAXW, VEC, DENSE>), dim3(blocks),
+                     dim3(kStepThreads), 0, stream, P);
+}
+
+template <typename IDX, int MAXW, bool DENSE>
+void launch_step_vec(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+  if (vec == 4) launch_step<IDX, MAXW, 4, DENSE>(P, blocks, stream);
+  else if (vec == 2) launch_step<IDX, MAXW, 2, DENSE>(P, blocks, stream);
+  else launch_step<IDX, MAXW, 1, DENSE>(P, blocks, stream);
+}
+
+template <typename IDX, bool DENSE>
+void launch_step_w(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+  if (P.writes <= 4) launch_step_vec<IDX, 4, DENSE>(P, blocks, vec, stream);
+  else if (P.writes <= 16) launch_step_vec<IDX, 16, DENSE>(P, blocks, vec, stream);
+  else launch_step_vec<IDX, 64, DENSE>(P, blocks, vec, stream);
+}
+
+
+}  // namespace cowsdm_impl

@@ -56,11 +56,12 @@ extern "C" {
 #define COWSDM_ERR_LOOKBACK 0x40     /* bank-order scan did not complete  */
 
 /* Word offsets inside the per-layer step scratch (int64 words). */
+/* EPOCH retires the previous launch's scan slots; TICKET packs the number
+ * of banks done (high 32 bits) with the rows they popped (low 32 bits);
+ * ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's scan slot. */
 #define COWSDM_SCRATCH_EPOCH 0
 #define COWSDM_SCRATCH_TICKET 1
-#define COWSDM_SCRATCH_SERVED 2
 #define COWSDM_SCRATCH_ERRORS 3
-#define COWSDM_SCRATCH_PRECHECK 4
 #define COWSDM_SCRATCH_SLOTS 8
 
 /* Shape shared by every layer of one step launch. */
@@ -104,6 +105,23 @@ typedef struct cowsdm_layer {
   int32_t* allocated_rows_out;  /* scalar or null */
 } cowsdm_layer_t;
 
+/* Consecutive launches over device-resident inputs of many decode steps;
+ * per-step inputs (and the output) sit at base + step * stride_bytes[k],
+ * k in the order write_indices, write_weights, step_values, input_gate,
+ * erase_gate, forget_log_gate, read_indices, read_weights, output.
+ * With step_index null, launch i runs step first_step + i (the host
+ * computes the offsets).  With step_index set, each launch reads the step
+ * from *step_index and the last bank to finish advances it by one, so the
+ * launches can be captured once in a hipGraph and replayed; ticket then
+ * points at 1 + nlayers int64 words that are zero before the first launch
+ * and stay zero between launches. */
+typedef struct cowsdm_trace {
+  int64_t* step_index;
+  int64_t* ticket;
+  int64_t first_step;
+  int64_t stride_bytes[9];
+} cowsdm_trace_t;
+
 /* ---------------------------------------------------------------- info */
 
 int32_t cowsdm_abi_version(void);
@@ -132,6 +150,16 @@ int32_t cowsdm_packed_step_layers(const cowsdm_layer_t* layers,
                                   int32_t nlayers,
                                   const cowsdm_shape_t* shape, void* stream);
 
+/* `steps` consecutive launches of cowsdm_packed_step_layers, each on the
+ * decode step *trace->step_index names (see cowsdm_trace_t).  Fixed
+ * arguments make the sequence capturable in one hipGraph.  No counterpart
+ * in the reference: for callers holding routes of many steps, such as
+ * synthetic-route benchmarks and teacher-forced decode. */
+int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
+                                 const cowsdm_shape_t* shape,
+                                 const cowsdm_trace_t* trace, int32_t steps,
+                                 void* stream);
+
 /* Dense-table control step on values = memory [B, N, D].
  * Replaces _dense_sdm_sparse_step_triton, allocator.py:1322-1378 (kernel
  * 367-460), with the torch semantics of 1612-1633. */
@@ -139,6 +167,11 @@ int32_t cowsdm_dense_step(const cowsdm_layer_t* layer,
                           const cowsdm_shape_t* shape, void* stream);
 int32_t cowsdm_dense_step_layers(const cowsdm_layer_t* layers, int32_t nlayers,
                                  const cowsdm_shape_t* shape, void* stream);
+/* Trace form of the dense control (see cowsdm_packed_step_trace). */
+int32_t cowsdm_dense_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
+                                const cowsdm_shape_t* shape,
+                                const cowsdm_trace_t* trace, int32_t steps,
+                                void* stream);
 
 /* Route and capacity validation before a step; writes the COWSDM_ERR_*
  * bits it finds to *result (int64, device).  check_capacity counts the
