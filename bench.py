@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Decode throughput of the packed copy-on-write SDM step on one MI355X.
 
-Workload (BASELINE config 2 at batch 64): L=7 SDM layers, H=1 memory head,
+Workload (the benchmark configuration at batch 64): L=7 SDM layers, H=1 memory head,
 N=256 slots, D=128, top-4 writes / top-16 reads drawn uniformly, FP32 state.
 A 256-token prefix runs through the dense-table kernel, each layer's union of
 written slots is packed into a copy-on-write slab with a growth quantum of

@@ -1,6 +1,6 @@
 """GPU parity of the state lifecycle: allocate, prefill handoff, growth and
 the capacity proof, release, bank retention, trim, admission, invariant
-checks, and the continuous-batching scenario of BASELINE config 4.
+checks, and a continuous-batching scenario (release, compact, trim, admit).
 
 Bar: map, free stack, live slab rows, counters and returned values equal
 the CPU oracle (oracle/state.py restating allocator.py:506-1095) exactly.
@@ -282,7 +282,7 @@ def _decode_both(states, oracles, dense, seq, device):
 
 
 def test_continuous_batching_config4(device):
-    """BASELINE config 4 (experiments/benchmark_serving.py:472-613 pattern):
+    """Continuous batching (experiments/benchmark_serving.py:472-613 pattern):
     4 requests decode, requests 0 and 2 are released, survivors compacted
     and the pools trimmed, 2 new requests with 128-token prefixes admitted,
     decode continues at mixed positions.  Packed state must equal the dense

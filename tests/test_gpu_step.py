@@ -85,7 +85,7 @@ def test_reference_known_answers(device):
 
 @pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
 def test_baseline_shape_trace(device, index_dtype):
-    """BASELINE layer shape: B=64, N=256, D=128, top-4 write, top-16 read."""
+    """Benchmark layer shape: B=64, N=256, D=128, top-4 write, top-16 read."""
 
     _trace(device, banks=64, slots=256, width=128, writes=4, reads=16, steps=24, seed=21,
            index_dtype=index_dtype)
