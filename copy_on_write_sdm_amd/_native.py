@@ -39,7 +39,6 @@ ERR_CORRUPT = 0x20
 ERR_LOOKBACK = 0x40
 
 SCRATCH_EPOCH = 0
-SCRATCH_TICKET = 1
 SCRATCH_ERRORS = 3
 SCRATCH_SLOTS = 8
 
@@ -142,6 +141,10 @@ class Trace(ctypes.Structure):
         ("ticket", ctypes.c_void_p),
         ("first_step", ctypes.c_int64),
         ("stride_bytes", ctypes.c_int64 * 9),
+        ("scan", ctypes.c_void_p),
+        ("scan_words", ctypes.c_int64),
+        ("persistent", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -155,6 +158,7 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_last_error_string": (ctypes.c_char_p, []),
     "cowsdm_step_scratch_words": (_I64, [_I64]),
     "cowsdm_workspace_bytes": (_I64, [_I64, _I64]),
+    "cowsdm_trace_scan_words": (_I64, [_I64, _I32]),
     "cowsdm_packed_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
     "cowsdm_packed_step_layers": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),

@@ -1131,7 +1131,7 @@ class DecodeTrace:
 
     def __init__(self, *, states=None, memories=None, write_indices, write_weights, values,
                  input_gate, forget_log_gate, read_indices, read_weights, erase_gate=None,
-                 outputs=None):
+                 outputs=None, persistent: bool = True, max_steps_per_launch: int = 64):
         if (states is None) == (memories is None):
             raise ValueError("give exactly one of states or memories")
         self.dense = memories is not None
@@ -1175,6 +1175,14 @@ class DecodeTrace:
                             write_indices.shape[3], read_indices.shape[3],
                             1 if self.dense else first.shared_initial_memory.shape[0],
                             _index_code(write_indices, read_indices))
+        # persistent launches run up to max_steps_per_launch steps in one kernel
+        self.persistent = persistent
+        self.max_steps_per_launch = max(1, int(max_steps_per_launch))
+        words = int(nat.lib().cowsdm_trace_scan_words(banks, self.max_steps_per_launch))
+        self.scan = (torch.zeros(layers, words, dtype=torch.int64, device=device)
+                     if persistent and not self.dense else None)
+        self.trace.scan = None if self.scan is None else self.scan.data_ptr()
+        self.trace.scan_words = words
 
     def set_step(self, step: int) -> None:
         """Make the next launch run step ``step``."""
@@ -1205,14 +1213,23 @@ class DecodeTrace:
         device counter names."""
 
         layers = self.layer_array() if layers is None else layers
-        if start is not None:
-            if start < 0 or start + steps > self.steps:
-                raise ValueError("trace launch runs past the recorded steps")
-            self.trace.step_index = None
-            self.trace.first_step = start
-        else:
+        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
+        stream = nat.stream_handle(self.device)
+        if start is None:
             self.trace.step_index = self.step_index.data_ptr()
             self.trace.first_step = 0
-        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
-        nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps,
-                     nat.stream_handle(self.device)), "decode trace launch")
+            self.trace.persistent = 0
+            nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
+                      "decode trace launch")
+            return
+        if start < 0 or start + steps > self.steps:
+            raise ValueError("trace launch runs past the recorded steps")
+        self.trace.step_index = None
+        self.trace.persistent = int(self.persistent)
+        done = 0
+        while done < steps:
+            n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
+            self.trace.first_step = start + done
+            nat.check(fn(layers, len(self.tables), self.shape, self.trace, n, stream),
+                      "decode trace launch")
+            done += n

@@ -41,6 +41,9 @@ struct StepParams {
   int64_t* trace_ticket;         // [0] launch, [1 + layer] dense per-layer
   int64_t trace_first;           // step of this launch when trace_step is null
   int64_t trace_stride[9];
+  int64_t* scan;                 // persistent launches: per-layer scan words
+  int64_t scan_words;            // words per layer in `scan`
+  int32_t steps;                 // persistent launches: steps per launch
   int32_t nlayers;
   int32_t banks;
   int32_t slots;

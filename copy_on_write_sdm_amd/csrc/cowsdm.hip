@@ -46,6 +46,12 @@ extern template void launch_step_w<int32_t, false>(const StepParams&, int, int, 
 extern template void launch_step_w<int32_t, true>(const StepParams&, int, int, hipStream_t);
 extern template void launch_step_w<int64_t, false>(const StepParams&, int, int, hipStream_t);
 extern template void launch_step_w<int64_t, true>(const StepParams&, int, int, hipStream_t);
+template <typename IDX, bool DENSE>
+bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream);
+extern template bool launch_trace<int32_t, false>(const StepParams&, int, int, hipStream_t);
+extern template bool launch_trace<int32_t, true>(const StepParams&, int, int, hipStream_t);
+extern template bool launch_trace<int64_t, false>(const StepParams&, int, int, hipStream_t);
+extern template bool launch_trace<int64_t, true>(const StepParams&, int, int, hipStream_t);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -695,10 +701,26 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     }
   }
   if (steps < 0) return fail(COWSDM_EARG, "steps must be non-negative");
+  // persistent multi-step launch: one launch for all steps
+  const int64_t Dw = shape->width;
+  int trace_vec = Dw <= kWave ? 1 : (Dw <= 2 * kWave ? 2 : (Dw <= 4 * kWave ? 4 : 0));
+  if (trace_vec && Dw % trace_vec != 0) trace_vec = 0;
+  if (trace_vec > vec) trace_vec = 0;  // alignment of some pointer forbids it
+  const int64_t blocks_per_layer_p = (shape->banks + kBanksPerBlock - 1) / kBanksPerBlock;
+  const bool persistent =
+      trace && !trace->step_index && trace->persistent && steps > 0 && trace_vec &&
+      shape->writes <= 4 && shape->reads <= 16 && nlayers <= kMaxLayers &&
+      (dense || (trace->scan && trace->scan_words >= COWSDM_SCRATCH_SLOTS +
+                                                      static_cast<int64_t>(steps) * shape->banks)) &&
+      static_cast<int64_t>(steps) * shape->banks * shape->writes < (1ll << 30);
+  (void)blocks_per_layer_p;
   StepParams P;
   P.trace_step = trace ? trace->step_index : nullptr;
   P.trace_ticket = trace ? trace->ticket : nullptr;
   P.trace_first = trace ? trace->first_step : 0;
+  P.scan = trace ? trace->scan : nullptr;
+  P.scan_words = trace ? trace->scan_words : 0;
+  P.steps = steps;
   for (int k = 0; k < 9; ++k) P.trace_stride[k] = trace ? trace->stride_bytes[k] : 0;
   P.banks = static_cast<int32_t>(shape->banks);
   P.slots = static_cast<int32_t>(shape->slots);
@@ -713,6 +735,20 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     for (int32_t i = 0; i < kMaxLayers; ++i) P.layer[i] = layers[start + (i < n ? i : 0)];
     const int blocks = P.blocks_per_layer * n;
     const bool i64 = shape->index_dtype == COWSDM_INDEX_INT64;
+    if (persistent) {
+      bool launched;
+      if (dense) {
+        launched = i64 ? launch_trace<int64_t, true>(P, blocks, trace_vec, stream)
+                       : launch_trace<int32_t, true>(P, blocks, trace_vec, stream);
+      } else {
+        launched = i64 ? launch_trace<int64_t, false>(P, blocks, trace_vec, stream)
+                       : launch_trace<int32_t, false>(P, blocks, trace_vec, stream);
+      }
+      if (launched) {
+        if (int32_t e = launch_status(dense ? "dense trace" : "packed trace")) return e;
+        continue;
+      }
+    }
     for (int32_t it = 0; it < steps; ++it) {
       if (trace && !trace->step_index) P.trace_first = trace->first_step + it;
       if (dense) {
@@ -765,6 +801,11 @@ const char* cowsdm_last_error_string(void) { return last_error(); }
 
 int64_t cowsdm_step_scratch_words(int64_t banks) {
   return banks < 0 ? -1 : COWSDM_SCRATCH_SLOTS + banks;
+}
+
+int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps) {
+  if (banks < 0 || steps < 0) return -1;
+  return COWSDM_SCRATCH_SLOTS + banks * steps;
 }
 
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows) {

@@ -1,5 +1,9 @@
-// packed step kernels over int32_t route indices.
+// packed step kernels (single-step and persistent multi-step) over int32_t
+// route indices.
 #include "step_kernel.h"
+#include "trace_kernel.h"
 
-template void cowsdm_impl::launch_step_w<int32_t, false>(const cowsdm_impl::StepParams&, int, int,
-                                                         hipStream_t);
+template void cowsdm_impl::launch_step_w<int32_t, false>(const cowsdm_impl::StepParams&, int,
+                                                         int, hipStream_t);
+template bool cowsdm_impl::launch_trace<int32_t, false>(const cowsdm_impl::StepParams&, int,
+                                                        int, hipStream_t);

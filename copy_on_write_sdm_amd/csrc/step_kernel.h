@@ -4,63 +4,9 @@
 #pragma once
 
 #include "common.h"
+#include "lookback.h"
 
 namespace cowsdm_impl {
-
-// Exclusive prefix over banks [0, bank) of the per-bank first-touch counts,
-// by decoupled look-back.  Publishes this bank's aggregate first, then its
-// inclusive prefix.  Waits only on lower banks; each wait is bounded.
-__device__ inline int64_t bank_prefix(int64_t* slots, int bank, uint32_t epoch,
-                               int count, int lane, bool* poisoned) {
-  if (lane == 0) {
-    atomic_store_u64(&slots[bank], slot_word(epoch, kStatusAggregate, count));
-  }
-  int64_t exclusive = 0;
-  bool bad = false;
-  int end = bank;
-  while (end > 0) {
-    const int j = end - 1 - lane;
-    uint32_t status = kStatusInclusive;
-    int64_t value = 0;
-    if (j >= 0) {
-      uint64_t w = atomic_load_u64(&slots[j]);
-      int spins = 0;
-      while ((static_cast<uint32_t>(w >> 32) != epoch ||
-              ((w >> 30) & 3u) == kStatusEmpty) &&
-             spins < kSpinLimit) {
-        __builtin_amdgcn_s_sleep(1);
-        w = atomic_load_u64(&slots[j]);
-        ++spins;
-      }
-      if (static_cast<uint32_t>(w >> 32) != epoch ||
-          ((w >> 30) & 3u) == kStatusEmpty) {
-        status = kStatusPoison;
-      } else {
-        status = static_cast<uint32_t>((w >> 30) & 3u);
-        value = static_cast<int64_t>(w & kValueMask);
-      }
-    }
-    const uint64_t inclusive = __ballot(status == kStatusInclusive);
-    const uint64_t poison = __ballot(status == kStatusPoison);
-    if (inclusive != 0) {
-      const int k = __ffsll(static_cast<long long>(inclusive)) - 1;
-      const uint64_t upto = (k == 63) ? ~0ull : ((2ull << k) - 1);
-      if (poison & upto) bad = true;
-      exclusive += wave_sum64(lane <= k ? value : 0);
-      break;
-    }
-    if (poison != 0) bad = true;
-    exclusive += wave_sum64(value);
-    end -= kWave;
-  }
-  if (lane == 0) {
-    atomic_store_u64(&slots[bank],
-                     slot_word(epoch, bad ? kStatusPoison : kStatusInclusive,
-                               static_cast<uint64_t>(exclusive + count)));
-  }
-  *poisoned = bad;
-  return exclusive;
-}
 
 // --------------------------------------------------------- the fused step
 
@@ -77,7 +23,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   if (layer_id >= P.nlayers || bank >= P.banks) return;
   const cowsdm_layer_t& L = P.layer[layer_id];
   const int64_t trace_s = P.trace_step ? *P.trace_step : P.trace_first;
-  auto step_ptr = [&](const void* base, int k) -> const char* {
+  auto step_ptr = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
     return static_cast<const char*>(base) + trace_s * P.trace_stride[k];
   };
   const void* const write_indices = step_ptr(L.write_indices, 0);
@@ -218,7 +164,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
     for (int v = 0; v < VEC; ++v) rv[i][v] = 0.0f;
   }
 
-  auto write_row_src = [&](int j) -> const float* {
+  auto write_row_src = [&](int j) __attribute__((always_inline)) -> const float* {
     const int slot = rl(widx, j);
     if constexpr (DENSE) {
       return table_bank + static_cast<int64_t>(slot) * D;
@@ -233,13 +179,13 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
     const int v = k == 0 ? arr[0] : k == 1 ? arr[1] : k == 2 ? arr[2] : arr[3];
     return rl(v, r % kWave);
   };
-  auto read_weight = [&](int r) -> float {
+  auto read_weight = [&](int r) __attribute__((always_inline)) -> float {
     const int k = r / kWave;
     const float v = k == 0 ? rweight[0] : k == 1 ? rweight[1]
                   : k == 2 ? rweight[2] : rweight[3];
     return rlf(v, r % kWave);
   };
-  auto read_row_src = [&](int r) -> const float* {
+  auto read_row_src = [&](int r) __attribute__((always_inline)) -> const float* {
     const int slot = read_meta(ridx, r);
     if constexpr (DENSE) {
       return table_bank + static_cast<int64_t>(slot) * D;
@@ -249,7 +195,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
                    : L.values + static_cast<int64_t>(p) * D;
     }
   };
-  auto load_writes = [&](int chunk) {
+  auto load_writes = [&](int chunk) __attribute__((always_inline)) {
     const int col = chunk * chunk_cols + lane * VEC;
 #pragma unroll
     for (int j = 0; j < MAXW; ++j) {
@@ -259,7 +205,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
       }
     }
   };
-  auto load_read_batch = [&](int chunk, int r0) {
+  auto load_read_batch = [&](int chunk, int r0) __attribute__((always_inline)) {
     const int col = chunk * chunk_cols + lane * VEC;
 #pragma unroll
     for (int i = 0; i < kReadBatch; ++i) {
@@ -274,46 +220,51 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   load_writes(0);
   load_read_batch(0, 0);
 
-  // ---- free-stack resolution (packed): bank-major pop positions
+  // ---- free-stack resolution (packed): bank-major pop positions.  The row
+  // math never depends on physical row ids, so the scan waits only in front
+  // of the stores of first-touch rows and map entries.
   bool fits = true;
+  bool poisoned = false;
+  bool resolved = DENSE;
   int new_row = -1;
-  if constexpr (!DENSE) {
-    bool poisoned = false;
-    int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
-    const int64_t prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
-    fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
-    int bad_row = 0;
-    const int64_t from_top = prefix + rank;  // pop position counted from the top
-    const int src_lane = static_cast<int>(from_top % kWave);
-    int window_row = -1;
+  int64_t prefix = 0;
+  auto resolve = [&]() __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
+      prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
+      fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
+      int bad_row = 0;
+      const int64_t from_top = prefix + rank;  // pop position counted from the top
+      const int src_lane = static_cast<int>(from_top % kWave);
+      int window_row = -1;
 #pragma unroll
-    for (int k = 0; k < kFreeWindow / kWave; ++k) {
-      const int v = __shfl(free_top[k], src_lane, kWave);
-      if (from_top / kWave == k) window_row = v;
-    }
-    if (fits && first) {
-      new_row = from_top < kFreeWindow ? window_row : L.free_rows[old_free - 1 - from_top];
-      if (new_row < 0 || new_row >= C) bad_row = 1;
-    }
-    if (__ballot(bad_row) != 0) {
-      fits = false;
+      for (int k = 0; k < kFreeWindow / kWave; ++k) {
+        const int v = __shfl(free_top[k], src_lane, kWave);
+        if (from_top / kWave == k) window_row = v;
+      }
+      if (fits && first) {
+        new_row = from_top < kFreeWindow ? window_row : L.free_rows[old_free - 1 - from_top];
+        if (new_row < 0 || new_row >= C) bad_row = 1;
+      }
+      if (__ballot(bad_row) != 0) {
+        fits = false;
+        if (lane == 0) {
+          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                static_cast<int64_t>(COWSDM_ERR_CORRUPT),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
       if (lane == 0) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_CORRUPT),
-                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
+        if (poisoned) {
+          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
-    if (lane == 0) {
-      if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
-      if (poisoned) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  const bool commit = ok && fits;
-  const int dest = DENSE ? widx : (first ? new_row : wphys);
+    resolved = true;
+  };
 
   // ---- gated-delta update and sparse read, chunk by chunk
   for (int chunk = 0; chunk < nchunks; ++chunk) {
@@ -395,47 +346,66 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
       }
     }
     if (col_ok) store_row<VEC>(output + b * D + col, acc);
-    if (commit) {
+    if (ok) {
+      // rows already private (and every dense row) need no pop
 #pragma unroll
       for (int j = 0; j < MAXW; ++j) {
         if (j < W) {
-          const int row = rl(dest, j);
-          float* dst = DENSE ? table_bank + static_cast<int64_t>(row) * D
-                             : L.values + static_cast<int64_t>(row) * D;
-          if (col_ok) store_row<VEC>(dst + col, cur[j]);
+          const bool is_first = DENSE ? false : (rl(wphys, j) < 0);
+          if (!is_first) {
+            const int row = DENSE ? rl(widx, j) : rl(wphys, j);
+            float* dst = DENSE ? table_bank + static_cast<int64_t>(row) * D
+                               : L.values + static_cast<int64_t>(row) * D;
+            if (col_ok) store_row<VEC>(dst + col, cur[j]);
+          }
+        }
+      }
+    }
+    if constexpr (!DENSE) {
+      if (!resolved) resolve();
+      if (ok && fits && count > 0) {
+#pragma unroll
+        for (int j = 0; j < MAXW; ++j) {
+          if (j < W && rl(wphys, j) < 0) {
+            float* dst = L.values + static_cast<int64_t>(rl(new_row, j)) * D;
+            if (col_ok) store_row<VEC>(dst + col, cur[j]);
+          }
         }
       }
     }
   }
+  const bool commit = ok && fits;
 
   bool closed_layer = false;
   if constexpr (!DENSE) {
     if (commit && first) L.logical_to_physical[b * N + widx] = new_row;
     if (lane == 0) {
       if (L.first_touches_out) L.first_touches_out[b] = commit ? count : 0;
-      if (L.repeated_writes_out) L.repeated_writes_out[b] = commit ? W - count : W;
+      if (L.repeated_writes_out) L.repeated_writes_out[b] = ok ? W - count : W;
       if (err) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                               static_cast<int64_t>(err), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
       }
-      // one relaxed atomic carries both the finished-bank count (high word)
-      // and the rows this bank popped (low word): the last bank to arrive
-      // gets the layer's total from its own return value, so no fence and
-      // no second atomic are needed
-      const int64_t mine = commit ? count : 0;
-      const uint64_t before = static_cast<uint64_t>(__hip_atomic_fetch_add(
-          &L.scratch[COWSDM_SCRATCH_TICKET], static_cast<int64_t>((1ull << 32) | mine),
-          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      if (static_cast<int64_t>(before >> 32) == P.banks - 1) {
-        closed_layer = true;
-        const int64_t served = static_cast<int64_t>(before & 0xffffffffull) + mine;
+    }
+    // The last bank closes the layer.  Its scan ran after every lower bank
+    // had published (so all of them read free_count, the epoch and the trace
+    // step already).  When it fits, every bank fit and its inclusive prefix
+    // is the number of rows popped; otherwise the popped rows are the
+    // largest inclusive prefix that fits, read from the other banks' slots.
+    if (bank == P.banks - 1) {
+      closed_layer = true;
+      int64_t served = prefix + count;
+      if (poisoned || served > old_free) {
+        served = fitting_prefix(L.scratch + COWSDM_SCRATCH_SLOTS, P.banks, epoch, old_free,
+                                lane);
+      }
+      if (lane == 0) {
         const int64_t now_free = old_free - served;
         *L.free_count = static_cast<int32_t>(now_free);
         if (L.allocated_rows_out) {
           *L.allocated_rows_out = static_cast<int32_t>(C - now_free);
         }
-        atomic_store_u64(&L.scratch[COWSDM_SCRATCH_TICKET], 0);
         atomic_store_u64(&L.scratch[COWSDM_SCRATCH_EPOCH],
                          static_cast<uint64_t>(epoch + 1u));
       }

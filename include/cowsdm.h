@@ -56,11 +56,10 @@ extern "C" {
 #define COWSDM_ERR_LOOKBACK 0x40     /* bank-order scan did not complete  */
 
 /* Word offsets inside the per-layer step scratch (int64 words). */
-/* EPOCH retires the previous launch's scan slots; TICKET packs the number
- * of banks done (high 32 bits) with the rows they popped (low 32 bits);
- * ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's scan slot. */
+/* EPOCH retires the previous launch's scan slots (the layer's last bank
+ * advances it); ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's
+ * scan slot.  Words 1, 2 and 4-7 are reserved. */
 #define COWSDM_SCRATCH_EPOCH 0
-#define COWSDM_SCRATCH_TICKET 1
 #define COWSDM_SCRATCH_ERRORS 3
 #define COWSDM_SCRATCH_SLOTS 8
 
@@ -120,6 +119,16 @@ typedef struct cowsdm_trace {
   int64_t* ticket;
   int64_t first_step;
   int64_t stride_bytes[9];
+  /* Persistent launches (host offsets only): with persistent != 0 one launch
+   * runs all `steps` steps when the shape allows it (W <= 4, R <= 16,
+   * D <= 256, every workgroup resident), else one launch per step.  Packed
+   * launches then need `scan`: nlayers blocks of scan_words int64 words
+   * (>= cowsdm_trace_scan_words(banks, steps)), zero before first use and
+   * kept valid by the kernels. */
+  int64_t* scan;
+  int64_t scan_words;
+  int32_t persistent;
+  int32_t reserved;
 } cowsdm_trace_t;
 
 /* ---------------------------------------------------------------- info */
@@ -128,6 +137,8 @@ int32_t cowsdm_abi_version(void);
 const char* cowsdm_last_error_string(void);
 /* int64 words of step scratch one layer with `banks` banks needs. */
 int64_t cowsdm_step_scratch_words(int64_t banks);
+/* int64 words per layer of a persistent trace launch's scan buffer. */
+int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps);
 /* Bytes of lifecycle workspace for a ranking over `entries` map entries
  * (release / trim / append / pack handoff / invariant checks). */
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows);

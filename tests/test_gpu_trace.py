@@ -1,0 +1,178 @@
+"""GPU parity of decode traces: the persistent multi-step kernel (many
+steps per launch, forwarding rows between steps in registers, bank-major
+pops over (step, bank) pairs) and device-counter launches must equal
+single-step launches, and the oracle, bit for bit.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import copy_on_write_sdm_amd as cow
+from copy_on_write_sdm_amd import synthetic
+from gpu_helpers import assert_state_equal
+from oracle import state as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(device, *, layers, banks, slots, width, writes, reads, steps, seed,
+           index_dtype=torch.int32, capacity=None, sticky=False):
+    m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=seed, device=device)
+    routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
+                                  width=width, writes=writes, reads=reads, seed=seed + 1,
+                                  device=device, index_dtype=index_dtype)
+    if sticky:
+        # consecutive steps rewrite and reread the same slots: every row a
+        # step needs was written by the step before it
+        keep = torch.rand(steps, layers, banks, 1, device=device) < 0.7
+        for s in range(1, steps):
+            routes.write_indices[s] = torch.where(keep[s], routes.write_indices[s - 1],
+                                                  routes.write_indices[s])
+            routes.write_indices[s] = routes.write_indices[s].sort(-1).values
+            take = min(reads, writes)
+            routes.read_indices[s, ..., :take] = routes.write_indices[s - 1, ..., :take]
+        # reads must stay unique per bank for nothing; only writes must
+    capacity = capacity or banks * slots
+
+    def states():
+        out = []
+        for l in range(layers):
+            st = cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks,
+                                                        capacity_rows=capacity)
+            st.capacity_is_proven = True
+            out.append(st)
+        return out
+
+    kw = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+              values=routes.values, input_gate=routes.input_gate,
+              forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+              read_weights=routes.read_weights)
+    return m0, routes, states, kw
+
+
+def _per_step(states, routes, steps, layers):
+    outs = []
+    for s in range(steps):
+        row = []
+        for l in range(layers):
+            r, _ = cow.packed_sdm_cow_step(states[l], **routes.step(s, l), validate_routes=False,
+                                           collect_diagnostics=False)
+            row.append(r)
+        outs.append(torch.stack(row))
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("layers,banks,slots,width,writes,reads,steps,group", [
+    (7, 64, 256, 128, 4, 16, 40, 16),    # benchmark shape
+    (3, 5, 64, 64, 4, 16, 20, 7),        # float per lane, partial block
+    (2, 130, 64, 256, 3, 9, 12, 12),     # float4 lanes, 3 look-back windows per step
+    (1, 1, 16, 8, 1, 1, 30, 30),         # one bank, one route
+    (4, 33, 32, 100, 2, 5, 25, 64),      # odd width > 64 (two floats per lane)
+])
+def test_persistent_trace_matches_single_steps(device, layers, banks, slots, width, writes,
+                                              reads, steps, group):
+    print(f"trace L={layers} B={banks} N={slots} D={width} W={writes} R={reads} S={steps} "
+          f"G={group}", flush=True)
+    m0, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=slots,
+                                    width=width, writes=writes, reads=reads, steps=steps,
+                                    seed=banks + width)
+    traced, single = states(), states()
+    outputs = torch.empty(steps, layers, banks, width, device=device)
+    tr = cow.DecodeTrace(states=traced, outputs=outputs, max_steps_per_launch=group, **kw)
+    tr.launch(steps, start=0)
+    want = _per_step(single, routes, steps, layers)
+    assert torch.equal(outputs, want)
+    for a, b in zip(traced, single):
+        assert torch.equal(a.logical_to_physical, b.logical_to_physical)
+        assert int(a.free_count) == int(b.free_count)
+        n = int(a.free_count)
+        assert torch.equal(a.free_rows[:n], b.free_rows[:n])
+        assert torch.equal(a.materialize_dense(), b.materialize_dense())
+        a.validate_invariants()
+    dense = [m0[l, 0].expand(banks, -1, -1).contiguous() for l in range(layers)]
+    dout = torch.empty_like(outputs)
+    cow.DecodeTrace(memories=dense, outputs=dout, max_steps_per_launch=group,
+                    **kw).launch(steps, start=0)
+    assert torch.equal(dout, want)
+    for l in range(layers):
+        assert torch.equal(dense[l], traced[l].materialize_dense())
+
+
+def test_persistent_trace_matches_oracle(device):
+    banks, slots, width, steps = 6, 32, 128, 24
+    m0, routes, states, kw = _setup(device, layers=1, banks=banks, slots=slots, width=width,
+                                    writes=4, reads=16, steps=steps, seed=3, sticky=True)
+    traced = states()
+    outputs = torch.empty(steps, 1, banks, width, device=device)
+    cow.DecodeTrace(states=traced, outputs=outputs, max_steps_per_launch=10,
+                    **kw).launch(steps, start=0)
+    oracle = ref.allocate(m0[0].cpu().numpy(), banks=banks, capacity_rows=banks * slots)
+    oracle.capacity_is_proven = True
+    for s in range(steps):
+        x = {k: v.cpu().numpy() for k, v in routes.step(s, 0).items()}
+        want, _ = ref.packed_step(oracle, **x, validate_routes=False)
+        assert np.array_equal(outputs[s, 0].cpu().numpy(), want), f"step {s}"
+    assert_state_equal(traced[0], oracle)
+
+
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_sticky_routes_forwarding(device, index_dtype):
+    """Most writes of a step hit the slots the previous step wrote (and its
+    reads too): the rows must come from the register forwarding path."""
+
+    layers, banks, steps = 2, 40, 48
+    _, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=48, width=128,
+                                   writes=4, reads=12, steps=steps, seed=9, sticky=True,
+                                   index_dtype=index_dtype)
+    traced, single = states(), states()
+    outputs = torch.empty(steps, layers, banks, 128, device=device)
+    cow.DecodeTrace(states=traced, outputs=outputs, max_steps_per_launch=48,
+                    **kw).launch(steps, start=0)
+    want = _per_step(single, routes, steps, layers)
+    assert torch.equal(outputs, want)
+    for a, b in zip(traced, single):
+        assert torch.equal(a.materialize_dense(), b.materialize_dense())
+        assert torch.equal(a.logical_to_physical, b.logical_to_physical)
+
+
+def test_device_counter_graph_replay(device):
+    layers, banks, steps, group = 3, 16, 24, 4
+    _, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=64, width=128,
+                                   writes=4, reads=16, steps=steps, seed=17)
+    traced, single = states(), states()
+    outputs = torch.empty(steps, layers, banks, 128, device=device)
+    tr = cow.DecodeTrace(states=traced, outputs=outputs, **kw)
+    layer_array = tr.layer_array()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
+        tr.launch(group, layer_array)
+    tr.set_step(0)
+    for _ in range(steps // group):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert int(tr.step_index.item()) == steps
+    want = _per_step(single, routes, steps, layers)
+    assert torch.equal(outputs, want)
+    for a, b in zip(traced, single):
+        assert torch.equal(a.materialize_dense(), b.materialize_dense())
+
+
+def test_persistent_overflow_sets_flag_and_keeps_partition(device):
+    """A proven state whose slab is too small for the trace: the overflow
+    flag latches, the launch stops committing first touches where the free
+    stack runs out, and the slab stays a partition."""
+
+    layers, banks, slots, steps = 1, 8, 64, 20
+    _, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=slots, width=64,
+                                   writes=4, reads=8, steps=steps, seed=23, capacity=60)
+    st = states()
+    cow.DecodeTrace(states=st, max_steps_per_launch=steps, **kw).launch(steps, start=0)
+    assert int(st[0].overflow_flag) == 1
+    mapping = st[0].logical_to_physical.cpu()
+    live = mapping[mapping >= 0]
+    free = st[0].free_rows[: int(st[0].free_count)].cpu()
+    rows = torch.cat((live, free)).sort().values
+    assert torch.equal(rows, torch.arange(60, dtype=rows.dtype))
