@@ -22,6 +22,12 @@ constexpr int kFreeWindow = 256;            // prefetched free-stack entries
 constexpr int kTile = 2048;                 // ranking tile (entries)
 constexpr int kTileThreads = 256;
 constexpr int kPerThread = kTile / kTileThreads;
+// persistent multi-step launches
+constexpr int kTraceMaxWrites = 4;
+constexpr int kTraceMaxReads = 16;
+constexpr int kTraceMaxSteps = 64;          // each step's gates live in one lane
+constexpr int kTraceScanWindows = 4;        // up to 256 banks per layer
+constexpr int kTraceFreeWindow = 1024;      // top of the free stack staged in LDS
 
 constexpr uint32_t kStatusEmpty = 0;
 constexpr uint32_t kStatusAggregate = 1;

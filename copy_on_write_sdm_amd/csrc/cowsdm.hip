@@ -707,12 +707,17 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   if (trace_vec && Dw % trace_vec != 0) trace_vec = 0;
   if (trace_vec > vec) trace_vec = 0;  // alignment of some pointer forbids it
   const int64_t blocks_per_layer_p = (shape->banks + kBanksPerBlock - 1) / kBanksPerBlock;
-  const bool persistent =
+  const int64_t chunk = steps < kTraceMaxSteps ? steps : kTraceMaxSteps;
+  bool strides_fit = true;  // the persistent kernel advances inputs by 32-bit strides
+  for (int k = 0; k < 9 && trace; ++k) {
+    if (trace->stride_bytes[k] < 0 || trace->stride_bytes[k] >= (1ll << 32)) strides_fit = false;
+  }
+  const bool persistent = strides_fit &&
       trace && !trace->step_index && trace->persistent && steps > 0 && trace_vec &&
-      shape->writes <= 4 && shape->reads <= 16 && nlayers <= kMaxLayers &&
-      (dense || (trace->scan && trace->scan_words >= COWSDM_SCRATCH_SLOTS +
-                                                      static_cast<int64_t>(steps) * shape->banks)) &&
-      static_cast<int64_t>(steps) * shape->banks * shape->writes < (1ll << 30);
+      shape->writes <= kTraceMaxWrites && shape->reads <= kTraceMaxReads &&
+      nlayers <= kMaxLayers &&
+      (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan &&
+                 trace->scan_words >= COWSDM_SCRATCH_SLOTS + chunk * shape->banks));
   (void)blocks_per_layer_p;
   StepParams P;
   P.trace_step = trace ? trace->step_index : nullptr;
@@ -736,18 +741,28 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     const int blocks = P.blocks_per_layer * n;
     const bool i64 = shape->index_dtype == COWSDM_INDEX_INT64;
     if (persistent) {
-      bool launched;
-      if (dense) {
-        launched = i64 ? launch_trace<int64_t, true>(P, blocks, trace_vec, stream)
-                       : launch_trace<int32_t, true>(P, blocks, trace_vec, stream);
-      } else {
-        launched = i64 ? launch_trace<int64_t, false>(P, blocks, trace_vec, stream)
-                       : launch_trace<int32_t, false>(P, blocks, trace_vec, stream);
+      // launches of at most kTraceMaxSteps steps each, in order
+      bool launched = true;
+      for (int32_t done = 0; done < steps && launched; done += kTraceMaxSteps) {
+        P.steps = (steps - done) < kTraceMaxSteps ? (steps - done) : kTraceMaxSteps;
+        P.trace_first = trace->first_step + done;
+        if (dense) {
+          launched = i64 ? launch_trace<int64_t, true>(P, blocks, trace_vec, stream)
+                         : launch_trace<int32_t, true>(P, blocks, trace_vec, stream);
+        } else {
+          launched = i64 ? launch_trace<int64_t, false>(P, blocks, trace_vec, stream)
+                         : launch_trace<int32_t, false>(P, blocks, trace_vec, stream);
+        }
+        if (!launched && done > 0) {
+          return fail(COWSDM_ELIMIT, "trace launch stopped after %d steps", done);
+        }
+        if (launched) {
+          if (int32_t e = launch_status(dense ? "dense trace" : "packed trace")) return e;
+        }
       }
-      if (launched) {
-        if (int32_t e = launch_status(dense ? "dense trace" : "packed trace")) return e;
-        continue;
-      }
+      if (launched) continue;
+      P.steps = steps;
+      P.trace_first = trace->first_step;
     }
     for (int32_t it = 0; it < steps; ++it) {
       if (trace && !trace->step_index) P.trace_first = trace->first_step + it;

@@ -3,64 +3,132 @@
 // bank), with results identical to G single-step launches.
 //
 // Each wave owns one (layer, bank) for all G steps and software-pipelines
-// them.  In iteration s it
-//   0. issues the map lookups of step s+1;
-//   1. resolves step s-1's pops (bank-order prefix over the (step, bank)
-//      sequence) and stores s-1's first-touch rows and map entries;
-//   2. classifies step s+1 (first touches, read-after-write), publishes its
-//      first-touch count and issues its row loads;
-//   3. computes step s (gated-delta update, sparse read), stores its reading
-//      and the rows that were already private;
-//   4. copies into step s+1's rows the slots step s wrote.
-// Step s+1's map entries are read before step s-1's first touches are stored
-// and before step s's are known: slots written at s come from step s's
-// registers and slots written at s-1 take the physical rows resolved in 1.
-// Step s+1's rows are loaded before step s is computed: slots written at s
-// are copied in 4, every other row was stored earlier by the same wave, in
-// program order.  Row buffers alternate between even and odd steps (the loop
-// is unrolled by two), so every buffer index is a compile-time constant and
-// all rows stay in registers.
+// them, so that every memory access has about one iteration to land before
+// its value is used.  Iteration s
+//   1. loads the slots of step s+4;
+//   2. loads the map entries of step s+3;
+//   3. computes step s (gated-delta update, sparse read) from rows loaded two
+//      iterations earlier; stores its reading and the rows already private;
+//   4. classifies step s+2 (first touches, rows written by steps s+1 and s,
+//      read-after-write), publishes its first-touch count and loads its rows;
+//   5. pops the free rows of step s's first touches and stores them and their
+//      map entries;
+//   6. loads every bank's first-touch count of step s+1.
+// Step t's map entries are read before steps t-3 .. t-1 have stored their
+// first touches: slots written at t-1 and t-2 take their rows from those
+// steps' results, kept in LDS, and slots written at t-3 take the physical rows
+// popped in 5.  Every other row step t needs was stored earlier by the same
+// wave, in program order.  Row buffers alternate between even and odd steps
+// (the loop is unrolled by two), so all of them stay in registers; per-row
+// values that depend on run-time lanes are read from LDS, never selected out
+// of registers.
 //
 // First touches of (step t, bank b) pop free_rows[F - 1 - Q(t, b) - rank],
 // where F is free_count at launch and Q the exclusive prefix of first-touch
-// counts over (step, bank) pairs in step-major, bank-minor order: exactly
-// the rows G single-step launches would pop.  The pair (G-1, B-1) closes the
-// launch: it writes free_count and advances the scan epoch.
+// counts over (step, bank) pairs in step-major, bank-minor order: exactly the
+// rows G single-step launches would pop.  Each wave publishes one count per
+// step and reads the counts of every bank of the layer, so it knows both its
+// own prefix and the running total without waiting on another wave's prefix.
+// The wave of bank B-1 closes the launch: it writes free_count and advances
+// the scan epoch.
 #pragma once
 
 #include "common.h"
-#include "lookback.h"
 
 namespace cowsdm_impl {
 
-constexpr int kTraceMaxWrites = 4;
-constexpr int kTraceMaxReads = 16;
+template <int VEC>
+struct TraceRows {                  // operands of one step, loaded two steps ahead
+  float w[kTraceMaxWrites][VEC];    // rows of the write slots, before the decay
+  float r[kTraceMaxReads][VEC];     // rows of the read slots, before this step
+  float vin[VEC];                   // the step's value
+  float ww, rw;                     // lane j: weight of write j / read j
+};
+
+struct TraceIdx {                   // lane j: write slot j / read slot j
+  int widx, ridx, err;
+};
+
+struct TraceRoute {                 // a classified step
+  int widx, ridx;
+  int wrow;       // write lane: physical row (-1: M0, or a first touch not yet popped)
+  int wsrc;       // write lane: written by step t-1 lane j (j) or t-2 lane j (4+j); else -1
+  int rsrc;       // read lane: the same
+  int rraw;       // read lane: write lane of step t itself with this slot, else -1
+  int rank;       // write lane: rank among the bank's first touches
+  uint32_t u;     // wave-uniform: bits 0-3 first-touch write lanes, 4-7 their count,
+                  // 8 the step runs (routes valid, every earlier step ran),
+                  // 9 a row comes from step t-1 or t-2, 10 a read sees a write of step t
+};
+
+__device__ __forceinline__ uint32_t route_fmask(uint32_t u) { return u & 15u; }
+__device__ __forceinline__ int route_count(uint32_t u) { return static_cast<int>((u >> 4) & 15u); }
+__device__ __forceinline__ bool route_ok(uint32_t u) { return (u >> 8) & 1u; }
+__device__ __forceinline__ bool route_fix(uint32_t u) { return (u >> 9) & 1u; }
+__device__ __forceinline__ bool route_raw(uint32_t u) { return (u >> 10) & 1u; }
+
+typedef __attribute__((address_space(1))) float gfloat;
+typedef float vf2 __attribute__((ext_vector_type(2)));
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+// Row accesses through global-address-space pointers (global_load/store with
+// a scalar base), not generic ones.
+template <int VEC>
+__device__ __forceinline__ void gload_row(const float* p, float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    const vf4 t = *(const __attribute__((address_space(1))) vf4*)(p);
+    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+  } else if constexpr (VEC == 2) {
+    const vf2 t = *(const __attribute__((address_space(1))) vf2*)(p);
+    x[0] = t.x; x[1] = t.y;
+  } else {
+    x[0] = *(const gfloat*)(p);
+  }
+}
 
 template <int VEC>
-struct TraceMeta {
-  int widx, ridx, err;
-  float ww, rw;
-  float gate;  // lane 0: forget log gate, lane 1: input gate, lane 2: erase gate
-  float vin[VEC];
-};
+__device__ __forceinline__ void gstore_row(float* p, const float (&x)[VEC]) {
+  if constexpr (VEC == 4) {
+    vf4 t;
+    t.x = x[0]; t.y = x[1]; t.z = x[2]; t.w = x[3];
+    *(__attribute__((address_space(1))) vf4*)(p) = t;
+  } else if constexpr (VEC == 2) {
+    vf2 t;
+    t.x = x[0]; t.y = x[1];
+    *(__attribute__((address_space(1))) vf2*)(p) = t;
+  } else {
+    *(gfloat*)(p) = x[0];
+  }
+}
 
-struct TraceClass {
-  int wraw, rraw;   // physical rows of the write / read slot (-1: shared M0)
-  int wfwd, rfwd;   // write lane of the previous step holding this slot, or -1
-  int rsrc;         // write lane of this step holding this read slot, or -1
-  int wphys;        // physical row of this write lane (first touches: after pops)
-  int first;        // this write lane is a first touch
-  int count, rank;  // first touches of the bank / rank of this lane among them
-  int ok;           // the step runs (no error so far in this bank)
-};
+__device__ __forceinline__ const float* rl_ptr(const float* p, int lane) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), lane);
+  return reinterpret_cast<const float*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+// Weighted population count of per-lane values 0..7 held as three bit masks.
+__device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t m) {
+  return __popcll(b0 & m) + 2 * __popcll(b1 & m) + 4 * __popcll(b2 & m);
+}
 
 template <typename IDX, int VEC, bool DENSE>
 __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
-  const int layer_id = blockIdx.x / P.blocks_per_layer;
-  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock +
-                   static_cast<int>(threadIdx.x) / kWave;
+  constexpr int kRow = kWave * VEC;  // floats of one LDS row
+  __shared__ float lds_rows[kBanksPerBlock][2][kTraceMaxWrites][kRow];
+  __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
+
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
-  if (layer_id >= P.nlayers || bank >= P.banks) return;
+  const int layer_id = blockIdx.x / P.blocks_per_layer;
+  if (layer_id >= P.nlayers) return;  // whole workgroup
+  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock + wave;
   const cowsdm_layer_t& L = P.layer[layer_id];
 
   const int N = P.slots;
@@ -69,246 +137,301 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const int R = P.reads;
   const int B = P.banks;
   const int G = P.steps;
-  const int64_t C = L.capacity_rows;
-  const int64_t b = bank;
-  const int col = lane * VEC;
-  const bool col_ok = col < D;
+  const int C = static_cast<int>(L.capacity_rows);  // rows are int32
+  // lanes past the row width repeat the last columns: they load, compute and
+  // store exactly what the last full lane does, so no access needs a lane mask
+  const int col = lane * VEC < D ? lane * VEC : D - VEC;
 
-  // ---- launch constants of this (layer, bank)
+  // ---- launch constants
   int base_err = 0;
-  int64_t tmpl = 0;
-  int64_t old_free = 0;
-  uint32_t epoch = 0;
-  int64_t* scan = nullptr;
-  int free_top[kFreeWindow / kWave];
+  int old_free = 0;
+  int window = 0;
   if constexpr (!DENSE) {
-    tmpl = L.template_indices[b];
-    if (tmpl < 0 || tmpl >= P.templates) base_err |= COWSDM_ERR_TEMPLATE;
     old_free = *L.free_count;
-    if (old_free < 0 || old_free > C) base_err |= COWSDM_ERR_CORRUPT;
-    scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
-    epoch = static_cast<uint32_t>(scan[COWSDM_SCRATCH_EPOCH]);
-#pragma unroll
-    for (int k = 0; k < kFreeWindow / kWave; ++k) {
-      const int64_t pos = old_free - 1 - (k * kWave + lane);
-      free_top[k] = (pos >= 0 && pos < C) ? L.free_rows[pos] : -1;
+    if (old_free < 0 || old_free > C) {
+      base_err |= COWSDM_ERR_CORRUPT;
+    } else {
+      window = old_free < kTraceFreeWindow ? old_free : kTraceFreeWindow;
     }
+    for (int k = static_cast<int>(threadIdx.x); k < window; k += kStepThreads) {
+      lds_free[k] = L.free_rows[old_free - 1 - k];
+    }
+    __syncthreads();
   }
-  int64_t* const slots = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS;
+  if (bank >= B) return;
+  int64_t tmpl = 0;
+  uint32_t epoch = 0;
+  int64_t* slots = nullptr;
+  if constexpr (!DENSE) {
+    tmpl = L.template_indices[bank];
+    if (tmpl < 0 || tmpl >= P.templates) {
+      base_err |= COWSDM_ERR_TEMPLATE;
+      tmpl = 0;
+    }
+    int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
+    epoch = static_cast<uint32_t>(scan[COWSDM_SCRATCH_EPOCH]);
+    slots = scan + COWSDM_SCRATCH_SLOTS + bank;  // + t * B: this bank's word of step t
+  }
   const float* const m0_bank =
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
-  float* const table_bank = DENSE ? L.values + b * N * D : nullptr;
-  int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + b * N;
+  float* const table_bank = DENSE ? L.values + static_cast<int64_t>(bank) * N * D : nullptr;
+  int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
+  float* const lds_wave = &lds_rows[wave][0][0][0];
 
-  auto step_in = [&](const void* base, int k, int s) __attribute__((always_inline)) -> const char* {
-    return static_cast<const char*>(base) + (P.trace_first + s) * P.trace_stride[k];
+  // ---- this lane's inputs at the launch's first step; step t adds t * stride
+  const int wl = lane < W ? lane : 0;
+  const int rl_ = lane < R ? lane : 0;
+  auto first_step = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
+    return static_cast<const char*>(base) + P.trace_first * P.trace_stride[k];
+  };
+  const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
+  const char* const ww_l = first_step(L.write_weights, 1) + (static_cast<int64_t>(bank) * W + wl) * 4;
+  const char* const v_l = first_step(L.step_values, 2) + (static_cast<int64_t>(bank) * D + col) * 4;
+  const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
+  const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
+  const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
+  const uint32_t st_wi = static_cast<uint32_t>(P.trace_stride[0]);
+  const uint32_t st_ww = static_cast<uint32_t>(P.trace_stride[1]);
+  const uint32_t st_v = static_cast<uint32_t>(P.trace_stride[2]);
+  const uint32_t st_ri = static_cast<uint32_t>(P.trace_stride[6]);
+  const uint32_t st_rw = static_cast<uint32_t>(P.trace_stride[7]);
+  const uint32_t st_out = static_cast<uint32_t>(P.trace_stride[8]);
+  auto at = [](const char* p, uint32_t stride, int t) __attribute__((always_inline)) -> const char* {
+    return p + static_cast<uint64_t>(static_cast<uint32_t>(t)) * stride;
   };
 
-  // ---- stage helpers
-  auto load_meta = [&](int s, TraceMeta<VEC>& m) __attribute__((always_inline)) {
-    m.err = 0;
-    m.widx = 0;
-    m.ridx = 0;
-    m.ww = 0.0f;
-    m.rw = 0.0f;
-    m.gate = 0.0f;
-    const void* wi = step_in(L.write_indices, 0, s);
-    const float* ww = reinterpret_cast<const float*>(step_in(L.write_weights, 1, s));
-    const float* vv = reinterpret_cast<const float*>(step_in(L.step_values, 2, s));
-    const void* ri = step_in(L.read_indices, 6, s);
-    const float* rw = reinterpret_cast<const float*>(step_in(L.read_weights, 7, s));
-    if (lane < W) {
-      const int64_t x = load_index<IDX>(wi, b * W + lane);
-      m.ww = ww[b * W + lane];
-      if (x < 0 || x >= N) m.err |= COWSDM_ERR_WRITE_INDEX;
-      else m.widx = static_cast<int>(x);
-    }
-    if (lane < R) {
-      const int64_t x = load_index<IDX>(ri, b * R + lane);
-      m.rw = rw[b * R + lane];
-      if (x < 0 || x >= N) m.err |= COWSDM_ERR_READ_INDEX;
-      else m.ridx = static_cast<int>(x);
-    }
-    // per-lane addresses keep the gates on vector loads: a scalar load here
-    // would make every later scalar use wait for the newest step's gates
-    if (lane < 3) {
-      const int k = lane == 0 ? 5 : (lane == 1 ? 3 : 4);
-      const void* base = lane == 0 ? L.forget_log_gate : (lane == 1 ? L.input_gate : L.erase_gate);
-      m.gate = reinterpret_cast<const float*>(step_in(base, k, s))[b];
-    }
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) m.vin[v] = 0.0f;
-    if (col_ok) load_row<VEC>(vv + b * D + col, m.vin);
+  // ---- gates of every step, lane t holding step t's
+  float alpha_l = 0.0f, in_l = 0.0f, er_l = 0.0f;
+  if (lane < G) {
+    const float fg = reinterpret_cast<const float*>(first_step(L.forget_log_gate, 5) +
+                                                    static_cast<int64_t>(lane) * P.trace_stride[5])[bank];
+    in_l = reinterpret_cast<const float*>(first_step(L.input_gate, 3) +
+                                          static_cast<int64_t>(lane) * P.trace_stride[3])[bank];
+    er_l = reinterpret_cast<const float*>(first_step(L.erase_gate, 4) +
+                                          static_cast<int64_t>(lane) * P.trace_stride[4])[bank];
+    alpha_l = static_cast<float>(exp(static_cast<double>(fg)));
+  }
+
+  // ---- stages
+  auto load_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
+    const int tc = t < G ? t : G - 1;
+    const int64_t xw = static_cast<int64_t>(*(const __attribute__((address_space(1))) IDX*)(at(wi_l, st_wi, tc)));
+    const int64_t xr = static_cast<int64_t>(*(const __attribute__((address_space(1))) IDX*)(at(ri_l, st_ri, tc)));
+    const bool bw = xw < 0 || xw >= N;
+    const bool br = xr < 0 || xr >= N;
+    m.err = (lane < W && bw ? COWSDM_ERR_WRITE_INDEX : 0) | (lane < R && br ? COWSDM_ERR_READ_INDEX : 0);
+    m.widx = (lane < W && !bw) ? static_cast<int>(xw) : 0;
+    m.ridx = (lane < R && !br) ? static_cast<int>(xr) : 0;
   };
 
-  auto issue_map = [&](const TraceMeta<VEC>& m, TraceClass& c) __attribute__((always_inline)) {
-    c.wraw = -1;
-    c.rraw = -1;
+  auto issue_map = [&](const TraceIdx& m, int& wraw, int& rraw) __attribute__((always_inline)) {
+    wraw = -1;
+    rraw = -1;
     if constexpr (!DENSE) {
-      if (lane < W && !(m.err & COWSDM_ERR_WRITE_INDEX)) c.wraw = map_bank[m.widx];
-      if (lane < R && !(m.err & COWSDM_ERR_READ_INDEX)) c.rraw = map_bank[m.ridx];
+      const __attribute__((address_space(1))) int32_t* map_g =
+          (const __attribute__((address_space(1))) int32_t*)(map_bank);
+      const int a = map_g[m.widx];
+      const int c = map_g[m.ridx];
+      wraw = lane < W ? a : -1;
+      rraw = lane < R ? c : -1;
     }
   };
 
-  // First touches and forwarding of step t.  p* is step t-1 (its rows in
-  // registers, its first touches possibly unresolved), q* is step t-2 (its
-  // physical rows resolved, its map entries possibly not yet visible in c).
-  auto classify = [&](const TraceMeta<VEC>& m, TraceClass& c, const TraceMeta<VEC>& pmeta,
-                      const TraceClass& pcls, const TraceMeta<VEC>& qmeta,
-                      const TraceClass& qcls, bool have_p, bool have_q,
-                      bool alive_in) __attribute__((always_inline)) {
+  // Step t from its slots and map entries; r1, r2: steps t-1, t-2 (classified),
+  // r3: step t-3 (its first touches popped).  Returns the read lane's row.
+  auto classify = [&](int t, const TraceIdx& m, int wraw, int rraw, TraceRoute& rt,
+                      const TraceRoute& r1, const TraceRoute& r2, const TraceRoute& r3,
+                      bool ok_prev) __attribute__((always_inline)) -> int {
     int lerr = m.err | base_err;
     if constexpr (!DENSE) {
-      if (lane < W && c.wraw >= C) lerr |= COWSDM_ERR_CORRUPT;
-      if (lane < R && c.rraw >= C) lerr |= COWSDM_ERR_CORRUPT;
+      if (lane < W && wraw >= C) { lerr |= COWSDM_ERR_CORRUPT; wraw = -1; }
+      if (lane < R && rraw >= C) { lerr |= COWSDM_ERR_CORRUPT; rraw = -1; }
     }
-    c.rsrc = -1;
-    c.wfwd = -1;
-    c.rfwd = -1;
+    int wsrc = -1, rsrc = -1, rraw_lane = -1;
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) {
       if (j < W) {
-        const int other = rl(m.widx, j);
-        if (lane < W && j < lane && other == m.widx) lerr |= COWSDM_ERR_DUP_WRITE;
-        if (lane < R && m.ridx == other) c.rsrc = j;
+        const int sj = rl(m.widx, j);
+        if (lane < W && lane > j && m.widx == sj) lerr |= COWSDM_ERR_DUP_WRITE;
+        if (lane < R && m.ridx == sj) rraw_lane = j;
       }
     }
-    if (have_p) {
+    if (!DENSE && t >= 2) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const int prev_slot = rl(pmeta.widx, j);
-          if (lane < W && m.widx == prev_slot) c.wfwd = j;
-          if (lane < R && c.rsrc < 0 && m.ridx == prev_slot) c.rfwd = j;
+          const int sj = rl(r2.widx, j);
+          if (lane < W && m.widx == sj) wsrc = 4 + j;
+          if (lane < R && m.ridx == sj) rsrc = 4 + j;
         }
       }
     }
-    if (!DENSE && have_q) {
+    if (t >= 1) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const int slot = rl(qmeta.widx, j);
-          const int row = rl(qcls.wphys, j);
-          if (lane < W && c.wfwd < 0 && m.widx == slot) c.wraw = row;
-          if (lane < R && c.rsrc < 0 && c.rfwd < 0 && m.ridx == slot) c.rraw = row;
+          const int sj = rl(r1.widx, j);
+          if (lane < W && m.widx == sj) wsrc = j;
+          if (lane < R && m.ridx == sj) rsrc = j;
         }
       }
     }
-    const int err = wave_or(lerr);
-    c.ok = alive_in && err == 0;
-    if (err && lane == 0 && !DENSE) {
-      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(err),
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!DENSE && t >= 3) {
+#pragma unroll
+      for (int j = 0; j < kTraceMaxWrites; ++j) {
+        if (j < W) {
+          const int sj = rl(r3.widx, j);
+          const int row = rl(r3.wrow, j);
+          if (lane < W && wsrc < 0 && m.widx == sj) wraw = row;
+          if (lane < R && rsrc < 0 && m.ridx == sj) rraw = row;
+        }
+      }
     }
-    c.first = (!DENSE && c.ok && lane < W && c.wfwd < 0 && c.wraw < 0) ? 1 : 0;
-    const uint64_t mask = __ballot(c.first);
-    c.count = c.ok ? __popcll(mask) : 0;
-    c.rank = __popcll(mask & ((1ull << lane) - 1));
-    c.wphys = c.wraw;
+    if (rraw_lane >= 0) rsrc = -1;
+    const bool any_err = __ballot(lerr != 0) != 0;
+    if (!DENSE && any_err && t < G) {
+      const int e = wave_or(lerr);
+      if (lane == 0) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(e),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    const bool ok = ok_prev && !any_err;
+    const bool first = !DENSE && ok && lane < W && wsrc < 0 && wraw < 0;
+    const uint64_t fm = __ballot(first);
+    const bool fix = __ballot((lane < W && wsrc >= 0) || (lane < R && rsrc >= 0)) != 0;
+    const bool raw = __ballot(lane < R && rraw_lane >= 0) != 0;
+    rt.u = static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
+           (ok ? 1u << 8 : 0u) | (fix ? 1u << 9 : 0u) | (raw ? 1u << 10 : 0u);
+    rt.rank = lanes_below(fm);
+    rt.widx = m.widx;
+    rt.ridx = m.ridx;
+    rt.wrow = lane < W ? wraw : -1;
+    rt.wsrc = lane < W ? wsrc : -1;
+    rt.rsrc = lane < R ? rsrc : -1;
+    rt.rraw = lane < R ? rraw_lane : -1;
+    return rraw;
   };
 
-  // updated rows of the last computed step, element j * VEC + v; one vector
-  // value so that the forwarding below (a wave-uniform but run-time row
-  // index) stays in registers
-  typedef float RowSet __attribute__((ext_vector_type(kTraceMaxWrites * VEC)));
-  RowSet cur = 0.0f;
-  float ncur_a[kTraceMaxWrites][VEC], ncur_b[kTraceMaxWrites][VEC];
-  float rv_a[kTraceMaxReads][VEC], rv_b[kTraceMaxReads][VEC];
+  auto publish = [&](int t, const TraceRoute& rt) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      if (lane == 0 && t < G) {
+        atomic_store_u64(&slots[static_cast<int64_t>(t) * B],
+                         slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(route_count(rt.u))));
+      }
+    }
+  };
+
+  auto issue_rows = [&](int t, const TraceRoute& rt, int rrow, TraceRows<VEC>& buf)
+      __attribute__((always_inline)) {
+    const int tc = t < G ? t : G - 1;
+    const float* wp;
+    const float* rp;
+    if constexpr (DENSE) {
+      wp = table_bank + static_cast<int64_t>(rt.widx) * D;
+      rp = table_bank + static_cast<int64_t>(rt.ridx) * D;
+    } else {
+      wp = rt.wrow < 0 ? m0_bank + static_cast<int64_t>(rt.widx) * D
+                       : L.values + static_cast<int64_t>(rt.wrow) * D;
+      rp = rrow < 0 ? m0_bank + static_cast<int64_t>(rt.ridx) * D
+                    : L.values + static_cast<int64_t>(rrow) * D;
+    }
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      if (j < W) {
+        const float* p = rl_ptr(wp, j);
+        gload_row<VEC>(p + col, buf.w[j]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kTraceMaxReads; ++i) {
+      if (i < R) {
+        const float* p = rl_ptr(rp, i);
+        gload_row<VEC>(p + col, buf.r[i]);
+      }
+    }
+    gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), buf.vin);
+    buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+    buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+  };
+
+  auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
+    const float* p = lds_wave + row * kRow + col;
+    if constexpr (VEC == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(p);
+      x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+    } else if constexpr (VEC == 2) {
+      const float2 t = *reinterpret_cast<const float2*>(p);
+      x[0] = t.x; x[1] = t.y;
+    } else {
+      x[0] = *p;
+    }
+  };
+  auto lds_put = [&](int row, const float (&x)[VEC]) __attribute__((always_inline)) {
+    float* p = lds_wave + row * kRow + col;
+    if constexpr (VEC == 4) {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    } else if constexpr (VEC == 2) {
+      *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+    } else {
+      *p = x[0];
+    }
+  };
+
+  // updated rows of the last computed step
+  float cur[kTraceMaxWrites][VEC];
 #pragma unroll
   for (int j = 0; j < kTraceMaxWrites; ++j) {
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) { ncur_a[j][v] = 0.0f; ncur_b[j][v] = 0.0f; }
+    for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
   }
-#pragma unroll
-  for (int i = 0; i < kTraceMaxReads; ++i) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) { rv_a[i][v] = 0.0f; rv_b[i][v] = 0.0f; }
-  }
+  bool alive = true;
 
-  // dst = row j of cur, j wave-uniform
-  auto copy_from_cur = [&](int j, float (&dst)[VEC]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) dst[v] = cur[j * VEC + v];
-  };
-
-  // loads of the rows step m needs that the previous step did not write
-  auto issue_loads = [&](const TraceMeta<VEC>& m, const TraceClass& c,
-                         float (&nc)[kTraceMaxWrites][VEC],
-                         float (&rv)[kTraceMaxReads][VEC]) __attribute__((always_inline)) {
-    if (!c.ok) return;
-#pragma unroll
-    for (int j = 0; j < kTraceMaxWrites; ++j) {
-      if (j < W && rl(c.wfwd, j) < 0) {
-        const int slot = rl(m.widx, j);
-        const float* src;
-        if constexpr (DENSE) {
-          src = table_bank + static_cast<int64_t>(slot) * D;
-        } else {
-          const int p = rl(c.wraw, j);
-          src = p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
-                      : L.values + static_cast<int64_t>(p) * D;
-        }
-        if (col_ok) load_row<VEC>(src + col, nc[j]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kTraceMaxReads; ++i) {
-      if (i < R && rl(c.rsrc, i) < 0 && rl(c.rfwd, i) < 0) {
-        const int slot = rl(m.ridx, i);
-        const float* src;
-        if constexpr (DENSE) {
-          src = table_bank + static_cast<int64_t>(slot) * D;
-        } else {
-          const int p = rl(c.rraw, i);
-          src = p < 0 ? m0_bank + static_cast<int64_t>(slot) * D
-                      : L.values + static_cast<int64_t>(p) * D;
-        }
-        if (col_ok) load_row<VEC>(src + col, rv[i]);
-      }
-    }
-  };
-
-  // rows of step m that the step just computed wrote, from registers
-  auto copy_forwarded = [&](const TraceClass& c, float (&nc)[kTraceMaxWrites][VEC],
-                            float (&rv)[kTraceMaxReads][VEC]) __attribute__((always_inline)) {
-    if (!c.ok) return;
-#pragma unroll
-    for (int j = 0; j < kTraceMaxWrites; ++j) {
-      if (j < W) {
-        const int fwd = rl(c.wfwd, j);
-        if (fwd >= 0) copy_from_cur(fwd, nc[j]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kTraceMaxReads; ++i) {
-      if (i < R && rl(c.rsrc, i) < 0) {
-        const int fwd = rl(c.rfwd, i);
-        if (fwd >= 0) copy_from_cur(fwd, rv[i]);
-      }
-    }
-  };
-
-  // gated-delta update of nc into cur and the sparse read of step s
-  auto compute = [&](const TraceMeta<VEC>& m, const TraceClass& c, int s,
-                     float (&nc)[kTraceMaxWrites][VEC],
-                     float (&rv)[kTraceMaxReads][VEC]) __attribute__((always_inline)) {
+  // Step t (parity par): LDS rows par*4 + j hold step t-2 until this step
+  // replaces them, rows (par^1)*4 + j hold step t-1.
+  auto compute = [&](int t, int par, const TraceRoute& rt, TraceRows<VEC>& buf)
+      __attribute__((always_inline)) {
+    const bool run = route_ok(rt.u) && alive;
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-    if (c.ok) {
-      const float forget = rlf(m.gate, 0);
-      const float in_gate = rlf(m.gate, 1);
-      const float er_gate = rlf(m.gate, 2);
-      const float alpha = static_cast<float>(exp(static_cast<double>(forget)));
+    if (run) {
+      if (route_fix(rt.u)) {
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          if (j < W) {
+            const int src = rl(rt.wsrc, j);
+            if (src >= 0) {
+              const int row = src < 4 ? (par ^ 1) * 4 + src : par * 4 + (src - 4);
+              lds_get(row, buf.w[j]);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kTraceMaxReads; ++i) {
+          if (i < R) {
+            const int src = rl(rt.rsrc, i);
+            if (src >= 0) {
+              const int row = src < 4 ? (par ^ 1) * 4 + src : par * 4 + (src - 4);
+              lds_get(row, buf.r[i]);
+            }
+          }
+        }
+      }
+      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t));
+      const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t));
+      const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t));
       float ret[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) ret[v] = 0.0f;
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = rlf(m.ww, j);
+          const float wj = rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
-            const float d = nc[j][v] * alpha;
-            cur[j * VEC + v] = d;
+            const float d = buf.w[j][v] * alpha;
+            cur[j][v] = d;
             const float term = wj * d;
             ret[v] = (j == 0) ? term : ret[v] + term;
           }
@@ -317,177 +440,261 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       float delta[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        const float a = in_gate * m.vin[v];
+        const float a = in_gate * buf.vin[v];
         const float e = er_gate * ret[v];
         delta[v] = a - e;
       }
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = rlf(m.ww, j);
+          const float wj = rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
-            const float t = wj * delta[v];
-            cur[j * VEC + v] = cur[j * VEC + v] + t;
+            const float u = wj * delta[v];
+            cur[j][v] = cur[j][v] + u;
+          }
+          lds_put(par * 4 + j, cur[j]);
+        }
+      }
+      if (route_raw(rt.u)) {
+#pragma unroll
+        for (int i = 0; i < kTraceMaxReads; ++i) {
+          if (i < R) {
+            const int src = rl(rt.rraw, i);
+            if (src >= 0) lds_get(par * 4 + src, buf.r[i]);
           }
         }
       }
 #pragma unroll
       for (int i = 0; i < kTraceMaxReads; ++i) {
         if (i < R) {
-          const int src = rl(c.rsrc, i);
-          float x[VEC];
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) x[v] = rv[i][v];
-          if (src >= 0) copy_from_cur(src, x);
-          const float wr = rlf(m.rw, i);
+          const float wr = rlf(buf.rw, i);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
-            const float term = wr * x[v];
+            const float term = wr * buf.r[i][v];
             acc[v] = (i == 0) ? term : acc[v] + term;
           }
         }
       }
     }
-    float* out = reinterpret_cast<float*>(const_cast<char*>(step_in(L.output, 8, s)));
-    if (col_ok) store_row<VEC>(out + b * D + col, acc);
-    if (c.ok) {
+    gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), acc);
+    if (run) {
+      float* const dst = DENSE ? table_bank + static_cast<int64_t>(rt.widx) * D
+                               : L.values + static_cast<int64_t>(rt.wrow < 0 ? 0 : rt.wrow) * D;
+      const uint32_t fmask = route_fmask(rt.u);
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W && !rl(c.first, j)) {
-          float* dst = DENSE ? table_bank + static_cast<int64_t>(rl(m.widx, j)) * D
-                             : L.values + static_cast<int64_t>(rl(c.wphys, j)) * D;
-          float row[VEC];
-          copy_from_cur(j, row);
-          if (col_ok) store_row<VEC>(dst + col, row);
+        if (j < W && !((fmask >> j) & 1u)) {
+          float* p = const_cast<float*>(rl_ptr(dst, j));
+          gstore_row<VEC>(p + col, cur[j]);
         }
       }
     }
   };
 
-  // pops of step s: rows, map entries; returns false when the step did not fit
-  int64_t last_inclusive = 0;
-  bool last_poisoned = false;
-  auto resolve = [&](const TraceMeta<VEC>& m, TraceClass& c, int s) __attribute__((always_inline)) -> bool {
-    bool poisoned = false;
-    const int q = s * B + bank;
-    const int64_t prefix = resolve_prefix(slots, q, epoch, c.count, lane, &poisoned);
-    last_inclusive = prefix + c.count;
-    last_poisoned = poisoned;
-    bool fits = c.ok && !poisoned && (c.count == 0 || prefix + c.count <= old_free);
-    const int64_t from_top = prefix + c.rank;
-    const int src_lane = static_cast<int>(from_top % kWave);
-    int window_row = -1;
+  // ---- pops (packed)
+  int base = 0;     // first touches of the launch's earlier steps, all banks
+  int served = 0;   // largest inclusive prefix that fits the free stack
+  bool over = false;
+  uint64_t sw[kTraceScanWindows];
 #pragma unroll
-    for (int k = 0; k < kFreeWindow / kWave; ++k) {
-      const int v = __shfl(free_top[k], src_lane, kWave);
-      if (from_top / kWave == k) window_row = v;
+  for (int k = 0; k < kTraceScanWindows; ++k) sw[k] = 0;
+  const int64_t* const step_words = DENSE ? nullptr : slots - bank;  // word of (t, b): t*B + b
+
+  auto issue_scan = [&](int t) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      const int64_t tc = t < G ? t : G - 1;
+#pragma unroll
+      for (int k = 0; k < kTraceScanWindows; ++k) {
+        if (k * kWave < B) {
+          const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
+          sw[k] = atomic_load_u64(&step_words[tc * B + bk]);
+        }
+      }
     }
+  };
+
+  // Step t's first touches, after its counts (sw) have been loaded.  r1, r2:
+  // steps t+1 and t+2, whose rewrites of step t's slots take its physical rows.
+  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, TraceRoute& r2)
+      __attribute__((always_inline)) {
+    int partial = 0, total = 0;
+    bool poisoned = false;
+    auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+      return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
+    };
+#pragma unroll
+    for (int k = 0; k < kTraceScanWindows; ++k) {
+      if (k * kWave < B) {
+        const bool in = k * kWave + lane < B;
+        uint64_t w = sw[k];
+        bool ready = !in || word_ready(w);
+        if (__ballot(!ready) != 0) {
+          // a bank has not published step t yet: bounded wait
+          int spins = 0;
+          while (!ready && spins < kSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+            w = atomic_load_u64(&step_words[static_cast<int64_t>(t) * B + k * kWave + lane]);
+            ready = word_ready(w);
+            ++spins;
+          }
+          if (__ballot(!ready) != 0) poisoned = true;
+          sw[k] = ready ? w : 0;
+        }
+        const int v = (in && ready) ? static_cast<int>(w & 7u) : 0;
+        const uint64_t b0 = __ballot(v & 1), b1 = __ballot(v & 2), b2 = __ballot(v & 4);
+        const int below = bank - k * kWave;
+        const uint64_t m = below <= 0 ? 0ull : (below >= kWave ? ~0ull : ((1ull << below) - 1));
+        partial += static_cast<int>(sum3(b0, b1, b2, m));
+        total += static_cast<int>(sum3(b0, b1, b2, ~0ull));
+      }
+    }
+    if (!over) {
+      if (base + total <= old_free) {
+        served = base + total;
+      } else {
+        // largest inclusive prefix of this step's banks that still fits
+        over = true;
+        int carry = base;
+        bool done = false;
+#pragma unroll
+        for (int k = 0; k < kTraceScanWindows; ++k) {
+          if (k * kWave < B && !done) {
+            const bool in = k * kWave + lane < B;
+            const int v = (in && word_ready(sw[k])) ? static_cast<int>(sw[k] & 7u) : 0;
+            const uint64_t b0 = __ballot(v & 1), b1 = __ballot(v & 2), b2 = __ballot(v & 4);
+            const int incl = carry + lanes_below(b0) + 2 * lanes_below(b1) + 4 * lanes_below(b2) + v;
+            const uint64_t fit = __ballot(in && incl <= old_free);
+            if (fit != 0) served = __shfl(incl, 63 - __clzll(static_cast<long long>(fit)), kWave);
+            if (fit != __ballot(in)) done = true;
+            carry += static_cast<int>(sum3(b0, b1, b2, ~0ull));
+          }
+        }
+      }
+    }
+    const int prefix = base + partial;
+    base += total;
+
+    const int count = route_count(rt.u);
+    const uint32_t fmask = route_fmask(rt.u);
+    const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
+    bool fits = route_ok(rt.u) && alive && !poisoned && (count == 0 || prefix + count <= old_free);
     int new_row = -1;
-    int bad_row = 0;
-    if (fits && c.first) {
-      new_row = from_top < kFreeWindow ? window_row : L.free_rows[old_free - 1 - from_top];
-      if (new_row < 0 || new_row >= C) bad_row = 1;
-    }
-    if (__ballot(bad_row) != 0) {
-      fits = false;
-      if (lane == 0) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+    if (fits && count > 0) {
+      const int k = prefix + rt.rank;
+      if (first && k < window) new_row = lds_free[k];
+      if (__ballot(first && k >= window) != 0) {
+        if (first && k >= window) new_row = L.free_rows[old_free - 1 - k];
+      }
+      if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
+        fits = false;
+        if (lane == 0) {
+          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
     if (lane == 0) {
-      if (c.ok && !fits && c.count > 0 && !poisoned) *L.overflow_flag = 1;
+      if (route_ok(rt.u) && alive && !poisoned && !fits && count > 0) *L.overflow_flag = 1;
       if (poisoned) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                               static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (fits && c.count > 0) {
-      if (c.first) {
-        c.wphys = new_row;
-        map_bank[m.widx] = new_row;
+    if (fits && count > 0) {
+      if (first) {
+        rt.wrow = new_row;
+        map_bank[rt.widx] = new_row;
       }
+      float* const dst = L.values + static_cast<int64_t>(rt.wrow < 0 ? 0 : rt.wrow) * D;
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W && rl(c.first, j)) {
-          float* dst = L.values + static_cast<int64_t>(rl(c.wphys, j)) * D;
-          float row[VEC];
-          copy_from_cur(j, row);
-          if (col_ok) store_row<VEC>(dst + col, row);
+        if (j < W && ((fmask >> j) & 1u)) {
+          float* p = const_cast<float*>(rl_ptr(dst, j));
+          gstore_row<VEC>(p + col, cur[j]);
         }
       }
     }
-    return fits;
+    alive = alive && fits;
+    // steps t+1 and t+2 rewrite some of step t's slots in the rows just found
+    const int s1 = r1.wsrc;
+    const int v1 = __shfl(rt.wrow, s1 >= 0 ? (s1 & 3) : 0, kWave);
+    if (s1 >= 0 && s1 < 4) r1.wrow = v1;
+    const int s2 = r2.wsrc;
+    const int v2 = __shfl(rt.wrow, s2 >= 0 ? (s2 & 3) : 0, kWave);
+    if (s2 >= 4) r2.wrow = v2;
   };
 
-  // ---- prologue: step 0 classified, published, its rows in flight
-  TraceMeta<VEC> cm, nm, pm;   // steps s, s+1, s-1
-  TraceClass cc, nc, pc;
-  bool alive = true;
-  load_meta(0, cm);
-  issue_map(cm, cc);
-  classify(cm, cc, cm, cc, cm, cc, false, false, alive);
-  if constexpr (!DENSE) publish_aggregate(slots, bank, epoch, cc.count, lane);
-  issue_loads(cm, cc, ncur_a, rv_a);
-  if (G > 1) load_meta(1, nm);
-  pm = cm;
-  pc = cc;
+  // ---- prologue: steps 0 and 1 classified with their rows in flight
+  TraceRows<VEC> bufA, bufB;
+#pragma unroll
+  for (int j = 0; j < kTraceMaxWrites; ++j) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) { bufA.w[j][v] = 0.0f; bufB.w[j][v] = 0.0f; }
+  }
+#pragma unroll
+  for (int i = 0; i < kTraceMaxReads; ++i) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) { bufA.r[i][v] = 0.0f; bufB.r[i][v] = 0.0f; }
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) { bufA.vin[v] = 0.0f; bufB.vin[v] = 0.0f; }
+  TraceIdx i0, i1, i2, i3;
+  load_idx(0, i0);
+  load_idx(1, i1);
+  load_idx(2, i2);
+  load_idx(3, i3);
+  int mw0, mr0, mw1, mr1, mw2, mr2;
+  issue_map(i0, mw0, mr0);
+  issue_map(i1, mw1, mr1);
+  issue_map(i2, mw2, mr2);
+  TraceRoute q, r0, r1;
+  q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
+  {
+    const int rrow = classify(0, i0, mw0, mr0, r0, q, q, q, true);
+    publish(0, r0);
+    issue_rows(0, r0, rrow, bufA);
+  }
+  {
+    const int rrow = classify(1, i1, mw1, mr1, r1, r0, q, q, route_ok(r0.u));
+    publish(1, r1);
+    issue_rows(1, r1, rrow, bufB);
+  }
+  issue_scan(0);
 
-  auto iteration = [&](int s, float (&nc_c)[kTraceMaxWrites][VEC],
-                       float (&rv_c)[kTraceMaxReads][VEC], float (&nc_n)[kTraceMaxWrites][VEC],
-                       float (&rv_n)[kTraceMaxReads][VEC]) __attribute__((always_inline)) {
-    const bool has_next = s + 1 < G;
-    // 0. map lookups of step s+1
-    if (has_next) issue_map(nm, nc);
-    // 1. pops of step s-1 (its updated rows are still in cur)
-    if constexpr (!DENSE) {
-      if (s > 0) {
-        const bool fits = resolve(pm, pc, s - 1);
-        alive = alive && fits;
-        if (!fits) cc.ok = 0;
-        const int fwd_row = __shfl(pc.wphys, cc.wfwd < 0 ? 0 : cc.wfwd, kWave);
-        if (cc.wfwd >= 0) cc.wphys = fwd_row;
-      }
-    }
-    // 2. step s+1: classify, publish, issue its loads
-    if (has_next) {
-      classify(nm, nc, cm, cc, pm, pc, true, s > 0, alive && cc.ok);
-      if constexpr (!DENSE) publish_aggregate(slots, (s + 1) * B + bank, epoch, nc.count, lane);
-      issue_loads(nm, nc, nc_n, rv_n);
-    }
-    // 3. step s
-    compute(cm, cc, s, nc_c, rv_c);
-    // 4. rows step s wrote, into step s+1
-    if (has_next) copy_forwarded(nc, nc_n, rv_n);
-    // 5. rotate
-    pm = cm;
-    pc = cc;
-    if (has_next) {
-      cm = nm;
-      cc = nc;
-      if (s + 2 < G) load_meta(s + 2, nm);
-    }
+  auto iteration = [&](int s, int par, TraceRows<VEC>& buf) __attribute__((always_inline)) {
+    TraceIdx i4;
+    load_idx(s + 4, i4);
+    int mw3, mr3;
+    issue_map(i3, mw3, mr3);
+    compute(s, par, r0, buf);
+    TraceRoute r2;
+    const int rrow = classify(s + 2, i2, mw2, mr2, r2, r1, r0, q, route_ok(r1.u));
+    publish(s + 2, r2);
+    issue_rows(s + 2, r2, rrow, buf);
+    if constexpr (!DENSE) resolve(s, r0, r1, r2);
+    issue_scan(s + 1);
+    q = r0;
+    r0 = r1;
+    r1 = r2;
+    i2 = i3;
+    i3 = i4;
+    mw2 = mw3;
+    mr2 = mr3;
   };
   for (int s = 0; s < G; s += 2) {
-    iteration(s, ncur_a, rv_a, ncur_b, rv_b);
-    if (s + 1 < G) iteration(s + 1, ncur_b, rv_b, ncur_a, rv_a);
+    iteration(s, 0, bufA);
+    if (s + 1 < G) iteration(s + 1, 1, bufB);
   }
 
-  // ---- epilogue: pops of the last step; the last pair closes the launch
+  // ---- the last bank closes the launch
   if constexpr (!DENSE) {
-    resolve(pm, pc, G - 1);
-    if (bank == B - 1) {
-      int64_t served = last_inclusive;
-      if (last_poisoned || served > old_free) {
-        served = fitting_prefix(slots, G * B, epoch, old_free, lane);
-      }
-      if (lane == 0) {
-        *L.free_count = static_cast<int32_t>(old_free - served);
-        atomic_store_u64(&scan[COWSDM_SCRATCH_EPOCH], static_cast<uint64_t>(epoch + 1u));
-      }
+    if (bank == B - 1 && lane == 0) {
+      *L.free_count = old_free - served;
+      int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
+      atomic_store_u64(&scan[COWSDM_SCRATCH_EPOCH], static_cast<uint64_t>(epoch + 1u));
     }
   }
 }
