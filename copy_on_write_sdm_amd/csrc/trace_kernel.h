@@ -71,10 +71,13 @@ typedef __attribute__((address_space(1))) float gfloat;
 typedef float vf2 __attribute__((ext_vector_type(2)));
 typedef float vf4 __attribute__((ext_vector_type(4)));
 
-// Row accesses through global-address-space pointers (global_load/store with
-// a scalar base), not generic ones.
+// Row accesses at a wave-uniform base plus this lane's 32-bit byte offset,
+// through global-address-space pointers: global_load/store with a scalar
+// base, no per-lane 64-bit address arithmetic.
 template <int VEC>
-__device__ __forceinline__ void gload_row(const float* p, float (&x)[VEC]) {
+__device__ __forceinline__ void gload_row(const float* base, uint32_t off, float (&x)[VEC]) {
+  const __attribute__((address_space(1))) char* p =
+      (const __attribute__((address_space(1))) char*)(base) + off;
   if constexpr (VEC == 4) {
     const vf4 t = *(const __attribute__((address_space(1))) vf4*)(p);
     x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
@@ -87,7 +90,8 @@ __device__ __forceinline__ void gload_row(const float* p, float (&x)[VEC]) {
 }
 
 template <int VEC>
-__device__ __forceinline__ void gstore_row(float* p, const float (&x)[VEC]) {
+__device__ __forceinline__ void gstore_row(float* base, uint32_t off, const float (&x)[VEC]) {
+  __attribute__((address_space(1))) char* p = (__attribute__((address_space(1))) char*)(base) + off;
   if constexpr (VEC == 4) {
     vf4 t;
     t.x = x[0]; t.y = x[1]; t.z = x[2]; t.w = x[3];
@@ -118,7 +122,8 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
   return __popcll(b0 & m) + 2 * __popcll(b1 & m) + 4 * __popcll(b2 & m);
 }
 
-template <typename IDX, int VEC, bool DENSE>
+// FULL: W == kTraceMaxWrites and R == kTraceMaxReads, every row guard folds away.
+template <typename IDX, int VEC, bool DENSE, bool FULL>
 __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
   __shared__ float lds_rows[kBanksPerBlock][2][kTraceMaxWrites][kRow];
@@ -133,14 +138,15 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 
   const int N = P.slots;
   const int D = P.width;
-  const int W = P.writes;
-  const int R = P.reads;
+  const int W = FULL ? kTraceMaxWrites : P.writes;
+  const int R = FULL ? kTraceMaxReads : P.reads;
   const int B = P.banks;
   const int G = P.steps;
   const int C = static_cast<int>(L.capacity_rows);  // rows are int32
   // lanes past the row width repeat the last columns: they load, compute and
   // store exactly what the last full lane does, so no access needs a lane mask
   const int col = lane * VEC < D ? lane * VEC : D - VEC;
+  const uint32_t coff = static_cast<uint32_t>(col) * 4u;
 
   // ---- launch constants
   int base_err = 0;
@@ -340,17 +346,17 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
     for (int j = 0; j < kTraceMaxWrites; ++j) {
       if (j < W) {
         const float* p = rl_ptr(wp, j);
-        gload_row<VEC>(p + col, buf.w[j]);
+        gload_row<VEC>(p, coff, buf.w[j]);
       }
     }
 #pragma unroll
     for (int i = 0; i < kTraceMaxReads; ++i) {
       if (i < R) {
         const float* p = rl_ptr(rp, i);
-        gload_row<VEC>(p + col, buf.r[i]);
+        gload_row<VEC>(p, coff, buf.r[i]);
       }
     }
-    gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), buf.vin);
+    gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
     buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
     buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
   };
@@ -477,7 +483,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         }
       }
     }
-    gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), acc);
+    gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), 0u, acc);
     if (run) {
       float* const dst = DENSE ? table_bank + static_cast<int64_t>(rt.widx) * D
                                : L.values + static_cast<int64_t>(rt.wrow < 0 ? 0 : rt.wrow) * D;
@@ -486,7 +492,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W && !((fmask >> j) & 1u)) {
           float* p = const_cast<float*>(rl_ptr(dst, j));
-          gstore_row<VEC>(p + col, cur[j]);
+          gstore_row<VEC>(p, coff, cur[j]);
         }
       }
     }
@@ -613,7 +619,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W && ((fmask >> j) & 1u)) {
           float* p = const_cast<float*>(rl_ptr(dst, j));
-          gstore_row<VEC>(p + col, cur[j]);
+          gstore_row<VEC>(p, coff, cur[j]);
         }
       }
     }
@@ -705,13 +711,18 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 // back to one launch per step.
 template <typename IDX, bool DENSE>
 bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) {
-  static int resident[3] = {-1, -1, -1};
+  const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
+  const void* kernels[2][3] = {
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true>)}};
+  static int resident[2][3] = {{-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
-  const void* kernel =
-      vec == 4 ? reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE>)
-      : vec == 2 ? reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE>)
-                 : reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE>);
-  if (resident[which] < 0) {
+  const void* kernel = kernels[full][which];
+  if (resident[full][which] < 0) {
     int device = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
@@ -719,23 +730,15 @@ bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) 
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStepThreads, 0) !=
             hipSuccess) {
       (void)hipGetLastError();
-      resident[which] = 0;
+      resident[full][which] = 0;
     } else {
-      resident[which] = cus * per_cu;
+      resident[full][which] = cus * per_cu;
     }
   }
-  if (blocks > resident[which]) return false;
-  if (vec == 4) {
-    hipLaunchKernelGGL((sdm_trace_kernel<IDX, 4, DENSE>), dim3(blocks), dim3(kStepThreads), 0,
-                       stream, P);
-  } else if (vec == 2) {
-    hipLaunchKernelGGL((sdm_trace_kernel<IDX, 2, DENSE>), dim3(blocks), dim3(kStepThreads), 0,
-                       stream, P);
-  } else {
-    hipLaunchKernelGGL((sdm_trace_kernel<IDX, 1, DENSE>), dim3(blocks), dim3(kStepThreads), 0,
-                       stream, P);
-  }
-  return true;
+  if (blocks > resident[full][which]) return false;
+  void* args[] = {const_cast<StepParams*>(&P)};
+  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kStepThreads), args, 0, stream);
+  return true;  // a failed launch is reported by the caller's launch_status()
 }
 
 }  // namespace cowsdm_impl
