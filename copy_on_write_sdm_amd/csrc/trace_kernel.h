@@ -3,25 +3,25 @@
 // bank), with results identical to G single-step launches.
 //
 // Each wave owns one (layer, bank) for all G steps and software-pipelines
-// them, so that every memory access has about one iteration to land before
+// them so that every memory access has about one iteration to land before
 // its value is used.  Iteration s
-//   1. loads the slots of step s+4;
-//   2. loads the map entries of step s+3;
-//   3. computes step s (gated-delta update, sparse read) from rows loaded two
-//      iterations earlier; stores its reading and the rows already private;
-//   4. classifies step s+2 (first touches, rows written by steps s+1 and s,
+//   1. loads every bank's first-touch count of step s (published one
+//      iteration earlier), the slots of step s+3 (s+2 for dense tables) and
+//      the map entries of step s+2;
+//   2. classifies step s+1 (first touches, slots written by steps s and s-1,
 //      read-after-write), publishes its first-touch count and loads its rows;
-//   5. pops the free rows of step s's first touches and stores them and their
-//      map entries;
-//   6. loads every bank's first-touch count of step s+1.
-// Step t's map entries are read before steps t-3 .. t-1 have stored their
-// first touches: slots written at t-1 and t-2 take their rows from those
-// steps' results, kept in LDS, and slots written at t-3 take the physical rows
-// popped in 5.  Every other row step t needs was stored earlier by the same
-// wave, in program order.  Row buffers alternate between even and odd steps
-// (the loop is unrolled by two), so all of them stay in registers; per-row
-// values that depend on run-time lanes are read from LDS, never selected out
-// of registers.
+//   3. computes step s (gated-delta update, sparse read) from rows loaded one
+//      iteration earlier; stores its reading and the rows already private;
+//   4. pops the free rows of step s's first touches and stores them and their
+//      map entries.
+// Step t's map entries are read before steps t-2 and t-1 have stored their
+// first touches: slots written at t-1 take their rows from that step's
+// result, kept in LDS, and slots written at t-2 take the physical rows popped
+// for them.  Every other row step t needs was stored earlier by the same
+// wave, in program order.  Values in flight live in even/odd homes (the loop
+// is unrolled by two) and are only read one iteration after their load was
+// issued, so no register copy waits on memory; per-row values picked by
+// run-time lanes are read from LDS, never selected out of registers.
 //
 // First touches of (step t, bank b) pop free_rows[F - 1 - Q(t, b) - rank],
 // where F is free_count at launch and Q the exclusive prefix of first-touch
@@ -52,13 +52,13 @@ struct TraceIdx {                   // lane j: write slot j / read slot j
 struct TraceRoute {                 // a classified step
   int widx, ridx;
   int wrow;       // write lane: physical row (-1: M0, or a first touch not yet popped)
-  int wsrc;       // write lane: written by step t-1 lane j (j) or t-2 lane j (4+j); else -1
+  int wsrc;       // write lane: written by step t-1 lane j (j), else -1
   int rsrc;       // read lane: the same
   int rraw;       // read lane: write lane of step t itself with this slot, else -1
   int rank;       // write lane: rank among the bank's first touches
   uint32_t u;     // wave-uniform: bits 0-3 first-touch write lanes, 4-7 their count,
                   // 8 the step runs (routes valid, every earlier step ran),
-                  // 9 a row comes from step t-1 or t-2, 10 a read sees a write of step t
+                  // 9 a row comes from step t-1, 10 a read sees a write of step t
 };
 
 __device__ __forceinline__ uint32_t route_fmask(uint32_t u) { return u & 15u; }
@@ -126,7 +126,7 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
 template <typename IDX, int VEC, bool DENSE, bool FULL>
 __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
-  __shared__ float lds_rows[kBanksPerBlock][2][kTraceMaxWrites][kRow];
+  __shared__ float lds_rows[kBanksPerBlock][kTraceMaxWrites][kRow];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
 
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   float* const table_bank = DENSE ? L.values + static_cast<int64_t>(bank) * N * D : nullptr;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
-  float* const lds_wave = &lds_rows[wave][0][0][0];
+  float* const lds_wave = &lds_rows[wave][0][0];
 
   // ---- this lane's inputs at the launch's first step; step t adds t * stride
   const int wl = lane < W ? lane : 0;
@@ -243,11 +243,11 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // Step t from its slots and map entries; r1, r2: steps t-1, t-2 (classified),
-  // r3: step t-3 (its first touches popped).  Returns the read lane's row.
+  // Step t from its slots and map entries.  r1: step t-1 (classified), r2:
+  // step t-2 (its first touches popped).  Returns the read lane's row.
   auto classify = [&](int t, const TraceIdx& m, int wraw, int rraw, TraceRoute& rt,
-                      const TraceRoute& r1, const TraceRoute& r2, const TraceRoute& r3,
-                      bool ok_prev) __attribute__((always_inline)) -> int {
+                      const TraceRoute& r1, const TraceRoute& r2, bool ok_prev)
+      __attribute__((always_inline)) -> int {
     int lerr = m.err | base_err;
     if constexpr (!DENSE) {
       if (lane < W && wraw >= C) { lerr |= COWSDM_ERR_CORRUPT; wraw = -1; }
@@ -262,16 +262,6 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         if (lane < R && m.ridx == sj) rraw_lane = j;
       }
     }
-    if (!DENSE && t >= 2) {
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W) {
-          const int sj = rl(r2.widx, j);
-          if (lane < W && m.widx == sj) wsrc = 4 + j;
-          if (lane < R && m.ridx == sj) rsrc = 4 + j;
-        }
-      }
-    }
     if (t >= 1) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
@@ -282,12 +272,12 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         }
       }
     }
-    if (!DENSE && t >= 3) {
+    if (!DENSE && t >= 2) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const int sj = rl(r3.widx, j);
-          const int row = rl(r3.wrow, j);
+          const int sj = rl(r2.widx, j);
+          const int row = rl(r2.wrow, j);
           if (lane < W && wsrc < 0 && m.widx == sj) wraw = row;
           if (lane < R && rsrc < 0 && m.ridx == sj) rraw = row;
         }
@@ -393,9 +383,8 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   }
   bool alive = true;
 
-  // Step t (parity par): LDS rows par*4 + j hold step t-2 until this step
-  // replaces them, rows (par^1)*4 + j hold step t-1.
-  auto compute = [&](int t, int par, const TraceRoute& rt, TraceRows<VEC>& buf)
+  // Step t: LDS row j holds write j of step t-1 until this step replaces it.
+  auto compute = [&](int t, const TraceRoute& rt, TraceRows<VEC>& buf)
       __attribute__((always_inline)) {
     const bool run = route_ok(rt.u) && alive;
     float acc[VEC];
@@ -407,20 +396,14 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         for (int j = 0; j < kTraceMaxWrites; ++j) {
           if (j < W) {
             const int src = rl(rt.wsrc, j);
-            if (src >= 0) {
-              const int row = src < 4 ? (par ^ 1) * 4 + src : par * 4 + (src - 4);
-              lds_get(row, buf.w[j]);
-            }
+            if (src >= 0) lds_get(src, buf.w[j]);
           }
         }
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
           if (i < R) {
             const int src = rl(rt.rsrc, i);
-            if (src >= 0) {
-              const int row = src < 4 ? (par ^ 1) * 4 + src : par * 4 + (src - 4);
-              lds_get(row, buf.r[i]);
-            }
+            if (src >= 0) lds_get(src, buf.r[i]);
           }
         }
       }
@@ -459,7 +442,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
             const float u = wj * delta[v];
             cur[j][v] = cur[j][v] + u;
           }
-          lds_put(par * 4 + j, cur[j]);
+          lds_put(j, cur[j]);
         }
       }
       if (route_raw(rt.u)) {
@@ -467,7 +450,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         for (int i = 0; i < kTraceMaxReads; ++i) {
           if (i < R) {
             const int src = rl(rt.rraw, i);
-            if (src >= 0) lds_get(par * 4 + src, buf.r[i]);
+            if (src >= 0) lds_get(src, buf.r[i]);
           }
         }
       }
@@ -520,9 +503,9 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // Step t's first touches, after its counts (sw) have been loaded.  r1, r2:
-  // steps t+1 and t+2, whose rewrites of step t's slots take its physical rows.
-  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, TraceRoute& r2)
+  // Step t's first touches, after its counts (sw) have been loaded.  r1: step
+  // t+1, whose rewrites of step t's slots take its physical rows.
+  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1)
       __attribute__((always_inline)) {
     int partial = 0, total = 0;
     bool poisoned = false;
@@ -591,6 +574,9 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       if (first && k < window) new_row = lds_free[k];
       if (__ballot(first && k >= window) != 0) {
         if (first && k >= window) new_row = L.free_rows[old_free - 1 - k];
+        // wait for it here, on this rare path, so that no later use of the
+        // popped rows has to drain every load in flight
+        asm volatile("" ::"v"(new_row));
       }
       if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
         fits = false;
@@ -624,16 +610,13 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       }
     }
     alive = alive && fits;
-    // steps t+1 and t+2 rewrite some of step t's slots in the rows just found
+    // step t+1 rewrites some of step t's slots in the rows just found
     const int s1 = r1.wsrc;
-    const int v1 = __shfl(rt.wrow, s1 >= 0 ? (s1 & 3) : 0, kWave);
-    if (s1 >= 0 && s1 < 4) r1.wrow = v1;
-    const int s2 = r2.wsrc;
-    const int v2 = __shfl(rt.wrow, s2 >= 0 ? (s2 & 3) : 0, kWave);
-    if (s2 >= 4) r2.wrow = v2;
+    const int v1 = __shfl(rt.wrow, s1 >= 0 ? s1 : 0, kWave);
+    if (s1 >= 0) r1.wrow = v1;
   };
 
-  // ---- prologue: steps 0 and 1 classified with their rows in flight
+  // ---- prologue: step 0 classified with its rows in flight
   TraceRows<VEC> bufA, bufB;
 #pragma unroll
   for (int j = 0; j < kTraceMaxWrites; ++j) {
@@ -647,52 +630,59 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   }
 #pragma unroll
   for (int v = 0; v < VEC; ++v) { bufA.vin[v] = 0.0f; bufB.vin[v] = 0.0f; }
-  TraceIdx i0, i1, i2, i3;
-  load_idx(0, i0);
-  load_idx(1, i1);
-  load_idx(2, i2);
-  load_idx(3, i3);
-  int mw0, mr0, mw1, mr1, mw2, mr2;
-  issue_map(i0, mw0, mr0);
-  issue_map(i1, mw1, mr1);
-  issue_map(i2, mw2, mr2);
-  TraceRoute q, r0, r1;
+  // slots and map entries in flight, homed by the parity of the iteration
+  // that issued them
+  TraceIdx idxA, idxB, ready1, ready2;
+  int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
+  TraceRoute q, r0;
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   {
-    const int rrow = classify(0, i0, mw0, mr0, r0, q, q, q, true);
+    TraceIdx i0;
+    load_idx(0, i0);
+    int mw0, mr0;
+    issue_map(i0, mw0, mr0);
+    const int rrow = classify(0, i0, mw0, mr0, r0, q, q, true);
     publish(0, r0);
     issue_rows(0, r0, rrow, bufA);
   }
-  {
-    const int rrow = classify(1, i1, mw1, mr1, r1, r0, q, q, route_ok(r0.u));
-    publish(1, r1);
-    issue_rows(1, r1, rrow, bufB);
+  if constexpr (DENSE) {
+    load_idx(1, idxB);             // classified in iteration 0
+  } else {
+    load_idx(1, ready1);           // its map entries, classified in iteration 0
+    issue_map(ready1, mwB, mrB);
+    load_idx(2, idxB);             // its map entries are loaded in iteration 0
   }
-  issue_scan(0);
 
-  auto iteration = [&](int s, int par, TraceRows<VEC>& buf) __attribute__((always_inline)) {
-    TraceIdx i4;
-    load_idx(s + 4, i4);
-    int mw3, mr3;
-    issue_map(i3, mw3, mr3);
-    compute(s, par, r0, buf);
-    TraceRoute r2;
-    const int rrow = classify(s + 2, i2, mw2, mr2, r2, r1, r0, q, route_ok(r1.u));
-    publish(s + 2, r2);
-    issue_rows(s + 2, r2, rrow, buf);
-    if constexpr (!DENSE) resolve(s, r0, r1, r2);
-    issue_scan(s + 1);
+  // Iteration s.  `self` homes are written now and read in iteration s+1,
+  // `other` homes were written in iteration s-1 and are read now.
+  auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
+                       TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
+                       int& mw_other, int& mr_other) __attribute__((always_inline)) {
+    issue_scan(s);
+    TraceRoute r1;
+    if constexpr (DENSE) {
+      load_idx(s + 2, idx_self);
+      const int rrow = classify(s + 1, idx_other, -1, -1, r1, r0, q, route_ok(r0.u));
+      publish(s + 1, r1);
+      issue_rows(s + 1, r1, rrow, rows_next);
+      compute(s, r0, rows_s);
+    } else {
+      load_idx(s + 3, idx_self);
+      issue_map(idx_other, mw_self, mr_self);   // step s+2
+      ready2 = idx_other;
+      const int rrow = classify(s + 1, ready1, mw_other, mr_other, r1, r0, q, route_ok(r0.u));
+      publish(s + 1, r1);
+      issue_rows(s + 1, r1, rrow, rows_next);
+      compute(s, r0, rows_s);
+      resolve(s, r0, r1);
+      ready1 = ready2;
+    }
     q = r0;
     r0 = r1;
-    r1 = r2;
-    i2 = i3;
-    i3 = i4;
-    mw2 = mw3;
-    mr2 = mr3;
   };
   for (int s = 0; s < G; s += 2) {
-    iteration(s, 0, bufA);
-    if (s + 1 < G) iteration(s + 1, 1, bufB);
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
+    if (s + 1 < G) iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA);
   }
 
   // ---- the last bank closes the launch
