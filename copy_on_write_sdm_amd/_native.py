@@ -37,6 +37,7 @@ ERR_EXHAUSTED = 0x8
 ERR_TEMPLATE = 0x10
 ERR_CORRUPT = 0x20
 ERR_LOOKBACK = 0x40
+ERR_TRACE_RANGE = 0x80
 
 SCRATCH_EPOCH = 0
 SCRATCH_ERRORS = 3
@@ -145,6 +146,7 @@ class Trace(ctypes.Structure):
         ("scan_words", ctypes.c_int64),
         ("persistent", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("steps_recorded", ctypes.c_int64),
     ]
 
 
@@ -224,7 +226,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = restype
                 fn.argtypes = argtypes
-            if handle.cowsdm_abi_version() != 1:
+            if handle.cowsdm_abi_version() != 2:
                 raise RuntimeError("libcowsdm.so ABI version mismatch")
             _lib = handle
     return _lib

@@ -1183,6 +1183,7 @@ class DecodeTrace:
                      if persistent and not self.dense else None)
         self.trace.scan = None if self.scan is None else self.scan.data_ptr()
         self.trace.scan_words = words
+        self.trace.steps_recorded = steps
 
     def set_step(self, step: int) -> None:
         """Make the next launch run step ``step``."""
@@ -1218,9 +1219,13 @@ class DecodeTrace:
         if start is None:
             self.trace.step_index = self.step_index.data_ptr()
             self.trace.first_step = 0
-            self.trace.persistent = 0
-            nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
-                      "decode trace launch")
+            self.trace.persistent = int(self.persistent)
+            done = 0
+            while done < steps:
+                n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
+                nat.check(fn(layers, len(self.tables), self.shape, self.trace, n, stream),
+                          "decode trace launch")
+                done += n
             return
         if start < 0 or start + steps > self.steps:
             raise ValueError("trace launch runs past the recorded steps")

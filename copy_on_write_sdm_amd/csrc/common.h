@@ -46,6 +46,7 @@ struct StepParams {
   const int64_t* trace_step;     // device step counter, or null
   int64_t* trace_ticket;         // [0] launch, [1 + layer] dense per-layer
   int64_t trace_first;           // step of this launch when trace_step is null
+  int64_t trace_len;             // steps the trace inputs hold
   int64_t trace_stride[9];
   int64_t* scan;                 // persistent launches: per-layer scan words
   int64_t scan_words;            // words per layer in `scan`

@@ -691,6 +691,13 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   if (trace) {
     if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
     if (trace->first_step < 0) return fail(COWSDM_EARG, "trace: negative first step");
+    if (trace->steps_recorded <= 0) return fail(COWSDM_EARG, "trace: no recorded steps");
+    if (!trace->step_index && trace->first_step + steps > trace->steps_recorded) {
+      return fail(COWSDM_EARG, "trace: steps %lld..%lld past the %lld recorded",
+                  static_cast<long long>(trace->first_step),
+                  static_cast<long long>(trace->first_step + steps - 1),
+                  static_cast<long long>(trace->steps_recorded));
+    }
     if (nlayers > kMaxLayers) {
       return fail(COWSDM_ELIMIT, "trace launches take at most %d layers", kMaxLayers);
     }
@@ -713,7 +720,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     if (trace->stride_bytes[k] < 0 || trace->stride_bytes[k] >= (1ll << 32)) strides_fit = false;
   }
   const bool persistent = strides_fit &&
-      trace && !trace->step_index && trace->persistent && steps > 0 && trace_vec &&
+      trace && trace->persistent && steps > 0 && trace_vec &&
       shape->writes <= kTraceMaxWrites && shape->reads <= kTraceMaxReads &&
       nlayers <= kMaxLayers &&
       (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan &&
@@ -723,6 +730,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   P.trace_step = trace ? trace->step_index : nullptr;
   P.trace_ticket = trace ? trace->ticket : nullptr;
   P.trace_first = trace ? trace->first_step : 0;
+  P.trace_len = trace ? trace->steps_recorded : 0;
   P.scan = trace ? trace->scan : nullptr;
   P.scan_words = trace ? trace->scan_words : 0;
   P.steps = steps;
@@ -745,7 +753,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
       bool launched = true;
       for (int32_t done = 0; done < steps && launched; done += kTraceMaxSteps) {
         P.steps = (steps - done) < kTraceMaxSteps ? (steps - done) : kTraceMaxSteps;
-        P.trace_first = trace->first_step + done;
+        P.trace_first = trace->first_step + done;  // ignored when step_index is set
         if (dense) {
           launched = i64 ? launch_trace<int64_t, true>(P, blocks, trace_vec, stream)
                          : launch_trace<int32_t, true>(P, blocks, trace_vec, stream);

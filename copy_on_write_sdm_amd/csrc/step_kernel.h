@@ -23,6 +23,15 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   if (layer_id >= P.nlayers || bank >= P.banks) return;
   const cowsdm_layer_t& L = P.layer[layer_id];
   const int64_t trace_s = P.trace_step ? *P.trace_step : P.trace_first;
+  if (P.trace_step && (trace_s < 0 || trace_s >= P.trace_len)) {
+    // a replay past the recorded steps: touch no input, leave the counter
+    if (!DENSE && lane == 0 && L.scratch) {
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;
+  }
   auto step_ptr = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
     return static_cast<const char*>(base) + trace_s * P.trace_stride[k];
   };

@@ -135,6 +135,18 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   if (layer_id >= P.nlayers) return;  // whole workgroup
   const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock + wave;
   const cowsdm_layer_t& L = P.layer[layer_id];
+  // device-counted launches read their first step from the counter; every
+  // thread reads the same value (it changes only after all waves are done)
+  const int64_t first = P.trace_step ? *P.trace_step : P.trace_first;
+  if (P.trace_step && (first < 0 || first + P.steps > P.trace_len)) {
+    // a replay past the recorded steps: touch no input, leave the counter
+    if (!DENSE && threadIdx.x == 0) {
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return;  // whole workgroup
+  }
 
   const int N = P.slots;
   const int D = P.width;
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const int wl = lane < W ? lane : 0;
   const int rl_ = lane < R ? lane : 0;
   auto first_step = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
-    return static_cast<const char*>(base) + P.trace_first * P.trace_stride[k];
+    return static_cast<const char*>(base) + first * P.trace_stride[k];
   };
   const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
   const char* const ww_l = first_step(L.write_weights, 1) + (static_cast<int64_t>(bank) * W + wl) * 4;
@@ -691,6 +703,17 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       *L.free_count = old_free - served;
       int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
       atomic_store_u64(&scan[COWSDM_SCRATCH_EPOCH], static_cast<uint64_t>(epoch + 1u));
+    }
+  }
+  // ---- device-counted launches: the last wave to finish (every wave read
+  // the counter before taking its ticket) moves the counter past this launch
+  if (P.trace_step && lane == 0) {
+    const int64_t waves = static_cast<int64_t>(P.nlayers) * B;
+    const int64_t done = __hip_atomic_fetch_add(P.trace_ticket, int64_t{1}, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (done == waves - 1) {
+      atomic_store_u64(P.trace_ticket, 0);
+      atomic_store_u64(const_cast<int64_t*>(P.trace_step), static_cast<uint64_t>(first + G));
     }
   }
 }

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 1
+#define COWSDM_ABI_VERSION 2
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -54,6 +54,7 @@ extern "C" {
 #define COWSDM_ERR_TEMPLATE 0x10     /* template index outside [0, T)     */
 #define COWSDM_ERR_CORRUPT 0x20      /* map/free entry outside [0, C)     */
 #define COWSDM_ERR_LOOKBACK 0x40     /* bank-order scan did not complete  */
+#define COWSDM_ERR_TRACE_RANGE 0x80  /* trace step past steps_recorded    */
 
 /* Word offsets inside the per-layer step scratch (int64 words). */
 /* EPOCH retires the previous launch's scan slots (the layer's last bank
@@ -104,31 +105,34 @@ typedef struct cowsdm_layer {
   int32_t* allocated_rows_out;  /* scalar or null */
 } cowsdm_layer_t;
 
-/* Consecutive launches over device-resident inputs of many decode steps;
+/* Consecutive steps over device-resident inputs of many decode steps;
  * per-step inputs (and the output) sit at base + step * stride_bytes[k],
  * k in the order write_indices, write_weights, step_values, input_gate,
- * erase_gate, forget_log_gate, read_indices, read_weights, output.
- * With step_index null, launch i runs step first_step + i (the host
- * computes the offsets).  With step_index set, each launch reads the step
- * from *step_index and the last bank to finish advances it by one, so the
- * launches can be captured once in a hipGraph and replayed; ticket then
- * points at 1 + nlayers int64 words that are zero before the first launch
- * and stay zero between launches. */
+ * erase_gate, forget_log_gate, read_indices, read_weights, output, and the
+ * inputs hold steps_recorded steps.  With step_index null, the call runs
+ * steps first_step .. first_step + steps - 1 (the host computes the
+ * offsets).  With step_index set, the call runs `steps` steps from
+ * *step_index and the kernels advance *step_index by `steps`, so the call can
+ * be captured once in a hipGraph and replayed; ticket then points at
+ * 1 + nlayers int64 words that are zero before the first launch and stay zero
+ * between launches.  A device-counted launch whose steps would pass
+ * steps_recorded does nothing (packed state: sets COWSDM_ERR_TRACE_RANGE). */
 typedef struct cowsdm_trace {
   int64_t* step_index;
   int64_t* ticket;
   int64_t first_step;
   int64_t stride_bytes[9];
-  /* Persistent launches (host offsets only): with persistent != 0 one launch
-   * runs all `steps` steps when the shape allows it (W <= 4, R <= 16,
-   * D <= 256, every workgroup resident), else one launch per step.  Packed
-   * launches then need `scan`: nlayers blocks of scan_words int64 words
-   * (>= cowsdm_trace_scan_words(banks, steps)), zero before first use and
-   * kept valid by the kernels. */
+  /* Persistent launches: with persistent != 0 one launch runs up to 64
+   * steps when the shape allows it (W <= 4, R <= 16, D <= 256, banks <= 256
+   * for packed state, every workgroup resident), else one launch per step.
+   * Packed launches then need `scan`: nlayers blocks of scan_words int64
+   * words (>= cowsdm_trace_scan_words(banks, min(steps, 64))), zero before
+   * first use and kept valid by the kernels. */
   int64_t* scan;
   int64_t scan_words;
   int32_t persistent;
   int32_t reserved;
+  int64_t steps_recorded;
 } cowsdm_trace_t;
 
 /* ---------------------------------------------------------------- info */

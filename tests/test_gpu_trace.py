@@ -11,6 +11,7 @@ import pytest
 import torch
 
 import copy_on_write_sdm_amd as cow
+from copy_on_write_sdm_amd import _native as nat
 from copy_on_write_sdm_amd import synthetic
 from gpu_helpers import assert_state_equal
 from oracle import state as ref
@@ -138,26 +139,52 @@ def test_sticky_routes_forwarding(device, index_dtype):
         assert torch.equal(a.logical_to_physical, b.logical_to_physical)
 
 
-def test_device_counter_graph_replay(device):
+@pytest.mark.parametrize("persistent", [True, False])
+def test_device_counter_graph_replay(device, persistent):
+    """A captured launch of `group` device-counted steps, replayed: every
+    replay runs the next group, and a replay past the recorded steps does
+    nothing (packed state records COWSDM_ERR_TRACE_RANGE)."""
+
     layers, banks, steps, group = 3, 16, 24, 4
     _, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=64, width=128,
                                    writes=4, reads=16, steps=steps, seed=17)
     traced, single = states(), states()
     outputs = torch.empty(steps, layers, banks, 128, device=device)
-    tr = cow.DecodeTrace(states=traced, outputs=outputs, **kw)
+    tr = cow.DecodeTrace(states=traced, outputs=outputs, persistent=persistent, **kw)
     layer_array = tr.layer_array()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
         tr.launch(group, layer_array)
     tr.set_step(0)
-    for _ in range(steps // group):
+    for k in range(steps // group):
         graph.replay()
+        if k % 2:
+            torch.cuda.synchronize()   # eager work between replays
+            assert int(tr.step_index.item()) == (k + 1) * group
     torch.cuda.synchronize()
     assert int(tr.step_index.item()) == steps
     want = _per_step(single, routes, steps, layers)
     assert torch.equal(outputs, want)
     for a, b in zip(traced, single):
         assert torch.equal(a.materialize_dense(), b.materialize_dense())
+        a.validate_invariants()
+    before = outputs.clone()
+    graph.replay()                     # past the end of the recorded steps
+    torch.cuda.synchronize()
+    assert int(tr.step_index.item()) == steps
+    assert torch.equal(outputs, before)
+    for a in traced:
+        assert int(a.scratch[nat.SCRATCH_ERRORS]) & nat.ERR_TRACE_RANGE
+        with pytest.raises(AssertionError, match="recorded errors"):
+            a.validate_invariants()
+
+
+def test_host_offsets_past_recorded_steps_raise(device):
+    _, routes, states, kw = _setup(device, layers=1, banks=4, slots=32, width=64, writes=2,
+                                   reads=4, steps=6, seed=5)
+    tr = cow.DecodeTrace(states=states(), **kw)
+    with pytest.raises(ValueError, match="past the recorded steps"):
+        tr.launch(4, start=3)
 
 
 def test_persistent_overflow_sets_flag_and_keeps_partition(device):
