@@ -7,17 +7,18 @@ A 256-token prefix runs through the dense-table kernel, each layer's union of
 written slots is packed into a copy-on-write slab with a growth quantum of
 four decode steps (max(16, B*4*4) rows), then decode runs on the packed
 state.  One bench "step" is one decode token for all 7 layers and all B
-requests: one fused launch covering every (layer, bank).
+requests.
 
-Timing: W untimed warmup steps, then exactly K timed steps between
-synchronisations.  Steps run in groups of G (the growth quantum, 4): before a
-group every layer proves capacity for the group's worst case
-(prepare_step_capacity(B*W*G), growing the slab by the quantum when short),
-then one captured hipGraph replays the group's G launches; a graph is
-recaptured only when a slab grew.  The dense-table control runs the same
-routes the same way from the same packed state; both end states must be
-equal.  The CPU baseline is the torch restatement of the reference's
-dense-table step on the host cores, on a bounded sample.
+Decode loop: persistent launches of up to 64 steps for every (layer, bank);
+before every 4 steps each packed layer proves on the device that its free
+rows cover the worst case (prepare_step_capacity(B*W*4) of the reference's
+decode loop); a layer that would not is stopped there, grown on the host by
+prepare_step_capacity itself, and resumed, so growth matches the host-proven
+loop exactly.  W untimed warmup steps, then exactly K timed steps between
+synchronisations.  The dense-table control runs the same routes the same way
+from the same packed state; both end states must be equal.  The CPU baseline
+is the torch restatement of the reference's dense-table step on the host
+cores, on a bounded sample.
 """
 
 from __future__ import annotations
@@ -45,7 +46,9 @@ def parse():
     p.add_argument("--steps", type=int, default=448)
     p.add_argument("--warmup", type=int, default=64)
     p.add_argument("--batch", type=int, default=64)
-    p.add_argument("--group", type=int, default=4, help="decode steps per graph replay")
+    p.add_argument("--proof-steps", type=int, default=4,
+                   help="decode steps per capacity proof (the growth quantum's steps)")
+    p.add_argument("--launch-steps", type=int, default=64, help="decode steps per launch")
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")
@@ -119,7 +122,7 @@ def main() -> int:
     from copy_on_write_sdm_amd import synthetic
 
     dev = torch.device("cuda:0")
-    B, K, Wm, G = args.batch, args.steps, args.warmup, args.group
+    B, K, Wm = args.batch, args.steps, args.warmup
     total_steps = Wm + K
     quantum = max(16, B * WRITES * 4)
 
@@ -164,88 +167,40 @@ def main() -> int:
             growth_quantum_rows=quantum) for l in range(LAYERS)]
     packed = cow.DecodeTrace(states=states, **inputs)
     dense = cow.DecodeTrace(memories=dense_tables, **inputs)
-    capture_stream = torch.cuda.Stream()
 
-    class Runner:
-        """Replays groups of G steps; recaptures when slab pointers move."""
-
-        def __init__(self, trace, proof):
-            self.trace, self.proof = trace, proof
-            self.graphs, self.key = {}, None
-            self.launch_ms, self.launches, self.recaptures = 0.0, 0, 0
-            self.events = []
-
-        def pointers(self):
-            if self.trace.dense:
-                return tuple(t.data_ptr() for t in self.trace.tables)
-            return tuple((st.values.data_ptr(), st.free_rows.data_ptr())
-                         for st in self.trace.tables)
-
-        def group(self, n, timed):
-            if self.proof:
-                cow.PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
-                    self.trace.tables, B * WRITES * n)
-            key = self.pointers()
-            if key != self.key:
-                self.graphs, self.key = {}, key
-                self.recaptures += 1
-            if n not in self.graphs:
-                layers = self.trace.layer_array()
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=capture_stream):
-                    self.trace.launch(n, layers)
-                self.graphs[n] = graph
-            if timed:
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                self.graphs[n].replay()
-                e1.record()
-                self.events.append((e0, e1))
-                self.launches += n
-            else:
-                self.graphs[n].replay()
-
-        def run(self, steps, timed):
-            done = 0
-            while done < steps:
-                n = min(G, steps - done)
-                self.group(n, timed)
-                done += n
-
-        def kernel_ms(self):
-            return sum(a.elapsed_time(b) for a, b in self.events)
-
-    def measure(runner, label):
-        runner.trace.set_step(0)
-        runner.run(Wm, timed=False)
+    def measure(trace):
+        trace.set_step(0)
+        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
-        alloc0 = (sum(int(st.allocated_rows_tensor()) for st in runner.trace.tables)
-                  if not runner.trace.dense else 0)
-        grow0 = (sum(st.growth_events for st in runner.trace.tables)
-                 if not runner.trace.dense else 0)
+        alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
+                  if not trace.dense else 0)
+        grow0 = sum(st.growth_events for st in trace.tables) if not trace.dense else 0
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        runner.run(K, timed=True)
+        e0.record()
+        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
+        e1.record()
         torch.cuda.synchronize()
         seconds = time.perf_counter() - t0
-        new_rows = ((sum(int(st.allocated_rows_tensor()) for st in runner.trace.tables) - alloc0)
-                    if not runner.trace.dense else 0)
-        grows = ((sum(st.growth_events for st in runner.trace.tables) - grow0)
-                 if not runner.trace.dense else 0)
-        return seconds, new_rows, grows
+        new_rows = ((sum(int(st.allocated_rows_tensor()) for st in trace.tables) - alloc0)
+                    if not trace.dense else 0)
+        grows = (sum(st.growth_events for st in trace.tables) - grow0) if not trace.dense else 0
+        return dict(seconds=seconds, gpu_ms=e0.elapsed_time(e1), new_rows=new_rows,
+                    growths=grows, **report)
 
-    p_runner = Runner(packed, proof=True)
-    d_runner = Runner(dense, proof=False)
-    p_seconds, new_rows, timed_growths = measure(p_runner, "packed")
-    d_seconds, _, _ = measure(d_runner, "dense")
+    p_run = measure(packed)
+    d_run = measure(dense)
+    p_seconds, d_seconds = p_run["seconds"], d_run["seconds"]
+    new_rows, timed_growths = p_run["new_rows"], p_run["growths"]
 
     # both paths ran identical routes from identical logical state
     state_diff = max(float((st.materialize_dense() - t).abs().max())
                      for st, t in zip(states, dense_tables))
     for st in states:
         st.validate_invariants()
-    if int(packed.step_index.item()) != total_steps:
+    if packed.step_index.tolist() != [total_steps] * LAYERS:
         raise AssertionError("packed decode did not consume the trace")
 
     # ---- per-layer Python drop-in path (exact reference call pattern)
@@ -267,12 +222,13 @@ def main() -> int:
         torch.cuda.synchronize()
         eager = B * (n - 2) / (time.perf_counter() - t0)
 
-    launches = p_runner.launches
-    kernel_ms = p_runner.kernel_ms()
-    launch_us = 1000.0 * kernel_ms / launches
-    bytes_per_launch = algorithmic_bytes(B, LAYERS) + 8 * new_rows / max(1, launches)
+    # one launch runs launch_steps steps of all layers; its algorithmic bytes
+    # are the per-step bytes times the steps it ran
+    launches = p_run["launches"]
+    launch_us = 1000.0 * p_run["gpu_ms"] / launches
+    bytes_per_launch = (algorithmic_bytes(B, LAYERS) * K + 8 * new_rows) / launches
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
-    dense_launch_us = 1000.0 * d_runner.kernel_ms() / d_runner.launches
+    dense_launch_us = 1000.0 * d_run["gpu_ms"] / d_run["launches"]
 
     result = {
         "metric": METRIC,
@@ -293,8 +249,9 @@ def main() -> int:
                          f"batch {B}, prefix {PREFIX}, growth quantum 4 steps"),
             "batch": B, "layers": LAYERS, "slots": SLOTS, "width": WIDTH,
             "writes": WRITES, "reads": READS, "prefix": PREFIX,
-            "growth_quantum_rows": quantum, "steps_per_graph": G,
-            "launch": "one fused launch per step for all layers; hipGraph of G steps",
+            "growth_quantum_rows": quantum, "steps_per_launch": args.launch_steps,
+            "capacity_proof": f"on the device, every {args.proof_steps} steps per layer",
+            "launch": "persistent launches over all layers and banks",
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -304,13 +261,16 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": None,
-            "kernel": "sdm_step_kernel<int, 4, 2, false> (packed, 7 layers x 64 banks)",
+            "kernel": "sdm_trace_kernel<int, 2, false, true> (packed, 7 layers x 64 banks)",
             "launch_us": round(launch_us, 3),
+            "steps_per_launch": round(K / launches, 3),
+            "us_per_step": round(1000.0 * p_run["gpu_ms"] / K, 4),
             "algorithmic_bytes_per_launch": int(bytes_per_launch),
         },
         "dense_control": {
             "tokens_per_s": round(B * K / d_seconds, 1),
             "launch_us": round(dense_launch_us, 3),
+            "us_per_step": round(1000.0 * d_run["gpu_ms"] / K, 4),
             "packed_over_dense_latency": round(p_seconds / d_seconds, 4),
             "state_max_abs_diff": state_diff,
         },
@@ -322,7 +282,7 @@ def main() -> int:
             "growth_events": sum(st.growth_events for st in states),
             "growth_rows_copied": sum(st.growth_rows_copied for st in states),
             "timed_growth_events": timed_growths,
-            "graph_recaptures": p_runner.recaptures,
+            "timed_growth_rounds": p_run["growth_rounds"],
         },
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
     }

@@ -39,6 +39,9 @@ ERR_CORRUPT = 0x20
 ERR_LOOKBACK = 0x40
 ERR_TRACE_RANGE = 0x80
 
+TRACE_REFUSED = 0x1   # status bit: a device capacity proof failed
+TRACE_ENDED = 0x2     # status bit: no recorded step left
+
 SCRATCH_EPOCH = 0
 SCRATCH_ERRORS = 3
 SCRATCH_SLOTS = 8
@@ -145,8 +148,10 @@ class Trace(ctypes.Structure):
         ("scan", ctypes.c_void_p),
         ("scan_words", ctypes.c_int64),
         ("persistent", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("proof_steps", ctypes.c_int32),
         ("steps_recorded", ctypes.c_int64),
+        ("proof_rows", ctypes.c_int64),
+        ("status", ctypes.c_void_p),
     ]
 
 
@@ -226,7 +231,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = restype
                 fn.argtypes = argtypes
-            if handle.cowsdm_abi_version() != 2:
+            if handle.cowsdm_abi_version() != 3:
                 raise RuntimeError("libcowsdm.so ABI version mismatch")
             _lib = handle
     return _lib

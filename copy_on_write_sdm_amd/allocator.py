@@ -1112,18 +1112,21 @@ def mark_written(active: torch.Tensor, indices: torch.Tensor) -> None:
 
 class DecodeTrace:
     """Routes of many decode steps for several independent layers, resident
-    on the device, launched ``steps`` at a time.
+    on the device.
 
     Inputs are stacked [S, L, B, ...] (``values`` [S, L, B, D], gates
-    [S, L, B]).  Each launch runs all layers for one step, as
-    ``packed_sdm_cow_step_layers`` would.  ``launch(k, start=s)`` enqueues
-    steps s..s+k-1 from the host; ``launch(k)`` without ``start`` runs the
-    steps named by the device counter ``step_index``, which the kernels
-    advance themselves, so a captured hipGraph of ``launch(k)`` replays k
-    consecutive steps per replay without host work.  ``outputs`` is [S, L, B, D] (one reading per step) or
-    [L, B, D] (every step overwrites the same buffer).  ``memories`` given
-    instead of ``states`` runs the dense-table control.  No counterpart in
-    the reference.
+    [S, L, B]).  Every step does for each layer what ``packed_sdm_cow_step``
+    does.  ``launch(k, start=s)`` runs steps s..s+k-1 of every layer;
+    ``launch(k)`` without ``start`` runs k steps of each layer from its device
+    counter (``step_index[l]``), which the kernels advance, so a captured
+    hipGraph of ``launch(k)`` replays k consecutive steps per replay without
+    host work.  ``run(n)`` is the decode loop: n steps with the capacity of
+    packed layers proven on the device every few steps, growing a layer
+    exactly when ``prepare_step_capacity`` would.  ``outputs`` is
+    [S, L, B, D] (one reading per step) or [L, B, D] (every step overwrites
+    the same buffer).  ``memories`` given instead of ``states`` runs the
+    dense-table control.  Persistent launches run up to 64 steps per kernel.
+    No counterpart in the reference.
     """
 
     _INPUTS = ("write_indices", "write_weights", "values", "input_gate", "erase_gate",
@@ -1161,11 +1164,14 @@ class DecodeTrace:
         self.outputs = outputs
         self.steps = steps
         self.device = device
-        self.step_index = torch.zeros(1, dtype=torch.int64, device=device)
+        self.step_index = torch.zeros(layers, dtype=torch.int64, device=device)
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
+        self.status = torch.zeros(layers, dtype=torch.int32, device=device)
+        self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.ticket = self.ticket.data_ptr()
+        self.trace.status = self.status.data_ptr()
         for k, name in enumerate(self._INPUTS):
             tensor = self.inputs[name]
             self.trace.stride_bytes[k] = tensor.stride(0) * tensor.element_size()
@@ -1186,7 +1192,7 @@ class DecodeTrace:
         self.trace.steps_recorded = steps
 
     def set_step(self, step: int) -> None:
-        """Make the next launch run step ``step``."""
+        """Make the next device-counted launch run step ``step`` of every layer."""
 
         if not 0 <= step <= self.steps:
             raise ValueError("trace step outside the trace")
@@ -1209,32 +1215,105 @@ class DecodeTrace:
         return layers
 
     def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
-        """Enqueue ``steps`` consecutive step launches on the current stream:
-        steps start..start+steps-1, or, without ``start``, the steps the
-        device counter names."""
+        """Enqueue ``steps`` consecutive steps on the current stream: steps
+        start..start+steps-1, or, without ``start``, the next ``steps`` steps
+        of each layer's device counter."""
 
         layers = self.layer_array() if layers is None else layers
-        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
         stream = nat.stream_handle(self.device)
+        self.trace.persistent = int(self.persistent)
         if start is None:
             self.trace.step_index = self.step_index.data_ptr()
             self.trace.first_step = 0
-            self.trace.persistent = int(self.persistent)
             done = 0
             while done < steps:
                 n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
-                nat.check(fn(layers, len(self.tables), self.shape, self.trace, n, stream),
-                          "decode trace launch")
+                self._call(layers, n, stream)
                 done += n
             return
         if start < 0 or start + steps > self.steps:
             raise ValueError("trace launch runs past the recorded steps")
         self.trace.step_index = None
-        self.trace.persistent = int(self.persistent)
         done = 0
         while done < steps:
             n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
             self.trace.first_step = start + done
-            nat.check(fn(layers, len(self.tables), self.shape, self.trace, n, stream),
-                      "decode trace launch")
+            self._call(layers, n, stream)
             done += n
+
+    def _call(self, layers, steps, stream):
+        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
+        nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
+                  "decode trace launch")
+
+    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 64) -> dict:
+        """Decode the next ``steps`` steps of every layer from the device
+        counters (which must agree), ``launch_steps`` steps per launch.
+
+        Packed layers prove capacity on the device before every
+        ``proof_steps`` steps: the check prepare_step_capacity(banks * W *
+        proof_steps) makes in the reference's decode loop (inference.py:
+        551-552, allocator.py:745-773).  A layer whose free rows would not
+        cover the worst case stops before that step; once the launches have
+        drained, it is grown by prepare_step_capacity itself (the same read of
+        free_count, the same growth) and decoding resumes, so capacities and
+        growth counters match a host-proven loop exactly.  Returns the number
+        of launches and of growth rounds."""
+
+        if steps <= 0:
+            return {"launches": 0, "growth_rounds": 0}
+        positions = self.step_index.tolist()
+        if len(set(positions)) != 1:
+            raise ValueError("decode trace layers stand at different steps")
+        target = positions[0] + steps
+        if target > self.steps:
+            raise ValueError("trace run passes the recorded steps")
+        packed = not self.dense
+        need = 0
+        if packed:
+            if proof_steps <= 0 or steps % proof_steps:
+                raise ValueError("steps must be a multiple of proof_steps")
+            need = self.banks * self.writes * proof_steps
+            launch_steps = max(proof_steps, launch_steps // proof_steps * proof_steps)
+        launch_steps = max(1, min(int(launch_steps), self.max_steps_per_launch))
+        saved = self.trace.steps_recorded
+        self.trace.steps_recorded = target
+        self.trace.proof_rows = need
+        self.trace.proof_steps = proof_steps if packed else 0
+        self.trace.step_index = self.step_index.data_ptr()
+        self.trace.first_step = 0
+        self.trace.persistent = int(self.persistent)
+        self.status.zero_()
+        stream = nat.stream_handle(self.device)
+        launches = rounds = 0
+        remaining = steps
+        try:
+            while True:
+                layers = self.layer_array()
+                for _ in range(-(-remaining // launch_steps)):
+                    self._call(layers, launch_steps, stream)
+                    launches += 1
+                positions = self.step_index.tolist()
+                behind = [l for l, p in enumerate(positions) if p < target]
+                if not behind:
+                    break
+                status = self.status.tolist()
+                refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]
+                if refused != behind:
+                    raise RuntimeError(f"decode trace stopped short at steps {positions}")
+                for l in refused:
+                    state = self.tables[l]
+                    state.proven_maximum_additional_allocations = 0
+                    state.prepare_step_capacity(need)
+                self.status.zero_()
+                remaining = target - min(positions)
+                rounds += 1
+        finally:
+            self.trace.steps_recorded = saved
+            self.trace.proof_rows = 0
+            self.trace.proof_steps = 0
+        if packed:
+            # the device spent the allowance: the next host proof re-reads
+            for state in self.tables:
+                state.proven_maximum_additional_allocations = 0
+        return {"launches": launches, "growth_rounds": rounds}

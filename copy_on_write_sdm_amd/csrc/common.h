@@ -43,10 +43,13 @@ const char* last_error();
 
 struct StepParams {
   cowsdm_layer_t layer[kMaxLayers];
-  const int64_t* trace_step;     // device step counter, or null
-  int64_t* trace_ticket;         // [0] launch, [1 + layer] dense per-layer
+  int64_t* trace_step;           // per-layer device step counters, or null
+  int64_t* trace_ticket;         // [1 + layer]: waves of a layer done with the launch
   int64_t trace_first;           // step of this launch when trace_step is null
   int64_t trace_len;             // steps the trace inputs hold
+  int64_t trace_proof_rows;      // device capacity proof per run of proof steps, or 0
+  int32_t* trace_status;         // per-layer status bits, or null
+  int32_t trace_proof_steps;
   int64_t trace_stride[9];
   int64_t* scan;                 // persistent launches: per-layer scan words
   int64_t scan_words;            // words per layer in `scan`

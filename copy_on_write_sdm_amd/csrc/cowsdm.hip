@@ -731,6 +731,18 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   P.trace_ticket = trace ? trace->ticket : nullptr;
   P.trace_first = trace ? trace->first_step : 0;
   P.trace_len = trace ? trace->steps_recorded : 0;
+  P.trace_proof_rows = trace ? trace->proof_rows : 0;
+  P.trace_proof_steps = trace ? trace->proof_steps : 0;
+  P.trace_status = trace ? trace->status : nullptr;
+  if (P.trace_proof_rows > 0) {
+    if (dense) return fail(COWSDM_EARG, "trace: capacity proofs apply to packed state");
+    if (!trace->step_index) return fail(COWSDM_EARG, "trace: capacity proofs need device counters");
+    if (P.trace_proof_steps <= 0) return fail(COWSDM_EARG, "trace: proof_steps must be positive");
+    if (!persistent) {
+      return fail(COWSDM_ELIMIT, "trace: capacity proofs need a persistent launch "
+                                 "(W <= 4, R <= 16, D <= 256, banks <= 256)");
+    }
+  }
   P.scan = trace ? trace->scan : nullptr;
   P.scan_words = trace ? trace->scan_words : 0;
   P.steps = steps;

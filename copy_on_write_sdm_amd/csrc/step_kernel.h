@@ -22,13 +22,18 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   if (layer_id >= P.nlayers || bank >= P.banks) return;
   const cowsdm_layer_t& L = P.layer[layer_id];
-  const int64_t trace_s = P.trace_step ? *P.trace_step : P.trace_first;
+  const int64_t trace_s = P.trace_step ? P.trace_step[layer_id] : P.trace_first;
   if (P.trace_step && (trace_s < 0 || trace_s >= P.trace_len)) {
-    // a replay past the recorded steps: touch no input, leave the counter
-    if (!DENSE && lane == 0 && L.scratch) {
-      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                            static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
+    // no recorded step left for this layer: touch no input, leave the counter
+    if (lane == 0) {
+      if (P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{2}, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      } else if (!DENSE && L.scratch) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     return;
   }
@@ -426,9 +431,9 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
                             __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // device-counted trace launches: the bank that closes the last layer moves
-  // the trace to the next step (every bank read *trace_step before its
-  // ticket); tickets are per layer, then per launch, to spread the atomics
+  // device-counted trace launches: the bank that closes the layer moves the
+  // layer's counter to the next step (every bank of the layer read it before:
+  // packed banks before the bank-order scan, dense banks before their ticket)
   if (P.trace_step && lane == 0) {
     if constexpr (DENSE) {
       int64_t* layer_ticket = P.trace_ticket + 1 + layer_id;
@@ -438,13 +443,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
       if (closed_layer) atomic_store_u64(layer_ticket, 0);
     }
     if (closed_layer) {
-      const int64_t layers_done = __hip_atomic_fetch_add(
-          P.trace_ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (layers_done == P.nlayers - 1) {
-        atomic_store_u64(P.trace_ticket, 0);
-        atomic_store_u64(const_cast<int64_t*>(P.trace_step),
-                         static_cast<uint64_t>(trace_s + 1));
-      }
+      atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(trace_s + 1));
     }
   }
 }

@@ -135,15 +135,26 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   if (layer_id >= P.nlayers) return;  // whole workgroup
   const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock + wave;
   const cowsdm_layer_t& L = P.layer[layer_id];
-  // device-counted launches read their first step from the counter; every
-  // thread reads the same value (it changes only after all waves are done)
-  const int64_t first = P.trace_step ? *P.trace_step : P.trace_first;
-  if (P.trace_step && (first < 0 || first + P.steps > P.trace_len)) {
-    // a replay past the recorded steps: touch no input, leave the counter
-    if (!DENSE && threadIdx.x == 0) {
-      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                            static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
+  // Device-counted launches read the layer's first step from its counter
+  // (every thread reads the same value: it changes only after all waves of
+  // the layer are done) and run at most the steps recorded after it.
+  const int64_t first = P.trace_step ? P.trace_step[layer_id] : P.trace_first;
+  int64_t left = P.steps;
+  if (P.trace_step) {
+    const int64_t recorded = P.trace_len - first;
+    left = first < 0 ? 0 : (recorded < left ? recorded : left);
+  }
+  if (left <= 0) {
+    // no recorded step left for this layer: touch no input, leave the counter
+    if (threadIdx.x == 0 && blockIdx.x % P.blocks_per_layer == 0) {
+      if (P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{2}, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      } else if (!DENSE) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     return;  // whole workgroup
   }
@@ -153,7 +164,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const int W = FULL ? kTraceMaxWrites : P.writes;
   const int R = FULL ? kTraceMaxReads : P.reads;
   const int B = P.banks;
-  const int G = P.steps;
+  const int G = static_cast<int>(left);
   const int C = static_cast<int>(L.capacity_rows);  // rows are int32
   // lanes past the row width repeat the last columns: they load, compute and
   // store exactly what the last full lane does, so no access needs a lane mask
@@ -667,9 +678,19 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 
   // Iteration s.  `self` homes are written now and read in iteration s+1,
   // `other` homes were written in iteration s-1 and are read now.
+  // device capacity proof: before each run of proof_steps steps the layer
+  // needs proof_rows free rows; every wave of the layer sees the same pops
+  // (base), so all of them stop at the same step
+  const int64_t proof_rows = DENSE ? 0 : P.trace_proof_rows;
+  const int proof_steps = P.trace_proof_steps > 0 ? P.trace_proof_steps : 1;
+  int done_steps = G;
   auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
                        TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other) __attribute__((always_inline)) {
+                       int& mw_other, int& mr_other) __attribute__((always_inline)) -> bool {
+    if (proof_rows > 0 && s % proof_steps == 0 && old_free - base < proof_rows) {
+      done_steps = s;
+      return false;
+    }
     issue_scan(s);
     TraceRoute r1;
     if constexpr (DENSE) {
@@ -691,10 +712,11 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
     }
     q = r0;
     r0 = r1;
+    return true;
   };
   for (int s = 0; s < G; s += 2) {
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
-    if (s + 1 < G) iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA);
+    if (!iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB)) break;
+    if (s + 1 < G && !iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA)) break;
   }
 
   // ---- the last bank closes the launch
@@ -703,17 +725,22 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       *L.free_count = old_free - served;
       int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
       atomic_store_u64(&scan[COWSDM_SCRATCH_EPOCH], static_cast<uint64_t>(epoch + 1u));
+      if (done_steps < G && P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
-  // ---- device-counted launches: the last wave to finish (every wave read
-  // the counter before taking its ticket) moves the counter past this launch
+  // ---- device counters: the layer's last wave to finish (every wave of the
+  // layer read the counter before taking its ticket) moves the counter past
+  // the steps the layer ran
   if (P.trace_step && lane == 0) {
-    const int64_t waves = static_cast<int64_t>(P.nlayers) * B;
-    const int64_t done = __hip_atomic_fetch_add(P.trace_ticket, int64_t{1}, __ATOMIC_RELAXED,
+    int64_t* const ticket = P.trace_ticket + 1 + layer_id;
+    const int64_t done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-    if (done == waves - 1) {
-      atomic_store_u64(P.trace_ticket, 0);
-      atomic_store_u64(const_cast<int64_t*>(P.trace_step), static_cast<uint64_t>(first + G));
+    if (done == B - 1) {
+      atomic_store_u64(ticket, 0);
+      atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
     }
   }
 }

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 2
+#define COWSDM_ABI_VERSION 3
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -109,14 +109,27 @@ typedef struct cowsdm_layer {
  * per-step inputs (and the output) sit at base + step * stride_bytes[k],
  * k in the order write_indices, write_weights, step_values, input_gate,
  * erase_gate, forget_log_gate, read_indices, read_weights, output, and the
- * inputs hold steps_recorded steps.  With step_index null, the call runs
- * steps first_step .. first_step + steps - 1 (the host computes the
- * offsets).  With step_index set, the call runs `steps` steps from
- * *step_index and the kernels advance *step_index by `steps`, so the call can
- * be captured once in a hipGraph and replayed; ticket then points at
- * 1 + nlayers int64 words that are zero before the first launch and stay zero
- * between launches.  A device-counted launch whose steps would pass
- * steps_recorded does nothing (packed state: sets COWSDM_ERR_TRACE_RANGE). */
+ * inputs hold steps_recorded steps.
+ *
+ * Host offsets (step_index null): the call runs steps first_step ..
+ * first_step + steps - 1 of every layer.
+ *
+ * Device counters (step_index set, nlayers int64 counters): layer l runs up
+ * to `steps` steps from step_index[l], never past steps_recorded, and the
+ * kernels advance step_index[l] by the steps it ran, so the call can be
+ * captured once in a hipGraph and replayed.  ticket points at 1 + nlayers
+ * int64 words that are zero before the first launch and stay zero between
+ * launches.  A layer with no step left runs nothing and sets bit 1 of
+ * status[l] (status null, packed state: COWSDM_ERR_TRACE_RANGE instead).
+ *
+ * Device capacity proof (packed state, persistent launches on device
+ * counters): with proof_rows > 0, before each run of proof_steps steps a
+ * layer checks free_count >= proof_rows -- what prepare_step_capacity(
+ * proof_rows) proves before a group of proof_steps steps.  A layer that
+ * fails stops there, keeps its counter at the first step it did not run and
+ * sets bit 0 of status[l]; the caller grows that layer exactly as
+ * prepare_step_capacity would and calls again.  status words are sticky
+ * (the kernels only set bits); status is device memory. */
 typedef struct cowsdm_trace {
   int64_t* step_index;
   int64_t* ticket;
@@ -131,8 +144,10 @@ typedef struct cowsdm_trace {
   int64_t* scan;
   int64_t scan_words;
   int32_t persistent;
-  int32_t reserved;
+  int32_t proof_steps;
   int64_t steps_recorded;
+  int64_t proof_rows;
+  int32_t* status;
 } cowsdm_trace_t;
 
 /* ---------------------------------------------------------------- info */
