@@ -53,6 +53,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run one 256 MiB device copy first, so that counter passes "
+                        "(FETCH_SIZE, WRITE_SIZE) can be scaled by a kernel of known traffic")
     p.add_argument("--eager-steps", type=int, default=32,
                    help="steps of the per-layer Python drop-in path to time (0: skip)")
     return p.parse_args()
@@ -67,6 +70,20 @@ def algorithmic_bytes(banks: int, layers: int) -> int:
     vectors = 2 * WIDTH * 4
     metadata = (WRITES + READS) * (4 + 4 + 4) + 3 * 4
     return banks * layers * (rows + vectors + metadata)
+
+
+def profiled_traffic(batch: int, launch_steps: int) -> dict | None:
+    """HBM bytes per launch of the packed decode kernel from the committed
+    counter passes (FETCH_SIZE and WRITE_SIZE, scaled by a copy of known
+    size), when this run has the profiled configuration."""
+
+    path = ROOT / "profiles" / "traffic_packed_trace_config2_b64.json"
+    if not path.exists():
+        return None
+    traffic = json.loads(path.read_text())
+    if traffic["batch"] != batch or traffic["steps_per_launch"] != launch_steps:
+        return None
+    return traffic
 
 
 def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
@@ -123,6 +140,11 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     B, K, Wm = args.batch, args.steps, args.warmup
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     total_steps = Wm + K
     quantum = max(16, B * WRITES * 4)
 
@@ -175,20 +197,19 @@ def main() -> int:
         alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
                   if not trace.dense else 0)
         grow0 = sum(st.growth_events for st in trace.tables) if not trace.dense else 0
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        events = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        e0.record()
-        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
-        e1.record()
+        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps,
+                           timing=events)
         torch.cuda.synchronize()
         seconds = time.perf_counter() - t0
         new_rows = ((sum(int(st.allocated_rows_tensor()) for st in trace.tables) - alloc0)
                     if not trace.dense else 0)
         grows = (sum(st.growth_events for st in trace.tables) - grow0) if not trace.dense else 0
-        return dict(seconds=seconds, gpu_ms=e0.elapsed_time(e1), new_rows=new_rows,
-                    growths=grows, **report)
+        # kernel time: HIP events around every launch, on the launch stream
+        gpu_ms = sum(a.elapsed_time(b) for a, b in events)
+        return dict(seconds=seconds, gpu_ms=gpu_ms, new_rows=new_rows, growths=grows, **report)
 
     p_run = measure(packed)
     d_run = measure(dense)
@@ -229,6 +250,7 @@ def main() -> int:
     bytes_per_launch = (algorithmic_bytes(B, LAYERS) * K + 8 * new_rows) / launches
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     dense_launch_us = 1000.0 * d_run["gpu_ms"] / d_run["launches"]
+    traffic = profiled_traffic(B, args.launch_steps)
 
     result = {
         "metric": METRIC,
@@ -260,7 +282,8 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else traffic["bytes_per_launch"],
+            "traffic_source": None if traffic is None else traffic["source"],
             "kernel": "sdm_trace_kernel<int, 2, false, true> (packed, 7 layers x 64 banks)",
             "launch_us": round(launch_us, 3),
             "steps_per_launch": round(K / launches, 3),

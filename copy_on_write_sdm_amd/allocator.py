@@ -1190,6 +1190,8 @@ class DecodeTrace:
         self.trace.scan = None if self.scan is None else self.scan.data_ptr()
         self.trace.scan_words = words
         self.trace.steps_recorded = steps
+        self._layers = None
+        self._positions = [0] * layers   # host copy of step_index, None when unknown
 
     def set_step(self, step: int) -> None:
         """Make the next device-counted launch run step ``step`` of every layer."""
@@ -1197,11 +1199,20 @@ class DecodeTrace:
         if not 0 <= step <= self.steps:
             raise ValueError("trace step outside the trace")
         self.step_index.fill_(step)
+        self._positions = [step] * len(self.tables)
 
     def layer_array(self):
         """The per-layer C structs for the current state pointers (they
-        change when a slab grows or is trimmed)."""
+        change when a slab grows or is trimmed); rebuilt only when a pointer
+        moved."""
 
+        key = tuple((t.data_ptr(),) if self.dense else
+                    (t.values.data_ptr(), t.free_rows.data_ptr(), t.free_count.data_ptr(),
+                     t.overflow_flag.data_ptr(), t.logical_to_physical.data_ptr(),
+                     t.template_indices.data_ptr(), t.shared_initial_memory.data_ptr(),
+                     t.scratch.data_ptr(), t.capacity_rows) for t in self.tables)
+        if self._layers is not None and self._layers[0] == key:
+            return self._layers[1]
         count = len(self.tables)
         layers = (nat.Layer * count)()
         for l, table in enumerate(self.tables):
@@ -1212,6 +1223,7 @@ class DecodeTrace:
                 x["write_indices"], x["write_weights"], x["values"], x["input_gate"],
                 x["erase_gate"], x["forget_log_gate"], x["read_indices"], x["read_weights"],
                 out, None, None, None)
+        self._layers = (key, layers)
         return layers
 
     def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
@@ -1223,6 +1235,7 @@ class DecodeTrace:
         stream = nat.stream_handle(self.device)
         self.trace.persistent = int(self.persistent)
         if start is None:
+            self._positions = None
             self.trace.step_index = self.step_index.data_ptr()
             self.trace.first_step = 0
             done = 0
@@ -1246,7 +1259,8 @@ class DecodeTrace:
         nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
                   "decode trace launch")
 
-    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 64) -> dict:
+    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 64,
+            timing: list | None = None) -> dict:
         """Decode the next ``steps`` steps of every layer from the device
         counters (which must agree), ``launch_steps`` steps per launch.
 
@@ -1257,12 +1271,14 @@ class DecodeTrace:
         cover the worst case stops before that step; once the launches have
         drained, it is grown by prepare_step_capacity itself (the same read of
         free_count, the same growth) and decoding resumes, so capacities and
-        growth counters match a host-proven loop exactly.  Returns the number
-        of launches and of growth rounds."""
+        growth counters match a host-proven loop exactly.  With ``timing``
+        given, a pair of timing events brackets every launch on the stream
+        and is appended to it.  Returns the number of launches and of growth
+        rounds."""
 
         if steps <= 0:
             return {"launches": 0, "growth_rounds": 0}
-        positions = self.step_index.tolist()
+        positions = self._positions if self._positions is not None else self.step_index.tolist()
         if len(set(positions)) != 1:
             raise ValueError("decode trace layers stand at different steps")
         target = positions[0] + steps
@@ -1291,7 +1307,15 @@ class DecodeTrace:
             while True:
                 layers = self.layer_array()
                 for _ in range(-(-remaining // launch_steps)):
-                    self._call(layers, launch_steps, stream)
+                    if timing is not None:
+                        e0 = torch.cuda.Event(enable_timing=True)
+                        e1 = torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        self._call(layers, launch_steps, stream)
+                        e1.record()
+                        timing.append((e0, e1))
+                    else:
+                        self._call(layers, launch_steps, stream)
                     launches += 1
                 positions = self.step_index.tolist()
                 behind = [l for l, p in enumerate(positions) if p < target]
@@ -1312,6 +1336,8 @@ class DecodeTrace:
             self.trace.steps_recorded = saved
             self.trace.proof_rows = 0
             self.trace.proof_steps = 0
+            self._positions = None
+        self._positions = [target] * len(self.tables)
         if packed:
             # the device spent the allowance: the next host proof re-reads
             for state in self.tables:
