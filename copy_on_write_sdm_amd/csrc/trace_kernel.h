@@ -37,12 +37,15 @@
 
 namespace cowsdm_impl {
 
+typedef float vf4_t __attribute__((ext_vector_type(4)));
+
 template <int VEC>
-struct TraceRows {                  // operands of one step, loaded two steps ahead
+struct TraceRows {                  // operands of one step, loaded one step ahead
   float w[kTraceMaxWrites][VEC];    // rows of the write slots, before the decay
   float r[kTraceMaxReads][VEC];     // rows of the read slots, before this step
   float vin[VEC];                   // the step's value
   float ww, rw;                     // lane j: weight of write j / read j
+  vf4_t wwv, rwv[kTraceMaxReads / 4];  // full shape: every weight in every lane
 };
 
 struct TraceIdx {                   // lane j: write slot j / read slot j
@@ -218,6 +221,8 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const char* const v_l = first_step(L.step_values, 2) + (static_cast<int64_t>(bank) * D + col) * 4;
   const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
   const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
+  const char* const ww_b = first_step(L.write_weights, 1) + static_cast<int64_t>(bank) * W * 4;
+  const char* const rw_b = first_step(L.read_weights, 7) + static_cast<int64_t>(bank) * R * 4;
   const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
   const uint32_t st_wi = static_cast<uint32_t>(P.trace_stride[0]);
   const uint32_t st_ww = static_cast<uint32_t>(P.trace_stride[1]);
@@ -370,8 +375,18 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       }
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
-    buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-    buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    if constexpr (FULL) {
+      // the bank's 4 + 16 weights, the same address in every lane: one
+      // cache line each, no readlane per weight later
+      typedef __attribute__((address_space(1))) const vf4_t gvf4;
+      buf.wwv = *(gvf4*)(at(ww_b, st_ww, tc));
+      const char* const rb = at(rw_b, st_rw, tc);
+#pragma unroll
+      for (int k = 0; k < kTraceMaxReads / 4; ++k) buf.rwv[k] = *(gvf4*)(rb + 16 * k);
+    } else {
+      buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+      buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    }
   };
 
   auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
@@ -439,7 +454,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = rlf(buf.ww, j);
+          const float wj = FULL ? buf.wwv[j] : rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float d = buf.w[j][v] * alpha;
@@ -459,7 +474,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = rlf(buf.ww, j);
+          const float wj = FULL ? buf.wwv[j] : rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float u = wj * delta[v];
@@ -480,7 +495,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int i = 0; i < kTraceMaxReads; ++i) {
         if (i < R) {
-          const float wr = rlf(buf.rw, i);
+          const float wr = FULL ? buf.rwv[i / 4][i % 4] : rlf(buf.rw, i);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float term = wr * buf.r[i][v];
@@ -751,7 +766,15 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 // back to one launch per step.
 template <typename IDX, bool DENSE>
 bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) {
-  const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
+  // the full-shape variant loads each bank's weights as 16-byte vectors
+  bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads &&
+              P.trace_stride[1] % 16 == 0 && P.trace_stride[7] % 16 == 0;
+  for (int l = 0; l < P.nlayers && full; ++l) {
+    if ((reinterpret_cast<uintptr_t>(P.layer[l].write_weights) |
+         reinterpret_cast<uintptr_t>(P.layer[l].read_weights)) % 16 != 0) {
+      full = false;
+    }
+  }
   const void* kernels[2][3] = {
       {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false>),
