@@ -126,7 +126,8 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
 }
 
 // FULL: W == kTraceMaxWrites and R == kTraceMaxReads, every row guard folds away.
-template <typename IDX, int VEC, bool DENSE, bool FULL>
+// SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
+template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW>
 __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
   __shared__ float lds_rows[kBanksPerBlock][kTraceMaxWrites][kRow];
@@ -523,16 +524,16 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   int base = 0;     // first touches of the launch's earlier steps, all banks
   int served = 0;   // largest inclusive prefix that fits the free stack
   bool over = false;
-  uint64_t sw[kTraceScanWindows];
+  uint64_t sw[SCANW];
 #pragma unroll
-  for (int k = 0; k < kTraceScanWindows; ++k) sw[k] = 0;
+  for (int k = 0; k < SCANW; ++k) sw[k] = 0;
   const int64_t* const step_words = DENSE ? nullptr : slots - bank;  // word of (t, b): t*B + b
 
   auto issue_scan = [&](int t) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       const int64_t tc = t < G ? t : G - 1;
 #pragma unroll
-      for (int k = 0; k < kTraceScanWindows; ++k) {
+      for (int k = 0; k < SCANW; ++k) {
         if (k * kWave < B) {
           const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
           sw[k] = atomic_load_u64(&step_words[tc * B + bk]);
@@ -551,7 +552,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
     };
 #pragma unroll
-    for (int k = 0; k < kTraceScanWindows; ++k) {
+    for (int k = 0; k < SCANW; ++k) {
       if (k * kWave < B) {
         const bool in = k * kWave + lane < B;
         uint64_t w = sw[k];
@@ -585,7 +586,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
         int carry = base;
         bool done = false;
 #pragma unroll
-        for (int k = 0; k < kTraceScanWindows; ++k) {
+        for (int k = 0; k < SCANW; ++k) {
           if (k * kWave < B && !done) {
             const bool in = k * kWave + lane < B;
             const int v = (in && word_ready(sw[k])) ? static_cast<int>(sw[k] & 7u) : 0;
@@ -775,17 +776,22 @@ bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) 
       full = false;
     }
   }
-  const void* kernels[2][3] = {
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true>)}};
-  static int resident[2][3] = {{-1, -1, -1}, {-1, -1, -1}};
+  // one scan window when a layer has at most 64 banks (full shape only)
+  const int variant = !full ? 0 : (!DENSE && P.banks <= kWave ? 2 : 1);
+  const void* kernels[3][3] = {
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kTraceScanWindows>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kTraceScanWindows>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kTraceScanWindows>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kTraceScanWindows>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kTraceScanWindows>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kTraceScanWindows>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, DENSE ? kTraceScanWindows : 1>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, DENSE ? kTraceScanWindows : 1>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, DENSE ? kTraceScanWindows : 1>)}};
+  static int resident[3][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
-  const void* kernel = kernels[full][which];
-  if (resident[full][which] < 0) {
+  const void* kernel = kernels[variant][which];
+  if (resident[variant][which] < 0) {
     int device = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
@@ -793,12 +799,12 @@ bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) 
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStepThreads, 0) !=
             hipSuccess) {
       (void)hipGetLastError();
-      resident[full][which] = 0;
+      resident[variant][which] = 0;
     } else {
-      resident[full][which] = cus * per_cu;
+      resident[variant][which] = cus * per_cu;
     }
   }
-  if (blocks > resident[full][which]) return false;
+  if (blocks > resident[variant][which]) return false;
   void* args[] = {const_cast<StepParams*>(&P)};
   (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kStepThreads), args, 0, stream);
   return true;  // a failed launch is reported by the caller's launch_status()
