@@ -142,9 +142,13 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   // Device-counted launches read the layer's first step from its counter
   // (every thread reads the same value: it changes only after all waves of
   // the layer are done) and run at most the steps recorded after it.
-  const int64_t first = P.trace_step ? P.trace_step[layer_id] : P.trace_first;
+  int64_t first = P.trace_first;
   int64_t left = P.steps;
   if (P.trace_step) {
+    const uint64_t f = static_cast<uint64_t>(P.trace_step[layer_id]);
+    first = static_cast<int64_t>(
+        (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(f >> 32))) << 32) |
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(f)));
     const int64_t recorded = P.trace_len - first;
     left = first < 0 ? 0 : (recorded < left ? recorded : left);
   }
@@ -180,7 +184,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   int old_free = 0;
   int window = 0;
   if constexpr (!DENSE) {
-    old_free = *L.free_count;
+    old_free = __builtin_amdgcn_readfirstlane(*L.free_count);
     if (old_free < 0 || old_free > C) {
       base_err |= COWSDM_ERR_CORRUPT;
     } else {
@@ -703,7 +707,10 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
                        TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
                        int& mw_other, int& mr_other) __attribute__((always_inline)) -> bool {
-    if (proof_rows > 0 && s % proof_steps == 0 && old_free - base < proof_rows) {
+    // wave-uniform by construction; readfirstlane lets the compiler see it,
+    // so the loop exit stays a scalar branch
+    if (__builtin_amdgcn_readfirstlane(
+            (proof_rows > 0 && s % proof_steps == 0 && old_free - base < proof_rows) ? 1 : 0)) {
       done_steps = s;
       return false;
     }
