@@ -1287,7 +1287,9 @@ class DecodeTrace:
         packed = not self.dense
         need = 0
         if packed:
-            if proof_steps <= 0 or steps % proof_steps:
+            if proof_steps <= 0 or proof_steps % 2:
+                raise ValueError("proof_steps must be positive and even")
+            if steps % proof_steps:
                 raise ValueError("steps must be a multiple of proof_steps")
             need = self.banks * self.writes * proof_steps
             launch_steps = max(proof_steps, launch_steps // proof_steps * proof_steps)

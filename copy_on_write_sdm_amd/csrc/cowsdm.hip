@@ -737,7 +737,9 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   if (P.trace_proof_rows > 0) {
     if (dense) return fail(COWSDM_EARG, "trace: capacity proofs apply to packed state");
     if (!trace->step_index) return fail(COWSDM_EARG, "trace: capacity proofs need device counters");
-    if (P.trace_proof_steps <= 0) return fail(COWSDM_EARG, "trace: proof_steps must be positive");
+    if (P.trace_proof_steps <= 0 || P.trace_proof_steps % 2 != 0) {
+      return fail(COWSDM_EARG, "trace: proof_steps must be positive and even");
+    }
     if (!persistent) {
       return fail(COWSDM_ELIMIT, "trace: capacity proofs need a persistent launch "
                                  "(W <= 4, R <= 16, D <= 256, banks <= 256)");

@@ -45,7 +45,6 @@ struct TraceRows {                  // operands of one step, loaded one step ahe
   float r[kTraceMaxReads][VEC];     // rows of the read slots, before this step
   float vin[VEC];                   // the step's value
   float ww, rw;                     // lane j: weight of write j / read j
-  vf4_t wwv, rwv[kTraceMaxReads / 4];  // full shape: every weight in every lane
 };
 
 struct TraceIdx {                   // lane j: write slot j / read slot j
@@ -128,9 +127,13 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
 // FULL: W == kTraceMaxWrites and R == kTraceMaxReads, every row guard folds away.
 // SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
 template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW>
-__global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
+__global__ __launch_bounds__(kStepThreads)
+__attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
+void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
   __shared__ float lds_rows[kBanksPerBlock][kTraceMaxWrites][kRow];
+  // full shape: the step's weights, written per lane, read back broadcast
+  __shared__ vf4_t lds_weights[kBanksPerBlock][2][kWave / 4];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
 
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -226,8 +229,6 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const char* const v_l = first_step(L.step_values, 2) + (static_cast<int64_t>(bank) * D + col) * 4;
   const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
   const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
-  const char* const ww_b = first_step(L.write_weights, 1) + static_cast<int64_t>(bank) * W * 4;
-  const char* const rw_b = first_step(L.read_weights, 7) + static_cast<int64_t>(bank) * R * 4;
   const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
   const uint32_t st_wi = static_cast<uint32_t>(P.trace_stride[0]);
   const uint32_t st_ww = static_cast<uint32_t>(P.trace_stride[1]);
@@ -380,18 +381,8 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
       }
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
-    if constexpr (FULL) {
-      // the bank's 4 + 16 weights, the same address in every lane: one
-      // cache line each, no readlane per weight later
-      typedef __attribute__((address_space(1))) const vf4_t gvf4;
-      buf.wwv = *(gvf4*)(at(ww_b, st_ww, tc));
-      const char* const rb = at(rw_b, st_rw, tc);
-#pragma unroll
-      for (int k = 0; k < kTraceMaxReads / 4; ++k) buf.rwv[k] = *(gvf4*)(rb + 16 * k);
-    } else {
-      buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-      buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
-    }
+    buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+    buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
   };
 
   auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
@@ -450,6 +441,17 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
           }
         }
       }
+      vf4_t wwv = 0.0f, rwv[kTraceMaxReads / 4];
+      if constexpr (FULL) {
+        // lane j holds weight j; one LDS round trip gives every lane all of
+        // them as vectors, instead of a readlane per weight
+        float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
+        wl[lane] = buf.ww;
+        wl[kWave + lane] = buf.rw;
+        wwv = lds_weights[wave][0][0];
+#pragma unroll
+        for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
+      }
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t));
       const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t));
       const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t));
@@ -459,7 +461,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = FULL ? buf.wwv[j] : rlf(buf.ww, j);
+          const float wj = FULL ? wwv[j] : rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float d = buf.w[j][v] * alpha;
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
-          const float wj = FULL ? buf.wwv[j] : rlf(buf.ww, j);
+          const float wj = FULL ? wwv[j] : rlf(buf.ww, j);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float u = wj * delta[v];
@@ -500,7 +502,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
 #pragma unroll
       for (int i = 0; i < kTraceMaxReads; ++i) {
         if (i < R) {
-          const float wr = FULL ? buf.rwv[i / 4][i % 4] : rlf(buf.rw, i);
+          const float wr = FULL ? rwv[i / 4][i % 4] : rlf(buf.rw, i);
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float term = wr * buf.r[i][v];
@@ -704,16 +706,20 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
   const int64_t proof_rows = DENSE ? 0 : P.trace_proof_rows;
   const int proof_steps = P.trace_proof_steps > 0 ? P.trace_proof_steps : 1;
   int done_steps = G;
-  auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
-                       TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other) __attribute__((always_inline)) -> bool {
-    // wave-uniform by construction; readfirstlane lets the compiler see it,
-    // so the loop exit stays a scalar branch
+  // does the capacity proof stop the layer before step s?  Wave-uniform by
+  // construction; readfirstlane lets the compiler see it, so the loop exit
+  // stays a scalar branch.
+  auto proof_stops = [&](int s) __attribute__((always_inline)) -> bool {
     if (__builtin_amdgcn_readfirstlane(
             (proof_rows > 0 && s % proof_steps == 0 && old_free - base < proof_rows) ? 1 : 0)) {
       done_steps = s;
-      return false;
+      return true;
     }
+    return false;
+  };
+  auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
+                       TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
+                       int& mw_other, int& mr_other) __attribute__((always_inline)) {
     issue_scan(s);
     TraceRoute r1;
     if constexpr (DENSE) {
@@ -735,11 +741,28 @@ __global__ __launch_bounds__(kStepThreads) void sdm_trace_kernel(StepParams P) {
     }
     q = r0;
     r0 = r1;
-    return true;
   };
-  for (int s = 0; s < G; s += 2) {
-    if (!iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB)) break;
-    if (s + 1 < G && !iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA)) break;
+  // Drain the prologue's loads: the loop head then has one state of loads in
+  // flight (the back edge's), and the waits the compiler places there stay
+  // as loose as the steady state allows.
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // Pairs of steps, then an odd last step outside the loop.  Capacity proofs
+  // come in runs of an even number of steps (the host checks), so the only
+  // exit from the loop body is at its head: the compiler then sees one state
+  // of the loads in flight there and waits on none of them early.
+  int s = 0;
+  bool stopped = false;
+  for (; s + 1 < G; s += 2) {
+    if (proof_stops(s)) {
+      stopped = true;
+      break;
+    }
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
+    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA);
+  }
+  if (!stopped && s < G && !proof_stops(s)) {
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
   }
 
   // ---- the last bank closes the launch

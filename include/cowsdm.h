@@ -123,7 +123,8 @@ typedef struct cowsdm_layer {
  * status[l] (status null, packed state: COWSDM_ERR_TRACE_RANGE instead).
  *
  * Device capacity proof (packed state, persistent launches on device
- * counters): with proof_rows > 0, before each run of proof_steps steps a
+ * counters): with proof_rows > 0 and proof_steps even, before each run of
+ * proof_steps steps a
  * layer checks free_count >= proof_rows -- what prepare_step_capacity(
  * proof_rows) proves before a group of proof_steps steps.  A layer that
  * fails stops there, keeps its counter at the first step it did not run and
