@@ -1116,7 +1116,11 @@ class DecodeTrace:
 
     Inputs are stacked [S, L, B, ...] (``values`` [S, L, B, D], gates
     [S, L, B]).  Every step does for each layer what ``packed_sdm_cow_step``
-    does.  ``launch(k, start=s)`` runs steps s..s+k-1 of every layer;
+    does, except that persistent launches give first touches their physical
+    rows in the order of an atomic claim per (step, bank), as the reference's
+    proven kernel does (allocator.py:120-135): the same logical rows become
+    private, with the same values, the same set of physical rows and an
+    identical free stack.  ``launch(k, start=s)`` runs steps s..s+k-1 of every layer;
     ``launch(k)`` without ``start`` runs k steps of each layer from its device
     counter (``step_index[l]``), which the kernels advance, so a captured
     hipGraph of ``launch(k)`` replays k consecutive steps per replay without

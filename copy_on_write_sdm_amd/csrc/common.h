@@ -28,6 +28,8 @@ constexpr int kTraceMaxReads = 16;
 constexpr int kTraceMaxSteps = 64;          // each step's gates live in one lane
 constexpr int kTraceScanWindows = 4;        // up to 256 banks per layer
 constexpr int kTraceFreeWindow = 1024;      // top of the free stack staged in LDS
+constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are staged in LDS
+constexpr int64_t kClaimFailBase = int64_t{1} << 40;  // failed claim p recorded as base - p
 
 constexpr uint32_t kStatusEmpty = 0;
 constexpr uint32_t kStatusAggregate = 1;

@@ -723,7 +723,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
       trace && trace->persistent && steps > 0 && trace_vec &&
       shape->writes <= kTraceMaxWrites && shape->reads <= kTraceMaxReads &&
       nlayers <= kMaxLayers &&
-      (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan &&
+      (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan && trace->ticket &&
                  trace->scan_words >= COWSDM_SCRATCH_SLOTS + chunk * shape->banks));
   (void)blocks_per_layer_p;
   StepParams P;

@@ -1,36 +1,46 @@
 // Persistent multi-step form of the copy-on-write SDM step: one launch runs
 // G consecutive decode steps of device-resident routes for every (layer,
-// bank), with results identical to G single-step launches.
+// bank), with the results of G single-step launches (physical rows of first
+// touches may be assigned in another order, as in the reference's proven
+// kernel, whose banks pop with an atomic add).
 //
 // Each wave owns one (layer, bank) for all G steps and software-pipelines
 // them so that every memory access has about one iteration to land before
 // its value is used.  Iteration s
-//   1. loads every bank's first-touch count of step s (published one
-//      iteration earlier), the slots of step s+3 (s+2 for dense tables) and
-//      the map entries of step s+2;
+//   1. loads the slots of step s+2 (s+3 when the slot map stays in global
+//      memory, whose entries for step s+2 are loaded too);
 //   2. classifies step s+1 (first touches, slots written by steps s and s-1,
-//      read-after-write), publishes its first-touch count and loads its rows;
+//      read-after-write), claims rows for its first touches and loads its
+//      rows;
 //   3. computes step s (gated-delta update, sparse read) from rows loaded one
 //      iteration earlier; stores its reading and the rows already private;
-//   4. pops the free rows of step s's first touches and stores them and their
-//      map entries.
+//   4. takes the rows claimed for step s's first touches and stores them and
+//      their map entries.
 // Step t's map entries are read before steps t-2 and t-1 have stored their
 // first touches: slots written at t-1 take their rows from that step's
 // result, kept in LDS, and slots written at t-2 take the physical rows popped
 // for them.  Every other row step t needs was stored earlier by the same
-// wave, in program order.  Values in flight live in even/odd homes (the loop
-// is unrolled by two) and are only read one iteration after their load was
-// issued, so no register copy waits on memory; per-row values picked by
-// run-time lanes are read from LDS, never selected out of registers.
+// wave, in program order.  When a bank's map fits (N <= kTraceMapSlots), the
+// wave keeps it in LDS for the launch (it is the only writer of its bank's
+// entries) and reads step t+1's entries there in iteration t, after step
+// t-1's pops: only the slots of step t still need their rows forwarded, and
+// the global map is written alongside.  Values in flight live in even/odd
+// homes (the loop is unrolled by two) and are only read one iteration after
+// their load was issued, so no register copy waits on memory; per-row values
+// picked by run-time lanes are read from LDS, never selected out of registers.
 //
-// First touches of (step t, bank b) pop free_rows[F - 1 - Q(t, b) - rank],
-// where F is free_count at launch and Q the exclusive prefix of first-touch
-// counts over (step, bank) pairs in step-major, bank-minor order: exactly the
-// rows G single-step launches would pop.  Each wave publishes one count per
-// step and reads the counts of every bank of the layer, so it knows both its
-// own prefix and the running total without waiting on another wave's prefix.
-// The wave of bank B-1 closes the launch: it writes free_count and advances
-// the scan epoch.
+// Rows: free_count stays F (its value at launch) until the launch ends.  A
+// (step, bank) with c first touches adds c to the layer's claim counter and
+// gets p, the rows claimed before it; its first touches take
+// free_rows[F - 1 - p - rank], and the step fits if p + c <= F.  Claims only
+// grow, so once one fails every later one fails too, and the claims that fit
+// are exactly the top of the free stack.  The layer's last wave to finish
+// writes free_count = F - (claims that fit) and clears the counter.  Waves
+// do not otherwise wait on one another, except for the capacity proof: with
+// proofs on, each bank publishes its first touches so far at the end of each
+// run of proof steps, and every wave sums them before the next run starts, so
+// all banks of the layer stop at the same step.  The claims of a run's first
+// step wait for that proof.
 #pragma once
 
 #include "common.h"
@@ -60,7 +70,8 @@ struct TraceRoute {                 // a classified step
   int rank;       // write lane: rank among the bank's first touches
   uint32_t u;     // wave-uniform: bits 0-3 first-touch write lanes, 4-7 their count,
                   // 8 the step runs (routes valid, every earlier step ran),
-                  // 9 a row comes from step t-1, 10 a read sees a write of step t
+                  // 9 a row comes from step t-1, 10 a read sees a write of step t,
+                  // 11 a write rewrites a slot of step t-1
 };
 
 __device__ __forceinline__ uint32_t route_fmask(uint32_t u) { return u & 15u; }
@@ -68,6 +79,7 @@ __device__ __forceinline__ int route_count(uint32_t u) { return static_cast<int>
 __device__ __forceinline__ bool route_ok(uint32_t u) { return (u >> 8) & 1u; }
 __device__ __forceinline__ bool route_fix(uint32_t u) { return (u >> 9) & 1u; }
 __device__ __forceinline__ bool route_raw(uint32_t u) { return (u >> 10) & 1u; }
+__device__ __forceinline__ bool route_wfwd(uint32_t u) { return (u >> 11) & 1u; }
 
 typedef __attribute__((address_space(1))) float gfloat;
 typedef float vf2 __attribute__((ext_vector_type(2)));
@@ -119,6 +131,22 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
 }
 
+// A wave-uniform value the loop keeps in a register: values read from the
+// kernel arguments would otherwise be reloaded, and waited on, inside it.
+template <typename T>
+__device__ __forceinline__ T pin(T x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+// The lane's column offset as a fresh 32-bit value: the compiler then pairs
+// it with a wave-uniform row base as global_load/store's scalar base plus
+// vector offset, instead of materialising a 64-bit address per row.
+__device__ __forceinline__ uint32_t fresh(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Weighted population count of per-lane values 0..7 held as three bit masks.
 __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t m) {
   return __popcll(b0 & m) + 2 * __popcll(b1 & m) + 4 * __popcll(b2 & m);
@@ -126,7 +154,8 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
 
 // FULL: W == kTraceMaxWrites and R == kTraceMaxReads, every row guard folds away.
 // SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
-template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW>
+// MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per wave).
+template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW, bool MAPLDS>
 __global__ __launch_bounds__(kStepThreads)
 __attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
 void sdm_trace_kernel(StepParams P) {
@@ -135,8 +164,9 @@ void sdm_trace_kernel(StepParams P) {
   // full shape: the step's weights, written per lane, read back broadcast
   __shared__ vf4_t lds_weights[kBanksPerBlock][2][kWave / 4];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
+  extern __shared__ int lds_map_all[];
 
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int layer_id = blockIdx.x / P.blocks_per_layer;
   if (layer_id >= P.nlayers) return;  // whole workgroup
@@ -176,11 +206,12 @@ void sdm_trace_kernel(StepParams P) {
   const int R = FULL ? kTraceMaxReads : P.reads;
   const int B = P.banks;
   const int G = static_cast<int>(left);
-  const int C = static_cast<int>(L.capacity_rows);  // rows are int32
+  const int C = pin(static_cast<int>(L.capacity_rows));  // rows are int32
   // lanes past the row width repeat the last columns: they load, compute and
   // store exactly what the last full lane does, so no access needs a lane mask
   const int col = lane * VEC < D ? lane * VEC : D - VEC;
   const uint32_t coff = static_cast<uint32_t>(col) * 4u;
+  const uint32_t row_bytes = static_cast<uint32_t>(D) * 4u;
 
   // ---- launch constants
   int base_err = 0;
@@ -201,22 +232,24 @@ void sdm_trace_kernel(StepParams P) {
   if (bank >= B) return;
   int64_t tmpl = 0;
   uint32_t epoch = 0;
-  int64_t* slots = nullptr;
   if constexpr (!DENSE) {
     tmpl = L.template_indices[bank];
     if (tmpl < 0 || tmpl >= P.templates) {
       base_err |= COWSDM_ERR_TEMPLATE;
       tmpl = 0;
     }
-    int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
-    epoch = static_cast<uint32_t>(scan[COWSDM_SCRATCH_EPOCH]);
-    slots = scan + COWSDM_SCRATCH_SLOTS + bank;  // + t * B: this bank's word of step t
+    epoch = static_cast<uint32_t>(
+        P.scan[static_cast<int64_t>(layer_id) * P.scan_words + COWSDM_SCRATCH_EPOCH]);
   }
   const float* const m0_bank =
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   float* const table_bank = DENSE ? L.values + static_cast<int64_t>(bank) * N * D : nullptr;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
   float* const lds_wave = &lds_rows[wave][0][0];
+  int* const lds_map = MAPLDS ? lds_map_all + wave * N : nullptr;
+  if constexpr (MAPLDS) {
+    for (int k = lane; k < N; k += kWave) lds_map[k] = map_bank[k];
+  }
 
   // ---- this lane's inputs at the launch's first step; step t adds t * stride
   const int wl = lane < W ? lane : 0;
@@ -230,12 +263,13 @@ void sdm_trace_kernel(StepParams P) {
   const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
   const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
   const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
-  const uint32_t st_wi = static_cast<uint32_t>(P.trace_stride[0]);
-  const uint32_t st_ww = static_cast<uint32_t>(P.trace_stride[1]);
-  const uint32_t st_v = static_cast<uint32_t>(P.trace_stride[2]);
-  const uint32_t st_ri = static_cast<uint32_t>(P.trace_stride[6]);
-  const uint32_t st_rw = static_cast<uint32_t>(P.trace_stride[7]);
-  const uint32_t st_out = static_cast<uint32_t>(P.trace_stride[8]);
+  const uint32_t st_wi = pin(static_cast<uint32_t>(P.trace_stride[0]));
+  const uint32_t st_ww = pin(static_cast<uint32_t>(P.trace_stride[1]));
+  const uint32_t st_v = pin(static_cast<uint32_t>(P.trace_stride[2]));
+  const uint32_t st_ri = pin(static_cast<uint32_t>(P.trace_stride[6]));
+  const uint32_t st_rw = pin(static_cast<uint32_t>(P.trace_stride[7]));
+  const uint32_t st_out = pin(static_cast<uint32_t>(P.trace_stride[8]));
+  float* const slab = DENSE ? nullptr : pin(L.values);
   auto at = [](const char* p, uint32_t stride, int t) __attribute__((always_inline)) -> const char* {
     return p + static_cast<uint64_t>(static_cast<uint32_t>(t)) * stride;
   };
@@ -283,6 +317,11 @@ void sdm_trace_kernel(StepParams P) {
                       const TraceRoute& r1, const TraceRoute& r2, bool ok_prev)
       __attribute__((always_inline)) -> int {
     int lerr = m.err | base_err;
+    if constexpr (MAPLDS) {
+      // every step up to t-2 has stored its pops here
+      wraw = lane < W ? lds_map[m.widx] : -1;
+      rraw = lane < R ? lds_map[m.ridx] : -1;
+    }
     if constexpr (!DENSE) {
       if (lane < W && wraw >= C) { lerr |= COWSDM_ERR_CORRUPT; wraw = -1; }
       if (lane < R && rraw >= C) { lerr |= COWSDM_ERR_CORRUPT; rraw = -1; }
@@ -306,7 +345,7 @@ void sdm_trace_kernel(StepParams P) {
         }
       }
     }
-    if (!DENSE && t >= 2) {
+    if (!DENSE && !MAPLDS && t >= 2) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
@@ -329,10 +368,12 @@ void sdm_trace_kernel(StepParams P) {
     const bool ok = ok_prev && !any_err;
     const bool first = !DENSE && ok && lane < W && wsrc < 0 && wraw < 0;
     const uint64_t fm = __ballot(first);
-    const bool fix = __ballot((lane < W && wsrc >= 0) || (lane < R && rsrc >= 0)) != 0;
+    const bool wfwd = __ballot(lane < W && wsrc >= 0) != 0;
+    const bool fix = wfwd || __ballot(lane < R && rsrc >= 0) != 0;
     const bool raw = __ballot(lane < R && rraw_lane >= 0) != 0;
     rt.u = static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
-           (ok ? 1u << 8 : 0u) | (fix ? 1u << 9 : 0u) | (raw ? 1u << 10 : 0u);
+           (ok ? 1u << 8 : 0u) | (fix ? 1u << 9 : 0u) | (raw ? 1u << 10 : 0u) |
+           (wfwd ? 1u << 11 : 0u);
     rt.rank = lanes_below(fm);
     rt.widx = m.widx;
     rt.ridx = m.ridx;
@@ -343,41 +384,36 @@ void sdm_trace_kernel(StepParams P) {
     return rraw;
   };
 
-  auto publish = [&](int t, const TraceRoute& rt) __attribute__((always_inline)) {
-    if constexpr (!DENSE) {
-      if (lane == 0 && t < G) {
-        atomic_store_u64(&slots[static_cast<int64_t>(t) * B],
-                         slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(route_count(rt.u))));
-      }
-    }
-  };
-
   auto issue_rows = [&](int t, const TraceRoute& rt, int rrow, TraceRows<VEC>& buf)
       __attribute__((always_inline)) {
     const int tc = t < G ? t : G - 1;
+    // row r of a base: base + r * D floats, r non-negative
+    auto row_at = [&](const float* base, int r) __attribute__((always_inline)) -> const float* {
+      return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) +
+                                            static_cast<uint64_t>(static_cast<uint32_t>(r)) * row_bytes);
+    };
     const float* wp;
     const float* rp;
     if constexpr (DENSE) {
-      wp = table_bank + static_cast<int64_t>(rt.widx) * D;
-      rp = table_bank + static_cast<int64_t>(rt.ridx) * D;
+      wp = row_at(table_bank, rt.widx);
+      rp = row_at(table_bank, rt.ridx);
     } else {
-      wp = rt.wrow < 0 ? m0_bank + static_cast<int64_t>(rt.widx) * D
-                       : L.values + static_cast<int64_t>(rt.wrow) * D;
-      rp = rrow < 0 ? m0_bank + static_cast<int64_t>(rt.ridx) * D
-                    : L.values + static_cast<int64_t>(rrow) * D;
+      wp = rt.wrow < 0 ? row_at(m0_bank, rt.widx) : row_at(slab, rt.wrow);
+      rp = rrow < 0 ? row_at(m0_bank, rt.ridx) : row_at(slab, rrow);
     }
+    const uint32_t co = fresh(coff);
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) {
       if (j < W) {
         const float* p = rl_ptr(wp, j);
-        gload_row<VEC>(p, coff, buf.w[j]);
+        gload_row<VEC>(p, co, buf.w[j]);
       }
     }
 #pragma unroll
     for (int i = 0; i < kTraceMaxReads; ++i) {
       if (i < R) {
         const float* p = rl_ptr(rp, i);
-        gload_row<VEC>(p, coff, buf.r[i]);
+        gload_row<VEC>(p, co, buf.r[i]);
       }
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
@@ -513,152 +549,209 @@ void sdm_trace_kernel(StepParams P) {
     }
     gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), 0u, acc);
     if (run) {
-      float* const dst = DENSE ? table_bank + static_cast<int64_t>(rt.widx) * D
-                               : L.values + static_cast<int64_t>(rt.wrow < 0 ? 0 : rt.wrow) * D;
+      const uint32_t r = static_cast<uint32_t>(DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow));
+      float* const dst = reinterpret_cast<float*>(
+          reinterpret_cast<char*>(DENSE ? table_bank : slab) + static_cast<uint64_t>(r) * row_bytes);
       const uint32_t fmask = route_fmask(rt.u);
+      const uint32_t co = fresh(coff);
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W && !((fmask >> j) & 1u)) {
           float* p = const_cast<float*>(rl_ptr(dst, j));
-          gstore_row<VEC>(p, coff, cur[j]);
+          gstore_row<VEC>(p, co, cur[j]);
         }
       }
     }
   };
 
-  // ---- pops (packed)
-  int base = 0;     // first touches of the launch's earlier steps, all banks
-  int served = 0;   // largest inclusive prefix that fits the free stack
-  bool over = false;
-  uint64_t sw[SCANW];
-#pragma unroll
-  for (int k = 0; k < SCANW; ++k) sw[k] = 0;
-  const int64_t* const step_words = DENSE ? nullptr : slots - bank;  // word of (t, b): t*B + b
+  // ---- claims (packed)
+  int64_t* const scan = DENSE ? nullptr : P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
+  int64_t* const claims = DENSE ? nullptr : scan + COWSDM_SCRATCH_CLAIMS;
 
-  auto issue_scan = [&](int t) __attribute__((always_inline)) {
+  // Step t's first touches claim their rows: one atomic add per (step, bank)
+  // with first touches, its result read when the step resolves.
+  auto claim = [&](const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      const int64_t tc = t < G ? t : G - 1;
-#pragma unroll
-      for (int k = 0; k < SCANW; ++k) {
-        if (k * kWave < B) {
-          const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
-          sw[k] = atomic_load_u64(&step_words[tc * B + bk]);
+      if (route_count(rt.u) > 0 && route_ok(rt.u)) {
+        if (lane == 0) {
+          home = static_cast<int>(__hip_atomic_fetch_add(
+              claims, static_cast<int64_t>(route_count(rt.u)), __ATOMIC_RELAXED,
+              __HIP_MEMORY_SCOPE_AGENT));
         }
       }
     }
   };
 
-  // Step t's first touches, after its counts (sw) have been loaded.  r1: step
-  // t+1, whose rewrites of step t's slots take its physical rows.
-  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1)
+  // Step t's first touches, from the rows claimed for them (home: lane 0
+  // holds p, the rows the layer claimed before).  r1: step t+1, whose
+  // rewrites of step t's slots take its physical rows.
+  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, int home)
       __attribute__((always_inline)) {
-    int partial = 0, total = 0;
-    bool poisoned = false;
-    auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-      return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
-    };
-#pragma unroll
-    for (int k = 0; k < SCANW; ++k) {
-      if (k * kWave < B) {
-        const bool in = k * kWave + lane < B;
-        uint64_t w = sw[k];
-        bool ready = !in || word_ready(w);
-        if (__ballot(!ready) != 0) {
-          // a bank has not published step t yet: bounded wait
-          int spins = 0;
-          while (!ready && spins < kSpinLimit) {
-            __builtin_amdgcn_s_sleep(1);
-            w = atomic_load_u64(&step_words[static_cast<int64_t>(t) * B + k * kWave + lane]);
-            ready = word_ready(w);
-            ++spins;
-          }
-          if (__ballot(!ready) != 0) poisoned = true;
-          sw[k] = ready ? w : 0;
+    const int count = route_count(rt.u);
+    if (count > 0 && route_ok(rt.u) && alive) {
+      const uint32_t fmask = route_fmask(rt.u);
+      const int p = __builtin_amdgcn_readfirstlane(home);
+      bool fits = p + count <= old_free;
+      if (fits) {
+        const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
+        const int k = p + rt.rank;
+        int new_row = first && k < window ? lds_free[k] : -1;
+        if (__ballot(first && k >= window) != 0) {
+          if (first && k >= window) new_row = L.free_rows[old_free - 1 - k];
+          // wait for it here, on this rare path, so that no later use of the
+          // popped rows has to drain every load in flight
+          asm volatile("" ::"v"(new_row));
         }
-        const int v = (in && ready) ? static_cast<int>(w & 7u) : 0;
-        const uint64_t b0 = __ballot(v & 1), b1 = __ballot(v & 2), b2 = __ballot(v & 4);
-        const int below = bank - k * kWave;
-        const uint64_t m = below <= 0 ? 0ull : (below >= kWave ? ~0ull : ((1ull << below) - 1));
-        partial += static_cast<int>(sum3(b0, b1, b2, m));
-        total += static_cast<int>(sum3(b0, b1, b2, ~0ull));
+        if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
+          fits = false;
+          if (lane == 0) {
+            __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                  static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+          }
+        } else {
+          if (first) {
+            rt.wrow = new_row;
+            map_bank[rt.widx] = new_row;
+            if constexpr (MAPLDS) lds_map[rt.widx] = new_row;
+          }
+          float* const dst = reinterpret_cast<float*>(
+              reinterpret_cast<char*>(slab) +
+              static_cast<uint64_t>(static_cast<uint32_t>(rt.wrow < 0 ? 0 : rt.wrow)) * row_bytes);
+          const uint32_t co = fresh(coff);
+#pragma unroll
+          for (int j = 0; j < kTraceMaxWrites; ++j) {
+            if (j < W && ((fmask >> j) & 1u)) {
+              float* p = const_cast<float*>(rl_ptr(dst, j));
+              gstore_row<VEC>(p, co, cur[j]);
+            }
+          }
+        }
+      }
+      if (!fits) {
+        // rare: the free stack is exhausted; every later claim fails too,
+        // and the launch's end counts only the claims before this one
+        if (lane == 0) {
+          *L.overflow_flag = 1;
+          __hip_atomic_fetch_max(scan + COWSDM_SCRATCH_CLAIM_FAIL,
+                                 kClaimFailBase - static_cast<int64_t>(p), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      alive = fits;
+    }
+    // step t+1 rewrites some of step t's slots in the rows just found
+    if (route_wfwd(r1.u)) {
+      const int s1 = r1.wsrc;
+      const int v1 = __shfl(rt.wrow, s1 >= 0 ? s1 : 0, kWave);
+      if (s1 >= 0) r1.wrow = v1;
+    }
+  };
+
+  // ---- capacity proof (packed): every proof_steps steps, the first touches
+  // each bank made so far, published per run and summed by every wave
+  const int64_t proof_rows = DENSE ? 0 : P.trace_proof_rows;
+  const bool proofs = proof_rows > 0;
+  const int proof_steps = P.trace_proof_steps > 0 ? P.trace_proof_steps : 1;
+  int done_steps = G;
+  int cum = 0;                        // this bank's first touches so far
+  int run_left = proof_steps - 1;     // classified steps before the next run ends
+  int runs_published = 0;
+  int next_proof = 0;                 // step of the next proof
+  uint64_t pw[SCANW];                 // the published counts of the next proof
+#pragma unroll
+  for (int k = 0; k < SCANW; ++k) pw[k] = 0;
+  const int64_t* run_l[SCANW];        // this lane's bank in each window
+#pragma unroll
+  for (int k = 0; k < SCANW; ++k) {
+    const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
+    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk;
+  }
+
+  // after classifying step t: claim (unless t starts a run, whose claims wait
+  // for its proof), and publish the bank's count when t ends a run
+  auto after_classify = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      if (t < G && (!proofs || run_left != proof_steps - 1)) claim(rt, home);
+      if (proofs) {
+        if (route_ok(rt.u)) cum += route_count(rt.u);
+        if (run_left == 0) {
+          ++runs_published;
+          if (t < G && lane == 0) {
+            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + runs_published * B + bank,
+                             slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(cum)));
+          }
+          run_left = proof_steps;
+        }
+        --run_left;
       }
     }
-    if (!over) {
-      if (base + total <= old_free) {
-        served = base + total;
-      } else {
-        // largest inclusive prefix of this step's banks that still fits
-        over = true;
-        int carry = base;
-        bool done = false;
+  };
+
+  // iteration s-1 loads the counts that the proof before step s sums
+  auto issue_proof = [&](int s) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      if (proofs && s + 1 == next_proof && s + 1 > 0) {
+        const uint32_t off = static_cast<uint32_t>((s + 1) / proof_steps * B);
 #pragma unroll
         for (int k = 0; k < SCANW; ++k) {
-          if (k * kWave < B && !done) {
-            const bool in = k * kWave + lane < B;
-            const int v = (in && word_ready(sw[k])) ? static_cast<int>(sw[k] & 7u) : 0;
-            const uint64_t b0 = __ballot(v & 1), b1 = __ballot(v & 2), b2 = __ballot(v & 4);
-            const int incl = carry + lanes_below(b0) + 2 * lanes_below(b1) + 4 * lanes_below(b2) + v;
-            const uint64_t fit = __ballot(in && incl <= old_free);
-            if (fit != 0) served = __shfl(incl, 63 - __clzll(static_cast<long long>(fit)), kWave);
-            if (fit != __ballot(in)) done = true;
-            carry += static_cast<int>(sum3(b0, b1, b2, ~0ull));
-          }
+          if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + off);
         }
       }
     }
-    const int prefix = base + partial;
-    base += total;
+  };
 
-    const int count = route_count(rt.u);
-    const uint32_t fmask = route_fmask(rt.u);
-    const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
-    bool fits = route_ok(rt.u) && alive && !poisoned && (count == 0 || prefix + count <= old_free);
-    int new_row = -1;
-    if (fits && count > 0) {
-      const int k = prefix + rt.rank;
-      if (first && k < window) new_row = lds_free[k];
-      if (__ballot(first && k >= window) != 0) {
-        if (first && k >= window) new_row = L.free_rows[old_free - 1 - k];
-        // wait for it here, on this rare path, so that no later use of the
-        // popped rows has to drain every load in flight
-        asm volatile("" ::"v"(new_row));
-      }
-      if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
-        fits = false;
-        if (lane == 0) {
-          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-    if (lane == 0) {
-      if (route_ok(rt.u) && alive && !poisoned && !fits && count > 0) *L.overflow_flag = 1;
-      if (poisoned) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    if (fits && count > 0) {
-      if (first) {
-        rt.wrow = new_row;
-        map_bank[rt.widx] = new_row;
-      }
-      float* const dst = L.values + static_cast<int64_t>(rt.wrow < 0 ? 0 : rt.wrow) * D;
+  // Does the proof before step s stop the layer?  Wave-uniform: every wave
+  // sums the same counts.  When it passes, step s claims its rows.
+  auto proof_stops = [&](int s, const TraceRoute& rs, int& home) __attribute__((always_inline)) -> bool {
+    if constexpr (!DENSE) {
+      if (proofs && s == next_proof) {
+        int total = 0;
+        if (s > 0) {
+          const uint32_t off = static_cast<uint32_t>(s / proof_steps * B);
+          auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+            return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
+          };
 #pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W && ((fmask >> j) & 1u)) {
-          float* p = const_cast<float*>(rl_ptr(dst, j));
-          gstore_row<VEC>(p, coff, cur[j]);
+          for (int k = 0; k < SCANW; ++k) {
+            if (k * kWave < B) {
+              uint64_t w = pw[k];
+              bool ready = word_ready(w);
+              if (__ballot(!ready) != 0) {
+                // a bank has not finished the run yet: bounded wait
+                int spins = 0;
+                while (!ready && spins < kSpinLimit) {
+                  __builtin_amdgcn_s_sleep(1);
+                  w = atomic_load_u64(run_l[k] + off);
+                  ready = word_ready(w);
+                  ++spins;
+                }
+                if (__ballot(!ready) != 0) {
+                  // never arrived: record it and stop the layer here
+                  if (lane == 0) {
+                    __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                          static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                  }
+                  done_steps = s;
+                  return true;
+                }
+              }
+              const bool in = k * kWave + lane < B;
+              total += static_cast<int>(wave_sum64(in ? static_cast<int64_t>(w & kValueMask) : 0));
+            }
+          }
+          total = __builtin_amdgcn_readfirstlane(total);
         }
+        if (old_free - total < proof_rows) {
+          done_steps = s;
+          return true;
+        }
+        next_proof += proof_steps;
+        claim(rs, home);
       }
     }
-    alive = alive && fits;
-    // step t+1 rewrites some of step t's slots in the rows just found
-    const int s1 = r1.wsrc;
-    const int v1 = __shfl(rt.wrow, s1 >= 0 ? s1 : 0, kWave);
-    if (s1 >= 0) r1.wrow = v1;
+    return false;
   };
 
   // ---- prologue: step 0 classified with its rows in flight
@@ -679,6 +772,7 @@ void sdm_trace_kernel(StepParams P) {
   // that issued them
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
+  int popA = 0, popB = 0;          // claims in flight, homed like the loads
   TraceRoute q, r0;
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   {
@@ -687,10 +781,10 @@ void sdm_trace_kernel(StepParams P) {
     int mw0, mr0;
     issue_map(i0, mw0, mr0);
     const int rrow = classify(0, i0, mw0, mr0, r0, q, q, true);
-    publish(0, r0);
+    after_classify(0, r0, popB);   // resolved in iteration 0
     issue_rows(0, r0, rrow, bufA);
   }
-  if constexpr (DENSE) {
+  if constexpr (DENSE || MAPLDS) {
     load_idx(1, idxB);             // classified in iteration 0
   } else {
     load_idx(1, ready1);           // its map entries, classified in iteration 0
@@ -700,43 +794,28 @@ void sdm_trace_kernel(StepParams P) {
 
   // Iteration s.  `self` homes are written now and read in iteration s+1,
   // `other` homes were written in iteration s-1 and are read now.
-  // device capacity proof: before each run of proof_steps steps the layer
-  // needs proof_rows free rows; every wave of the layer sees the same pops
-  // (base), so all of them stop at the same step
-  const int64_t proof_rows = DENSE ? 0 : P.trace_proof_rows;
-  const int proof_steps = P.trace_proof_steps > 0 ? P.trace_proof_steps : 1;
-  int done_steps = G;
-  // does the capacity proof stop the layer before step s?  Wave-uniform by
-  // construction; readfirstlane lets the compiler see it, so the loop exit
-  // stays a scalar branch.
-  auto proof_stops = [&](int s) __attribute__((always_inline)) -> bool {
-    if (__builtin_amdgcn_readfirstlane(
-            (proof_rows > 0 && s % proof_steps == 0 && old_free - base < proof_rows) ? 1 : 0)) {
-      done_steps = s;
-      return true;
-    }
-    return false;
-  };
   auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
                        TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other) __attribute__((always_inline)) {
-    issue_scan(s);
+                       int& mw_other, int& mr_other, int& pop_self, int pop_other)
+      __attribute__((always_inline)) {
+    issue_proof(s);
     TraceRoute r1;
-    if constexpr (DENSE) {
+    if constexpr (DENSE || MAPLDS) {
       load_idx(s + 2, idx_self);
       const int rrow = classify(s + 1, idx_other, -1, -1, r1, r0, q, route_ok(r0.u));
-      publish(s + 1, r1);
+      after_classify(s + 1, r1, pop_self);
       issue_rows(s + 1, r1, rrow, rows_next);
       compute(s, r0, rows_s);
+      if constexpr (MAPLDS) resolve(s, r0, r1, pop_other);
     } else {
       load_idx(s + 3, idx_self);
       issue_map(idx_other, mw_self, mr_self);   // step s+2
       ready2 = idx_other;
       const int rrow = classify(s + 1, ready1, mw_other, mr_other, r1, r0, q, route_ok(r0.u));
-      publish(s + 1, r1);
+      after_classify(s + 1, r1, pop_self);
       issue_rows(s + 1, r1, rrow, rows_next);
       compute(s, r0, rows_s);
-      resolve(s, r0, r1);
+      resolve(s, r0, r1, pop_other);
       ready1 = ready2;
     }
     q = r0;
@@ -754,39 +833,44 @@ void sdm_trace_kernel(StepParams P) {
   int s = 0;
   bool stopped = false;
   for (; s + 1 < G; s += 2) {
-    if (proof_stops(s)) {
+    if (proof_stops(s, r0, popB)) {
       stopped = true;
       break;
     }
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
-    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA);
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
+    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA);
   }
-  if (!stopped && s < G && !proof_stops(s)) {
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB);
+  if (!stopped && s < G && !proof_stops(s, r0, popB)) {
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
   }
 
-  // ---- the last bank closes the launch
-  if constexpr (!DENSE) {
-    if (bank == B - 1 && lane == 0) {
-      *L.free_count = old_free - served;
-      int64_t* const scan = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
-      atomic_store_u64(&scan[COWSDM_SCRATCH_EPOCH], static_cast<uint64_t>(epoch + 1u));
-      if (done_steps < G && P.trace_status) {
-        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-  // ---- device counters: the layer's last wave to finish (every wave of the
-  // layer read the counter before taking its ticket) moves the counter past
-  // the steps the layer ran
-  if (P.trace_step && lane == 0) {
+  // ---- the layer's last wave to finish closes the launch: every wave of the
+  // layer read free_count and the step counter before taking its ticket, and
+  // its claims (device-scope atomics) have returned before it: no release
+  // fence, whose L2 write-back every wave would pay
+  if (lane == 0 && (!DENSE || P.trace_step)) {
     int64_t* const ticket = P.trace_ticket + 1 + layer_id;
+    __builtin_amdgcn_s_waitcnt(0);
     const int64_t done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
     if (done == B - 1) {
+      if constexpr (!DENSE) {
+        const int64_t total = static_cast<int64_t>(atomic_load_u64(claims));
+        const int64_t fail = static_cast<int64_t>(atomic_load_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL));
+        const int64_t fit = fail > 0 && kClaimFailBase - fail < total ? kClaimFailBase - fail : total;
+        *L.free_count = static_cast<int32_t>(old_free - fit);
+        atomic_store_u64(claims, 0);
+        atomic_store_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL, 0);
+        atomic_store_u64(scan + COWSDM_SCRATCH_EPOCH, static_cast<uint64_t>(epoch + 1u));
+        if (done_steps < G && P.trace_status) {
+          __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
       atomic_store_u64(ticket, 0);
-      atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+      if (P.trace_step) {
+        atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+      }
     }
   }
 }
@@ -795,8 +879,8 @@ void sdm_trace_kernel(StepParams P) {
 // must be resident at once.  Returns false (nothing launched) when the grid
 // exceeds what the device can hold for this kernel; the caller then falls
 // back to one launch per step.
-template <typename IDX, bool DENSE>
-bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+template <typename IDX, bool DENSE, bool MAPLDS>
+bool launch_trace_kernels(const StepParams& P, int blocks, int vec, hipStream_t stream) {
   // the full-shape variant loads each bank's weights as 16-byte vectors
   bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads &&
               P.trace_stride[1] % 16 == 0 && P.trace_stride[7] % 16 == 0;
@@ -807,37 +891,52 @@ bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) 
     }
   }
   // one scan window when a layer has at most 64 banks (full shape only)
+  constexpr int kScan1 = DENSE ? kTraceScanWindows : 1;
   const int variant = !full ? 0 : (!DENSE && P.banks <= kWave ? 2 : 1);
   const void* kernels[3][3] = {
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kTraceScanWindows>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kTraceScanWindows>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kTraceScanWindows>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kTraceScanWindows>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kTraceScanWindows>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kTraceScanWindows>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, DENSE ? kTraceScanWindows : 1>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, DENSE ? kTraceScanWindows : 1>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, DENSE ? kTraceScanWindows : 1>)}};
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kTraceScanWindows, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kTraceScanWindows, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kTraceScanWindows, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kTraceScanWindows, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kTraceScanWindows, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kTraceScanWindows, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kScan1, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kScan1, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kScan1, MAPLDS>)}};
+  // residency depends on the LDS map's size: cached per kernel and slot count
   static int resident[3][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
+  static int resident_slots[3][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
-  if (resident[variant][which] < 0) {
+  const size_t lds_bytes = MAPLDS ? sizeof(int) * kBanksPerBlock * static_cast<size_t>(P.slots) : 0;
+  const int key = MAPLDS ? P.slots : 0;
+  if (resident[variant][which] < 0 || resident_slots[variant][which] != key) {
     int device = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStepThreads, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStepThreads, lds_bytes) !=
             hipSuccess) {
       (void)hipGetLastError();
       resident[variant][which] = 0;
     } else {
       resident[variant][which] = cus * per_cu;
     }
+    resident_slots[variant][which] = key;
   }
   if (blocks > resident[variant][which]) return false;
   void* args[] = {const_cast<StepParams*>(&P)};
-  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kStepThreads), args, 0, stream);
+  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kStepThreads), args, lds_bytes, stream);
   return true;  // a failed launch is reported by the caller's launch_status()
+}
+
+template <typename IDX, bool DENSE>
+bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+  // packed layers whose slot map fits keep it in LDS
+  if (!DENSE && P.slots <= kTraceMapSlots) {
+    return launch_trace_kernels<IDX, DENSE, true>(P, blocks, vec, stream);
+  }
+  return launch_trace_kernels<IDX, DENSE, false>(P, blocks, vec, stream);
 }
 
 }  // namespace cowsdm_impl

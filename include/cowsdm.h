@@ -57,10 +57,15 @@ extern "C" {
 #define COWSDM_ERR_TRACE_RANGE 0x80  /* trace step past steps_recorded    */
 
 /* Word offsets inside the per-layer step scratch (int64 words). */
-/* EPOCH retires the previous launch's scan slots (the layer's last bank
+/* EPOCH retires the previous launch's scan slots (the layer's last wave
  * advances it); ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's
- * scan slot.  Words 1, 2 and 4-7 are reserved. */
+ * scan slot.  In a decode trace's scan buffer, CLAIMS counts the rows the
+ * current persistent launch has claimed and CLAIM_FAIL records the first
+ * claim that did not fit (both zero between launches).  Words 4-7 are
+ * reserved. */
 #define COWSDM_SCRATCH_EPOCH 0
+#define COWSDM_SCRATCH_CLAIMS 1
+#define COWSDM_SCRATCH_CLAIM_FAIL 2
 #define COWSDM_SCRATCH_ERRORS 3
 #define COWSDM_SCRATCH_SLOTS 8
 
@@ -141,7 +146,12 @@ typedef struct cowsdm_trace {
    * for packed state, every workgroup resident), else one launch per step.
    * Packed launches then need `scan`: nlayers blocks of scan_words int64
    * words (>= cowsdm_trace_scan_words(banks, min(steps, 64))), zero before
-   * first use and kept valid by the kernels. */
+   * first use and kept valid by the kernels, and `ticket` (1 + nlayers
+   * int64 words, zero before the first launch), also with host offsets:
+   * the layer's last wave to finish writes free_count back.  First touches
+   * then claim their rows with an atomic add per (step, bank), as the
+   * reference's proven kernel does, so physical rows may be a permutation
+   * of those of single-step launches; everything else is identical. */
   int64_t* scan;
   int64_t scan_words;
   int32_t persistent;
