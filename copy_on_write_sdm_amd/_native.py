@@ -56,6 +56,9 @@ HIPCC_FLAGS = (
     "-ffp-contract=off",
     # never emit packed FP32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep each atomic as written: combining a lane-0 atomic across the wave
+    # makes its result (a row claim read an iteration later) wait at once
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 )
 
 

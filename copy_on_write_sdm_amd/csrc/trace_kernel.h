@@ -164,6 +164,9 @@ void sdm_trace_kernel(StepParams P) {
   // full shape: the step's weights, written per lane, read back broadcast
   __shared__ vf4_t lds_weights[kBanksPerBlock][2][kWave / 4];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
+  // each step's row addresses, lane j's write row and read row, read back
+  // by every lane as broadcasts
+  __shared__ uint64_t lds_ptrs[kBanksPerBlock][2][kWave];
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -313,26 +316,28 @@ void sdm_trace_kernel(StepParams P) {
 
   // Step t from its slots and map entries.  r1: step t-1 (classified), r2:
   // step t-2 (its first touches popped).  Returns the read lane's row.
+  // Lanes past W (R) hold slot 0 as their write (read) slot: they compute
+  // along, and their results are masked once at the end.
+  const uint64_t wlanes = W >= kWave ? ~0ull : ((1ull << W) - 1);
+  const uint64_t rlanes = R >= kWave ? ~0ull : ((1ull << R) - 1);
   auto classify = [&](int t, const TraceIdx& m, int wraw, int rraw, TraceRoute& rt,
                       const TraceRoute& r1, const TraceRoute& r2, bool ok_prev)
       __attribute__((always_inline)) -> int {
-    int lerr = m.err | base_err;
     if constexpr (MAPLDS) {
-      // every step up to t-2 has stored its pops here
-      wraw = lane < W ? lds_map[m.widx] : -1;
-      rraw = lane < R ? lds_map[m.ridx] : -1;
-    }
-    if constexpr (!DENSE) {
-      if (lane < W && wraw >= C) { lerr |= COWSDM_ERR_CORRUPT; wraw = -1; }
-      if (lane < R && rraw >= C) { lerr |= COWSDM_ERR_CORRUPT; rraw = -1; }
+      // every step up to t-2 has stored its pops here; read first, so that
+      // the matching below covers the LDS latency
+      wraw = lds_map[m.widx];
+      rraw = lds_map[m.ridx];
     }
     int wsrc = -1, rsrc = -1, rraw_lane = -1;
+    uint64_t dup = 0;
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) {
       if (j < W) {
         const int sj = rl(m.widx, j);
-        if (lane < W && lane > j && m.widx == sj) lerr |= COWSDM_ERR_DUP_WRITE;
-        if (lane < R && m.ridx == sj) rraw_lane = j;
+        // a write lane above j with the same slot
+        dup |= __ballot(m.widx == sj) & wlanes & ~((2ull << j) - 1);
+        if (m.ridx == sj) rraw_lane = j;
       }
     }
     if (t >= 1) {
@@ -340,9 +345,19 @@ void sdm_trace_kernel(StepParams P) {
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         if (j < W) {
           const int sj = rl(r1.widx, j);
-          if (lane < W && m.widx == sj) wsrc = j;
-          if (lane < R && m.ridx == sj) rsrc = j;
+          if (m.widx == sj) wsrc = j;
+          if (m.ridx == sj) rsrc = j;
         }
+      }
+    }
+    if (rraw_lane >= 0) rsrc = -1;
+    uint64_t bad = 0;  // map entries outside the slab
+    if constexpr (!DENSE) {
+      bad = (__ballot(wraw >= C) & wlanes) | (__ballot(rraw >= C) & rlanes);
+      if (bad != 0) {
+        // rare: report, and treat the entry as shared
+        wraw = wraw >= C ? -1 : wraw;
+        rraw = rraw >= C ? -1 : rraw;
       }
     }
     if (!DENSE && !MAPLDS && t >= 2) {
@@ -351,14 +366,17 @@ void sdm_trace_kernel(StepParams P) {
         if (j < W) {
           const int sj = rl(r2.widx, j);
           const int row = rl(r2.wrow, j);
-          if (lane < W && wsrc < 0 && m.widx == sj) wraw = row;
-          if (lane < R && rsrc < 0 && m.ridx == sj) rraw = row;
+          if (wsrc < 0 && m.widx == sj) wraw = row;
+          if (rsrc < 0 && m.ridx == sj) rraw = row;
         }
       }
     }
-    if (rraw_lane >= 0) rsrc = -1;
-    const bool any_err = __ballot(lerr != 0) != 0;
+    const bool any_err = (__ballot((m.err | base_err) != 0) | dup | bad) != 0;
     if (!DENSE && any_err && t < G) {
+      int lerr = m.err | base_err;
+      if (lane == 0) {
+        lerr |= (dup != 0 ? COWSDM_ERR_DUP_WRITE : 0) | (bad != 0 ? COWSDM_ERR_CORRUPT : 0);
+      }
       const int e = wave_or(lerr);
       if (lane == 0) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(e),
@@ -366,11 +384,10 @@ void sdm_trace_kernel(StepParams P) {
       }
     }
     const bool ok = ok_prev && !any_err;
-    const bool first = !DENSE && ok && lane < W && wsrc < 0 && wraw < 0;
-    const uint64_t fm = __ballot(first);
-    const bool wfwd = __ballot(lane < W && wsrc >= 0) != 0;
-    const bool fix = wfwd || __ballot(lane < R && rsrc >= 0) != 0;
-    const bool raw = __ballot(lane < R && rraw_lane >= 0) != 0;
+    const uint64_t fm = DENSE || !ok ? 0ull : __ballot(wsrc < 0 && wraw < 0) & wlanes;
+    const bool wfwd = (__ballot(wsrc >= 0) & wlanes) != 0;
+    const bool fix = wfwd || (__ballot(rsrc >= 0) & rlanes) != 0;
+    const bool raw = (__ballot(rraw_lane >= 0) & rlanes) != 0;
     rt.u = static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
            (ok ? 1u << 8 : 0u) | (fix ? 1u << 9 : 0u) | (raw ? 1u << 10 : 0u) |
            (wfwd ? 1u << 11 : 0u);
@@ -401,19 +418,28 @@ void sdm_trace_kernel(StepParams P) {
       wp = rt.wrow < 0 ? row_at(m0_bank, rt.widx) : row_at(slab, rt.wrow);
       rp = rrow < 0 ? row_at(m0_bank, rt.ridx) : row_at(slab, rrow);
     }
-    const uint32_t co = fresh(coff);
+    // lane j's row pointers through LDS: a broadcast read gives every lane
+    // two of them, and each row load takes its own 64-bit vector address (no
+    // scalar base, whose write by a readlane a load could not follow at once)
+    lds_ptrs[wave][0][lane] = reinterpret_cast<uint64_t>(wp);
+    lds_ptrs[wave][1][lane] = reinterpret_cast<uint64_t>(rp);
+    typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+    const u64x2* const pw = reinterpret_cast<const u64x2*>(&lds_ptrs[wave][0][0]);
+    const u64x2* const pr = reinterpret_cast<const u64x2*>(&lds_ptrs[wave][1][0]);
 #pragma unroll
-    for (int j = 0; j < kTraceMaxWrites; ++j) {
+    for (int j = 0; j < kTraceMaxWrites; j += 2) {
       if (j < W) {
-        const float* p = rl_ptr(wp, j);
-        gload_row<VEC>(p, co, buf.w[j]);
+        const u64x2 two = pw[j / 2];
+        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
+        if (j + 1 < W) gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
       }
     }
 #pragma unroll
-    for (int i = 0; i < kTraceMaxReads; ++i) {
+    for (int i = 0; i < kTraceMaxReads; i += 2) {
       if (i < R) {
-        const float* p = rl_ptr(rp, i);
-        gload_row<VEC>(p, co, buf.r[i]);
+        const u64x2 two = pr[i / 2];
+        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
+        if (i + 1 < R) gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
       }
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
