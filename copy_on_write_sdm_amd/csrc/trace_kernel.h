@@ -69,17 +69,14 @@ struct TraceRoute {                 // a classified step
   int rraw;       // read lane: write lane of step t itself with this slot, else -1
   int rank;       // write lane: rank among the bank's first touches
   uint32_t u;     // wave-uniform: bits 0-3 first-touch write lanes, 4-7 their count,
-                  // 8 the step runs (routes valid, every earlier step ran),
-                  // 9 a row comes from step t-1, 10 a read sees a write of step t,
-                  // 11 a write rewrites a slot of step t-1
+                  // 8 the step runs (routes valid, every earlier step ran)
+  uint32_t fwd;   // wave-uniform: rows from step t-1, bits 0-3 writes, 4-19 reads
+  uint32_t rawm;  // wave-uniform: reads that see a write of step t itself
 };
 
 __device__ __forceinline__ uint32_t route_fmask(uint32_t u) { return u & 15u; }
 __device__ __forceinline__ int route_count(uint32_t u) { return static_cast<int>((u >> 4) & 15u); }
 __device__ __forceinline__ bool route_ok(uint32_t u) { return (u >> 8) & 1u; }
-__device__ __forceinline__ bool route_fix(uint32_t u) { return (u >> 9) & 1u; }
-__device__ __forceinline__ bool route_raw(uint32_t u) { return (u >> 10) & 1u; }
-__device__ __forceinline__ bool route_wfwd(uint32_t u) { return (u >> 11) & 1u; }
 
 typedef __attribute__((address_space(1))) float gfloat;
 typedef float vf2 __attribute__((ext_vector_type(2)));
@@ -385,12 +382,13 @@ void sdm_trace_kernel(StepParams P) {
     }
     const bool ok = ok_prev && !any_err;
     const uint64_t fm = DENSE || !ok ? 0ull : __ballot(wsrc < 0 && wraw < 0) & wlanes;
-    const bool wfwd = (__ballot(wsrc >= 0) & wlanes) != 0;
-    const bool fix = wfwd || (__ballot(rsrc >= 0) & rlanes) != 0;
-    const bool raw = (__ballot(rraw_lane >= 0) & rlanes) != 0;
-    rt.u = static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
-           (ok ? 1u << 8 : 0u) | (fix ? 1u << 9 : 0u) | (raw ? 1u << 10 : 0u) |
-           (wfwd ? 1u << 11 : 0u);
+    rt.u = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
+        (ok ? 1u << 8 : 0u));
+    rt.fwd = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(__ballot(wsrc >= 0) & wlanes) |
+        (static_cast<uint32_t>(__ballot(rsrc >= 0) & rlanes) << kTraceMaxWrites));
+    rt.rawm = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(__ballot(rraw_lane >= 0) & rlanes));
     rt.rank = lanes_below(fm);
     rt.widx = m.widx;
     rt.ridx = m.ridx;
@@ -482,25 +480,20 @@ void sdm_trace_kernel(StepParams P) {
   // Step t: LDS row j holds write j of step t-1 until this step replaces it.
   auto compute = [&](int t, const TraceRoute& rt, TraceRows<VEC>& buf)
       __attribute__((always_inline)) {
-    const bool run = route_ok(rt.u) && alive;
+    const bool run = __builtin_amdgcn_readfirstlane(route_ok(rt.u) && alive ? 1 : 0) != 0;
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
     if (run) {
-      if (route_fix(rt.u)) {
+      const uint32_t fwd = rt.fwd;
+      if (fwd != 0) {
 #pragma unroll
         for (int j = 0; j < kTraceMaxWrites; ++j) {
-          if (j < W) {
-            const int src = rl(rt.wsrc, j);
-            if (src >= 0) lds_get(src, buf.w[j]);
-          }
+          if (j < W && ((fwd >> j) & 1u)) lds_get(rl(rt.wsrc, j), buf.w[j]);
         }
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
-          if (i < R) {
-            const int src = rl(rt.rsrc, i);
-            if (src >= 0) lds_get(src, buf.r[i]);
-          }
+          if (i < R && ((fwd >> (kTraceMaxWrites + i)) & 1u)) lds_get(rl(rt.rsrc, i), buf.r[i]);
         }
       }
       vf4_t wwv = 0.0f, rwv[kTraceMaxReads / 4];
@@ -552,12 +545,12 @@ void sdm_trace_kernel(StepParams P) {
           lds_put(j, cur[j]);
         }
       }
-      if (route_raw(rt.u)) {
+      const uint32_t rawm = rt.rawm;
+      if (rawm != 0) {
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
-          if (i < R) {
-            const int src = rl(rt.rraw, i);
-            if (src >= 0) lds_get(src, buf.r[i]);
+          if (i < R && ((rawm >> i) & 1u)) {
+            lds_get(rl(rt.rraw, i), buf.r[i]);
           }
         }
       }
@@ -667,7 +660,7 @@ void sdm_trace_kernel(StepParams P) {
       alive = fits;
     }
     // step t+1 rewrites some of step t's slots in the rows just found
-    if (route_wfwd(r1.u)) {
+    if ((r1.fwd & ((1u << kTraceMaxWrites) - 1)) != 0) {
       const int s1 = r1.wsrc;
       const int v1 = __shfl(rt.wrow, s1 >= 0 ? s1 : 0, kWave);
       if (s1 >= 0) r1.wrow = v1;
@@ -801,6 +794,7 @@ void sdm_trace_kernel(StepParams P) {
   int popA = 0, popB = 0;          // claims in flight, homed like the loads
   TraceRoute q, r0;
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
+  q.fwd = 0; q.rawm = 0;
   {
     TraceIdx i0;
     load_idx(0, i0);
