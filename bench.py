@@ -284,7 +284,7 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": None if traffic is None else traffic["bytes_per_launch"],
             "traffic_source": None if traffic is None else traffic["source"],
-            "kernel": "sdm_trace_kernel<int, 2, false, true> (packed, 7 layers x 64 banks)",
+            "kernel": "sdm_trace_kernel<int, 2, false, true, 1, true> (packed, 7 layers x 64 banks)",
             "launch_us": round(launch_us, 3),
             "steps_per_launch": round(K / launches, 3),
             "us_per_step": round(1000.0 * p_run["gpu_ms"] / K, 4),
