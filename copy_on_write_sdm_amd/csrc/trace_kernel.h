@@ -1,5 +1,5 @@
 // Persistent multi-step form of the copy-on-write SDM step: one launch runs
-// G consecutive decode steps of device-resident routes for every (layer,
+// G <= 256 consecutive decode steps of device-resident routes for every (layer,
 // bank), with the results of G single-step launches (physical rows of first
 // touches may be assigned in another order, as in the reference's proven
 // kernel, whose banks pop with an atomic add).
@@ -274,17 +274,38 @@ void sdm_trace_kernel(StepParams P) {
     return p + static_cast<uint64_t>(static_cast<uint32_t>(t)) * stride;
   };
 
-  // ---- gates of every step, lane t holding step t's
-  float alpha_l = 0.0f, in_l = 0.0f, er_l = 0.0f;
-  if (lane < G) {
-    const float fg = reinterpret_cast<const float*>(first_step(L.forget_log_gate, 5) +
-                                                    static_cast<int64_t>(lane) * P.trace_stride[5])[bank];
-    in_l = reinterpret_cast<const float*>(first_step(L.input_gate, 3) +
-                                          static_cast<int64_t>(lane) * P.trace_stride[3])[bank];
-    er_l = reinterpret_cast<const float*>(first_step(L.erase_gate, 4) +
-                                          static_cast<int64_t>(lane) * P.trace_stride[4])[bank];
-    alpha_l = static_cast<float>(exp(static_cast<double>(fg)));
+  // ---- gates in chunks of 64 steps, lane k holding step 64c + k of chunk c;
+  // the next chunk is loaded one chunk ahead
+  auto load_gates = [&](int c, float& fg, float& ig, float& eg) __attribute__((always_inline)) {
+    const int t = c * kWave + lane;
+    fg = 0.0f;
+    ig = 0.0f;
+    eg = 0.0f;
+    if (t < G) {
+      fg = reinterpret_cast<const float*>(first_step(L.forget_log_gate, 5) +
+                                          static_cast<int64_t>(t) * P.trace_stride[5])[bank];
+      ig = reinterpret_cast<const float*>(first_step(L.input_gate, 3) +
+                                          static_cast<int64_t>(t) * P.trace_stride[3])[bank];
+      eg = reinterpret_cast<const float*>(first_step(L.erase_gate, 4) +
+                                          static_cast<int64_t>(t) * P.trace_stride[4])[bank];
+    }
+  };
+  float alpha_l, in_l, er_l, fg_n, in_n, er_n;
+  {
+    float fg0;
+    load_gates(0, fg0, in_l, er_l);
+    alpha_l = static_cast<float>(exp(static_cast<double>(fg0)));
+    load_gates(1, fg_n, in_n, er_n);
   }
+  // before step s (s even): the step's chunk in the lane registers
+  auto gates_for = [&](int s) __attribute__((always_inline)) {
+    if (s > 0 && (s & (kWave - 1)) == 0) {
+      alpha_l = static_cast<float>(exp(static_cast<double>(fg_n)));
+      in_l = in_n;
+      er_l = er_n;
+      if (s + kWave < G) load_gates(s / kWave + 1, fg_n, in_n, er_n);
+    }
+  };
 
   // ---- stages
   auto load_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
@@ -507,9 +528,9 @@ void sdm_trace_kernel(StepParams P) {
 #pragma unroll
         for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
       }
-      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t));
-      const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t));
-      const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t));
+      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t & (kWave - 1)));
+      const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t & (kWave - 1)));
+      const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t & (kWave - 1)));
       float ret[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) ret[v] = 0.0f;
@@ -857,10 +878,12 @@ void sdm_trace_kernel(StepParams P) {
       stopped = true;
       break;
     }
+    gates_for(s);
     iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
     iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA);
   }
   if (!stopped && s < G && !proof_stops(s, r0, popB)) {
+    gates_for(s);
     iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
   }
 

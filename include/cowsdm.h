@@ -141,11 +141,11 @@ typedef struct cowsdm_trace {
   int64_t* ticket;
   int64_t first_step;
   int64_t stride_bytes[9];
-  /* Persistent launches: with persistent != 0 one launch runs up to 64
+  /* Persistent launches: with persistent != 0 one launch runs up to 256
    * steps when the shape allows it (W <= 4, R <= 16, D <= 256, banks <= 256
    * for packed state, every workgroup resident), else one launch per step.
    * Packed launches then need `scan`: nlayers blocks of scan_words int64
-   * words (>= cowsdm_trace_scan_words(banks, min(steps, 64))), zero before
+   * words (>= cowsdm_trace_scan_words(banks, min(steps, 256))), zero before
    * first use and kept valid by the kernels, and `ticket` (1 + nlayers
    * int64 words, zero before the first launch), also with host offsets:
    * the layer's last wave to finish writes free_count back.  First touches

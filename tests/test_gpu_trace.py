@@ -80,6 +80,8 @@ def _per_step(states, routes, steps, layers):
     (4, 33, 32, 100, 2, 5, 25, 64),      # odd width > 64 (two floats per lane)
     (2, 6, 4500, 128, 4, 16, 20, 8),     # slot map too large for LDS
     (1, 3, 4096, 64, 3, 7, 12, 5),       # largest slot map staged in LDS
+    (2, 6, 64, 128, 4, 16, 200, 200),    # 200 steps in one launch: gates in 4 chunks
+    (1, 4, 48, 64, 3, 5, 129, 129),      # odd launch whose last step starts a chunk
 ])
 def test_persistent_trace_matches_single_steps(device, layers, banks, slots, width, writes,
                                               reads, steps, group):
