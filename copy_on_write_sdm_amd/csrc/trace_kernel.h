@@ -728,7 +728,8 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // iteration s-1 loads the counts that the proof before step s sums
+  // iteration s-1 loads the counts that the proof before step s sums, after
+  // its compute: the later the load, the likelier every bank has published
   auto issue_proof = [&](int s) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (proofs && s + 1 == next_proof && s + 1 > 0) {
@@ -839,7 +840,6 @@ void sdm_trace_kernel(StepParams P) {
                        TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
                        int& mw_other, int& mr_other, int& pop_self, int pop_other)
       __attribute__((always_inline)) {
-    issue_proof(s);
     TraceRoute r1;
     if constexpr (DENSE || MAPLDS) {
       load_idx(s + 2, idx_self);
@@ -847,6 +847,7 @@ void sdm_trace_kernel(StepParams P) {
       after_classify(s + 1, r1, pop_self);
       issue_rows(s + 1, r1, rrow, rows_next);
       compute(s, r0, rows_s);
+      issue_proof(s);
       if constexpr (MAPLDS) resolve(s, r0, r1, pop_other);
     } else {
       load_idx(s + 3, idx_self);
@@ -856,6 +857,7 @@ void sdm_trace_kernel(StepParams P) {
       after_classify(s + 1, r1, pop_self);
       issue_rows(s + 1, r1, rrow, rows_next);
       compute(s, r0, rows_s);
+      issue_proof(s);
       resolve(s, r0, r1, pop_other);
       ready1 = ready2;
     }
