@@ -43,7 +43,7 @@ PREFIX = 256
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=448)
+    p.add_argument("--steps", type=int, default=512)
     p.add_argument("--warmup", type=int, default=64)
     p.add_argument("--batch", type=int, default=64)
     p.add_argument("--proof-steps", type=int, default=4,
