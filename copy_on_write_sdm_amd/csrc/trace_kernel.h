@@ -158,7 +158,8 @@ __attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
 void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
   __shared__ float lds_rows[kBanksPerBlock][kTraceMaxWrites][kRow];
-  // full shape: the step's weights, written per lane, read back broadcast
+  // full shape: the next step's weights, written per lane at the end of an
+  // iteration, read back as broadcasts by the step's compute
   __shared__ vf4_t lds_weights[kBanksPerBlock][2][kWave / 4];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
   // each step's row addresses, lane j's write row and read row, read back
@@ -462,8 +463,10 @@ void sdm_trace_kernel(StepParams P) {
       }
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
-    buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-    buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    if constexpr (!FULL) {
+      buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+      buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    }
   };
 
   auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
@@ -498,6 +501,23 @@ void sdm_trace_kernel(StepParams P) {
   }
   bool alive = true;
 
+  // full shape: lane j's write and read weight of step t, loaded two
+  // iterations ahead and handed to LDS at the end of the iteration before
+  auto load_weights = [&](int t, float& ww, float& rw) __attribute__((always_inline)) {
+    if constexpr (FULL) {
+      const int tc = t < G ? t : G - 1;
+      ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+      rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    }
+  };
+  auto put_weights = [&](float ww, float rw) __attribute__((always_inline)) {
+    if constexpr (FULL) {
+      float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
+      wl[lane] = ww;
+      wl[kWave + lane] = rw;
+    }
+  };
+
   // Step t: LDS row j holds write j of step t-1 until this step replaces it.
   auto compute = [&](int t, const TraceRoute& rt, TraceRows<VEC>& buf)
       __attribute__((always_inline)) {
@@ -519,11 +539,8 @@ void sdm_trace_kernel(StepParams P) {
       }
       vf4_t wwv = 0.0f, rwv[kTraceMaxReads / 4];
       if constexpr (FULL) {
-        // lane j holds weight j; one LDS round trip gives every lane all of
-        // them as vectors, instead of a readlane per weight
-        float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
-        wl[lane] = buf.ww;
-        wl[kWave + lane] = buf.rw;
+        // lane j put weight j there in the iteration before: every lane reads
+        // all of them as vectors, instead of a readlane per weight
         wwv = lds_weights[wave][0][0];
 #pragma unroll
         for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
@@ -814,6 +831,13 @@ void sdm_trace_kernel(StepParams P) {
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
   int popA = 0, popB = 0;          // claims in flight, homed like the loads
+  float wwA = 0.0f, rwA = 0.0f, wwB = 0.0f, rwB = 0.0f;  // weights in flight
+  {
+    float ww0 = 0.0f, rw0 = 0.0f;
+    load_weights(0, ww0, rw0);
+    put_weights(ww0, rw0);
+    load_weights(1, wwB, rwB);     // handed over at the end of iteration 0
+  }
   TraceRoute q, r0;
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   q.fwd = 0; q.rawm = 0;
@@ -838,8 +862,10 @@ void sdm_trace_kernel(StepParams P) {
   // `other` homes were written in iteration s-1 and are read now.
   auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
                        TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other, int& pop_self, int pop_other)
+                       int& mw_other, int& mr_other, int& pop_self, int pop_other,
+                       float& ww_self, float& rw_self, float ww_other, float rw_other)
       __attribute__((always_inline)) {
+    load_weights(s + 2, ww_self, rw_self);
     TraceRoute r1;
     if constexpr (DENSE || MAPLDS) {
       load_idx(s + 2, idx_self);
@@ -861,6 +887,7 @@ void sdm_trace_kernel(StepParams P) {
       resolve(s, r0, r1, pop_other);
       ready1 = ready2;
     }
+    put_weights(ww_other, rw_other);   // step s+1's
     q = r0;
     r0 = r1;
   };
@@ -881,12 +908,12 @@ void sdm_trace_kernel(StepParams P) {
       break;
     }
     gates_for(s);
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
-    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA);
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB, wwA, rwA, wwB, rwB);
+    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA, wwB, rwB, wwA, rwA);
   }
   if (!stopped && s < G && !proof_stops(s, r0, popB)) {
     gates_for(s);
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
+    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB, wwA, rwA, wwB, rwB);
   }
 
   // ---- the layer's last wave to finish closes the launch: every wave of the
