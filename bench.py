@@ -14,7 +14,10 @@ before every 4 steps each packed layer proves on the device that its free
 rows cover the worst case (prepare_step_capacity(B*W*4) of the reference's
 decode loop); a layer that would not is stopped there, grown on the host by
 prepare_step_capacity itself, and resumed, so growth matches the host-proven
-loop exactly.  W untimed warmup steps, then exactly K timed steps between
+loop exactly.  --config 3 (2,048-token prefill, packed handoff timed) and
+--config 5 (4 heads, N = 65,536, Zipf routes, decode from an empty slab) run
+BASELINE's other single-GPU configurations; --batch sets B (1/16/64).
+W untimed warmup steps, then exactly K timed steps between
 synchronisations.  The dense-table control runs the same routes the same way
 from the same packed state; both end states must be equal.  The CPU baseline
 is the torch restatement of the reference's dense-table step on the host
@@ -36,15 +39,27 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "decode tokens/s at batch 64 (L=7,N=256,D=128); achieved HBM GB/s % of peak"
 PEAK_HBM_GBPS = 8000.0
-LAYERS, HEADS, SLOTS, WIDTH, WRITES, READS = 7, 1, 256, 128, 4, 16
-PREFIX = 256
+LAYERS, WIDTH, WRITES, READS = 7, 128, 4, 16
+
+# BASELINE configurations on one GPU: heads, slots, dense prefill tokens,
+# default warmup + timed decode steps, route distribution
+CONFIGS = {
+    2: dict(heads=1, slots=256, prefix=256, warmup=64, steps=512, distribution="uniform",
+            text="packed copy-on-write SDM decode, prefix 256"),
+    3: dict(heads=1, slots=256, prefix=2048, warmup=64, steps=192, distribution="uniform",
+            text="long-prefix handoff: 2048-token dense prefill packed, then 256 decode steps"),
+    5: dict(heads=4, slots=65536, prefix=0, warmup=64, steps=960, distribution="zipf",
+            text="large address space: Zipf(1.1) routes, decode from an empty slab"),
+}
 
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=512)
-    p.add_argument("--warmup", type=int, default=64)
+    p.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS),
+                   help="BASELINE configuration (2 is the headline metric's)")
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default: the config's)")
+    p.add_argument("--warmup", type=int, default=None, help="warmup steps (default: the config's)")
     p.add_argument("--batch", type=int, default=64)
     p.add_argument("--proof-steps", type=int, default=4,
                    help="decode steps per capacity proof (the growth quantum's steps)")
@@ -56,8 +71,9 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="run one 256 MiB device copy first, so that counter passes "
                         "(FETCH_SIZE, WRITE_SIZE) can be scaled by a kernel of known traffic")
-    p.add_argument("--eager-steps", type=int, default=32,
-                   help="steps of the per-layer Python drop-in path to time (0: skip)")
+    p.add_argument("--eager-steps", type=int, default=None,
+                   help="steps of the per-layer Python drop-in path to time (0: skip; "
+                        "default 32 for config 2, else 0)")
     return p.parse_args()
 
 
@@ -88,7 +104,9 @@ def profiled_traffic(batch: int, launch_steps: int) -> dict | None:
 
 def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
     """Time the torch restatement of the reference's dense-table CPU step
-    (allocator.py:1612-1633) at the benchmark's shape on the host cores."""
+    (allocator.py:1612-1633) at config 2's shape on the host cores."""
+
+    SLOTS = CONFIGS[2]["slots"]
 
     import torch
 
@@ -98,7 +116,7 @@ def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     steps = 48
-    m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=seed)
+    m0 = synthetic.make_initial_memory(LAYERS, 1, SLOTS, WIDTH, seed=seed)
     batch_inputs = synthetic.make_steps(steps=steps, layers=LAYERS, banks=batch, slots=SLOTS,
                                         width=WIDTH, writes=WRITES, reads=READS, seed=seed + 1)
     tables = [m0[l, 0].expand(batch, -1, -1).contiguous() for l in range(LAYERS)]
@@ -139,54 +157,72 @@ def main() -> int:
     from copy_on_write_sdm_amd import synthetic
 
     dev = torch.device("cuda:0")
-    B, K, Wm = args.batch, args.steps, args.warmup
+    cfg = CONFIGS[args.config]
+    HEADS, SLOTS, PREFIX = cfg["heads"], cfg["slots"], cfg["prefix"]
+    B = args.batch
+    K = cfg["steps"] if args.steps is None else args.steps
+    Wm = cfg["warmup"] if args.warmup is None else args.warmup
+    eager_steps = (32 if args.config == 2 else 0) if args.eager_steps is None else args.eager_steps
+    banks = B * HEADS                       # bank = request * H + head
+    templates = torch.arange(HEADS, dtype=torch.int64, device=dev).repeat(B)
     if args.copy_calibration:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
     total_steps = Wm + K
-    quantum = max(16, B * WRITES * 4)
+    quantum = max(16, banks * WRITES * 4)
 
-    # ---- prefill (dense kernel) and copy-on-write handoff, untimed
+    # ---- prefill (dense kernel) and copy-on-write handoff, untimed except the
+    # handoff itself
     m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=args.seed, device=dev)
-    prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=B, slots=SLOTS, width=WIDTH,
-                                  writes=WRITES, reads=READS, seed=args.seed + 1, device=dev)
-    tables = [m0[l, 0].expand(B, -1, -1).contiguous() for l in range(LAYERS)]
-    prefill = cow.DecodeTrace(memories=tables, write_indices=prefix.write_indices,
-                              write_weights=prefix.write_weights, values=prefix.values,
-                              input_gate=prefix.input_gate,
-                              forget_log_gate=prefix.forget_log_gate,
-                              read_indices=prefix.read_indices, read_weights=prefix.read_weights)
-    for s0 in range(0, PREFIX, 64):
-        prefill.launch(min(64, PREFIX - s0), start=s0)
-    states = []
-    for l in range(LAYERS):
-        active = torch.zeros(B, SLOTS, dtype=torch.bool, device=dev)
-        cow.mark_written(active, prefix.write_indices[:, l].permute(1, 0, 2).reshape(B, -1))
-        states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
-            m0[l], tables[l], active, template_indices=torch.zeros(B, dtype=torch.int64,
-                                                                  device=dev),
-            growth_quantum_rows=quantum))
-    del prefill, prefix
+    handoff_ms = None
+    if PREFIX:
+        prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=banks, slots=SLOTS,
+                                      width=WIDTH, writes=WRITES, reads=READS,
+                                      seed=args.seed + 1, device=dev,
+                                      distribution=cfg["distribution"], heads=HEADS)
+        tables = [m0[l][templates].contiguous() for l in range(LAYERS)]
+        prefill = cow.DecodeTrace(memories=tables, write_indices=prefix.write_indices,
+                                  write_weights=prefix.write_weights, values=prefix.values,
+                                  input_gate=prefix.input_gate,
+                                  forget_log_gate=prefix.forget_log_gate,
+                                  read_indices=prefix.read_indices,
+                                  read_weights=prefix.read_weights)
+        prefill.launch(PREFIX, start=0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        states = []
+        for l in range(LAYERS):
+            active = torch.zeros(banks, SLOTS, dtype=torch.bool, device=dev)
+            cow.mark_written(active, prefix.write_indices[:, l].permute(1, 0, 2).reshape(banks, -1))
+            states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
+                m0[l], tables[l], active, template_indices=templates,
+                growth_quantum_rows=quantum))
+        torch.cuda.synchronize()
+        handoff_ms = 1000.0 * (time.perf_counter() - t0)
+        del prefill, prefix, tables
+    else:
+        states = [cow.PackedSDMCopyOnWriteState.allocate(
+            m0[l], banks=banks, capacity_rows=quantum, template_indices=templates,
+            growth_quantum_rows=quantum) for l in range(LAYERS)]
     handoff_rows = [int(st.allocated_rows_tensor()) for st in states]
     handoff_capacity = [st.capacity_rows for st in states]
 
     # ---- decode routes
-    routes = synthetic.make_steps(steps=total_steps, layers=LAYERS, banks=B, slots=SLOTS,
+    routes = synthetic.make_steps(steps=total_steps, layers=LAYERS, banks=banks, slots=SLOTS,
                                   width=WIDTH, writes=WRITES, reads=READS, seed=args.seed + 2,
-                                  device=dev)
+                                  device=dev, distribution=cfg["distribution"], heads=HEADS)
     inputs = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
                   values=routes.values, input_gate=routes.input_gate,
                   forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
                   read_weights=routes.read_weights)
     dense_tables = [st.materialize_dense() for st in states]
     eager_states = None
-    if args.eager_steps:
+    if eager_steps:
         eager_states = [cow.PackedSDMCopyOnWriteState.from_dense_overlay(
             m0[l], dense_tables[l], (states[l].logical_to_physical >= 0),
-            template_indices=torch.zeros(B, dtype=torch.int64, device=dev),
-            growth_quantum_rows=quantum) for l in range(LAYERS)]
+            template_indices=templates, growth_quantum_rows=quantum) for l in range(LAYERS)]
     packed = cow.DecodeTrace(states=states, **inputs)
     dense = cow.DecodeTrace(memories=dense_tables, **inputs)
 
@@ -227,17 +263,17 @@ def main() -> int:
     # ---- per-layer Python drop-in path (exact reference call pattern)
     eager = None
     if eager_states is not None:
-        n = min(args.eager_steps, total_steps)
+        n = min(eager_steps, total_steps)
         for s in range(2):
             for l in range(LAYERS):
-                eager_states[l].prepare_step_capacity(B * WRITES)
+                eager_states[l].prepare_step_capacity(banks * WRITES)
                 cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
                                         validate_routes=False, collect_diagnostics=False)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for s in range(2, n):
             for l in range(LAYERS):
-                eager_states[l].prepare_step_capacity(B * WRITES)
+                eager_states[l].prepare_step_capacity(banks * WRITES)
                 cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
                                         validate_routes=False, collect_diagnostics=False)
         torch.cuda.synchronize()
@@ -247,13 +283,19 @@ def main() -> int:
     # are the per-step bytes times the steps it ran
     launches = p_run["launches"]
     launch_us = 1000.0 * p_run["gpu_ms"] / launches
-    bytes_per_launch = (algorithmic_bytes(B, LAYERS) * K + 8 * new_rows) / launches
+    bytes_per_launch = (algorithmic_bytes(banks, LAYERS) * K + 8 * new_rows) / launches
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     dense_launch_us = 1000.0 * d_run["gpu_ms"] / d_run["launches"]
-    traffic = profiled_traffic(B, args.launch_steps)
+    traffic = profiled_traffic(B, args.launch_steps) if args.config == 2 else None
+    # the persistent variant that ran: full shape (W = 4, R = 16), one scan
+    # window up to 64 banks, slot map in LDS up to 4,096 slots
+    kernel = (f"sdm_trace_kernel<int, 2, false, true, {1 if banks <= 64 else 4}, "
+              f"{'true' if SLOTS <= 4096 else 'false'}>")
 
     result = {
-        "metric": METRIC,
+        "metric": (METRIC if args.config == 2 and B == 64 else
+                   f"decode tokens/s, config {args.config} at batch {B} (L={LAYERS},H={HEADS},"
+                   f"N={SLOTS},D={WIDTH}); achieved HBM GB/s % of peak"),
         "value": round(B * K / p_seconds, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -266,11 +308,12 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": (f"config 2: packed copy-on-write SDM decode, L={LAYERS} H={HEADS} "
-                         f"N={SLOTS} D={WIDTH} top-{WRITES} write / top-{READS} read, "
-                         f"batch {B}, prefix {PREFIX}, growth quantum 4 steps"),
-            "batch": B, "layers": LAYERS, "slots": SLOTS, "width": WIDTH,
-            "writes": WRITES, "reads": READS, "prefix": PREFIX,
+            "workload": (f"config {args.config}: {cfg['text']}; L={LAYERS} H={HEADS} "
+                         f"N={SLOTS} D={WIDTH} top-{WRITES} write / top-{READS} read "
+                         f"({cfg['distribution']}), batch {B}, growth quantum 4 steps"),
+            "batch": B, "heads": HEADS, "banks": banks, "layers": LAYERS, "slots": SLOTS,
+            "width": WIDTH, "writes": WRITES, "reads": READS, "prefix": PREFIX,
+            "distribution": cfg["distribution"],
             "growth_quantum_rows": quantum, "steps_per_launch": args.launch_steps,
             "capacity_proof": f"on the device, every {args.proof_steps} steps per layer",
             "launch": "persistent launches over all layers and banks",
@@ -284,7 +327,7 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": None if traffic is None else traffic["bytes_per_launch"],
             "traffic_source": None if traffic is None else traffic["source"],
-            "kernel": "sdm_trace_kernel<int, 2, false, true, 1, true> (packed, 7 layers x 64 banks)",
+            "kernel": f"{kernel} (packed, {LAYERS} layers x {banks} banks)",
             "launch_us": round(launch_us, 3),
             "steps_per_launch": round(K / launches, 3),
             "us_per_step": round(1000.0 * p_run["gpu_ms"] / K, 4),
@@ -298,6 +341,7 @@ def main() -> int:
             "state_max_abs_diff": state_diff,
         },
         "allocator": {
+            "handoff_ms": None if handoff_ms is None else round(handoff_ms, 3),
             "handoff_live_rows": sum(handoff_rows),
             "handoff_capacity_rows": sum(handoff_capacity),
             "live_rows_after": sum(int(st.allocated_rows_tensor()) for st in states),
@@ -309,7 +353,7 @@ def main() -> int:
         },
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.config == 2:
         result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)
     print(json.dumps(result))
     return 0

@@ -703,8 +703,11 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     }
     for (int k = 0; k < 9; ++k) {
       if (trace->stride_bytes[k] % 4 != 0) return fail(COWSDM_EARG, "trace: stride not float aligned");
-      // every step's rows must keep the vector alignment of step 0
-      while (vec > 1 && (trace->stride_bytes[k] % (4 * vec)) != 0) vec /= 2;
+      // every step's value and output rows (the only vector accesses to
+      // trace inputs) must keep the vector alignment of step 0
+      if (k == 2 || k == 8) {
+        while (vec > 1 && (trace->stride_bytes[k] % (4 * vec)) != 0) vec /= 2;
+      }
     }
   }
   if (steps < 0) return fail(COWSDM_EARG, "steps must be non-negative");

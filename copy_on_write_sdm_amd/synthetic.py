@@ -81,12 +81,12 @@ def make_steps(
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     shape = (steps, layers, banks)
-    if distribution == "uniform":
-        write_keys = torch.rand(*shape, slots, generator=gen, device=device)
-        read_keys = torch.rand(*shape, slots, generator=gen, device=device)
-    elif distribution == "zipf":
-        if banks % heads:
-            raise ValueError("banks must be a multiple of heads")
+    if distribution not in ("uniform", "zipf"):
+        raise ValueError("distribution must be uniform or zipf")
+    if distribution == "zipf" and banks % heads:
+        raise ValueError("banks must be a multiple of heads")
+    logw = None
+    if distribution == "zipf":
         logw = torch.stack([
             torch.stack([
                 zipf_log_weights(slots, zipf_exponent,
@@ -94,17 +94,33 @@ def make_steps(
                 for _ in range(heads)])
             for _ in range(layers)])                    # [L, H, N]
         logw = logw.repeat(1, banks // heads, 1)        # bank = seq * H + h
-        gumbel_w = -torch.log(-torch.log(
-            torch.rand(*shape, slots, generator=gen, device=device).clamp_min(1e-20)))
-        gumbel_r = -torch.log(-torch.log(
-            torch.rand(*shape, slots, generator=gen, device=device).clamp_min(1e-20)))
-        write_keys = logw + gumbel_w
-        read_keys = logw + gumbel_r
+
+    def keys(n: int) -> torch.Tensor:
+        if distribution == "uniform":
+            return torch.rand(n, layers, banks, slots, generator=gen, device=device)
+        gumbel = -torch.log(-torch.log(
+            torch.rand(n, layers, banks, slots, generator=gen, device=device).clamp_min(1e-20)))
+        return logw + gumbel
+
+    # one key per (step, layer, bank, slot); large address spaces draw them a
+    # few steps at a time (the routes then differ from a single draw)
+    per_step = layers * banks * slots
+    chunk = steps if steps * per_step <= (1 << 28) else max(1, (1 << 26) // per_step)
+    if chunk >= steps:
+        write_keys = keys(steps)
+        read_keys = keys(steps)
+        write_indices = _subset(write_keys, writes).to(index_dtype)
+        read_indices = _subset(read_keys, reads).to(index_dtype)
+        del write_keys, read_keys
     else:
-        raise ValueError("distribution must be uniform or zipf")
-    write_indices = _subset(write_keys, writes).to(index_dtype)
-    read_indices = _subset(read_keys, reads).to(index_dtype)
-    del write_keys, read_keys
+        w_parts, r_parts = [], []
+        for s0 in range(0, steps, chunk):
+            n = min(chunk, steps - s0)
+            w_parts.append(_subset(keys(n), writes).to(index_dtype))
+            r_parts.append(_subset(keys(n), reads).to(index_dtype))
+        write_indices = torch.cat(w_parts)
+        read_indices = torch.cat(r_parts)
+        del w_parts, r_parts
     write_weights = torch.softmax(
         torch.randn(*shape, writes, generator=gen, device=device), dim=-1)
     read_weights = torch.softmax(
