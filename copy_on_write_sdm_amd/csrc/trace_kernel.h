@@ -49,12 +49,15 @@ namespace cowsdm_impl {
 
 typedef float vf4_t __attribute__((ext_vector_type(4)));
 
+// A row of zeros, read (never written) by the read lanes past R: with a
+// weight of -0.0 each of their terms is -0.0, which leaves any sum unchanged.
+static __device__ __align__(16) const float kTraceZeroRow[kWave * 4] = {};
+
 template <int VEC>
 struct TraceRows {                  // operands of one step, loaded one step ahead
   float w[kTraceMaxWrites][VEC];    // rows of the write slots, before the decay
   float r[kTraceMaxReads][VEC];     // rows of the read slots, before this step
   float vin[VEC];                   // the step's value
-  float ww, rw;                     // lane j: weight of write j / read j
 };
 
 struct TraceIdx {                   // lane j: write slot j / read slot j
@@ -149,7 +152,9 @@ __device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, u
   return __popcll(b0 & m) + 2 * __popcll(b1 & m) + 4 * __popcll(b2 & m);
 }
 
-// FULL: W == kTraceMaxWrites and R == kTraceMaxReads, every row guard folds away.
+// Every step handles kTraceMaxWrites write rows and kTraceMaxReads read rows
+// without a branch on W or R; FULL (W and R at those maxima) drops the
+// selects and the zero rows that leave the others out.
 // SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
 // MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per wave).
 template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW, bool MAPLDS>
@@ -350,23 +355,23 @@ void sdm_trace_kernel(StepParams P) {
     }
     int wsrc = -1, rsrc = -1, rraw_lane = -1;
     uint64_t dup = 0;
+    // write j's slot, or -1 (no slot) past W: every row runs without a branch
+    auto wslot = [&](int x, int j) __attribute__((always_inline)) -> int {
+      return j < W ? rl(x, j) : -1;
+    };
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) {
-      if (j < W) {
-        const int sj = rl(m.widx, j);
-        // a write lane above j with the same slot
-        dup |= __ballot(m.widx == sj) & wlanes & ~((2ull << j) - 1);
-        if (m.ridx == sj) rraw_lane = j;
-      }
+      const int sj = wslot(m.widx, j);
+      // a write lane above j with the same slot
+      dup |= __ballot(m.widx == sj) & wlanes & ~((2ull << j) - 1);
+      if (m.ridx == sj) rraw_lane = j;
     }
     if (t >= 1) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W) {
-          const int sj = rl(r1.widx, j);
-          if (m.widx == sj) wsrc = j;
-          if (m.ridx == sj) rsrc = j;
-        }
+        const int sj = wslot(r1.widx, j);
+        if (m.widx == sj) wsrc = j;
+        if (m.ridx == sj) rsrc = j;
       }
     }
     if (rraw_lane >= 0) rsrc = -1;
@@ -382,12 +387,10 @@ void sdm_trace_kernel(StepParams P) {
     if (!DENSE && !MAPLDS && t >= 2) {
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W) {
-          const int sj = rl(r2.widx, j);
-          const int row = rl(r2.wrow, j);
-          if (wsrc < 0 && m.widx == sj) wraw = row;
-          if (rsrc < 0 && m.ridx == sj) rraw = row;
-        }
+        const int sj = wslot(r2.widx, j);
+        const int row = rl(r2.wrow, j);
+        if (wsrc < 0 && m.widx == sj) wraw = row;
+        if (rsrc < 0 && m.ridx == sj) rraw = row;
       }
     }
     const bool any_err = (__ballot((m.err | base_err) != 0) | dup | bad) != 0;
@@ -418,7 +421,9 @@ void sdm_trace_kernel(StepParams P) {
     rt.wsrc = lane < W ? wsrc : -1;
     rt.rsrc = lane < R ? rsrc : -1;
     rt.rraw = lane < R ? rraw_lane : -1;
-    return rraw;
+    // past R the lane loads the shared row of slot 0, never a slab row that
+    // the bad-entry check above did not cover
+    return lane < R ? rraw : -1;
   };
 
   auto issue_rows = [&](int t, const TraceRoute& rt, int rrow, TraceRows<VEC>& buf)
@@ -438,9 +443,14 @@ void sdm_trace_kernel(StepParams P) {
       wp = rt.wrow < 0 ? row_at(m0_bank, rt.widx) : row_at(slab, rt.wrow);
       rp = rrow < 0 ? row_at(m0_bank, rt.ridx) : row_at(slab, rrow);
     }
+    if constexpr (!FULL) {
+      if (lane >= R) rp = kTraceZeroRow;
+    }
     // lane j's row pointers through LDS: a broadcast read gives every lane
     // two of them, and each row load takes its own 64-bit vector address (no
-    // scalar base, whose write by a readlane a load could not follow at once)
+    // scalar base, whose write by a readlane a load could not follow at once).
+    // Every row is loaded: write lanes past W point at a row of slot 0, read
+    // lanes past R at the zero row, and the step leaves both out.
     lds_ptrs[wave][0][lane] = reinterpret_cast<uint64_t>(wp);
     lds_ptrs[wave][1][lane] = reinterpret_cast<uint64_t>(rp);
     typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
@@ -448,25 +458,17 @@ void sdm_trace_kernel(StepParams P) {
     const u64x2* const pr = reinterpret_cast<const u64x2*>(&lds_ptrs[wave][1][0]);
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; j += 2) {
-      if (j < W) {
-        const u64x2 two = pw[j / 2];
-        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
-        if (j + 1 < W) gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
-      }
+      const u64x2 two = pw[j / 2];
+      gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
+      gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
     }
 #pragma unroll
     for (int i = 0; i < kTraceMaxReads; i += 2) {
-      if (i < R) {
-        const u64x2 two = pr[i / 2];
-        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
-        if (i + 1 < R) gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
-      }
+      const u64x2 two = pr[i / 2];
+      gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
+      gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
     }
     gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
-    if constexpr (!FULL) {
-      buf.ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-      buf.rw = *(const gfloat*)(at(rw_l, st_rw, tc));
-    }
   };
 
   auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
@@ -501,21 +503,17 @@ void sdm_trace_kernel(StepParams P) {
   }
   bool alive = true;
 
-  // full shape: lane j's write and read weight of step t, loaded two
-  // iterations ahead and handed to LDS at the end of the iteration before
+  // lane j's write and read weight of step t, loaded two iterations ahead and
+  // handed to LDS at the end of the iteration before
   auto load_weights = [&](int t, float& ww, float& rw) __attribute__((always_inline)) {
-    if constexpr (FULL) {
-      const int tc = t < G ? t : G - 1;
-      ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-      rw = *(const gfloat*)(at(rw_l, st_rw, tc));
-    }
+    const int tc = t < G ? t : G - 1;
+    ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+    rw = *(const gfloat*)(at(rw_l, st_rw, tc));
   };
   auto put_weights = [&](float ww, float rw) __attribute__((always_inline)) {
-    if constexpr (FULL) {
-      float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
-      wl[lane] = ww;
-      wl[kWave + lane] = rw;
-    }
+    float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
+    wl[lane] = ww;
+    wl[kWave + lane] = FULL || lane < R ? rw : -0.0f;
   };
 
   // Step t: LDS row j holds write j of step t-1 until this step replaces it.
@@ -526,42 +524,42 @@ void sdm_trace_kernel(StepParams P) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
     if (run) {
+      // fwd and rawm hold bits of lanes below W (R) only
       const uint32_t fwd = rt.fwd;
       if (fwd != 0) {
 #pragma unroll
         for (int j = 0; j < kTraceMaxWrites; ++j) {
-          if (j < W && ((fwd >> j) & 1u)) lds_get(rl(rt.wsrc, j), buf.w[j]);
+          if ((fwd >> j) & 1u) lds_get(rl(rt.wsrc, j), buf.w[j]);
         }
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
-          if (i < R && ((fwd >> (kTraceMaxWrites + i)) & 1u)) lds_get(rl(rt.rsrc, i), buf.r[i]);
+          if ((fwd >> (kTraceMaxWrites + i)) & 1u) lds_get(rl(rt.rsrc, i), buf.r[i]);
         }
       }
-      vf4_t wwv = 0.0f, rwv[kTraceMaxReads / 4];
-      if constexpr (FULL) {
-        // lane j put weight j there in the iteration before: every lane reads
-        // all of them as vectors, instead of a readlane per weight
-        wwv = lds_weights[wave][0][0];
+      // lane j put weight j there in the iteration before: every lane reads
+      // all of them as vectors, instead of a readlane per weight
+      const vf4_t wwv = lds_weights[wave][0][0];
+      vf4_t rwv[kTraceMaxReads / 4];
 #pragma unroll
-        for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
-      }
+      for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
       const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t & (kWave - 1)));
       const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t & (kWave - 1)));
       const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t & (kWave - 1)));
       float ret[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) ret[v] = 0.0f;
+      // rows past W are computed and left out of the sum by a select on the
+      // wave-uniform row count (a decayed row can be infinite or NaN, so no
+      // term of theirs is exactly neutral); rows past R add -0.0
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W) {
-          const float wj = FULL ? wwv[j] : rlf(buf.ww, j);
+        const float wj = wwv[j];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            const float d = buf.w[j][v] * alpha;
-            cur[j][v] = d;
-            const float term = wj * d;
-            ret[v] = (j == 0) ? term : ret[v] + term;
-          }
+        for (int v = 0; v < VEC; ++v) {
+          const float d = buf.w[j][v] * alpha;
+          cur[j][v] = d;
+          const float term = wj * d;
+          ret[v] = (j == 0) ? term : (j < W ? ret[v] + term : ret[v]);
         }
       }
       float delta[VEC];
@@ -573,34 +571,28 @@ void sdm_trace_kernel(StepParams P) {
       }
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W) {
-          const float wj = FULL ? wwv[j] : rlf(buf.ww, j);
+        const float wj = wwv[j];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            const float u = wj * delta[v];
-            cur[j][v] = cur[j][v] + u;
-          }
-          lds_put(j, cur[j]);
+        for (int v = 0; v < VEC; ++v) {
+          const float u = wj * delta[v];
+          cur[j][v] = cur[j][v] + u;
         }
+        lds_put(j, cur[j]);
       }
       const uint32_t rawm = rt.rawm;
       if (rawm != 0) {
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
-          if (i < R && ((rawm >> i) & 1u)) {
-            lds_get(rl(rt.rraw, i), buf.r[i]);
-          }
+          if ((rawm >> i) & 1u) lds_get(rl(rt.rraw, i), buf.r[i]);
         }
       }
 #pragma unroll
       for (int i = 0; i < kTraceMaxReads; ++i) {
-        if (i < R) {
-          const float wr = FULL ? rwv[i / 4][i % 4] : rlf(buf.rw, i);
+        const float wr = rwv[i / 4][i % 4];
 #pragma unroll
-          for (int v = 0; v < VEC; ++v) {
-            const float term = wr * buf.r[i][v];
-            acc[v] = (i == 0) ? term : acc[v] + term;
-          }
+        for (int v = 0; v < VEC; ++v) {
+          const float term = wr * buf.r[i][v];
+          acc[v] = (i == 0) ? term : acc[v] + term;
         }
       }
     }
@@ -609,11 +601,12 @@ void sdm_trace_kernel(StepParams P) {
       const uint32_t r = static_cast<uint32_t>(DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow));
       float* const dst = reinterpret_cast<float*>(
           reinterpret_cast<char*>(DENSE ? table_bank : slab) + static_cast<uint64_t>(r) * row_bytes);
-      const uint32_t fmask = route_fmask(rt.u);
+      // rows in use that are not first touches (those wait for their claims)
+      const uint32_t smask = static_cast<uint32_t>(wlanes) & ~route_fmask(rt.u);
       const uint32_t co = fresh(coff);
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (j < W && !((fmask >> j) & 1u)) {
+        if ((smask >> j) & 1u) {
           float* p = const_cast<float*>(rl_ptr(dst, j));
           gstore_row<VEC>(p, co, cur[j]);
         }
@@ -678,7 +671,7 @@ void sdm_trace_kernel(StepParams P) {
           const uint32_t co = fresh(coff);
 #pragma unroll
           for (int j = 0; j < kTraceMaxWrites; ++j) {
-            if (j < W && ((fmask >> j) & 1u)) {
+            if ((fmask >> j) & 1u) {  // first touches are lanes below W
               float* p = const_cast<float*>(rl_ptr(dst, j));
               gstore_row<VEC>(p, co, cur[j]);
             }
@@ -953,31 +946,27 @@ void sdm_trace_kernel(StepParams P) {
 // back to one launch per step.
 template <typename IDX, bool DENSE, bool MAPLDS>
 bool launch_trace_kernels(const StepParams& P, int blocks, int vec, hipStream_t stream) {
-  // the full-shape variant loads each bank's weights as 16-byte vectors
-  bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads &&
-              P.trace_stride[1] % 16 == 0 && P.trace_stride[7] % 16 == 0;
-  for (int l = 0; l < P.nlayers && full; ++l) {
-    if ((reinterpret_cast<uintptr_t>(P.layer[l].write_weights) |
-         reinterpret_cast<uintptr_t>(P.layer[l].read_weights)) % 16 != 0) {
-      full = false;
-    }
-  }
-  // one scan window when a layer has at most 64 banks (full shape only)
+  // the full shape folds every row count; other shapes select per row
+  const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
+  // one scan window when a packed layer has at most 64 banks
   constexpr int kScan1 = DENSE ? kTraceScanWindows : 1;
-  const int variant = !full ? 0 : (!DENSE && P.banks <= kWave ? 2 : 1);
-  const void* kernels[3][3] = {
+  const int variant = (full ? 1 : 0) + (!DENSE && P.banks <= kWave ? 2 : 0);
+  const void* kernels[4][3] = {
       {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kTraceScanWindows, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kTraceScanWindows, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kTraceScanWindows, MAPLDS>)},
       {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kTraceScanWindows, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kTraceScanWindows, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kTraceScanWindows, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kScan1, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kScan1, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kScan1, MAPLDS>)},
       {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kScan1, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kScan1, MAPLDS>),
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kScan1, MAPLDS>)}};
   // residency depends on the LDS map's size: cached per kernel and slot count
-  static int resident[3][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
-  static int resident_slots[3][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
+  static int resident[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
+  static int resident_slots[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
   const size_t lds_bytes = MAPLDS ? sizeof(int) * kBanksPerBlock * static_cast<size_t>(P.slots) : 0;

@@ -125,6 +125,40 @@ def test_persistent_trace_matches_oracle(device):
     assert_state_equal(traced[0], oracle, permuted=True)
 
 
+@pytest.mark.parametrize("writes,reads,zero_values", [
+    (2, 5, False), (2, 5, True), (3, 16, True), (4, 16, True)])
+def test_signed_zero_sums_match_oracle_bits(device, writes, reads, zero_values):
+    """Zero memory and negative weights: every term of a reading of an
+    untouched slot (and, with zero values, of every reading) is -0.0, so the
+    reading is -0.0.  Rows past W and R that a shape leaves out must not turn
+    such a sum into +0.0.  Compared as bit patterns: torch.equal and
+    np.array_equal hold -0.0 == +0.0."""
+
+    banks, slots, width, steps = 6, 64, 128, 12
+    print(f"signed zeros W={writes} R={reads} zero_values={zero_values}", flush=True)
+    m0, routes, states, kw = _setup(device, layers=1, banks=banks, slots=slots, width=width,
+                                    writes=writes, reads=reads, steps=steps, seed=41)
+    m0.zero_()
+    routes.read_weights.copy_(-routes.read_weights.abs() - 0.01)
+    routes.write_weights.copy_(-routes.write_weights.abs() - 0.01)
+    if zero_values:
+        routes.values.zero_()
+    traced, single = states(), states()
+    outputs = torch.empty(steps, 1, banks, width, device=device)
+    cow.DecodeTrace(states=traced, outputs=outputs, max_steps_per_launch=steps,
+                    **kw).launch(steps, start=0)
+    want = _per_step(single, routes, steps, 1)
+    bits = outputs.view(torch.int32)
+    assert torch.equal(bits, want.view(torch.int32))
+    assert (bits == -2 ** 31).any()
+    oracle = ref.allocate(m0[0].cpu().numpy(), banks=banks, capacity_rows=banks * slots)
+    oracle.capacity_is_proven = True
+    for s in range(steps):
+        x = {k: v.cpu().numpy() for k, v in routes.step(s, 0).items()}
+        got, _ = ref.packed_step(oracle, **x, validate_routes=False)
+        assert np.array_equal(bits[s, 0].cpu().numpy(), got.view(np.int32)), f"step {s}"
+
+
 @pytest.mark.parametrize("slots,reads,lag,index_dtype", [
     (48, 12, 1, torch.int32),
     (48, 12, 1, torch.int64),
