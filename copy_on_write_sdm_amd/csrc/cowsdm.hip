@@ -47,11 +47,11 @@ extern template void launch_step_w<int32_t, true>(const StepParams&, int, int, h
 extern template void launch_step_w<int64_t, false>(const StepParams&, int, int, hipStream_t);
 extern template void launch_step_w<int64_t, true>(const StepParams&, int, int, hipStream_t);
 template <typename IDX, bool DENSE>
-bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream);
-extern template bool launch_trace<int32_t, false>(const StepParams&, int, int, hipStream_t);
-extern template bool launch_trace<int32_t, true>(const StepParams&, int, int, hipStream_t);
-extern template bool launch_trace<int64_t, false>(const StepParams&, int, int, hipStream_t);
-extern template bool launch_trace<int64_t, true>(const StepParams&, int, int, hipStream_t);
+bool launch_trace(const StepParams& P, int vec, hipStream_t stream);
+extern template bool launch_trace<int32_t, false>(const StepParams&, int, hipStream_t);
+extern template bool launch_trace<int32_t, true>(const StepParams&, int, hipStream_t);
+extern template bool launch_trace<int64_t, false>(const StepParams&, int, hipStream_t);
+extern template bool launch_trace<int64_t, true>(const StepParams&, int, hipStream_t);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -772,11 +772,11 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
         P.steps = (steps - done) < kTraceMaxSteps ? (steps - done) : kTraceMaxSteps;
         P.trace_first = trace->first_step + done;  // ignored when step_index is set
         if (dense) {
-          launched = i64 ? launch_trace<int64_t, true>(P, blocks, trace_vec, stream)
-                         : launch_trace<int32_t, true>(P, blocks, trace_vec, stream);
+          launched = i64 ? launch_trace<int64_t, true>(P, trace_vec, stream)
+                         : launch_trace<int32_t, true>(P, trace_vec, stream);
         } else {
-          launched = i64 ? launch_trace<int64_t, false>(P, blocks, trace_vec, stream)
-                         : launch_trace<int32_t, false>(P, blocks, trace_vec, stream);
+          launched = i64 ? launch_trace<int64_t, false>(P, trace_vec, stream)
+                         : launch_trace<int32_t, false>(P, trace_vec, stream);
         }
         if (!launched && done > 0) {
           return fail(COWSDM_ELIMIT, "trace launch stopped after %d steps", done);

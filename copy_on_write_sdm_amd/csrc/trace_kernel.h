@@ -4,43 +4,48 @@
 // touches may be assigned in another order, as in the reference's proven
 // kernel, whose banks pop with an atomic add).
 //
-// Each wave owns one (layer, bank) for all G steps and software-pipelines
-// them so that every memory access has about one iteration to land before
-// its value is used.  Iteration s
-//   1. loads the slots of step s+2 (s+3 when the slot map stays in global
-//      memory, whose entries for step s+2 are loaded too);
-//   2. classifies step s+1 (first touches, slots written by steps s and s-1,
-//      read-after-write), claims rows for its first touches and loads its
-//      rows;
-//   3. computes step s (gated-delta update, sparse read) from rows loaded one
-//      iteration earlier; stores its reading and the rows already private;
-//   4. takes the rows claimed for step s's first touches and stores them and
-//      their map entries.
-// Step t's map entries are read before steps t-2 and t-1 have stored their
-// first touches: slots written at t-1 take their rows from that step's
-// result, kept in LDS, and slots written at t-2 take the physical rows popped
-// for them.  Every other row step t needs was stored earlier by the same
-// wave, in program order.  When a bank's map fits (N <= kTraceMapSlots), the
-// wave keeps it in LDS for the launch (it is the only writer of its bank's
-// entries) and reads step t+1's entries there in iteration t, after step
-// t-1's pops: only the slots of step t still need their rows forwarded, and
-// the global map is written alongside.  Values in flight live in even/odd
-// homes (the loop is unrolled by two) and are only read one iteration after
-// their load was issued, so no register copy waits on memory; per-row values
-// picked by run-time lanes are read from LDS, never selected out of registers.
+// Each (layer, bank) has two waves in one workgroup, which hand steps over
+// through a ring of kTraceRing slots in LDS:
+//
+//   the control wave loads the step's slots and map entries, classifies the
+//   step (first touches, slots written by the step before, read-after-write),
+//   claims rows for its first touches, and publishes the addresses of the
+//   rows the step loads; one step later it takes the claimed rows, stores
+//   them in the map and publishes the rows the step's updates are stored to
+//   and the step's masks;
+//
+//   the data wave loads the rows of step s+1 from the published addresses
+//   while it computes step s (gated-delta update, sparse read) from rows
+//   loaded one iteration earlier, stores the reading and the updated rows,
+//   and keeps the updated rows in LDS for the step after.
+//
+// Only the data wave reads or writes rows, in program order: a step's rows
+// were stored by earlier steps of the same wave, except the rows of the step
+// just before, which it takes from LDS.  The control wave runs up to
+// kTraceRing - 1 steps ahead, so the atomics and map lookups it waits on stay
+// off the data wave's path.  Step t's map entries are read before steps t-2
+// and t-1 have stored their first touches: slots written at t-1 take their
+// rows from that step's result, and slots written at t-2 take the physical
+// rows popped for them.  When a bank's map fits (N <= kTraceMapSlots), the
+// control wave keeps it in LDS for the launch (it is the only writer of its
+// bank's entries) and reads step t+1's entries there after step t-1's pops:
+// only the slots of step t still need their rows forwarded, and the global
+// map is written alongside.  Values in flight live in even/odd homes (both
+// loops are unrolled by two) and are only read one iteration after their
+// load was issued, so no register copy waits on memory.
 //
 // Rows: free_count stays F (its value at launch) until the launch ends.  A
 // (step, bank) with c first touches adds c to the layer's claim counter and
 // gets p, the rows claimed before it; its first touches take
 // free_rows[F - 1 - p - rank], and the step fits if p + c <= F.  Claims only
 // grow, so once one fails every later one fails too, and the claims that fit
-// are exactly the top of the free stack.  The layer's last wave to finish
-// writes free_count = F - (claims that fit) and clears the counter.  Waves
-// do not otherwise wait on one another, except for the capacity proof: with
-// proofs on, each bank publishes its first touches so far at the end of each
-// run of proof steps, and every wave sums them before the next run starts, so
-// all banks of the layer stop at the same step.  The claims of a run's first
-// step wait for that proof.
+// are exactly the top of the free stack.  The layer's last control wave to
+// finish writes free_count = F - (claims that fit) and clears the counter.
+// Banks do not otherwise wait on one another, except for the capacity proof:
+// with proofs on, each bank publishes its first touches so far at the end of
+// each run of proof steps, and every control wave sums them before the next
+// run starts, so all banks of the layer stop at the same step.  The claims
+// of a run's first step wait for that proof.
 #pragma once
 
 #include "common.h"
@@ -48,6 +53,9 @@
 namespace cowsdm_impl {
 
 typedef float vf4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef uint64_t u64x2_t __attribute__((ext_vector_type(2)));
 
 // A row of zeros, read (never written) by the read lanes past R: with a
 // weight of -0.0 each of their terms is -0.0, which leaves any sum unchanged.
@@ -80,6 +88,20 @@ struct TraceRoute {                 // a classified step
 __device__ __forceinline__ uint32_t route_fmask(uint32_t u) { return u & 15u; }
 __device__ __forceinline__ int route_count(uint32_t u) { return static_cast<int>((u >> 4) & 15u); }
 __device__ __forceinline__ bool route_ok(uint32_t u) { return (u >> 8) & 1u; }
+
+// One step handed from the control wave to the data wave.
+struct TraceSlot {
+  uint64_t wptr[kTraceMaxWrites];   // address of write j's row before the step
+  uint64_t rptr[kTraceMaxReads];    // address of read i's row (a zero row past R)
+  int32_t drow[kTraceMaxWrites];    // row write j's update is stored to
+  // ctl[0]: bits 0-19 rows forwarded from the step before (0-3 writes, 4-19
+  //         reads), bit 20 the step runs, bits 24-27 write rows to store;
+  // ctl[1]: bits 0-15 reads of the step's own writes, bits 16-19 and 20-23
+  //         the low and high bits of each forwarded write's source row;
+  // ctl[2]: bits 0-15 and 16-31, the same for forwarded reads;
+  // ctl[3]: the same for reads of the step's own writes.
+  uint32_t ctl[4];
+};
 
 typedef __attribute__((address_space(1))) float gfloat;
 typedef float vf2 __attribute__((ext_vector_type(2)));
@@ -119,13 +141,6 @@ __device__ __forceinline__ void gstore_row(float* base, uint32_t off, const floa
   }
 }
 
-__device__ __forceinline__ const float* rl_ptr(const float* p, int lane) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), lane);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), lane);
-  return reinterpret_cast<const float*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
@@ -147,36 +162,54 @@ __device__ __forceinline__ uint32_t fresh(uint32_t x) {
   return x;
 }
 
-// Weighted population count of per-lane values 0..7 held as three bit masks.
-__device__ __forceinline__ int64_t sum3(uint64_t b0, uint64_t b1, uint64_t b2, uint64_t m) {
-  return __popcll(b0 & m) + 2 * __popcll(b1 & m) + 4 * __popcll(b2 & m);
+// Hand-over words between the two waves of a bank (LDS, workgroup scope):
+// a release store orders the ring writes before it, an acquire load the
+// ring reads after it.
+__device__ __forceinline__ uint32_t sync_load(uint32_t* p) {
+  return __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
+__device__ __forceinline__ void sync_store(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Source row (0..3) of entry i from two bit planes of a control word.
+__device__ __forceinline__ int plane_code(uint32_t w, int lo, int hi) {
+  return static_cast<int>(((w >> lo) & 1u) | (((w >> hi) & 1u) << 1));
 }
 
 // Every step handles kTraceMaxWrites write rows and kTraceMaxReads read rows
 // without a branch on W or R; FULL (W and R at those maxima) drops the
 // selects and the zero rows that leave the others out.
 // SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
-// MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per wave).
+// MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per bank).
 template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW, bool MAPLDS>
-__global__ __launch_bounds__(kStepThreads)
+__global__ __launch_bounds__(kTraceThreads)
 __attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
 void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
-  __shared__ float lds_rows[kBanksPerBlock][kTraceMaxWrites][kRow];
-  // full shape: the next step's weights, written per lane at the end of an
+  constexpr int NB = kTraceBanksPerBlock;
+  constexpr uint32_t kNoStop = 0xFFFFu;
+  // data wave: the last computed step's updated rows
+  __shared__ float lds_rows[NB][kTraceMaxWrites][kRow];
+  // data wave: the next step's weights, written per lane at the end of an
   // iteration, read back as broadcasts by the step's compute
-  __shared__ vf4_t lds_weights[kBanksPerBlock][2][kWave / 4];
+  __shared__ vf4_t lds_weights[NB][2][kWave / 4];
   __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
-  // each step's row addresses, lane j's write row and read row, read back
-  // by every lane as broadcasts
-  __shared__ uint64_t lds_ptrs[kBanksPerBlock][2][kWave];
+  __shared__ TraceSlot lds_ring[NB][kTraceRing];
+  // [0]: control -> data, (stop step << 16) | steps whose row addresses are
+  // published (the masks and store rows of all but the last of them);
+  // [1]: data -> control, steps computed
+  __shared__ uint32_t lds_sync[NB][2];
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+  const int pair = wave >> 1;
+  const bool data_wave = (wave & 1) != 0;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int layer_id = blockIdx.x / P.blocks_per_layer;
   if (layer_id >= P.nlayers) return;  // whole workgroup
-  const int bank = (blockIdx.x % P.blocks_per_layer) * kBanksPerBlock + wave;
+  const int bank = (blockIdx.x % P.blocks_per_layer) * NB + pair;
   const cowsdm_layer_t& L = P.layer[layer_id];
   // Device-counted launches read the layer's first step from its counter
   // (every thread reads the same value: it changes only after all waves of
@@ -230,12 +263,348 @@ void sdm_trace_kernel(StepParams P) {
     } else {
       window = old_free < kTraceFreeWindow ? old_free : kTraceFreeWindow;
     }
-    for (int k = static_cast<int>(threadIdx.x); k < window; k += kStepThreads) {
+    for (int k = static_cast<int>(threadIdx.x); k < window; k += kTraceThreads) {
       lds_free[k] = L.free_rows[old_free - 1 - k];
     }
-    __syncthreads();
   }
-  if (bank >= B) return;
+  if (lane == 0 && !data_wave) {
+    lds_sync[pair][0] = kNoStop << 16;
+    lds_sync[pair][1] = 0;
+  }
+  __syncthreads();
+  if (bank >= B) return;  // both waves of the bank
+
+  uint32_t* const sync = lds_sync[pair];
+  TraceSlot* const ring = lds_ring[pair];
+  auto slot_of = [&](int t) __attribute__((always_inline)) -> TraceSlot& {
+    return ring[static_cast<uint32_t>(t) % kTraceRing];
+  };
+  const uint64_t wlanes = W >= kWave ? ~0ull : ((1ull << W) - 1);
+  const uint64_t rlanes = R >= kWave ? ~0ull : ((1ull << R) - 1);
+  float* const slab = DENSE ? nullptr : pin(L.values);
+  float* const table_bank = DENSE ? L.values + static_cast<int64_t>(bank) * N * D : nullptr;
+  auto first_step = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
+    return static_cast<const char*>(base) + first * P.trace_stride[k];
+  };
+  auto at = [](const char* p, uint32_t stride, int t) __attribute__((always_inline)) -> const char* {
+    return p + static_cast<uint64_t>(static_cast<uint32_t>(t)) * stride;
+  };
+  const int wl = lane < W ? lane : 0;
+  const int rl_ = lane < R ? lane : 0;
+
+  if (data_wave) {
+    // ======================= data wave =======================
+    float* const lds_wave = &lds_rows[pair][0][0];
+    float* const store_base = DENSE ? table_bank : slab;
+    const char* const ww_l = first_step(L.write_weights, 1) + (static_cast<int64_t>(bank) * W + wl) * 4;
+    const char* const v_l = first_step(L.step_values, 2) + (static_cast<int64_t>(bank) * D + col) * 4;
+    const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
+    const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
+    const uint32_t st_ww = pin(static_cast<uint32_t>(P.trace_stride[1]));
+    const uint32_t st_v = pin(static_cast<uint32_t>(P.trace_stride[2]));
+    const uint32_t st_rw = pin(static_cast<uint32_t>(P.trace_stride[7]));
+    const uint32_t st_out = pin(static_cast<uint32_t>(P.trace_stride[8]));
+
+    // gates in chunks of 64 steps, lane k holding step 64c + k of chunk c;
+    // the next chunk is loaded one chunk ahead
+    auto load_gates = [&](int c, float& fg, float& ig, float& eg) __attribute__((always_inline)) {
+      const int t = c * kWave + lane;
+      fg = 0.0f;
+      ig = 0.0f;
+      eg = 0.0f;
+      if (t < G) {
+        fg = reinterpret_cast<const float*>(first_step(L.forget_log_gate, 5) +
+                                            static_cast<int64_t>(t) * P.trace_stride[5])[bank];
+        ig = reinterpret_cast<const float*>(first_step(L.input_gate, 3) +
+                                            static_cast<int64_t>(t) * P.trace_stride[3])[bank];
+        eg = reinterpret_cast<const float*>(first_step(L.erase_gate, 4) +
+                                            static_cast<int64_t>(t) * P.trace_stride[4])[bank];
+      }
+    };
+    float alpha_l, in_l, er_l, fg_n, in_n, er_n;
+    {
+      float fg0;
+      load_gates(0, fg0, in_l, er_l);
+      alpha_l = static_cast<float>(exp(static_cast<double>(fg0)));
+      load_gates(1, fg_n, in_n, er_n);
+    }
+    // before step s (s even): the step's chunk in the lane registers
+    auto gates_for = [&](int s) __attribute__((always_inline)) {
+      if (s > 0 && (s & (kWave - 1)) == 0) {
+        alpha_l = static_cast<float>(exp(static_cast<double>(fg_n)));
+        in_l = in_n;
+        er_l = er_n;
+        if (s + kWave < G) load_gates(s / kWave + 1, fg_n, in_n, er_n);
+      }
+    };
+
+    // lane j's write and read weight of step t, loaded two iterations ahead
+    // and handed to LDS at the end of the iteration before
+    auto load_weights = [&](int t, float& ww, float& rw) __attribute__((always_inline)) {
+      const int tc = t < G ? t : G - 1;
+      ww = *(const gfloat*)(at(ww_l, st_ww, tc));
+      rw = *(const gfloat*)(at(rw_l, st_rw, tc));
+    };
+    auto put_weights = [&](float ww, float rw) __attribute__((always_inline)) {
+      float* const wv = reinterpret_cast<float*>(&lds_weights[pair][0][0]);
+      wv[lane] = ww;
+      wv[kWave + lane] = FULL || lane < R ? rw : -0.0f;
+    };
+
+    // Step t's rows from the addresses the control wave published: a
+    // broadcast read gives every lane two of them, and each row load takes
+    // its own 64-bit vector address (no scalar base, whose write by a
+    // readlane a load could not follow at once).  Every row is loaded: write
+    // lanes past W point at a row of slot 0, read lanes past R at the zero
+    // row, and the step leaves both out.
+    auto issue_rows = [&](int t, TraceRows<VEC>& buf) __attribute__((always_inline)) {
+      const int tc = t < G ? t : G - 1;
+      const TraceSlot& sl = slot_of(t);
+      const u64x2_t* const pw = reinterpret_cast<const u64x2_t*>(sl.wptr);
+      const u64x2_t* const pr = reinterpret_cast<const u64x2_t*>(sl.rptr);
+#pragma unroll
+      for (int j = 0; j < kTraceMaxWrites; j += 2) {
+        const u64x2_t two = pw[j / 2];
+        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
+        gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
+      }
+#pragma unroll
+      for (int i = 0; i < kTraceMaxReads; i += 2) {
+        const u64x2_t two = pr[i / 2];
+        gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
+        gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
+      }
+      gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
+    };
+
+    auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
+      const float* p = lds_wave + row * kRow + col;
+      if constexpr (VEC == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+      } else if constexpr (VEC == 2) {
+        const float2 t = *reinterpret_cast<const float2*>(p);
+        x[0] = t.x; x[1] = t.y;
+      } else {
+        x[0] = *p;
+      }
+    };
+    auto lds_put = [&](int row, const float (&x)[VEC]) __attribute__((always_inline)) {
+      float* p = lds_wave + row * kRow + col;
+      if constexpr (VEC == 4) {
+        *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+      } else if constexpr (VEC == 2) {
+        *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+      } else {
+        *p = x[0];
+      }
+    };
+
+    // updated rows of the last computed step
+    float cur[kTraceMaxWrites][VEC];
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
+    }
+
+    // Step t: LDS row j holds write j of step t-1 until this step replaces it.
+    auto compute = [&](int t, const u32x4_t& cw, const i32x4_t& dr, TraceRows<VEC>& buf)
+        __attribute__((always_inline)) {
+      const uint32_t c0 = __builtin_amdgcn_readfirstlane(cw.x);
+      const bool run = ((c0 >> 20) & 1u) != 0;
+      float acc[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+      if (run) {
+        const uint32_t c1 = __builtin_amdgcn_readfirstlane(cw.y);
+        const uint32_t fwd = c0 & 0xFFFFFu;
+        if (fwd != 0) {
+          const uint32_t c2 = __builtin_amdgcn_readfirstlane(cw.z);
+#pragma unroll
+          for (int j = 0; j < kTraceMaxWrites; ++j) {
+            if ((fwd >> j) & 1u) lds_get(plane_code(c1, 16 + j, 20 + j), buf.w[j]);
+          }
+#pragma unroll
+          for (int i = 0; i < kTraceMaxReads; ++i) {
+            if ((fwd >> (kTraceMaxWrites + i)) & 1u) lds_get(plane_code(c2, i, 16 + i), buf.r[i]);
+          }
+        }
+        // lane j put weight j there in the iteration before: every lane reads
+        // all of them as vectors, instead of a readlane per weight
+        const vf4_t wwv = lds_weights[pair][0][0];
+        vf4_t rwv[kTraceMaxReads / 4];
+#pragma unroll
+        for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[pair][1][k];
+        const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t & (kWave - 1)));
+        const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t & (kWave - 1)));
+        const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t & (kWave - 1)));
+        float ret[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) ret[v] = 0.0f;
+        // rows past W are computed and left out of the sum by a select on the
+        // wave-uniform row count (a decayed row can be infinite or NaN, so no
+        // term of theirs is exactly neutral); rows past R add -0.0
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          const float wj = wwv[j];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float d = buf.w[j][v] * alpha;
+            cur[j][v] = d;
+            const float term = wj * d;
+            ret[v] = (j == 0) ? term : (j < W ? ret[v] + term : ret[v]);
+          }
+        }
+        float delta[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          const float a = in_gate * buf.vin[v];
+          const float e = er_gate * ret[v];
+          delta[v] = a - e;
+        }
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          const float wj = wwv[j];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float u = wj * delta[v];
+            cur[j][v] = cur[j][v] + u;
+          }
+          lds_put(j, cur[j]);
+        }
+        const uint32_t rawm = c1 & 0xFFFFu;
+        if (rawm != 0) {
+          const uint32_t c3 = __builtin_amdgcn_readfirstlane(cw.w);
+#pragma unroll
+          for (int i = 0; i < kTraceMaxReads; ++i) {
+            if ((rawm >> i) & 1u) lds_get(plane_code(c3, i, 16 + i), buf.r[i]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kTraceMaxReads; ++i) {
+          const float wr = rwv[i / 4][i % 4];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) {
+            const float term = wr * buf.r[i][v];
+            acc[v] = (i == 0) ? term : acc[v] + term;
+          }
+        }
+      }
+      gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), 0u, acc);
+      if (run) {
+        const uint32_t smask = (c0 >> 24) & 15u;
+        const uint32_t co = fresh(coff);
+        const int32_t rows[kTraceMaxWrites] = {dr.x, dr.y, dr.z, dr.w};
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          if ((smask >> j) & 1u) {
+            const uint32_t r = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(rows[j]));
+            float* const dst = reinterpret_cast<float*>(reinterpret_cast<char*>(store_base) +
+                                                        static_cast<uint64_t>(r) * row_bytes);
+            gstore_row<VEC>(dst, co, cur[j]);
+          }
+        }
+      }
+    };
+
+    // the control wave has published `need` steps' row addresses (and the
+    // masks of all but the last); false if it never does
+    uint32_t seen = 0, stop = kNoStop;
+    auto await = [&](uint32_t need) __attribute__((always_inline)) -> bool {
+      if (seen >= need) return true;
+      for (int spins = 0; spins < 4 * kSpinLimit; ++spins) {
+        const uint32_t w = sync_load(&sync[0]);
+        seen = w & 0xFFFFu;
+        stop = w >> 16;
+        if (seen >= need) return true;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      return false;
+    };
+
+    TraceRows<VEC> bufA, bufB;
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) { bufA.w[j][v] = 0.0f; bufB.w[j][v] = 0.0f; }
+    }
+#pragma unroll
+    for (int i = 0; i < kTraceMaxReads; ++i) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) { bufA.r[i][v] = 0.0f; bufB.r[i][v] = 0.0f; }
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) { bufA.vin[v] = 0.0f; bufB.vin[v] = 0.0f; }
+    float wwA = 0.0f, rwA = 0.0f, wwB = 0.0f, rwB = 0.0f;  // weights in flight
+    {
+      float ww0 = 0.0f, rw0 = 0.0f;
+      load_weights(0, ww0, rw0);
+      put_weights(ww0, rw0);
+      load_weights(1, wwB, rwB);     // handed over at the end of iteration 0
+    }
+
+    // Iteration t: loads step t+1's rows, computes step t.
+    auto iteration = [&](int t, TraceRows<VEC>& rows_t, TraceRows<VEC>& rows_next,
+                         float& ww_self, float& rw_self, float ww_other, float rw_other)
+        __attribute__((always_inline)) {
+      load_weights(t + 2, ww_self, rw_self);
+      const TraceSlot& sl = slot_of(t);
+      const u32x4_t cw = *reinterpret_cast<const u32x4_t*>(sl.ctl);
+      const i32x4_t dr = *reinterpret_cast<const i32x4_t*>(sl.drow);
+      issue_rows(t + 1, rows_next);
+      compute(t, cw, dr, rows_t);
+      put_weights(ww_other, rw_other);   // step t+1's
+      if (lane == 0) sync_store(&sync[1], static_cast<uint32_t>(t + 1));
+    };
+
+    bool go = await(1);
+    bool lost = !go;
+    if (go) issue_rows(0, bufA);
+    // Drain the prologue's loads: the loop head then has one state of loads
+    // in flight (the back edge's), and the waits the compiler places there
+    // stay as loose as the steady state allows.
+    __builtin_amdgcn_s_waitcnt(0);
+    // Pairs of steps, then an odd last step; the control wave stops only
+    // before an even step (capacity proofs come in even runs) or the last,
+    // so the loop's only exit is at its head.
+    int s = 0;
+    for (; go && s + 1 < G; s += 2) {
+      if (!await(static_cast<uint32_t>(s + 3))) {
+        lost = true;
+        go = false;
+        break;
+      }
+      if (static_cast<uint32_t>(s) >= stop) {
+        go = false;
+        break;
+      }
+      gates_for(s);
+      iteration(s, bufA, bufB, wwA, rwA, wwB, rwB);
+      iteration(s + 1, bufB, bufA, wwB, rwB, wwA, rwA);
+    }
+    if (go && s < G) {
+      if (!await(static_cast<uint32_t>(s + 2))) {
+        lost = true;
+      } else if (static_cast<uint32_t>(s) < stop) {
+        gates_for(s);
+        iteration(s, bufA, bufB, wwA, rwA, wwB, rwB);
+      }
+    }
+    if (lost && lane == 0) {
+      // the control wave never published (a bounded wait): record it, and
+      // never hold the control wave back
+      if constexpr (!DENSE) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      sync_store(&sync[1], kNoStop);
+    }
+    return;
+  }
+
+  // ======================= control wave =======================
   int64_t tmpl = 0;
   uint32_t epoch = 0;
   if constexpr (!DENSE) {
@@ -249,69 +618,17 @@ void sdm_trace_kernel(StepParams P) {
   }
   const float* const m0_bank =
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
-  float* const table_bank = DENSE ? L.values + static_cast<int64_t>(bank) * N * D : nullptr;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
-  float* const lds_wave = &lds_rows[wave][0][0];
-  int* const lds_map = MAPLDS ? lds_map_all + wave * N : nullptr;
+  int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
   if constexpr (MAPLDS) {
     for (int k = lane; k < N; k += kWave) lds_map[k] = map_bank[k];
   }
 
-  // ---- this lane's inputs at the launch's first step; step t adds t * stride
-  const int wl = lane < W ? lane : 0;
-  const int rl_ = lane < R ? lane : 0;
-  auto first_step = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
-    return static_cast<const char*>(base) + first * P.trace_stride[k];
-  };
+  // ---- this lane's slots at the launch's first step; step t adds t * stride
   const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
-  const char* const ww_l = first_step(L.write_weights, 1) + (static_cast<int64_t>(bank) * W + wl) * 4;
-  const char* const v_l = first_step(L.step_values, 2) + (static_cast<int64_t>(bank) * D + col) * 4;
   const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
-  const char* const rw_l = first_step(L.read_weights, 7) + (static_cast<int64_t>(bank) * R + rl_) * 4;
-  const char* const out_l = first_step(L.output, 8) + (static_cast<int64_t>(bank) * D + col) * 4;
   const uint32_t st_wi = pin(static_cast<uint32_t>(P.trace_stride[0]));
-  const uint32_t st_ww = pin(static_cast<uint32_t>(P.trace_stride[1]));
-  const uint32_t st_v = pin(static_cast<uint32_t>(P.trace_stride[2]));
   const uint32_t st_ri = pin(static_cast<uint32_t>(P.trace_stride[6]));
-  const uint32_t st_rw = pin(static_cast<uint32_t>(P.trace_stride[7]));
-  const uint32_t st_out = pin(static_cast<uint32_t>(P.trace_stride[8]));
-  float* const slab = DENSE ? nullptr : pin(L.values);
-  auto at = [](const char* p, uint32_t stride, int t) __attribute__((always_inline)) -> const char* {
-    return p + static_cast<uint64_t>(static_cast<uint32_t>(t)) * stride;
-  };
-
-  // ---- gates in chunks of 64 steps, lane k holding step 64c + k of chunk c;
-  // the next chunk is loaded one chunk ahead
-  auto load_gates = [&](int c, float& fg, float& ig, float& eg) __attribute__((always_inline)) {
-    const int t = c * kWave + lane;
-    fg = 0.0f;
-    ig = 0.0f;
-    eg = 0.0f;
-    if (t < G) {
-      fg = reinterpret_cast<const float*>(first_step(L.forget_log_gate, 5) +
-                                          static_cast<int64_t>(t) * P.trace_stride[5])[bank];
-      ig = reinterpret_cast<const float*>(first_step(L.input_gate, 3) +
-                                          static_cast<int64_t>(t) * P.trace_stride[3])[bank];
-      eg = reinterpret_cast<const float*>(first_step(L.erase_gate, 4) +
-                                          static_cast<int64_t>(t) * P.trace_stride[4])[bank];
-    }
-  };
-  float alpha_l, in_l, er_l, fg_n, in_n, er_n;
-  {
-    float fg0;
-    load_gates(0, fg0, in_l, er_l);
-    alpha_l = static_cast<float>(exp(static_cast<double>(fg0)));
-    load_gates(1, fg_n, in_n, er_n);
-  }
-  // before step s (s even): the step's chunk in the lane registers
-  auto gates_for = [&](int s) __attribute__((always_inline)) {
-    if (s > 0 && (s & (kWave - 1)) == 0) {
-      alpha_l = static_cast<float>(exp(static_cast<double>(fg_n)));
-      in_l = in_n;
-      er_l = er_n;
-      if (s + kWave < G) load_gates(s / kWave + 1, fg_n, in_n, er_n);
-    }
-  };
 
   // ---- stages
   auto load_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
@@ -342,8 +659,6 @@ void sdm_trace_kernel(StepParams P) {
   // step t-2 (its first touches popped).  Returns the read lane's row.
   // Lanes past W (R) hold slot 0 as their write (read) slot: they compute
   // along, and their results are masked once at the end.
-  const uint64_t wlanes = W >= kWave ? ~0ull : ((1ull << W) - 1);
-  const uint64_t rlanes = R >= kWave ? ~0ull : ((1ull << R) - 1);
   auto classify = [&](int t, const TraceIdx& m, int wraw, int rraw, TraceRoute& rt,
                       const TraceRoute& r1, const TraceRoute& r2, bool ok_prev)
       __attribute__((always_inline)) -> int {
@@ -421,14 +736,13 @@ void sdm_trace_kernel(StepParams P) {
     rt.wsrc = lane < W ? wsrc : -1;
     rt.rsrc = lane < R ? rsrc : -1;
     rt.rraw = lane < R ? rraw_lane : -1;
-    // past R the lane loads the shared row of slot 0, never a slab row that
-    // the bad-entry check above did not cover
+    // past R the lane loads the zero row, never a slab row that the
+    // bad-entry check above did not cover
     return lane < R ? rraw : -1;
   };
 
-  auto issue_rows = [&](int t, const TraceRoute& rt, int rrow, TraceRows<VEC>& buf)
-      __attribute__((always_inline)) {
-    const int tc = t < G ? t : G - 1;
+  // Publish step t's row addresses: lane j's write row and read row.
+  auto publish_rows = [&](int t, const TraceRoute& rt, int rrow) __attribute__((always_inline)) {
     // row r of a base: base + r * D floats, r non-negative
     auto row_at = [&](const float* base, int r) __attribute__((always_inline)) -> const float* {
       return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) +
@@ -446,177 +760,39 @@ void sdm_trace_kernel(StepParams P) {
     if constexpr (!FULL) {
       if (lane >= R) rp = kTraceZeroRow;
     }
-    // lane j's row pointers through LDS: a broadcast read gives every lane
-    // two of them, and each row load takes its own 64-bit vector address (no
-    // scalar base, whose write by a readlane a load could not follow at once).
-    // Every row is loaded: write lanes past W point at a row of slot 0, read
-    // lanes past R at the zero row, and the step leaves both out.
-    lds_ptrs[wave][0][lane] = reinterpret_cast<uint64_t>(wp);
-    lds_ptrs[wave][1][lane] = reinterpret_cast<uint64_t>(rp);
-    typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-    const u64x2* const pw = reinterpret_cast<const u64x2*>(&lds_ptrs[wave][0][0]);
-    const u64x2* const pr = reinterpret_cast<const u64x2*>(&lds_ptrs[wave][1][0]);
-#pragma unroll
-    for (int j = 0; j < kTraceMaxWrites; j += 2) {
-      const u64x2 two = pw[j / 2];
-      gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
-      gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
-    }
-#pragma unroll
-    for (int i = 0; i < kTraceMaxReads; i += 2) {
-      const u64x2 two = pr[i / 2];
-      gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
-      gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
-    }
-    gload_row<VEC>(reinterpret_cast<const float*>(at(v_l, st_v, tc)), 0u, buf.vin);
+    TraceSlot& sl = slot_of(t);
+    if (lane < kTraceMaxWrites) sl.wptr[lane] = reinterpret_cast<uint64_t>(wp);
+    if (lane < kTraceMaxReads) sl.rptr[lane] = reinterpret_cast<uint64_t>(rp);
   };
 
-  auto lds_get = [&](int row, float (&x)[VEC]) __attribute__((always_inline)) {
-    const float* p = lds_wave + row * kRow + col;
-    if constexpr (VEC == 4) {
-      const float4 t = *reinterpret_cast<const float4*>(p);
-      x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
-    } else if constexpr (VEC == 2) {
-      const float2 t = *reinterpret_cast<const float2*>(p);
-      x[0] = t.x; x[1] = t.y;
-    } else {
-      x[0] = *p;
-    }
-  };
-  auto lds_put = [&](int row, const float (&x)[VEC]) __attribute__((always_inline)) {
-    float* p = lds_wave + row * kRow + col;
-    if constexpr (VEC == 4) {
-      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
-    } else if constexpr (VEC == 2) {
-      *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
-    } else {
-      *p = x[0];
-    }
-  };
-
-  // updated rows of the last computed step
-  float cur[kTraceMaxWrites][VEC];
-#pragma unroll
-  for (int j = 0; j < kTraceMaxWrites; ++j) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) cur[j][v] = 0.0f;
-  }
-  bool alive = true;
-
-  // lane j's write and read weight of step t, loaded two iterations ahead and
-  // handed to LDS at the end of the iteration before
-  auto load_weights = [&](int t, float& ww, float& rw) __attribute__((always_inline)) {
-    const int tc = t < G ? t : G - 1;
-    ww = *(const gfloat*)(at(ww_l, st_ww, tc));
-    rw = *(const gfloat*)(at(rw_l, st_rw, tc));
-  };
-  auto put_weights = [&](float ww, float rw) __attribute__((always_inline)) {
-    float* const wl = reinterpret_cast<float*>(&lds_weights[wave][0][0]);
-    wl[lane] = ww;
-    wl[kWave + lane] = FULL || lane < R ? rw : -0.0f;
-  };
-
-  // Step t: LDS row j holds write j of step t-1 until this step replaces it.
-  auto compute = [&](int t, const TraceRoute& rt, TraceRows<VEC>& buf)
+  // Publish step t's masks and the rows its updates are stored to.  run: the
+  // step runs; fitted: its first touches got rows.
+  auto publish_step = [&](int t, const TraceRoute& rt, bool run, bool fitted)
       __attribute__((always_inline)) {
-    const bool run = __builtin_amdgcn_readfirstlane(route_ok(rt.u) && alive ? 1 : 0) != 0;
-    float acc[VEC];
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-    if (run) {
-      // fwd and rawm hold bits of lanes below W (R) only
-      const uint32_t fwd = rt.fwd;
-      if (fwd != 0) {
-#pragma unroll
-        for (int j = 0; j < kTraceMaxWrites; ++j) {
-          if ((fwd >> j) & 1u) lds_get(rl(rt.wsrc, j), buf.w[j]);
-        }
-#pragma unroll
-        for (int i = 0; i < kTraceMaxReads; ++i) {
-          if ((fwd >> (kTraceMaxWrites + i)) & 1u) lds_get(rl(rt.rsrc, i), buf.r[i]);
-        }
-      }
-      // lane j put weight j there in the iteration before: every lane reads
-      // all of them as vectors, instead of a readlane per weight
-      const vf4_t wwv = lds_weights[wave][0][0];
-      vf4_t rwv[kTraceMaxReads / 4];
-#pragma unroll
-      for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[wave][1][k];
-      const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t & (kWave - 1)));
-      const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t & (kWave - 1)));
-      const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t & (kWave - 1)));
-      float ret[VEC];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) ret[v] = 0.0f;
-      // rows past W are computed and left out of the sum by a select on the
-      // wave-uniform row count (a decayed row can be infinite or NaN, so no
-      // term of theirs is exactly neutral); rows past R add -0.0
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        const float wj = wwv[j];
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float d = buf.w[j][v] * alpha;
-          cur[j][v] = d;
-          const float term = wj * d;
-          ret[v] = (j == 0) ? term : (j < W ? ret[v] + term : ret[v]);
-        }
-      }
-      float delta[VEC];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const float a = in_gate * buf.vin[v];
-        const float e = er_gate * ret[v];
-        delta[v] = a - e;
-      }
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        const float wj = wwv[j];
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float u = wj * delta[v];
-          cur[j][v] = cur[j][v] + u;
-        }
-        lds_put(j, cur[j]);
-      }
-      const uint32_t rawm = rt.rawm;
-      if (rawm != 0) {
-#pragma unroll
-        for (int i = 0; i < kTraceMaxReads; ++i) {
-          if ((rawm >> i) & 1u) lds_get(rl(rt.rraw, i), buf.r[i]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < kTraceMaxReads; ++i) {
-        const float wr = rwv[i / 4][i % 4];
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float term = wr * buf.r[i][v];
-          acc[v] = (i == 0) ? term : acc[v] + term;
-        }
-      }
-    }
-    gstore_row<VEC>(reinterpret_cast<float*>(const_cast<char*>(at(out_l, st_out, t))), 0u, acc);
-    if (run) {
-      const uint32_t r = static_cast<uint32_t>(DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow));
-      float* const dst = reinterpret_cast<float*>(
-          reinterpret_cast<char*>(DENSE ? table_bank : slab) + static_cast<uint64_t>(r) * row_bytes);
-      // rows in use that are not first touches (those wait for their claims)
-      const uint32_t smask = static_cast<uint32_t>(wlanes) & ~route_fmask(rt.u);
-      const uint32_t co = fresh(coff);
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if ((smask >> j) & 1u) {
-          float* p = const_cast<float*>(rl_ptr(dst, j));
-          gstore_row<VEC>(p, co, cur[j]);
-        }
-      }
+    TraceSlot& sl = slot_of(t);
+    const uint32_t fm = route_fmask(rt.u);
+    const uint32_t smask = run ? ((static_cast<uint32_t>(wlanes) & ~fm) | (fitted ? fm : 0u)) : 0u;
+    if (lane < kTraceMaxWrites) sl.drow[lane] = DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow);
+    const uint32_t w0 = static_cast<uint32_t>(__ballot((rt.wsrc & 1) != 0)) & 15u;
+    const uint32_t w1 = static_cast<uint32_t>(__ballot((rt.wsrc & 2) != 0)) & 15u;
+    const uint32_t f0 = static_cast<uint32_t>(__ballot((rt.rsrc & 1) != 0)) & 0xFFFFu;
+    const uint32_t f1 = static_cast<uint32_t>(__ballot((rt.rsrc & 2) != 0)) & 0xFFFFu;
+    const uint32_t a0 = static_cast<uint32_t>(__ballot((rt.rraw & 1) != 0)) & 0xFFFFu;
+    const uint32_t a1 = static_cast<uint32_t>(__ballot((rt.rraw & 2) != 0)) & 0xFFFFu;
+    if (lane == 0) {
+      u32x4_t c;
+      c.x = rt.fwd | (run ? 1u << 20 : 0u) | (smask << 24);
+      c.y = rt.rawm | (w0 << 16) | (w1 << 20);
+      c.z = f0 | (f1 << 16);
+      c.w = a0 | (a1 << 16);
+      *reinterpret_cast<u32x4_t*>(sl.ctl) = c;
     }
   };
 
   // ---- claims (packed)
   int64_t* const scan = DENSE ? nullptr : P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
   int64_t* const claims = DENSE ? nullptr : scan + COWSDM_SCRATCH_CLAIMS;
+  bool alive = true;  // every claim so far fitted
 
   // Step t's first touches claim their rows: one atomic add per (step, bank)
   // with first touches, its result read when the step resolves.
@@ -659,23 +835,10 @@ void sdm_trace_kernel(StepParams P) {
                                   static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
           }
-        } else {
-          if (first) {
-            rt.wrow = new_row;
-            map_bank[rt.widx] = new_row;
-            if constexpr (MAPLDS) lds_map[rt.widx] = new_row;
-          }
-          float* const dst = reinterpret_cast<float*>(
-              reinterpret_cast<char*>(slab) +
-              static_cast<uint64_t>(static_cast<uint32_t>(rt.wrow < 0 ? 0 : rt.wrow)) * row_bytes);
-          const uint32_t co = fresh(coff);
-#pragma unroll
-          for (int j = 0; j < kTraceMaxWrites; ++j) {
-            if ((fmask >> j) & 1u) {  // first touches are lanes below W
-              float* p = const_cast<float*>(rl_ptr(dst, j));
-              gstore_row<VEC>(p, co, cur[j]);
-            }
-          }
+        } else if (first) {
+          rt.wrow = new_row;
+          map_bank[rt.widx] = new_row;
+          if constexpr (MAPLDS) lds_map[rt.widx] = new_row;
         }
       }
       if (!fits) {
@@ -738,8 +901,8 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // iteration s-1 loads the counts that the proof before step s sums, after
-  // its compute: the later the load, the likelier every bank has published
+  // iteration s-1 loads the counts that the proof before step s sums, at its
+  // end: the later the load, the likelier every bank has published
   auto issue_proof = [&](int s) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (proofs && s + 1 == next_proof && s + 1 > 0) {
@@ -805,32 +968,26 @@ void sdm_trace_kernel(StepParams P) {
     return false;
   };
 
-  // ---- prologue: step 0 classified with its rows in flight
-  TraceRows<VEC> bufA, bufB;
-#pragma unroll
-  for (int j = 0; j < kTraceMaxWrites; ++j) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) { bufA.w[j][v] = 0.0f; bufB.w[j][v] = 0.0f; }
-  }
-#pragma unroll
-  for (int i = 0; i < kTraceMaxReads; ++i) {
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) { bufA.r[i][v] = 0.0f; bufB.r[i][v] = 0.0f; }
-  }
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) { bufA.vin[v] = 0.0f; bufB.vin[v] = 0.0f; }
-  // slots and map entries in flight, homed by the parity of the iteration
-  // that issued them
+  // the data wave has finished `need` steps, so the ring slots the next
+  // steps reuse are free; false if it never does.  Iteration u overwrites
+  // the addresses of step u+1-K and the masks of step u-K, which the data
+  // wave has read once it finished step u+1-K (it reads step 0's addresses
+  // before its first step): iteration u needs u+2-K steps finished.
+  uint32_t dseen = 0;
+  auto room = [&](int need) __attribute__((always_inline)) -> bool {
+    if (need <= 0 || dseen >= static_cast<uint32_t>(need)) return true;
+    for (int spins = 0; spins < kSpinLimit; ++spins) {
+      dseen = sync_load(&sync[1]);
+      if (dseen >= static_cast<uint32_t>(need)) return true;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+  };
+
+  // ---- prologue: step 0 classified and its rows published
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
   int popA = 0, popB = 0;          // claims in flight, homed like the loads
-  float wwA = 0.0f, rwA = 0.0f, wwB = 0.0f, rwB = 0.0f;  // weights in flight
-  {
-    float ww0 = 0.0f, rw0 = 0.0f;
-    load_weights(0, ww0, rw0);
-    put_weights(ww0, rw0);
-    load_weights(1, wwB, rwB);     // handed over at the end of iteration 0
-  }
   TraceRoute q, r0;
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   q.fwd = 0; q.rawm = 0;
@@ -841,8 +998,9 @@ void sdm_trace_kernel(StepParams P) {
     issue_map(i0, mw0, mr0);
     const int rrow = classify(0, i0, mw0, mr0, r0, q, q, true);
     after_classify(0, r0, popB);   // resolved in iteration 0
-    issue_rows(0, r0, rrow, bufA);
+    publish_rows(0, r0, rrow);
   }
+  if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | 1u);
   if constexpr (DENSE || MAPLDS) {
     load_idx(1, idxB);             // classified in iteration 0
   } else {
@@ -851,68 +1009,85 @@ void sdm_trace_kernel(StepParams P) {
     load_idx(2, idxB);             // its map entries are loaded in iteration 0
   }
 
-  // Iteration s.  `self` homes are written now and read in iteration s+1,
-  // `other` homes were written in iteration s-1 and are read now.
-  auto iteration = [&](int s, TraceRows<VEC>& rows_s, TraceRows<VEC>& rows_next,
-                       TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other, int& pop_self, int pop_other,
-                       float& ww_self, float& rw_self, float ww_other, float rw_other)
+  // Iteration s: classifies step s+1 and publishes its rows, resolves step s
+  // and publishes its masks.  `self` homes are written now and read in
+  // iteration s+1, `other` homes were written in iteration s-1 and are read now.
+  auto iteration = [&](int s, TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
+                       int& mw_other, int& mr_other, int& pop_self, int pop_other)
       __attribute__((always_inline)) {
-    load_weights(s + 2, ww_self, rw_self);
     TraceRoute r1;
     if constexpr (DENSE || MAPLDS) {
       load_idx(s + 2, idx_self);
       const int rrow = classify(s + 1, idx_other, -1, -1, r1, r0, q, route_ok(r0.u));
       after_classify(s + 1, r1, pop_self);
-      issue_rows(s + 1, r1, rrow, rows_next);
-      compute(s, r0, rows_s);
-      issue_proof(s);
-      if constexpr (MAPLDS) resolve(s, r0, r1, pop_other);
+      publish_rows(s + 1, r1, rrow);
     } else {
       load_idx(s + 3, idx_self);
       issue_map(idx_other, mw_self, mr_self);   // step s+2
       ready2 = idx_other;
       const int rrow = classify(s + 1, ready1, mw_other, mr_other, r1, r0, q, route_ok(r0.u));
       after_classify(s + 1, r1, pop_self);
-      issue_rows(s + 1, r1, rrow, rows_next);
-      compute(s, r0, rows_s);
-      issue_proof(s);
-      resolve(s, r0, r1, pop_other);
+      publish_rows(s + 1, r1, rrow);
       ready1 = ready2;
     }
-    put_weights(ww_other, rw_other);   // step s+1's
+    const bool run = route_ok(r0.u) && alive;
+    if constexpr (!DENSE) resolve(s, r0, r1, pop_other);
+    publish_step(s, r0, run, alive);
+    issue_proof(s);
+    if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | static_cast<uint32_t>(s + 2));
     q = r0;
     r0 = r1;
   };
-  // Drain the prologue's loads: the loop head then has one state of loads in
-  // flight (the back edge's), and the waits the compiler places there stay
-  // as loose as the steady state allows.
+  // Drain the prologue's loads (see the data wave).
   __builtin_amdgcn_s_waitcnt(0);
 
-  // Pairs of steps, then an odd last step outside the loop.  Capacity proofs
-  // come in runs of an even number of steps (the host checks), so the only
-  // exit from the loop body is at its head: the compiler then sees one state
-  // of the loads in flight there and waits on none of them early.
   int s = 0;
   bool stopped = false;
   for (; s + 1 < G; s += 2) {
+    if (!room(s + 3 - kTraceRing)) {
+      // the data wave stopped taking steps: record it and stop here
+      if (lane == 0 && !DENSE) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      done_steps = s;
+      stopped = true;
+      break;
+    }
     if (proof_stops(s, r0, popB)) {
       stopped = true;
       break;
     }
-    gates_for(s);
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB, wwA, rwA, wwB, rwB);
-    iteration(s + 1, bufB, bufA, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA, wwB, rwB, wwA, rwA);
+    iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
+    iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA);
   }
-  if (!stopped && s < G && !proof_stops(s, r0, popB)) {
-    gates_for(s);
-    iteration(s, bufA, bufB, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB, wwA, rwA, wwB, rwB);
+  if (!stopped && s < G) {
+    if (!room(s + 2 - kTraceRing)) {
+      if (lane == 0 && !DENSE) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      done_steps = s;
+      stopped = true;
+    } else if (proof_stops(s, r0, popB)) {
+      stopped = true;
+    } else {
+      iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
+    }
+  }
+  // the data wave computes the steps before done_steps, and no more
+  if (stopped && lane == 0) {
+    sync_store(&sync[0], (static_cast<uint32_t>(done_steps) << 16) | kNoStop);
   }
 
-  // ---- the layer's last wave to finish closes the launch: every wave of the
-  // layer read free_count and the step counter before taking its ticket, and
-  // its claims (device-scope atomics) have returned before it: no release
-  // fence, whose L2 write-back every wave would pay
+  // ---- the layer's last control wave to finish closes the launch: every
+  // wave of the layer read free_count and the step counter before taking its
+  // ticket, and its claims (device-scope atomics) have returned before it:
+  // no release fence, whose L2 write-back every wave would pay.  The data
+  // waves' row stores need no ordering here: the next launch on the stream
+  // starts after this one has ended.
   if (lane == 0 && (!DENSE || P.trace_step)) {
     int64_t* const ticket = P.trace_ticket + 1 + layer_id;
     __builtin_amdgcn_s_waitcnt(0);
@@ -945,7 +1120,10 @@ void sdm_trace_kernel(StepParams P) {
 // exceeds what the device can hold for this kernel; the caller then falls
 // back to one launch per step.
 template <typename IDX, bool DENSE, bool MAPLDS>
-bool launch_trace_kernels(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
+  StepParams P = P0;
+  P.blocks_per_layer = (P.banks + kTraceBanksPerBlock - 1) / kTraceBanksPerBlock;
+  const int blocks = P.blocks_per_layer * P.nlayers;
   // the full shape folds every row count; other shapes select per row
   const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
   // one scan window when a packed layer has at most 64 banks
@@ -969,14 +1147,14 @@ bool launch_trace_kernels(const StepParams& P, int blocks, int vec, hipStream_t 
   static int resident_slots[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
-  const size_t lds_bytes = MAPLDS ? sizeof(int) * kBanksPerBlock * static_cast<size_t>(P.slots) : 0;
+  const size_t lds_bytes = MAPLDS ? sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
   const int key = MAPLDS ? P.slots : 0;
   if (resident[variant][which] < 0 || resident_slots[variant][which] != key) {
     int device = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStepThreads, lds_bytes) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kTraceThreads, lds_bytes) !=
             hipSuccess) {
       (void)hipGetLastError();
       resident[variant][which] = 0;
@@ -986,18 +1164,18 @@ bool launch_trace_kernels(const StepParams& P, int blocks, int vec, hipStream_t 
     resident_slots[variant][which] = key;
   }
   if (blocks > resident[variant][which]) return false;
-  void* args[] = {const_cast<StepParams*>(&P)};
-  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kStepThreads), args, lds_bytes, stream);
+  void* args[] = {&P};
+  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kTraceThreads), args, lds_bytes, stream);
   return true;  // a failed launch is reported by the caller's launch_status()
 }
 
 template <typename IDX, bool DENSE>
-bool launch_trace(const StepParams& P, int blocks, int vec, hipStream_t stream) {
+bool launch_trace(const StepParams& P, int vec, hipStream_t stream) {
   // packed layers whose slot map fits keep it in LDS
   if (!DENSE && P.slots <= kTraceMapSlots) {
-    return launch_trace_kernels<IDX, DENSE, true>(P, blocks, vec, stream);
+    return launch_trace_kernels<IDX, DENSE, true>(P, vec, stream);
   }
-  return launch_trace_kernels<IDX, DENSE, false>(P, blocks, vec, stream);
+  return launch_trace_kernels<IDX, DENSE, false>(P, vec, stream);
 }
 
 }  // namespace cowsdm_impl
