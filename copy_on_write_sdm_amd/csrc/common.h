@@ -31,7 +31,7 @@ constexpr int kTraceFreeWindow = 1024;      // top of the free stack staged in L
 constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are staged in LDS
 constexpr int kTraceBanksPerBlock = 2;      // banks per persistent workgroup
 constexpr int kTraceThreads = 2 * kWave * kTraceBanksPerBlock;  // a control and a data wave per bank
-constexpr int kTraceRing = 8;               // steps handed from control to data wave in flight
+constexpr int kTraceRing = 16;              // steps handed from control to data wave in flight
 constexpr int64_t kClaimFailBase = int64_t{1} << 40;  // failed claim p recorded as base - p
 
 constexpr uint32_t kStatusEmpty = 0;

@@ -10,9 +10,9 @@
 //   the control wave loads the step's slots and map entries, classifies the
 //   step (first touches, slots written by the step before, read-after-write),
 //   claims rows for its first touches, and publishes the addresses of the
-//   rows the step loads; one step later it takes the claimed rows, stores
-//   them in the map and publishes the rows the step's updates are stored to
-//   and the step's masks;
+//   rows the step loads, two steps ahead of the data wave's loads; two steps
+//   later it takes the claimed rows, stores them in the map and publishes
+//   the rows the step's updates are stored to and the step's masks;
 //
 //   the data wave loads the rows of step s+1 from the published addresses
 //   while it computes step s (gated-delta update, sparse read) from rows
@@ -22,15 +22,14 @@
 // Only the data wave reads or writes rows, in program order: a step's rows
 // were stored by earlier steps of the same wave, except the rows of the step
 // just before, which it takes from LDS.  The control wave runs up to
-// kTraceRing - 1 steps ahead, so the atomics and map lookups it waits on stay
-// off the data wave's path.  Step t's map entries are read before steps t-2
-// and t-1 have stored their first touches: slots written at t-1 take their
-// rows from that step's result, and slots written at t-2 take the physical
-// rows popped for them.  When a bank's map fits (N <= kTraceMapSlots), the
+// kTraceRing - 3 steps ahead, so the atomics and map lookups it waits on stay
+// off the data wave's path.  It classifies step t after resolving step t-2,
+// but before step t-1 has its rows: slots written at t-1 take their rows from
+// that step's result.  When a bank's map fits (N <= kTraceMapSlots), the
 // control wave keeps it in LDS for the launch (it is the only writer of its
-// bank's entries) and reads step t+1's entries there after step t-1's pops:
-// only the slots of step t still need their rows forwarded, and the global
-// map is written alongside.  Values in flight live in even/odd homes (both
+// bank's entries) and the global map is written alongside; otherwise step
+// t's entries are loaded from the global map an iteration early, before
+// step t-2's pops, and slots written at t-2 take the rows popped for them.  Values in flight live in even/odd homes (both
 // loops are unrolled by two) and are only read one iteration after their
 // load was issued, so no register copy waits on memory.
 //
@@ -351,26 +350,49 @@ void sdm_trace_kernel(StepParams P) {
       wv[kWave + lane] = FULL || lane < R ? rw : -0.0f;
     };
 
-    // Step t's rows from the addresses the control wave published: a
-    // broadcast read gives every lane two of them, and each row load takes
-    // its own 64-bit vector address (no scalar base, whose write by a
-    // readlane a load could not follow at once).  Every row is loaded: write
-    // lanes past W point at a row of slot 0, read lanes past R at the zero
-    // row, and the step leaves both out.
-    auto issue_rows = [&](int t, TraceRows<VEC>& buf) __attribute__((always_inline)) {
-      const int tc = t < G ? t : G - 1;
+    // What the data wave reads from LDS for a step, one iteration before it
+    // needs it: step t+1's row addresses (a broadcast read gives every lane
+    // two of them), step t's masks, store rows and weights.
+    constexpr int kPtrPairs = (kTraceMaxWrites + kTraceMaxReads) / 2;
+    struct Handed {
+      u64x2_t ptr[kPtrPairs];  // wptr then rptr, as laid out in the slot
+      u32x4_t cw;
+      i32x4_t dr;
+      vf4_t wwv;
+      vf4_t rwv[kTraceMaxReads / 4];
+    };
+    auto read_ptrs = [&](int t, Handed& h) __attribute__((always_inline)) {
+      const u64x2_t* const p = reinterpret_cast<const u64x2_t*>(slot_of(t).wptr);
+#pragma unroll
+      for (int k = 0; k < kPtrPairs; ++k) h.ptr[k] = p[k];
+    };
+    // lane j put weight j there: every lane reads all of them as vectors,
+    // instead of a readlane per weight
+    auto read_step = [&](int t, Handed& h) __attribute__((always_inline)) {
       const TraceSlot& sl = slot_of(t);
-      const u64x2_t* const pw = reinterpret_cast<const u64x2_t*>(sl.wptr);
-      const u64x2_t* const pr = reinterpret_cast<const u64x2_t*>(sl.rptr);
+      h.cw = *reinterpret_cast<const u32x4_t*>(sl.ctl);
+      h.dr = *reinterpret_cast<const i32x4_t*>(sl.drow);
+      h.wwv = lds_weights[pair][0][0];
+#pragma unroll
+      for (int k = 0; k < kTraceMaxReads / 4; ++k) h.rwv[k] = lds_weights[pair][1][k];
+    };
+
+    // Step t's rows from the published addresses: each row load takes its
+    // own 64-bit vector address (no scalar base, whose write by a readlane a
+    // load could not follow at once).  Every row is loaded: write lanes past
+    // W point at a row of slot 0, read lanes past R at the zero row, and the
+    // step leaves both out.
+    auto issue_rows = [&](int t, const Handed& h, TraceRows<VEC>& buf) __attribute__((always_inline)) {
+      const int tc = t < G ? t : G - 1;
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; j += 2) {
-        const u64x2_t two = pw[j / 2];
+        const u64x2_t two = h.ptr[j / 2];
         gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.w[j]);
         gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.w[j + 1]);
       }
 #pragma unroll
       for (int i = 0; i < kTraceMaxReads; i += 2) {
-        const u64x2_t two = pr[i / 2];
+        const u64x2_t two = h.ptr[(kTraceMaxWrites + i) / 2];
         gload_row<VEC>(reinterpret_cast<const float*>(two.x), coff, buf.r[i]);
         gload_row<VEC>(reinterpret_cast<const float*>(two.y), coff, buf.r[i + 1]);
       }
@@ -409,8 +431,10 @@ void sdm_trace_kernel(StepParams P) {
     }
 
     // Step t: LDS row j holds write j of step t-1 until this step replaces it.
-    auto compute = [&](int t, const u32x4_t& cw, const i32x4_t& dr, TraceRows<VEC>& buf)
+    auto compute = [&](int t, const Handed& h, TraceRows<VEC>& buf)
         __attribute__((always_inline)) {
+      const u32x4_t cw = h.cw;
+      const i32x4_t dr = h.dr;
       const uint32_t c0 = __builtin_amdgcn_readfirstlane(cw.x);
       const bool run = ((c0 >> 20) & 1u) != 0;
       float acc[VEC];
@@ -430,12 +454,7 @@ void sdm_trace_kernel(StepParams P) {
             if ((fwd >> (kTraceMaxWrites + i)) & 1u) lds_get(plane_code(c2, i, 16 + i), buf.r[i]);
           }
         }
-        // lane j put weight j there in the iteration before: every lane reads
-        // all of them as vectors, instead of a readlane per weight
-        const vf4_t wwv = lds_weights[pair][0][0];
-        vf4_t rwv[kTraceMaxReads / 4];
-#pragma unroll
-        for (int k = 0; k < kTraceMaxReads / 4; ++k) rwv[k] = lds_weights[pair][1][k];
+        const vf4_t wwv = h.wwv;
         const float alpha = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha_l), t & (kWave - 1)));
         const float in_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(in_l), t & (kWave - 1)));
         const float er_gate = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(er_l), t & (kWave - 1)));
@@ -483,7 +502,7 @@ void sdm_trace_kernel(StepParams P) {
         }
 #pragma unroll
         for (int i = 0; i < kTraceMaxReads; ++i) {
-          const float wr = rwv[i / 4][i % 4];
+          const float wr = h.rwv[i / 4][i % 4];
 #pragma unroll
           for (int v = 0; v < VEC; ++v) {
             const float term = wr * buf.r[i][v];
@@ -544,23 +563,36 @@ void sdm_trace_kernel(StepParams P) {
       load_weights(1, wwB, rwB);     // handed over at the end of iteration 0
     }
 
-    // Iteration t: loads step t+1's rows, computes step t.
+    // Iteration t: loads step t+1's rows, computes step t, then reads what
+    // iteration t+1 needs from LDS.  The progress word goes out after this
+    // step's LDS writes and before those reads, so its release waits for no
+    // read in flight.
+    Handed hd;
     auto iteration = [&](int t, TraceRows<VEC>& rows_t, TraceRows<VEC>& rows_next,
                          float& ww_self, float& rw_self, float ww_other, float rw_other)
         __attribute__((always_inline)) {
       load_weights(t + 2, ww_self, rw_self);
-      const TraceSlot& sl = slot_of(t);
-      const u32x4_t cw = *reinterpret_cast<const u32x4_t*>(sl.ctl);
-      const i32x4_t dr = *reinterpret_cast<const i32x4_t*>(sl.drow);
-      issue_rows(t + 1, rows_next);
-      compute(t, cw, dr, rows_t);
+      issue_rows(t + 1, hd, rows_next);
+      compute(t, hd, rows_t);
       put_weights(ww_other, rw_other);   // step t+1's
       if (lane == 0) sync_store(&sync[1], static_cast<uint32_t>(t + 1));
+      read_step(t + 1, hd);
+      read_ptrs(t + 2, hd);
     };
 
-    bool go = await(1);
+    // the published steps the reads of iteration t+1 need (capped at what
+    // the control wave publishes in all: addresses up to step G+1)
+    auto need = [&](int t) __attribute__((always_inline)) -> uint32_t {
+      return static_cast<uint32_t>(t + 3 < G + 1 ? t + 3 : G + 1);
+    };
+    bool go = await(need(-1));
     bool lost = !go;
-    if (go) issue_rows(0, bufA);
+    if (go) {
+      read_ptrs(0, hd);
+      issue_rows(0, hd, bufA);
+      read_step(0, hd);
+      read_ptrs(1, hd);
+    }
     // Drain the prologue's loads: the loop head then has one state of loads
     // in flight (the back edge's), and the waits the compiler places there
     // stay as loose as the steady state allows.
@@ -570,7 +602,7 @@ void sdm_trace_kernel(StepParams P) {
     // so the loop's only exit is at its head.
     int s = 0;
     for (; go && s + 1 < G; s += 2) {
-      if (!await(static_cast<uint32_t>(s + 3))) {
+      if (!await(need(s + 1))) {
         lost = true;
         go = false;
         break;
@@ -584,7 +616,7 @@ void sdm_trace_kernel(StepParams P) {
       iteration(s + 1, bufB, bufA, wwB, rwB, wwA, rwA);
     }
     if (go && s < G) {
-      if (!await(static_cast<uint32_t>(s + 2))) {
+      if (!await(need(s))) {
         lost = true;
       } else if (static_cast<uint32_t>(s) < stop) {
         gates_for(s);
@@ -881,11 +913,54 @@ void sdm_trace_kernel(StepParams P) {
     run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk;
   }
 
-  // after classifying step t: claim (unless t starts a run, whose claims wait
-  // for its proof), and publish the bank's count when t ends a run
+  // Does the proof before step s stop the layer?  Wave-uniform: every wave
+  // sums the same counts, the first touches of every bank before step s.
+  auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {
+    int total = 0;
+    if (s > 0) {
+      const uint32_t off = static_cast<uint32_t>(s / proof_steps * B);
+      auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+        return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
+      };
+#pragma unroll
+      for (int k = 0; k < SCANW; ++k) {
+        if (k * kWave < B) {
+          uint64_t w = pw[k];
+          bool ready = word_ready(w);
+          if (__ballot(!ready) != 0) {
+            // a bank has not finished the run yet: bounded wait
+            int spins = 0;
+            while (!ready && spins < kSpinLimit) {
+              __builtin_amdgcn_s_sleep(1);
+              w = atomic_load_u64(run_l[k] + off);
+              ready = word_ready(w);
+              ++spins;
+            }
+            if (__ballot(!ready) != 0) {
+              // never arrived: record it and stop the layer here
+              if (lane == 0) {
+                __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                      static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+              return true;
+            }
+          }
+          const bool in = k * kWave + lane < B;
+          total += static_cast<int>(wave_sum64(in ? static_cast<int64_t>(w & kValueMask) : 0));
+        }
+      }
+      total = __builtin_amdgcn_readfirstlane(total);
+    }
+    return old_free - total < proof_rows;
+  };
+
+  // After classifying step t: claim its rows (a run's first step waits for
+  // its proof), and publish the bank's count when t ends a run.
+  bool halted = false;  // a proof failed: no claims from its step on
   auto after_classify = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (t < G && (!proofs || run_left != proof_steps - 1)) claim(rt, home);
+      if (t < G && !halted && !(proofs && t == next_proof)) claim(rt, home);
       if (proofs) {
         if (route_ok(rt.u)) cum += route_count(rt.u);
         if (run_left == 0) {
@@ -901,12 +976,30 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // iteration s-1 loads the counts that the proof before step s sums, at its
-  // end: the later the load, the likelier every bank has published
+  // The proof before step t, at the end of the iteration that classified t:
+  // when it passes, t claims its rows (resolved two iterations later, like
+  // every claim); when it fails, the layer halts before t.
+  auto prove = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      if (proofs && t == next_proof && t < G && !halted) {
+        if (proof_fails(t)) {
+          done_steps = t;
+          halted = true;
+        } else {
+          next_proof += proof_steps;
+          claim(rt, home);
+        }
+      }
+    }
+  };
+
+  // iteration s loads, at its start, the counts that the proof before step
+  // s+2 sums at its end: every bank published them when it classified step
+  // s+1, in iteration s-1
   auto issue_proof = [&](int s) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (proofs && s + 1 == next_proof && s + 1 > 0) {
-        const uint32_t off = static_cast<uint32_t>((s + 1) / proof_steps * B);
+      if (proofs && s + 2 == next_proof && !halted) {
+        const uint32_t off = static_cast<uint32_t>((s + 2) / proof_steps * B);
 #pragma unroll
         for (int k = 0; k < SCANW; ++k) {
           if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + off);
@@ -915,64 +1008,11 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // Does the proof before step s stop the layer?  Wave-uniform: every wave
-  // sums the same counts.  When it passes, step s claims its rows.
-  auto proof_stops = [&](int s, const TraceRoute& rs, int& home) __attribute__((always_inline)) -> bool {
-    if constexpr (!DENSE) {
-      if (proofs && s == next_proof) {
-        int total = 0;
-        if (s > 0) {
-          const uint32_t off = static_cast<uint32_t>(s / proof_steps * B);
-          auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-            return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
-          };
-#pragma unroll
-          for (int k = 0; k < SCANW; ++k) {
-            if (k * kWave < B) {
-              uint64_t w = pw[k];
-              bool ready = word_ready(w);
-              if (__ballot(!ready) != 0) {
-                // a bank has not finished the run yet: bounded wait
-                int spins = 0;
-                while (!ready && spins < kSpinLimit) {
-                  __builtin_amdgcn_s_sleep(1);
-                  w = atomic_load_u64(run_l[k] + off);
-                  ready = word_ready(w);
-                  ++spins;
-                }
-                if (__ballot(!ready) != 0) {
-                  // never arrived: record it and stop the layer here
-                  if (lane == 0) {
-                    __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                          static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                  }
-                  done_steps = s;
-                  return true;
-                }
-              }
-              const bool in = k * kWave + lane < B;
-              total += static_cast<int>(wave_sum64(in ? static_cast<int64_t>(w & kValueMask) : 0));
-            }
-          }
-          total = __builtin_amdgcn_readfirstlane(total);
-        }
-        if (old_free - total < proof_rows) {
-          done_steps = s;
-          return true;
-        }
-        next_proof += proof_steps;
-        claim(rs, home);
-      }
-    }
-    return false;
-  };
-
   // the data wave has finished `need` steps, so the ring slots the next
   // steps reuse are free; false if it never does.  Iteration u overwrites
-  // the addresses of step u+1-K and the masks of step u-K, which the data
-  // wave has read once it finished step u+1-K (it reads step 0's addresses
-  // before its first step): iteration u needs u+2-K steps finished.
+  // the addresses of step u+2-K and the masks of step u-K, which the data
+  // wave has read once it finished step u+2-K (it reads step 0's addresses
+  // before its first step): iteration u needs u+3-K steps finished.
   uint32_t dseen = 0;
   auto room = [&](int need) __attribute__((always_inline)) -> bool {
     if (need <= 0 || dseen >= static_cast<uint32_t>(need)) return true;
@@ -984,59 +1024,70 @@ void sdm_trace_kernel(StepParams P) {
     return false;
   };
 
-  // ---- prologue: step 0 classified and its rows published
+  // ---- prologue: steps 0 and 1 classified, claimed and their rows published
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
-  int popA = 0, popB = 0;          // claims in flight, homed like the loads
-  TraceRoute q, r0;
+  int popA = 0, popB = 0;          // claims in flight, homed by the parity of their step
+  TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   q.fwd = 0; q.rawm = 0;
   {
-    TraceIdx i0;
+    TraceIdx i0, i1;
     load_idx(0, i0);
-    int mw0, mr0;
+    load_idx(1, i1);
+    int mw0, mr0, mw1, mr1;
     issue_map(i0, mw0, mr0);
-    const int rrow = classify(0, i0, mw0, mr0, r0, q, q, true);
-    after_classify(0, r0, popB);   // resolved in iteration 0
-    publish_rows(0, r0, rrow);
+    issue_map(i1, mw1, mr1);
+    const int rrow0 = classify(0, i0, mw0, mr0, rA, q, q, true);
+    after_classify(0, rA, popA);
+    prove(0, rA, popA);
+    publish_rows(0, rA, rrow0);
+    const int rrow1 = classify(1, i1, mw1, mr1, rB, rA, q, route_ok(rA.u));
+    after_classify(1, rB, popB);
+    publish_rows(1, rB, rrow1);
   }
   if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | 1u);
   if constexpr (DENSE || MAPLDS) {
-    load_idx(1, idxB);             // classified in iteration 0
+    load_idx(2, idxB);             // classified in iteration 0
   } else {
-    load_idx(1, ready1);           // its map entries, classified in iteration 0
+    load_idx(2, ready1);           // its map entries, classified in iteration 0
     issue_map(ready1, mwB, mrB);
-    load_idx(2, idxB);             // its map entries are loaded in iteration 0
+    load_idx(3, idxB);             // its map entries are loaded in iteration 0
   }
 
-  // Iteration s: classifies step s+1 and publishes its rows, resolves step s
-  // and publishes its masks.  `self` homes are written now and read in
-  // iteration s+1, `other` homes were written in iteration s-1 and are read now.
+  // Iteration s: resolves step s (claimed two iterations before), classifies
+  // and claims step s+2 and publishes its rows, publishes step s's masks.
+  // Step s+2's map lookups see every pop up to step s (in LDS; the global
+  // map's entries, loaded earlier, take step s's pops from its route), and
+  // its slots written at step s+1 take their rows from that step.  `self`
+  // homes are written now and read in iteration s+1 (claims: s+2), `other`
+  // homes were written in iteration s-1 and are read now.
   auto iteration = [&](int s, TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other, int& pop_self, int pop_other)
+                       int& mw_other, int& mr_other, int& pop)
       __attribute__((always_inline)) {
-    TraceRoute r1;
+    issue_proof(s);
+    const bool run = route_ok(rA.u) && alive;
+    if constexpr (!DENSE) resolve(s, rA, rB, pop);
+    TraceRoute rC;
     if constexpr (DENSE || MAPLDS) {
-      load_idx(s + 2, idx_self);
-      const int rrow = classify(s + 1, idx_other, -1, -1, r1, r0, q, route_ok(r0.u));
-      after_classify(s + 1, r1, pop_self);
-      publish_rows(s + 1, r1, rrow);
-    } else {
       load_idx(s + 3, idx_self);
-      issue_map(idx_other, mw_self, mr_self);   // step s+2
+      const int rrow = classify(s + 2, idx_other, -1, -1, rC, rB, rA, route_ok(rB.u));
+      after_classify(s + 2, rC, pop);
+      publish_rows(s + 2, rC, rrow);
+    } else {
+      load_idx(s + 4, idx_self);
+      issue_map(idx_other, mw_self, mr_self);   // step s+3
       ready2 = idx_other;
-      const int rrow = classify(s + 1, ready1, mw_other, mr_other, r1, r0, q, route_ok(r0.u));
-      after_classify(s + 1, r1, pop_self);
-      publish_rows(s + 1, r1, rrow);
+      const int rrow = classify(s + 2, ready1, mw_other, mr_other, rC, rB, rA, route_ok(rB.u));
+      after_classify(s + 2, rC, pop);
+      publish_rows(s + 2, rC, rrow);
       ready1 = ready2;
     }
-    const bool run = route_ok(r0.u) && alive;
-    if constexpr (!DENSE) resolve(s, r0, r1, pop_other);
-    publish_step(s, r0, run, alive);
-    issue_proof(s);
+    publish_step(s, rA, run, alive);
+    prove(s + 2, rC, pop);
     if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | static_cast<uint32_t>(s + 2));
-    q = r0;
-    r0 = r1;
+    rA = rB;
+    rB = rC;
   };
   // Drain the prologue's loads (see the data wave).
   __builtin_amdgcn_s_waitcnt(0);
@@ -1044,7 +1095,7 @@ void sdm_trace_kernel(StepParams P) {
   int s = 0;
   bool stopped = false;
   for (; s + 1 < G; s += 2) {
-    if (!room(s + 3 - kTraceRing)) {
+    if (!room(s + 4 - kTraceRing)) {
       // the data wave stopped taking steps: record it and stop here
       if (lane == 0 && !DENSE) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
@@ -1055,15 +1106,16 @@ void sdm_trace_kernel(StepParams P) {
       stopped = true;
       break;
     }
-    if (proof_stops(s, r0, popB)) {
+    // a failed proof before step s (decided in iteration s-2) halts here
+    if (halted) {
       stopped = true;
       break;
     }
-    iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
-    iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB, popA);
+    iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
+    iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB);
   }
   if (!stopped && s < G) {
-    if (!room(s + 2 - kTraceRing)) {
+    if (!room(s + 3 - kTraceRing)) {
       if (lane == 0 && !DENSE) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                               static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
@@ -1071,10 +1123,10 @@ void sdm_trace_kernel(StepParams P) {
       }
       done_steps = s;
       stopped = true;
-    } else if (proof_stops(s, r0, popB)) {
+    } else if (halted) {
       stopped = true;
     } else {
-      iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA, popB);
+      iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
     }
   }
   // the data wave computes the steps before done_steps, and no more
