@@ -786,6 +786,11 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
         }
       }
       if (launched) continue;
+      if (P.trace_proof_rows > 0) {
+        // one launch per step would skip the proofs the caller asked for
+        return fail(COWSDM_ELIMIT, "trace: capacity proofs need a persistent launch, and not "
+                                   "even one layer's workgroups fit on the device at once");
+      }
       P.steps = steps;
       P.trace_first = trace->first_step;
     }

@@ -172,6 +172,17 @@ __device__ __forceinline__ void sync_store(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Sum over the wave of per-lane counts of one launch's first touches (at
+// most kTraceMaxWrites * kTraceMaxSteps = 1024 per bank, 11 bits), by bit
+// planes: ballots and scalar adds, no LDS round trip.
+__device__ __forceinline__ int wave_sum_launch(int v) {
+  static_assert(kTraceMaxWrites * kTraceMaxSteps < (1 << 11), "counts exceed 11 bits");
+  int sum = 0;
+#pragma unroll
+  for (int b = 0; b < 11; ++b) sum += __popcll(__ballot((v >> b) & 1)) << b;
+  return sum;
+}
+
 // Source row (0..3) of entry i from two bit planes of a control word.
 __device__ __forceinline__ int plane_code(uint32_t w, int lo, int hi) {
   return static_cast<int>(((w >> lo) & 1u) | (((w >> hi) & 1u) << 1));
@@ -350,9 +361,9 @@ void sdm_trace_kernel(StepParams P) {
       wv[kWave + lane] = FULL || lane < R ? rw : -0.0f;
     };
 
-    // What the data wave reads from LDS for a step, one iteration before it
-    // needs it: step t+1's row addresses (a broadcast read gives every lane
-    // two of them), step t's masks, store rows and weights.
+    // What the data wave reads from LDS for a step: step t+1's row addresses
+    // (a broadcast read gives every lane two of them), and, one iteration
+    // before it needs them, step t's masks, store rows and weights.
     constexpr int kPtrPairs = (kTraceMaxWrites + kTraceMaxReads) / 2;
     struct Handed {
       u64x2_t ptr[kPtrPairs];  // wptr then rptr, as laid out in the slot
@@ -563,21 +574,22 @@ void sdm_trace_kernel(StepParams P) {
       load_weights(1, wwB, rwB);     // handed over at the end of iteration 0
     }
 
-    // Iteration t: loads step t+1's rows, computes step t, then reads what
-    // iteration t+1 needs from LDS.  The progress word goes out after this
-    // step's LDS writes and before those reads, so its release waits for no
-    // read in flight.
+    // Iteration t: loads step t+1's rows, computes step t, then reads step
+    // t+1's masks, store rows and weights from LDS.  The progress word goes
+    // out after this step's LDS writes and before those reads, so its release
+    // waits for no read in flight.  (The row addresses are read just before
+    // their loads: held across an iteration they would cost 40 registers.)
     Handed hd;
     auto iteration = [&](int t, TraceRows<VEC>& rows_t, TraceRows<VEC>& rows_next,
                          float& ww_self, float& rw_self, float ww_other, float rw_other)
         __attribute__((always_inline)) {
       load_weights(t + 2, ww_self, rw_self);
+      read_ptrs(t + 1, hd);
       issue_rows(t + 1, hd, rows_next);
       compute(t, hd, rows_t);
       put_weights(ww_other, rw_other);   // step t+1's
       if (lane == 0) sync_store(&sync[1], static_cast<uint32_t>(t + 1));
       read_step(t + 1, hd);
-      read_ptrs(t + 2, hd);
     };
 
     // the published steps the reads of iteration t+1 need (capped at what
@@ -591,7 +603,6 @@ void sdm_trace_kernel(StepParams P) {
       read_ptrs(0, hd);
       issue_rows(0, hd, bufA);
       read_step(0, hd);
-      read_ptrs(1, hd);
     }
     // Drain the prologue's loads: the loop head then has one state of loads
     // in flight (the back edge's), and the waits the compiler places there
@@ -904,53 +915,82 @@ void sdm_trace_kernel(StepParams P) {
   int runs_published = 0;
   int next_proof = 0;                 // step of the next proof
   uint64_t pw[SCANW];                 // the published counts of the next proof
+  // this lane's bank in each window: its last count known exactly, and the
+  // number of runs that count covers
+  int known[SCANW], known_runs[SCANW];
 #pragma unroll
-  for (int k = 0; k < SCANW; ++k) pw[k] = 0;
+  for (int k = 0; k < SCANW; ++k) {
+    pw[k] = 0;
+    known[k] = 0;
+    known_runs[k] = 0;
+  }
+  // Bank b's count after its r-th run is word b * P.steps + r of the slots
+  // (a launch has fewer runs than steps): each bank writes words of its own,
+  // never a cache line another bank writes to.
+  const int64_t run_stride = P.steps;
   const int64_t* run_l[SCANW];        // this lane's bank in each window
 #pragma unroll
   for (int k = 0; k < SCANW; ++k) {
     const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
-    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk;
+    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk * run_stride;
   }
 
   // Does the proof before step s stop the layer?  Wave-uniform: every wave
-  // sums the same counts, the first touches of every bank before step s.
+  // decides from the same counts, the first touches of every bank before
+  // step s.  A bank whose count for the run just ended has not arrived is
+  // bounded by its last known count plus W first touches per step since:
+  // when the layer passes even so, it passes exactly, and only otherwise
+  // does the wave wait for the missing counts.
   auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {
-    int total = 0;
-    if (s > 0) {
-      const uint32_t off = static_cast<uint32_t>(s / proof_steps * B);
-      auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-        return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
-      };
-#pragma unroll
-      for (int k = 0; k < SCANW; ++k) {
-        if (k * kWave < B) {
-          uint64_t w = pw[k];
-          bool ready = word_ready(w);
-          if (__ballot(!ready) != 0) {
-            // a bank has not finished the run yet: bounded wait
-            int spins = 0;
-            while (!ready && spins < kSpinLimit) {
-              __builtin_amdgcn_s_sleep(1);
-              w = atomic_load_u64(run_l[k] + off);
-              ready = word_ready(w);
-              ++spins;
-            }
-            if (__ballot(!ready) != 0) {
-              // never arrived: record it and stop the layer here
-              if (lane == 0) {
-                __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                      static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              }
-              return true;
-            }
-          }
-          const bool in = k * kWave + lane < B;
-          total += static_cast<int>(wave_sum64(in ? static_cast<int64_t>(w & kValueMask) : 0));
-        }
+    if (s == 0) return old_free < proof_rows;
+    const int r = s / proof_steps;   // runs that end before step s
+    const int per_run = W * proof_steps;
+    const uint32_t off = static_cast<uint32_t>(r);
+    auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+      return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
+    };
+    auto take = [&](int k, uint64_t w) __attribute__((always_inline)) {
+      if (word_ready(w)) {
+        known[k] = static_cast<int>(w & kValueMask);
+        known_runs[k] = r;
       }
-      total = __builtin_amdgcn_readfirstlane(total);
+    };
+    int upper = 0;
+    uint64_t missing = 0;
+#pragma unroll
+    for (int k = 0; k < SCANW; ++k) {
+      if (k * kWave < B) {
+        take(k, pw[k]);
+        const bool in = k * kWave + lane < B;
+        upper += wave_sum_launch(in ? known[k] + per_run * (r - known_runs[k]) : 0);
+        missing |= __ballot(in && known_runs[k] != r);
+      }
+    }
+    if (old_free - upper >= proof_rows) return false;
+    if (missing == 0) return true;
+    // the bound decides nothing: wait (bounded) for the missing counts
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < SCANW; ++k) {
+      if (k * kWave < B) {
+        const bool in = k * kWave + lane < B;
+        int spins = 0;
+        while (__ballot(in && known_runs[k] != r) != 0 && spins < kSpinLimit) {
+          __builtin_amdgcn_s_sleep(1);
+          if (known_runs[k] != r) take(k, atomic_load_u64(run_l[k] + off));
+          ++spins;
+        }
+        if (__ballot(in && known_runs[k] != r) != 0) {
+          // never arrived: record it and stop the layer here
+          if (lane == 0) {
+            __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                  static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          return true;
+        }
+        total += wave_sum_launch(in ? known[k] : 0);
+      }
     }
     return old_free - total < proof_rows;
   };
@@ -966,7 +1006,7 @@ void sdm_trace_kernel(StepParams P) {
         if (run_left == 0) {
           ++runs_published;
           if (t < G && lane == 0) {
-            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + runs_published * B + bank,
+            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + runs_published,
                              slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(cum)));
           }
           run_left = proof_steps;
@@ -999,7 +1039,7 @@ void sdm_trace_kernel(StepParams P) {
   auto issue_proof = [&](int s) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (proofs && s + 2 == next_proof && !halted) {
-        const uint32_t off = static_cast<uint32_t>((s + 2) / proof_steps * B);
+        const uint32_t off = static_cast<uint32_t>((s + 2) / proof_steps);
 #pragma unroll
         for (int k = 0; k < SCANW; ++k) {
           if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + off);
@@ -1215,10 +1255,29 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
     }
     resident_slots[variant][which] = key;
   }
-  if (blocks > resident[variant][which]) return false;
-  void* args[] = {&P};
-  (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kTraceThreads), args, lds_bytes, stream);
-  return true;  // a failed launch is reported by the caller's launch_status()
+  // Layers are independent within a launch: when the whole grid cannot be
+  // resident, launch groups of layers that can, one after another on the
+  // stream, each with its per-layer words offset to its first layer.
+  const int per_launch = resident[variant][which] / P.blocks_per_layer;
+  if (per_launch <= 0) return false;
+  if (blocks <= resident[variant][which]) {
+    void* args[] = {&P};
+    (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kTraceThreads), args, lds_bytes, stream);
+    return true;  // a failed launch is reported by the caller's launch_status()
+  }
+  for (int l0 = 0; l0 < P0.nlayers; l0 += per_launch) {
+    StepParams Q = P;
+    Q.nlayers = P0.nlayers - l0 < per_launch ? P0.nlayers - l0 : per_launch;
+    for (int i = 0; i < kMaxLayers; ++i) Q.layer[i] = P0.layer[l0 + i < P0.nlayers ? l0 + i : l0];
+    if (P0.trace_step) Q.trace_step = P0.trace_step + l0;
+    if (P0.trace_ticket) Q.trace_ticket = P0.trace_ticket + l0;  // word 1 + layer
+    if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
+    if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
+    void* args[] = {&Q};
+    (void)hipLaunchKernel(kernel, dim3(Q.blocks_per_layer * Q.nlayers), dim3(kTraceThreads), args,
+                          lds_bytes, stream);
+  }
+  return true;
 }
 
 template <typename IDX, bool DENSE>

@@ -110,6 +110,39 @@ def test_config2_and_config3_handoff_then_decode(device, prefix, steps):
     _check(traced, host, dense, outputs, want, dense_out)
 
 
+def test_layer_groups_when_grid_exceeds_residency(device):
+    """8 layers x 256 banks is twice the workgroups the device holds at once:
+    the persistent decode runs the layers in groups, each still proven on the
+    device, and matches the dense decode and the host-proven loop."""
+
+    heads, requests, slots, steps, proof_steps, layers = 4, 64, 64, 48, 4, 8
+    banks = heads * requests
+    print(f"layer groups: L={layers} banks={banks} N={slots} steps={steps}", flush=True)
+    quantum = banks * W * proof_steps
+    m0 = synthetic.make_initial_memory(layers, heads, slots, D, seed=61, device=device)
+    templates = torch.arange(heads, dtype=torch.int64, device=device).repeat(requests)
+    batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=62,
+                        heads=heads)
+
+    def states():
+        return [cow.PackedSDMCopyOnWriteState.allocate(
+            m0[l], banks=banks, capacity_rows=quantum, template_indices=templates,
+            growth_quantum_rows=quantum) for l in range(layers)]
+
+    traced, host = states(), states()
+    dense = [m0[l][templates].contiguous() for l in range(layers)]
+    outputs = torch.empty(steps, layers, banks, D, device=device)
+    report = cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps,
+                                                                      proof_steps=proof_steps)
+    assert report["growth_rounds"] > 0
+    dense_out = torch.empty_like(outputs)
+    cow.DecodeTrace(memories=dense, outputs=dense_out, **kw).launch(steps, start=0)
+    want = _host_proven(host, batch, steps=steps, layers=layers, banks=banks,
+                        proof_steps=proof_steps)
+    torch.cuda.synchronize()
+    _check(traced, host, dense, outputs, want, dense_out)
+
+
 def test_config5_layer_zipf_growth(device):
     heads, requests, slots, steps, proof_steps = 4, 64, 65536, 64, 4
     banks = heads * requests
