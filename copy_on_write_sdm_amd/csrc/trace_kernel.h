@@ -211,6 +211,11 @@ void sdm_trace_kernel(StepParams P) {
   // published (the masks and store rows of all but the last of them);
   // [1]: data -> control, steps computed
   __shared__ uint32_t lds_sync[NB][2];
+  // control wave: the slots of two 64-step chunks, per step W write slots
+  // then R read slots (-1: outside [0, N)), staged from registers a chunk
+  // ahead (map in LDS, or dense)
+  constexpr int kIdxRow = kTraceMaxWrites + kTraceMaxReads;
+  __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxRow];
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -685,6 +690,56 @@ void sdm_trace_kernel(StepParams P) {
     m.ridx = (lane < R && !br) ? static_cast<int>(xr) : 0;
   };
 
+  // Map in LDS (or dense): the slots reach the wave through LDS, 64 steps at
+  // a time.  Lane l loads step 64c + l of chunk c into registers a chunk
+  // ahead and writes it to LDS when the chunk before starts being used, so
+  // vector memory is waited on once per 64 steps instead of every step (it
+  // completes in order, so a per-step wait would also wait for every claim
+  // and device-scope store issued before it).
+  const char* const wbase = first_step(L.write_indices, 0) + static_cast<int64_t>(bank) * W * sizeof(IDX);
+  const char* const rbase = first_step(L.read_indices, 6) + static_cast<int64_t>(bank) * R * sizeof(IDX);
+  IDX chunk[kIdxRow];
+#pragma unroll
+  for (int k = 0; k < kIdxRow; ++k) chunk[k] = 0;
+  auto load_chunk = [&](int c) __attribute__((always_inline)) {
+    const int st = c * kWave + lane < G ? c * kWave + lane : G - 1;
+    const char* const w = at(wbase, st_wi, st);
+    const char* const r = at(rbase, st_ri, st);
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      chunk[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : 0) * sizeof(IDX));
+    }
+#pragma unroll
+    for (int i = 0; i < kTraceMaxReads; ++i) {
+      chunk[kTraceMaxWrites + i] =
+          *(const __attribute__((address_space(1))) IDX*)(r + (i < R ? i : 0) * sizeof(IDX));
+    }
+  };
+  auto write_chunk = [&](int c) __attribute__((always_inline)) {
+    int v[kIdxRow];
+#pragma unroll
+    for (int k = 0; k < kIdxRow; ++k) {
+      const int64_t x = static_cast<int64_t>(chunk[k]);
+      v[k] = x >= 0 && x < N ? static_cast<int>(x) : -1;
+    }
+    i32x4_t* const row = reinterpret_cast<i32x4_t*>(&lds_idx[(DENSE || MAPLDS) ? pair : 0][c & 1][lane][0]);
+#pragma unroll
+    for (int k = 0; k < kIdxRow / 4; ++k) {
+      i32x4_t q;
+      q.x = v[4 * k]; q.y = v[4 * k + 1]; q.z = v[4 * k + 2]; q.w = v[4 * k + 3];
+      row[k] = q;
+    }
+  };
+  auto read_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
+    const int tc = t < G ? t : G - 1;
+    const int* const row = &lds_idx[(DENSE || MAPLDS) ? pair : 0][(tc >> 6) & 1][tc & (kWave - 1)][0];
+    const int xw = row[lane < kTraceMaxWrites ? lane : 0];
+    const int xr = row[kTraceMaxWrites + (lane < kTraceMaxReads ? lane : 0)];
+    m.err = (lane < W && xw < 0 ? COWSDM_ERR_WRITE_INDEX : 0) | (lane < R && xr < 0 ? COWSDM_ERR_READ_INDEX : 0);
+    m.widx = lane < W && xw >= 0 ? xw : 0;
+    m.ridx = lane < R && xr >= 0 ? xr : 0;
+  };
+
   auto issue_map = [&](const TraceIdx& m, int& wraw, int& rraw) __attribute__((always_inline)) {
     wraw = -1;
     rraw = -1;
@@ -839,13 +894,18 @@ void sdm_trace_kernel(StepParams P) {
 
   // Step t's first touches claim their rows: one atomic add per (step, bank)
   // with first touches, its result read when the step resolves.
+  // The atomic is 32-bit, on the counter's low word: a launch claims at most
+  // W * B * G < 2^31 rows, so the high word stays zero and 64-bit reads of the
+  // counter hold the total.  (A 64-bit atomic would leave the returned high
+  // half unused; the compiler reuses that register, and writing a register a
+  // load or atomic in flight will write waits for every access in flight.)
+  int32_t* const claims32 = DENSE ? nullptr : reinterpret_cast<int32_t*>(claims);
   auto claim = [&](const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (route_count(rt.u) > 0 && route_ok(rt.u)) {
         if (lane == 0) {
-          home = static_cast<int>(__hip_atomic_fetch_add(
-              claims, static_cast<int64_t>(route_count(rt.u)), __ATOMIC_RELAXED,
-              __HIP_MEMORY_SCOPE_AGENT));
+          home = __hip_atomic_fetch_add(claims32, static_cast<int32_t>(route_count(rt.u)),
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
@@ -1071,10 +1131,20 @@ void sdm_trace_kernel(StepParams P) {
   TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
   q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
   q.fwd = 0; q.rawm = 0;
+  if constexpr (DENSE || MAPLDS) {
+    load_chunk(0);
+    write_chunk(0);
+    if (G > kWave) load_chunk(1);  // written before step 64 is read
+  }
   {
     TraceIdx i0, i1;
-    load_idx(0, i0);
-    load_idx(1, i1);
+    if constexpr (DENSE || MAPLDS) {
+      read_idx(0, i0);
+      read_idx(1, i1);
+    } else {
+      load_idx(0, i0);
+      load_idx(1, i1);
+    }
     int mw0, mr0, mw1, mr1;
     issue_map(i0, mw0, mr0);
     issue_map(i1, mw1, mr1);
@@ -1088,7 +1158,7 @@ void sdm_trace_kernel(StepParams P) {
   }
   if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | 1u);
   if constexpr (DENSE || MAPLDS) {
-    load_idx(2, idxB);             // classified in iteration 0
+    read_idx(2, idxB);             // classified in iteration 0
   } else {
     load_idx(2, ready1);           // its map entries, classified in iteration 0
     issue_map(ready1, mwB, mrB);
@@ -1110,7 +1180,7 @@ void sdm_trace_kernel(StepParams P) {
     if constexpr (!DENSE) resolve(s, rA, rB, pop);
     TraceRoute rC;
     if constexpr (DENSE || MAPLDS) {
-      load_idx(s + 3, idx_self);
+      read_idx(s + 3, idx_self);
       const int rrow = classify(s + 2, idx_other, -1, -1, rC, rB, rA, route_ok(rB.u));
       after_classify(s + 2, rC, pop);
       publish_rows(s + 2, rC, rrow);
@@ -1150,6 +1220,15 @@ void sdm_trace_kernel(StepParams P) {
     if (halted) {
       stopped = true;
       break;
+    }
+    if constexpr (DENSE || MAPLDS) {
+      // chunk c's first slots are read in iteration 64c - 3; the buffer it
+      // replaces held chunk c - 2, whose last step was read long before
+      if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
+        const int c = (s + 4) >> 6;
+        write_chunk(c);
+        if ((c + 1) * kWave < G) load_chunk(c + 1);
+      }
     }
     iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
     iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB);
