@@ -89,10 +89,12 @@ __device__ __forceinline__ int route_count(uint32_t u) { return static_cast<int>
 __device__ __forceinline__ bool route_ok(uint32_t u) { return (u >> 8) & 1u; }
 
 // One step handed from the control wave to the data wave.
+// The per-lane arrays have kTraceMaxReads entries (writes use the first
+// kTraceMaxWrites), so that lanes 0-15 write all three in one store pass.
 struct TraceSlot {
-  uint64_t wptr[kTraceMaxWrites];   // address of write j's row before the step
+  uint64_t wptr[kTraceMaxReads];    // address of write j's row before the step
   uint64_t rptr[kTraceMaxReads];    // address of read i's row (a zero row past R)
-  int32_t drow[kTraceMaxWrites];    // row write j's update is stored to
+  int32_t drow[kTraceMaxReads];     // row write j's update is stored to
   // ctl[0]: bits 0-19 rows forwarded from the step before (0-3 writes, 4-19
   //         reads), bit 20 the step runs, bits 24-27 write rows to store;
   // ctl[1]: bits 0-15 reads of the step's own writes, bits 16-19 and 20-23
@@ -371,16 +373,20 @@ void sdm_trace_kernel(StepParams P) {
     // before it needs them, step t's masks, store rows and weights.
     constexpr int kPtrPairs = (kTraceMaxWrites + kTraceMaxReads) / 2;
     struct Handed {
-      u64x2_t ptr[kPtrPairs];  // wptr then rptr, as laid out in the slot
+      u64x2_t ptr[kPtrPairs];  // the W write addresses, then the R read addresses
       u32x4_t cw;
       i32x4_t dr;
       vf4_t wwv;
       vf4_t rwv[kTraceMaxReads / 4];
     };
     auto read_ptrs = [&](int t, Handed& h) __attribute__((always_inline)) {
-      const u64x2_t* const p = reinterpret_cast<const u64x2_t*>(slot_of(t).wptr);
+      const TraceSlot& sl = slot_of(t);
+      const u64x2_t* const pw = reinterpret_cast<const u64x2_t*>(sl.wptr);
+      const u64x2_t* const pr = reinterpret_cast<const u64x2_t*>(sl.rptr);
 #pragma unroll
-      for (int k = 0; k < kPtrPairs; ++k) h.ptr[k] = p[k];
+      for (int k = 0; k < kTraceMaxWrites / 2; ++k) h.ptr[k] = pw[k];
+#pragma unroll
+      for (int k = 0; k < kTraceMaxReads / 2; ++k) h.ptr[kTraceMaxWrites / 2 + k] = pr[k];
     };
     // lane j put weight j there: every lane reads all of them as vectors,
     // instead of a readlane per weight
@@ -840,14 +846,14 @@ void sdm_trace_kernel(StepParams P) {
   };
 
   // Publish step t's row addresses: lane j's write row and read row.
-  auto publish_rows = [&](int t, const TraceRoute& rt, int rrow) __attribute__((always_inline)) {
+  // Lane j's write row and read row of a step (M0 row or slab row).
+  auto row_addrs = [&](const TraceRoute& rt, int rrow, const float*& wp, const float*& rp)
+      __attribute__((always_inline)) {
     // row r of a base: base + r * D floats, r non-negative
     auto row_at = [&](const float* base, int r) __attribute__((always_inline)) -> const float* {
       return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) +
                                             static_cast<uint64_t>(static_cast<uint32_t>(r)) * row_bytes);
     };
-    const float* wp;
-    const float* rp;
     if constexpr (DENSE) {
       wp = row_at(table_bank, rt.widx);
       rp = row_at(table_bank, rt.ridx);
@@ -858,32 +864,58 @@ void sdm_trace_kernel(StepParams P) {
     if constexpr (!FULL) {
       if (lane >= R) rp = kTraceZeroRow;
     }
+  };
+  // Publish step t's row addresses (the prologue's steps).
+  auto publish_rows = [&](int t, const TraceRoute& rt, int rrow) __attribute__((always_inline)) {
+    const float* wp;
+    const float* rp;
+    row_addrs(rt, rrow, wp, rp);
     TraceSlot& sl = slot_of(t);
-    if (lane < kTraceMaxWrites) sl.wptr[lane] = reinterpret_cast<uint64_t>(wp);
-    if (lane < kTraceMaxReads) sl.rptr[lane] = reinterpret_cast<uint64_t>(rp);
+    if (lane < kTraceMaxReads) {
+      sl.wptr[lane] = reinterpret_cast<uint64_t>(wp);
+      sl.rptr[lane] = reinterpret_cast<uint64_t>(rp);
+    }
   };
 
-  // Publish step t's masks and the rows its updates are stored to.  run: the
-  // step runs; fitted: its first touches got rows.
-  auto publish_step = [&](int t, const TraceRoute& rt, bool run, bool fitted)
-      __attribute__((always_inline)) {
-    TraceSlot& sl = slot_of(t);
+  // End of iteration s: publish step s+2's row addresses (rc, rrow), step
+  // s's store rows and masks (rt; run: it runs, fitted: its first touches
+  // got rows) and the progress word, in one store pass of lanes 0-15 and one
+  // of lane 0.  The source-row planes of forwarded rows are only built for a
+  // step that forwards some.
+  auto publish = [&](int s, const TraceRoute& rt, bool run, bool fitted, const TraceRoute& rc,
+                     int rrow) __attribute__((always_inline)) {
+    const float* wp;
+    const float* rp;
+    row_addrs(rc, rrow, wp, rp);
     const uint32_t fm = route_fmask(rt.u);
     const uint32_t smask = run ? ((static_cast<uint32_t>(wlanes) & ~fm) | (fitted ? fm : 0u)) : 0u;
-    if (lane < kTraceMaxWrites) sl.drow[lane] = DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow);
-    const uint32_t w0 = static_cast<uint32_t>(__ballot((rt.wsrc & 1) != 0)) & 15u;
-    const uint32_t w1 = static_cast<uint32_t>(__ballot((rt.wsrc & 2) != 0)) & 15u;
-    const uint32_t f0 = static_cast<uint32_t>(__ballot((rt.rsrc & 1) != 0)) & 0xFFFFu;
-    const uint32_t f1 = static_cast<uint32_t>(__ballot((rt.rsrc & 2) != 0)) & 0xFFFFu;
-    const uint32_t a0 = static_cast<uint32_t>(__ballot((rt.rraw & 1) != 0)) & 0xFFFFu;
-    const uint32_t a1 = static_cast<uint32_t>(__ballot((rt.rraw & 2) != 0)) & 0xFFFFu;
-    if (lane == 0) {
-      u32x4_t c;
-      c.x = rt.fwd | (run ? 1u << 20 : 0u) | (smask << 24);
-      c.y = rt.rawm | (w0 << 16) | (w1 << 20);
+    const int drow = DENSE ? rt.widx : (rt.wrow < 0 ? 0 : rt.wrow);
+    u32x4_t c;
+    c.x = rt.fwd | (run ? 1u << 20 : 0u) | (smask << 24);
+    c.y = rt.rawm;
+    c.z = 0;
+    c.w = 0;
+    if ((rt.fwd | rt.rawm) != 0) {
+      const uint32_t w0 = static_cast<uint32_t>(__ballot((rt.wsrc & 1) != 0)) & 15u;
+      const uint32_t w1 = static_cast<uint32_t>(__ballot((rt.wsrc & 2) != 0)) & 15u;
+      const uint32_t f0 = static_cast<uint32_t>(__ballot((rt.rsrc & 1) != 0)) & 0xFFFFu;
+      const uint32_t f1 = static_cast<uint32_t>(__ballot((rt.rsrc & 2) != 0)) & 0xFFFFu;
+      const uint32_t a0 = static_cast<uint32_t>(__ballot((rt.rraw & 1) != 0)) & 0xFFFFu;
+      const uint32_t a1 = static_cast<uint32_t>(__ballot((rt.rraw & 2) != 0)) & 0xFFFFu;
+      c.y |= (w0 << 16) | (w1 << 20);
       c.z = f0 | (f1 << 16);
       c.w = a0 | (a1 << 16);
-      *reinterpret_cast<u32x4_t*>(sl.ctl) = c;
+    }
+    TraceSlot& ahead = slot_of(s + 2);
+    TraceSlot& now = slot_of(s);
+    if (lane < kTraceMaxReads) {
+      ahead.wptr[lane] = reinterpret_cast<uint64_t>(wp);
+      ahead.rptr[lane] = reinterpret_cast<uint64_t>(rp);
+      now.drow[lane] = drow;
+    }
+    if (lane == 0) {
+      *reinterpret_cast<u32x4_t*>(now.ctl) = c;
+      sync_store(&sync[0], (kNoStop << 16) | static_cast<uint32_t>(s + 2));
     }
   };
 
@@ -1179,23 +1211,21 @@ void sdm_trace_kernel(StepParams P) {
     const bool run = route_ok(rA.u) && alive;
     if constexpr (!DENSE) resolve(s, rA, rB, pop);
     TraceRoute rC;
+    int rrow;
     if constexpr (DENSE || MAPLDS) {
       read_idx(s + 3, idx_self);
-      const int rrow = classify(s + 2, idx_other, -1, -1, rC, rB, rA, route_ok(rB.u));
+      rrow = classify(s + 2, idx_other, -1, -1, rC, rB, rA, route_ok(rB.u));
       after_classify(s + 2, rC, pop);
-      publish_rows(s + 2, rC, rrow);
     } else {
       load_idx(s + 4, idx_self);
       issue_map(idx_other, mw_self, mr_self);   // step s+3
       ready2 = idx_other;
-      const int rrow = classify(s + 2, ready1, mw_other, mr_other, rC, rB, rA, route_ok(rB.u));
+      rrow = classify(s + 2, ready1, mw_other, mr_other, rC, rB, rA, route_ok(rB.u));
       after_classify(s + 2, rC, pop);
-      publish_rows(s + 2, rC, rrow);
       ready1 = ready2;
     }
-    publish_step(s, rA, run, alive);
     prove(s + 2, rC, pop);
-    if (lane == 0) sync_store(&sync[0], (kNoStop << 16) | static_cast<uint32_t>(s + 2));
+    publish(s, rA, run, alive, rC, rrow);
     rA = rB;
     rB = rC;
   };
