@@ -1171,6 +1171,9 @@ class DecodeTrace:
         self.step_index = torch.zeros(layers, dtype=torch.int64, device=device)
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.status = torch.zeros(layers, dtype=torch.int32, device=device)
+        # the kernels only set status bits: run() clears them when a launch
+        # may have left some (a refusal, a direct launch)
+        self._status_clean = True
         self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
         self.trace.step_index = self.step_index.data_ptr()
@@ -1238,6 +1241,7 @@ class DecodeTrace:
         layers = self.layer_array() if layers is None else layers
         stream = nat.stream_handle(self.device)
         self.trace.persistent = int(self.persistent)
+        self._status_clean = False
         if start is None:
             self._positions = None
             self.trace.step_index = self.step_index.data_ptr()
@@ -1305,7 +1309,9 @@ class DecodeTrace:
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.first_step = 0
         self.trace.persistent = int(self.persistent)
-        self.status.zero_()
+        if not self._status_clean:
+            self.status.zero_()
+        self._status_clean = False
         stream = nat.stream_handle(self.device)
         launches = rounds = 0
         remaining = steps
@@ -1326,6 +1332,9 @@ class DecodeTrace:
                 positions = self.step_index.tolist()
                 behind = [l for l, p in enumerate(positions) if p < target]
                 if not behind:
+                    # without growth rounds every layer ran from the same
+                    # step and none stopped short: no launch set a status bit
+                    self._status_clean = rounds == 0
                     break
                 status = self.status.tolist()
                 refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]

@@ -32,6 +32,11 @@ constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are sta
 constexpr int kTraceBanksPerBlock = 2;      // banks per persistent workgroup
 constexpr int kTraceThreads = 2 * kWave * kTraceBanksPerBlock;  // a control and a data wave per bank
 constexpr int kTraceRing = 16;              // steps handed from control to data wave in flight
+// packed layers of at most 64 banks: a fifth wave sums the capacity proofs
+constexpr int kTraceProofThreads = kTraceThreads + kWave;
+// claim counters of the runs of one launch (runs of at least 2 steps), at the
+// end of a layer's scan words
+constexpr int kTraceRunCounters = kTraceMaxSteps / 2 + 1;
 constexpr int64_t kClaimFailBase = int64_t{1} << 40;  // failed claim p recorded as base - p
 
 constexpr uint32_t kStatusEmpty = 0;

@@ -727,7 +727,8 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
       shape->writes <= kTraceMaxWrites && shape->reads <= kTraceMaxReads &&
       nlayers <= kMaxLayers &&
       (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan && trace->ticket &&
-                 trace->scan_words >= COWSDM_SCRATCH_SLOTS + chunk * shape->banks));
+                 trace->scan_words >= COWSDM_SCRATCH_SLOTS + chunk * shape->banks +
+                                          kTraceRunCounters));
   (void)blocks_per_layer_p;
   StepParams P;
   P.trace_step = trace ? trace->step_index : nullptr;
@@ -850,7 +851,7 @@ int64_t cowsdm_step_scratch_words(int64_t banks) {
 
 int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps) {
   if (banks < 0 || steps < 0) return -1;
-  return COWSDM_SCRATCH_SLOTS + banks * steps;
+  return COWSDM_SCRATCH_SLOTS + banks * steps + kTraceRunCounters;
 }
 
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows) {

@@ -42,9 +42,15 @@
 // finish writes free_count = F - (claims that fit) and clears the counter.
 // Banks do not otherwise wait on one another, except for the capacity proof:
 // with proofs on, each bank publishes its first touches so far at the end of
-// each run of proof steps, and every control wave sums them before the next
-// run starts, so all banks of the layer stop at the same step.  The claims
-// of a run's first step wait for that proof.
+// each run of proof steps, and before a run starts every control wave takes
+// their sum, so all banks of the layer stop at the same step.  With the map
+// in LDS a bank counts first touches from its write slots a 64-step chunk
+// ahead, so the counts are out long before a proof needs them; in layers of
+// at most 64 banks a fifth wave of each workgroup sums them and hands the
+// sum to the control waves through LDS.  Claims do not wait for proofs: each
+// run claims on a counter of its own, and the proof's sum is the run's base
+// (rows are claimed at base + p); a run that fails its proof never takes the
+// rows it claimed.
 #pragma once
 
 #include "common.h"
@@ -195,8 +201,10 @@ __device__ __forceinline__ int plane_code(uint32_t w, int lo, int hi) {
 // selects and the zero rows that leave the others out.
 // SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
 // MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per bank).
+// A packed kernel with SCANW 1 runs a fifth wave per workgroup that sums the
+// capacity proofs (kTraceProofThreads threads); the others run kTraceThreads.
 template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW, bool MAPLDS>
-__global__ __launch_bounds__(kTraceThreads)
+__global__ __launch_bounds__(!DENSE && SCANW == 1 ? kTraceProofThreads : kTraceThreads)
 __attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
 void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
@@ -218,10 +226,20 @@ void sdm_trace_kernel(StepParams P) {
   // ahead (map in LDS, or dense)
   constexpr int kIdxRow = kTraceMaxWrites + kTraceMaxReads;
   __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxRow];
+  // control wave (map in LDS): one bit per slot, set when the slot was
+  // mapped at the launch's start or is written by a step the first-touch
+  // count has passed
+  __shared__ uint32_t lds_seen[MAPLDS ? NB : 1][MAPLDS ? kTraceMapSlots / 32 : 1];
+  // proof wave -> control waves: the layer's first touches before run r
+  // (-1: a bank's count never arrived), and the last run summed
+  constexpr bool PWAVE = !DENSE && SCANW == 1;
+  __shared__ int lds_proof[PWAVE ? kTraceRunCounters : 1];
+  __shared__ uint32_t lds_proof_done;
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const int pair = wave >> 1;
+  const bool proof_wave = wave == 2 * NB;
+  const int pair = proof_wave ? 0 : wave >> 1;
   const bool data_wave = (wave & 1) != 0;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int layer_id = blockIdx.x / P.blocks_per_layer;
@@ -280,15 +298,73 @@ void sdm_trace_kernel(StepParams P) {
     } else {
       window = old_free < kTraceFreeWindow ? old_free : kTraceFreeWindow;
     }
-    for (int k = static_cast<int>(threadIdx.x); k < window; k += kTraceThreads) {
+    for (int k = static_cast<int>(threadIdx.x); k < window; k += static_cast<int>(blockDim.x)) {
       lds_free[k] = L.free_rows[old_free - 1 - k];
     }
   }
-  if (lane == 0 && !data_wave) {
+  if (lane == 0 && !data_wave && !proof_wave) {
     lds_sync[pair][0] = kNoStop << 16;
     lds_sync[pair][1] = 0;
   }
+  if (threadIdx.x == 0) lds_proof_done = 0;
   __syncthreads();
+
+  // ======================= proof wave =======================
+  // Sums the counts every bank of the layer publishes at the end of each
+  // run (word r of bank b: its first touches in runs 0..r-1), run after run,
+  // on a vector memory counter of its own: a control wave that loaded and
+  // waited for them itself would, at its first wait after the load, also
+  // wait for every claim and store it issued since.  Stops after the first
+  // run whose proof fails, as the layer does.
+  if (proof_wave) {
+    if constexpr (PWAVE) {
+      const int64_t proof_rows = P.trace_proof_rows;
+      const int k = P.trace_proof_steps;
+      if (proof_rows > 0 && k > 0) {
+        const int64_t* const scan_l = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
+        const uint32_t ep = static_cast<uint32_t>(scan_l[COWSDM_SCRATCH_EPOCH]);
+        const bool in = lane < B;
+        const int64_t* const word = scan_l + COWSDM_SCRATCH_SLOTS +
+                                    static_cast<int64_t>(in ? lane : 0) * P.steps;
+        auto ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+          return static_cast<uint32_t>(w >> 32) == ep && ((w >> 30) & 3u) == kStatusAggregate;
+        };
+        const int runs = (G - 1) / k;  // proofs before steps k, 2k, ... < G
+        // the words of kBatch runs in flight at once (a word not yet
+        // published when loaded is polled again on its own)
+        constexpr int kBatch = 8;
+        bool stop = false;
+        for (int r0 = 1; r0 <= runs && !stop; r0 += kBatch) {
+          uint64_t wb[kBatch];
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            wb[i] = r0 + i <= runs ? atomic_load_u64(word + r0 + i) : 0;
+          }
+#pragma unroll
+          for (int i = 0; i < kBatch; ++i) {
+            const int r = r0 + i;
+            if (stop || r > runs) break;
+            uint64_t w = wb[i];
+            int spins = 0;
+            while (__ballot(in && !ready(w)) != 0 && spins < kSpinLimit) {
+              __builtin_amdgcn_s_sleep(1);
+              if (!ready(w)) w = atomic_load_u64(word + r);
+              ++spins;
+            }
+            const bool lost = __ballot(in && !ready(w)) != 0;
+            const int total =
+                lost ? -1 : wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
+            if (lane == 0) {
+              lds_proof[r] = total;
+              sync_store(&lds_proof_done, static_cast<uint32_t>(r));
+            }
+            stop = lost || old_free - total < proof_rows;
+          }
+        }
+      }
+    }
+    return;
+  }
   if (bank >= B) return;  // both waves of the bank
 
   uint32_t* const sync = lds_sync[pair];
@@ -674,8 +750,15 @@ void sdm_trace_kernel(StepParams P) {
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
   int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
+  uint32_t* const seen = MAPLDS ? lds_seen[pair] : nullptr;
   if constexpr (MAPLDS) {
-    for (int k = lane; k < N; k += kWave) lds_map[k] = map_bank[k];
+    // slots 64i..64i+63 give bitmap words 2i and 2i+1 (N <= kTraceMapSlots)
+    for (int b = 0; b < N; b += kWave) {
+      const int v = b + lane < N ? map_bank[b + lane] : -1;
+      if (b + lane < N) lds_map[b + lane] = v;
+      const uint64_t m = __ballot(v >= 0);
+      if (lane < 2) seen[(b >> 5) + lane] = static_cast<uint32_t>(m >> (32 * lane));
+    }
   }
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
@@ -932,11 +1015,21 @@ void sdm_trace_kernel(StepParams P) {
   // half unused; the compiler reuses that register, and writing a register a
   // load or atomic in flight will write waits for every access in flight.)
   int32_t* const claims32 = DENSE ? nullptr : reinterpret_cast<int32_t*>(claims);
-  auto claim = [&](const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+  // With capacity proofs, each run of proof steps claims on a counter of its
+  // own (the low word of one of the last kTraceRunCounters scan words, zero
+  // between launches): a step's claims then need not wait for its run's
+  // proof, which gives the run's base, the exact number of rows every bank
+  // claimed before it.  Rows are claimed at base + p; a run that fails its
+  // proof never takes the rows it claimed.
+  int64_t* const run_claims = DENSE ? nullptr : scan + P.scan_words - kTraceRunCounters;
+  int base_cur = 0;   // base of the run the last passed proof opened
+  auto claim = [&](const TraceRoute& rt, int& home, int run) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (route_count(rt.u) > 0 && route_ok(rt.u)) {
         if (lane == 0) {
-          home = __hip_atomic_fetch_add(claims32, static_cast<int32_t>(route_count(rt.u)),
+          int32_t* const ctr = P.trace_proof_rows > 0
+                                   ? reinterpret_cast<int32_t*>(run_claims + run) : claims32;
+          home = __hip_atomic_fetch_add(ctr, static_cast<int32_t>(route_count(rt.u)),
                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
@@ -944,14 +1037,14 @@ void sdm_trace_kernel(StepParams P) {
   };
 
   // Step t's first touches, from the rows claimed for them (home: lane 0
-  // holds p, the rows the layer claimed before).  r1: step t+1, whose
+  // holds p, the rows claimed before it on its counter).  r1: step t+1, whose
   // rewrites of step t's slots take its physical rows.
   auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, int home)
       __attribute__((always_inline)) {
     const int count = route_count(rt.u);
     if (count > 0 && route_ok(rt.u) && alive) {
       const uint32_t fmask = route_fmask(rt.u);
-      const int p = __builtin_amdgcn_readfirstlane(home);
+      const int p = __builtin_amdgcn_readfirstlane(home) + base_cur;
       bool fits = p + count <= old_free;
       if (fits) {
         const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
@@ -1006,16 +1099,10 @@ void sdm_trace_kernel(StepParams P) {
   int run_left = proof_steps - 1;     // classified steps before the next run ends
   int runs_published = 0;
   int next_proof = 0;                 // step of the next proof
+  int proof_run = 0;                  // the run the next proof opens
   uint64_t pw[SCANW];                 // the published counts of the next proof
-  // this lane's bank in each window: its last count known exactly, and the
-  // number of runs that count covers
-  int known[SCANW], known_runs[SCANW];
 #pragma unroll
-  for (int k = 0; k < SCANW; ++k) {
-    pw[k] = 0;
-    known[k] = 0;
-    known_runs[k] = 0;
-  }
+  for (int k = 0; k < SCANW; ++k) pw[k] = 0;
   // Bank b's count after its r-th run is word b * P.steps + r of the slots
   // (a launch has fewer runs than steps): each bank writes words of its own,
   // never a cache line another bank writes to.
@@ -1027,77 +1114,134 @@ void sdm_trace_kernel(StepParams P) {
     run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk * run_stride;
   }
 
-  // Does the proof before step s stop the layer?  Wave-uniform: every wave
-  // decides from the same counts, the first touches of every bank before
-  // step s.  A bank whose count for the run just ended has not arrived is
-  // bounded by its last known count plus W first touches per step since:
-  // when the layer passes even so, it passes exactly, and only otherwise
-  // does the wave wait for the missing counts.
-  auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {
-    if (s == 0) return old_free < proof_rows;
-    const int r = s / proof_steps;   // runs that end before step s
-    const int per_run = W * proof_steps;
-    const uint32_t off = static_cast<uint32_t>(r);
-    auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-      return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
-    };
-    auto take = [&](int k, uint64_t w) __attribute__((always_inline)) {
-      if (word_ready(w)) {
-        known[k] = static_cast<int>(w & kValueMask);
-        known_runs[k] = r;
-      }
-    };
-    int upper = 0;
-    uint64_t missing = 0;
+  // Map in LDS: a bank counts its runs' first touches a chunk (64 steps)
+  // ahead of classification, from the write slots of the steps alone: a slot
+  // is first touched by the first step that writes it, unless it was mapped
+  // at the launch's start.  (A step with an invalid route claims nothing and
+  // stops the layer; the count runs on, which only makes later proofs
+  // stricter in a launch that reports an error.)  Each bank publishes its
+  // count at the end of a run at least 64 steps before the proof that sums
+  // it, so a proof does not wait for banks that run a few steps behind.
+  IDX wnext[kTraceMaxWrites];        // the write slots of the chunk counted next
 #pragma unroll
-    for (int k = 0; k < SCANW; ++k) {
-      if (k * kWave < B) {
-        take(k, pw[k]);
-        const bool in = k * kWave + lane < B;
-        upper += wave_sum_launch(in ? known[k] + per_run * (r - known_runs[k]) : 0);
-        missing |= __ballot(in && known_runs[k] != r);
-      }
+  for (int j = 0; j < kTraceMaxWrites; ++j) wnext[j] = 0;
+  auto load_writes = [&](int c) __attribute__((always_inline)) {
+    const int st = c * kWave + lane < G ? c * kWave + lane : G - 1;
+    const char* const w = at(wbase, st_wi, st);
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      wnext[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : 0) * sizeof(IDX));
     }
-    if (old_free - upper >= proof_rows) return false;
-    if (missing == 0) return true;
-    // the bound decides nothing: wait (bounded) for the missing counts
-    int total = 0;
+  };
+  // Chunk c's steps (lane l: step 64c + l), run by run, in order: the
+  // bitmap updates of one wave apply in the order they are issued, so a run
+  // counts the bits it is first to set whatever the order of its lanes.
+  int ahead_cum = 0;
+  auto count_chunk = [&](int c, const IDX (&ws)[kTraceMaxWrites]) __attribute__((always_inline)) {
+    if constexpr (MAPLDS) {
+      const int t0 = c * kWave;
+      if (t0 >= G) return;
+      const int t1 = t0 + kWave < G ? t0 + kWave : G;
+      const int t = t0 + lane;
+      int x[kTraceMaxWrites];
 #pragma unroll
-    for (int k = 0; k < SCANW; ++k) {
-      if (k * kWave < B) {
-        const bool in = k * kWave + lane < B;
-        int spins = 0;
-        while (__ballot(in && known_runs[k] != r) != 0 && spins < kSpinLimit) {
-          __builtin_amdgcn_s_sleep(1);
-          if (known_runs[k] != r) take(k, atomic_load_u64(run_l[k] + off));
-          ++spins;
-        }
-        if (__ballot(in && known_runs[k] != r) != 0) {
-          // never arrived: record it and stop the layer here
-          if (lane == 0) {
-            __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                  static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int j = 0; j < kTraceMaxWrites; ++j) {
+        const int64_t v = static_cast<int64_t>(ws[j]);
+        x[j] = j < W && t < t1 && v >= 0 && v < N ? static_cast<int>(v) : -1;
+      }
+      int r = t0 / proof_steps;       // the run holding step t0
+      for (int a = r * proof_steps; a < t1; a += proof_steps, ++r) {
+        const bool in = t >= a && t < a + proof_steps;
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          bool newly = false;
+          if (in && x[j] >= 0) {
+            const uint32_t bit = 1u << (x[j] & 31);
+            newly = (__hip_atomic_fetch_or(&seen[x[j] >> 5], bit, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0;
           }
-          return true;
+          ahead_cum += __popcll(__ballot(newly));
         }
-        total += wave_sum_launch(in ? known[k] : 0);
+        // run r ends in this chunk: its count is word r + 1
+        if (a + proof_steps <= t1 && lane == 0) {
+          atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + r + 1,
+                           slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(ahead_cum)));
+        }
       }
     }
+  };
+
+  // The proof before step s, at the loop head before iteration s (s even,
+  // the first step of run r = s / proof_steps): every bank published its
+  // count of first touches in runs 0..r-1 when it classified step s-1, three
+  // iterations earlier, and every wave sums the same counts, so the layer
+  // stops at the same step on every wave.  The sum is also run r's base.
+  // Returns true (and the layer stops before s) when free_count minus the
+  // base is below proof_rows, or when a count never arrives (bounded wait).
+  auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {
+    int total = 0;
+    if (PWAVE && s > 0) {
+      // summed by the proof wave (it waits for slow banks on its own)
+      const uint32_t r = static_cast<uint32_t>(proof_run);
+      uint32_t d = sync_load(&lds_proof_done);
+      for (int spins = 0; d < r && spins < 4 * kSpinLimit; ++spins) {
+        __builtin_amdgcn_s_sleep(1);
+        d = sync_load(&lds_proof_done);
+      }
+      total = d >= r ? lds_proof[r] : -1;
+      if (total < 0) {
+        if (lane == 0) {
+          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return true;
+      }
+    } else if (s > 0) {
+      const uint32_t off = static_cast<uint32_t>(proof_run);
+      auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
+        return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
+      };
+#pragma unroll
+      for (int k = 0; k < SCANW; ++k) {
+        if (k * kWave < B) {
+          const bool in = k * kWave + lane < B;
+          uint64_t w = pw[k];
+          int spins = 0;
+          while (__ballot(in && !word_ready(w)) != 0 && spins < kSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+            if (!word_ready(w)) w = atomic_load_u64(run_l[k] + off);
+            ++spins;
+          }
+          if (__ballot(in && !word_ready(w)) != 0) {
+            // never arrived: record it and stop the layer here
+            if (lane == 0) {
+              __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                    static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return true;
+          }
+          total += wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
+        }
+      }
+    }
+    base_cur = total;
     return old_free - total < proof_rows;
   };
 
-  // After classifying step t: claim its rows (a run's first step waits for
-  // its proof), and publish the bank's count when t ends a run.
-  bool halted = false;  // a proof failed: no claims from its step on
+  // After classifying step t: claim its rows (on its run's counter when
+  // proofs are on), and publish the bank's count when t ends a run.
+  bool halted = false;  // a proof failed: the layer stops at its step
   auto after_classify = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (t < G && !halted && !(proofs && t == next_proof)) claim(rt, home);
+      if (t < G && !halted) claim(rt, home, runs_published);
       if (proofs) {
-        if (route_ok(rt.u)) cum += route_count(rt.u);
+        if (!MAPLDS && route_ok(rt.u)) cum += route_count(rt.u);
         if (run_left == 0) {
           ++runs_published;
-          if (t < G && lane == 0) {
+          // (map in LDS: published by the count ahead)
+          if (!MAPLDS && t < G && lane == 0) {
             atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + runs_published,
                              slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(cum)));
           }
@@ -1108,30 +1252,29 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // The proof before step t, at the end of the iteration that classified t:
-  // when it passes, t claims its rows (resolved two iterations later, like
-  // every claim); when it fails, the layer halts before t.
-  auto prove = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+  // The proof at the loop head before step s, when one is due there.
+  auto prove = [&](int s) __attribute__((always_inline)) -> bool {
     if constexpr (!DENSE) {
-      if (proofs && t == next_proof && t < G && !halted) {
-        if (proof_fails(t)) {
-          done_steps = t;
+      if (proofs && s == next_proof) {
+        if (proof_fails(s)) {
+          done_steps = s;
           halted = true;
-        } else {
-          next_proof += proof_steps;
-          claim(rt, home);
+          return true;
         }
+        next_proof += proof_steps;
+        ++proof_run;
       }
     }
+    return false;
   };
 
-  // iteration s loads, at its start, the counts that the proof before step
-  // s+2 sums at its end: every bank published them when it classified step
-  // s+1, in iteration s-1
+  // iteration s loads, at its start, the counts that the proof at the next
+  // loop head sums (before step s+1): every bank published them when it
+  // classified step s, in iteration s-2
   auto issue_proof = [&](int s) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (proofs && s + 2 == next_proof && !halted) {
-        const uint32_t off = static_cast<uint32_t>((s + 2) / proof_steps);
+      if (!PWAVE && proofs && s + 1 == next_proof) {
+        const uint32_t off = static_cast<uint32_t>(proof_run);
 #pragma unroll
         for (int k = 0; k < SCANW; ++k) {
           if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + off);
@@ -1165,7 +1308,16 @@ void sdm_trace_kernel(StepParams P) {
   q.fwd = 0; q.rawm = 0;
   if constexpr (DENSE || MAPLDS) {
     load_chunk(0);
+    if (MAPLDS && proofs && G > kWave) load_writes(1);
     write_chunk(0);
+    if (MAPLDS && proofs) {
+      IDX w0[kTraceMaxWrites];
+#pragma unroll
+      for (int j = 0; j < kTraceMaxWrites; ++j) w0[j] = chunk[j];
+      count_chunk(0, w0);
+      count_chunk(1, wnext);
+      if (2 * kWave < G) load_writes(2);
+    }
     if (G > kWave) load_chunk(1);  // written before step 64 is read
   }
   {
@@ -1182,7 +1334,6 @@ void sdm_trace_kernel(StepParams P) {
     issue_map(i1, mw1, mr1);
     const int rrow0 = classify(0, i0, mw0, mr0, rA, q, q, true);
     after_classify(0, rA, popA);
-    prove(0, rA, popA);
     publish_rows(0, rA, rrow0);
     const int rrow1 = classify(1, i1, mw1, mr1, rB, rA, q, route_ok(rA.u));
     after_classify(1, rB, popB);
@@ -1224,7 +1375,6 @@ void sdm_trace_kernel(StepParams P) {
       after_classify(s + 2, rC, pop);
       ready1 = ready2;
     }
-    prove(s + 2, rC, pop);
     publish(s, rA, run, alive, rC, rrow);
     rA = rB;
     rB = rC;
@@ -1246,8 +1396,9 @@ void sdm_trace_kernel(StepParams P) {
       stopped = true;
       break;
     }
-    // a failed proof before step s (decided in iteration s-2) halts here
-    if (halted) {
+    // the proof before step s: a run's claims were made without waiting
+    // for it, and a run that fails it never takes their rows
+    if (prove(s)) {
       stopped = true;
       break;
     }
@@ -1257,6 +1408,10 @@ void sdm_trace_kernel(StepParams P) {
       if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
         const int c = (s + 4) >> 6;
         write_chunk(c);
+        if (MAPLDS && proofs) {
+          count_chunk(c + 1, wnext);
+          if ((c + 2) * kWave < G) load_writes(c + 2);
+        }
         if ((c + 1) * kWave < G) load_chunk(c + 1);
       }
     }
@@ -1272,7 +1427,7 @@ void sdm_trace_kernel(StepParams P) {
       }
       done_steps = s;
       stopped = true;
-    } else if (halted) {
+    } else if (prove(s)) {
       stopped = true;
     } else {
       iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
@@ -1289,28 +1444,48 @@ void sdm_trace_kernel(StepParams P) {
   // no release fence, whose L2 write-back every wave would pay.  The data
   // waves' row stores need no ordering here: the next launch on the stream
   // starts after this one has ended.
-  if (lane == 0 && (!DENSE || P.trace_step)) {
-    int64_t* const ticket = P.trace_ticket + 1 + layer_id;
-    __builtin_amdgcn_s_waitcnt(0);
-    const int64_t done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    if (done == B - 1) {
+  if (!DENSE || P.trace_step) {
+    int64_t done = 0;
+    if (lane == 0) {
+      int64_t* const ticket = P.trace_ticket + 1 + layer_id;
+      __builtin_amdgcn_s_waitcnt(0);
+      done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
       if constexpr (!DENSE) {
-        const int64_t total = static_cast<int64_t>(atomic_load_u64(claims));
+        int64_t total;
+        if (proofs) {
+          // the runs proven: the last one's claims count unless its proof
+          // failed (then the layer stopped at its first step)
+          total = base_cur;
+          if (!halted && proof_run > 0) {
+            total += static_cast<int64_t>(atomic_load_u64(run_claims + proof_run - 1));
+          }
+          // clear the counter of every run any wave may have claimed on
+          const int runs = (G - 1) / proof_steps + 1;
+          for (int k = lane; k < runs; k += kWave) atomic_store_u64(run_claims + k, 0);
+        } else {
+          total = static_cast<int64_t>(atomic_load_u64(claims));
+        }
+        // the first claim that did not fit (at position p) cuts the total
         const int64_t fail = static_cast<int64_t>(atomic_load_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL));
         const int64_t fit = fail > 0 && kClaimFailBase - fail < total ? kClaimFailBase - fail : total;
-        *L.free_count = static_cast<int32_t>(old_free - fit);
-        atomic_store_u64(claims, 0);
-        atomic_store_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL, 0);
-        atomic_store_u64(scan + COWSDM_SCRATCH_EPOCH, static_cast<uint64_t>(epoch + 1u));
-        if (done_steps < G && P.trace_status) {
-          __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+          *L.free_count = static_cast<int32_t>(old_free - fit);
+          atomic_store_u64(claims, 0);
+          atomic_store_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL, 0);
+          atomic_store_u64(scan + COWSDM_SCRATCH_EPOCH, static_cast<uint64_t>(epoch + 1u));
+          if (done_steps < G && P.trace_status) {
+            __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
       }
-      atomic_store_u64(ticket, 0);
-      if (P.trace_step) {
-        atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+      if (lane == 0) {
+        atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
+        if (P.trace_step) {
+          atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+        }
       }
     }
   }
@@ -1350,12 +1525,14 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
   const void* kernel = kernels[variant][which];
   const size_t lds_bytes = MAPLDS ? sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
   const int key = MAPLDS ? P.slots : 0;
+  // packed layers of at most 64 banks (SCANW 1) add the proof wave
+  const int threads = !DENSE && variant >= 2 ? kTraceProofThreads : kTraceThreads;
   if (resident[variant][which] < 0 || resident_slots[variant][which] != key) {
     int device = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&device) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kTraceThreads, lds_bytes) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds_bytes) !=
             hipSuccess) {
       (void)hipGetLastError();
       resident[variant][which] = 0;
@@ -1371,7 +1548,7 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
   if (per_launch <= 0) return false;
   if (blocks <= resident[variant][which]) {
     void* args[] = {&P};
-    (void)hipLaunchKernel(kernel, dim3(blocks), dim3(kTraceThreads), args, lds_bytes, stream);
+    (void)hipLaunchKernel(kernel, dim3(blocks), dim3(threads), args, lds_bytes, stream);
     return true;  // a failed launch is reported by the caller's launch_status()
   }
   for (int l0 = 0; l0 < P0.nlayers; l0 += per_launch) {
@@ -1383,7 +1560,7 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
     if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
     if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
     void* args[] = {&Q};
-    (void)hipLaunchKernel(kernel, dim3(Q.blocks_per_layer * Q.nlayers), dim3(kTraceThreads), args,
+    (void)hipLaunchKernel(kernel, dim3(Q.blocks_per_layer * Q.nlayers), dim3(threads), args,
                           lds_bytes, stream);
   }
   return true;
