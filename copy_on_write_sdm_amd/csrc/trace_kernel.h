@@ -75,6 +75,8 @@ struct TraceRows {                  // operands of one step, loaded one step ahe
 
 struct TraceIdx {                   // lane j: write slot j / read slot j
   int widx, ridx, err;
+  int k0, k1;                       // staged slots: the step's class words 0 and 1 (in
+                                    // every lane, made scalar when the step is classified)
 };
 
 struct TraceRoute {                 // a classified step
@@ -222,19 +224,18 @@ void sdm_trace_kernel(StepParams P) {
   // [1]: data -> control, steps computed
   __shared__ uint32_t lds_sync[NB][2];
   // control wave: the slots of two 64-step chunks, per step W write slots
-  // then R read slots (-1: outside [0, N)), staged from registers a chunk
-  // ahead (map in LDS, or dense)
+  // then R read slots (-1: outside [0, N)) and the step's four class words,
+  // staged from registers a chunk ahead (map in LDS, or dense)
   constexpr int kIdxRow = kTraceMaxWrites + kTraceMaxReads;
-  __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxRow];
-  // control wave (map in LDS): one bit per slot, set when the slot was
-  // mapped at the launch's start or is written by a step the first-touch
-  // count has passed
-  __shared__ uint32_t lds_seen[MAPLDS ? NB : 1][MAPLDS ? kTraceMapSlots / 32 : 1];
+  constexpr int kIdxLds = kIdxRow + 4;
+  __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxLds];
   // proof wave -> control waves: the layer's first touches before run r
   // (-1: a bank's count never arrived), and the last run summed
   constexpr bool PWAVE = !DENSE && SCANW == 1;
   __shared__ int lds_proof[PWAVE ? kTraceRunCounters : 1];
   __shared__ uint32_t lds_proof_done;
+  // map in LDS (dynamic, 2 banks x 2 x N ints): each bank's slot map, then
+  // each bank's first step of the launch writing each slot
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -750,15 +751,20 @@ void sdm_trace_kernel(StepParams P) {
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
   int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
-  uint32_t* const seen = MAPLDS ? lds_seen[pair] : nullptr;
+  uint32_t* const first_write =
+      MAPLDS ? reinterpret_cast<uint32_t*>(lds_map_all + (NB + pair) * N) : nullptr;
+  bool any_bad = false;  // a map entry outside the slab (checked per chunk only then)
   if constexpr (MAPLDS) {
-    // slots 64i..64i+63 give bitmap words 2i and 2i+1 (N <= kTraceMapSlots)
+    uint64_t bad = 0;
     for (int b = 0; b < N; b += kWave) {
       const int v = b + lane < N ? map_bank[b + lane] : -1;
-      if (b + lane < N) lds_map[b + lane] = v;
-      const uint64_t m = __ballot(v >= 0);
-      if (lane < 2) seen[(b >> 5) + lane] = static_cast<uint32_t>(m >> (32 * lane));
+      if (b + lane < N) {
+        lds_map[b + lane] = v;
+        first_write[b + lane] = ~0u;
+      }
+      bad |= __ballot(v >= C);
     }
+    any_bad = bad != 0;
   }
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
@@ -804,29 +810,121 @@ void sdm_trace_kernel(StepParams P) {
           *(const __attribute__((address_space(1))) IDX*)(r + (i < R ? i : 0) * sizeof(IDX));
     }
   };
-  auto write_chunk = [&](int c) __attribute__((always_inline)) {
+  // Chunk c's slots and class words, lane l for step t = 64c + l: the step's
+  // classification, done here for 64 steps at once with plain per-lane
+  // compares instead of per step with cross-lane reads (slot values past W
+  // or R take no part; an invalid slot compares as slot 0, as the per-step
+  // path reads it):
+  //   word 0: bits 0-19 rows from step t-1 (write lanes 0-3, read lanes
+  //           4-19), 20-23 first touches (fm: lane l's first-touch mask from
+  //           the bitmap pass), 24-31 the COWSDM_ERR_* bits of its routes
+  //   word 1: bits 0-15 reads of a slot step t writes, 16-19 and 20-23 the
+  //           two bit planes of each write lane's source lane in step t-1
+  //   words 2, 3: the planes of each read lane's source lane in step t-1 and
+  //           in step t (read-after-write)
+  // (Source planes are zero when the step forwards nothing; lanes without a
+  // source have both plane bits set.)
+  auto write_chunk = [&](int c, uint32_t fm) __attribute__((always_inline)) {
     int v[kIdxRow];
 #pragma unroll
     for (int k = 0; k < kIdxRow; ++k) {
       const int64_t x = static_cast<int64_t>(chunk[k]);
       v[k] = x >= 0 && x < N ? static_cast<int>(x) : -1;
     }
-    i32x4_t* const row = reinterpret_cast<i32x4_t*>(&lds_idx[(DENSE || MAPLDS) ? pair : 0][c & 1][lane][0]);
+    int (*const buf)[kWave][kIdxLds] = lds_idx[(DENSE || MAPLDS) ? pair : 0];
+    // write slots: this step's and step t-1's (lane 0: the last step of
+    // chunk c-1, or none before step 0), invalid ones as slot 0, -1 past W
+    int w[kTraceMaxWrites], pw[kTraceMaxWrites];
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      w[j] = j < W ? (v[j] < 0 ? 0 : v[j]) : -1;
+      int up = __shfl_up(w[j], 1, kWave);
+      if (lane == 0) {
+        const int last = c > 0 ? buf[(c - 1) & 1][kWave - 1][j] : -2;
+        up = c > 0 && j < W ? (last < 0 ? 0 : last) : -2;
+      }
+      pw[j] = up;
+    }
+    int err = 0;
+    bool dup = false;
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      if (j < W && v[j] < 0) err |= COWSDM_ERR_WRITE_INDEX;
+#pragma unroll
+      for (int k = j + 1; k < kTraceMaxWrites; ++k) dup |= k < W && w[k] == w[j];
+    }
+    uint32_t fwd = 0, w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) {
+      int src = -1;
+#pragma unroll
+      for (int k = 0; k < kTraceMaxWrites; ++k) src = w[j] >= 0 && w[j] == pw[k] ? k : src;
+      fwd |= (src >= 0 ? 1u : 0u) << j;
+      w0 |= static_cast<uint32_t>(src & 1) << j;
+      w1 |= static_cast<uint32_t>((src >> 1) & 1) << j;
+    }
+    uint32_t rawm = 0, f0 = 0, f1 = 0, a0 = 0, a1 = 0;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < kTraceMaxReads; ++i) {
+      const int x = i < R ? (v[kTraceMaxWrites + i] < 0 ? 0 : v[kTraceMaxWrites + i]) : -3;
+      if (i < R && v[kTraceMaxWrites + i] < 0) err |= COWSDM_ERR_READ_INDEX;
+      int raw = -1, src = -1;
+#pragma unroll
+      for (int k = 0; k < kTraceMaxWrites; ++k) {
+        raw = x == w[k] ? k : raw;
+        src = x == pw[k] ? k : src;
+      }
+      if (raw >= 0) src = -1;
+      rawm |= (raw >= 0 ? 1u : 0u) << i;
+      fwd |= (src >= 0 ? 1u : 0u) << (kTraceMaxWrites + i);
+      f0 |= static_cast<uint32_t>(src & 1) << i;
+      f1 |= static_cast<uint32_t>((src >> 1) & 1) << i;
+      a0 |= static_cast<uint32_t>(raw & 1) << i;
+      a1 |= static_cast<uint32_t>((raw >> 1) & 1) << i;
+      if constexpr (MAPLDS) {
+        // a map entry outside the slab (only one present at launch start can be)
+        if (any_bad && i < R) bad |= lds_map[x] >= C;
+      }
+    }
+    if constexpr (MAPLDS) {
+      if (any_bad) {
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          if (j < W) bad |= lds_map[w[j]] >= C;
+        }
+      }
+    }
+    if (dup) err |= COWSDM_ERR_DUP_WRITE;
+    if (bad) err |= COWSDM_ERR_CORRUPT;
+    const bool planes = (fwd | rawm) != 0;
+    i32x4_t q[kIdxLds / 4];
 #pragma unroll
     for (int k = 0; k < kIdxRow / 4; ++k) {
-      i32x4_t q;
-      q.x = v[4 * k]; q.y = v[4 * k + 1]; q.z = v[4 * k + 2]; q.w = v[4 * k + 3];
-      row[k] = q;
+      q[k].x = v[4 * k]; q[k].y = v[4 * k + 1]; q[k].z = v[4 * k + 2]; q[k].w = v[4 * k + 3];
     }
+    q[kIdxRow / 4].x = static_cast<int>(fwd | (fm << 20) | (static_cast<uint32_t>(err) << 24));
+    q[kIdxRow / 4].y = static_cast<int>(rawm | (planes ? (w0 << 16) | (w1 << 20) : 0u));
+    q[kIdxRow / 4].z = static_cast<int>(planes ? f0 | (f1 << 16) : 0u);
+    q[kIdxRow / 4].w = static_cast<int>(planes ? a0 | (a1 << 16) : 0u);
+    i32x4_t* const row = reinterpret_cast<i32x4_t*>(&buf[c & 1][lane][0]);
+#pragma unroll
+    for (int k = 0; k < kIdxLds / 4; ++k) row[k] = q[k];
+  };
+  auto idx_row = [&](int t) __attribute__((always_inline)) -> const int* {
+    const int tc = t < G ? t : G - 1;
+    return &lds_idx[(DENSE || MAPLDS) ? pair : 0][(tc >> 6) & 1][tc & (kWave - 1)][0];
   };
   auto read_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
-    const int tc = t < G ? t : G - 1;
-    const int* const row = &lds_idx[(DENSE || MAPLDS) ? pair : 0][(tc >> 6) & 1][tc & (kWave - 1)][0];
+    const int* const row = idx_row(t);
     const int xw = row[lane < kTraceMaxWrites ? lane : 0];
     const int xr = row[kTraceMaxWrites + (lane < kTraceMaxReads ? lane : 0)];
+    const u32x4_t k = *reinterpret_cast<const u32x4_t*>(row + kIdxRow);
     m.err = (lane < W && xw < 0 ? COWSDM_ERR_WRITE_INDEX : 0) | (lane < R && xr < 0 ? COWSDM_ERR_READ_INDEX : 0);
     m.widx = lane < W && xw >= 0 ? xw : 0;
     m.ridx = lane < R && xr >= 0 ? xr : 0;
+    m.k0 = static_cast<int>(k.x);
+    m.k1 = static_cast<int>(k.y);
   };
 
   auto issue_map = [&](const TraceIdx& m, int& wraw, int& rraw) __attribute__((always_inline)) {
@@ -854,6 +952,38 @@ void sdm_trace_kernel(StepParams P) {
       // the matching below covers the LDS latency
       wraw = lds_map[m.widx];
       rraw = lds_map[m.ridx];
+    }
+    if constexpr (DENSE || MAPLDS) {
+      // staged slots: the chunk's pass classified the step (class words)
+      const uint32_t k0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(m.k0));
+      const uint32_t k1 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(m.k1));
+      const int e = static_cast<int>(k0 >> 24) | base_err;
+      if (!DENSE && e != 0 && t < G) {
+        if (lane == 0) {
+          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(e),
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      if constexpr (!DENSE) {
+        // an entry outside the slab (reported above) reads as shared
+        wraw = wraw >= C ? -1 : wraw;
+        rraw = rraw >= C ? -1 : rraw;
+      }
+      const bool ok = ok_prev && e == 0;
+      const uint32_t fwd = k0 & 0xFFFFFu;
+      const uint32_t fm = DENSE || !ok ? 0u : (k0 >> 20) & 15u;
+      rt.u = fm | (static_cast<uint32_t>(__popc(fm)) << 4) | (ok ? 1u << 8 : 0u);
+      rt.fwd = fwd;
+      rt.rawm = k1 & 0xFFFFu;
+      rt.rank = lanes_below(fm);
+      rt.widx = m.widx;
+      rt.ridx = m.ridx;
+      rt.wrow = lane < W ? wraw : -1;
+      rt.wsrc = lane < W && ((fwd >> (lane & 3)) & 1u) != 0
+                    ? plane_code(k1, 16 + (lane & 3), 20 + (lane & 3)) : -1;
+      rt.rsrc = -1;   // (the read lanes' sources reach the data wave as class words)
+      rt.rraw = -1;
+      return lane < R ? rraw : -1;
     }
     int wsrc = -1, rsrc = -1, rraw_lane = -1;
     uint64_t dup = 0;
@@ -965,8 +1095,10 @@ void sdm_trace_kernel(StepParams P) {
   // got rows) and the progress word, in one store pass of lanes 0-15 and one
   // of lane 0.  The source-row planes of forwarded rows are only built for a
   // step that forwards some.
+  // kq: step s's class words (map in LDS, or dense), read at the start of
+  // the iteration: the release store below waits for every LDS access anyway
   auto publish = [&](int s, const TraceRoute& rt, bool run, bool fitted, const TraceRoute& rc,
-                     int rrow) __attribute__((always_inline)) {
+                     int rrow, const u32x4_t& kq) __attribute__((always_inline)) {
     const float* wp;
     const float* rp;
     row_addrs(rc, rrow, wp, rp);
@@ -978,7 +1110,12 @@ void sdm_trace_kernel(StepParams P) {
     c.y = rt.rawm;
     c.z = 0;
     c.w = 0;
-    if ((rt.fwd | rt.rawm) != 0) {
+    if constexpr (DENSE || MAPLDS) {
+      // the source planes were built with the chunk (class words 1-3)
+      c.y = kq.y;
+      c.z = kq.z;
+      c.w = kq.w;
+    } else if ((rt.fwd | rt.rawm) != 0) {
       const uint32_t w0 = static_cast<uint32_t>(__ballot((rt.wsrc & 1) != 0)) & 15u;
       const uint32_t w1 = static_cast<uint32_t>(__ballot((rt.wsrc & 2) != 0)) & 15u;
       const uint32_t f0 = static_cast<uint32_t>(__ballot((rt.rsrc & 1) != 0)) & 0xFFFFu;
@@ -1133,10 +1270,17 @@ void sdm_trace_kernel(StepParams P) {
       wnext[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : 0) * sizeof(IDX));
     }
   };
-  // Chunk c's steps (lane l: step 64c + l), run by run, in order: the
-  // bitmap updates of one wave apply in the order they are issued, so a run
-  // counts the bits it is first to set whatever the order of its lanes.
+  // Chunk c's steps (lane l: step 64c + l): step t first-touches slot x
+  // when x was unmapped at the launch's start and t is the first step of the
+  // launch that writes x.  Chunks come in order, so a minimum over the steps
+  // of this chunk and the chunks before gives that first step: one LDS
+  // minimum per write slot, all lanes at once, then a read back.  (An entry
+  // read here was not rewritten yet: the launch pops a slot's row only at
+  // its first write, which comes after the steps resolved so far.)  Lane l
+  // keeps its step's first-touch mask for the chunk's class words (fm_next),
+  // and with proofs on the bank publishes its count at the end of every run.
   int ahead_cum = 0;
+  uint32_t fm_next = 0;
   auto count_chunk = [&](int c, const IDX (&ws)[kTraceMaxWrites]) __attribute__((always_inline)) {
     if constexpr (MAPLDS) {
       const int t0 = c * kWave;
@@ -1148,24 +1292,34 @@ void sdm_trace_kernel(StepParams P) {
       for (int j = 0; j < kTraceMaxWrites; ++j) {
         const int64_t v = static_cast<int64_t>(ws[j]);
         x[j] = j < W && t < t1 && v >= 0 && v < N ? static_cast<int>(v) : -1;
-      }
-      int r = t0 / proof_steps;       // the run holding step t0
-      for (int a = r * proof_steps; a < t1; a += proof_steps, ++r) {
-        const bool in = t >= a && t < a + proof_steps;
-#pragma unroll
-        for (int j = 0; j < kTraceMaxWrites; ++j) {
-          bool newly = false;
-          if (in && x[j] >= 0) {
-            const uint32_t bit = 1u << (x[j] & 31);
-            newly = (__hip_atomic_fetch_or(&seen[x[j] >> 5], bit, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0;
-          }
-          ahead_cum += __popcll(__ballot(newly));
+        if (x[j] >= 0) {
+          __hip_atomic_fetch_min(&first_write[x[j]], static_cast<uint32_t>(t), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        // run r ends in this chunk: its count is word r + 1
-        if (a + proof_steps <= t1 && lane == 0) {
-          atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + r + 1,
-                           slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(ahead_cum)));
+      }
+      // one wave's LDS accesses apply in issue order: keep the reads after
+      asm volatile("" ::: "memory");
+      uint32_t f = 0;
+#pragma unroll
+      for (int j = 0; j < kTraceMaxWrites; ++j) {
+        if (x[j] >= 0 && first_write[x[j]] == static_cast<uint32_t>(t) && lds_map[x[j]] < 0) {
+          f |= 1u << j;
+        }
+      }
+      fm_next = f;
+      if (proofs) {
+        int r = t0 / proof_steps;       // the run holding step t0
+        for (int a = r * proof_steps; a < t1; a += proof_steps, ++r) {
+          const bool in = t >= a && t < a + proof_steps;
+#pragma unroll
+          for (int j = 0; j < kTraceMaxWrites; ++j) {
+            ahead_cum += __popcll(__ballot(in && ((f >> j) & 1u) != 0));
+          }
+          // run r ends in this chunk: its count is word r + 1
+          if (a + proof_steps <= t1 && lane == 0) {
+            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + r + 1,
+                             slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(ahead_cum)));
+          }
         }
       }
     }
@@ -1308,13 +1462,15 @@ void sdm_trace_kernel(StepParams P) {
   q.fwd = 0; q.rawm = 0;
   if constexpr (DENSE || MAPLDS) {
     load_chunk(0);
-    if (MAPLDS && proofs && G > kWave) load_writes(1);
-    write_chunk(0);
-    if (MAPLDS && proofs) {
+    if (MAPLDS && G > kWave) load_writes(1);
+    if constexpr (MAPLDS) {
       IDX w0[kTraceMaxWrites];
 #pragma unroll
       for (int j = 0; j < kTraceMaxWrites; ++j) w0[j] = chunk[j];
       count_chunk(0, w0);
+    }
+    write_chunk(0, fm_next);
+    if constexpr (MAPLDS) {
       count_chunk(1, wnext);
       if (2 * kWave < G) load_writes(2);
     }
@@ -1359,6 +1515,8 @@ void sdm_trace_kernel(StepParams P) {
                        int& mw_other, int& mr_other, int& pop)
       __attribute__((always_inline)) {
     issue_proof(s);
+    u32x4_t kq = {0u, 0u, 0u, 0u};
+    if constexpr (DENSE || MAPLDS) kq = *reinterpret_cast<const u32x4_t*>(idx_row(s) + kIdxRow);
     const bool run = route_ok(rA.u) && alive;
     if constexpr (!DENSE) resolve(s, rA, rB, pop);
     TraceRoute rC;
@@ -1375,7 +1533,7 @@ void sdm_trace_kernel(StepParams P) {
       after_classify(s + 2, rC, pop);
       ready1 = ready2;
     }
-    publish(s, rA, run, alive, rC, rrow);
+    publish(s, rA, run, alive, rC, rrow, kq);
     rA = rB;
     rB = rC;
   };
@@ -1407,8 +1565,8 @@ void sdm_trace_kernel(StepParams P) {
       // replaces held chunk c - 2, whose last step was read long before
       if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
         const int c = (s + 4) >> 6;
-        write_chunk(c);
-        if (MAPLDS && proofs) {
+        write_chunk(c, fm_next);
+        if constexpr (MAPLDS) {
           count_chunk(c + 1, wnext);
           if ((c + 2) * kWave < G) load_writes(c + 2);
         }
@@ -1523,7 +1681,9 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
   static int resident_slots[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
-  const size_t lds_bytes = MAPLDS ? sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
+  // map in LDS: per bank the slot map and each slot's first writing step
+  const size_t lds_bytes =
+      MAPLDS ? 2 * sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
   const int key = MAPLDS ? P.slots : 0;
   // packed layers of at most 64 banks (SCANW 1) add the proof wave
   const int threads = !DENSE && variant >= 2 ? kTraceProofThreads : kTraceThreads;

@@ -108,6 +108,70 @@ def test_persistent_trace_matches_single_steps(device, layers, banks, slots, wid
         assert torch.equal(dense[l], traced[l].materialize_dense())
 
 
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_invalid_routes_stop_only_their_bank(device, index_dtype):
+    """One launch of 100 steps (two 64-step chunks) with an out-of-range
+    write slot, an out-of-range read slot, a slot written twice in one step,
+    and a map entry outside the slab: each layer records exactly those
+    errors, each failing bank keeps the state it had before its first failing
+    step (the dense run of the steps before it) for the rest of the launch,
+    and every other bank decodes as the clean routes do."""
+
+    layers, banks, slots, width, writes, reads, steps = 2, 6, 64, 64, 4, 8, 100
+    group = steps
+    print(f"invalid routes {index_dtype}", flush=True)
+    m0, routes, states, kw = _setup(device, layers=layers, banks=banks, slots=slots,
+                                    width=width, writes=writes, reads=reads, steps=steps,
+                                    seed=41, index_dtype=index_dtype)
+    clean_kw = dict(kw)
+    bad_w = routes.write_indices.clone()
+    bad_r = routes.read_indices.clone()
+    bad_w[10, 0, 2, 1] = slots                     # write slot outside [0, N)
+    bad_r[70, 0, 5, 3] = -1                        # read slot outside [0, N)
+    bad_w[65, 1, 4, 2] = bad_w[65, 1, 4, 0]        # one slot written twice
+    kw = dict(kw, write_indices=bad_w, read_indices=bad_r)
+    # layer 1, bank 1: a map entry outside the slab, first touched at step k1
+    x = int(routes.read_indices[30, 1, 1, 0])
+    k1 = min(s for s in range(steps)
+             if x in routes.write_indices[s, 1, 1].tolist() or x in routes.read_indices[s, 1, 1].tolist())
+    stops = {(0, 2): 10, (0, 5): 70, (1, 4): 65, (1, 1): k1}
+
+    packed = states()
+    packed[1].logical_to_physical[1, x] = packed[1].capacity_rows
+    outputs = torch.zeros(steps, layers, banks, width, device=device)
+    cow.DecodeTrace(states=packed, outputs=outputs, max_steps_per_launch=group,
+                    **kw).launch(steps, start=0)
+    torch.cuda.synchronize()
+    errors = [int(st.scratch[nat.SCRATCH_ERRORS]) for st in packed]
+    assert errors == [nat.ERR_WRITE_INDEX | nat.ERR_READ_INDEX,
+                      nat.ERR_DUP_WRITE | nat.ERR_CORRUPT]
+    # the failing step never ran, so the entry was never rewritten
+    assert int(packed[1].logical_to_physical[1, x]) == packed[1].capacity_rows
+    packed[1].logical_to_physical[1, x] = -1
+
+    def dense_run(n):
+        tables = [m0[l, 0].expand(banks, -1, -1).contiguous() for l in range(layers)]
+        out = torch.zeros(steps, layers, banks, width, device=device)
+        if n:
+            cow.DecodeTrace(memories=tables, outputs=out, max_steps_per_launch=group,
+                            **clean_kw).launch(n, start=0)
+        return tables, out
+
+    clean_tables, clean_out = dense_run(steps)
+    for l in range(layers):
+        got = packed[l].materialize_dense()
+        for b in range(banks):
+            k = stops.get((l, b))
+            if k is None:
+                assert torch.equal(outputs[:, l, b], clean_out[:, l, b]), (l, b)
+                assert torch.equal(got[b], clean_tables[l][b]), (l, b)
+            else:
+                assert torch.equal(outputs[:k, l, b], clean_out[:k, l, b]), (l, b, k)
+                assert torch.equal(got[b], dense_run(k)[0][l][b]), (l, b, k)
+        packed[l].scratch[nat.SCRATCH_ERRORS] = 0   # recorded above, as expected
+        packed[l].validate_invariants()
+
+
 def test_persistent_trace_matches_oracle(device):
     banks, slots, width, steps = 6, 32, 128, 24
     m0, routes, states, kw = _setup(device, layers=1, banks=banks, slots=slots, width=width,
