@@ -331,36 +331,35 @@ void sdm_trace_kernel(StepParams P) {
           return static_cast<uint32_t>(w >> 32) == ep && ((w >> 30) & 3u) == kStatusAggregate;
         };
         const int runs = (G - 1) / k;  // proofs before steps k, 2k, ... < G
-        // the words of kBatch runs in flight at once (a word not yet
-        // published when loaded is polled again on its own)
-        constexpr int kBatch = 8;
+        // Run r's words are loaded once the workgroup's first control wave
+        // has published steps up to kLead before the proof that needs them
+        // (with the map in LDS the counts went out at least 64 steps ahead
+        // of it; with the map in HBM three steps ahead, so the load polls a
+        // little).  Loading earlier would poll words not yet published, and
+        // every poll gathers one cache line per bank from L2 beside the data
+        // waves' row loads.  (A stopped control wave publishes 0xFFFF steps.)
+        constexpr int kLead = 12;
         bool stop = false;
-        for (int r0 = 1; r0 <= runs && !stop; r0 += kBatch) {
-          uint64_t wb[kBatch];
-#pragma unroll
-          for (int i = 0; i < kBatch; ++i) {
-            wb[i] = r0 + i <= runs ? atomic_load_u64(word + r0 + i) : 0;
+        for (int r = 1; r <= runs && !stop; ++r) {
+          for (int spins = 0; spins < 4 * kSpinLimit; ++spins) {
+            const uint32_t published = sync_load(&lds_sync[0][0]) & 0xFFFFu;
+            if (static_cast<int>(published) + kLead >= r * k) break;
+            __builtin_amdgcn_s_sleep(8);
           }
-#pragma unroll
-          for (int i = 0; i < kBatch; ++i) {
-            const int r = r0 + i;
-            if (stop || r > runs) break;
-            uint64_t w = wb[i];
-            int spins = 0;
-            while (__ballot(in && !ready(w)) != 0 && spins < kSpinLimit) {
-              __builtin_amdgcn_s_sleep(1);
-              if (!ready(w)) w = atomic_load_u64(word + r);
-              ++spins;
-            }
-            const bool lost = __ballot(in && !ready(w)) != 0;
-            const int total =
-                lost ? -1 : wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
-            if (lane == 0) {
-              lds_proof[r] = total;
-              sync_store(&lds_proof_done, static_cast<uint32_t>(r));
-            }
-            stop = lost || old_free - total < proof_rows;
+          uint64_t w = atomic_load_u64(word + r);
+          int spins = 0;
+          while (__ballot(in && !ready(w)) != 0 && spins < kSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+            if (!ready(w)) w = atomic_load_u64(word + r);
+            ++spins;
           }
+          const bool lost = __ballot(in && !ready(w)) != 0;
+          const int total = lost ? -1 : wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
+          if (lane == 0) {
+            lds_proof[r] = total;
+            sync_store(&lds_proof_done, static_cast<uint32_t>(r));
+          }
+          stop = lost || old_free - total < proof_rows;
         }
       }
     }
