@@ -325,8 +325,7 @@ void sdm_trace_kernel(StepParams P) {
         const int64_t* const scan_l = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
         const uint32_t ep = static_cast<uint32_t>(scan_l[COWSDM_SCRATCH_EPOCH]);
         const bool in = lane < B;
-        const int64_t* const word = scan_l + COWSDM_SCRATCH_SLOTS +
-                                    static_cast<int64_t>(in ? lane : 0) * P.steps;
+        const int64_t* const word = scan_l + COWSDM_SCRATCH_SLOTS + (in ? lane : 0);
         auto ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
           return static_cast<uint32_t>(w >> 32) == ep && ((w >> 30) & 3u) == kStatusAggregate;
         };
@@ -346,11 +345,11 @@ void sdm_trace_kernel(StepParams P) {
             if (static_cast<int>(published) + kLead >= r * k) break;
             __builtin_amdgcn_s_sleep(8);
           }
-          uint64_t w = atomic_load_u64(word + r);
+          uint64_t w = atomic_load_u64(word + static_cast<int64_t>(r) * B);
           int spins = 0;
           while (__ballot(in && !ready(w)) != 0 && spins < kSpinLimit) {
             __builtin_amdgcn_s_sleep(1);
-            if (!ready(w)) w = atomic_load_u64(word + r);
+            if (!ready(w)) w = atomic_load_u64(word + static_cast<int64_t>(r) * B);
             ++spins;
           }
           const bool lost = __ballot(in && !ready(w)) != 0;
@@ -1239,15 +1238,14 @@ void sdm_trace_kernel(StepParams P) {
   uint64_t pw[SCANW];                 // the published counts of the next proof
 #pragma unroll
   for (int k = 0; k < SCANW; ++k) pw[k] = 0;
-  // Bank b's count after its r-th run is word b * P.steps + r of the slots
-  // (a launch has fewer runs than steps): each bank writes words of its own,
-  // never a cache line another bank writes to.
-  const int64_t run_stride = P.steps;
-  const int64_t* run_l[SCANW];        // this lane's bank in each window
+  // Bank b's count after its r-th run is word r * B + b of the slots (a
+  // launch has fewer runs than steps): the counts a proof sums are B
+  // consecutive words, loaded with one cache line per eight banks.
+  const int64_t* run_l[SCANW];        // this lane's bank in each window (run 0)
 #pragma unroll
   for (int k = 0; k < SCANW; ++k) {
     const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
-    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk * run_stride;
+    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk;
   }
 
   // Map in LDS: a bank counts its runs' first touches a chunk (64 steps)
@@ -1316,7 +1314,7 @@ void sdm_trace_kernel(StepParams P) {
           }
           // run r ends in this chunk: its count is word r + 1
           if (a + proof_steps <= t1 && lane == 0) {
-            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + r + 1,
+            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + static_cast<int64_t>(r + 1) * B + bank,
                              slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(ahead_cum)));
           }
         }
@@ -1363,7 +1361,7 @@ void sdm_trace_kernel(StepParams P) {
           int spins = 0;
           while (__ballot(in && !word_ready(w)) != 0 && spins < kSpinLimit) {
             __builtin_amdgcn_s_sleep(1);
-            if (!word_ready(w)) w = atomic_load_u64(run_l[k] + off);
+            if (!word_ready(w)) w = atomic_load_u64(run_l[k] + static_cast<int64_t>(off) * B);
             ++spins;
           }
           if (__ballot(in && !word_ready(w)) != 0) {
@@ -1395,7 +1393,7 @@ void sdm_trace_kernel(StepParams P) {
           ++runs_published;
           // (map in LDS: published by the count ahead)
           if (!MAPLDS && t < G && lane == 0) {
-            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + bank * run_stride + runs_published,
+            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + static_cast<int64_t>(runs_published) * B + bank,
                              slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(cum)));
           }
           run_left = proof_steps;
@@ -1430,7 +1428,7 @@ void sdm_trace_kernel(StepParams P) {
         const uint32_t off = static_cast<uint32_t>(proof_run);
 #pragma unroll
         for (int k = 0; k < SCANW; ++k) {
-          if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + off);
+          if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + static_cast<int64_t>(off) * B);
         }
       }
     }
