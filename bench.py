@@ -9,7 +9,7 @@ four decode steps (max(16, B*4*4) rows), then decode runs on the packed
 state.  One bench "step" is one decode token for all 7 layers and all B
 requests.
 
-Decode loop: persistent launches of up to 256 steps for every (layer, bank);
+Decode loop: persistent launches of up to 512 steps for every (layer, bank);
 before every 4 steps each packed layer proves on the device that its free
 rows cover the worst case (prepare_step_capacity(B*W*4) of the reference's
 decode loop); a layer that would not is stopped there, grown on the host by
@@ -63,7 +63,7 @@ def parse():
     p.add_argument("--batch", type=int, default=64)
     p.add_argument("--proof-steps", type=int, default=4,
                    help="decode steps per capacity proof (the growth quantum's steps)")
-    p.add_argument("--launch-steps", type=int, default=256, help="decode steps per launch")
+    p.add_argument("--launch-steps", type=int, default=512, help="decode steps per launch")
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")

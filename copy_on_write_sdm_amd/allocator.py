@@ -1129,7 +1129,7 @@ class DecodeTrace:
     exactly when ``prepare_step_capacity`` would.  ``outputs`` is
     [S, L, B, D] (one reading per step) or [L, B, D] (every step overwrites
     the same buffer).  ``memories`` given instead of ``states`` runs the
-    dense-table control.  Persistent launches run up to 256 steps per kernel.
+    dense-table control.  Persistent launches run up to 512 steps per kernel.
     No counterpart in the reference.
     """
 
@@ -1138,7 +1138,7 @@ class DecodeTrace:
 
     def __init__(self, *, states=None, memories=None, write_indices, write_weights, values,
                  input_gate, forget_log_gate, read_indices, read_weights, erase_gate=None,
-                 outputs=None, persistent: bool = True, max_steps_per_launch: int = 256):
+                 outputs=None, persistent: bool = True, max_steps_per_launch: int = 512):
         if (states is None) == (memories is None):
             raise ValueError("give exactly one of states or memories")
         self.dense = memories is not None
@@ -1267,7 +1267,7 @@ class DecodeTrace:
         nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
                   "decode trace launch")
 
-    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 256,
+    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 512,
             timing: list | None = None) -> dict:
         """Decode the next ``steps`` steps of every layer from the device
         counters (which must agree), ``launch_steps`` steps per launch.

@@ -25,7 +25,7 @@ constexpr int kPerThread = kTile / kTileThreads;
 // persistent multi-step launches
 constexpr int kTraceMaxWrites = 4;
 constexpr int kTraceMaxReads = 16;
-constexpr int kTraceMaxSteps = 256;         // steps per persistent launch
+constexpr int kTraceMaxSteps = 512;         // steps per persistent launch
 constexpr int kTraceScanWindows = 4;        // up to 256 banks per layer
 constexpr int kTraceFreeWindow = 1024;      // top of the free stack staged in LDS
 constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are staged in LDS

@@ -183,13 +183,13 @@ __device__ __forceinline__ void sync_store(uint32_t* p, uint32_t v) {
 }
 
 // Sum over the wave of per-lane counts of one launch's first touches (at
-// most kTraceMaxWrites * kTraceMaxSteps = 1024 per bank, 11 bits), by bit
-// planes: ballots and scalar adds, no LDS round trip.
+// most kTraceMaxWrites * kTraceMaxSteps per bank), by bit planes: ballots
+// and scalar adds, no LDS round trip.
+constexpr int kLaunchCountBits = 32 - __builtin_clz(kTraceMaxWrites * kTraceMaxSteps);
 __device__ __forceinline__ int wave_sum_launch(int v) {
-  static_assert(kTraceMaxWrites * kTraceMaxSteps < (1 << 11), "counts exceed 11 bits");
   int sum = 0;
 #pragma unroll
-  for (int b = 0; b < 11; ++b) sum += __popcll(__ballot((v >> b) & 1)) << b;
+  for (int b = 0; b < kLaunchCountBits; ++b) sum += __popcll(__ballot((v >> b) & 1)) << b;
   return sum;
 }
 

@@ -141,14 +141,14 @@ typedef struct cowsdm_trace {
   int64_t* ticket;
   int64_t first_step;
   int64_t stride_bytes[9];
-  /* Persistent launches: with persistent != 0 one launch runs up to 256
+  /* Persistent launches: with persistent != 0 one launch runs up to 512
    * steps when the shape allows it (W <= 4, R <= 16, D <= 256, banks <= 256
    * for packed state, and every workgroup of one layer resident; layers
    * whose workgroups do not all fit at once run as groups of layers, one
    * launch after another), else one launch per step -- and with proof_rows
    * > 0 a COWSDM_ELIMIT error, since per-step launches make no proofs.
    * Packed launches then need `scan`: nlayers blocks of scan_words int64
-   * words (>= cowsdm_trace_scan_words(banks, min(steps, 256))), zero before
+   * words (>= cowsdm_trace_scan_words(banks, min(steps, 512))), zero before
    * first use and kept valid by the kernels, and `ticket` (1 + nlayers
    * int64 words, zero before the first launch), also with host offsets:
    * the layer's last wave to finish writes free_count back.  First touches

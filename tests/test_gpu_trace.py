@@ -82,6 +82,7 @@ def _per_step(states, routes, steps, layers):
     (1, 3, 4096, 64, 3, 7, 12, 5),       # largest slot map staged in LDS
     (2, 6, 64, 128, 4, 16, 200, 200),    # 200 steps in one launch: gates in 4 chunks
     (1, 4, 48, 64, 3, 5, 129, 129),      # odd launch whose last step starts a chunk
+    (1, 3, 96, 64, 4, 8, 300, 300),      # one launch of more than 256 steps
 ])
 def test_persistent_trace_matches_single_steps(device, layers, banks, slots, width, writes,
                                               reads, steps, group):
@@ -293,12 +294,28 @@ def test_device_counter_graph_replay(device, persistent):
 
 @pytest.mark.parametrize("proof_steps,launch_steps", [(4, 64), (4, 8), (2, 6)])
 def test_device_proof_matches_host_proofs(device, proof_steps, launch_steps):
+    _device_proof_case(device, proof_steps, launch_steps, layers=3, banks=8, slots=64,
+                       width=128, steps=40, capacity=24, quantum=16, grows=True)
+
+
+def test_device_proof_long_launch(device):
+    """One launch of 400 steps over 4,096 slots with room for every slot: a
+    bank's first touches in the launch pass 1,024, so the proofs sum counts
+    of twelve bits."""
+
+    states = _device_proof_case(device, 2, 400, layers=1, banks=4, slots=4096, width=64,
+                                steps=400, capacity=4 * 4096, quantum=256, grows=False)
+    assert int((states[0].logical_to_physical >= 0).sum(1).min()) > 1024
+
+
+def _device_proof_case(device, proof_steps, launch_steps, *, layers, banks, slots, width,
+                       steps, capacity, quantum, grows):
     """run(): capacity proven on the device every proof_steps steps, a layer
     stopped and grown when prepare_step_capacity would grow it, must leave
     the same slabs, maps, free stacks, growth counters and readings as the
     host loop that proves each group and then runs its single steps."""
 
-    layers, banks, slots, width, writes, reads, steps = 3, 8, 64, 128, 4, 8, 40
+    writes, reads = 4, 8
     m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=31, device=device)
     routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
                                   width=width, writes=writes, reads=reads, seed=32, device=device)
@@ -308,8 +325,9 @@ def test_device_proof_matches_host_proofs(device, proof_steps, launch_steps):
               read_weights=routes.read_weights)
 
     def fresh():
-        return [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks, capacity_rows=24,
-                                                       growth_quantum_rows=16)
+        return [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks,
+                                                       capacity_rows=capacity,
+                                                       growth_quantum_rows=quantum)
                 for l in range(layers)]
 
     host, dev_states = fresh(), fresh()
@@ -327,7 +345,7 @@ def test_device_proof_matches_host_proofs(device, proof_steps, launch_steps):
     tr = cow.DecodeTrace(states=dev_states, outputs=outputs, **kw)
     report = tr.run(steps, proof_steps=proof_steps, launch_steps=launch_steps)
     torch.cuda.synchronize()
-    assert report["growth_rounds"] > 0
+    assert (report["growth_rounds"] > 0) == grows
     assert tr.step_index.tolist() == [steps] * layers
     assert torch.equal(outputs, want)
     for a, b in zip(dev_states, host):
@@ -336,6 +354,7 @@ def test_device_proof_matches_host_proofs(device, proof_steps, launch_steps):
             b.growth_events, b.growth_rows_added, b.growth_rows_copied)
         assert_states_match(a, b)
         a.validate_invariants()
+    return dev_states
 
 
 def test_host_offsets_past_recorded_steps_raise(device):
