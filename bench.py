@@ -223,7 +223,8 @@ def main() -> int:
 
     def measure(trace):
         trace.set_step(0)
-        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
+        # the warmup takes the same host path as the timed run, events included
+        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps, timing=[])
         torch.cuda.synchronize()
         alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
                   if not trace.dense else 0)

@@ -1357,4 +1357,12 @@ class DecodeTrace:
             # the device spent the allowance: the next host proof re-reads
             for state in self.tables:
                 state.proven_maximum_additional_allocations = 0
+        if rounds:
+            # growth moved slabs and the last round's launches may have marked
+            # layers already at the target: rebuild the launch structs and
+            # clear the status now, on this already slow path, rather than at
+            # the start of the next run
+            self.layer_array()
+            self.status.zero_()
+            self._status_clean = True
         return {"launches": launches, "growth_rounds": rounds}
