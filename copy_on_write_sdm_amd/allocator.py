@@ -1340,10 +1340,12 @@ class DecodeTrace:
                 refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]
                 if refused != behind:
                     raise RuntimeError(f"decode trace stopped short at steps {positions}")
-                for l in refused:
-                    state = self.tables[l]
+                # prepare_step_capacity on each refused layer, the free
+                # counts read in one transfer
+                grown = [self.tables[l] for l in refused]
+                for state in grown:
                     state.proven_maximum_additional_allocations = 0
-                    state.prepare_step_capacity(need)
+                PackedSDMCopyOnWriteState.prepare_step_capacity_layers(grown, need)
                 self.status.zero_()
                 remaining = target - min(positions)
                 rounds += 1
