@@ -24,7 +24,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Any, Sequence
 
 import torch
@@ -117,7 +117,9 @@ class PackedSDMCopyOnWriteState:
     (model-shared M0), ``template_indices`` [B] int64, ``values`` [C,D] slab,
     ``logical_to_physical`` [B,N] int32 (-1 = shared M0), ``free_rows`` [C]
     int32 stack with ``free_count`` entries, ``overflow_flag``; plus
-    ``scratch``, the device words of the bank-order scan.
+    ``scratch``, the device words of the bank-order scan.  After a growth,
+    ``values`` and ``free_rows`` are the leading rows of buffers with
+    headroom (``slab_buffers``), so later growths that fit move no rows.
     """
 
     shared_initial_memory: torch.Tensor
@@ -134,6 +136,8 @@ class PackedSDMCopyOnWriteState:
     growth_rows_added: int = 0
     growth_rows_copied: int = 0
     scratch: torch.Tensor | None = None
+    # (values buffer, free-row buffer) that values and free_rows lead, or None
+    slab_buffers: Any = field(default=None, repr=False, compare=False)
 
     # --------------------------------------------------------- creation
 
@@ -295,7 +299,8 @@ class PackedSDMCopyOnWriteState:
     def grow_capacity(self, minimum_capacity_rows: int) -> int:
         """Grow the shared value slab without changing logical state
         (allocator.py:691-743).  Row ids stay stable; new ids join the top of
-        the free stack; every old row is counted as copied."""
+        the free stack; every old row is counted as copied, as the reference
+        counts them, though a slab growing within its headroom moves none."""
 
         if minimum_capacity_rows <= self.capacity_rows:
             return 0
@@ -308,8 +313,24 @@ class PackedSDMCopyOnWriteState:
         old_capacity = self.capacity_rows
         added = selected - old_capacity
         device = self.values.device
-        values = torch.empty(selected, self.width, device=device, dtype=self.values.dtype)
-        free_rows = torch.empty(selected, device=device, dtype=self.free_rows.dtype)
+        buffers = self.slab_buffers
+        if (buffers is not None and buffers[0].shape[0] >= selected
+                and buffers[0].data_ptr() == self.values.data_ptr()
+                and buffers[1].data_ptr() == self.free_rows.data_ptr()):
+            # the slab leads a buffer with room: grow in place
+            values, free_rows = buffers[0][:selected], buffers[1][:selected]
+        else:
+            # new buffers with headroom for as much growth again (at most
+            # one row per logical slot beyond it), so that the growths of a
+            # decode move rows a logarithmic number of times
+            room = max(selected, min(growth_target(2 * selected, quantum),
+                                     selected + self.banks * self.slots))
+            if room >= 2**31:
+                room = selected
+            vbuf = torch.empty(room, self.width, device=device, dtype=self.values.dtype)
+            fbuf = torch.empty(room, device=device, dtype=self.free_rows.dtype)
+            self.slab_buffers = (vbuf, fbuf)
+            values, free_rows = vbuf[:selected], fbuf[:selected]
         nat.check(
             nat.lib().cowsdm_grow(
                 self.values.data_ptr(), old_capacity, values.data_ptr(), selected,
@@ -432,6 +453,7 @@ class PackedSDMCopyOnWriteState:
         self.values = values
         self.logical_to_physical = mapping
         self.free_rows = free_rows
+        self.slab_buffers = None
         self.capacity_is_proven = False
         self.proven_maximum_additional_allocations = selected - active_count
         return removed
@@ -585,8 +607,9 @@ class PackedSDMCopyOnWriteState:
 
     def storage_bytes(self) -> dict[str, int]:
         """Retained tensor storage, shared model state separate
-        (allocator.py:965-982); ``step_scratch`` is this build's extra
-        allocator metadata."""
+        (allocator.py:965-982); ``step_scratch`` (allocator metadata) and
+        ``slab_headroom`` (growth room beyond the capacity rows) are this
+        build's extras."""
 
         private = {
             "value_slab_reserved": _tensor_bytes(self.values),
@@ -596,6 +619,10 @@ class PackedSDMCopyOnWriteState:
             "overflow_flag": _tensor_bytes(self.overflow_flag),
             "template_indices": _tensor_bytes(self.template_indices),
             "step_scratch": 0 if self.scratch is None else _tensor_bytes(self.scratch),
+            # this build's growth headroom beyond the capacity rows
+            "slab_headroom": 0 if self.slab_buffers is None else (
+                _tensor_bytes(self.slab_buffers[0]) - _tensor_bytes(self.values)
+                + _tensor_bytes(self.slab_buffers[1]) - _tensor_bytes(self.free_rows)),
         }
         private["private_allocator_reserved_total"] = sum(private.values())
         private["shared_initial_memory"] = _tensor_bytes(self.shared_initial_memory)

@@ -957,12 +957,15 @@ int32_t cowsdm_grow(const float* old_values, int64_t old_capacity, float* new_va
     return fail(COWSDM_EARG, "grow: invalid arguments");
   }
   const hipStream_t s = as_stream(stream);
-  const int64_t vecs = old_capacity * (width % 4 == 0 ? width / 4 : width);
-  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s,
-                     new_values, static_cast<const int32_t*>(nullptr), old_values,
-                     static_cast<const int32_t*>(nullptr), static_cast<const int64_t*>(nullptr),
-                     old_capacity, width);
-  if (int32_t e = launch_status("grow copy")) return e;
+  if (new_values != old_values) {
+    // (a slab with headroom grows in place: its rows stay where they are)
+    const int64_t vecs = old_capacity * (width % 4 == 0 ? width / 4 : width);
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(vecs, 256)), dim3(256), 0, s,
+                       new_values, static_cast<const int32_t*>(nullptr), old_values,
+                       static_cast<const int32_t*>(nullptr), static_cast<const int64_t*>(nullptr),
+                       old_capacity, width);
+    if (int32_t e = launch_status("grow copy")) return e;
+  }
   hipLaunchKernelGGL(grow_free_kernel, dim3(grid_for(new_capacity, 256)), dim3(256), 0, s,
                      old_free_rows, new_free_rows, free_count, old_capacity, new_capacity);
   if (int32_t e = launch_status("grow free")) return e;

@@ -243,7 +243,9 @@ int32_t cowsdm_init_state(int32_t* logical_to_physical, int64_t banks,
 
 /* Slab growth: new_values[:old_C] = old_values; new_free_rows =
  * old free entries ++ (old_C .. new_C-1); free_count += new_C - old_C;
- * overflow = 0.  Replaces grow_capacity, allocator.py:691-743. */
+ * overflow = 0.  Replaces grow_capacity, allocator.py:691-743.  new_values
+ * may be old_values (and new_free_rows old_free_rows): a slab allocated with
+ * headroom grows in place, and no row moves. */
 int32_t cowsdm_grow(const float* old_values, int64_t old_capacity,
                     float* new_values, int64_t new_capacity, int64_t width,
                     const int32_t* old_free_rows, int32_t* new_free_rows,
