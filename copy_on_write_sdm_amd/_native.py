@@ -155,6 +155,7 @@ class Trace(ctypes.Structure):
         ("steps_recorded", ctypes.c_int64),
         ("proof_rows", ctypes.c_int64),
         ("status", ctypes.c_void_p),
+        ("free_out", ctypes.c_void_p),
     ]
 
 
@@ -234,7 +235,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = restype
                 fn.argtypes = argtypes
-            if handle.cowsdm_abi_version() != 3:
+            if handle.cowsdm_abi_version() != 4:
                 raise RuntimeError("libcowsdm.so ABI version mismatch")
             _lib = handle
     return _lib

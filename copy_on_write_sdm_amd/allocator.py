@@ -372,9 +372,12 @@ class PackedSDMCopyOnWriteState:
     @staticmethod
     @torch.no_grad()
     def prepare_step_capacity_layers(states: Sequence["PackedSDMCopyOnWriteState"],
-                                     maximum_new_rows: int) -> list[int]:
+                                     maximum_new_rows: int,
+                                     free_counts: Sequence[int] | None = None) -> list[int]:
         """``prepare_step_capacity(maximum_new_rows)`` on every state, with
-        the free counts the proofs need read in one device-to-host transfer.
+        the free counts the proofs need read in one device-to-host transfer
+        (or taken from ``free_counts``, one per state, when the caller has
+        just read them at the same point of the stream).
 
         Decisions equal separate calls made at the same point of the stream:
         each state still reads its free count only when its running proof is
@@ -383,11 +386,15 @@ class PackedSDMCopyOnWriteState:
 
         if maximum_new_rows < 0:
             raise ValueError("maximum new SDM rows cannot be negative")
-        short = [st for st in states
+        picks = [i for i, st in enumerate(states)
                  if st.growth_quantum_rows > 0
                  and st.proven_maximum_additional_allocations < maximum_new_rows]
+        short = [states[i] for i in picks]
         if short:
-            frees = torch.stack([st.free_count for st in short]).tolist()
+            if free_counts is not None:
+                frees = [int(free_counts[i]) for i in picks]
+            else:
+                frees = torch.stack([st.free_count for st in short]).tolist()
             for st, free_rows in zip(short, frees):
                 if free_rows < maximum_new_rows:
                     free_rows += st.grow_capacity(
@@ -1195,9 +1202,13 @@ class DecodeTrace:
         self.outputs = outputs
         self.steps = steps
         self.device = device
-        self.step_index = torch.zeros(layers, dtype=torch.int64, device=device)
+        # one int64 report read back per round: row 0 the per-layer step
+        # counters, row 1 the int32 status words, row 2 the free counts the
+        # launches leave (packed state)
+        self._report = torch.zeros(3, layers, dtype=torch.int64, device=device)
+        self.step_index = self._report[0]
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
-        self.status = torch.zeros(layers, dtype=torch.int32, device=device)
+        self.status = self._report[1].view(torch.int32)[:layers]
         # the kernels only set status bits: run() clears them when a launch
         # may have left some (a refusal, a direct launch)
         self._status_clean = True
@@ -1206,6 +1217,7 @@ class DecodeTrace:
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.ticket = self.ticket.data_ptr()
         self.trace.status = self.status.data_ptr()
+        self.trace.free_out = None if self.dense else self._report[2].data_ptr()
         for k, name in enumerate(self._INPUTS):
             tensor = self.inputs[name]
             self.trace.stride_bytes[k] = tensor.stride(0) * tensor.element_size()
@@ -1237,16 +1249,23 @@ class DecodeTrace:
 
     def layer_array(self):
         """The per-layer C structs for the current state pointers (they
-        change when a slab grows or is trimmed); rebuilt only when a pointer
-        moved."""
+        change when a slab is reallocated or trimmed); rebuilt only when a
+        pointer moved, patched when only capacities changed (a slab grown
+        within its headroom)."""
 
         key = tuple((t.data_ptr(),) if self.dense else
                     (t.values.data_ptr(), t.free_rows.data_ptr(), t.free_count.data_ptr(),
                      t.overflow_flag.data_ptr(), t.logical_to_physical.data_ptr(),
                      t.template_indices.data_ptr(), t.shared_initial_memory.data_ptr(),
-                     t.scratch.data_ptr(), t.capacity_rows) for t in self.tables)
+                     t.scratch.data_ptr()) for t in self.tables)
+        capacities = tuple(0 if self.dense else t.capacity_rows for t in self.tables)
         if self._layers is not None and self._layers[0] == key:
-            return self._layers[1]
+            layers = self._layers[1]
+            if self._layers[2] != capacities:
+                for l, capacity in enumerate(capacities):
+                    layers[l].capacity_rows = capacity
+                self._layers = (key, layers, capacities)
+            return layers
         count = len(self.tables)
         layers = (nat.Layer * count)()
         for l, table in enumerate(self.tables):
@@ -1257,7 +1276,7 @@ class DecodeTrace:
                 x["write_indices"], x["write_weights"], x["values"], x["input_gate"],
                 x["erase_gate"], x["forget_log_gate"], x["read_indices"], x["read_weights"],
                 out, None, None, None)
-        self._layers = (key, layers)
+        self._layers = (key, layers, capacities)
         return layers
 
     def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
@@ -1356,23 +1375,27 @@ class DecodeTrace:
                     else:
                         self._call(layers, launch_steps, stream)
                     launches += 1
-                positions = self.step_index.tolist()
+                report = self._report.tolist()    # counters, status, free counts
+                positions = report[0]
                 behind = [l for l, p in enumerate(positions) if p < target]
                 if not behind:
                     # without growth rounds every layer ran from the same
                     # step and none stopped short: no launch set a status bit
                     self._status_clean = rounds == 0
                     break
-                status = self.status.tolist()
+                words = report[1]   # int32 status word l is half l % 2 of word l // 2
+                status = [(words[l // 2] >> (32 * (l % 2))) & 0xFFFFFFFF
+                          for l in range(len(self.tables))]
                 refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]
                 if refused != behind:
                     raise RuntimeError(f"decode trace stopped short at steps {positions}")
-                # prepare_step_capacity on each refused layer, the free
-                # counts read in one transfer
+                # prepare_step_capacity on each refused layer, with the free
+                # counts its launches left (read back with the counters)
                 grown = [self.tables[l] for l in refused]
                 for state in grown:
                     state.proven_maximum_additional_allocations = 0
-                PackedSDMCopyOnWriteState.prepare_step_capacity_layers(grown, need)
+                PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
+                    grown, need, free_counts=[report[2][l] for l in refused])
                 self.status.zero_()
                 remaining = target - min(positions)
                 rounds += 1

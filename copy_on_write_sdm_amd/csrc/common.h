@@ -59,6 +59,7 @@ struct StepParams {
   int64_t trace_len;             // steps the trace inputs hold
   int64_t trace_proof_rows;      // device capacity proof per run of proof steps, or 0
   int32_t* trace_status;         // per-layer status bits, or null
+  int64_t* trace_free_out;       // per-layer free_count after a launch, or null
   int32_t trace_proof_steps;
   int64_t trace_stride[9];
   int64_t* scan;                 // persistent launches: per-layer scan words

@@ -738,6 +738,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   P.trace_proof_rows = trace ? trace->proof_rows : 0;
   P.trace_proof_steps = trace ? trace->proof_steps : 0;
   P.trace_status = trace ? trace->status : nullptr;
+  P.trace_free_out = trace ? trace->free_out : nullptr;
   if (P.trace_proof_rows > 0) {
     if (dense) return fail(COWSDM_EARG, "trace: capacity proofs apply to packed state");
     if (!trace->step_index) return fail(COWSDM_EARG, "trace: capacity proofs need device counters");

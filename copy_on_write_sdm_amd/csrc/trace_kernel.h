@@ -1627,6 +1627,9 @@ void sdm_trace_kernel(StepParams P) {
         const int64_t fit = fail > 0 && kClaimFailBase - fail < total ? kClaimFailBase - fail : total;
         if (lane == 0) {
           *L.free_count = static_cast<int32_t>(old_free - fit);
+          if (P.trace_free_out) {
+            atomic_store_u64(&P.trace_free_out[layer_id], static_cast<uint64_t>(old_free - fit));
+          }
           atomic_store_u64(claims, 0);
           atomic_store_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL, 0);
           atomic_store_u64(scan + COWSDM_SCRATCH_EPOCH, static_cast<uint64_t>(epoch + 1u));
@@ -1715,6 +1718,7 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
     if (P0.trace_step) Q.trace_step = P0.trace_step + l0;
     if (P0.trace_ticket) Q.trace_ticket = P0.trace_ticket + l0;  // word 1 + layer
     if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
+    if (P0.trace_free_out) Q.trace_free_out = P0.trace_free_out + l0;
     if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
     void* args[] = {&Q};
     (void)hipLaunchKernel(kernel, dim3(Q.blocks_per_layer * Q.nlayers), dim3(threads), args,

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 3
+#define COWSDM_ABI_VERSION 4
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -162,6 +162,10 @@ typedef struct cowsdm_trace {
   int64_t steps_recorded;
   int64_t proof_rows;
   int32_t* status;
+  /* Packed state, or null: the layer's last wave to finish a launch also
+   * writes the layer's free_count to free_out[l] (int64), so that a caller
+   * reads the counters, the status words and the free counts back at once. */
+  int64_t* free_out;
 } cowsdm_trace_t;
 
 /* ---------------------------------------------------------------- info */

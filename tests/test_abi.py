@@ -38,7 +38,7 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == 3
+    assert lib.cowsdm_abi_version() == 4
     assert lib.cowsdm_step_scratch_words(64) == 8 + 64
     assert lib.cowsdm_step_scratch_words(-1) == -1
     assert lib.cowsdm_workspace_bytes(0, 0) == 256
@@ -65,7 +65,7 @@ def test_structure_layout_matches_header():
     # 21 pointer-sized fields and one int64 in cowsdm_layer_t
     assert ctypes.sizeof(nat.Layer) == 21 * 8
     assert ctypes.sizeof(nat.Shape) == 7 * 8
-    assert ctypes.sizeof(nat.Trace) == 18 * 8
+    assert ctypes.sizeof(nat.Trace) == 19 * 8
 
 
 @pytest.mark.parametrize("name", ["cowsdm_packed_step", "cowsdm_dense_step",
