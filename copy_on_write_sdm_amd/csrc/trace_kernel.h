@@ -815,7 +815,7 @@ void sdm_trace_kernel(StepParams P) {
   // path reads it):
   //   word 0: bits 0-19 rows from step t-1 (write lanes 0-3, read lanes
   //           4-19), 20-23 first touches (fm: lane l's first-touch mask from
-  //           the bitmap pass), 24-31 the COWSDM_ERR_* bits of its routes
+  //           the first-write pass), 24-31 the COWSDM_ERR_* bits of its routes
   //   word 1: bits 0-15 reads of a slot step t writes, 16-19 and 20-23 the
   //           two bit planes of each write lane's source lane in step t-1
   //   words 2, 3: the planes of each read lane's source lane in step t-1 and
@@ -1324,9 +1324,11 @@ void sdm_trace_kernel(StepParams P) {
 
   // The proof before step s, at the loop head before iteration s (s even,
   // the first step of run r = s / proof_steps): every bank published its
-  // count of first touches in runs 0..r-1 when it classified step s-1, three
-  // iterations earlier, and every wave sums the same counts, so the layer
-  // stops at the same step on every wave.  The sum is also run r's base.
+  // count of first touches in runs 0..r-1 (with the map in LDS a chunk
+  // ahead, otherwise when it classified step s-1, three iterations
+  // earlier), and every wave takes the same sum (from the proof wave, or
+  // summed here), so the layer stops at the same step on every wave.  The
+  // sum is also run r's base.
   // Returns true (and the layer stops before s) when free_count minus the
   // base is below proof_rows, or when a count never arrives (bounded wait).
   auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {

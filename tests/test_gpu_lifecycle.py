@@ -82,6 +82,34 @@ def test_reference_growth_known_answer(device):
     assert st.free_rows.tolist() == list(range(8))
 
 
+def test_growth_within_headroom_moves_no_rows(device):
+    """After a growth the slab leads a buffer with room for as much growth
+    again: a later growth that fits keeps every row where it is (the slab's
+    address does not change), one that does not fit moves them, and the
+    state equals the oracle's after the same growths either way."""
+
+    st, orc, _ = _pair(device, steps=4)
+    width = st.width
+    # the smallest growth (new buffers on the first), one that fits, one
+    # past the buffer, and one that fits again
+    for case in ("first", "fits", "past", "fits"):
+        if case == "past":
+            minimum = st.slab_buffers[0].shape[0] + 1
+        else:
+            minimum = st.capacity_rows + 1
+        before = st.values.data_ptr()
+        added = st.grow_capacity(minimum)
+        assert added == ref.grow_capacity(orc, minimum)
+        if case != "first":
+            assert (st.values.data_ptr() == before) == (case == "fits"), case
+        assert_state_equal(st, orc)
+        room = st.slab_buffers[0].shape[0] - st.capacity_rows
+        assert room > 0
+        assert st.storage_bytes()["slab_headroom"] == room * (width * 4 + 4)
+    assert st.growth_rows_copied == orc.growth_rows_copied
+    st.validate_invariants()
+
+
 def test_batched_proof_equals_per_state_proofs(device):
     pairs = [_pair(device, seed=s, steps=3) for s in (5, 6, 7)]
     states = [p[0] for p in pairs]
