@@ -312,7 +312,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": Wm,
-        "ms_per_step": round(1000.0 * p_seconds / K, 5),
+        "ms_per_step": round(1000.0 * p_seconds / K, 7),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
