@@ -153,7 +153,10 @@ def main() -> int:
         return 2
     import torch
 
+    import ctypes
+
     import copy_on_write_sdm_amd as cow
+    from copy_on_write_sdm_amd import _native as nat
     from copy_on_write_sdm_amd import synthetic
 
     dev = torch.device("cuda:0")
@@ -221,26 +224,38 @@ def main() -> int:
     packed = cow.DecodeTrace(states=states, **inputs)
     dense = cow.DecodeTrace(memories=dense_tables, **inputs)
 
+    lib = nat.lib()
+
+    def kernel_ms() -> float:
+        """Summed duration of the trace kernels launched since timing was
+        switched on: HIP events the library records at each kernel's start
+        and end on its stream (hipExtLaunchKernel)."""
+        total, kernels = ctypes.c_double(), ctypes.c_int32()
+        nat.check(lib.cowsdm_trace_timing_read(ctypes.byref(total), ctypes.byref(kernels)),
+                  "trace timing")
+        return total.value
+
     def measure(trace):
         trace.set_step(0)
-        # the warmup takes the same host path as the timed run, events included
-        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps, timing=[])
+        # the warmup takes the same host path as the timed run, timing included
+        lib.cowsdm_trace_timing(1)
+        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
+        kernel_ms()
         alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
                   if not trace.dense else 0)
         grow0 = sum(st.growth_events for st in trace.tables) if not trace.dense else 0
-        events = []
+        lib.cowsdm_trace_timing(1)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps,
-                           timing=events)
+        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
         seconds = time.perf_counter() - t0
+        gpu_ms = kernel_ms()
+        lib.cowsdm_trace_timing(0)
         new_rows = ((sum(int(st.allocated_rows_tensor()) for st in trace.tables) - alloc0)
                     if not trace.dense else 0)
         grows = (sum(st.growth_events for st in trace.tables) - grow0) if not trace.dense else 0
-        # kernel time: HIP events around every launch, on the launch stream
-        gpu_ms = sum(a.elapsed_time(b) for a, b in events)
         return dict(seconds=seconds, gpu_ms=gpu_ms, new_rows=new_rows, growths=grows, **report)
 
     p_run = measure(packed)

@@ -49,6 +49,9 @@ constexpr uint64_t kValueMask = (1ull << 30) - 1;
 int32_t fail(int32_t code, const char* fmt, ...);
 // 0, or the pending hipError_t of the last launch (recorded by fail()).
 int32_t launch_status(const char* where);
+// cowsdm_trace_timing: the start/stop events to record around the next
+// trace kernel launch, or false when timing is off (or its slots are full).
+bool trace_timing_events(hipEvent_t* start, hipEvent_t* stop);
 const char* last_error();
 
 struct StepParams {

@@ -75,6 +75,32 @@ int32_t launch_status(const char* where) {
 
 const char* last_error() { return g_error; }
 
+// cowsdm_trace_timing: event pairs recorded at trace kernels' start and end
+namespace {
+constexpr int kTimingSlots = 1024;
+bool timing_on = false;
+int timing_used = 0;
+int timing_made = 0;
+hipEvent_t timing_start[kTimingSlots];
+hipEvent_t timing_stop[kTimingSlots];
+}  // namespace
+
+bool trace_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  if (!timing_on || timing_used >= kTimingSlots) return false;
+  if (timing_used == timing_made) {
+    if (hipEventCreate(&timing_start[timing_made]) != hipSuccess) return false;
+    if (hipEventCreate(&timing_stop[timing_made]) != hipSuccess) {
+      (void)hipEventDestroy(timing_start[timing_made]);
+      return false;
+    }
+    ++timing_made;
+  }
+  *start = timing_start[timing_used];
+  *stop = timing_stop[timing_used];
+  ++timing_used;
+  return true;
+}
+
 // Validation before a step (validate_routes=True, or a packed state whose
 // capacity has no proof): bounds, duplicate writes, first touches vs the
 // free stack.  One workgroup; writes its result word once.
@@ -853,6 +879,31 @@ int64_t cowsdm_step_scratch_words(int64_t banks) {
 int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps) {
   if (banks < 0 || steps < 0) return -1;
   return COWSDM_SCRATCH_SLOTS + banks * steps + kTraceRunCounters;
+}
+
+int32_t cowsdm_trace_timing(int32_t enable) {
+  timing_on = enable != 0;
+  timing_used = 0;
+  return 0;
+}
+
+int32_t cowsdm_trace_timing_read(double* total_ms, int32_t* kernels) {
+  if (!total_ms || !kernels) return fail(COWSDM_EARG, "trace timing: null argument");
+  double sum = 0.0;
+  for (int i = 0; i < timing_used; ++i) {
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(timing_stop[i]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, timing_start[i], timing_stop[i]);
+    if (e != hipSuccess) {
+      timing_used = 0;
+      return fail(static_cast<int32_t>(e), "trace timing: kernel %d: %s", i, hipGetErrorString(e));
+    }
+    sum += ms;
+  }
+  *total_ms = sum;
+  *kernels = timing_used;
+  timing_used = 0;
+  return 0;
 }
 
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows) {

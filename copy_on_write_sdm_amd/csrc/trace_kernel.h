@@ -53,6 +53,8 @@
 // rows it claimed.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 namespace cowsdm_impl {
@@ -1708,9 +1710,19 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
   // stream, each with its per-layer words offset to its first layer.
   const int per_launch = resident[variant][which] / P.blocks_per_layer;
   if (per_launch <= 0) return false;
+  // plain launches, or with start/stop events when the caller measures
+  auto launch = [&](StepParams* q, int grid) {
+    void* args[] = {q};
+    hipEvent_t start, stop;
+    if (trace_timing_events(&start, &stop)) {
+      (void)hipExtLaunchKernel(kernel, dim3(grid), dim3(threads), args, lds_bytes, stream, start,
+                               stop, 0);
+    } else {
+      (void)hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, lds_bytes, stream);
+    }
+  };
   if (blocks <= resident[variant][which]) {
-    void* args[] = {&P};
-    (void)hipLaunchKernel(kernel, dim3(blocks), dim3(threads), args, lds_bytes, stream);
+    launch(&P, blocks);
     return true;  // a failed launch is reported by the caller's launch_status()
   }
   for (int l0 = 0; l0 < P0.nlayers; l0 += per_launch) {
@@ -1722,9 +1734,7 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
     if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
     if (P0.trace_free_out) Q.trace_free_out = P0.trace_free_out + l0;
     if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
-    void* args[] = {&Q};
-    (void)hipLaunchKernel(kernel, dim3(Q.blocks_per_layer * Q.nlayers), dim3(threads), args,
-                          lds_bytes, stream);
+    launch(&Q, Q.blocks_per_layer * Q.nlayers);
   }
   return true;
 }

@@ -176,6 +176,16 @@ const char* cowsdm_last_error_string(void);
 int64_t cowsdm_step_scratch_words(int64_t banks);
 /* int64 words per layer of a persistent trace launch's scan buffer. */
 int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps);
+
+/* Kernel timing of persistent trace launches, for measurement (no
+ * reference counterpart; one host thread): after cowsdm_trace_timing(1)
+ * each trace kernel launch (up to 1,024) records HIP start and stop events
+ * at the kernel's own start and end on its stream (hipExtLaunchKernel);
+ * cowsdm_trace_timing_read waits for them, returns the summed kernel time
+ * in milliseconds and the number of kernels, and forgets them.
+ * cowsdm_trace_timing(0) stops recording. */
+int32_t cowsdm_trace_timing(int32_t enable);
+int32_t cowsdm_trace_timing_read(double* total_ms, int32_t* kernels);
 /* Bytes of lifecycle workspace for a ranking over `entries` map entries
  * (release / trim / append / pack handoff / invariant checks). */
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows);

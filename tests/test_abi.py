@@ -61,6 +61,16 @@ def test_argument_errors_return_codes_without_launching():
     assert lib.cowsdm_grow(None, 0, None, 0, 0, None, None, None, None, None) == -1
 
 
+def test_trace_timing_without_launches():
+    lib = nat.lib()
+    assert lib.cowsdm_trace_timing(1) == 0
+    total, kernels = ctypes.c_double(-1.0), ctypes.c_int32(-1)
+    assert lib.cowsdm_trace_timing_read(ctypes.byref(total), ctypes.byref(kernels)) == 0
+    assert (total.value, kernels.value) == (0.0, 0)
+    assert lib.cowsdm_trace_timing(0) == 0
+    assert lib.cowsdm_trace_timing_read(None, None) == -1
+
+
 def test_structure_layout_matches_header():
     # 21 pointer-sized fields and one int64 in cowsdm_layer_t
     assert ctypes.sizeof(nat.Layer) == 21 * 8
