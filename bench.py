@@ -74,7 +74,58 @@ def parse():
     p.add_argument("--eager-steps", type=int, default=None,
                    help="steps of the per-layer Python drop-in path to time (0: skip; "
                         "default 32 for config 2, else 0)")
+    p.add_argument("--routes", action="store_true",
+                   help="time product_key_routes (the route producer) instead of the decode "
+                        "step: one JSON line per shape")
     return p.parse_args()
+
+
+ROUTE_SHAPES = ((64, 256, 16), (64, 256, 4), (448, 256, 16), (256, 65536, 16),
+                (4096, 65536, 16), (65536, 256, 16))
+
+
+def bench_routes(steps: int) -> int:
+    """Kernel time of product_key_routes per call (HIP events on torch's
+    current stream, the stream the kernel is launched on) at config 2's
+    shapes (64 rows, N = 256; 448 = 7 layers x 64 banks in one call),
+    config 5's (256 rows, N = 65,536) and two large batches.  Algorithmic
+    bytes per row: 2*sqrt(N)*4 read, K*(4 + 8) written."""
+
+    import torch
+
+    import copy_on_write_sdm_amd as cow
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for rows, slots, k in ROUTE_SHAPES:
+        root = int(round(slots ** 0.5))
+        projected = torch.randn(rows, 1, 2 * root, device=dev, generator=gen)
+        w = torch.empty((rows, 1, k), device=dev)
+        i = torch.empty((rows, 1, k), dtype=torch.int64, device=dev)
+        lib = cow.routing.nat.lib()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+
+        def call():
+            rc = lib.cowsdm_product_key_routes(projected.data_ptr(), rows, slots, k,
+                                               w.data_ptr(), i.data_ptr(), stream)
+            assert rc == 0, rc
+
+        for _ in range(20):
+            call()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            call()
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) * 1e3 / steps
+        nbytes = rows * (2 * root * 4 + k * 12)
+        print(json.dumps({"kernel": "product_key_routes_kernel", "rows": rows, "slots": slots,
+                          "selected": k, "calls": steps, "us_per_call": round(us, 3),
+                          "algorithmic_bytes": nbytes,
+                          "achieved_GBs": round(nbytes / us / 1e3, 1)}), flush=True)
+    return 0
 
 
 def algorithmic_bytes(banks: int, layers: int) -> int:
@@ -151,6 +202,8 @@ def main() -> int:
         print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
               "(the packed SDM step has no multi-GPU path in this build)", file=sys.stderr)
         return 2
+    if args.routes:
+        return bench_routes(args.steps or 500)
     import torch
 
     import ctypes

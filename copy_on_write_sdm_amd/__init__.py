@@ -23,6 +23,7 @@ from .inference import (
     decode_sdm_layer_dense,
     pack_prefill_layer,
 )
+from .routing import product_key_routes
 
 __all__ = [
     "DecodeTrace",
@@ -38,4 +39,5 @@ __all__ = [
     "pack_prefill_layer",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
+    "product_key_routes",
 ]

@@ -22,7 +22,7 @@ REPO_DIR = PACKAGE_DIR.parent
 SOURCE_DIR = PACKAGE_DIR / "csrc"
 # one translation unit per step-kernel family so hipcc can run in parallel
 SOURCES = ("cowsdm.hip", "step_i32_packed.hip", "step_i32_dense.hip", "step_i64_packed.hip",
-           "step_i64_dense.hip")
+           "step_i64_dense.hip", "routes.hip")
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
@@ -206,6 +206,7 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_check_invariants": (
         _I32, [_P, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P]),
     "cowsdm_mark_written": (_I32, [_P, _I64, _I64, _P, _I64, _I32, _P, _P]),
+    "cowsdm_product_key_routes": (_I32, [_P, _I64, _I64, _I64, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

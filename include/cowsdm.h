@@ -383,6 +383,22 @@ int32_t cowsdm_mark_written(uint8_t* active_mask, int64_t banks, int64_t slots,
                             int32_t index_dtype, int64_t* result,
                             void* stream);
 
+/* Product-key routes, sdm.py:96-159 (product_key_routes; called for the
+ * write and read routes of a decode step at inference.py:479-488).
+ * projected is [rows, 2*sqrt(slots)] float32: each row's two halves are
+ * shortlisted to their top min(selected, sqrt(slots)) scores, the pair sums
+ * ranked, and the best K = min(selected, min(selected, sqrt(slots))^2) pairs
+ * written as slots first*sqrt(slots)+second, ascending, to indices[rows, K]
+ * (int64) with the softmax of their scores in weights[rows, K].  Equal scores
+ * are taken lowest position first; inputs must be finite.  Returns -1 for the
+ * reference's argument errors (slots not a square, selected outside
+ * [1, slots]) and -2 beyond the HIP path's limits (sqrt(slots) <= 1024,
+ * min(selected, sqrt(slots)) <= 32, K <= 32). */
+int32_t cowsdm_product_key_routes(const float* projected, int64_t rows,
+                                  int64_t slots, int64_t selected,
+                                  float* weights, int64_t* indices,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif
