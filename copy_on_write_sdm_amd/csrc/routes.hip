@@ -88,12 +88,69 @@ __device__ __forceinline__ void wave_top(const float (&val)[J], const int (&pos)
   wave_lds_sync();
 }
 
+// wave_top for J > 1 (root > 64, every lane holds at least one entry).  The
+// count-th largest lane maximum T bounds the selection: count lane maxima
+// are >= T, so an entry below T ranks at least count and is never selected.
+// The entries >= T (about count + count/4 for random scores) are compacted
+// into one per lane and ranked once; if more than 64 remain (many equal
+// scores), every entry is ranked.
+template <int J>
+__device__ __forceinline__ void wave_top_pruned(const float (&val)[J], const int (&pos)[J],
+                                                int count, int lane, float* stage_val,
+                                                int* stage_pos, float* pool_val, int* pool_pos,
+                                                float& top_val, int& top_pos) {
+  uint64_t key[J];
+  uint64_t best[1] = {0};
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    key[j] = pos[j] >= 0 ? route_key(val[j], pos[j]) : 0;
+    best[0] = key[j] > best[0] ? key[j] : best[0];
+  }
+  int best_rank[1];
+  wave_rank<1>(best, best_rank);   // 64 unique lane maxima: ranks 0..63
+  const uint64_t at = __ballot(best_rank[0] == count - 1);
+  const int holder = at ? __builtin_ctzll(at) : 0;
+  const uint64_t bound =
+      (static_cast<uint64_t>(static_cast<uint32_t>(rl(static_cast<int>(best[0] >> 32), holder)))
+       << 32) |
+      static_cast<uint32_t>(rl(static_cast<int>(static_cast<uint32_t>(best[0])), holder));
+  uint64_t mask[J];
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    mask[j] = __ballot(pos[j] >= 0 && key[j] >= bound);
+    total += __popcll(mask[j]);
+  }
+  if (total > kWave) {
+    wave_top<J>(val, pos, count, lane, stage_val, stage_pos, top_val, top_pos);
+    return;
+  }
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  int base = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if ((mask[j] >> lane) & 1) {
+      const int slot = base + __popcll(mask[j] & below);   // < total <= 64
+      pool_val[slot] = val[j];
+      pool_pos[slot] = pos[j];
+    }
+    base += __popcll(mask[j]);
+  }
+  wave_lds_sync();
+  float one_val[1] = {lane < total ? pool_val[lane] : -__builtin_inff()};
+  int one_pos[1] = {lane < total ? pool_pos[lane] : -1};
+  wave_lds_sync();
+  wave_top<1>(one_val, one_pos, count, lane, stage_val, stage_pos, top_val, top_pos);
+}
+
 template <int J, int M>
 __global__ __launch_bounds__(kWave * kRouteWaves) void product_key_routes_kernel(
     const float* __restrict__ projected, int64_t rows, int root, int sub, int final_k,
     float* __restrict__ weights, int64_t* __restrict__ indices) {
   __shared__ float stage_val[kRouteWaves][kRouteMaxSelected];
   __shared__ int stage_pos[kRouteWaves][kRouteMaxSelected];
+  __shared__ float pool_val[kRouteWaves][kWave];
+  __shared__ int pool_pos[kRouteWaves][kWave];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRouteWaves + wave;
@@ -115,8 +172,15 @@ __global__ __launch_bounds__(kWave * kRouteWaves) void product_key_routes_kernel
   }
   float first_val, second_val;
   int first_idx, second_idx;
-  wave_top<J>(fv, fp, sub, lane, stage_val[wave], stage_pos[wave], first_val, first_idx);
-  wave_top<J>(sv, sp, sub, lane, stage_val[wave], stage_pos[wave], second_val, second_idx);
+  if constexpr (J > 1) {
+    wave_top_pruned<J>(fv, fp, sub, lane, stage_val[wave], stage_pos[wave], pool_val[wave],
+                       pool_pos[wave], first_val, first_idx);
+    wave_top_pruned<J>(sv, sp, sub, lane, stage_val[wave], stage_pos[wave], pool_val[wave],
+                       pool_pos[wave], second_val, second_idx);
+  } else {
+    wave_top<J>(fv, fp, sub, lane, stage_val[wave], stage_pos[wave], first_val, first_idx);
+    wave_top<J>(sv, sp, sub, lane, stage_val[wave], stage_pos[wave], second_val, second_idx);
+  }
 
   // 2. pair c = a * sub + b scores first_val[a] + second_val[b].  Every pair
   // (a', b') <= (a, b) scores at least as high (float addition is monotone)

@@ -36,7 +36,8 @@ def test_routes_match_oracle(slots, selected, batch, steps):
     _check(rng.standard_normal((batch, steps, 2 * root), dtype=np.float32), slots, selected)
 
 
-@pytest.mark.parametrize("slots,selected", [(256, 16), (4096, 32), (16, 16)])
+@pytest.mark.parametrize("slots,selected", [(256, 16), (4096, 32), (16, 16), (65536, 16),
+                                            (1 << 20, 32)])
 def test_routes_with_many_equal_scores(slots, selected):
     rng = np.random.default_rng(selected)
     root = int(np.sqrt(slots))
