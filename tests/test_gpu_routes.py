@@ -45,6 +45,20 @@ def test_routes_with_many_equal_scores(slots, selected):
     _check(projected, slots, selected)
 
 
+@pytest.mark.parametrize("slots,selected", [(65536, 32), (1 << 20, 16)])
+def test_routes_first_stage_fallback(slots, selected):
+    # entries e sit in lane e % 64; giving the first `selected` lanes every
+    # large score leaves selected * sqrt(N) / 64 > 64 entries above the
+    # selected-th lane maximum, so the first stage ranks every entry
+    rng = np.random.default_rng(5)
+    root = int(np.sqrt(slots))
+    projected = rng.standard_normal((12, 1, 2 * root), dtype=np.float32)
+    lanes = np.arange(2 * root) % root % 64
+    projected[..., lanes < selected] += 100.0
+    assert selected * (root // 64) > 64
+    _check(projected, slots, selected)
+
+
 def test_routes_empty_batch_and_errors():
     w, i = cow.product_key_routes(torch.zeros((0, 1, 32), device=DEV), slots=256, selected=16)
     assert w.shape == (0, 1, 16) and i.shape == (0, 1, 16)
