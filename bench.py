@@ -61,8 +61,6 @@ def parse():
     p.add_argument("--steps", type=int, default=None, help="timed steps (default: the config's)")
     p.add_argument("--warmup", type=int, default=None, help="warmup steps (default: the config's)")
     p.add_argument("--batch", type=int, default=64)
-    p.add_argument("--proof-steps", type=int, default=4,
-                   help="decode steps per capacity proof (the growth quantum's steps)")
     p.add_argument("--launch-steps", type=int, default=512, help="decode steps per launch")
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -139,10 +137,10 @@ def algorithmic_bytes(banks: int, layers: int) -> int:
     return banks * layers * (rows + vectors + metadata)
 
 
-def profiled_traffic(batch: int, launch_steps: int) -> dict | None:
+def profiled_traffic(batch: int, launch_steps: float) -> dict | None:
     """HBM bytes per launch of the packed decode kernel from the committed
     counter passes (FETCH_SIZE and WRITE_SIZE, scaled by a copy of known
-    size), when this run has the profiled configuration."""
+    size), when this run's launches ran the profiled number of steps."""
 
     path = ROOT / "profiles" / "traffic_packed_trace_config2_b64.json"
     if not path.exists():
@@ -170,7 +168,7 @@ def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
     m0 = synthetic.make_initial_memory(LAYERS, 1, SLOTS, WIDTH, seed=seed)
     batch_inputs = synthetic.make_steps(steps=steps, layers=LAYERS, banks=batch, slots=SLOTS,
                                         width=WIDTH, writes=WRITES, reads=READS, seed=seed + 1)
-    tables = [m0[l, 0].expand(batch, -1, -1).contiguous() for l in range(LAYERS)]
+    tables = [m0[l, 0].expand(batch, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(LAYERS)]
     for s in range(2):
         for l in range(LAYERS):
             torch_port.dense_step(tables[l], **batch_inputs.step(s, l))
@@ -292,7 +290,7 @@ def main() -> int:
         trace.set_step(0)
         # the warmup takes the same host path as the timed run, timing included
         lib.cowsdm_trace_timing(1)
-        trace.run(Wm, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
+        trace.run(Wm, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
         kernel_ms()
         alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
@@ -301,7 +299,7 @@ def main() -> int:
         lib.cowsdm_trace_timing(1)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        report = trace.run(K, proof_steps=args.proof_steps, launch_steps=args.launch_steps)
+        report = trace.run(K, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
         seconds = time.perf_counter() - t0
         gpu_ms = kernel_ms()
@@ -365,7 +363,7 @@ def main() -> int:
     bytes_per_launch = (algorithmic_bytes(banks, LAYERS) * K + 8 * new_rows) / launches
     achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
     dense_launch_us = 1000.0 * d_run["gpu_ms"] / d_run["launches"]
-    traffic = profiled_traffic(B, args.launch_steps) if args.config == 2 else None
+    traffic = profiled_traffic(B, K / launches) if args.config == 2 else None
     # the persistent variant that ran: full shape (W = 4, R = 16), one scan
     # window up to 64 banks, slot map in LDS up to 4,096 slots
     kernel = (f"sdm_trace_kernel<int, 2, false, true, {1 if banks <= 64 else 4}, "
@@ -394,7 +392,7 @@ def main() -> int:
             "width": WIDTH, "writes": WRITES, "reads": READS, "prefix": PREFIX,
             "distribution": cfg["distribution"],
             "growth_quantum_rows": quantum, "steps_per_launch": args.launch_steps,
-            "capacity_proof": f"on the device, every {args.proof_steps} steps per layer",
+            "capacity_proof": "the reference's per-step proof, planned on the device per launch",
             "launch": "persistent launches over all layers and banks",
             "parallelism": "single GPU",
         },

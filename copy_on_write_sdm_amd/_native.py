@@ -22,7 +22,7 @@ REPO_DIR = PACKAGE_DIR.parent
 SOURCE_DIR = PACKAGE_DIR / "csrc"
 # one translation unit per step-kernel family so hipcc can run in parallel
 SOURCES = ("cowsdm.hip", "step_i32_packed.hip", "step_i32_dense.hip", "step_i64_packed.hip",
-           "step_i64_dense.hip", "routes.hip")
+           "step_i64_dense.hip", "trace_plan.hip", "routes.hip")
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
@@ -39,8 +39,25 @@ ERR_CORRUPT = 0x20
 ERR_LOOKBACK = 0x40
 ERR_TRACE_RANGE = 0x80
 
-TRACE_REFUSED = 0x1   # status bit: a device capacity proof failed
+TRACE_REFUSED = 0x1   # status bit: stopped before a growth past the slab buffers
 TRACE_ENDED = 0x2     # status bit: no recorded step left
+TRACE_FAULT = 0x4     # status bit: a timed-out wait or corrupt state stopped the layer
+
+# control words of a packed decode trace layer (cowsdm_trace_t.control)
+CTRL_PROVEN = 0
+CTRL_CAPACITY = 1
+CTRL_ROOM = 2
+CTRL_QUANTUM = 3
+CTRL_NEED = 4
+CTRL_EVENTS = 5
+CTRL_ADDED = 6
+CTRL_COPIED = 7
+CTRL_FREE = 8
+CTRL_STEPS = 9
+CTRL_FIT = 10
+CTRL_WORDS = 12
+
+ABI_VERSION = 5
 
 SCRATCH_EPOCH = 0
 SCRATCH_ERRORS = 3
@@ -151,11 +168,11 @@ class Trace(ctypes.Structure):
         ("scan", ctypes.c_void_p),
         ("scan_words", ctypes.c_int64),
         ("persistent", ctypes.c_int32),
-        ("proof_steps", ctypes.c_int32),
+        ("scan_steps", ctypes.c_int32),
         ("steps_recorded", ctypes.c_int64),
-        ("proof_rows", ctypes.c_int64),
         ("status", ctypes.c_void_p),
-        ("free_out", ctypes.c_void_p),
+        ("control", ctypes.c_void_p),
+        ("control_stride", ctypes.c_int64),
     ]
 
 
@@ -169,7 +186,9 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_last_error_string": (ctypes.c_char_p, []),
     "cowsdm_step_scratch_words": (_I64, [_I64]),
     "cowsdm_workspace_bytes": (_I64, [_I64, _I64]),
-    "cowsdm_trace_scan_words": (_I64, [_I64, _I32]),
+    "cowsdm_trace_scan_words": (_I64, [_I64, _I64, _I32]),
+    "cowsdm_trace_persistent": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32]),
     "cowsdm_trace_timing": (_I32, [_I32]),
     "cowsdm_trace_timing_read": (_I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I32)]),
     "cowsdm_packed_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
@@ -238,7 +257,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = restype
                 fn.argtypes = argtypes
-            if handle.cowsdm_abi_version() != 4:
+            if handle.cowsdm_abi_version() != ABI_VERSION:
                 raise RuntimeError("libcowsdm.so ABI version mismatch")
             _lib = handle
     return _lib

@@ -348,6 +348,32 @@ class PackedSDMCopyOnWriteState:
         return added
 
     @torch.no_grad()
+    def reserve_rows(self, rows: int) -> None:
+        """Make ``values`` and ``free_rows`` lead buffers of at least
+        ``rows`` rows, so that growth up to that capacity (on the host or
+        inside a decode trace) moves no rows.  Capacity, logical state and
+        growth counters are unchanged.  No counterpart in the reference."""
+
+        rows = int(rows)
+        if rows >= 2**31:
+            raise ValueError("SDM COW slab cannot grow past 2^31 rows")
+        buffers = self.slab_buffers
+        if (buffers is not None and buffers[0].data_ptr() == self.values.data_ptr()
+                and buffers[1].data_ptr() == self.free_rows.data_ptr()
+                and min(buffers[0].shape[0], buffers[1].shape[0]) >= rows):
+            return
+        if rows <= self.capacity_rows and buffers is None:
+            return
+        capacity = self.capacity_rows
+        rows = max(rows, capacity)
+        vbuf = torch.empty(rows, self.width, device=self.values.device, dtype=self.values.dtype)
+        fbuf = torch.empty(rows, device=self.values.device, dtype=self.free_rows.dtype)
+        vbuf[:capacity].copy_(self.values)
+        fbuf[:capacity].copy_(self.free_rows)
+        self.slab_buffers = (vbuf, fbuf)
+        self.values, self.free_rows = vbuf[:capacity], fbuf[:capacity]
+
+    @torch.no_grad()
     def prepare_step_capacity(self, maximum_new_rows: int) -> int:
         """Prove one fused decode step, growing pooled headroom if short
         (allocator.py:745-773).  Host bookkeeping; reads free_count only
@@ -1146,25 +1172,38 @@ def mark_written(active: torch.Tensor, indices: torch.Tensor) -> None:
 
 class DecodeTrace:
     """Routes of many decode steps for several independent layers, resident
-    on the device.
+    on the device, and the decode loop that runs them.
 
     Inputs are stacked [S, L, B, ...] (``values`` [S, L, B, D], gates
-    [S, L, B]).  Every step does for each layer what ``packed_sdm_cow_step``
-    does, except that persistent launches give first touches their physical
-    rows in the order of an atomic claim per (step, bank), as the reference's
-    proven kernel does (allocator.py:120-135): the same logical rows become
-    private, with the same values, the same set of physical rows and an
-    identical free stack.  ``launch(k, start=s)`` runs steps s..s+k-1 of every layer;
-    ``launch(k)`` without ``start`` runs k steps of each layer from its device
-    counter (``step_index[l]``), which the kernels advance, so a captured
-    hipGraph of ``launch(k)`` replays k consecutive steps per replay without
-    host work.  ``run(n)`` is the decode loop: n steps with the capacity of
-    packed layers proven on the device every few steps, growing a layer
-    exactly when ``prepare_step_capacity`` would.  ``outputs`` is
-    [S, L, B, D] (one reading per step) or [L, B, D] (every step overwrites
-    the same buffer).  ``memories`` given instead of ``states`` runs the
-    dense-table control.  Persistent launches run up to 512 steps per kernel.
-    No counterpart in the reference.
+    [S, L, B]).  ``run(n)`` is the reference's decode loop for the next n
+    steps of every layer (inference.py:538-566): before each step of a
+    packed layer with a growth quantum, ``prepare_step_capacity(banks * W)``
+    (allocator.py:745-773), then ``packed_sdm_cow_step``.  Readings, maps,
+    slab rows, free stacks, capacities and growth counters equal that loop's
+    bit for bit.
+
+    When the shape allows it (W <= 4, R <= 16, D <= 256, banks <= 256 for
+    packed state), the loop runs as persistent launches of up to
+    ``max_steps_per_launch`` steps.  Each packed launch is planned on the
+    device first: the capacity proof of every step, slab growth within the
+    slab's buffers (``slab_buffers``) and the row of every first touch are
+    decided before the steps run, from the control words (``control``: the
+    proof counter, capacity, buffer rows, quantum, growth counters) that
+    ``run`` uploads from the states and reads back, with the step counters,
+    in one transfer.  A layer whose growth would pass its buffers stops
+    there; the host then grows it exactly as ``prepare_step_capacity`` does
+    and decoding goes on.  Otherwise each step is one launch after a host
+    proof.
+
+    ``launch(k)`` enqueues k steps of every layer from its device counter
+    (``step_index[l]``), which the kernels advance, so a captured hipGraph of
+    ``launch(k)`` replays k consecutive steps per replay without host work;
+    for packed state call ``upload()`` before the first launch and ``sync()``
+    after the last (and give the slabs room with ``reserve_steps``).
+    ``outputs`` is [S, L, B, D] (one reading per step) or [L, B, D] (every
+    step overwrites the same buffer).  ``memories`` given instead of
+    ``states`` runs the dense-table control.  No counterpart in the
+    reference.
     """
 
     _INPUTS = ("write_indices", "write_weights", "values", "input_gate", "erase_gate",
@@ -1203,21 +1242,21 @@ class DecodeTrace:
         self.steps = steps
         self.device = device
         # one int64 report read back per round: row 0 the per-layer step
-        # counters, row 1 the int32 status words, row 2 the free counts the
-        # launches leave (packed state)
-        self._report = torch.zeros(3, layers, dtype=torch.int64, device=device)
+        # counters, row 1 the int32 status words, rows 2.. the control words
+        # of packed layers (word k of layer l at row 2 + k)
+        self._report = torch.zeros(2 + nat.CTRL_WORDS, layers, dtype=torch.int64, device=device)
         self.step_index = self._report[0]
-        self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.status = self._report[1].view(torch.int32)[:layers]
-        # the kernels only set status bits: run() clears them when a launch
-        # may have left some (a refusal, a direct launch)
-        self._status_clean = True
+        self.control = self._report[2:]
+        self._upload_buf = (torch.zeros(nat.CTRL_WORDS, layers, dtype=torch.int64).pin_memory()
+                            if not self.dense else None)
+        self._uploaded = None   # event after the last upload's copy
+        self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.ticket = self.ticket.data_ptr()
         self.trace.status = self.status.data_ptr()
-        self.trace.free_out = None if self.dense else self._report[2].data_ptr()
         for k, name in enumerate(self._INPUTS):
             tensor = self.inputs[name]
             self.trace.stride_bytes[k] = tensor.stride(0) * tensor.element_size()
@@ -1227,17 +1266,24 @@ class DecodeTrace:
                             write_indices.shape[3], read_indices.shape[3],
                             1 if self.dense else first.shared_initial_memory.shape[0],
                             _index_code(write_indices, read_indices))
-        # persistent launches run up to max_steps_per_launch steps in one kernel
         self.persistent = persistent
-        self.max_steps_per_launch = max(1, int(max_steps_per_launch))
-        words = int(nat.lib().cowsdm_trace_scan_words(banks, self.max_steps_per_launch))
-        self.scan = (torch.zeros(layers, words, dtype=torch.int64, device=device)
-                     if persistent and not self.dense else None)
-        self.trace.scan = None if self.scan is None else self.scan.data_ptr()
-        self.trace.scan_words = words
+        self.max_steps_per_launch = max(1, min(512, int(max_steps_per_launch)))
+        self.trace.persistent = int(persistent)
         self.trace.steps_recorded = steps
+        self.scan = None
+        self.planned = False
+        if not self.dense and persistent:
+            words = int(nat.lib().cowsdm_trace_scan_words(banks, self.writes,
+                                                          self.max_steps_per_launch))
+            self.scan = torch.zeros(layers, max(words, 1), dtype=torch.int64, device=device)
+            self.trace.scan = self.scan.data_ptr()
+            self.trace.scan_words = self.scan.shape[1]
+            self.trace.scan_steps = self.max_steps_per_launch
+            self.trace.control_stride = layers
         self._layers = None
         self._positions = [0] * layers   # host copy of step_index, None when unknown
+
+    # ------------------------------------------------------------ set-up
 
     def set_step(self, step: int) -> None:
         """Make the next device-counted launch run step ``step`` of every layer."""
@@ -1249,15 +1295,15 @@ class DecodeTrace:
 
     def layer_array(self):
         """The per-layer C structs for the current state pointers (they
-        change when a slab is reallocated or trimmed); rebuilt only when a
-        pointer moved, patched when only capacities changed (a slab grown
-        within its headroom)."""
+        change when a slab moves to larger buffers or is trimmed); rebuilt
+        only when a pointer moved."""
 
         key = tuple((t.data_ptr(),) if self.dense else
                     (t.values.data_ptr(), t.free_rows.data_ptr(), t.free_count.data_ptr(),
                      t.overflow_flag.data_ptr(), t.logical_to_physical.data_ptr(),
                      t.template_indices.data_ptr(), t.shared_initial_memory.data_ptr(),
-                     t.scratch.data_ptr()) for t in self.tables)
+                     t.scratch.data_ptr() if t.scratch is not None else 0)
+                    for t in self.tables)
         capacities = tuple(0 if self.dense else t.capacity_rows for t in self.tables)
         if self._layers is not None and self._layers[0] == key:
             layers = self._layers[1]
@@ -1277,34 +1323,139 @@ class DecodeTrace:
                 x["erase_gate"], x["forget_log_gate"], x["read_indices"], x["read_weights"],
                 out, None, None, None)
         self._layers = (key, layers, capacities)
+        if not self.dense:
+            # planned persistent launches need the shape, the pointers'
+            # alignment and the strides to allow a persistent kernel
+            self.planned = self.persistent and bool(nat.lib().cowsdm_trace_persistent(
+                layers, count, self.shape, self.trace, 0))
+            self.trace.control = self.control.data_ptr() if self.planned else None
         return layers
 
-    def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
-        """Enqueue ``steps`` consecutive steps on the current stream: steps
-        start..start+steps-1, or, without ``start``, the next ``steps`` steps
-        of each layer's device counter."""
+    @staticmethod
+    def _room(state: PackedSDMCopyOnWriteState) -> int:
+        """Rows the slab can grow to without moving: its buffers' rows when
+        values and free_rows lead them, else its capacity."""
 
+        buffers = state.slab_buffers
+        if (buffers is not None and buffers[0].data_ptr() == state.values.data_ptr()
+                and buffers[1].data_ptr() == state.free_rows.data_ptr()):
+            return min(buffers[0].shape[0], buffers[1].shape[0])
+        return state.capacity_rows
+
+    def need(self) -> int:
+        """Rows the decode loop proves before each step: banks * W
+        (inference.py:551-552)."""
+
+        return self.banks * self.writes
+
+    def upload(self) -> None:
+        """Write the packed layers' control words from their states: the
+        proof counter, capacity, buffer rows, quantum and rows proven per step
+        (zero for a layer without a growth quantum, whose decode makes no
+        proof), with the growth counters zeroed."""
+
+        if self.dense:
+            return
+        buf = self._upload_buf
+        if self._uploaded is not None:
+            self._uploaded.synchronize()   # the last upload has left the pinned buffer
+        buf.zero_()
+        for l, st in enumerate(self.tables):
+            q = st.growth_quantum_rows
+            buf[nat.CTRL_PROVEN, l] = st.proven_maximum_additional_allocations
+            buf[nat.CTRL_CAPACITY, l] = st.capacity_rows
+            buf[nat.CTRL_ROOM, l] = self._room(st)
+            buf[nat.CTRL_QUANTUM, l] = q
+            buf[nat.CTRL_NEED, l] = self.need() if q > 0 else 0
+        self.control.copy_(buf, non_blocking=True)
+        if self._uploaded is None:
+            self._uploaded = torch.cuda.Event()
+        self._uploaded.record()
+
+    def _absorb(self, control_rows) -> None:
+        """Take a launch's control words (host lists, row k = word k of each
+        layer) into the states: proof counter, capacity (grown within the
+        buffers) and growth counters."""
+
+        for l, st in enumerate(self.tables):
+            st.proven_maximum_additional_allocations = int(control_rows[nat.CTRL_PROVEN][l])
+            capacity = int(control_rows[nat.CTRL_CAPACITY][l])
+            if capacity != st.capacity_rows:
+                vbuf, fbuf = st.slab_buffers
+                st.values, st.free_rows = vbuf[:capacity], fbuf[:capacity]
+            st.growth_events += int(control_rows[nat.CTRL_EVENTS][l])
+            st.growth_rows_added += int(control_rows[nat.CTRL_ADDED][l])
+            st.growth_rows_copied += int(control_rows[nat.CTRL_COPIED][l])
+            if st.growth_quantum_rows > 0:
+                st.capacity_is_proven = True
+
+    def sync(self) -> None:
+        """Read the control words back into the states after ``launch``
+        calls (one synchronisation), and zero the growth counters the next
+        launches add to."""
+
+        if self.dense or not self.planned:
+            return
+        control = self.control.tolist()
+        self._absorb(control)
+        self.control[nat.CTRL_EVENTS:nat.CTRL_COPIED + 1].zero_()
+        self._positions = None
+
+    def reserve_steps(self, steps: int) -> None:
+        """Give every packed slab buffers with room for ``steps`` more steps
+        of first touches and the rounding of one growth, so that launches of
+        that many steps grow on the device and never stop for the host.  No
+        counterpart in the reference."""
+
+        if self.dense:
+            return
+        need = self.need()
+        for st in self.tables:
+            q = st.growth_quantum_rows
+            if q <= 0:
+                continue   # a slab without a quantum never grows
+            # a proof grows the slab to at most one step's need (rounded to
+            # the quantum) past its live rows, and live rows never pass B * N
+            want = min(st.capacity_rows + steps * need + q,
+                       _ceil_to(st.banks * st.slots + need + q, q))
+            st.reserve_rows(max(want, st.capacity_rows))
+        self._layers = None
+
+    # ---------------------------------------------------------- launches
+
+    def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
+        """Run ``steps`` consecutive steps of every layer: steps
+        start..start+steps-1 (packed state: the decode loop ``run``), or,
+        without ``start``, enqueue the next ``steps`` steps of each layer's
+        device counter on the current stream."""
+
+        if start is not None:
+            if start < 0 or start + steps > self.steps:
+                raise ValueError("trace launch runs past the recorded steps")
+            if not self.dense:
+                self.set_step(start)
+                self.run(steps)
+                return
+            layers = self.layer_array() if layers is None else layers
+            stream = nat.stream_handle(self.device)
+            self.trace.step_index = None
+            try:
+                done = 0
+                while done < steps:
+                    n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
+                    self.trace.first_step = start + done
+                    self._call(layers, n, stream)
+                    done += n
+            finally:
+                self.trace.step_index = self.step_index.data_ptr()
+                self.trace.first_step = 0
+            return
         layers = self.layer_array() if layers is None else layers
         stream = nat.stream_handle(self.device)
-        self.trace.persistent = int(self.persistent)
-        self._status_clean = False
-        if start is None:
-            self._positions = None
-            self.trace.step_index = self.step_index.data_ptr()
-            self.trace.first_step = 0
-            done = 0
-            while done < steps:
-                n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
-                self._call(layers, n, stream)
-                done += n
-            return
-        if start < 0 or start + steps > self.steps:
-            raise ValueError("trace launch runs past the recorded steps")
-        self.trace.step_index = None
+        self._positions = None
         done = 0
         while done < steps:
             n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
-            self.trace.first_step = start + done
             self._call(layers, n, stream)
             done += n
 
@@ -1313,57 +1464,53 @@ class DecodeTrace:
         nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
                   "decode trace launch")
 
-    def run(self, steps: int, *, proof_steps: int = 4, launch_steps: int = 512,
+    def _fault(self, layers_at_fault) -> None:
+        errors = [int(self.tables[l].ensure_scratch()[nat.SCRATCH_ERRORS].item())
+                  for l in layers_at_fault]
+        raise RuntimeError(
+            f"decode trace layers {layers_at_fault} stopped on a fault "
+            f"(error words {[hex(e) for e in errors]}): a bounded wait timed out or the "
+            "state is corrupt")
+
+    # -------------------------------------------------------- decode loop
+
+    def run(self, steps: int, *, launch_steps: int | None = None,
             timing: list | None = None) -> dict:
         """Decode the next ``steps`` steps of every layer from the device
-        counters (which must agree), ``launch_steps`` steps per launch.
-
-        Packed layers prove capacity on the device before every
-        ``proof_steps`` steps: the check prepare_step_capacity(banks * W *
-        proof_steps) makes in the reference's decode loop (inference.py:
-        551-552, allocator.py:745-773).  A layer whose free rows would not
-        cover the worst case stops before that step; once the launches have
-        drained, it is grown by prepare_step_capacity itself (the same read of
-        free_count, the same growth) and decoding resumes, so capacities and
-        growth counters match a host-proven loop exactly.  With ``timing``
-        given, a pair of timing events brackets every launch on the stream
-        and is appended to it.  Returns the number of launches and of growth
-        rounds."""
+        counters (which must agree): the reference's per-step loop,
+        ``prepare_step_capacity(banks * W)`` then the step, for every packed
+        layer with a growth quantum.  Persistent launches run
+        ``launch_steps`` (default ``max_steps_per_launch``) steps each.
+        With ``timing`` given, a pair of timing events brackets every launch
+        on the stream and is appended to it.  Returns the number of launches
+        and of host growth rounds."""
 
         if steps <= 0:
             return {"launches": 0, "growth_rounds": 0}
         positions = self._positions if self._positions is not None else self.step_index.tolist()
         if len(set(positions)) != 1:
             raise ValueError("decode trace layers stand at different steps")
-        target = positions[0] + steps
+        start = positions[0]
+        target = start + steps
         if target > self.steps:
             raise ValueError("trace run passes the recorded steps")
-        packed = not self.dense
-        need = 0
-        if packed:
-            if proof_steps <= 0 or proof_steps % 2:
-                raise ValueError("proof_steps must be positive and even")
-            if steps % proof_steps:
-                raise ValueError("steps must be a multiple of proof_steps")
-            need = self.banks * self.writes * proof_steps
-            launch_steps = max(proof_steps, launch_steps // proof_steps * proof_steps)
+        launch_steps = self.max_steps_per_launch if launch_steps is None else launch_steps
         launch_steps = max(1, min(int(launch_steps), self.max_steps_per_launch))
+        layers = self.layer_array()
+        if not self.dense and not self.planned:
+            return self._run_stepwise(start, steps, timing)
         saved = self.trace.steps_recorded
         self.trace.steps_recorded = target
-        self.trace.proof_rows = need
-        self.trace.proof_steps = proof_steps if packed else 0
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.first_step = 0
-        self.trace.persistent = int(self.persistent)
-        if not self._status_clean:
-            self.status.zero_()
-        self._status_clean = False
+        self.status.zero_()
+        self.upload()
         stream = nat.stream_handle(self.device)
         launches = rounds = 0
         remaining = steps
+        self._positions = None
         try:
             while True:
-                layers = self.layer_array()
                 for _ in range(-(-remaining // launch_steps)):
                     if timing is not None:
                         e0 = torch.cuda.Event(enable_timing=True)
@@ -1375,46 +1522,71 @@ class DecodeTrace:
                     else:
                         self._call(layers, launch_steps, stream)
                     launches += 1
-                report = self._report.tolist()    # counters, status, free counts
+                report = self._report.tolist()    # counters, status, control words
                 positions = report[0]
-                behind = [l for l, p in enumerate(positions) if p < target]
-                if not behind:
-                    # without growth rounds every layer ran from the same
-                    # step and none stopped short: no launch set a status bit
-                    self._status_clean = rounds == 0
-                    break
+                if not self.dense:
+                    self._absorb(report[2:])
                 words = report[1]   # int32 status word l is half l % 2 of word l // 2
                 status = [(words[l // 2] >> (32 * (l % 2))) & 0xFFFFFFFF
                           for l in range(len(self.tables))]
+                faults = [l for l, s in enumerate(status) if s & nat.TRACE_FAULT]
+                if faults:
+                    self._fault(faults)
+                behind = [l for l, p in enumerate(positions) if p < target]
+                if not behind:
+                    break
                 refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]
-                if refused != behind:
+                if self.dense or refused != behind:
                     raise RuntimeError(f"decode trace stopped short at steps {positions}")
-                # prepare_step_capacity on each refused layer, with the free
-                # counts its launches left (read back with the counters)
+                # The refused layers stand at a step whose proof reads
+                # free_count and grows the slab past its buffers: the
+                # reference's prepare_step_capacity at that step, on the
+                # host (new buffers with headroom), except that the step's own
+                # charge is left to the device, which proves it again.
                 grown = [self.tables[l] for l in refused]
-                for state in grown:
-                    state.proven_maximum_additional_allocations = 0
                 PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
-                    grown, need, free_counts=[report[2][l] for l in refused])
+                    grown, self.need(),
+                    free_counts=[report[2 + nat.CTRL_FREE][l] for l in refused])
+                for st in grown:
+                    st.proven_maximum_additional_allocations += self.need()
                 self.status.zero_()
+                self.upload()
+                layers = self.layer_array()
                 remaining = target - min(positions)
                 rounds += 1
         finally:
             self.trace.steps_recorded = saved
-            self.trace.proof_rows = 0
-            self.trace.proof_steps = 0
-            self._positions = None
         self._positions = [target] * len(self.tables)
-        if packed:
-            # the device spent the allowance: the next host proof re-reads
-            for state in self.tables:
-                state.proven_maximum_additional_allocations = 0
-        if rounds:
-            # growth moved slabs and the last round's launches may have marked
-            # layers already at the target: rebuild the launch structs and
-            # clear the status now, on this already slow path, rather than at
-            # the start of the next run
-            self.layer_array()
-            self.status.zero_()
-            self._status_clean = True
         return {"launches": launches, "growth_rounds": rounds}
+
+    def _run_stepwise(self, start: int, steps: int, timing: list | None) -> dict:
+        """The decode loop one step at a time, for packed shapes without a
+        persistent kernel: per step ``prepare_step_capacity(banks * W)`` on
+        every layer with a growth quantum, then one fused launch of all
+        layers (``packed_sdm_cow_step_layers``, which checks the capacity of
+        unproven layers first and raises the reference's errors)."""
+
+        need = self.need()
+        x = self.inputs
+        outs = self.outputs
+        rounds = 0
+        for t in range(start, start + steps):
+            proven = [st for st in self.tables if st.growth_quantum_rows > 0]
+            events = sum(st.growth_events for st in proven)
+            PackedSDMCopyOnWriteState.prepare_step_capacity_layers(proven, need)
+            rounds += sum(st.growth_events for st in proven) - events
+            out = outs[t] if outs.ndim == 4 else outs
+            if timing is not None:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+            packed_sdm_cow_step_layers(
+                self.tables, x["write_indices"][t], x["write_weights"][t], x["values"][t],
+                x["input_gate"][t], x["forget_log_gate"][t], x["read_indices"][t],
+                x["read_weights"][t], erase_gate=x["erase_gate"][t], outputs=list(out))
+            if timing is not None:
+                e1.record()
+                timing.append((e0, e1))
+        self.step_index.fill_(start + steps)
+        self._positions = [start + steps] * len(self.tables)
+        return {"launches": steps, "growth_rounds": rounds}

@@ -26,18 +26,18 @@ constexpr int kPerThread = kTile / kTileThreads;
 constexpr int kTraceMaxWrites = 4;
 constexpr int kTraceMaxReads = 16;
 constexpr int kTraceMaxSteps = 512;         // steps per persistent launch
-constexpr int kTraceScanWindows = 4;        // up to 256 banks per layer
-constexpr int kTraceFreeWindow = 1024;      // top of the free stack staged in LDS
+constexpr int kTraceMaxBanks = 256;         // banks per packed layer of a persistent launch
 constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are staged in LDS
 constexpr int kTraceBanksPerBlock = 2;      // banks per persistent workgroup
 constexpr int kTraceThreads = 2 * kWave * kTraceBanksPerBlock;  // a control and a data wave per bank
 constexpr int kTraceRing = 16;              // steps handed from control to data wave in flight
-// packed layers of at most 64 banks: a fifth wave sums the capacity proofs
-constexpr int kTraceProofThreads = kTraceThreads + kWave;
-// claim counters of the runs of one launch (runs of at least 2 steps), at the
-// end of a layer's scan words
-constexpr int kTraceRunCounters = kTraceMaxSteps / 2 + 1;
-constexpr int64_t kClaimFailBase = int64_t{1} << 40;  // failed claim p recorded as base - p
+// Plan word of a (step, bank) in a packed decode trace's scan block: bits
+// 0-23 the first touches of the launch before it (step-major, bank-major
+// within a step), bits 24-27 its first-touch write lanes, bit 28 set from the
+// bank's first step with an invalid route on.
+constexpr uint32_t kPlanBaseMask = (1u << 24) - 1;
+constexpr int kPlanMaskShift = 24;
+constexpr int kPlanStopBit = 28;
 
 constexpr uint32_t kStatusEmpty = 0;
 constexpr uint32_t kStatusAggregate = 1;
@@ -60,13 +60,14 @@ struct StepParams {
   int64_t* trace_ticket;         // [1 + layer]: waves of a layer done with the launch
   int64_t trace_first;           // step of this launch when trace_step is null
   int64_t trace_len;             // steps the trace inputs hold
-  int64_t trace_proof_rows;      // device capacity proof per run of proof steps, or 0
   int32_t* trace_status;         // per-layer status bits, or null
-  int64_t* trace_free_out;       // per-layer free_count after a launch, or null
-  int32_t trace_proof_steps;
   int64_t trace_stride[9];
-  int64_t* scan;                 // persistent launches: per-layer scan words
+  int64_t* scan;                 // packed persistent launches: per-layer plan blocks
   int64_t scan_words;            // words per layer in `scan`
+  int64_t* control;              // packed persistent launches: COWSDM_CTRL_* words
+  int64_t control_stride;        // word k of layer l at control[k * stride + l]
+  int32_t plan_steps;            // steps per launch a plan block holds
+  int32_t count_table;           // count pass: LDS hash entries per bank (N > kTraceMapSlots)
   int32_t steps;                 // persistent launches: steps per launch
   int32_t nlayers;
   int32_t banks;
@@ -141,6 +142,33 @@ __device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
                                               uint64_t value) {
   return (static_cast<uint64_t>(epoch) << 32) |
          (static_cast<uint64_t>(status) << 30) | (value & kValueMask);
+}
+
+// A packed decode trace layer's plan block: plan words [banks][plan_steps]
+// (int32), then the rows the launch's first touches pop, in pop order.
+__device__ __forceinline__ int32_t* plan_words(const StepParams& P, int layer) {
+  return reinterpret_cast<int32_t*>(P.scan + static_cast<int64_t>(layer) * P.scan_words);
+}
+__device__ __forceinline__ int32_t* plan_pops(const StepParams& P, int layer) {
+  return plan_words(P, layer) + static_cast<int64_t>(P.banks) * P.plan_steps;
+}
+__device__ __forceinline__ int64_t& control_word(const StepParams& P, int layer, int k) {
+  return P.control[static_cast<int64_t>(k) * P.control_stride + layer];
+}
+
+// The steps a trace launch runs for a layer: its first step (from the
+// device counter when there is one) and how many, never past the recorded
+// steps.  Every thread reading it gets the same value: a counter changes only
+// after every wave of its layer is done with the launch.
+__device__ __forceinline__ void trace_span(const StepParams& P, int layer, int64_t& first,
+                                           int64_t& left) {
+  first = P.trace_first;
+  left = P.steps;
+  if (P.trace_step) {
+    first = P.trace_step[layer];
+    const int64_t recorded = P.trace_len - first;
+    left = first < 0 ? 0 : (recorded < left ? recorded : left);
+  }
 }
 
 

@@ -47,11 +47,11 @@ extern template void launch_step_w<int32_t, true>(const StepParams&, int, int, h
 extern template void launch_step_w<int64_t, false>(const StepParams&, int, int, hipStream_t);
 extern template void launch_step_w<int64_t, true>(const StepParams&, int, int, hipStream_t);
 template <typename IDX, bool DENSE>
-bool launch_trace(const StepParams& P, int vec, hipStream_t stream);
-extern template bool launch_trace<int32_t, false>(const StepParams&, int, hipStream_t);
-extern template bool launch_trace<int32_t, true>(const StepParams&, int, hipStream_t);
-extern template bool launch_trace<int64_t, false>(const StepParams&, int, hipStream_t);
-extern template bool launch_trace<int64_t, true>(const StepParams&, int, hipStream_t);
+int32_t launch_trace(const StepParams& P, int vec, hipStream_t stream);
+extern template int32_t launch_trace<int32_t, false>(const StepParams&, int, hipStream_t);
+extern template int32_t launch_trace<int32_t, true>(const StepParams&, int, hipStream_t);
+extern template int32_t launch_trace<int64_t, false>(const StepParams&, int, hipStream_t);
+extern template int32_t launch_trace<int64_t, true>(const StepParams&, int, hipStream_t);
 
 namespace {
 thread_local char g_error[512] = "";
@@ -691,6 +691,49 @@ int32_t check_layer(const cowsdm_layer_t& L, bool dense) {
   return 0;
 }
 
+// Float lanes per row access that the row width, the layers' pointers and a
+// trace's per-step strides allow: 4, 2 or 1.
+int row_vec(const cowsdm_layer_t* layers, int32_t nlayers, const cowsdm_shape_t* shape,
+            bool dense, const cowsdm_trace_t* trace) {
+  const int64_t D = shape->width;
+  int vec = (D % 4 == 0 && D >= 4 * kWave) ? 4 : (D % 2 == 0 ? 2 : 1);
+  // float2/float4 lanes need every row pointer aligned to the vector size
+  for (int32_t i = 0; i < nlayers; ++i) {
+    const cowsdm_layer_t& L = layers[i];
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(L.values) |
+                           reinterpret_cast<uintptr_t>(L.step_values) |
+                           reinterpret_cast<uintptr_t>(L.output) |
+                           (dense ? 0 : reinterpret_cast<uintptr_t>(L.shared_initial_memory));
+    while (vec > 1 && (bits % (4u * vec)) != 0) vec /= 2;
+  }
+  if (trace) {
+    // every step's value and output rows (the only vector accesses to trace
+    // inputs) must keep the vector alignment of step 0
+    for (int k : {2, 8}) {
+      while (vec > 1 && (trace->stride_bytes[k] % (4 * vec)) != 0) vec /= 2;
+    }
+  }
+  return vec;
+}
+
+// Float lanes of a persistent trace launch (a row of D <= 64 floats takes
+// one per lane, <= 128 two, <= 256 four), or 0 when the shape, the alignment
+// or the strides rule one out.
+int persistent_vec(int vec, const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                   int32_t nlayers, bool dense) {
+  const int64_t D = shape->width;
+  int tv = D <= kWave ? 1 : (D <= 2 * kWave ? 2 : (D <= 4 * kWave ? 4 : 0));
+  if (tv && D % tv != 0) tv = 0;
+  if (tv > vec) tv = 0;  // alignment of some pointer forbids it
+  for (int k = 0; k < 9; ++k) {
+    // the persistent kernel advances inputs by 32-bit strides
+    if (trace->stride_bytes[k] < 0 || trace->stride_bytes[k] >= (1ll << 32)) tv = 0;
+  }
+  if (shape->writes > kTraceMaxWrites || shape->reads > kTraceMaxReads || nlayers > kMaxLayers) tv = 0;
+  if (!dense && shape->banks > kTraceMaxBanks) tv = 0;
+  return tv;
+}
+
 int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
                  const cowsdm_shape_t* shape, bool dense, hipStream_t stream,
                  const cowsdm_trace_t* trace = nullptr, int32_t steps = 1) {
@@ -703,17 +746,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   if (!dense && (shape->templates <= 0 || shape->templates >= (1ll << 31))) {
     return fail(COWSDM_EARG, "templates must be positive");
   }
-  const int64_t D = shape->width;
-  int vec = (D % 4 == 0 && D >= 4 * kWave) ? 4 : (D % 2 == 0 ? 2 : 1);
-  // float2/float4 lanes need every row pointer aligned to the vector size
-  for (int32_t i = 0; i < nlayers; ++i) {
-    const cowsdm_layer_t& L = layers[i];
-    const uintptr_t bits = reinterpret_cast<uintptr_t>(L.values) |
-                           reinterpret_cast<uintptr_t>(L.step_values) |
-                           reinterpret_cast<uintptr_t>(L.output) |
-                           (dense ? 0 : reinterpret_cast<uintptr_t>(L.shared_initial_memory));
-    while (vec > 1 && (bits % (4u * vec)) != 0) vec /= 2;
-  }
+  int vec = row_vec(layers, nlayers, shape, dense, trace);
   if (trace) {
     if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
     if (trace->first_step < 0) return fail(COWSDM_EARG, "trace: negative first step");
@@ -729,55 +762,42 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     }
     for (int k = 0; k < 9; ++k) {
       if (trace->stride_bytes[k] % 4 != 0) return fail(COWSDM_EARG, "trace: stride not float aligned");
-      // every step's value and output rows (the only vector accesses to
-      // trace inputs) must keep the vector alignment of step 0
-      if (k == 2 || k == 8) {
-        while (vec > 1 && (trace->stride_bytes[k] % (4 * vec)) != 0) vec /= 2;
-      }
     }
   }
   if (steps < 0) return fail(COWSDM_EARG, "steps must be non-negative");
-  // persistent multi-step launch: one launch for all steps
-  const int64_t Dw = shape->width;
-  int trace_vec = Dw <= kWave ? 1 : (Dw <= 2 * kWave ? 2 : (Dw <= 4 * kWave ? 4 : 0));
-  if (trace_vec && Dw % trace_vec != 0) trace_vec = 0;
-  if (trace_vec > vec) trace_vec = 0;  // alignment of some pointer forbids it
-  const int64_t blocks_per_layer_p = (shape->banks + kBanksPerBlock - 1) / kBanksPerBlock;
-  const int64_t chunk = steps < kTraceMaxSteps ? steps : kTraceMaxSteps;
-  bool strides_fit = true;  // the persistent kernel advances inputs by 32-bit strides
-  for (int k = 0; k < 9 && trace; ++k) {
-    if (trace->stride_bytes[k] < 0 || trace->stride_bytes[k] >= (1ll << 32)) strides_fit = false;
+  // persistent multi-step launches: up to scan_steps steps per launch
+  const int trace_vec = trace ? persistent_vec(vec, shape, trace, nlayers, dense) : 0;
+  // packed persistent launches are planned: they need the control words and
+  // scan blocks of enough steps
+  const bool planned = !dense && trace && trace->control;
+  int32_t launch_steps = kTraceMaxSteps;
+  if (planned) {
+    if (trace->scan_steps <= 0 || trace->scan_steps > kTraceMaxSteps || !trace->scan ||
+        trace->control_stride < nlayers ||
+        trace->scan_words < cowsdm_trace_scan_words(shape->banks, shape->writes, trace->scan_steps)) {
+      return fail(COWSDM_EARG, "trace: control words need scan blocks of scan_steps steps");
+    }
+    if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
+    launch_steps = trace->scan_steps;
   }
-  const bool persistent = strides_fit &&
-      trace && trace->persistent && steps > 0 && trace_vec &&
-      shape->writes <= kTraceMaxWrites && shape->reads <= kTraceMaxReads &&
-      nlayers <= kMaxLayers &&
-      (dense || (shape->banks <= kTraceScanWindows * kWave && trace->scan && trace->ticket &&
-                 trace->scan_words >= COWSDM_SCRATCH_SLOTS + chunk * shape->banks +
-                                          kTraceRunCounters));
-  (void)blocks_per_layer_p;
+  const bool persistent = trace && trace->persistent && steps > 0 && trace_vec &&
+                          (dense || planned);
+  if (planned && !persistent && steps > 0) {
+    return fail(COWSDM_ELIMIT, "trace: planned launches need a persistent launch "
+                               "(W <= 4, R <= 16, D <= 256 in even lanes, banks <= 256)");
+  }
   StepParams P;
   P.trace_step = trace ? trace->step_index : nullptr;
   P.trace_ticket = trace ? trace->ticket : nullptr;
   P.trace_first = trace ? trace->first_step : 0;
   P.trace_len = trace ? trace->steps_recorded : 0;
-  P.trace_proof_rows = trace ? trace->proof_rows : 0;
-  P.trace_proof_steps = trace ? trace->proof_steps : 0;
   P.trace_status = trace ? trace->status : nullptr;
-  P.trace_free_out = trace ? trace->free_out : nullptr;
-  if (P.trace_proof_rows > 0) {
-    if (dense) return fail(COWSDM_EARG, "trace: capacity proofs apply to packed state");
-    if (!trace->step_index) return fail(COWSDM_EARG, "trace: capacity proofs need device counters");
-    if (P.trace_proof_steps <= 0 || P.trace_proof_steps % 2 != 0) {
-      return fail(COWSDM_EARG, "trace: proof_steps must be positive and even");
-    }
-    if (!persistent) {
-      return fail(COWSDM_ELIMIT, "trace: capacity proofs need a persistent launch "
-                                 "(W <= 4, R <= 16, D <= 256, banks <= 256)");
-    }
-  }
-  P.scan = trace ? trace->scan : nullptr;
-  P.scan_words = trace ? trace->scan_words : 0;
+  P.scan = planned ? trace->scan : nullptr;
+  P.scan_words = planned ? trace->scan_words : 0;
+  P.control = planned ? trace->control : nullptr;
+  P.control_stride = planned ? trace->control_stride : 0;
+  P.plan_steps = planned ? trace->scan_steps : 0;
+  P.count_table = 0;
   P.steps = steps;
   for (int k = 0; k < 9; ++k) P.trace_stride[k] = trace ? trace->stride_bytes[k] : 0;
   P.banks = static_cast<int32_t>(shape->banks);
@@ -794,31 +814,31 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     const int blocks = P.blocks_per_layer * n;
     const bool i64 = shape->index_dtype == COWSDM_INDEX_INT64;
     if (persistent) {
-      // launches of at most kTraceMaxSteps steps each, in order
-      bool launched = true;
-      for (int32_t done = 0; done < steps && launched; done += kTraceMaxSteps) {
-        P.steps = (steps - done) < kTraceMaxSteps ? (steps - done) : kTraceMaxSteps;
+      // launches of at most launch_steps steps each, in order
+      int32_t rc = 0;
+      for (int32_t done = 0; done < steps; done += launch_steps) {
+        P.steps = (steps - done) < launch_steps ? (steps - done) : launch_steps;
         P.trace_first = trace->first_step + done;  // ignored when step_index is set
+        // count pass: an LDS hash of at least twice the launch's write routes
+        int table = 64;
+        while (table < 2 * P.steps * P.writes) table *= 2;
+        P.count_table = table;
         if (dense) {
-          launched = i64 ? launch_trace<int64_t, true>(P, trace_vec, stream)
-                         : launch_trace<int32_t, true>(P, trace_vec, stream);
+          rc = i64 ? launch_trace<int64_t, true>(P, trace_vec, stream)
+                   : launch_trace<int32_t, true>(P, trace_vec, stream);
         } else {
-          launched = i64 ? launch_trace<int64_t, false>(P, trace_vec, stream)
-                         : launch_trace<int32_t, false>(P, trace_vec, stream);
+          rc = i64 ? launch_trace<int64_t, false>(P, trace_vec, stream)
+                   : launch_trace<int32_t, false>(P, trace_vec, stream);
         }
-        if (!launched && done > 0) {
-          return fail(COWSDM_ELIMIT, "trace launch stopped after %d steps", done);
+        if (rc == 1 && (done > 0 || planned)) {
+          return fail(COWSDM_ELIMIT, "trace: not even one layer's workgroups fit on the device "
+                                     "at once (after %d steps)", done);
         }
-        if (launched) {
-          if (int32_t e = launch_status(dense ? "dense trace" : "packed trace")) return e;
-        }
+        if (rc == 1) break;
+        if (rc != 0) return rc;
+        if (int32_t e = launch_status(dense ? "dense trace" : "packed trace")) return e;
       }
-      if (launched) continue;
-      if (P.trace_proof_rows > 0) {
-        // one launch per step would skip the proofs the caller asked for
-        return fail(COWSDM_ELIMIT, "trace: capacity proofs need a persistent launch, and not "
-                                   "even one layer's workgroups fit on the device at once");
-      }
+      if (rc == 0) continue;
       P.steps = steps;
       P.trace_first = trace->first_step;
     }
@@ -876,9 +896,20 @@ int64_t cowsdm_step_scratch_words(int64_t banks) {
   return banks < 0 ? -1 : COWSDM_SCRATCH_SLOTS + banks;
 }
 
-int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps) {
-  if (banks < 0 || steps < 0) return -1;
-  return COWSDM_SCRATCH_SLOTS + banks * steps + kTraceRunCounters;
+int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
+                                const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                                int32_t dense) {
+  if (!layers || !shape || !trace || nlayers <= 0) return 0;
+  if (check_shape(shape) != 0) return 0;
+  const int vec = row_vec(layers, nlayers, shape, dense != 0, trace);
+  return persistent_vec(vec, shape, trace, nlayers, dense != 0) > 0 ? 1 : 0;
+}
+
+int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
+  if (banks < 0 || writes < 0 || steps < 0) return -1;
+  // plan words [banks][steps] and the launch's pops (at most banks * W per
+  // step), int32 each
+  return (banks * steps * (1 + writes) + 1) / 2;
 }
 
 int32_t cowsdm_trace_timing(int32_t enable) {

@@ -5,4 +5,4 @@
 
 template void cowsdm_impl::launch_step_w<int32_t, false>(const cowsdm_impl::StepParams&, int,
                                                          int, hipStream_t);
-template bool cowsdm_impl::launch_trace<int32_t, false>(const cowsdm_impl::StepParams&, int, hipStream_t);
+template int32_t cowsdm_impl::launch_trace<int32_t, false>(const cowsdm_impl::StepParams&, int, hipStream_t);

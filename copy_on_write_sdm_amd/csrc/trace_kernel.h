@@ -1,18 +1,17 @@
 // Persistent multi-step form of the copy-on-write SDM step: one launch runs
-// G <= 256 consecutive decode steps of device-resident routes for every (layer,
-// bank), with the results of G single-step launches (physical rows of first
-// touches may be assigned in another order, as in the reference's proven
-// kernel, whose banks pop with an atomic add).
+// G <= 512 consecutive decode steps of device-resident routes for every
+// (layer, bank), with the results of G single-step launches.
 //
 // Each (layer, bank) has two waves in one workgroup, which hand steps over
 // through a ring of kTraceRing slots in LDS:
 //
 //   the control wave loads the step's slots and map entries, classifies the
 //   step (first touches, slots written by the step before, read-after-write),
-//   claims rows for its first touches, and publishes the addresses of the
-//   rows the step loads, two steps ahead of the data wave's loads; two steps
-//   later it takes the claimed rows, stores them in the map and publishes
-//   the rows the step's updates are stored to and the step's masks;
+//   fetches the rows its first touches pop from the launch's plan, and
+//   publishes the addresses of the rows the step loads, two steps ahead of
+//   the data wave's loads; two steps later it takes the popped rows, stores
+//   them in the map and publishes the rows the step's updates are stored to
+//   and the step's masks;
 //
 //   the data wave loads the rows of step s+1 from the published addresses
 //   while it computes step s (gated-delta update, sparse read) from rows
@@ -22,35 +21,29 @@
 // Only the data wave reads or writes rows, in program order: a step's rows
 // were stored by earlier steps of the same wave, except the rows of the step
 // just before, which it takes from LDS.  The control wave runs up to
-// kTraceRing - 3 steps ahead, so the atomics and map lookups it waits on stay
-// off the data wave's path.  It classifies step t after resolving step t-2,
-// but before step t-1 has its rows: slots written at t-1 take their rows from
-// that step's result.  When a bank's map fits (N <= kTraceMapSlots), the
-// control wave keeps it in LDS for the launch (it is the only writer of its
-// bank's entries) and the global map is written alongside; otherwise step
-// t's entries are loaded from the global map an iteration early, before
-// step t-2's pops, and slots written at t-2 take the rows popped for them.  Values in flight live in even/odd homes (both
-// loops are unrolled by two) and are only read one iteration after their
-// load was issued, so no register copy waits on memory.
+// kTraceRing - 3 steps ahead, so the map lookups and pop-list loads it waits
+// on stay off the data wave's path.  It classifies step t after resolving
+// step t-2, but before step t-1 has its rows: slots written at t-1 take their
+// rows from that step's result.  When a bank's map fits (N <=
+// kTraceMapSlots), the control wave keeps it in LDS for the launch (it is the
+// only writer of its bank's entries) and the global map is written
+// alongside; otherwise step t's entries are loaded from the global map an
+// iteration early, before step t-2's pops, and slots written at t-2 take the
+// rows popped for them.  Values in flight live in even/odd homes (both loops
+// are unrolled by two) and are only read one iteration after their load was
+// issued, so no register copy waits on memory.
 //
-// Rows: free_count stays F (its value at launch) until the launch ends.  A
-// (step, bank) with c first touches adds c to the layer's claim counter and
-// gets p, the rows claimed before it; its first touches take
-// free_rows[F - 1 - p - rank], and the step fits if p + c <= F.  Claims only
-// grow, so once one fails every later one fails too, and the claims that fit
-// are exactly the top of the free stack.  The layer's last control wave to
-// finish writes free_count = F - (claims that fit) and clears the counter.
-// Banks do not otherwise wait on one another, except for the capacity proof:
-// with proofs on, each bank publishes its first touches so far at the end of
-// each run of proof steps, and before a run starts every control wave takes
-// their sum, so all banks of the layer stop at the same step.  With the map
-// in LDS a bank counts first touches from its write slots a 64-step chunk
-// ahead, so the counts are out long before a proof needs them; in layers of
-// at most 64 banks a fifth wave of each workgroup sums them and hands the
-// sum to the control waves through LDS.  Claims do not wait for proofs: each
-// run claims on a counter of its own, and the proof's sum is the run's base
-// (rows are claimed at base + p); a run that fails its proof never takes the
-// rows it claimed.
+// Rows (packed state): the count and plan passes (trace_plan.hip) ran before
+// the launch.  They fixed how many steps each layer runs (the decode loop's
+// capacity proof may stop a layer before a growth its slab buffers cannot
+// hold), the capacity the launch grows to, each (step, bank)'s first-touch
+// lanes and its offset in pop order (step-major, bank-major within a step,
+// as single steps pop), and the row of every pop; they also wrote the free
+// stack and free_count the launch leaves.  A (step, bank) with c first
+// touches at offset e takes pops e .. e+c-1 if e + c fits the rows the plan
+// could give out (the launch's FIT word; every step fits unless a capacity
+// proof was missing or dishonest), else it overflows and the bank stops for
+// the rest of the launch.  Banks never wait on one another.
 #pragma once
 
 #include <hip/hip_ext.h>
@@ -83,6 +76,7 @@ struct TraceIdx {                   // lane j: write slot j / read slot j
 
 struct TraceRoute {                 // a classified step
   int widx, ridx;
+  int base;       // wave-uniform (packed): first touches before it in pop order
   int wrow;       // write lane: physical row (-1: M0, or a first touch not yet popped)
   int wsrc;       // write lane: written by step t-1 lane j (j), else -1
   int rsrc;       // read lane: the same
@@ -203,13 +197,12 @@ __device__ __forceinline__ int plane_code(uint32_t w, int lo, int hi) {
 // Every step handles kTraceMaxWrites write rows and kTraceMaxReads read rows
 // without a branch on W or R; FULL (W and R at those maxima) drops the
 // selects and the zero rows that leave the others out.
-// SCANW: 64-bank windows of the count scan (1: at most 64 banks per layer).
+// FEW: at most 64 banks per layer (the compiler may then give a wave every
+// register; a grid of more banks needs two workgroups per CU).
 // MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per bank).
-// A packed kernel with SCANW 1 runs a fifth wave per workgroup that sums the
-// capacity proofs (kTraceProofThreads threads); the others run kTraceThreads.
-template <typename IDX, int VEC, bool DENSE, bool FULL, int SCANW, bool MAPLDS>
-__global__ __launch_bounds__(!DENSE && SCANW == 1 ? kTraceProofThreads : kTraceThreads)
-__attribute__((amdgpu_waves_per_eu(1, SCANW == 1 ? 1 : 2)))
+template <typename IDX, int VEC, bool DENSE, bool FULL, bool FEW, bool MAPLDS>
+__global__ __launch_bounds__(kTraceThreads)
+__attribute__((amdgpu_waves_per_eu(1, FEW ? 1 : 2)))
 void sdm_trace_kernel(StepParams P) {
   constexpr int kRow = kWave * VEC;  // floats of one LDS row
   constexpr int NB = kTraceBanksPerBlock;
@@ -219,7 +212,6 @@ void sdm_trace_kernel(StepParams P) {
   // data wave: the next step's weights, written per lane at the end of an
   // iteration, read back as broadcasts by the step's compute
   __shared__ vf4_t lds_weights[NB][2][kWave / 4];
-  __shared__ int lds_free[DENSE ? 1 : kTraceFreeWindow];
   __shared__ TraceSlot lds_ring[NB][kTraceRing];
   // [0]: control -> data, (stop step << 16) | steps whose row addresses are
   // published (the masks and store rows of all but the last of them);
@@ -231,18 +223,14 @@ void sdm_trace_kernel(StepParams P) {
   constexpr int kIdxRow = kTraceMaxWrites + kTraceMaxReads;
   constexpr int kIdxLds = kIdxRow + 4;
   __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxLds];
-  // proof wave -> control waves: the layer's first touches before run r
-  // (-1: a bank's count never arrived), and the last run summed
-  constexpr bool PWAVE = !DENSE && SCANW == 1;
-  __shared__ int lds_proof[PWAVE ? kTraceRunCounters : 1];
-  __shared__ uint32_t lds_proof_done;
-  // map in LDS (dynamic, 2 banks x 2 x N ints): each bank's slot map, then
-  // each bank's first step of the launch writing each slot
+  // control wave (packed): the plan words of two 64-step chunks, staged from
+  // registers a chunk ahead
+  __shared__ int lds_plan[DENSE ? 1 : NB][2][kWave];
+  // map in LDS (dynamic, 2 banks x N ints): each bank's slot map
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
-  const bool proof_wave = wave == 2 * NB;
-  const int pair = proof_wave ? 0 : wave >> 1;
+  const int pair = wave >> 1;
   const bool data_wave = (wave & 1) != 0;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int layer_id = blockIdx.x / P.blocks_per_layer;
@@ -266,8 +254,8 @@ void sdm_trace_kernel(StepParams P) {
     // no recorded step left for this layer: touch no input, leave the counter
     if (threadIdx.x == 0 && blockIdx.x % P.blocks_per_layer == 0) {
       if (P.trace_status) {
-        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{2}, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_ENDED},
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else if (!DENSE) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                               static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
@@ -276,6 +264,14 @@ void sdm_trace_kernel(StepParams P) {
     }
     return;  // whole workgroup
   }
+  if constexpr (!DENSE) {
+    // the steps the plan lets the layer run (it stops a layer before a
+    // growth its slab buffers cannot hold)
+    const int64_t planned = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_STEPS))));
+    left = planned < left ? planned : left;
+    if (left <= 0) return;  // whole workgroup: the plan set the layer's status
+  }
 
   const int N = P.slots;
   const int D = P.width;
@@ -283,89 +279,21 @@ void sdm_trace_kernel(StepParams P) {
   const int R = FULL ? kTraceMaxReads : P.reads;
   const int B = P.banks;
   const int G = static_cast<int>(left);
-  const int C = pin(static_cast<int>(L.capacity_rows));  // rows are int32
+  // the capacity the launch grows to (rows are int32)
+  const int C = DENSE ? 0 : pin(__builtin_amdgcn_readfirstlane(
+                                static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_CAPACITY))));
   // lanes past the row width repeat the last columns: they load, compute and
   // store exactly what the last full lane does, so no access needs a lane mask
   const int col = lane * VEC < D ? lane * VEC : D - VEC;
   const uint32_t coff = static_cast<uint32_t>(col) * 4u;
   const uint32_t row_bytes = static_cast<uint32_t>(D) * 4u;
 
-  // ---- launch constants
   int base_err = 0;
-  int old_free = 0;
-  int window = 0;
-  if constexpr (!DENSE) {
-    old_free = __builtin_amdgcn_readfirstlane(*L.free_count);
-    if (old_free < 0 || old_free > C) {
-      base_err |= COWSDM_ERR_CORRUPT;
-    } else {
-      window = old_free < kTraceFreeWindow ? old_free : kTraceFreeWindow;
-    }
-    for (int k = static_cast<int>(threadIdx.x); k < window; k += static_cast<int>(blockDim.x)) {
-      lds_free[k] = L.free_rows[old_free - 1 - k];
-    }
-  }
-  if (lane == 0 && !data_wave && !proof_wave) {
+  if (lane == 0 && !data_wave) {
     lds_sync[pair][0] = kNoStop << 16;
     lds_sync[pair][1] = 0;
   }
-  if (threadIdx.x == 0) lds_proof_done = 0;
   __syncthreads();
-
-  // ======================= proof wave =======================
-  // Sums the counts every bank of the layer publishes at the end of each
-  // run (word r of bank b: its first touches in runs 0..r-1), run after run,
-  // on a vector memory counter of its own: a control wave that loaded and
-  // waited for them itself would, at its first wait after the load, also
-  // wait for every claim and store it issued since.  Stops after the first
-  // run whose proof fails, as the layer does.
-  if (proof_wave) {
-    if constexpr (PWAVE) {
-      const int64_t proof_rows = P.trace_proof_rows;
-      const int k = P.trace_proof_steps;
-      if (proof_rows > 0 && k > 0) {
-        const int64_t* const scan_l = P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
-        const uint32_t ep = static_cast<uint32_t>(scan_l[COWSDM_SCRATCH_EPOCH]);
-        const bool in = lane < B;
-        const int64_t* const word = scan_l + COWSDM_SCRATCH_SLOTS + (in ? lane : 0);
-        auto ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-          return static_cast<uint32_t>(w >> 32) == ep && ((w >> 30) & 3u) == kStatusAggregate;
-        };
-        const int runs = (G - 1) / k;  // proofs before steps k, 2k, ... < G
-        // Run r's words are loaded once the workgroup's first control wave
-        // has published steps up to kLead before the proof that needs them
-        // (with the map in LDS the counts went out at least 64 steps ahead
-        // of it; with the map in HBM three steps ahead, so the load polls a
-        // little).  Loading earlier would poll words not yet published, and
-        // every poll gathers one cache line per bank from L2 beside the data
-        // waves' row loads.  (A stopped control wave publishes 0xFFFF steps.)
-        constexpr int kLead = 12;
-        bool stop = false;
-        for (int r = 1; r <= runs && !stop; ++r) {
-          for (int spins = 0; spins < 4 * kSpinLimit; ++spins) {
-            const uint32_t published = sync_load(&lds_sync[0][0]) & 0xFFFFu;
-            if (static_cast<int>(published) + kLead >= r * k) break;
-            __builtin_amdgcn_s_sleep(8);
-          }
-          uint64_t w = atomic_load_u64(word + static_cast<int64_t>(r) * B);
-          int spins = 0;
-          while (__ballot(in && !ready(w)) != 0 && spins < kSpinLimit) {
-            __builtin_amdgcn_s_sleep(1);
-            if (!ready(w)) w = atomic_load_u64(word + static_cast<int64_t>(r) * B);
-            ++spins;
-          }
-          const bool lost = __ballot(in && !ready(w)) != 0;
-          const int total = lost ? -1 : wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
-          if (lane == 0) {
-            lds_proof[r] = total;
-            sync_store(&lds_proof_done, static_cast<uint32_t>(r));
-          }
-          stop = lost || old_free - total < proof_rows;
-        }
-      }
-    }
-    return;
-  }
   if (bank >= B) return;  // both waves of the bank
 
   uint32_t* const sync = lds_sync[pair];
@@ -696,9 +624,9 @@ void sdm_trace_kernel(StepParams P) {
     // in flight (the back edge's), and the waits the compiler places there
     // stay as loose as the steady state allows.
     __builtin_amdgcn_s_waitcnt(0);
-    // Pairs of steps, then an odd last step; the control wave stops only
-    // before an even step (capacity proofs come in even runs) or the last,
-    // so the loop's only exit is at its head.
+    // Pairs of steps, then an odd last step; the control wave stops early
+    // only before an even step (when this wave stopped taking steps), so the
+    // loop's only exit is at its head.
     int s = 0;
     for (; go && s + 1 < G; s += 2) {
       if (!await(need(s + 1))) {
@@ -730,6 +658,10 @@ void sdm_trace_kernel(StepParams P) {
                               static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
       }
+      if (P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       sync_store(&sync[1], kNoStop);
     }
     return;
@@ -737,35 +669,50 @@ void sdm_trace_kernel(StepParams P) {
 
   // ======================= control wave =======================
   int64_t tmpl = 0;
-  uint32_t epoch = 0;
   if constexpr (!DENSE) {
     tmpl = L.template_indices[bank];
     if (tmpl < 0 || tmpl >= P.templates) {
       base_err |= COWSDM_ERR_TEMPLATE;
       tmpl = 0;
     }
-    epoch = static_cast<uint32_t>(
-        P.scan[static_cast<int64_t>(layer_id) * P.scan_words + COWSDM_SCRATCH_EPOCH]);
   }
   const float* const m0_bank =
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
   int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
-  uint32_t* const first_write =
-      MAPLDS ? reinterpret_cast<uint32_t*>(lds_map_all + (NB + pair) * N) : nullptr;
   bool any_bad = false;  // a map entry outside the slab (checked per chunk only then)
   if constexpr (MAPLDS) {
     uint64_t bad = 0;
     for (int b = 0; b < N; b += kWave) {
       const int v = b + lane < N ? map_bank[b + lane] : -1;
-      if (b + lane < N) {
-        lds_map[b + lane] = v;
-        first_write[b + lane] = ~0u;
-      }
+      if (b + lane < N) lds_map[b + lane] = v;
       bad |= __ballot(v >= C);
     }
     any_bad = bad != 0;
   }
+  // ---- plan words (packed): lane l holds step 64c + l's of chunk c, loaded a
+  // chunk ahead and staged into LDS when the chunk before starts being used
+  const int32_t* const plan_bank =
+      DENSE ? nullptr : plan_words(P, layer_id) + static_cast<int64_t>(bank) * P.plan_steps;
+  const int32_t* const pops = DENSE ? nullptr : plan_pops(P, layer_id);
+  const int fit_rows = DENSE ? 0 : pin(__builtin_amdgcn_readfirstlane(
+                                       static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_FIT))));
+  uint32_t plan_next = 0;
+  auto load_plan = [&](int c) __attribute__((always_inline)) {
+    if constexpr (!DENSE) {
+      const int t = c * kWave + lane;
+      plan_next = t < G ? static_cast<uint32_t>(plan_bank[t]) : 0u;
+    }
+  };
+  auto stage_plan = [&](int c) __attribute__((always_inline)) {
+    if constexpr (!DENSE) lds_plan[pair][c & 1][lane] = static_cast<int>(plan_next);
+  };
+  auto plan_of = [&](int t) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (DENSE) return 0u;
+    const int tc = t < G ? t : G - 1;
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(lds_plan[DENSE ? 0 : pair][(tc >> 6) & 1][tc & (kWave - 1)]));
+  };
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
   const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
@@ -817,7 +764,7 @@ void sdm_trace_kernel(StepParams P) {
   // path reads it):
   //   word 0: bits 0-19 rows from step t-1 (write lanes 0-3, read lanes
   //           4-19), 20-23 first touches (fm: lane l's first-touch mask from
-  //           the first-write pass), 24-31 the COWSDM_ERR_* bits of its routes
+  //           the launch's plan), 24-31 the COWSDM_ERR_* bits of its routes
   //   word 1: bits 0-15 reads of a slot step t writes, 16-19 and 20-23 the
   //           two bit planes of each write lane's source lane in step t-1
   //   words 2, 3: the planes of each read lane's source lane in step t-1 and
@@ -969,10 +916,13 @@ void sdm_trace_kernel(StepParams P) {
         wraw = wraw >= C ? -1 : wraw;
         rraw = rraw >= C ? -1 : rraw;
       }
-      const bool ok = ok_prev && e == 0;
+      // the plan stops the bank from its first step with an invalid route
+      const uint32_t pw = plan_of(t);
+      const bool ok = ok_prev && e == 0 && ((pw >> kPlanStopBit) & 1u) == 0;
       const uint32_t fwd = k0 & 0xFFFFFu;
       const uint32_t fm = DENSE || !ok ? 0u : (k0 >> 20) & 15u;
       rt.u = fm | (static_cast<uint32_t>(__popc(fm)) << 4) | (ok ? 1u << 8 : 0u);
+      rt.base = static_cast<int>(pw & kPlanBaseMask);
       rt.fwd = fwd;
       rt.rawm = k1 & 0xFFFFu;
       rt.rank = lanes_below(fm);
@@ -1037,11 +987,24 @@ void sdm_trace_kernel(StepParams P) {
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    const bool ok = ok_prev && !any_err;
-    const uint64_t fm = DENSE || !ok ? 0ull : __ballot(wsrc < 0 && wraw < 0) & wlanes;
+    const uint32_t pw = plan_of(t);
+    bool ok = ok_prev && !any_err && ((pw >> kPlanStopBit) & 1u) == 0;
+    uint64_t fm = DENSE || !ok ? 0ull : __ballot(wsrc < 0 && wraw < 0) & wlanes;
+    if (!DENSE && ok && static_cast<uint32_t>(fm) != ((pw >> kPlanMaskShift) & 15u)) {
+      // the plan counted other first touches: the state changed under the
+      // launch; stop the bank rather than pop rows meant for others
+      if (lane == 0 && t < G) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+      ok = false;
+      fm = 0;
+    }
     rt.u = __builtin_amdgcn_readfirstlane(
         static_cast<uint32_t>(fm & 15u) | (static_cast<uint32_t>(__popcll(fm)) << 4) |
         (ok ? 1u << 8 : 0u));
+    rt.base = static_cast<int>(pw & kPlanBaseMask);
     rt.fwd = __builtin_amdgcn_readfirstlane(
         static_cast<uint32_t>(__ballot(wsrc >= 0) & wlanes) |
         (static_cast<uint32_t>(__ballot(rsrc >= 0) & rlanes) << kTraceMaxWrites));
@@ -1139,60 +1102,37 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // ---- claims (packed)
-  int64_t* const scan = DENSE ? nullptr : P.scan + static_cast<int64_t>(layer_id) * P.scan_words;
-  int64_t* const claims = DENSE ? nullptr : scan + COWSDM_SCRATCH_CLAIMS;
-  bool alive = true;  // every claim so far fitted
+  // ---- pops (packed)
+  bool alive = true;  // every step of this bank so far got its rows
 
-  // Step t's first touches claim their rows: one atomic add per (step, bank)
-  // with first touches, its result read when the step resolves.
-  // The atomic is 32-bit, on the counter's low word: a launch claims at most
-  // W * B * G < 2^31 rows, so the high word stays zero and 64-bit reads of the
-  // counter hold the total.  (A 64-bit atomic would leave the returned high
-  // half unused; the compiler reuses that register, and writing a register a
-  // load or atomic in flight will write waits for every access in flight.)
-  int32_t* const claims32 = DENSE ? nullptr : reinterpret_cast<int32_t*>(claims);
-  // With capacity proofs, each run of proof steps claims on a counter of its
-  // own (the low word of one of the last kTraceRunCounters scan words, zero
-  // between launches): a step's claims then need not wait for its run's
-  // proof, which gives the run's base, the exact number of rows every bank
-  // claimed before it.  Rows are claimed at base + p; a run that fails its
-  // proof never takes the rows it claimed.
-  int64_t* const run_claims = DENSE ? nullptr : scan + P.scan_words - kTraceRunCounters;
-  int base_cur = 0;   // base of the run the last passed proof opened
-  auto claim = [&](const TraceRoute& rt, int& home, int run) __attribute__((always_inline)) {
+  // Step t's first touches take their rows from the plan's pop list: write
+  // lane j, of rank k among the step's first touches, loads pop base + k when
+  // the step is classified, and the row is used two iterations later, when
+  // the step resolves.  A step whose pops reach past the rows the plan could
+  // give out (a capacity proof that was missing or not honest) overflows: it
+  // takes none, and the bank stops.
+  auto claim = [&](const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (route_count(rt.u) > 0 && route_ok(rt.u)) {
-        if (lane == 0) {
-          int32_t* const ctr = P.trace_proof_rows > 0
-                                   ? reinterpret_cast<int32_t*>(run_claims + run) : claims32;
-          home = __hip_atomic_fetch_add(ctr, static_cast<int32_t>(route_count(rt.u)),
-                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+      const int count = route_count(rt.u);
+      if (count > 0 && route_ok(rt.u) && rt.base + count <= fit_rows) {
+        const bool first = lane < kTraceMaxWrites && ((route_fmask(rt.u) >> lane) & 1u);
+        if (first) home = pops[rt.base + rt.rank];
       }
     }
   };
 
-  // Step t's first touches, from the rows claimed for them (home: lane 0
-  // holds p, the rows claimed before it on its counter).  r1: step t+1, whose
-  // rewrites of step t's slots take its physical rows.
+  // Step t's first touches, from the rows loaded for them (home: lane j holds
+  // write j's row).  r1: step t+1, whose rewrites of step t's slots take its
+  // physical rows.
   auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, int home)
       __attribute__((always_inline)) {
     const int count = route_count(rt.u);
     if (count > 0 && route_ok(rt.u) && alive) {
       const uint32_t fmask = route_fmask(rt.u);
-      const int p = __builtin_amdgcn_readfirstlane(home) + base_cur;
-      bool fits = p + count <= old_free;
+      bool fits = rt.base + count <= fit_rows;
       if (fits) {
         const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
-        const int k = p + rt.rank;
-        int new_row = first && k < window ? lds_free[k] : -1;
-        if (__ballot(first && k >= window) != 0) {
-          if (first && k >= window) new_row = L.free_rows[old_free - 1 - k];
-          // wait for it here, on this rare path, so that no later use of the
-          // popped rows has to drain every load in flight
-          asm volatile("" ::"v"(new_row));
-        }
+        const int new_row = first ? home : -1;
         if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
           fits = false;
           if (lane == 0) {
@@ -1206,16 +1146,7 @@ void sdm_trace_kernel(StepParams P) {
           if constexpr (MAPLDS) lds_map[rt.widx] = new_row;
         }
       }
-      if (!fits) {
-        // rare: the free stack is exhausted; every later claim fails too,
-        // and the launch's end counts only the claims before this one
-        if (lane == 0) {
-          *L.overflow_flag = 1;
-          __hip_atomic_fetch_max(scan + COWSDM_SCRATCH_CLAIM_FAIL,
-                                 kClaimFailBase - static_cast<int64_t>(p), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
+      // an overflow stops the bank (the plan set the overflow flag)
       alive = fits;
     }
     // step t+1 rewrites some of step t's slots in the rows just found
@@ -1226,215 +1157,10 @@ void sdm_trace_kernel(StepParams P) {
     }
   };
 
-  // ---- capacity proof (packed): every proof_steps steps, the first touches
-  // each bank made so far, published per run and summed by every wave
-  const int64_t proof_rows = DENSE ? 0 : P.trace_proof_rows;
-  const bool proofs = proof_rows > 0;
-  const int proof_steps = P.trace_proof_steps > 0 ? P.trace_proof_steps : 1;
-  int done_steps = G;
-  int cum = 0;                        // this bank's first touches so far
-  int run_left = proof_steps - 1;     // classified steps before the next run ends
-  int runs_published = 0;
-  int next_proof = 0;                 // step of the next proof
-  int proof_run = 0;                  // the run the next proof opens
-  uint64_t pw[SCANW];                 // the published counts of the next proof
-#pragma unroll
-  for (int k = 0; k < SCANW; ++k) pw[k] = 0;
-  // Bank b's count after its r-th run is word r * B + b of the slots (a
-  // launch has fewer runs than steps): the counts a proof sums are B
-  // consecutive words, loaded with one cache line per eight banks.
-  const int64_t* run_l[SCANW];        // this lane's bank in each window (run 0)
-#pragma unroll
-  for (int k = 0; k < SCANW; ++k) {
-    const int bk = k * kWave + lane < B ? k * kWave + lane : B - 1;
-    run_l[k] = DENSE ? nullptr : scan + COWSDM_SCRATCH_SLOTS + bk;
-  }
-
-  // Map in LDS: a bank counts its runs' first touches a chunk (64 steps)
-  // ahead of classification, from the write slots of the steps alone: a slot
-  // is first touched by the first step that writes it, unless it was mapped
-  // at the launch's start.  (A step with an invalid route claims nothing and
-  // stops the layer; the count runs on, which only makes later proofs
-  // stricter in a launch that reports an error.)  Each bank publishes its
-  // count at the end of a run at least 64 steps before the proof that sums
-  // it, so a proof does not wait for banks that run a few steps behind.
-  IDX wnext[kTraceMaxWrites];        // the write slots of the chunk counted next
-#pragma unroll
-  for (int j = 0; j < kTraceMaxWrites; ++j) wnext[j] = 0;
-  auto load_writes = [&](int c) __attribute__((always_inline)) {
-    const int st = c * kWave + lane < G ? c * kWave + lane : G - 1;
-    const char* const w = at(wbase, st_wi, st);
-#pragma unroll
-    for (int j = 0; j < kTraceMaxWrites; ++j) {
-      wnext[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : 0) * sizeof(IDX));
-    }
-  };
-  // Chunk c's steps (lane l: step 64c + l): step t first-touches slot x
-  // when x was unmapped at the launch's start and t is the first step of the
-  // launch that writes x.  Chunks come in order, so a minimum over the steps
-  // of this chunk and the chunks before gives that first step: one LDS
-  // minimum per write slot, all lanes at once, then a read back.  (An entry
-  // read here was not rewritten yet: the launch pops a slot's row only at
-  // its first write, which comes after the steps resolved so far.)  Lane l
-  // keeps its step's first-touch mask for the chunk's class words (fm_next),
-  // and with proofs on the bank publishes its count at the end of every run.
-  int ahead_cum = 0;
-  uint32_t fm_next = 0;
-  auto count_chunk = [&](int c, const IDX (&ws)[kTraceMaxWrites]) __attribute__((always_inline)) {
-    if constexpr (MAPLDS) {
-      const int t0 = c * kWave;
-      if (t0 >= G) return;
-      const int t1 = t0 + kWave < G ? t0 + kWave : G;
-      const int t = t0 + lane;
-      int x[kTraceMaxWrites];
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        const int64_t v = static_cast<int64_t>(ws[j]);
-        x[j] = j < W && t < t1 && v >= 0 && v < N ? static_cast<int>(v) : -1;
-        if (x[j] >= 0) {
-          __hip_atomic_fetch_min(&first_write[x[j]], static_cast<uint32_t>(t), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-      }
-      // one wave's LDS accesses apply in issue order: keep the reads after
-      asm volatile("" ::: "memory");
-      uint32_t f = 0;
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) {
-        if (x[j] >= 0 && first_write[x[j]] == static_cast<uint32_t>(t) && lds_map[x[j]] < 0) {
-          f |= 1u << j;
-        }
-      }
-      fm_next = f;
-      if (proofs) {
-        int r = t0 / proof_steps;       // the run holding step t0
-        for (int a = r * proof_steps; a < t1; a += proof_steps, ++r) {
-          const bool in = t >= a && t < a + proof_steps;
-#pragma unroll
-          for (int j = 0; j < kTraceMaxWrites; ++j) {
-            ahead_cum += __popcll(__ballot(in && ((f >> j) & 1u) != 0));
-          }
-          // run r ends in this chunk: its count is word r + 1
-          if (a + proof_steps <= t1 && lane == 0) {
-            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + static_cast<int64_t>(r + 1) * B + bank,
-                             slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(ahead_cum)));
-          }
-        }
-      }
-    }
-  };
-
-  // The proof before step s, at the loop head before iteration s (s even,
-  // the first step of run r = s / proof_steps): every bank published its
-  // count of first touches in runs 0..r-1 (with the map in LDS a chunk
-  // ahead, otherwise when it classified step s-1, three iterations
-  // earlier), and every wave takes the same sum (from the proof wave, or
-  // summed here), so the layer stops at the same step on every wave.  The
-  // sum is also run r's base.
-  // Returns true (and the layer stops before s) when free_count minus the
-  // base is below proof_rows, or when a count never arrives (bounded wait).
-  auto proof_fails = [&](int s) __attribute__((always_inline)) -> bool {
-    int total = 0;
-    if (PWAVE && s > 0) {
-      // summed by the proof wave (it waits for slow banks on its own)
-      const uint32_t r = static_cast<uint32_t>(proof_run);
-      uint32_t d = sync_load(&lds_proof_done);
-      for (int spins = 0; d < r && spins < 4 * kSpinLimit; ++spins) {
-        __builtin_amdgcn_s_sleep(1);
-        d = sync_load(&lds_proof_done);
-      }
-      total = d >= r ? lds_proof[r] : -1;
-      if (total < 0) {
-        if (lane == 0) {
-          __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return true;
-      }
-    } else if (s > 0) {
-      const uint32_t off = static_cast<uint32_t>(proof_run);
-      auto word_ready = [&](uint64_t w) __attribute__((always_inline)) -> bool {
-        return static_cast<uint32_t>(w >> 32) == epoch && ((w >> 30) & 3u) == kStatusAggregate;
-      };
-#pragma unroll
-      for (int k = 0; k < SCANW; ++k) {
-        if (k * kWave < B) {
-          const bool in = k * kWave + lane < B;
-          uint64_t w = pw[k];
-          int spins = 0;
-          while (__ballot(in && !word_ready(w)) != 0 && spins < kSpinLimit) {
-            __builtin_amdgcn_s_sleep(1);
-            if (!word_ready(w)) w = atomic_load_u64(run_l[k] + static_cast<int64_t>(off) * B);
-            ++spins;
-          }
-          if (__ballot(in && !word_ready(w)) != 0) {
-            // never arrived: record it and stop the layer here
-            if (lane == 0) {
-              __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                                    static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
-                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            return true;
-          }
-          total += wave_sum_launch(in ? static_cast<int>(w & kValueMask) : 0);
-        }
-      }
-    }
-    base_cur = total;
-    return old_free - total < proof_rows;
-  };
-
-  // After classifying step t: claim its rows (on its run's counter when
-  // proofs are on), and publish the bank's count when t ends a run.
-  bool halted = false;  // a proof failed: the layer stops at its step
+  // After classifying step t: load the rows its first touches pop.
   auto after_classify = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
-      if (t < G && !halted) claim(rt, home, runs_published);
-      if (proofs) {
-        if (!MAPLDS && route_ok(rt.u)) cum += route_count(rt.u);
-        if (run_left == 0) {
-          ++runs_published;
-          // (map in LDS: published by the count ahead)
-          if (!MAPLDS && t < G && lane == 0) {
-            atomic_store_u64(scan + COWSDM_SCRATCH_SLOTS + static_cast<int64_t>(runs_published) * B + bank,
-                             slot_word(epoch, kStatusAggregate, static_cast<uint64_t>(cum)));
-          }
-          run_left = proof_steps;
-        }
-        --run_left;
-      }
-    }
-  };
-
-  // The proof at the loop head before step s, when one is due there.
-  auto prove = [&](int s) __attribute__((always_inline)) -> bool {
-    if constexpr (!DENSE) {
-      if (proofs && s == next_proof) {
-        if (proof_fails(s)) {
-          done_steps = s;
-          halted = true;
-          return true;
-        }
-        next_proof += proof_steps;
-        ++proof_run;
-      }
-    }
-    return false;
-  };
-
-  // iteration s loads, at its start, the counts that the proof at the next
-  // loop head sums (before step s+1): every bank published them when it
-  // classified step s, in iteration s-2
-  auto issue_proof = [&](int s) __attribute__((always_inline)) {
-    if constexpr (!DENSE) {
-      if (!PWAVE && proofs && s + 1 == next_proof) {
-        const uint32_t off = static_cast<uint32_t>(proof_run);
-#pragma unroll
-        for (int k = 0; k < SCANW; ++k) {
-          if (k * kWave < B) pw[k] = atomic_load_u64(run_l[k] + static_cast<int64_t>(off) * B);
-        }
-      }
+      if (t < G) claim(rt, home);
     }
   };
 
@@ -1454,29 +1180,22 @@ void sdm_trace_kernel(StepParams P) {
     return false;
   };
 
-  // ---- prologue: steps 0 and 1 classified, claimed and their rows published
+  // ---- prologue: steps 0 and 1 classified, their pops loaded and their rows
+  // published
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
-  int popA = 0, popB = 0;          // claims in flight, homed by the parity of their step
+  int popA = -1, popB = -1;        // pops in flight, homed by the parity of their step
   TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
-  q.widx = 0; q.ridx = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1; q.rank = 0; q.u = 0;
-  q.fwd = 0; q.rawm = 0;
+  q.widx = 0; q.ridx = 0; q.base = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1;
+  q.rank = 0; q.u = 0; q.fwd = 0; q.rawm = 0;
+  load_plan(0);
+  if constexpr (DENSE || MAPLDS) load_chunk(0);
   if constexpr (DENSE || MAPLDS) {
-    load_chunk(0);
-    if (MAPLDS && G > kWave) load_writes(1);
-    if constexpr (MAPLDS) {
-      IDX w0[kTraceMaxWrites];
-#pragma unroll
-      for (int j = 0; j < kTraceMaxWrites; ++j) w0[j] = chunk[j];
-      count_chunk(0, w0);
-    }
-    write_chunk(0, fm_next);
-    if constexpr (MAPLDS) {
-      count_chunk(1, wnext);
-      if (2 * kWave < G) load_writes(2);
-    }
+    write_chunk(0, DENSE ? 0u : (plan_next >> kPlanMaskShift) & 15u);
     if (G > kWave) load_chunk(1);  // written before step 64 is read
   }
+  stage_plan(0);
+  if (G > kWave) load_plan(1);
   {
     TraceIdx i0, i1;
     if constexpr (DENSE || MAPLDS) {
@@ -1515,7 +1234,6 @@ void sdm_trace_kernel(StepParams P) {
   auto iteration = [&](int s, TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
                        int& mw_other, int& mr_other, int& pop)
       __attribute__((always_inline)) {
-    issue_proof(s);
     u32x4_t kq = {0u, 0u, 0u, 0u};
     if constexpr (DENSE || MAPLDS) kq = *reinterpret_cast<const u32x4_t*>(idx_row(s) + kIdxRow);
     const bool run = route_ok(rA.u) && alive;
@@ -1542,51 +1260,48 @@ void sdm_trace_kernel(StepParams P) {
   __builtin_amdgcn_s_waitcnt(0);
 
   int s = 0;
+  int done_steps = G;
   bool stopped = false;
-  for (; s + 1 < G; s += 2) {
-    if (!room(s + 4 - kTraceRing)) {
-      // the data wave stopped taking steps: record it and stop here
-      if (lane == 0 && !DENSE) {
+  // the data wave stopped taking steps (a bounded wait ran out): record it
+  auto lost = [&]() __attribute__((always_inline)) {
+    if (lane == 0) {
+      if constexpr (!DENSE) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                               static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
                               __HIP_MEMORY_SCOPE_AGENT);
       }
+      if (P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  };
+  for (; s + 1 < G; s += 2) {
+    if (!room(s + 4 - kTraceRing)) {
+      lost();
       done_steps = s;
       stopped = true;
       break;
     }
-    // the proof before step s: a run's claims were made without waiting
-    // for it, and a run that fails it never takes their rows
-    if (prove(s)) {
-      stopped = true;
-      break;
-    }
-    if constexpr (DENSE || MAPLDS) {
-      // chunk c's first slots are read in iteration 64c - 3; the buffer it
-      // replaces held chunk c - 2, whose last step was read long before
-      if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
-        const int c = (s + 4) >> 6;
-        write_chunk(c, fm_next);
-        if constexpr (MAPLDS) {
-          count_chunk(c + 1, wnext);
-          if ((c + 2) * kWave < G) load_writes(c + 2);
-        }
+    // chunk c's first slots and plan words are read in iteration 64c - 2;
+    // the buffers they replace held chunk c - 2, whose last step was read
+    // long before
+    if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
+      const int c = (s + 4) >> 6;
+      if constexpr (DENSE || MAPLDS) {
+        write_chunk(c, DENSE ? 0u : (plan_next >> kPlanMaskShift) & 15u);
         if ((c + 1) * kWave < G) load_chunk(c + 1);
       }
+      stage_plan(c);
+      if ((c + 1) * kWave < G) load_plan(c + 1);
     }
     iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
     iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB);
   }
   if (!stopped && s < G) {
     if (!room(s + 3 - kTraceRing)) {
-      if (lane == 0 && !DENSE) {
-        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
-                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-      }
+      lost();
       done_steps = s;
-      stopped = true;
-    } else if (prove(s)) {
       stopped = true;
     } else {
       iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
@@ -1597,133 +1312,121 @@ void sdm_trace_kernel(StepParams P) {
     sync_store(&sync[0], (static_cast<uint32_t>(done_steps) << 16) | kNoStop);
   }
 
-  // ---- the layer's last control wave to finish closes the launch: every
-  // wave of the layer read free_count and the step counter before taking its
-  // ticket, and its claims (device-scope atomics) have returned before it:
-  // no release fence, whose L2 write-back every wave would pay.  The data
-  // waves' row stores need no ordering here: the next launch on the stream
-  // starts after this one has ended.
-  if (!DENSE || P.trace_step) {
+  // ---- device counters: the layer's last control wave to finish advances
+  // the layer's counter.  Every wave of the layer read the counter before
+  // taking its ticket.  The data waves' row stores need no ordering here: the
+  // next launch on the stream starts after this one has ended.
+  if (P.trace_step) {
     int64_t done = 0;
     if (lane == 0) {
       int64_t* const ticket = P.trace_ticket + 1 + layer_id;
-      __builtin_amdgcn_s_waitcnt(0);
       done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
-      if constexpr (!DENSE) {
-        int64_t total;
-        if (proofs) {
-          // the runs proven: the last one's claims count unless its proof
-          // failed (then the layer stopped at its first step)
-          total = base_cur;
-          if (!halted && proof_run > 0) {
-            total += static_cast<int64_t>(atomic_load_u64(run_claims + proof_run - 1));
-          }
-          // clear the counter of every run any wave may have claimed on
-          const int runs = (G - 1) / proof_steps + 1;
-          for (int k = lane; k < runs; k += kWave) atomic_store_u64(run_claims + k, 0);
-        } else {
-          total = static_cast<int64_t>(atomic_load_u64(claims));
-        }
-        // the first claim that did not fit (at position p) cuts the total
-        const int64_t fail = static_cast<int64_t>(atomic_load_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL));
-        const int64_t fit = fail > 0 && kClaimFailBase - fail < total ? kClaimFailBase - fail : total;
-        if (lane == 0) {
-          *L.free_count = static_cast<int32_t>(old_free - fit);
-          if (P.trace_free_out) {
-            atomic_store_u64(&P.trace_free_out[layer_id], static_cast<uint64_t>(old_free - fit));
-          }
-          atomic_store_u64(claims, 0);
-          atomic_store_u64(scan + COWSDM_SCRATCH_CLAIM_FAIL, 0);
-          atomic_store_u64(scan + COWSDM_SCRATCH_EPOCH, static_cast<uint64_t>(epoch + 1u));
-          if (done_steps < G && P.trace_status) {
-            __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{1}, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-      if (lane == 0) {
-        atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
-        if (P.trace_step) {
-          atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
-        }
-      }
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1 && lane == 0) {
+      atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
+      atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
     }
   }
 }
 
+// Count and plan passes of a packed persistent launch (trace_plan.hip).
+template <typename IDX>
+int32_t launch_trace_plan(const StepParams& P, hipStream_t stream, hipEvent_t start);
+extern template int32_t launch_trace_plan<int32_t>(const StepParams&, hipStream_t, hipEvent_t);
+extern template int32_t launch_trace_plan<int64_t>(const StepParams&, hipStream_t, hipEvent_t);
+
+// Residency of one persistent kernel variant on one device: how many of its
+// workgroups the device holds at once for a given slot-map size.
+struct TraceResidency {
+  int device = -1;
+  int slots = -1;
+  int blocks = 0;
+};
+
 // Workgroups of a persistent launch wait on one another, so every one of them
-// must be resident at once.  Returns false (nothing launched) when the grid
-// exceeds what the device can hold for this kernel; the caller then falls
-// back to one launch per step.
+// must be resident at once.  Returns 0 when launched, 1 (nothing launched)
+// when the grid exceeds what the device can hold for this kernel (the caller
+// then falls back to one launch per step), else an error code.  The residency check assumes the launch has
+// the device's compute units to itself: another process's kernels holding
+// CUs meanwhile could delay the launch's last workgroups until the bounded
+// waits of the first ones run out (the launch then reports
+// COWSDM_TRACE_FAULT, it does not hang).
 template <typename IDX, bool DENSE, bool MAPLDS>
-bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
+int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
   StepParams P = P0;
   P.blocks_per_layer = (P.banks + kTraceBanksPerBlock - 1) / kTraceBanksPerBlock;
   const int blocks = P.blocks_per_layer * P.nlayers;
   // the full shape folds every row count; other shapes select per row
   const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
-  // one scan window when a packed layer has at most 64 banks
-  constexpr int kScan1 = DENSE ? kTraceScanWindows : 1;
-  const int variant = (full ? 1 : 0) + (!DENSE && P.banks <= kWave ? 2 : 0);
+  const bool few = P.banks <= kWave;
+  const int variant = (full ? 1 : 0) + (few ? 2 : 0);
   const void* kernels[4][3] = {
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kTraceScanWindows, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kTraceScanWindows, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kTraceScanWindows, MAPLDS>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kTraceScanWindows, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kTraceScanWindows, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kTraceScanWindows, MAPLDS>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, kScan1, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, kScan1, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, kScan1, MAPLDS>)},
-      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, kScan1, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, kScan1, MAPLDS>),
-       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, kScan1, MAPLDS>)}};
-  // residency depends on the LDS map's size: cached per kernel and slot count
-  static int resident[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
-  static int resident_slots[4][3] = {{-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}, {-1, -1, -1}};
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, false, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, false, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, false, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, false, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, false, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, false, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, false, true, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, false, true, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, false, true, MAPLDS>)},
+      {reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 1, DENSE, true, true, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 2, DENSE, true, true, MAPLDS>),
+       reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, true, MAPLDS>)}};
+  // Residency depends on the device and on the LDS map's size: cached per
+  // kernel variant for the last (device, slot count) it was asked for.  The
+  // cache is process-wide; a library call made from several host threads at
+  // once may query the occupancy twice, which is harmless.
+  static TraceResidency resident[4][3];
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
-  // map in LDS: per bank the slot map and each slot's first writing step
+  // map in LDS: per bank the slot map
   const size_t lds_bytes =
-      MAPLDS ? 2 * sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
+      MAPLDS ? sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
   const int key = MAPLDS ? P.slots : 0;
-  // packed layers of at most 64 banks (SCANW 1) add the proof wave
-  const int threads = !DENSE && variant >= 2 ? kTraceProofThreads : kTraceThreads;
-  if (resident[variant][which] < 0 || resident_slots[variant][which] != key) {
-    int device = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  TraceResidency& cached = resident[variant][which];
+  if (cached.device != device || cached.slots != key) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds_bytes) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kTraceThreads, lds_bytes) !=
             hipSuccess) {
       (void)hipGetLastError();
-      resident[variant][which] = 0;
+      cached.blocks = 0;
     } else {
-      resident[variant][which] = cus * per_cu;
+      cached.blocks = cus * per_cu;
     }
-    resident_slots[variant][which] = key;
+    cached.device = device;
+    cached.slots = key;
   }
   // Layers are independent within a launch: when the whole grid cannot be
   // resident, launch groups of layers that can, one after another on the
   // stream, each with its per-layer words offset to its first layer.
-  const int per_launch = resident[variant][which] / P.blocks_per_layer;
-  if (per_launch <= 0) return false;
-  // plain launches, or with start/stop events when the caller measures
-  auto launch = [&](StepParams* q, int grid) {
+  const int per_launch = cached.blocks / P.blocks_per_layer;
+  if (per_launch <= 0) return 1;
+  // With timing on, one event pair spans the launch: the count pass's start
+  // (packed state) or the first kernel's, and the last kernel's end.
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (!trace_timing_events(&start, &stop)) start = stop = nullptr;
+  if constexpr (!DENSE) {
+    // the plan of every layer's launch, before any of its steps run
+    if (int32_t e = launch_trace_plan<IDX>(P, stream, start)) return e;
+    start = nullptr;
+  }
+  auto launch = [&](StepParams* q, int grid, bool last) {
     void* args[] = {q};
-    hipEvent_t start, stop;
-    if (trace_timing_events(&start, &stop)) {
-      (void)hipExtLaunchKernel(kernel, dim3(grid), dim3(threads), args, lds_bytes, stream, start,
-                               stop, 0);
-    } else {
-      (void)hipLaunchKernel(kernel, dim3(grid), dim3(threads), args, lds_bytes, stream);
-    }
+    (void)hipExtLaunchKernel(kernel, dim3(grid), dim3(kTraceThreads), args, lds_bytes, stream,
+                             start, last ? stop : nullptr, 0);
+    start = nullptr;
   };
-  if (blocks <= resident[variant][which]) {
-    launch(&P, blocks);
-    return true;  // a failed launch is reported by the caller's launch_status()
+  if (blocks <= cached.blocks) {
+    launch(&P, blocks, true);
+    return 0;  // a failed launch is reported by the caller's launch_status()
   }
   for (int l0 = 0; l0 < P0.nlayers; l0 += per_launch) {
     StepParams Q = P;
@@ -1732,15 +1435,15 @@ bool launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) {
     if (P0.trace_step) Q.trace_step = P0.trace_step + l0;
     if (P0.trace_ticket) Q.trace_ticket = P0.trace_ticket + l0;  // word 1 + layer
     if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
-    if (P0.trace_free_out) Q.trace_free_out = P0.trace_free_out + l0;
+    if (P0.control) Q.control = P0.control + l0;
     if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
-    launch(&Q, Q.blocks_per_layer * Q.nlayers);
+    launch(&Q, Q.blocks_per_layer * Q.nlayers, l0 + per_launch >= P0.nlayers);
   }
-  return true;
+  return 0;
 }
 
 template <typename IDX, bool DENSE>
-bool launch_trace(const StepParams& P, int vec, hipStream_t stream) {
+int32_t launch_trace(const StepParams& P, int vec, hipStream_t stream) {
   // packed layers whose slot map fits keep it in LDS
   if (!DENSE && P.slots <= kTraceMapSlots) {
     return launch_trace_kernels<IDX, DENSE, true>(P, vec, stream);

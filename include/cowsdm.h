@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 4
+#define COWSDM_ABI_VERSION 5
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -59,13 +59,8 @@ extern "C" {
 /* Word offsets inside the per-layer step scratch (int64 words). */
 /* EPOCH retires the previous launch's scan slots (the layer's last wave
  * advances it); ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's
- * scan slot.  In a decode trace's scan buffer, CLAIMS counts the rows the
- * current persistent launch has claimed and CLAIM_FAIL records the first
- * claim that did not fit (both zero between launches).  Words 4-7 are
- * reserved. */
+ * scan slot.  Words 1, 2 and 4-7 are reserved. */
 #define COWSDM_SCRATCH_EPOCH 0
-#define COWSDM_SCRATCH_CLAIMS 1
-#define COWSDM_SCRATCH_CLAIM_FAIL 2
 #define COWSDM_SCRATCH_ERRORS 3
 #define COWSDM_SCRATCH_SLOTS 8
 
@@ -124,49 +119,80 @@ typedef struct cowsdm_layer {
  * kernels advance step_index[l] by the steps it ran, so the call can be
  * captured once in a hipGraph and replayed.  ticket points at 1 + nlayers
  * int64 words that are zero before the first launch and stay zero between
- * launches.  A layer with no step left runs nothing and sets bit 1 of
- * status[l] (status null, packed state: COWSDM_ERR_TRACE_RANGE instead).
+ * launches.  A layer with no step left runs nothing and sets
+ * COWSDM_TRACE_ENDED in status[l] (status null, packed state:
+ * COWSDM_ERR_TRACE_RANGE instead).
  *
- * Device capacity proof (packed state, persistent launches on device
- * counters): with proof_rows > 0 and proof_steps even, before each run of
- * proof_steps steps a
- * layer checks free_count >= proof_rows -- what prepare_step_capacity(
- * proof_rows) proves before a group of proof_steps steps.  A layer that
- * fails stops there, keeps its counter at the first step it did not run and
- * sets bit 0 of status[l]; the caller grows that layer exactly as
- * prepare_step_capacity would and calls again.  status words are sticky
- * (the kernels only set bits); status is device memory. */
+ * Persistent launches: with persistent != 0 one launch runs up to
+ * scan_steps (at most 512) steps when the shape allows it (W <= 4, R <= 16,
+ * D <= 256, banks <= 256 for packed state, and every workgroup of one layer
+ * resident; layers whose workgroups do not all fit at once run as groups of
+ * layers, one launch after another), else one launch per step.
+ *
+ * Packed persistent launches plan each launch before running it: a count
+ * pass finds every (step, bank)'s first touches, and a plan pass, one
+ * workgroup per layer, replays the decode loop's capacity proof
+ * (prepare_step_capacity(need) before every step, allocator.py:745-773,
+ * inference.py:551-552), grows the slab within its buffer as grow_capacity
+ * would (allocator.py:691-743), and lists the rows every first touch pops in
+ * the order of single-step launches (step-major, bank-major within a step,
+ * allocator.py:1471-1481), writing the free stack and free_count the launch
+ * leaves.  The launch then takes its rows from that list.  Readings, maps,
+ * slab rows, free stacks and growth counters equal those of the loop of
+ * single steps.  The proof state lives on the device in `control`
+ * (COWSDM_CTRL_WORDS words per layer, word k of layer l at
+ * control[k * control_stride + l]); the caller sets it before the launches
+ * and reads it back after them.  `scan` holds nlayers blocks of scan_words
+ * int64 words (>= cowsdm_trace_scan_words(banks, writes, scan_steps)) for
+ * the plan. */
 typedef struct cowsdm_trace {
   int64_t* step_index;
   int64_t* ticket;
   int64_t first_step;
   int64_t stride_bytes[9];
-  /* Persistent launches: with persistent != 0 one launch runs up to 512
-   * steps when the shape allows it (W <= 4, R <= 16, D <= 256, banks <= 256
-   * for packed state, and every workgroup of one layer resident; layers
-   * whose workgroups do not all fit at once run as groups of layers, one
-   * launch after another), else one launch per step -- and with proof_rows
-   * > 0 a COWSDM_ELIMIT error, since per-step launches make no proofs.
-   * Packed launches then need `scan`: nlayers blocks of scan_words int64
-   * words (>= cowsdm_trace_scan_words(banks, min(steps, 512))), zero before
-   * first use and kept valid by the kernels, and `ticket` (1 + nlayers
-   * int64 words, zero before the first launch), also with host offsets:
-   * the layer's last wave to finish writes free_count back.  First touches
-   * then claim their rows with an atomic add per (step, bank), as the
-   * reference's proven kernel does, so physical rows may be a permutation
-   * of those of single-step launches; everything else is identical. */
   int64_t* scan;
   int64_t scan_words;
   int32_t persistent;
-  int32_t proof_steps;
+  int32_t scan_steps;       /* steps per launch the scan blocks hold */
   int64_t steps_recorded;
-  int64_t proof_rows;
-  int32_t* status;
-  /* Packed state, or null: the layer's last wave to finish a launch also
-   * writes the layer's free_count to free_out[l] (int64), so that a caller
-   * reads the counters, the status words and the free counts back at once. */
-  int64_t* free_out;
+  int32_t* status;          /* per-layer COWSDM_TRACE_* bits, or null */
+  int64_t* control;         /* packed persistent launches, see above */
+  int64_t control_stride;
 } cowsdm_trace_t;
+
+/* Control words of one layer of a packed decode trace (int64, word k of
+ * layer l at control[k * control_stride + l]).  The caller sets them from
+ * its state; a launch's plan reads and updates them.
+ *   PROVEN    rows proven but not yet charged (the reference's
+ *             proven_maximum_additional_allocations)
+ *   CAPACITY  slab capacity C in rows (grows within ROOM)
+ *   ROOM      rows of the slab's buffers (values and free_rows)
+ *   QUANTUM   growth quantum in rows (0: no growth)
+ *   NEED      rows proven before every step (banks * W), 0: no proof
+ *   EVENTS, ADDED, COPIED  growth counters, added to by each launch
+ *   FREE      free_count after the last launch
+ *   STEPS     steps the last launch ran (its plan stops a layer before a
+ *             growth past ROOM and sets COWSDM_TRACE_REFUSED)
+ *   FIT       first touches of the last launch that got rows */
+#define COWSDM_CTRL_PROVEN 0
+#define COWSDM_CTRL_CAPACITY 1
+#define COWSDM_CTRL_ROOM 2
+#define COWSDM_CTRL_QUANTUM 3
+#define COWSDM_CTRL_NEED 4
+#define COWSDM_CTRL_EVENTS 5
+#define COWSDM_CTRL_ADDED 6
+#define COWSDM_CTRL_COPIED 7
+#define COWSDM_CTRL_FREE 8
+#define COWSDM_CTRL_STEPS 9
+#define COWSDM_CTRL_FIT 10
+#define COWSDM_CTRL_WORDS 12
+
+/* Bits of a decode trace's per-layer status word (sticky: the kernels only
+ * set them). */
+#define COWSDM_TRACE_REFUSED 0x1  /* stopped before a growth past ROOM     */
+#define COWSDM_TRACE_ENDED 0x2    /* no recorded step left                 */
+#define COWSDM_TRACE_FAULT 0x4    /* stopped by a timed-out wait or corrupt
+                                     state (see the scratch error word)    */
 
 /* ---------------------------------------------------------------- info */
 
@@ -174,8 +200,16 @@ int32_t cowsdm_abi_version(void);
 const char* cowsdm_last_error_string(void);
 /* int64 words of step scratch one layer with `banks` banks needs. */
 int64_t cowsdm_step_scratch_words(int64_t banks);
-/* int64 words per layer of a persistent trace launch's scan buffer. */
-int64_t cowsdm_trace_scan_words(int64_t banks, int32_t steps);
+/* int64 words per layer of a packed decode trace's scan blocks for launches
+ * of up to `steps` steps (cowsdm_trace_t.scan). */
+int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps);
+/* 1 when trace launches of these layers run persistent (shape, pointer
+ * alignment and strides allow it; see cowsdm_trace_t), else 0: packed
+ * launches then need control null and run one launch per step.  No
+ * counterpart in the reference. */
+int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
+                                const struct cowsdm_shape* shape,
+                                const struct cowsdm_trace* trace, int32_t dense);
 
 /* Kernel timing of persistent trace launches, for measurement (no
  * reference counterpart; one host thread): after cowsdm_trace_timing(1)

@@ -87,3 +87,41 @@ def make_case(*, banks, slots, width, writes, reads, steps, seed, index_dtype=to
                                  writes=writes, reads=reads, seed=seed + 1,
                                  index_dtype=index_dtype, distribution=distribution)
     return m0, [batch.step(s, 0) for s in range(steps)]
+
+
+def assert_states_identical(a, b) -> None:
+    """Two product states equal bit for bit: maps (physical rows included),
+    free stacks, live rows, flags, capacities, growth counters and proofs."""
+
+    x, y = snapshot(a), snapshot(b)
+    assert x["capacity"] == y["capacity"]
+    assert x["free_count"] == y["free_count"]
+    assert np.array_equal(x["map"], y["map"])
+    assert np.array_equal(x["free_rows"], y["free_rows"])
+    assert np.array_equal(x["live_values"], y["live_values"])
+    assert x["overflow"] == y["overflow"]
+    assert (a.growth_events, a.growth_rows_added, a.growth_rows_copied) == (
+        b.growth_events, b.growth_rows_added, b.growth_rows_copied)
+    assert a.capacity_is_proven == b.capacity_is_proven
+    assert (a.proven_maximum_additional_allocations
+            == b.proven_maximum_additional_allocations)
+
+
+def oracle_decode_loop(oracles, batch, steps, *, start=0, need=None):
+    """The reference's decode loop on oracle states (inference.py:538-566):
+    per step and layer, prepare_step_capacity(need) when the state has a
+    growth quantum (allocator.py:745-773), then the packed step.  ``batch``
+    is a synthetic.StepBatch on any device.  Returns the readings
+    [steps, L, B, D]."""
+
+    out = []
+    for s in range(start, start + steps):
+        row = []
+        for l, orc in enumerate(oracles):
+            if orc.growth_quantum_rows and need is not None:
+                ref.prepare_step_capacity(orc, need)
+            x = {k: v.cpu().numpy() for k, v in batch.step(s, l).items()}
+            reading, _ = ref.packed_step(orc, **x, validate_routes=False)
+            row.append(reading)
+        out.append(np.stack(row))
+    return np.stack(out)

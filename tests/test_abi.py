@@ -38,7 +38,10 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == 4
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 5
+    # plan words [banks][steps] and at most banks * W pops per step, int32
+    assert lib.cowsdm_trace_scan_words(64, 4, 512) == (64 * 512 * 5 + 1) // 2
+    assert lib.cowsdm_trace_scan_words(-1, 4, 512) == -1
     assert lib.cowsdm_step_scratch_words(64) == 8 + 64
     assert lib.cowsdm_step_scratch_words(-1) == -1
     assert lib.cowsdm_workspace_bytes(0, 0) == 256
@@ -59,6 +62,15 @@ def test_argument_errors_return_codes_without_launching():
     assert lib.cowsdm_packed_step(ctypes.byref(layer), ctypes.byref(shape), None) == -1
     assert b"null" in lib.cowsdm_last_error_string()
     assert lib.cowsdm_grow(None, 0, None, 0, 0, None, None, None, None, None) == -1
+    # persistent-launch query: null arguments and shapes past the kernel's
+    # limits answer 0 without touching a device
+    trace = nat.Trace()
+    assert lib.cowsdm_trace_persistent(None, 1, ctypes.byref(shape), ctypes.byref(trace), 0) == 0
+    layer = nat.Layer()
+    wide = nat.Shape(banks=4, slots=16, width=128, writes=5, reads=4, templates=1,
+                     index_dtype=0)
+    assert lib.cowsdm_trace_persistent(ctypes.byref(layer), 1, ctypes.byref(wide),
+                                       ctypes.byref(trace), 0) == 0
 
 
 def test_trace_timing_without_launches():

@@ -1,25 +1,37 @@
-"""BASELINE configurations at their real per-layer shapes, checked through
-properties that do not depend on size: the packed decode equals the
-dense-table decode bit for bit (readings and materialised state), equals the
-host-proven per-step loop of the reference (capacities, growth counters,
-private rows, free stack, readings; physical rows up to a permutation), and
-keeps the allocator invariants.
+"""BASELINE configurations on the HIP path.
 
-Config 2: L=7, B=64, N=256, D=128, 256-token prefill handed off, decode with
-the capacity proven on the device every 4 steps.  Config 3: B=64, 2,048-token
-prefill handed off.  Config 5: one layer of its shape (4 heads x 64 requests
-= 256 banks, N=65,536, Zipf(1.1) routes) decoded from an empty slab that
-grows by one quantum every few steps.
+Config 1 (1 layer, B=1, 16-token prefill, 64 decode tokens) end to end
+against the oracle, bit for bit.  The other configurations at their real
+shapes, checked through properties that do not depend on size: the packed
+decode (``DecodeTrace.run``) equals
+
+* the reference's decode loop run step by step on the device
+  (``decode_sdm_layer``: prepare_step_capacity(banks * W), then
+  ``packed_sdm_cow_step``; inference.py:538-566) in readings, maps, physical
+  rows, free stacks, capacities, growth counters and proofs;
+* the dense-table decode (``decode_sdm_layer_dense`` step by step, and the
+  dense persistent trace) in readings and materialised state;
+
+and keeps the allocator invariants.
+
+Config 2: L=7, N=256, D=128, 256-token prefill handed off, B = 1, 16, 64.
+Config 3: B=64, 2,048-token prefill handed off.  Config 5 (4 heads x 64
+requests = 256 banks, N=65,536, Zipf(1.1) routes) decoded from an empty slab
+that grows every few steps: one layer, and all 7 layers for 1,024 steps.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
 import copy_on_write_sdm_amd as cow
 from copy_on_write_sdm_amd import synthetic
-from gpu_helpers import assert_states_match
+from copy_on_write_sdm_amd.inference import (SDMStepInputs, decode_sdm_layer,
+                                             decode_sdm_layer_dense)
+from gpu_helpers import assert_state_equal, assert_states_identical, oracle_decode_loop
+from oracle import state as ref
 
 pytestmark = pytest.mark.gpu
 
@@ -38,10 +50,11 @@ def _routes(device, *, steps, layers, banks, slots, seed, distribution="uniform"
 
 def _handoff(device, m0, *, layers, banks, slots, prefix, quantum, seed):
     """Dense prefill of `prefix` tokens, then the copy-on-write handoff of
-    every layer (inference.py:314-366)."""
+    every layer (inference.py:314-366).  Returns a factory of fresh states
+    and the prefix routes."""
 
     pre, kw = _routes(device, steps=prefix, layers=layers, banks=banks, slots=slots, seed=seed)
-    tables = [m0[l, 0].expand(banks, -1, -1).contiguous() for l in range(layers)]
+    tables = [m0[l, 0].expand(banks, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(layers)]
     cow.DecodeTrace(memories=tables, **kw).launch(prefix, start=0)
 
     def states():
@@ -55,25 +68,27 @@ def _handoff(device, m0, *, layers, banks, slots, prefix, quantum, seed):
                 growth_quantum_rows=quantum))
         return out
 
-    return states
+    return states, pre
 
 
-def _host_proven(states, batch, *, steps, layers, banks, proof_steps):
-    """The reference's decode loop: prove capacity for a group of steps on
-    the host (prepare_step_capacity), then step every layer."""
+def _reference_loop(states, batch, *, steps, layers):
+    """The reference's per-layer decode call, step by step: readings
+    [steps, L, B, D]."""
 
-    need = banks * W * proof_steps
     outs = []
-    for g in range(0, steps, proof_steps):
-        for st in states:
-            st.prepare_step_capacity(need)
-        for s in range(g, min(g + proof_steps, steps)):
-            row = []
-            for l in range(layers):
-                r, _ = cow.packed_sdm_cow_step(states[l], **batch.step(s, l),
-                                               validate_routes=False, collect_diagnostics=False)
-                row.append(r)
-            outs.append(torch.stack(row))
+    for s in range(steps):
+        outs.append(torch.stack([
+            decode_sdm_layer(states[l], SDMStepInputs(**batch.step(s, l)))
+            for l in range(layers)]))
+    return torch.stack(outs)
+
+
+def _dense_loop(tables, batch, *, steps, layers):
+    outs = []
+    for s in range(steps):
+        outs.append(torch.stack([
+            decode_sdm_layer_dense(tables[l], SDMStepInputs(**batch.step(s, l)))
+            for l in range(layers)]))
     return torch.stack(outs)
 
 
@@ -81,44 +96,89 @@ def _check(states, host, dense, outputs, want, dense_out):
     assert torch.equal(outputs, want)
     assert torch.equal(dense_out, want)
     for a, b, t in zip(states, host, dense):
-        assert a.capacity_rows == b.capacity_rows
-        assert (a.growth_events, a.growth_rows_added, a.growth_rows_copied) == (
-            b.growth_events, b.growth_rows_added, b.growth_rows_copied)
-        assert_states_match(a, b)
+        assert_states_identical(a, b)
         assert torch.equal(a.materialize_dense(), t)
         a.validate_invariants()
 
 
-@pytest.mark.parametrize("prefix,steps", [(256, 128), (2048, 64)])
-def test_config2_and_config3_handoff_then_decode(device, prefix, steps):
-    layers, banks, slots, proof_steps = 7, 64, 256, 4
-    print(f"config handoff prefix={prefix} decode={steps}", flush=True)
-    quantum = max(16, banks * W * proof_steps)
+def test_config1_end_to_end_matches_oracle(device):
+    """Config 1: 1 layer, B=1, N=256, D=128, a 16-token dense prefill, the
+    handoff, then 64 decode tokens with a growth quantum of 16 rows, on the
+    HIP path (persistent decode and the per-step reference loop) against
+    the oracle, bit for bit (readings, physical rows, counters)."""
+
+    banks, slots, prefix, steps, quantum = 1, 256, 16, 64, 16
+    m0 = synthetic.make_initial_memory(1, 1, slots, D, seed=11, device=device)
+    make_states, pre = _handoff(device, m0, layers=1, banks=banks, slots=slots, prefix=prefix,
+                                quantum=quantum, seed=12)
+    batch, kw = _routes(device, steps=steps, layers=1, banks=banks, slots=slots, seed=13)
+    # the oracle: dense prefill, handoff, decode loop
+    dense = np.repeat(m0[0, 0].cpu().numpy()[None], banks, axis=0)
+    for s in range(prefix):
+        x = {k: v.cpu().numpy() for k, v in pre.step(s, 0).items()}
+        ref.dense_step(dense, **x, validate_routes=False)
+    active = np.zeros((banks, slots), dtype=bool)
+    for b in range(banks):
+        active[b, pre.write_indices[:, 0, b].cpu().numpy().ravel()] = True
+    orc = ref.from_dense_overlay(m0[0].cpu().numpy(), dense, active,
+                                 template_indices=np.zeros(banks, dtype=np.int64),
+                                 growth_quantum_rows=quantum)
+    traced, host = make_states(), make_states()
+    assert_state_equal(traced[0], orc)
+    want = oracle_decode_loop([orc], batch, steps, need=banks * W)
+    outputs = torch.empty(steps, 1, banks, D, device=device)
+    cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps)
+    got_host = _reference_loop(host, batch, steps=steps, layers=1)
+    assert np.array_equal(outputs.cpu().numpy(), want)
+    assert np.array_equal(got_host.cpu().numpy(), want)
+    assert_state_equal(traced[0], orc)
+    assert_state_equal(host[0], orc)
+    assert traced[0].growth_events > 0
+    traced[0].validate_invariants()
+
+
+@pytest.mark.parametrize("batch_size,prefix,steps", [
+    (64, 256, 128),    # config 2
+    (16, 256, 96),     # config 2, B=16
+    (1, 256, 96),      # config 2, B=1
+    (64, 2048, 64),    # config 3
+])
+def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, steps):
+    layers, banks, slots = 7, batch_size, 256
+    print(f"config handoff B={banks} prefix={prefix} decode={steps}", flush=True)
+    quantum = max(16, banks * W * 4)
     m0 = synthetic.make_initial_memory(layers, 1, slots, D, seed=31, device=device)
-    make_states = _handoff(device, m0, layers=layers, banks=banks, slots=slots, prefix=prefix,
-                           quantum=quantum, seed=32)
+    make_states, _ = _handoff(device, m0, layers=layers, banks=banks, slots=slots,
+                              prefix=prefix, quantum=quantum, seed=32)
     batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=33)
     traced, host = make_states(), make_states()
     dense = [st.materialize_dense() for st in traced]
+    dense_steps = [t.clone() for t in dense]
     outputs = torch.empty(steps, layers, banks, D, device=device)
-    cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps, proof_steps=proof_steps)
+    # two runs, the first of an odd length, as a warmup then a timed run would
+    tr = cow.DecodeTrace(states=traced, outputs=outputs, **kw)
+    tr.run(5)
+    tr.run(steps - 5)
     dense_out = torch.empty_like(outputs)
     cow.DecodeTrace(memories=dense, outputs=dense_out, **kw).launch(steps, start=0)
-    want = _host_proven(host, batch, steps=steps, layers=layers, banks=banks,
-                        proof_steps=proof_steps)
+    want = _reference_loop(host, batch, steps=steps, layers=layers)
+    dense_want = _dense_loop(dense_steps, batch, steps=steps, layers=layers)
     torch.cuda.synchronize()
+    assert torch.equal(dense_want, want)
     _check(traced, host, dense, outputs, want, dense_out)
+    for a, t in zip(traced, dense_steps):
+        assert torch.equal(a.materialize_dense(), t)
 
 
 def test_layer_groups_when_grid_exceeds_residency(device):
-    """8 layers x 256 banks is twice the workgroups the device holds at once:
-    the persistent decode runs the layers in groups, each still proven on the
-    device, and matches the dense decode and the host-proven loop."""
+    """8 layers x 256 banks is more workgroups than the device holds at once:
+    the persistent decode runs the layers in groups, each planned on the
+    device, and matches the dense decode and the reference loop."""
 
-    heads, requests, slots, steps, proof_steps, layers = 4, 64, 64, 48, 4, 8
+    heads, requests, slots, steps, layers = 4, 64, 64, 48, 8
     banks = heads * requests
     print(f"layer groups: L={layers} banks={banks} N={slots} steps={steps}", flush=True)
-    quantum = banks * W * proof_steps
+    quantum = banks * W * 4
     m0 = synthetic.make_initial_memory(layers, heads, slots, D, seed=61, device=device)
     templates = torch.arange(heads, dtype=torch.int64, device=device).repeat(requests)
     batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=62,
@@ -132,41 +192,60 @@ def test_layer_groups_when_grid_exceeds_residency(device):
     traced, host = states(), states()
     dense = [m0[l][templates].contiguous() for l in range(layers)]
     outputs = torch.empty(steps, layers, banks, D, device=device)
-    report = cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps,
-                                                                      proof_steps=proof_steps)
-    assert report["growth_rounds"] > 0
+    cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps)
+    assert all(st.growth_events > 0 for st in traced)
     dense_out = torch.empty_like(outputs)
     cow.DecodeTrace(memories=dense, outputs=dense_out, **kw).launch(steps, start=0)
-    want = _host_proven(host, batch, steps=steps, layers=layers, banks=banks,
-                        proof_steps=proof_steps)
+    want = _reference_loop(host, batch, steps=steps, layers=layers)
     torch.cuda.synchronize()
     _check(traced, host, dense, outputs, want, dense_out)
 
 
-def test_config5_layer_zipf_growth(device):
-    heads, requests, slots, steps, proof_steps = 4, 64, 65536, 64, 4
+def _config5(device, *, layers, steps, seed):
+    heads, requests, slots = 4, 64, 65536
     banks = heads * requests
-    print(f"config 5 layer: banks={banks} N={slots} steps={steps}", flush=True)
-    quantum = banks * W * proof_steps
-    m0 = synthetic.make_initial_memory(1, heads, slots, D, seed=51, device=device)
+    print(f"config 5: L={layers} banks={banks} N={slots} steps={steps}", flush=True)
+    quantum = banks * W * 4
+    m0 = synthetic.make_initial_memory(layers, heads, slots, D, seed=seed, device=device)
     templates = torch.arange(heads, dtype=torch.int64, device=device).repeat(requests)
-    batch, kw = _routes(device, steps=steps, layers=1, banks=banks, slots=slots, seed=52,
-                        distribution="zipf", heads=heads)
+    batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots,
+                        seed=seed + 1, distribution="zipf", heads=heads)
 
     def states():
         return [cow.PackedSDMCopyOnWriteState.allocate(
-            m0[0], banks=banks, capacity_rows=quantum, template_indices=templates,
-            growth_quantum_rows=quantum)]
+            m0[l], banks=banks, capacity_rows=quantum, template_indices=templates,
+            growth_quantum_rows=quantum) for l in range(layers)]
 
     traced, host = states(), states()
-    dense = [m0[0][templates].contiguous()]
-    outputs = torch.empty(steps, 1, banks, D, device=device)
-    report = cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps,
-                                                                      proof_steps=proof_steps)
-    assert report["growth_rounds"] > 0        # the slab grew on the way
-    dense_out = torch.empty_like(outputs)
-    cow.DecodeTrace(memories=dense, outputs=dense_out, **kw).launch(steps, start=0)
-    want = _host_proven(host, batch, steps=steps, layers=1, banks=banks,
-                        proof_steps=proof_steps)
+    outputs = torch.empty(steps, layers, banks, D, device=device)
+    report = cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps)
+    want = _reference_loop(host, batch, steps=steps, layers=layers)
     torch.cuda.synchronize()
-    _check(traced, host, dense, outputs, want, dense_out)
+    assert torch.equal(outputs, want)
+    del want
+    for a, b in zip(traced, host):
+        assert a.growth_events > 0
+        assert_states_identical(a, b)
+        a.validate_invariants()
+    del host
+    # the dense-table decode, one layer at a time (8 GiB per layer)
+    dense_out = torch.empty(steps, 1, banks, D, device=device)
+    for l in range(layers):
+        table = m0[l][templates].contiguous()
+        one = {k: v[:, l:l + 1].contiguous() for k, v in kw.items()}
+        cow.DecodeTrace(memories=[table], outputs=dense_out, **one).launch(steps, start=0)
+        assert torch.equal(dense_out[:, 0], outputs[:, l]), l
+        assert torch.equal(traced[l].materialize_dense(), table), l
+        del table
+    return report
+
+
+def test_config5_layer_zipf_growth(device):
+    _config5(device, layers=1, steps=64, seed=51)
+
+
+def test_config5_full_size(device):
+    """Config 5 at full size: 7 layers x 256 banks over N = 65,536 slots,
+    1,024 Zipf steps with the growth quantum of 4 steps."""
+
+    _config5(device, layers=7, steps=1024, seed=71)

@@ -326,7 +326,7 @@ def test_continuous_batching_config4(device):
                                       width=width, writes=writes, reads=reads, seed=seed)
         states, oracles = [], []
         for l in range(layers):
-            table = m0[l, 0].expand(requests, -1, -1).contiguous().to(device)
+            table = m0[l, 0].expand(requests, -1, -1).clone(memory_format=torch.contiguous_format).to(device)
             for t in range(time):
                 cow.dense_sdm_sparse_step(table, **to_device(routes.step(t, l), device),
                                           validate_routes=False)

@@ -33,7 +33,7 @@ def _trace(device, *, banks, slots, width, writes, reads, steps, seed,
     state.capacity_is_proven = True
     oracle = ref.allocate(m0.numpy(), banks=banks, capacity_rows=capacity)
     oracle.capacity_is_proven = True
-    dense = m0.expand(banks, -1, -1).contiguous().to(device)
+    dense = m0.expand(banks, -1, -1).clone(memory_format=torch.contiguous_format).to(device)
     for s, inputs in enumerate(seq):
         gpu = to_device(inputs, device)
         reading, diag = cow.packed_sdm_cow_step(state, **gpu, validate_routes=False)
@@ -168,7 +168,7 @@ def test_layers_launch_equals_per_layer_calls(device):
               for l in range(layers)]
     for st in fused + single:
         st.capacity_is_proven = True
-    dense = [m0[l].expand(banks, -1, -1).contiguous() for l in range(layers)]
+    dense = [m0[l].expand(banks, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(layers)]
     for s in range(5):
         outs = cow.packed_sdm_cow_step_layers(
             fused, batch.write_indices[s], batch.write_weights[s], batch.values[s],
@@ -235,7 +235,7 @@ def test_route_validation_errors(device):
         bad[key] = torch.tensor(value, dtype=torch.int64, device=device)
         with pytest.raises(ValueError, match=message):
             cow.packed_sdm_cow_step(state, **bad)
-        dense = initial.expand(rc.BANKS, -1, -1).contiguous().to(device)
+        dense = initial.expand(rc.BANKS, -1, -1).clone(memory_format=torch.contiguous_format).to(device)
         with pytest.raises(ValueError, match=message):
             cow.dense_sdm_sparse_step(dense, **bad)
     assert (state.logical_to_physical == -1).all()

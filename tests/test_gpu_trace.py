@@ -1,10 +1,10 @@
 """GPU parity of decode traces: the persistent multi-step kernel (many
 steps per launch, forwarding rows between steps through LDS, first touches
-claiming rows with an atomic add) and device-counter launches must equal
-single-step launches and the oracle bit for bit, except that physical rows
-of first touches may be assigned in another order (as in the reference's
-proven kernel): the same logical rows are private, with the same values, the
-same set of physical rows and an identical free stack.
+taking the rows a plan pass listed for them) and device-counter launches
+must equal single-step launches and the oracle bit for bit, physical rows
+included, and the decode loop ``run`` must equal the reference's per-step
+loop (prepare_step_capacity(banks * W), then the step) in capacities,
+growth counters, free stacks and readings.
 """
 
 from __future__ import annotations
@@ -16,7 +16,8 @@ import torch
 import copy_on_write_sdm_amd as cow
 from copy_on_write_sdm_amd import _native as nat
 from copy_on_write_sdm_amd import synthetic
-from gpu_helpers import assert_state_equal, assert_states_match
+from gpu_helpers import (assert_state_equal, assert_states_identical, assert_states_match,
+                         oracle_decode_loop)
 from oracle import state as ref
 
 pytestmark = pytest.mark.gpu
@@ -98,9 +99,9 @@ def test_persistent_trace_matches_single_steps(device, layers, banks, slots, wid
     want = _per_step(single, routes, steps, layers)
     assert torch.equal(outputs, want)
     for a, b in zip(traced, single):
-        assert_states_match(a, b)
+        assert_states_identical(a, b)
         a.validate_invariants()
-    dense = [m0[l, 0].expand(banks, -1, -1).contiguous() for l in range(layers)]
+    dense = [m0[l, 0].expand(banks, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(layers)]
     dout = torch.empty_like(outputs)
     cow.DecodeTrace(memories=dense, outputs=dout, max_steps_per_launch=group,
                     **kw).launch(steps, start=0)
@@ -151,7 +152,7 @@ def test_invalid_routes_stop_only_their_bank(device, index_dtype):
     packed[1].logical_to_physical[1, x] = -1
 
     def dense_run(n):
-        tables = [m0[l, 0].expand(banks, -1, -1).contiguous() for l in range(layers)]
+        tables = [m0[l, 0].expand(banks, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(layers)]
         out = torch.zeros(steps, layers, banks, width, device=device)
         if n:
             cow.DecodeTrace(memories=tables, outputs=out, max_steps_per_launch=group,
@@ -187,7 +188,7 @@ def test_persistent_trace_matches_oracle(device):
         x = {k: v.cpu().numpy() for k, v in routes.step(s, 0).items()}
         want, _ = ref.packed_step(oracle, **x, validate_routes=False)
         assert np.array_equal(outputs[s, 0].cpu().numpy(), want), f"step {s}"
-    assert_state_equal(traced[0], oracle, permuted=True)
+    assert_state_equal(traced[0], oracle)
 
 
 @pytest.mark.parametrize("writes,reads,zero_values", [
@@ -249,7 +250,7 @@ def test_sticky_routes_forwarding(device, slots, reads, lag, index_dtype):
     want = _per_step(single, routes, steps, layers)
     assert torch.equal(outputs, want)
     for a, b in zip(traced, single):
-        assert_states_match(a, b)
+        assert_states_identical(a, b)
 
 
 @pytest.mark.parametrize("persistent", [True, False])
@@ -265,6 +266,7 @@ def test_device_counter_graph_replay(device, persistent):
     outputs = torch.empty(steps, layers, banks, 128, device=device)
     tr = cow.DecodeTrace(states=traced, outputs=outputs, persistent=persistent, **kw)
     layer_array = tr.layer_array()
+    tr.upload()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
         tr.launch(group, layer_array)
@@ -277,10 +279,11 @@ def test_device_counter_graph_replay(device, persistent):
     torch.cuda.synchronize()
     assert tr.step_index.tolist() == [steps] * layers
     assert tr.status.tolist() == [0] * layers
+    tr.sync()
     want = _per_step(single, routes, steps, layers)
     assert torch.equal(outputs, want)
     for a, b in zip(traced, single):
-        assert torch.equal(a.materialize_dense(), b.materialize_dense())
+        assert_states_identical(a, b)
         a.validate_invariants()
     before = outputs.clone()
     graph.replay()                     # past the end of the recorded steps
@@ -292,30 +295,36 @@ def test_device_counter_graph_replay(device, persistent):
         a.validate_invariants()
 
 
-@pytest.mark.parametrize("proof_steps,launch_steps", [(4, 64), (4, 8), (2, 6)])
-def test_device_proof_matches_host_proofs(device, proof_steps, launch_steps):
-    _device_proof_case(device, proof_steps, launch_steps, layers=3, banks=8, slots=64,
-                       width=128, steps=40, capacity=24, quantum=16, grows=True)
+@pytest.mark.parametrize("launch_steps,capacity,quantum", [
+    (64, 24, 16),    # growth every few steps, many growths per launch
+    (8, 24, 16),     # launches shorter than a growth's reach
+    (7, 40, 48),     # odd launch length, quantum above a step's need
+    (64, 512, 16),   # never short: one proof covers the run
+])
+def test_decode_loop_matches_reference_loop(device, launch_steps, capacity, quantum):
+    """run() against the reference's per-step loop on the oracle: the proof
+    counter, the free-count reads, every growth (events, rows added and
+    copied), capacities, maps, free stacks and readings are equal, with any
+    step count; both growth inside the slab's buffers (on the device) and
+    growth past them (on the host) occur."""
+
+    _decode_loop_case(device, launch_steps, layers=3, banks=8, slots=64, width=128,
+                      steps=37, capacity=capacity, quantum=quantum)
 
 
-def test_device_proof_long_launch(device):
-    """One launch of 400 steps over 4,096 slots with room for every slot: a
-    bank's first touches in the launch pass 1,024, so the proofs sum counts
-    of twelve bits."""
+def test_decode_loop_long_launch(device):
+    """One launch of 400 steps over 4,096 slots with room for every slot."""
 
-    states = _device_proof_case(device, 2, 400, layers=1, banks=4, slots=4096, width=64,
-                                steps=400, capacity=4 * 4096, quantum=256, grows=False)
+    states = _decode_loop_case(device, 400, layers=1, banks=4, slots=4096, width=64,
+                               steps=400, capacity=4 * 4096, quantum=256)
     assert int((states[0].logical_to_physical >= 0).sum(1).min()) > 1024
 
 
-def _device_proof_case(device, proof_steps, launch_steps, *, layers, banks, slots, width,
-                       steps, capacity, quantum, grows):
-    """run(): capacity proven on the device every proof_steps steps, a layer
-    stopped and grown when prepare_step_capacity would grow it, must leave
-    the same slabs, maps, free stacks, growth counters and readings as the
-    host loop that proves each group and then runs its single steps."""
-
+def _decode_loop_case(device, launch_steps, *, layers, banks, slots, width, steps, capacity,
+                      quantum, reserve=0):
     writes, reads = 4, 8
+    print(f"decode loop L={layers} B={banks} N={slots} S={steps} C={capacity} q={quantum} "
+          f"launch={launch_steps}", flush=True)
     m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=31, device=device)
     routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
                                   width=width, writes=writes, reads=reads, seed=32, device=device)
@@ -323,38 +332,109 @@ def _device_proof_case(device, proof_steps, launch_steps, *, layers, banks, slot
               values=routes.values, input_gate=routes.input_gate,
               forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
               read_weights=routes.read_weights)
-
-    def fresh():
-        return [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks,
-                                                       capacity_rows=capacity,
-                                                       growth_quantum_rows=quantum)
-                for l in range(layers)]
-
-    host, dev_states = fresh(), fresh()
-    want = torch.empty(steps, layers, banks, width, device=device)
-    need = banks * writes * proof_steps
-    for g in range(0, steps, proof_steps):
-        for st in host:
-            st.prepare_step_capacity(need)
-        for s in range(g, g + proof_steps):
-            for l in range(layers):
-                want[s, l], _ = cow.packed_sdm_cow_step(host[l], **routes.step(s, l),
-                                                        validate_routes=False,
-                                                        collect_diagnostics=False)
+    states = [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks, capacity_rows=capacity,
+                                                     growth_quantum_rows=quantum)
+              for l in range(layers)]
+    oracles = [ref.allocate(m0[l].cpu().numpy(), banks=banks, capacity_rows=capacity,
+                            growth_quantum_rows=quantum) for l in range(layers)]
     outputs = torch.empty(steps, layers, banks, width, device=device)
-    tr = cow.DecodeTrace(states=dev_states, outputs=outputs, **kw)
-    report = tr.run(steps, proof_steps=proof_steps, launch_steps=launch_steps)
+    tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
+    if reserve:
+        tr.reserve_steps(reserve)
+    # two runs split at an odd step: the second continues the first's proof
+    first = steps // 3 + 1
+    tr.run(first, launch_steps=launch_steps)
+    want = oracle_decode_loop(oracles, routes, first, need=banks * writes)
+    for st, orc in zip(states, oracles):
+        assert_state_equal(st, orc)
+    tr.run(steps - first, launch_steps=launch_steps)
+    want = np.concatenate(
+        [want, oracle_decode_loop(oracles, routes, steps - first, start=first,
+                                  need=banks * writes)])
     torch.cuda.synchronize()
-    assert (report["growth_rounds"] > 0) == grows
     assert tr.step_index.tolist() == [steps] * layers
-    assert torch.equal(outputs, want)
-    for a, b in zip(dev_states, host):
-        assert a.capacity_rows == b.capacity_rows
-        assert (a.growth_events, a.growth_rows_added, a.growth_rows_copied) == (
-            b.growth_events, b.growth_rows_added, b.growth_rows_copied)
-        assert_states_match(a, b)
-        a.validate_invariants()
-    return dev_states
+    assert np.array_equal(outputs.cpu().numpy(), want)
+    for st, orc in zip(states, oracles):
+        assert_state_equal(st, orc)
+        st.validate_invariants()
+    return states
+
+
+def test_decode_loop_grows_on_device_with_reserved_room(device):
+    """With the slab's buffers reserved for the run, every growth happens
+    inside the persistent launches (no host round) and still equals the
+    reference loop."""
+
+    layers, banks, slots, steps = 2, 16, 64, 60
+    m0 = synthetic.make_initial_memory(layers, 1, slots, 128, seed=5, device=device)
+    routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
+                                  width=128, writes=4, reads=16, seed=6, device=device)
+    kw = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+              values=routes.values, input_gate=routes.input_gate,
+              forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+              read_weights=routes.read_weights)
+    states = [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks, capacity_rows=64,
+                                                     growth_quantum_rows=64)
+              for l in range(layers)]
+    oracles = [ref.allocate(m0[l].cpu().numpy(), banks=banks, capacity_rows=64,
+                            growth_quantum_rows=64) for l in range(layers)]
+    outputs = torch.empty(steps, layers, banks, 128, device=device)
+    tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
+    tr.reserve_steps(steps)
+    report = tr.run(steps)
+    assert report == {"launches": 1, "growth_rounds": 0}
+    want = oracle_decode_loop(oracles, routes, steps, need=banks * 4)
+    assert np.array_equal(outputs.cpu().numpy(), want)
+    for st, orc in zip(states, oracles):
+        assert st.growth_events > 3
+        assert_state_equal(st, orc)
+        st.validate_invariants()
+
+
+def test_graph_replay_grows_on_device(device):
+    """A captured 5-step launch replayed with the decode loop's proof and
+    growth on the device: after sync(), the states equal the reference loop
+    and no replay needed the host."""
+
+    layers, banks, slots, steps, group = 2, 16, 64, 40, 5
+    m0 = synthetic.make_initial_memory(layers, 1, slots, 128, seed=8, device=device)
+    routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
+                                  width=128, writes=4, reads=16, seed=9, device=device)
+    kw = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+              values=routes.values, input_gate=routes.input_gate,
+              forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+              read_weights=routes.read_weights)
+    states = [cow.PackedSDMCopyOnWriteState.allocate(m0[l], banks=banks, capacity_rows=64,
+                                                     growth_quantum_rows=128)
+              for l in range(layers)]
+    oracles = [ref.allocate(m0[l].cpu().numpy(), banks=banks, capacity_rows=64,
+                            growth_quantum_rows=128) for l in range(layers)]
+    outputs = torch.empty(steps, layers, banks, 128, device=device)
+    tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
+    tr.reserve_steps(steps)
+    layer_array = tr.layer_array()
+    assert tr.planned
+    tr.upload()
+    tr.set_step(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=torch.cuda.Stream()):
+        tr.launch(group, layer_array)
+    for k in range(steps // group):
+        graph.replay()
+        if k % 3 == 1:
+            torch.cuda.synchronize()   # eager work between replays
+            assert tr.step_index.tolist() == [(k + 1) * group] * layers
+    torch.cuda.synchronize()
+    assert tr.step_index.tolist() == [steps] * layers
+    assert tr.status.tolist() == [0] * layers
+    tr.sync()
+    want = oracle_decode_loop(oracles, routes, steps, need=banks * 4)
+    assert np.array_equal(outputs.cpu().numpy(), want)
+    for st, orc in zip(states, oracles):
+        assert st.growth_events > 1
+        assert_state_equal(st, orc)
+        st.validate_invariants()
 
 
 def test_host_offsets_past_recorded_steps_raise(device):
