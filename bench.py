@@ -9,19 +9,25 @@ four decode steps (max(16, B*4*4) rows), then decode runs on the packed
 state.  One bench "step" is one decode token for all 7 layers and all B
 requests.
 
-Decode loop: persistent launches of up to 512 steps for every (layer, bank);
-before every 4 steps each packed layer proves on the device that its free
-rows cover the worst case (prepare_step_capacity(B*W*4) of the reference's
-decode loop); a layer that would not is stopped there, grown on the host by
-prepare_step_capacity itself, and resumed, so growth matches the host-proven
-loop exactly.  --config 3 (2,048-token prefill, packed handoff timed) and
---config 5 (4 heads, N = 65,536, Zipf routes, decode from an empty slab) run
-BASELINE's other single-GPU configurations; --batch sets B (1/16/64).
-W untimed warmup steps, then exactly K timed steps between
-synchronisations.  The dense-table control runs the same routes the same way
-from the same packed state; both end states must be equal.  The CPU baseline
-is the torch restatement of the reference's dense-table step on the host
-cores, on a bounded sample.
+Decode loop: the reference's (inference.py:538-566: prepare_step_capacity
+(B*W) before every step of every layer, then the fused step), run as
+persistent launches of up to 512 steps for every (layer, bank), each planned
+on the device first (count and plan passes: the per-step capacity proof,
+growth within the slab's buffers, the row of every first touch).  The slab
+buffers are sized for the run before timing, so growth happens inside the
+launches; the growth counters still follow the reference's formula.
+--config 3 (2,048-token prefill, packed handoff timed) and --config 5
+(4 heads, N = 65,536, Zipf routes, decode from an empty slab) run BASELINE's
+other single-GPU configurations; --batch sets B (1/16/64).
+
+Timing, as the reference's benchmark (5 warmup and 20 timed steps, median of
+5 repetitions, experiments/benchmark_serving.py:1002-1066): W untimed warmup
+steps, then 5 repetitions of exactly K steps, each between synchronisations;
+the median repetition is reported.  The dense-table control runs the same
+routes the same way from the same packed state; both end states must be
+equal.  The CPU baseline is the torch restatement of the reference's
+dense-table step on the host cores (all cores and one
+thread, and a bounded sample at this workload's shape).
 """
 
 from __future__ import annotations
@@ -62,6 +68,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=None, help="warmup steps (default: the config's)")
     p.add_argument("--batch", type=int, default=64)
     p.add_argument("--launch-steps", type=int, default=512, help="decode steps per launch")
+    p.add_argument("--repeats", type=int, default=5, help="timed repetitions (median reported)")
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget of the CPU baseline sample")
@@ -138,37 +145,79 @@ def algorithmic_bytes(banks: int, layers: int) -> int:
 
 
 def profiled_traffic(batch: int, launch_steps: float) -> dict | None:
-    """HBM bytes per launch of the packed decode kernel from the committed
+    """HBM bytes per launch of the packed decode kernels from the committed
     counter passes (FETCH_SIZE and WRITE_SIZE, scaled by a copy of known
-    size), when this run's launches ran the profiled number of steps."""
+    size), when this run's launches ran a profiled number of steps."""
 
     path = ROOT / "profiles" / "traffic_packed_trace_config2_b64.json"
     if not path.exists():
         return None
-    traffic = json.loads(path.read_text())
-    if traffic["batch"] != batch or traffic["steps_per_launch"] != launch_steps:
-        return None
-    return traffic
+    for entry in json.loads(path.read_text()).get("launches", []):
+        if entry["batch"] == batch and entry["steps_per_launch"] == launch_steps:
+            return entry
+    return None
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
-    """Time the torch restatement of the reference's dense-table CPU step
-    (allocator.py:1612-1633) at config 2's shape on the host cores."""
+    """The torch restatement of the reference's dense-table CPU step
+    (allocator.py:1612-1633, oracle/torch_port.py) on the host cores:
 
-    SLOTS = CONFIGS[2]["slots"]
+    * 1 layer, B=1, N=256, D=128, a 16-token prefill,
+      then 64 decode tokens timed; median of 5, on the box's CPU share and
+      on one thread;
+    * this workload's shape (L=7, N=256, D=128, batch ``batch``) for a
+      bounded sample of about ``budget_s`` seconds on the CPU share, the
+      like-for-like point reported as ``value``."""
+
+    import statistics
 
     import torch
 
     from copy_on_write_sdm_amd import synthetic
     from oracle import torch_port
 
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    share = min(16, os.cpu_count() or 1)
+    slots = CONFIGS[2]["slots"]
+
+    def config1(threads: int) -> dict:
+        torch.set_num_threads(threads)
+        times = []
+        for rep in range(5):
+            m0 = synthetic.make_initial_memory(1, 1, slots, WIDTH, seed=seed + rep)
+            steps = synthetic.make_steps(steps=16 + 64, layers=1, banks=1, slots=slots,
+                                         width=WIDTH, writes=WRITES, reads=READS,
+                                         seed=seed + 10 + rep)
+            table = m0[0, 0][None].clone()
+            for s in range(16):
+                torch_port.dense_step(table, **steps.step(s, 0))
+            t0 = time.perf_counter()
+            for s in range(16, 80):
+                torch_port.dense_step(table, **steps.step(s, 0))
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        return {"tokens_per_s": round(64 / t, 1), "us_per_token": round(1e6 * t / 64, 2),
+                "threads": torch.get_num_threads()}
+
+    config1_share = config1(share)
+    config1_one = config1(1)
+
+    torch.set_num_threads(share)
     steps = 48
-    m0 = synthetic.make_initial_memory(LAYERS, 1, SLOTS, WIDTH, seed=seed)
-    batch_inputs = synthetic.make_steps(steps=steps, layers=LAYERS, banks=batch, slots=SLOTS,
+    m0 = synthetic.make_initial_memory(LAYERS, 1, slots, WIDTH, seed=seed)
+    batch_inputs = synthetic.make_steps(steps=steps, layers=LAYERS, banks=batch, slots=slots,
                                         width=WIDTH, writes=WRITES, reads=READS, seed=seed + 1)
-    tables = [m0[l, 0].expand(batch, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(LAYERS)]
+    tables = [m0[l, 0].expand(batch, -1, -1).clone(memory_format=torch.contiguous_format)
+              for l in range(LAYERS)]
     for s in range(2):
         for l in range(LAYERS):
             torch_port.dense_step(tables[l], **batch_inputs.step(s, l))
@@ -185,12 +234,16 @@ def cpu_baseline(batch: int, budget_s: float, seed: int) -> dict:
     return {
         "value": round(batch * done / elapsed, 1),
         "unit": "tokens/s",
-        "cores": threads,
+        "cores": share,
         "kind": "port",
         "sample": (f"{done} decode steps of the torch dense-table restatement "
-                   f"(oracle/torch_port.py) at L={LAYERS} B={batch} N={SLOTS} D={WIDTH} "
-                   f"W={WRITES} R={READS}, {elapsed:.1f} s on {threads} threads "
-                   f"({platform.processor() or platform.machine()})"),
+                   f"(oracle/torch_port.py) at L={LAYERS} B={batch} N={slots} D={WIDTH} "
+                   f"W={WRITES} R={READS}, {elapsed:.1f} s on {share} threads"),
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "config1": {"workload": "1 layer, B=1, N=256, D=128, 16-token prefill, 64 decode "
+                                "tokens timed, median of 5",
+                    "cpu_share": config1_share, "one_thread": config1_one},
     }
 
 
@@ -202,6 +255,8 @@ def main() -> int:
         return 2
     if args.routes:
         return bench_routes(args.steps or 500)
+    import statistics
+
     import torch
 
     import ctypes
@@ -216,6 +271,10 @@ def main() -> int:
     B = args.batch
     K = cfg["steps"] if args.steps is None else args.steps
     Wm = cfg["warmup"] if args.warmup is None else args.warmup
+    repeats = max(1, args.repeats)
+    if K <= 0 or Wm < 0:
+        print("--steps must be positive and --warmup non-negative", file=sys.stderr)
+        return 2
     eager_steps = (32 if args.config == 2 else 0) if args.eager_steps is None else args.eager_steps
     banks = B * HEADS                       # bank = request * H + head
     templates = torch.arange(HEADS, dtype=torch.int64, device=dev).repeat(B)
@@ -224,7 +283,7 @@ def main() -> int:
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
-    total_steps = Wm + K
+    total_steps = Wm + repeats * K
     quantum = max(16, banks * WRITES * 4)
 
     # ---- prefill (dense kernel) and copy-on-write handoff, untimed except the
@@ -274,45 +333,56 @@ def main() -> int:
     dense_tables = [st.materialize_dense() for st in states]
     packed = cow.DecodeTrace(states=states, **inputs)
     dense = cow.DecodeTrace(memories=dense_tables, **inputs)
+    # pool sizing before timing: slab buffers with room for every step of
+    # the run, so that growth happens inside the launches
+    packed.reserve_steps(total_steps)
+    torch.cuda.synchronize()
 
     lib = nat.lib()
 
-    def kernel_ms() -> float:
-        """Summed duration of the trace kernels launched since timing was
-        switched on: HIP events the library records at each kernel's start
-        and end on its stream (hipExtLaunchKernel)."""
-        total, kernels = ctypes.c_double(), ctypes.c_int32()
-        nat.check(lib.cowsdm_trace_timing_read(ctypes.byref(total), ctypes.byref(kernels)),
-                  "trace timing")
-        return total.value
+    def launch_times() -> tuple[float, float, int]:
+        """Summed launch time (first kernel's start to the decode kernel's
+        end), summed decode-kernel time (ms) and launches since timing was
+        switched on: HIP events the library records on the launch stream."""
+        span, kernel, count = ctypes.c_double(), ctypes.c_double(), ctypes.c_int32()
+        nat.check(lib.cowsdm_trace_timing_read(ctypes.byref(span), ctypes.byref(kernel),
+                                               ctypes.byref(count)), "trace timing")
+        return span.value, kernel.value, count.value
+
+    def live_rows(trace) -> int:
+        return 0 if trace.dense else sum(int(st.allocated_rows_tensor()) for st in trace.tables)
 
     def measure(trace):
         trace.set_step(0)
-        # the warmup takes the same host path as the timed run, timing included
+        # the warmup takes the same host path as the timed runs, timing included
         lib.cowsdm_trace_timing(1)
         trace.run(Wm, launch_steps=args.launch_steps)
         torch.cuda.synchronize()
-        kernel_ms()
-        alloc0 = (sum(int(st.allocated_rows_tensor()) for st in trace.tables)
-                  if not trace.dense else 0)
-        grow0 = sum(st.growth_events for st in trace.tables) if not trace.dense else 0
-        lib.cowsdm_trace_timing(1)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        report = trace.run(K, launch_steps=args.launch_steps)
-        torch.cuda.synchronize()
-        seconds = time.perf_counter() - t0
-        gpu_ms = kernel_ms()
+        launch_times()
+        reps = []
+        for _ in range(repeats):
+            rows0 = live_rows(trace)
+            grow0 = 0 if trace.dense else sum(st.growth_events for st in trace.tables)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            report = trace.run(K, launch_steps=args.launch_steps)
+            torch.cuda.synchronize()
+            seconds = time.perf_counter() - t0
+            span_ms, kernel_ms, launches = launch_times()
+            reps.append(dict(
+                seconds=seconds, span_ms=span_ms, kernel_ms=kernel_ms, timed_launches=launches,
+                new_rows=live_rows(trace) - rows0,
+                growths=(0 if trace.dense else
+                         sum(st.growth_events for st in trace.tables) - grow0), **report))
         lib.cowsdm_trace_timing(0)
-        new_rows = ((sum(int(st.allocated_rows_tensor()) for st in trace.tables) - alloc0)
-                    if not trace.dense else 0)
-        grows = (sum(st.growth_events for st in trace.tables) - grow0) if not trace.dense else 0
-        return dict(seconds=seconds, gpu_ms=gpu_ms, new_rows=new_rows, growths=grows, **report)
+        return reps
 
-    p_run = measure(packed)
-    d_run = measure(dense)
-    p_seconds, d_seconds = p_run["seconds"], d_run["seconds"]
-    new_rows, timed_growths = p_run["new_rows"], p_run["growths"]
+    p_reps = measure(packed)
+    d_reps = measure(dense)
+    order = sorted(range(repeats), key=lambda r: p_reps[r]["seconds"])
+    p_med = p_reps[order[(repeats - 1) // 2]]
+    d_med = sorted(d_reps, key=lambda r: r["seconds"])[(repeats - 1) // 2]
+    p_seconds, d_seconds = p_med["seconds"], d_med["seconds"]
 
     # both paths ran identical routes from identical logical state
     state_diff = max(float((st.materialize_dense() - t).abs().max())
@@ -328,45 +398,52 @@ def main() -> int:
         "live_rows_after": sum(int(st.allocated_rows_tensor()) for st in states),
         "capacity_rows_after": sum(st.capacity_rows for st in states),
         "growth_events": sum(st.growth_events for st in states),
+        "growth_rows_added": sum(st.growth_rows_added for st in states),
         "growth_rows_copied": sum(st.growth_rows_copied for st in states),
-        "timed_growth_events": timed_growths,
-        "timed_growth_rounds": p_run["growth_rounds"],
+        "timed_growth_events": sum(r["growths"] for r in p_reps),
+        "timed_host_growth_rounds": sum(r["growth_rounds"] for r in p_reps),
+        "slab_buffer_rows": sum(packed._room(st) for st in states),
     }
 
     # ---- per-layer Python drop-in path (exact reference call pattern), on
-    # the decoded packed states once every check on them is done: a second
-    # set of states held through the timed region slowed the persistent
-    # decode by about 3 %
+    # the decoded packed states once every check on them is done
     eager = None
-    eager_states = states if eager_steps else None
-    if eager_states is not None:
+    if eager_steps:
         n = min(eager_steps, total_steps)
         for s in range(2):
             for l in range(LAYERS):
-                eager_states[l].prepare_step_capacity(banks * WRITES)
-                cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
+                states[l].prepare_step_capacity(banks * WRITES)
+                cow.packed_sdm_cow_step(states[l], **routes.step(s, l),
                                         validate_routes=False, collect_diagnostics=False)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for s in range(2, n):
             for l in range(LAYERS):
-                eager_states[l].prepare_step_capacity(banks * WRITES)
-                cow.packed_sdm_cow_step(eager_states[l], **routes.step(s, l),
+                states[l].prepare_step_capacity(banks * WRITES)
+                cow.packed_sdm_cow_step(states[l], **routes.step(s, l),
                                         validate_routes=False, collect_diagnostics=False)
         torch.cuda.synchronize()
         eager = B * (n - 2) / (time.perf_counter() - t0)
 
-    # one launch runs launch_steps steps of all layers; its algorithmic bytes
-    # are the per-step bytes times the steps it ran
-    launches = p_run["launches"]
-    launch_us = 1000.0 * p_run["gpu_ms"] / launches
-    bytes_per_launch = (algorithmic_bytes(banks, LAYERS) * K + 8 * new_rows) / launches
-    achieved = bytes_per_launch / (launch_us * 1e-6) / 1e9
-    dense_launch_us = 1000.0 * d_run["gpu_ms"] / d_run["launches"]
-    traffic = profiled_traffic(B, K / launches) if args.config == 2 else None
-    # the persistent variant that ran: full shape (W = 4, R = 16), one scan
-    # window up to 64 banks, slot map in LDS up to 4,096 slots
-    kernel = (f"sdm_trace_kernel<int, 2, false, true, {1 if banks <= 64 else 4}, "
+    # roofline of the dominant kernel, the persistent decode kernel: the
+    # algorithmic bytes of the steps the timed launches ran over its mean
+    # duration (HIP events at its own start and end); the count and plan
+    # passes that precede it in each launch are reported beside it
+    launches = sum(r["timed_launches"] for r in p_reps)
+    timed_steps = repeats * K
+    kernel_us = 1000.0 * sum(r["kernel_ms"] for r in p_reps) / launches
+    span_us = 1000.0 * sum(r["span_ms"] for r in p_reps) / launches
+    new_rows = sum(r["new_rows"] for r in p_reps)
+    bytes_per_launch = (algorithmic_bytes(banks, LAYERS) * timed_steps + 8 * new_rows) / launches
+    achieved = bytes_per_launch / (kernel_us * 1e-6) / 1e9
+    d_launches = sum(r["timed_launches"] for r in d_reps)
+    dense_kernel_us = 1000.0 * sum(r["kernel_ms"] for r in d_reps) / d_launches
+    steps_per_launch = timed_steps / launches
+    traffic = (profiled_traffic(B, steps_per_launch)
+               if args.config == 2 and args.launch_steps == 512 else None)
+    # the persistent variant that ran: full shape (W = 4, R = 16), at most 64
+    # banks per layer, slot map in LDS up to 4,096 slots
+    kernel = (f"sdm_trace_kernel<int, 2, false, true, {'true' if banks <= 64 else 'false'}, "
               f"{'true' if SLOTS <= 4096 else 'false'}>")
 
     result = {
@@ -384,6 +461,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
+        "repeats": repeats,
+        "repeat_tokens_per_s": [round(B * K / r["seconds"], 1) for r in p_reps],
         "config": {
             "workload": (f"config {args.config}: {cfg['text']}; L={LAYERS} H={HEADS} "
                          f"N={SLOTS} D={WIDTH} top-{WRITES} write / top-{READS} read "
@@ -391,8 +470,9 @@ def main() -> int:
             "batch": B, "heads": HEADS, "banks": banks, "layers": LAYERS, "slots": SLOTS,
             "width": WIDTH, "writes": WRITES, "reads": READS, "prefix": PREFIX,
             "distribution": cfg["distribution"],
-            "growth_quantum_rows": quantum, "steps_per_launch": args.launch_steps,
-            "capacity_proof": "the reference's per-step proof, planned on the device per launch",
+            "growth_quantum_rows": quantum, "max_steps_per_launch": args.launch_steps,
+            "capacity_proof": ("the reference's prepare_step_capacity(B*W) before every "
+                               "step, planned on the device per launch"),
             "launch": "persistent launches over all layers and banks",
             "parallelism": "single GPU",
         },
@@ -405,16 +485,19 @@ def main() -> int:
             "traffic": None if traffic is None else traffic["bytes_per_launch"],
             "traffic_source": None if traffic is None else traffic["source"],
             "kernel": f"{kernel} (packed, {LAYERS} layers x {banks} banks)",
-            "launch_us": round(launch_us, 3),
-            "steps_per_launch": round(K / launches, 3),
-            "us_per_step": round(1000.0 * p_run["gpu_ms"] / K, 4),
+            "kernel_us": round(kernel_us, 3),
+            "steps_per_launch": round(steps_per_launch, 3),
+            "us_per_step": round(kernel_us / steps_per_launch, 4),
             "algorithmic_bytes_per_launch": int(bytes_per_launch),
+            "launch_us_with_plan": round(span_us, 3),
+            "frac_with_plan": round(bytes_per_launch / (span_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
         },
         "dense_control": {
             "tokens_per_s": round(B * K / d_seconds, 1),
-            "launch_us": round(dense_launch_us, 3),
-            "us_per_step": round(1000.0 * d_run["gpu_ms"] / K, 4),
+            "kernel_us": round(dense_kernel_us, 3),
+            "us_per_step": round(dense_kernel_us * d_launches / timed_steps, 4),
             "packed_over_dense_latency": round(p_seconds / d_seconds, 4),
+            "packed_over_dense_kernel": round(span_us * launches / (dense_kernel_us * d_launches), 4),
             "state_max_abs_diff": state_diff,
         },
         "allocator": allocator,

@@ -190,7 +190,9 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_trace_persistent": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32]),
     "cowsdm_trace_timing": (_I32, [_I32]),
-    "cowsdm_trace_timing_read": (_I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I32)]),
+    "cowsdm_trace_timing_read": (
+        _I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+               ctypes.POINTER(_I32)]),
     "cowsdm_packed_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),
     "cowsdm_packed_step_layers": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),

@@ -1245,12 +1245,17 @@ class DecodeTrace:
         # counters, row 1 the int32 status words, rows 2.. the control words
         # of packed layers (word k of layer l at row 2 + k)
         self._report = torch.zeros(2 + nat.CTRL_WORDS, layers, dtype=torch.int64, device=device)
+        self._report_host = torch.empty(self._report.shape, dtype=torch.int64).pin_memory()
+        self._report_ready = torch.cuda.Event()
         self.step_index = self._report[0]
         self.status = self._report[1].view(torch.int32)[:layers]
         self.control = self._report[2:]
         self._upload_buf = (torch.zeros(nat.CTRL_WORDS, layers, dtype=torch.int64).pin_memory()
                             if not self.dense else None)
         self._uploaded = None   # event after the last upload's copy
+        self._device_signature = None   # control words the device holds (host view)
+        self._counters_seen = [(0, 0, 0)] * layers
+        self._status_clean = False      # every status word is known to be zero
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
@@ -1348,34 +1353,49 @@ class DecodeTrace:
 
         return self.banks * self.writes
 
-    def upload(self) -> None:
-        """Write the packed layers' control words from their states: the
+    def _signature(self) -> list[tuple[int, int, int, int, int]]:
+        """Per packed layer, the control words a launch reads from its state:
         proof counter, capacity, buffer rows, quantum and rows proven per step
         (zero for a layer without a growth quantum, whose decode makes no
-        proof), with the growth counters zeroed."""
+        proof)."""
+
+        need = self.need()
+        return [(st.proven_maximum_additional_allocations, st.capacity_rows, self._room(st),
+                 st.growth_quantum_rows, need if st.growth_quantum_rows > 0 else 0)
+                for st in self.tables]
+
+    def upload(self, *, force: bool = True) -> None:
+        """Write the packed layers' control words from their states and zero
+        the growth counters the launches add to.  With ``force`` false the
+        copy is skipped when the device already holds these words (it does
+        after a launch whose words were read back, unless a state changed on
+        the host since)."""
 
         if self.dense:
+            return
+        signature = self._signature()
+        if not force and signature == self._device_signature:
             return
         buf = self._upload_buf
         if self._uploaded is not None:
             self._uploaded.synchronize()   # the last upload has left the pinned buffer
         buf.zero_()
-        for l, st in enumerate(self.tables):
-            q = st.growth_quantum_rows
-            buf[nat.CTRL_PROVEN, l] = st.proven_maximum_additional_allocations
-            buf[nat.CTRL_CAPACITY, l] = st.capacity_rows
-            buf[nat.CTRL_ROOM, l] = self._room(st)
-            buf[nat.CTRL_QUANTUM, l] = q
-            buf[nat.CTRL_NEED, l] = self.need() if q > 0 else 0
+        for l, words in enumerate(signature):
+            for k, value in zip((nat.CTRL_PROVEN, nat.CTRL_CAPACITY, nat.CTRL_ROOM,
+                                 nat.CTRL_QUANTUM, nat.CTRL_NEED), words):
+                buf[k, l] = value
         self.control.copy_(buf, non_blocking=True)
         if self._uploaded is None:
             self._uploaded = torch.cuda.Event()
         self._uploaded.record()
+        self._device_signature = signature
+        self._counters_seen = [(0, 0, 0)] * len(self.tables)
 
     def _absorb(self, control_rows) -> None:
-        """Take a launch's control words (host lists, row k = word k of each
-        layer) into the states: proof counter, capacity (grown within the
-        buffers) and growth counters."""
+        """Take the control words read back after launches (host lists, row
+        k = word k of each layer) into the states: proof counter, capacity
+        (grown within the buffers) and the growth the launches added since
+        the last read (the device counters run from the last upload)."""
 
         for l, st in enumerate(self.tables):
             st.proven_maximum_additional_allocations = int(control_rows[nat.CTRL_PROVEN][l])
@@ -1383,22 +1403,30 @@ class DecodeTrace:
             if capacity != st.capacity_rows:
                 vbuf, fbuf = st.slab_buffers
                 st.values, st.free_rows = vbuf[:capacity], fbuf[:capacity]
-            st.growth_events += int(control_rows[nat.CTRL_EVENTS][l])
-            st.growth_rows_added += int(control_rows[nat.CTRL_ADDED][l])
-            st.growth_rows_copied += int(control_rows[nat.CTRL_COPIED][l])
+            counters = (int(control_rows[nat.CTRL_EVENTS][l]),
+                        int(control_rows[nat.CTRL_ADDED][l]),
+                        int(control_rows[nat.CTRL_COPIED][l]))
+            seen = self._counters_seen[l]
+            st.growth_events += counters[0] - seen[0]
+            st.growth_rows_added += counters[1] - seen[1]
+            st.growth_rows_copied += counters[2] - seen[2]
+            self._counters_seen[l] = counters
             if st.growth_quantum_rows > 0:
                 st.capacity_is_proven = True
+        # the launches change only the proof counter and the capacity
+        previous = self._device_signature
+        self._device_signature = (
+            self._signature() if previous is None else
+            [(st.proven_maximum_additional_allocations, st.capacity_rows) + tuple(old[2:])
+             for st, old in zip(self.tables, previous)])
 
     def sync(self) -> None:
         """Read the control words back into the states after ``launch``
-        calls (one synchronisation), and zero the growth counters the next
-        launches add to."""
+        calls (one synchronisation)."""
 
         if self.dense or not self.planned:
             return
-        control = self.control.tolist()
-        self._absorb(control)
-        self.control[nat.CTRL_EVENTS:nat.CTRL_COPIED + 1].zero_()
+        self._absorb(self.control.tolist())
         self._positions = None
 
     def reserve_steps(self, steps: int) -> None:
@@ -1438,6 +1466,7 @@ class DecodeTrace:
                 return
             layers = self.layer_array() if layers is None else layers
             stream = nat.stream_handle(self.device)
+            self._status_clean = False
             self.trace.step_index = None
             try:
                 done = 0
@@ -1453,6 +1482,7 @@ class DecodeTrace:
         layers = self.layer_array() if layers is None else layers
         stream = nat.stream_handle(self.device)
         self._positions = None
+        self._status_clean = False
         done = 0
         while done < steps:
             n = min(steps - done, self.max_steps_per_launch) if self.persistent else steps
@@ -1463,6 +1493,15 @@ class DecodeTrace:
         fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
         nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
                   "decode trace launch")
+
+    def _read_report(self) -> list:
+        """The report (step counters, status words, control words) as host
+        lists, copied through pinned memory once the stream reaches it."""
+
+        self._report_host.copy_(self._report, non_blocking=True)
+        self._report_ready.record()
+        self._report_ready.synchronize()
+        return self._report_host.tolist()
 
     def _fault(self, layers_at_fault) -> None:
         errors = [int(self.tables[l].ensure_scratch()[nat.SCRATCH_ERRORS].item())
@@ -1503,8 +1542,10 @@ class DecodeTrace:
         self.trace.steps_recorded = target
         self.trace.step_index = self.step_index.data_ptr()
         self.trace.first_step = 0
-        self.status.zero_()
-        self.upload()
+        if not self._status_clean:
+            self.status.zero_()
+        self._status_clean = False
+        self.upload(force=False)
         stream = nat.stream_handle(self.device)
         launches = rounds = 0
         remaining = steps
@@ -1522,7 +1563,7 @@ class DecodeTrace:
                     else:
                         self._call(layers, launch_steps, stream)
                     launches += 1
-                report = self._report.tolist()    # counters, status, control words
+                report = self._read_report()      # counters, status, control words
                 positions = report[0]
                 if not self.dense:
                     self._absorb(report[2:])
@@ -1534,6 +1575,7 @@ class DecodeTrace:
                     self._fault(faults)
                 behind = [l for l, p in enumerate(positions) if p < target]
                 if not behind:
+                    self._status_clean = not any(status)
                     break
                 refused = [l for l in behind if status[l] & nat.TRACE_REFUSED]
                 if self.dense or refused != behind:

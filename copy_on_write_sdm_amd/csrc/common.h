@@ -51,7 +51,7 @@ int32_t fail(int32_t code, const char* fmt, ...);
 int32_t launch_status(const char* where);
 // cowsdm_trace_timing: the start/stop events to record around the next
 // trace kernel launch, or false when timing is off (or its slots are full).
-bool trace_timing_events(hipEvent_t* start, hipEvent_t* stop);
+bool trace_timing_events(hipEvent_t* first, hipEvent_t* start, hipEvent_t* stop);
 const char* last_error();
 
 struct StepParams {

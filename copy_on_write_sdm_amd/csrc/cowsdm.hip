@@ -75,26 +75,36 @@ int32_t launch_status(const char* where) {
 
 const char* last_error() { return g_error; }
 
-// cowsdm_trace_timing: event pairs recorded at trace kernels' start and end
+// cowsdm_trace_timing: per persistent launch, events at its first kernel's
+// start, at its decode kernel's start and at the decode kernel's end
 namespace {
 constexpr int kTimingSlots = 1024;
 bool timing_on = false;
 int timing_used = 0;
 int timing_made = 0;
+hipEvent_t timing_first[kTimingSlots];
 hipEvent_t timing_start[kTimingSlots];
 hipEvent_t timing_stop[kTimingSlots];
 }  // namespace
 
-bool trace_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+bool trace_timing_events(hipEvent_t* first, hipEvent_t* start, hipEvent_t* stop) {
   if (!timing_on || timing_used >= kTimingSlots) return false;
   if (timing_used == timing_made) {
-    if (hipEventCreate(&timing_start[timing_made]) != hipSuccess) return false;
-    if (hipEventCreate(&timing_stop[timing_made]) != hipSuccess) {
-      (void)hipEventDestroy(timing_start[timing_made]);
+    hipEvent_t e[3];
+    int made = 0;
+    for (; made < 3; ++made) {
+      if (hipEventCreate(&e[made]) != hipSuccess) break;
+    }
+    if (made < 3) {
+      for (int i = 0; i < made; ++i) (void)hipEventDestroy(e[i]);
       return false;
     }
+    timing_first[timing_made] = e[0];
+    timing_start[timing_made] = e[1];
+    timing_stop[timing_made] = e[2];
     ++timing_made;
   }
+  *first = timing_first[timing_used];
   *start = timing_start[timing_used];
   *stop = timing_stop[timing_used];
   ++timing_used;
@@ -918,21 +928,26 @@ int32_t cowsdm_trace_timing(int32_t enable) {
   return 0;
 }
 
-int32_t cowsdm_trace_timing_read(double* total_ms, int32_t* kernels) {
-  if (!total_ms || !kernels) return fail(COWSDM_EARG, "trace timing: null argument");
-  double sum = 0.0;
+int32_t cowsdm_trace_timing_read(double* launch_ms, double* kernel_ms, int32_t* launches) {
+  if (!launch_ms || !kernel_ms || !launches) {
+    return fail(COWSDM_EARG, "trace timing: null argument");
+  }
+  double span = 0.0, kernel = 0.0;
   for (int i = 0; i < timing_used; ++i) {
-    float ms = 0.0f;
+    float a = 0.0f, b = 0.0f;
     hipError_t e = hipEventSynchronize(timing_stop[i]);
-    if (e == hipSuccess) e = hipEventElapsedTime(&ms, timing_start[i], timing_stop[i]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&a, timing_first[i], timing_stop[i]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&b, timing_start[i], timing_stop[i]);
     if (e != hipSuccess) {
       timing_used = 0;
-      return fail(static_cast<int32_t>(e), "trace timing: kernel %d: %s", i, hipGetErrorString(e));
+      return fail(static_cast<int32_t>(e), "trace timing: launch %d: %s", i, hipGetErrorString(e));
     }
-    sum += ms;
+    span += a;
+    kernel += b;
   }
-  *total_ms = sum;
-  *kernels = timing_used;
+  *launch_ms = span;
+  *kernel_ms = kernel;
+  *launches = timing_used;
   timing_used = 0;
   return 0;
 }

@@ -1409,14 +1409,15 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
   // stream, each with its per-layer words offset to its first layer.
   const int per_launch = cached.blocks / P.blocks_per_layer;
   if (per_launch <= 0) return 1;
-  // With timing on, one event pair spans the launch: the count pass's start
-  // (packed state) or the first kernel's, and the last kernel's end.
-  hipEvent_t start = nullptr, stop = nullptr;
-  if (!trace_timing_events(&start, &stop)) start = stop = nullptr;
+  // With timing on, events at the launch's first kernel's start (the count
+  // pass of packed state), at the decode kernel's start and at its end.
+  hipEvent_t first = nullptr, start = nullptr, stop = nullptr;
+  if (!trace_timing_events(&first, &start, &stop)) first = start = stop = nullptr;
   if constexpr (!DENSE) {
     // the plan of every layer's launch, before any of its steps run
-    if (int32_t e = launch_trace_plan<IDX>(P, stream, start)) return e;
-    start = nullptr;
+    if (int32_t e = launch_trace_plan<IDX>(P, stream, first)) return e;
+  } else if (first) {
+    (void)hipEventRecord(first, stream);   // (the decode kernel is the first)
   }
   auto launch = [&](StepParams* q, int grid, bool last) {
     void* args[] = {q};

@@ -46,6 +46,7 @@ constexpr int kCountWaves = 4;
 constexpr int kCountThreads = kWave * kCountWaves;
 constexpr int kCountChunks = kTraceMaxSteps / kCountThreads;   // 64-step chunks per wave
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanBatch = 16;   // plan words a plan thread loads at once
 constexpr int kIntMax = 0x7fffffff;
 
 // Fibonacci hash of a slot into a table of 2^bits entries.
@@ -119,6 +120,26 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
   int* const lmap = lds_dyn;                               // MAPLDS: slot map [N]
   int* const keys = lds_dyn;                               // hash: slot of each entry
   int* const fw = lds_dyn + (MAPLDS ? N : TS);             // first writing step
+  // every route index this thread checks, loaded before anything waits
+  // (lane = step: each load is its own cache line, so all of them are
+  // issued at once)
+  IDX wv[kCountChunks][kTraceMaxWrites];
+  IDX rv[kCountChunks][kTraceMaxReads];
+#pragma unroll
+  for (int k = 0; k < kCountChunks; ++k) {
+    const int t0 = (wave + k * kCountWaves) * kWave + lane;
+    const int t = t0 < G ? t0 : G - 1;
+    const IDX* const w = reinterpret_cast<const IDX*>(
+        static_cast<const char*>(L.write_indices) + (first + t) * P.trace_stride[0]) +
+        static_cast<int64_t>(bank) * W;
+    const IDX* const r = reinterpret_cast<const IDX*>(
+        static_cast<const char*>(L.read_indices) + (first + t) * P.trace_stride[6]) +
+        static_cast<int64_t>(bank) * R;
+#pragma unroll
+    for (int j = 0; j < kTraceMaxWrites; ++j) wv[k][j] = w[j < W ? j : W - 1];
+#pragma unroll
+    for (int i = 0; i < kTraceMaxReads; ++i) rv[k][i] = r[i < R ? i : R - 1];
+  }
   if (threadIdx.x == 0) {
     const int64_t tmpl = L.template_indices[bank];
     s_stop = (tmpl < 0 || tmpl >= P.templates) ? 0 : G;
@@ -148,6 +169,7 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
   int slot[kCountChunks][kTraceMaxWrites];
   uint32_t mapped[kCountChunks];
   int err[kCountChunks];
+#pragma unroll
   for (int k = 0; k < kCountChunks; ++k) {
     const int t = (wave + k * kCountWaves) * kWave + lane;
     mapped[k] = 0;
@@ -155,17 +177,11 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) slot[k][j] = -1;
     if (t >= G) continue;
-    const IDX* const w = reinterpret_cast<const IDX*>(
-        static_cast<const char*>(L.write_indices) + (first + t) * P.trace_stride[0]) +
-        static_cast<int64_t>(bank) * W;
-    const IDX* const r = reinterpret_cast<const IDX*>(
-        static_cast<const char*>(L.read_indices) + (first + t) * P.trace_stride[6]) +
-        static_cast<int64_t>(bank) * R;
     int e = 0;
 #pragma unroll
     for (int j = 0; j < kTraceMaxWrites; ++j) {
       if (j < W) {
-        const int64_t v = static_cast<int64_t>(w[j]);
+        const int64_t v = static_cast<int64_t>(wv[k][j]);
         if (v < 0 || v >= N) {
           e |= COWSDM_ERR_WRITE_INDEX;
         } else {
@@ -183,7 +199,7 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
 #pragma unroll
     for (int i = 0; i < kTraceMaxReads; ++i) {
       if (i < R) {
-        const int64_t v = static_cast<int64_t>(r[i]);
+        const int64_t v = static_cast<int64_t>(rv[k][i]);
         if (v < 0 || v >= N) {
           e |= COWSDM_ERR_READ_INDEX;
         } else if (MAPLDS && lmap[v] >= C) {
@@ -222,6 +238,7 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
   }
   __syncthreads();
   const int stop = s_stop;
+#pragma unroll
   for (int k = 0; k < kCountChunks; ++k) {
     const int t = (wave + k * kCountWaves) * kWave + lane;
     if (t == stop) atomicOr(&s_bits, err[k]);
@@ -229,6 +246,7 @@ __global__ __launch_bounds__(kCountThreads) void trace_count_kernel(StepParams P
 
   // ---- phase 2: each step's first-touch write lanes
   int32_t* const words = plan_words(P, layer_id) + static_cast<int64_t>(bank) * P.plan_steps;
+#pragma unroll
   for (int k = 0; k < kCountChunks; ++k) {
     const int t = (wave + k * kCountWaves) * kWave + lane;
     if (t >= G) continue;
@@ -316,11 +334,25 @@ __global__ __launch_bounds__(kPlanThreads) void trace_plan_kernel(StepParams P) 
   const int b0 = part < parts ? static_cast<int>(static_cast<int64_t>(B) * part / parts) : B;
   const int b1 = part < parts ? static_cast<int>(static_cast<int64_t>(B) * (part + 1) / parts) : B;
   const bool mine = part < parts && t < G;
+  // A thread's plan words are kPlanBatch independent loads at a time (a
+  // loop of dependent-looking loads would wait for each one in turn).
+  auto load_words = [&](int b, uint32_t (&w)[kPlanBatch]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPlanBatch; ++i) {
+      const int bi = b + i < b1 ? b + i : b1 - 1;
+      w[i] = static_cast<uint32_t>(words[static_cast<int64_t>(bi) * S + t]);
+    }
+  };
   {
     int sum = 0;
     if (mine) {
-      for (int b = b0; b < b1; ++b) {
-        sum += __popc((static_cast<uint32_t>(words[static_cast<int64_t>(b) * S + t]) >> kPlanMaskShift) & 15u);
+      for (int b = b0; b < b1; b += kPlanBatch) {
+        uint32_t w[kPlanBatch];
+        load_words(b, w);
+#pragma unroll
+        for (int i = 0; i < kPlanBatch; ++i) {
+          if (b + i < b1) sum += __popc((w[i] >> kPlanMaskShift) & 15u);
+        }
       }
     }
     s_part[tid] = sum;
@@ -426,13 +458,20 @@ __global__ __launch_bounds__(kPlanThreads) void trace_plan_kernel(StepParams P) 
   // ---- plan words: first touches before each (step, bank) in pop order
   if (mine) {
     int run = s_part[tid];
-    for (int b = b0; b < b1; ++b) {
-      int32_t* const w = words + static_cast<int64_t>(b) * S + t;
-      const uint32_t v = static_cast<uint32_t>(*w);
-      const int c = __popc((v >> kPlanMaskShift) & 15u);
-      *w = static_cast<int32_t>((v & ~kPlanBaseMask) | static_cast<uint32_t>(run));
-      run += c;
-      if (over && c > 0 && run <= vlen) atomicMax(&s_fit, run);
+    for (int b = b0; b < b1; b += kPlanBatch) {
+      uint32_t w[kPlanBatch];
+      load_words(b, w);
+#pragma unroll
+      for (int i = 0; i < kPlanBatch; ++i) {
+        if (b + i < b1) {
+          const uint32_t v = w[i];
+          const int c = __popc((v >> kPlanMaskShift) & 15u);
+          words[static_cast<int64_t>(b + i) * S + t] =
+              static_cast<int32_t>((v & ~kPlanBaseMask) | static_cast<uint32_t>(run));
+          run += c;
+          if (over && c > 0 && run <= vlen) atomicMax(&s_fit, run);
+        }
+      }
     }
   }
 

@@ -213,13 +213,15 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
 
 /* Kernel timing of persistent trace launches, for measurement (no
  * reference counterpart; one host thread): after cowsdm_trace_timing(1)
- * each trace kernel launch (up to 1,024) records HIP start and stop events
- * at the kernel's own start and end on its stream (hipExtLaunchKernel);
- * cowsdm_trace_timing_read waits for them, returns the summed kernel time
- * in milliseconds and the number of kernels, and forgets them.
- * cowsdm_trace_timing(0) stops recording. */
+ * each persistent trace launch (up to 1,024) records HIP events on its
+ * stream at the start of its first kernel (a packed launch's count pass), at
+ * the start of its decode kernel and at the decode kernel's end
+ * (hipExtLaunchKernel).  cowsdm_trace_timing_read waits for them, returns
+ * the summed launch time (first kernel's start to the decode kernel's end)
+ * and the summed decode-kernel time in milliseconds and the number of
+ * launches, and forgets them.  cowsdm_trace_timing(0) stops recording. */
 int32_t cowsdm_trace_timing(int32_t enable);
-int32_t cowsdm_trace_timing_read(double* total_ms, int32_t* kernels);
+int32_t cowsdm_trace_timing_read(double* launch_ms, double* kernel_ms, int32_t* launches);
 /* Bytes of lifecycle workspace for a ranking over `entries` map entries
  * (release / trim / append / pack handoff / invariant checks). */
 int64_t cowsdm_workspace_bytes(int64_t entries, int64_t capacity_rows);

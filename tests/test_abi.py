@@ -76,11 +76,12 @@ def test_argument_errors_return_codes_without_launching():
 def test_trace_timing_without_launches():
     lib = nat.lib()
     assert lib.cowsdm_trace_timing(1) == 0
-    total, kernels = ctypes.c_double(-1.0), ctypes.c_int32(-1)
-    assert lib.cowsdm_trace_timing_read(ctypes.byref(total), ctypes.byref(kernels)) == 0
-    assert (total.value, kernels.value) == (0.0, 0)
+    span, kernel, launches = ctypes.c_double(-1.0), ctypes.c_double(-1.0), ctypes.c_int32(-1)
+    assert lib.cowsdm_trace_timing_read(ctypes.byref(span), ctypes.byref(kernel),
+                                        ctypes.byref(launches)) == 0
+    assert (span.value, kernel.value, launches.value) == (0.0, 0.0, 0)
     assert lib.cowsdm_trace_timing(0) == 0
-    assert lib.cowsdm_trace_timing_read(None, None) == -1
+    assert lib.cowsdm_trace_timing_read(None, None, None) == -1
 
 
 def test_structure_layout_matches_header():

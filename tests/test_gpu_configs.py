@@ -219,8 +219,11 @@ def _config5(device, *, layers, steps, seed):
     traced, host = states(), states()
     outputs = torch.empty(steps, layers, banks, D, device=device)
     report = cow.DecodeTrace(states=traced, outputs=outputs, **kw).run(steps)
+    torch.cuda.synchronize()
+    print(f"config 5: persistent decode done ({report})", flush=True)
     want = _reference_loop(host, batch, steps=steps, layers=layers)
     torch.cuda.synchronize()
+    print("config 5: reference loop done", flush=True)
     assert torch.equal(outputs, want)
     del want
     for a, b in zip(traced, host):
@@ -236,6 +239,7 @@ def _config5(device, *, layers, steps, seed):
         cow.DecodeTrace(memories=[table], outputs=dense_out, **one).launch(steps, start=0)
         assert torch.equal(dense_out[:, 0], outputs[:, l]), l
         assert torch.equal(traced[l].materialize_dense(), table), l
+        print(f"config 5: dense layer {l} equal", flush=True)
         del table
     return report
 
