@@ -58,6 +58,7 @@ CTRL_FIT = 10
 CTRL_WORDS = 12
 
 ABI_VERSION = 5
+STATIC_SCAN_WORDS = 1 << 20   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
 SCRATCH_ERRORS = 3
@@ -197,6 +198,9 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_packed_step_layers": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), _P]),
     "cowsdm_packed_step_trace": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32,
+               _P]),
+    "cowsdm_packed_step_trace_static": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32,
                _P]),
     "cowsdm_dense_step": (_I32, [ctypes.POINTER(Layer), ctypes.POINTER(Shape), _P]),

@@ -1211,7 +1211,8 @@ class DecodeTrace:
 
     def __init__(self, *, states=None, memories=None, write_indices, write_weights, values,
                  input_gate, forget_log_gate, read_indices, read_weights, erase_gate=None,
-                 outputs=None, persistent: bool = True, max_steps_per_launch: int = 512):
+                 outputs=None, persistent: bool = True, max_steps_per_launch: int = 512,
+                 static_scan: bool = False):
         if (states is None) == (memories is None):
             raise ValueError("give exactly one of states or memories")
         self.dense = memories is not None
@@ -1277,12 +1278,17 @@ class DecodeTrace:
         self.trace.steps_recorded = steps
         self.scan = None
         self.planned = False
+        # static_scan: packed launches take their plan blocks from the
+        # library's own device memory (cowsdm_packed_step_trace_static) and
+        # this trace allocates nothing per launch
+        self.static_scan = bool(static_scan) and not self.dense
         if not self.dense and persistent:
             words = int(nat.lib().cowsdm_trace_scan_words(banks, self.writes,
                                                           self.max_steps_per_launch))
-            self.scan = torch.zeros(layers, max(words, 1), dtype=torch.int64, device=device)
-            self.trace.scan = self.scan.data_ptr()
-            self.trace.scan_words = self.scan.shape[1]
+            if not self.static_scan:
+                self.scan = torch.zeros(layers, max(words, 1), dtype=torch.int64, device=device)
+                self.trace.scan = self.scan.data_ptr()
+                self.trace.scan_words = self.scan.shape[1]
             self.trace.scan_steps = self.max_steps_per_launch
             self.trace.control_stride = layers
         self._layers = None
@@ -1490,7 +1496,10 @@ class DecodeTrace:
             done += n
 
     def _call(self, layers, steps, stream):
-        fn = nat.lib().cowsdm_dense_step_trace if self.dense else nat.lib().cowsdm_packed_step_trace
+        lib = nat.lib()
+        fn = (lib.cowsdm_dense_step_trace if self.dense else
+              lib.cowsdm_packed_step_trace_static if self.static_scan else
+              lib.cowsdm_packed_step_trace)
         nat.check(fn(layers, len(self.tables), self.shape, self.trace, steps, stream),
                   "decode trace launch")
 

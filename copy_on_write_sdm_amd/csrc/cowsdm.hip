@@ -32,6 +32,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
+
+#include <mutex>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -890,6 +892,42 @@ int32_t rank_apply(const RankSource& src, const Workspace& ws, const RankApply& 
   return launch_status("rank apply");
 }
 
+// ---- plan blocks in the library's own device memory
+// (cowsdm_packed_step_trace_static, for callers that cannot allocate)
+
+// The array's name is a host-side stand-in: host code uses the per-device
+// address hipGetSymbolAddress returns for it, never the name itself.
+static __device__ __align__(256) int64_t scratch[COWSDM_STATIC_SCAN_WORDS];
+
+namespace {
+constexpr int kStaticDevices = 64;
+std::mutex g_static_lock;
+int64_t* g_static_scan[kStaticDevices] = {};  // per device: the array's address there
+}  // namespace
+
+// The array's address on the current device, looked up once per device.
+int32_t static_scan(int64_t** out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return fail(static_cast<int32_t>(e), "static scan: %s", hipGetErrorString(e));
+  if (device < 0 || device >= kStaticDevices) {
+    return fail(COWSDM_ELIMIT, "static scan: device %d past the library's %d", device,
+                kStaticDevices);
+  }
+  std::lock_guard<std::mutex> hold(g_static_lock);
+  if (!g_static_scan[device]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      return fail(e != hipSuccess ? static_cast<int32_t>(e) : COWSDM_EARG,
+                  "static scan: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    }
+    g_static_scan[device] = static_cast<int64_t*>(ptr);
+  }
+  *out = g_static_scan[device];
+  return 0;
+}
+
 }  // namespace cowsdm_impl
 
 using namespace cowsdm_impl;
@@ -983,6 +1021,31 @@ int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
                                  int32_t steps, void* stream) {
   if (!trace) return fail(COWSDM_EARG, "trace is null");
   return run_step(layers, nlayers, shape, false, as_stream(stream), trace, steps);
+}
+
+int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nlayers,
+                                        const cowsdm_shape_t* shape,
+                                        const cowsdm_trace_t* trace, int32_t steps,
+                                        void* stream) {
+  if (!trace || !shape) return fail(COWSDM_EARG, "trace or shape is null");
+  if (trace->scan) {
+    return fail(COWSDM_EARG, "static trace: scan must be null (the library supplies it)");
+  }
+  cowsdm_trace_t t = *trace;
+  if (t.control) {
+    const int64_t per_layer = cowsdm_trace_scan_words(shape->banks, shape->writes, t.scan_steps);
+    if (per_layer < 0 || nlayers < 0 || t.scan_steps <= 0 ||
+        per_layer * nlayers > COWSDM_STATIC_SCAN_WORDS) {
+      return fail(COWSDM_ELIMIT,
+                  "static trace: %d layers of %lld plan words pass the library's %lld "
+                  "(fewer steps per launch or fewer layers per call)",
+                  nlayers, static_cast<long long>(per_layer),
+                  static_cast<long long>(COWSDM_STATIC_SCAN_WORDS));
+    }
+    if (int32_t e = static_scan(&t.scan)) return e;
+    t.scan_words = per_layer;
+  }
+  return run_step(layers, nlayers, shape, false, as_stream(stream), &t, steps);
 }
 
 int32_t cowsdm_dense_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,

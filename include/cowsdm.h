@@ -254,6 +254,22 @@ int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
                                  const cowsdm_trace_t* trace, int32_t steps,
                                  void* stream);
 
+/* cowsdm_packed_step_trace with the plan blocks in the library's own device
+ * memory: trace->scan must be null (scan_words is ignored).  No counterpart
+ * in the reference; for callers that cannot allocate device memory, such as
+ * code under HIP graph capture and serving loops that forbid allocation.  It
+ * allocates nothing: the plan blocks live in a static device array of
+ * COWSDM_STATIC_SCAN_WORDS int64 words on each GPU (8 MiB, held until the
+ * process ends), which limits a call to nlayers *
+ * cowsdm_trace_scan_words(banks, W, scan_steps) words (COWSDM_ELIMIT
+ * beyond).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other host threads) race. */
+#define COWSDM_STATIC_SCAN_WORDS (1ll << 20)
+int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nlayers,
+                                        const cowsdm_shape_t* shape,
+                                        const cowsdm_trace_t* trace, int32_t steps,
+                                        void* stream);
+
 /* Dense-table control step on values = memory [B, N, D].
  * Replaces _dense_sdm_sparse_step_triton, allocator.py:1322-1378 (kernel
  * 367-460), with the torch semantics of 1612-1633. */
