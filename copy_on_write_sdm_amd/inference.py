@@ -82,112 +82,137 @@ class FaithfulSDMDecodeState:
                               dtype=torch.int64)
         return self.positions
 
-    def _banks(self, sequences: torch.Tensor, heads: int) -> torch.Tensor:
-        return (sequences[:, None] * heads
-                + torch.arange(heads, device=self.device)[None, :]).flatten()
+    # Requests are named by their index in the batch; request r owns bank
+    # r * H + h of a layer with H memory heads.  Index lists are handled on
+    # the host (one read of the activity mask per call) and sent to the
+    # device once per layer as the bank list its state operation takes.
+
+    def _position_list(self) -> list[int]:
+        """Every live request's decode position, on the host."""
+
+        if self.positions is None:
+            return [self.position] * self.batch
+        return [int(p) for p in self.positions.tolist()]
+
+    def _heads(self, state: PackedSDMCopyOnWriteState, batch: int) -> int:
+        heads, rest = divmod(state.banks, batch)
+        if rest:
+            raise AssertionError("SDM serving banks do not divide by batch")
+        return heads
+
+    def _bank_list(self, requests: list[int], heads: int) -> torch.Tensor:
+        banks = [request * heads + head for request in requests for head in range(heads)]
+        return torch.tensor(banks, device=self.device, dtype=torch.int64)
+
+    def _requests_to_release(self, sequence_indices) -> list[int]:
+        """The requests a release names, in the order given, after checking
+        that they are distinct live requests of this batch."""
+
+        live = self.active_sequences.tolist()
+        if sequence_indices is None:
+            return [r for r, on in enumerate(live) if on]
+        if isinstance(sequence_indices, torch.Tensor):
+            named = sequence_indices.detach().to("cpu", torch.int64)
+        else:
+            named = torch.as_tensor(sequence_indices, dtype=torch.int64)
+        if named.ndim != 1:
+            raise ValueError("released sequence indices must be a vector")
+        requests = named.tolist()
+        if (len(set(requests)) != len(requests)
+                or any(not 0 <= r < len(live) or not live[r] for r in requests)):
+            raise ValueError("released sequence is invalid, duplicated, or inactive")
+        return requests
 
     @torch.no_grad()
     def release(self, sequence_indices: torch.Tensor | Sequence[int] | None = None) -> int:
-        """Release completed requests from every SDM layer; their rows return
-        to each layer's shared slab (inference.py:71-114)."""
+        """Return the rows of finished requests to every SDM layer's shared
+        slab (inference.py:71-114): all live requests when none are named.
+        Their batch slots stay until ``compact``.  Returns the rows freed."""
 
-        if sequence_indices is None:
-            selected = self.active_sequences.nonzero().flatten()
-        else:
-            selected = torch.as_tensor(sequence_indices, device=self.device,
-                                       dtype=torch.int64)
-        if selected.ndim != 1:
-            raise ValueError("released sequence indices must be a vector")
-        if selected.numel() == 0:
+        requests = self._requests_to_release(sequence_indices)
+        if not requests:
             return 0
-        ordered = selected.sort().values
-        if (
-            bool((selected < 0).any())
-            or bool((selected >= self.batch).any())
-            or (ordered.numel() > 1 and bool((ordered[1:] == ordered[:-1]).any()))
-            or not bool(self.active_sequences[selected].all())
-        ):
-            raise ValueError("released sequence is invalid, duplicated, or inactive")
-        released = 0
+        freed = 0
         for state in self.sdm_states:
-            if state.banks % self.batch:
-                raise AssertionError("SDM serving banks do not divide by batch")
-            heads = state.banks // self.batch
-            released += int(state.release(self._banks(selected, heads)))
-        self.active_sequences[selected] = False
-        return released
+            banks = self._bank_list(requests, self._heads(state, self.batch))
+            freed += int(state.release(banks))
+        mask = torch.ones(self.batch, dtype=torch.bool)
+        mask[requests] = False
+        self.active_sequences &= mask.to(self.device)
+        return freed
 
     @torch.no_grad()
     def compact(self) -> torch.Tensor:
-        """Drop released request slots; live rows never move
-        (inference.py:116-159).  Returns the retained former indices."""
+        """Close the batch slots of released requests (inference.py:116-159):
+        survivors keep their order, their rows stay where they are in the
+        slabs, and each layer's map and template rows (and dense K/V batch
+        rows) are renumbered.  Returns the survivors' former indices."""
 
-        previous_batch = self.batch
-        retained = self.active_sequences.nonzero().flatten()
-        positions = self.current_positions()
+        live = self.active_sequences.tolist()
+        kept = [r for r, on in enumerate(live) if on]
         for state in self.sdm_states:
-            if previous_batch == 0:
-                if state.banks != 0:
+            if not live:
+                if state.banks:
                     raise AssertionError("empty serving batch retained SDM banks")
                 continue
-            if state.banks % previous_batch:
-                raise AssertionError("SDM serving banks do not divide by batch")
-            heads = state.banks // previous_batch
-            state.retain_banks(self._banks(retained, heads))
-        self.dense_keys = tuple(row[retained].contiguous() for row in self.dense_keys)
-        self.dense_values = tuple(row[retained].contiguous() for row in self.dense_values)
-        retained_positions = positions[retained].contiguous()
-        self.positions = retained_positions if self.positions is not None else None
-        self.active_sequences = torch.ones(retained.numel(), device=self.device,
-                                           dtype=torch.bool)
-        self.position = int(retained_positions.max().item()) if retained.numel() else 0
-        return retained
+            state.retain_banks(self._bank_list(kept, self._heads(state, len(live))))
+        index = torch.tensor(kept, device=self.device, dtype=torch.int64)
+        self.dense_keys = tuple(t.index_select(0, index).contiguous() for t in self.dense_keys)
+        self.dense_values = tuple(t.index_select(0, index).contiguous()
+                                  for t in self.dense_values)
+        if self.positions is None:
+            # one shared position: it stays, unless no request survives
+            self.position = self.position if kept else 0
+        else:
+            survivors = self.positions.index_select(0, index).contiguous()
+            self.positions = survivors
+            self.position = int(survivors.max()) if kept else 0
+        self.active_sequences = torch.ones(len(kept), device=self.device, dtype=torch.bool)
+        return index
 
     @torch.no_grad()
     def admit(self, incoming: "FaithfulSDMDecodeState") -> int:
-        """Admit a prefilled cohort into the same pooled slabs
-        (inference.py:161-206)."""
+        """Append a prefilled cohort to this batch (inference.py:161-206):
+        both batches are compacted, every SDM layer takes the cohort's banks
+        into its pooled slab, and the decode positions are merged (one shared
+        position when they agree).  Returns the requests admitted."""
 
         self.compact()
         incoming.compact()
-        if (
-            self.layout != incoming.layout
-            or self.capacity != incoming.capacity
-            or self.activation_dtype != incoming.activation_dtype
-            or self.device != incoming.device
-            or self.sdm_layer_positions != incoming.sdm_layer_positions
-            or len(self.sdm_states) != len(incoming.sdm_states)
-            or len(self.dense_keys) != len(incoming.dense_keys)
-        ):
+        same = (self.layout == incoming.layout and self.capacity == incoming.capacity
+                and self.activation_dtype == incoming.activation_dtype
+                and self.device == incoming.device
+                and self.sdm_layer_positions == incoming.sdm_layer_positions
+                and len(self.sdm_states) == len(incoming.sdm_states)
+                and len(self.dense_keys) == len(incoming.dense_keys))
+        if not same:
             raise ValueError("admitted faithful-SDM state is incompatible")
-        admitted = incoming.batch
-        for destination, source in zip(self.sdm_states, incoming.sdm_states):
-            destination.append_banks_from(source)
-        self.dense_keys = tuple(torch.cat((a, b), dim=0).contiguous()
+        for mine, theirs in zip(self.sdm_states, incoming.sdm_states):
+            mine.append_banks_from(theirs)
+        self.dense_keys = tuple(torch.cat((a, b)).contiguous()
                                 for a, b in zip(self.dense_keys, incoming.dense_keys))
-        self.dense_values = tuple(torch.cat((a, b), dim=0).contiguous()
+        self.dense_values = tuple(torch.cat((a, b)).contiguous()
                                   for a, b in zip(self.dense_values, incoming.dense_values))
-        admitted_positions = torch.cat(
-            (self.current_positions(), incoming.current_positions()), dim=0).contiguous()
-        if admitted_positions.numel() and bool(
-                (admitted_positions == admitted_positions[0]).all()):
-            self.position = int(admitted_positions[0].item())
-            self.positions = None
+        merged = self._position_list() + incoming._position_list()
+        if merged and min(merged) == max(merged):
+            self.position, self.positions = merged[0], None
         else:
-            self.positions = admitted_positions
-        self.active_sequences = torch.ones(admitted_positions.numel(), device=self.device,
-                                           dtype=torch.bool)
-        if admitted_positions.numel() and self.positions is not None:
-            self.position = int(admitted_positions.max().item())
-        return admitted
+            self.positions = torch.tensor(merged, device=self.device, dtype=torch.int64)
+            if merged:
+                self.position = max(merged)
+        self.active_sequences = torch.ones(len(merged), device=self.device, dtype=torch.bool)
+        return incoming.batch
 
     @torch.no_grad()
     def trim_sdm_pools(self, *, headroom_rows: int = 0) -> int:
-        """Return unused slab rows after a lifecycle transition
-        (inference.py:208-215)."""
+        """Shrink every SDM layer's slab to its live rows plus headroom after
+        a lifecycle transition (inference.py:208-215).  Returns the rows
+        removed."""
 
-        return sum(state.trim_capacity(headroom_rows=headroom_rows)
-                   for state in self.sdm_states)
+        removed = 0
+        for state in self.sdm_states:
+            removed += state.trim_capacity(headroom_rows=headroom_rows)
+        return removed
 
     @torch.no_grad()
     def release_and_compact(
@@ -197,13 +222,14 @@ class FaithfulSDMDecodeState:
         trim: bool = False,
         trim_headroom_rows: int = 0,
     ) -> int:
-        """Release, compact survivors and optionally trim (inference.py:217-231)."""
+        """``release``, ``compact`` and, with ``trim``, ``trim_sdm_pools``
+        (inference.py:217-231).  Returns the rows released."""
 
-        released = self.release(sequence_indices)
+        freed = self.release(sequence_indices)
         self.compact()
         if trim:
             self.trim_sdm_pools(headroom_rows=trim_headroom_rows)
-        return released
+        return freed
 
     def storage_bytes(self) -> dict[str, int]:
         """Private live/reserved SDM state, shared M0 and dense K/V
