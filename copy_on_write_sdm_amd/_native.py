@@ -58,7 +58,7 @@ CTRL_FIT = 10
 CTRL_WORDS = 12
 
 ABI_VERSION = 5
-STATIC_SCAN_WORDS = 1 << 20   # COWSDM_STATIC_SCAN_WORDS
+STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
 SCRATCH_ERRORS = 3

@@ -31,14 +31,26 @@ constexpr int kTraceMapSlots = 4096;        // largest N whose slot maps are sta
 constexpr int kTraceBanksPerBlock = 2;      // banks per persistent workgroup
 constexpr int kTraceThreads = 2 * kWave * kTraceBanksPerBlock;  // a control and a data wave per bank
 constexpr int kTraceRing = 16;              // steps handed from control to data wave in flight
-// Plan word of a (step, bank) in a packed decode trace's scan block: bits
-// 0-23 the first touches of the launch before it (step-major, bank-major
-// within a step), bits 24-27 its first-touch write lanes, bit 28 set from the
-// bank's first step with an invalid route on.
+// Plan word of a (step, bank) as the control wave stages it for its steps:
+// bits 0-23 the first touches of the launch before it (step-major,
+// bank-major within a step), bits 24-27 its first-touch write lanes, bit 28
+// set from the bank's first step with an invalid route on.
 constexpr uint32_t kPlanBaseMask = (1u << 24) - 1;
 constexpr int kPlanMaskShift = 24;
 constexpr int kPlanStopBit = 28;
-
+// Words a packed launch's plan exchanges between workgroups are 64-bit, the
+// launch's epoch in the high half and the value in the low half: a reader
+// polls a word until it carries the current epoch, so no fence orders one
+// word against another.  Count words (value: bits 0-3 the first-touch write
+// lanes, bit 4 the stop bit) become prefix words once the first touches of
+// lower banks at the same step are known (bits 5-28, bit 31 set).
+constexpr uint32_t kCountStop = 1u << 4;
+constexpr int kPrefixShift = 5;
+constexpr uint32_t kPrefixDone = 1u << 31;
+constexpr int kPlanHead = 8;        // header words (tagged): steps, fit, capacity
+constexpr int kPlanHeadWords = 8;
+constexpr int kPlanSegments = kTraceMaxSteps + 1;   // growth segments of one launch
+constexpr uint32_t kPlanReady = 1u << 31;            // the plan's steps are in a sync word
 constexpr uint32_t kStatusEmpty = 0;
 constexpr uint32_t kStatusAggregate = 1;
 constexpr uint32_t kStatusInclusive = 2;
@@ -52,6 +64,9 @@ int32_t launch_status(const char* where);
 // cowsdm_trace_timing: the start/stop events to record around the next
 // trace kernel launch, or false when timing is off (or its slots are full).
 bool trace_timing_events(hipEvent_t* first, hipEvent_t* start, hipEvent_t* stop);
+// the launch whose events trace_timing_events just gave out has no kernel
+// before its decode kernel: its launch time is the decode kernel's
+void trace_timing_first_is_start();
 const char* last_error();
 
 struct StepParams {
@@ -144,13 +159,48 @@ __device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
          (static_cast<uint64_t>(status) << 30) | (value & kValueMask);
 }
 
-// A packed decode trace layer's plan block: plan words [banks][plan_steps]
-// (int32), then the rows the launch's first touches pop, in pop order.
-__device__ __forceinline__ int32_t* plan_words(const StepParams& P, int layer) {
-  return reinterpret_cast<int32_t*>(P.scan + static_cast<int64_t>(layer) * P.scan_words);
+// A packed decode trace layer's plan block (int64 words; S = plan_steps,
+// B = banks, W = writes): the epoch, the header, the plan words [B][S]
+// (bank-major: a bank's words of consecutive steps are contiguous), the step
+// totals [S], the running totals [S + 1] and the pops [S * B * W].
+struct PlanBlock {
+  int64_t* epoch;
+  int64_t* head;
+  int64_t* words;
+  int64_t* totals;
+  int64_t* cum;
+  int64_t* pops;
+  int64_t steps;   // S
+  __device__ int64_t* word(int bank, int t) const {
+    return words + static_cast<int64_t>(bank) * steps + t;
+  }
+};
+__device__ __forceinline__ PlanBlock plan_block(const StepParams& P, int layer) {
+  int64_t* const b = P.scan + static_cast<int64_t>(layer) * P.scan_words;
+  const int64_t S = P.plan_steps;
+  PlanBlock pb;
+  pb.epoch = b;
+  pb.head = b + kPlanHead;
+  pb.words = pb.head + kPlanHeadWords;
+  pb.totals = pb.words + S * P.banks;
+  pb.cum = pb.totals + S;
+  pb.pops = pb.cum + S + 1;
+  pb.steps = S;
+  return pb;
 }
-__device__ __forceinline__ int32_t* plan_pops(const StepParams& P, int layer) {
-  return plan_words(P, layer) + static_cast<int64_t>(P.banks) * P.plan_steps;
+// The tag of a layer's words in the launch now starting: one past the epoch
+// word, which the layer's last control wave sets to it when the launch ends.
+// Never 0, so that zeroed memory carries no valid word.
+__device__ __forceinline__ uint32_t launch_epoch(const PlanBlock& pb) {
+  const uint32_t e = static_cast<uint32_t>(__hip_atomic_load(
+      const_cast<int64_t*>(pb.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  return e == 0 ? 1u : e;
+}
+__device__ __forceinline__ uint64_t tagged(uint32_t epoch, uint32_t value) {
+  return (static_cast<uint64_t>(epoch) << 32) | value;
+}
+__device__ __forceinline__ bool tag_is(uint64_t w, uint32_t epoch) {
+  return static_cast<uint32_t>(w >> 32) == epoch;
 }
 __device__ __forceinline__ int64_t& control_word(const StepParams& P, int layer, int k) {
   return P.control[static_cast<int64_t>(k) * P.control_stride + layer];

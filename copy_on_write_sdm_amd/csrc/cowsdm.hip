@@ -87,6 +87,7 @@ int timing_made = 0;
 hipEvent_t timing_first[kTimingSlots];
 hipEvent_t timing_start[kTimingSlots];
 hipEvent_t timing_stop[kTimingSlots];
+bool timing_single[kTimingSlots];   // the decode kernel is the launch's first
 }  // namespace
 
 bool trace_timing_events(hipEvent_t* first, hipEvent_t* start, hipEvent_t* stop) {
@@ -109,8 +110,13 @@ bool trace_timing_events(hipEvent_t* first, hipEvent_t* start, hipEvent_t* stop)
   *first = timing_first[timing_used];
   *start = timing_start[timing_used];
   *stop = timing_stop[timing_used];
+  timing_single[timing_used] = false;
   ++timing_used;
   return true;
+}
+
+void trace_timing_first_is_start() {
+  if (timing_used > 0) timing_single[timing_used - 1] = true;
 }
 
 // Validation before a step (validate_routes=True, or a packed state whose
@@ -789,7 +795,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
         trace->scan_words < cowsdm_trace_scan_words(shape->banks, shape->writes, trace->scan_steps)) {
       return fail(COWSDM_EARG, "trace: control words need scan blocks of scan_steps steps");
     }
-    if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
+    if (!trace->ticket) return fail(COWSDM_EARG, "trace: planned launches need the ticket words");
     launch_steps = trace->scan_steps;
   }
   const bool persistent = trace && trace->persistent && steps > 0 && trace_vec &&
@@ -903,10 +909,23 @@ namespace {
 constexpr int kStaticDevices = 64;
 std::mutex g_static_lock;
 int64_t* g_static_scan[kStaticDevices] = {};  // per device: the array's address there
+// per device: the layout (banks, W, steps per launch, layers) of the last
+// call, whose plan blocks the array holds
+struct StaticLayout {
+  int64_t banks = -1, writes = -1, steps = -1, layers = -1;
+  bool operator==(const StaticLayout& o) const {
+    return banks == o.banks && writes == o.writes && steps == o.steps && layers == o.layers;
+  }
+};
+StaticLayout g_static_layout[kStaticDevices];
 }  // namespace
 
 // The array's address on the current device, looked up once per device.
-int32_t static_scan(int64_t** out) {
+// When the call's layout differs from the last call's on this device, the
+// words it will use are zeroed first (a fill kernel on `stream`): words left
+// by another layout could otherwise pass for this one's epoch words.
+int32_t static_scan(int64_t** out, const StaticLayout& layout, int64_t words,
+                    hipStream_t stream) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return fail(static_cast<int32_t>(e), "static scan: %s", hipGetErrorString(e));
@@ -925,6 +944,12 @@ int32_t static_scan(int64_t** out) {
     g_static_scan[device] = static_cast<int64_t*>(ptr);
   }
   *out = g_static_scan[device];
+  if (!(g_static_layout[device] == layout)) {
+    hipLaunchKernelGGL(zero_i64_kernel, dim3(grid_for(words, 256)), dim3(256), 0, stream,
+                       *out, words);
+    if (int32_t e = launch_status("static scan clear")) return e;
+    g_static_layout[device] = layout;
+  }
   return 0;
 }
 
@@ -955,9 +980,9 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
 
 int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
   if (banks < 0 || writes < 0 || steps < 0) return -1;
-  // plan words [banks][steps] and the launch's pops (at most banks * W per
-  // step), int32 each
-  return (banks * steps * (1 + writes) + 1) / 2;
+  // epoch and header, plan words [steps][banks], step totals, running totals
+  // and the launch's pops (at most banks * W per step), int64 each
+  return kPlanHead + kPlanHeadWords + banks * steps + steps + (steps + 1) + banks * steps * writes;
 }
 
 int32_t cowsdm_trace_timing(int32_t enable) {
@@ -974,8 +999,11 @@ int32_t cowsdm_trace_timing_read(double* launch_ms, double* kernel_ms, int32_t* 
   for (int i = 0; i < timing_used; ++i) {
     float a = 0.0f, b = 0.0f;
     hipError_t e = hipEventSynchronize(timing_stop[i]);
-    if (e == hipSuccess) e = hipEventElapsedTime(&a, timing_first[i], timing_stop[i]);
     if (e == hipSuccess) e = hipEventElapsedTime(&b, timing_start[i], timing_stop[i]);
+    if (e == hipSuccess) {
+      a = b;
+      if (!timing_single[i]) e = hipEventElapsedTime(&a, timing_first[i], timing_stop[i]);
+    }
     if (e != hipSuccess) {
       timing_used = 0;
       return fail(static_cast<int32_t>(e), "trace timing: launch %d: %s", i, hipGetErrorString(e));
@@ -1042,7 +1070,12 @@ int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nl
                   nlayers, static_cast<long long>(per_layer),
                   static_cast<long long>(COWSDM_STATIC_SCAN_WORDS));
     }
-    if (int32_t e = static_scan(&t.scan)) return e;
+    StaticLayout layout;
+    layout.banks = shape->banks;
+    layout.writes = shape->writes;
+    layout.steps = t.scan_steps;
+    layout.layers = nlayers;
+    if (int32_t e = static_scan(&t.scan, layout, per_layer * nlayers, as_stream(stream))) return e;
     t.scan_words = per_layer;
   }
   return run_step(layers, nlayers, shape, false, as_stream(stream), &t, steps);

@@ -49,6 +49,7 @@
 #include <hip/hip_ext.h>
 
 #include "common.h"
+#include "trace_plan.h"
 
 namespace cowsdm_impl {
 
@@ -215,8 +216,9 @@ void sdm_trace_kernel(StepParams P) {
   __shared__ TraceSlot lds_ring[NB][kTraceRing];
   // [0]: control -> data, (stop step << 16) | steps whose row addresses are
   // published (the masks and store rows of all but the last of them);
-  // [1]: data -> control, steps computed
-  __shared__ uint32_t lds_sync[NB][2];
+  // [1]: data -> control, steps computed; [2]: control -> data, packed:
+  // kPlanReady | the steps the launch's plan lets the bank run
+  __shared__ uint32_t lds_sync[NB][3];
   // control wave: the slots of two 64-step chunks, per step W write slots
   // then R read slots (-1: outside [0, N)) and the step's four class words,
   // staged from registers a chunk ahead (map in LDS, or dense)
@@ -225,8 +227,10 @@ void sdm_trace_kernel(StepParams P) {
   __shared__ __align__(16) int lds_idx[(DENSE || MAPLDS) ? NB : 1][2][kWave][kIdxLds];
   // control wave (packed): the plan words of two 64-step chunks, staged from
   // registers a chunk ahead
-  __shared__ int lds_plan[DENSE ? 1 : NB][2][kWave];
-  // map in LDS (dynamic, 2 banks x N ints): each bank's slot map
+  __shared__ int lds_plan[DENSE ? 1 : NB][DENSE ? 1 : kTraceMaxSteps];
+  // map in LDS (dynamic, 2 banks x 2 x N ints): each bank's slot map, then
+  // each bank's first step of the launch writing each slot (the count part
+  // of the launch's plan)
   extern __shared__ int lds_map_all[];
 
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
@@ -264,24 +268,20 @@ void sdm_trace_kernel(StepParams P) {
     }
     return;  // whole workgroup
   }
-  if constexpr (!DENSE) {
-    // the steps the plan lets the layer run (it stops a layer before a
-    // growth its slab buffers cannot hold)
-    const int64_t planned = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
-        static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_STEPS))));
-    left = planned < left ? planned : left;
-    if (left <= 0) return;  // whole workgroup: the plan set the layer's status
-  }
-
   const int N = P.slots;
   const int D = P.width;
   const int W = FULL ? kTraceMaxWrites : P.writes;
   const int R = FULL ? kTraceMaxReads : P.reads;
   const int B = P.banks;
-  const int G = static_cast<int>(left);
-  // the capacity the launch grows to (rows are int32)
-  const int C = DENSE ? 0 : pin(__builtin_amdgcn_readfirstlane(
-                                static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_CAPACITY))));
+  // steps of this launch: G0 before the plan; the plan may stop a packed
+  // layer earlier (before a growth its slab buffers cannot hold), G
+  const int G0 = static_cast<int>(left);
+  int G = G0;
+  // slab capacity (rows are int32): at launch start, then the capacity the
+  // launch's plan grows the slab to
+  const int C0 = DENSE ? 0 : pin(__builtin_amdgcn_readfirstlane(
+                                 static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_CAPACITY))));
+  int C = C0;
   // lanes past the row width repeat the last columns: they load, compute and
   // store exactly what the last full lane does, so no access needs a lane mask
   const int col = lane * VEC < D ? lane * VEC : D - VEC;
@@ -292,6 +292,7 @@ void sdm_trace_kernel(StepParams P) {
   if (lane == 0 && !data_wave) {
     lds_sync[pair][0] = kNoStop << 16;
     lds_sync[pair][1] = 0;
+    lds_sync[pair][2] = 0;
   }
   __syncthreads();
   if (bank >= B) return;  // both waves of the bank
@@ -613,7 +614,25 @@ void sdm_trace_kernel(StepParams P) {
     auto need = [&](int t) __attribute__((always_inline)) -> uint32_t {
       return static_cast<uint32_t>(t + 3 < G + 1 ? t + 3 : G + 1);
     };
-    bool go = await(need(-1));
+    // packed: the steps the launch's plan lets this bank run, from the
+    // control wave before it publishes any step (bounded wait)
+    bool go = true;
+    if constexpr (!DENSE) {
+      uint32_t w = 0;
+      for (int spins = 0; spins < 64 * kSpinLimit; ++spins) {
+        w = sync_load(&sync[2]);
+        if (w & kPlanReady) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (w & kPlanReady) {
+        const int planned = static_cast<int>(w & ~kPlanReady);
+        G = planned < G ? planned : G;
+        if (G <= 0) return;
+      } else {
+        go = false;
+      }
+    }
+    go = go && await(need(-1));
     bool lost = !go;
     if (go) {
       read_ptrs(0, hd);
@@ -690,28 +709,65 @@ void sdm_trace_kernel(StepParams P) {
     }
     any_bad = bad != 0;
   }
-  // ---- plan words (packed): lane l holds step 64c + l's of chunk c, loaded a
-  // chunk ahead and staged into LDS when the chunk before starts being used
-  const int32_t* const plan_bank =
-      DENSE ? nullptr : plan_words(P, layer_id) + static_cast<int64_t>(bank) * P.plan_steps;
-  const int32_t* const pops = DENSE ? nullptr : plan_pops(P, layer_id);
-  const int fit_rows = DENSE ? 0 : pin(__builtin_amdgcn_readfirstlane(
-                                       static_cast<int>(control_word(P, layer_id, COWSDM_CTRL_FIT))));
-  uint32_t plan_next = 0;
-  auto load_plan = [&](int c) __attribute__((always_inline)) {
+  // ---- the launch's plan (packed): block, epoch, the pops that fit
+  PlanBlock pb{};
+  uint32_t epoch = 0;
+  int fit_rows = 0;
+  if constexpr (!DENSE) {
+    pb = plan_block(P, layer_id);
+    // the epoch word changes only when the layer's last control wave ends
+    epoch = static_cast<uint32_t>(
+        __builtin_amdgcn_readfirstlane(static_cast<int>(launch_epoch(pb))));
+  }
+  // ---- plan words (packed): every step's word of this bank, from its prefix
+  // word and the step's running total, staged into LDS once the plan's header
+  // is in (composed as: first touches before it | first-touch lanes << 24 |
+  // stop bit 28); false when a word never arrives
+  auto stage_plan = [&]() __attribute__((always_inline)) -> bool {
+    bool ok = true;
     if constexpr (!DENSE) {
-      const int t = c * kWave + lane;
-      plan_next = t < G ? static_cast<uint32_t>(plan_bank[t]) : 0u;
+      constexpr int KC = kTraceMaxSteps / kWave;
+      uint64_t w[KC], c[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int t = k * kWave + lane;
+        const int tc = t < G ? t : G - 1;
+        if (k * kWave < G) {
+          w[k] = atomic_load_u64(pb.word(bank, tc));
+          c[k] = atomic_load_u64(pb.cum + tc);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int t = k * kWave + lane;
+        const int tc = t < G ? t : G - 1;
+        if (k * kWave >= G) break;
+        if (__ballot(!tag_is(w[k], epoch) || !(w[k] & kPrefixDone)) != 0) {
+          ok = poll_tagged(pb.word(bank, tc), true, epoch, w[k], true) && ok;
+        }
+        if (__ballot(!tag_is(c[k], epoch)) != 0) {
+          ok = poll_tagged(pb.cum + tc, true, epoch, c[k]) && ok;
+        }
+        const uint32_t v = static_cast<uint32_t>(w[k]);
+        const uint32_t base = static_cast<uint32_t>(c[k]) + ((v & ~kPrefixDone) >> kPrefixShift);
+        if (t < G) {
+          lds_plan[pair][t] = static_cast<int>((base & kPlanBaseMask) | ((v & 15u) << kPlanMaskShift) |
+                                               ((v & kCountStop) ? 1u << kPlanStopBit : 0u));
+        }
+      }
     }
-  };
-  auto stage_plan = [&](int c) __attribute__((always_inline)) {
-    if constexpr (!DENSE) lds_plan[pair][c & 1][lane] = static_cast<int>(plan_next);
+    return ok;
   };
   auto plan_of = [&](int t) __attribute__((always_inline)) -> uint32_t {
     if constexpr (DENSE) return 0u;
     const int tc = t < G ? t : G - 1;
-    return static_cast<uint32_t>(
-        __builtin_amdgcn_readfirstlane(lds_plan[DENSE ? 0 : pair][(tc >> 6) & 1][tc & (kWave - 1)]));
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds_plan[DENSE ? 0 : pair][tc]));
+  };
+  // chunk c's first-touch lanes, lane l for step 64c + l
+  auto chunk_fm = [&](int c) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (DENSE) return 0u;
+    const int t = c * kWave + lane;
+    return (static_cast<uint32_t>(lds_plan[DENSE ? 0 : pair][t < G ? t : G - 1]) >> kPlanMaskShift) & 15u;
   };
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
@@ -1111,20 +1167,20 @@ void sdm_trace_kernel(StepParams P) {
   // the step resolves.  A step whose pops reach past the rows the plan could
   // give out (a capacity proof that was missing or not honest) overflows: it
   // takes none, and the bank stops.
-  auto claim = [&](const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+  auto claim = [&](const TraceRoute& rt, uint64_t& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       const int count = route_count(rt.u);
       if (count > 0 && route_ok(rt.u) && rt.base + count <= fit_rows) {
         const bool first = lane < kTraceMaxWrites && ((route_fmask(rt.u) >> lane) & 1u);
-        if (first) home = pops[rt.base + rt.rank];
+        if (first) home = atomic_load_u64(pb.pops + rt.base + rt.rank);
       }
     }
   };
 
   // Step t's first touches, from the rows loaded for them (home: lane j holds
-  // write j's row).  r1: step t+1, whose rewrites of step t's slots take its
-  // physical rows.
-  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, int home)
+  // write j's pop word, tagged with the epoch once the plan wrote it).  r1:
+  // step t+1, whose rewrites of step t's slots take its physical rows.
+  auto resolve = [&](int t, TraceRoute& rt, TraceRoute& r1, uint64_t home)
       __attribute__((always_inline)) {
     const int count = route_count(rt.u);
     if (count > 0 && route_ok(rt.u) && alive) {
@@ -1132,7 +1188,18 @@ void sdm_trace_kernel(StepParams P) {
       bool fits = rt.base + count <= fit_rows;
       if (fits) {
         const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
-        const int new_row = first ? home : -1;
+        if (__ballot(first && !tag_is(home, epoch)) != 0) {
+          // rare: the pop was loaded before it arrived
+          if (!poll_tagged(pb.pops + rt.base + rt.rank, first, epoch, home)) {
+            if (lane == 0) {
+              __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                                    static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+            }
+            home = tagged(epoch, 0xFFFFFFFFu);
+          }
+        }
+        const int new_row = first ? static_cast<int>(static_cast<uint32_t>(home)) : -1;
         if (__ballot(first && (new_row < 0 || new_row >= C)) != 0) {
           fits = false;
           if (lane == 0) {
@@ -1158,7 +1225,7 @@ void sdm_trace_kernel(StepParams P) {
   };
 
   // After classifying step t: load the rows its first touches pop.
-  auto after_classify = [&](int t, const TraceRoute& rt, int& home) __attribute__((always_inline)) {
+  auto after_classify = [&](int t, const TraceRoute& rt, uint64_t& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       if (t < G) claim(rt, home);
     }
@@ -1180,22 +1247,182 @@ void sdm_trace_kernel(StepParams P) {
     return false;
   };
 
+  // ---- the launch's plan (packed; trace_plan.h), before any step
+  if constexpr (!DENSE) {
+    bool ok = true;
+    if constexpr (MAPLDS) {
+      // count part: this bank's first touches, step by step.  A slot is
+      // first-touched by the launch's first step that writes it, unless it
+      // was mapped at launch start: one LDS minimum per write slot over all
+      // steps (lane = step, 64 steps a round) gives that step.  A step with
+      // an invalid route stops the bank from there on.
+      int* const first_write = lds_map_all + NB * N + pair * N;
+      for (int k = lane; k < N; k += kWave) first_write[k] = 0x7fffffff;
+      constexpr int KC = kTraceMaxSteps / kWave;
+      int wsl[KC][kTraceMaxWrites];   // write slots (-1: none) of step 64c + lane
+      uint32_t mapped[KC];
+      int err_step = (base_err & COWSDM_ERR_TEMPLATE) ? 0 : G0;
+      int err_bits[KC];
+      // the slots of chunk c + 1 load while chunk c is checked
+      IDX sbuf[2][kIdxRow];
+      auto load_slots = [&](int c, IDX (&dst)[kIdxRow]) __attribute__((always_inline)) {
+        const int t = c * kWave + lane;
+        const int tc = t < G0 ? t : G0 - 1;
+        const char* const w = at(wbase, st_wi, tc);
+        const char* const r = at(rbase, st_ri, tc);
+        if constexpr (FULL && sizeof(IDX) == 4) {
+          // a step's 4 write and 16 read slots are 16 and 64 contiguous,
+          // 16-byte aligned bytes: five vector loads per lane
+          const i32x4_t a = *(const __attribute__((address_space(1))) i32x4_t*)(w);
+          dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+#pragma unroll
+          for (int k = 0; k < kTraceMaxReads / 4; ++k) {
+            const i32x4_t b = *(const __attribute__((address_space(1))) i32x4_t*)(r + 16 * k);
+            dst[kTraceMaxWrites + 4 * k] = b.x;
+            dst[kTraceMaxWrites + 4 * k + 1] = b.y;
+            dst[kTraceMaxWrites + 4 * k + 2] = b.z;
+            dst[kTraceMaxWrites + 4 * k + 3] = b.w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < kTraceMaxWrites; ++j) {
+            dst[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : W - 1) * sizeof(IDX));
+          }
+#pragma unroll
+          for (int i = 0; i < kTraceMaxReads; ++i) {
+            dst[kTraceMaxWrites + i] =
+                *(const __attribute__((address_space(1))) IDX*)(r + (i < R ? i : R - 1) * sizeof(IDX));
+          }
+        }
+      };
+      load_slots(0, sbuf[0]);
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int t = c * kWave + lane;
+        mapped[c] = 0;
+        err_bits[c] = 0;
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) wsl[c][j] = -1;
+        if (c * kWave >= G0) continue;
+        if ((c + 1) * kWave < G0) load_slots(c + 1, sbuf[(c + 1) & 1]);
+        const IDX (&cur)[kIdxRow] = sbuf[c & 1];
+        int e = 0;
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+          if (j < W) {
+            const int64_t v = static_cast<int64_t>(cur[j]);
+            if (v < 0 || v >= N) {
+              e |= COWSDM_ERR_WRITE_INDEX;
+            } else {
+              wsl[c][j] = static_cast<int>(v);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < kTraceMaxReads; ++i) {
+          if (i < R) {
+            const int64_t v = static_cast<int64_t>(cur[kTraceMaxWrites + i]);
+            if (v < 0 || v >= N) {
+              e |= COWSDM_ERR_READ_INDEX;
+            } else if (lds_map[v] >= C0) {
+              e |= COWSDM_ERR_CORRUPT;
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kTraceMaxWrites; ++j) {
+#pragma unroll
+          for (int i = j + 1; i < kTraceMaxWrites; ++i) {
+            if (wsl[c][j] >= 0 && wsl[c][j] == wsl[c][i]) e |= COWSDM_ERR_DUP_WRITE;
+          }
+          const int x = wsl[c][j];
+          if (x >= 0) {
+            const int m = lds_map[x];
+            if (m >= C0) e |= COWSDM_ERR_CORRUPT;
+            if (m >= 0) mapped[c] |= 1u << j;
+            if (t < G0) {
+              __hip_atomic_fetch_min(&first_write[x], t, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+          }
+        }
+        if (t < G0 && e != 0) {
+          err_bits[c] = e;
+          err_step = t < err_step ? t : err_step;
+        }
+      }
+      // the bank's first invalid step and its errors
+      for (int o = kWave / 2; o > 0; o >>= 1) {
+        const int y = __shfl_xor(err_step, o, kWave);
+        err_step = y < err_step ? y : err_step;
+      }
+      int bits = 0;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) bits |= c * kWave + lane == err_step ? err_bits[c] : 0;
+      bits = wave_or(bits);
+      // one wave's LDS accesses apply in issue order: keep the reads after
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int t = c * kWave + lane;
+        if (c * kWave >= G0 || t >= G0) continue;
+        uint32_t mask = 0;
+        if (t < err_step) {
+#pragma unroll
+          for (int j = 0; j < kTraceMaxWrites; ++j) {
+            const int x = wsl[c][j];
+            if (x >= 0 && !((mapped[c] >> j) & 1u) && first_write[x] == t) mask |= 1u << j;
+          }
+        }
+        atomic_store_u64(pb.word(bank, t),
+                         tagged(epoch, mask | (t >= err_step ? kCountStop : 0u)));
+      }
+      if (lane == 0 && bits != 0) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(bits),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // prefix part (steps bank, bank + B, ...), the layer part (bank 0), the
+    // header
+    ok = plan_prefix(pb, bank, B, G0, epoch);
+    if (bank == 0) ok = plan_layer(P, layer_id, pb, B, G0, epoch, &lds_idx[0][0][0][0]) && ok;
+    int steps = 0, fit = 0, capacity = C0;
+    ok = plan_header(pb, epoch, steps, fit, capacity) && ok;
+    if (!ok) {
+      if (lane == 0) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        if (P.trace_status) {
+          __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
+                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      steps = 0;
+    }
+    G = steps < G0 ? steps : G0;
+    fit_rows = fit;
+    C = pin(capacity);
+    if (lane == 0) sync_store(&sync[2], kPlanReady | static_cast<uint32_t>(G));
+  }
+
+  int done_steps = G;
+  if (G > 0) {
   // ---- prologue: steps 0 and 1 classified, their pops loaded and their rows
   // published
   TraceIdx idxA, idxB, ready1, ready2;
   int mwA = -1, mrA = -1, mwB = -1, mrB = -1;
-  int popA = -1, popB = -1;        // pops in flight, homed by the parity of their step
+  uint64_t popA = 0, popB = 0;     // pops in flight, homed by the parity of their step
   TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
   q.widx = 0; q.ridx = 0; q.base = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1;
   q.rank = 0; q.u = 0; q.fwd = 0; q.rawm = 0;
-  load_plan(0);
   if constexpr (DENSE || MAPLDS) load_chunk(0);
+  const bool plan_ok = stage_plan();
   if constexpr (DENSE || MAPLDS) {
-    write_chunk(0, DENSE ? 0u : (plan_next >> kPlanMaskShift) & 15u);
+    write_chunk(0, chunk_fm(0));
     if (G > kWave) load_chunk(1);  // written before step 64 is read
   }
-  stage_plan(0);
-  if (G > kWave) load_plan(1);
   {
     TraceIdx i0, i1;
     if constexpr (DENSE || MAPLDS) {
@@ -1232,7 +1459,7 @@ void sdm_trace_kernel(StepParams P) {
   // homes are written now and read in iteration s+1 (claims: s+2), `other`
   // homes were written in iteration s-1 and are read now.
   auto iteration = [&](int s, TraceIdx& idx_self, TraceIdx& idx_other, int& mw_self, int& mr_self,
-                       int& mw_other, int& mr_other, int& pop)
+                       int& mw_other, int& mr_other, uint64_t& pop)
       __attribute__((always_inline)) {
     u32x4_t kq = {0u, 0u, 0u, 0u};
     if constexpr (DENSE || MAPLDS) kq = *reinterpret_cast<const u32x4_t*>(idx_row(s) + kIdxRow);
@@ -1260,7 +1487,6 @@ void sdm_trace_kernel(StepParams P) {
   __builtin_amdgcn_s_waitcnt(0);
 
   int s = 0;
-  int done_steps = G;
   bool stopped = false;
   // the data wave stopped taking steps (a bounded wait ran out): record it
   auto lost = [&]() __attribute__((always_inline)) {
@@ -1283,17 +1509,14 @@ void sdm_trace_kernel(StepParams P) {
       stopped = true;
       break;
     }
-    // chunk c's first slots and plan words are read in iteration 64c - 2;
-    // the buffers they replace held chunk c - 2, whose last step was read
-    // long before
-    if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
-      const int c = (s + 4) >> 6;
-      if constexpr (DENSE || MAPLDS) {
-        write_chunk(c, DENSE ? 0u : (plan_next >> kPlanMaskShift) & 15u);
+    // chunk c's first slots are read in iteration 64c - 2; the buffer they
+    // replace held chunk c - 2, whose last step was read long before
+    if constexpr (DENSE || MAPLDS) {
+      if (((s + 4) & (kWave - 1)) == 0 && s + 4 < G) {
+        const int c = (s + 4) >> 6;
+        write_chunk(c, chunk_fm(c));
         if ((c + 1) * kWave < G) load_chunk(c + 1);
       }
-      stage_plan(c);
-      if ((c + 1) * kWave < G) load_plan(c + 1);
     }
     iteration(s, idxA, idxB, mwA, mrA, mwB, mrB, popA);
     iteration(s + 1, idxB, idxA, mwB, mrB, mwA, mrA, popB);
@@ -1311,12 +1534,14 @@ void sdm_trace_kernel(StepParams P) {
   if (stopped && lane == 0) {
     sync_store(&sync[0], (static_cast<uint32_t>(done_steps) << 16) | kNoStop);
   }
+  if (!plan_ok) lost();   // a plan word never arrived: its steps took no rows
+  }  // G > 0
 
-  // ---- device counters: the layer's last control wave to finish advances
-  // the layer's counter.  Every wave of the layer read the counter before
-  // taking its ticket.  The data waves' row stores need no ordering here: the
-  // next launch on the stream starts after this one has ended.
-  if (P.trace_step) {
+  // ---- the layer's last control wave to finish advances the layer's device
+  // counter and (packed) the plan's epoch.  Every wave of the layer read both
+  // before taking its ticket.  The data waves' row stores need no ordering
+  // here: the next launch on the stream starts after this one has ended.
+  if (!DENSE || P.trace_step) {
     int64_t done = 0;
     if (lane == 0) {
       int64_t* const ticket = P.trace_ticket + 1 + layer_id;
@@ -1324,16 +1549,20 @@ void sdm_trace_kernel(StepParams P) {
     }
     if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1 && lane == 0) {
       atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
-      atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+      if (P.trace_step) {
+        atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+      }
+      if constexpr (!DENSE) atomic_store_u64(pb.epoch, static_cast<uint64_t>(epoch));
     }
   }
 }
 
-// Count and plan passes of a packed persistent launch (trace_plan.hip).
+// Count part of a packed persistent launch whose slot maps do not fit in LDS
+// (trace_plan.hip).
 template <typename IDX>
-int32_t launch_trace_plan(const StepParams& P, hipStream_t stream, hipEvent_t start);
-extern template int32_t launch_trace_plan<int32_t>(const StepParams&, hipStream_t, hipEvent_t);
-extern template int32_t launch_trace_plan<int64_t>(const StepParams&, hipStream_t, hipEvent_t);
+int32_t launch_trace_count(const StepParams& P, hipStream_t stream, hipEvent_t start);
+extern template int32_t launch_trace_count<int32_t>(const StepParams&, hipStream_t, hipEvent_t);
+extern template int32_t launch_trace_count<int64_t>(const StepParams&, hipStream_t, hipEvent_t);
 
 // Residency of one persistent kernel variant on one device: how many of its
 // workgroups the device holds at once for a given slot-map size.
@@ -1357,7 +1586,16 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
   P.blocks_per_layer = (P.banks + kTraceBanksPerBlock - 1) / kTraceBanksPerBlock;
   const int blocks = P.blocks_per_layer * P.nlayers;
   // the full shape folds every row count; other shapes select per row
-  const bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
+  bool full = P.writes == kTraceMaxWrites && P.reads == kTraceMaxReads;
+  if (full && sizeof(IDX) == 4) {
+    // the full variant loads a step's int32 slots as 16-byte vectors
+    uintptr_t bits = static_cast<uintptr_t>(P.trace_stride[0] | P.trace_stride[6]);
+    for (int l = 0; l < P.nlayers; ++l) {
+      bits |= reinterpret_cast<uintptr_t>(P.layer[l].write_indices) |
+              reinterpret_cast<uintptr_t>(P.layer[l].read_indices);
+    }
+    full = (bits % 16) == 0;
+  }
   const bool few = P.banks <= kWave;
   const int variant = (full ? 1 : 0) + (few ? 2 : 0);
   const void* kernels[4][3] = {
@@ -1381,8 +1619,9 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
   // map in LDS: per bank the slot map
+  // map in LDS: per bank the slot map and each slot's first writing step
   const size_t lds_bytes =
-      MAPLDS ? sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
+      MAPLDS ? 2 * sizeof(int) * kTraceBanksPerBlock * static_cast<size_t>(P.slots) : 0;
   const int key = MAPLDS ? P.slots : 0;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) {
@@ -1413,11 +1652,11 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
   // pass of packed state), at the decode kernel's start and at its end.
   hipEvent_t first = nullptr, start = nullptr, stop = nullptr;
   if (!trace_timing_events(&first, &start, &stop)) first = start = stop = nullptr;
-  if constexpr (!DENSE) {
-    // the plan of every layer's launch, before any of its steps run
-    if (int32_t e = launch_trace_plan<IDX>(P, stream, first)) return e;
+  if (!DENSE && !MAPLDS) {
+    // the count part of every layer's plan, before the decode kernel
+    if (int32_t e = launch_trace_count<IDX>(P, stream, first)) return e;
   } else if (first) {
-    (void)hipEventRecord(first, stream);   // (the decode kernel is the first)
+    trace_timing_first_is_start();   // the decode kernel is the launch's first
   }
   auto launch = [&](StepParams* q, int grid, bool last) {
     void* args[] = {q};

@@ -1,0 +1,465 @@
+// The plan of a packed decode-trace launch, made inside the persistent
+// kernel (trace_kernel.h) by its control waves before any step runs.
+//
+// The reference's decode loop proves every step on the host before running
+// it (inference.py:551-552: prepare_step_capacity(banks * W), allocator.py:
+// 745-773): the proven counter drops by banks * W per step, free_count is
+// read only when the counter runs short, and the slab grows by the pooled
+// quantum only when free_count is below banks * W at such a read
+// (grow_capacity, allocator.py:691-743: new row ids join the top of the free
+// stack).  Single steps pop first-touch rows bank-major from the top of the
+// stack (allocator.py:1471-1481).  Every one of those decisions depends only
+// on how many first touches each (step, bank) makes, and that depends only
+// on the routes and on which slots were mapped when the launch starts: slot
+// x is first-touched by the first step of the launch that writes it, unless
+// it was mapped already.  So the launch is settled up front, in four parts:
+//
+//   count (every control wave, its own bank; or the count kernel when the
+//   slot map does not fit in LDS): each step's first-touch write lanes and
+//   the bank's first step with an invalid route, after which the bank takes
+//   no step, as count words;
+//
+//   prefix (every control wave, steps bank, bank + B, ...): for each of its
+//   steps, the first touches of the lower banks at that step (a scan across
+//   the banks' count words) and the step's total;
+//
+//   layer (the control wave of bank 0): the running totals over the steps,
+//   the decode loop's proof step by step from the control words (growing
+//   the capacity within the slab's buffers, or stopping the layer before a
+//   growth that would not fit), the row every pop takes, the free stack,
+//   free_count and overflow flag the launch leaves, and a header with the
+//   steps the layer runs, the pops that fit and the capacity;
+//
+//   header (every control wave): waits for the header.
+//
+// Waves of different workgroups (on different XCDs) exchange only tagged
+// words (common.h): a word is read with device-scope atomic loads until it
+// carries the launch's epoch.  Every wait is bounded.  The persistent kernel
+// then takes each (step, bank)'s pops at the running total of its step plus
+// its prefix, so maps, slabs and free stacks equal those of the single-step
+// loop bit for bit.
+#pragma once
+
+#include "common.h"
+
+namespace cowsdm_impl {
+
+// Wave-inclusive sum over lanes (lane order).
+__device__ __forceinline__ int wave_inclusive(int v) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(v, o, kWave);
+    if (lane >= o) v += y;
+  }
+  return v;
+}
+
+// Loads *p (lanes with `want`) until every wanted word carries `epoch` (and,
+// with `prefix`, is a prefix word); false when some never does (bounded).
+__device__ __forceinline__ bool poll_tagged(const int64_t* p, bool want, uint32_t epoch,
+                                            uint64_t& w, bool prefix = false) {
+  const uint64_t done = prefix ? kPrefixDone : 0u;
+  auto ready = [&](uint64_t x) __attribute__((always_inline)) {
+    return tag_is(x, epoch) && (x & done) == done;
+  };
+  w = want ? atomic_load_u64(p) : tagged(epoch, static_cast<uint32_t>(done));
+  for (int spins = 0; __ballot(want && !ready(w)) != 0; ++spins) {
+    if (spins >= kSpinLimit) return false;
+    __builtin_amdgcn_s_sleep(1);
+    if (want && !ready(w)) w = atomic_load_u64(p);
+  }
+  return true;
+}
+
+// v, known to the compiler as the same in every lane
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// a / b for 0 <= a, 0 < b, in 32 bits when both fit
+__device__ __forceinline__ int64_t plan_div(int64_t a, int64_t b) {
+  if (a < (int64_t{1} << 31) && b < (int64_t{1} << 31)) {
+    return static_cast<int64_t>(static_cast<uint32_t>(a) / static_cast<uint32_t>(b));
+  }
+  return a / b;
+}
+
+// Prefix part: this wave's range of steps (a contiguous share of the G0
+// steps), each against every bank (lane = bank): waits for the banks' count
+// words of the step, replaces each with its prefix word and publishes the
+// step's total.  A bank's words of consecutive steps are contiguous, so a
+// lane loads kBatch steps at once.  False when a count never arrives.
+__device__ inline bool plan_prefix(const PlanBlock& pb, int bank, int B, int G0,
+                                   uint32_t epoch) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  constexpr int kBatch = 8;
+  const int per = (G0 + B - 1) / B;
+  const int t_begin = bank * per;
+  const int t_end = t_begin + per < G0 ? t_begin + per : G0;
+  for (int tb = t_begin; tb < t_end; tb += kBatch) {
+    int carry[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) carry[i] = 0;
+    for (int g = 0; g < B; g += kWave) {
+      const int b = g + lane;
+      const bool in = b < B;
+      int64_t* const row = pb.word(in ? b : 0, 0);
+      uint64_t w[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int t = tb + i < t_end ? tb + i : t_end - 1;
+        w[i] = atomic_load_u64(row + t);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int t = tb + i;
+        if (t >= t_end) break;
+        uint64_t x = in ? w[i] : tagged(epoch, 0);
+        if (__ballot(in && !tag_is(x, epoch)) != 0 && !poll_tagged(row + t, in, epoch, x)) {
+          return false;
+        }
+        const uint32_t v = static_cast<uint32_t>(x) & (kCountStop | 15u);
+        const int c = __popc(v & 15u);
+        const int incl = wave_inclusive(c);
+        if (in) {
+          const uint32_t pre = static_cast<uint32_t>(carry[i] + incl - c);
+          atomic_store_u64(row + t, tagged(epoch, v | (pre << kPrefixShift) | kPrefixDone));
+        }
+        carry[i] += __builtin_amdgcn_readlane(incl, kWave - 1);
+      }
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (tb + i < t_end) {
+          atomic_store_u64(pb.totals + tb + i, tagged(epoch, static_cast<uint32_t>(carry[i])));
+        }
+      }
+    }
+  }
+  return true;
+}
+
+// Layer part, by one wave (the control wave of bank 0).  `seg` is LDS of
+// 4 * kPlanSegments ints: the launch's growth segments.  Publishes the running totals, the pops and the
+// header (last); false when a step total never arrives (the header then
+// says the layer runs no step).
+__device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBlock& pb, int B,
+                                  int G0, uint32_t epoch, int* seg) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const cowsdm_layer_t& L = P.layer[layer];
+  constexpr int K = kTraceMaxSteps / kWave;
+  int* const seg_q = seg;                        // first touches before the segment
+  int* const seg_free = seg + kPlanSegments;     // stack height before its growth
+  int* const seg_top = seg + 2 * kPlanSegments;  // stack height after its growth
+  int* const seg_old = seg + 3 * kPlanSegments;  // capacity before its growth
+
+  auto publish_head = [&](int steps, int fit, int capacity) __attribute__((always_inline)) {
+    if (lane < 3) {
+      const int v = lane == 0 ? steps : (lane == 1 ? fit : capacity);
+      atomic_store_u64(pb.head + lane, tagged(epoch, static_cast<uint32_t>(v)));
+    }
+  };
+  auto fault = [&]() __attribute__((always_inline)) {
+    if (lane == 0 && P.trace_status) {
+      __hip_atomic_fetch_or(&P.trace_status[layer], int32_t{COWSDM_TRACE_FAULT},
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+
+  // the launch's control words and free count, loaded first so that their
+  // latency overlaps the wait for the step totals
+  const int64_t C0 = uniform64(control_word(P, layer, COWSDM_CTRL_CAPACITY));
+  int64_t proven = uniform64(control_word(P, layer, COWSDM_CTRL_PROVEN));
+  const int64_t room = uniform64(control_word(P, layer, COWSDM_CTRL_ROOM));
+  const int64_t quantum = uniform64(control_word(P, layer, COWSDM_CTRL_QUANTUM));
+  const int64_t need = uniform64(control_word(P, layer, COWSDM_CTRL_NEED));
+  const int64_t events0 = uniform64(control_word(P, layer, COWSDM_CTRL_EVENTS));
+  const int64_t added0 = uniform64(control_word(P, layer, COWSDM_CTRL_ADDED));
+  const int64_t copied0 = uniform64(control_word(P, layer, COWSDM_CTRL_COPIED));
+  const int F0 = __builtin_amdgcn_readfirstlane(*L.free_count);
+
+  // ---- running totals: lane l holds the first touches before steps l,
+  // l + 64, ... (exclusive), cum_g all of them
+  int cum[K];
+  int cum_g = 0;
+  bool lost = false;
+  {
+    // all totals loaded at once; only the ones not yet there are polled
+    uint64_t w[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int t = k * kWave + lane;
+      w[k] = k * kWave < G0 ? atomic_load_u64(pb.totals + (t < G0 ? t : 0)) : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int t = k * kWave + lane;
+      if (k * kWave < G0 && __ballot(t < G0 && !tag_is(w[k], epoch)) != 0) {
+        lost |= !poll_tagged(pb.totals + (t < G0 ? t : 0), t < G0, epoch, w[k]);
+      }
+      const int v = t < G0 && !lost ? static_cast<int>(static_cast<uint32_t>(w[k])) : 0;
+      const int incl = wave_inclusive(v);
+      cum[k] = cum_g + incl - v;
+      cum_g += __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
+  }
+  if (lost) {
+    if (lane == 0) {
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(COWSDM_ERR_LOOKBACK), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+    fault();
+    publish_head(0, 0, static_cast<int>(C0));
+    return false;
+  }
+  // lane l's value for step s = 64k + l of a per-lane array (s wave-uniform:
+  // a register picked by index, then one lane read)
+  auto step_value = [&](const int (&v)[K], int s) __attribute__((always_inline)) -> int {
+    return __builtin_amdgcn_readlane(v[s >> 6], s & (kWave - 1));
+  };
+  // first touches before step s (s in [0, G0]), wave-uniform
+  auto cum_at = [&](int s) __attribute__((always_inline)) -> int {
+    return s >= G0 ? cum_g : step_value(cum, s);
+  };
+
+  if (F0 < 0 || F0 > C0) {
+    // a corrupt free count: the layer runs nothing
+    if (lane == 0) {
+      control_word(P, layer, COWSDM_CTRL_STEPS) = 0;
+      __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                            static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    }
+    fault();
+    publish_head(0, 0, static_cast<int>(C0));
+    return true;
+  }
+
+  // ---- the decode loop's capacity proof, step by step (wave-uniform)
+  int64_t capacity = C0;
+  int64_t added = 0, events = 0, rows_added = 0, rows_copied = 0;
+  int nseg = 1;
+  auto put_seg = [&](int k, int q, int free_rows, int top, int old)
+      __attribute__((always_inline)) {
+    if (lane == 0) {
+      seg_q[k] = q;
+      seg_free[k] = free_rows;
+      seg_top[k] = top;
+      seg_old[k] = old;
+    }
+  };
+  put_seg(0, 0, F0, F0, static_cast<int>(C0));
+  int stop = G0;
+  bool over = false;
+  if (need > 0 && quantum > 0) {
+    // hop[k] (lane l): from a step t = 64k + l whose proof re-reads
+    // free_count, the steps until the next such read, given the growth so
+    // far: the free rows at t over need (at most the steps left), or 0 when
+    // they are short of need and the slab grows at t.  All lanes compute
+    // them at once; the walk below then takes one hop per read.
+    int hop[K];
+    auto hops = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int t = k * kWave + lane;
+        const int64_t f = F0 + added - cum[k];
+        const int64_t j = t >= G0 || f < need ? 0 : plan_div(f, need);
+        hop[k] = static_cast<int>(j < G0 - t ? j : G0 - t);
+      }
+    };
+    int s = 0;
+    if (proven >= need) {
+      // steps still covered by the proof the launch starts with
+      int64_t j = plan_div(proven, need);
+      if (j > G0) j = G0;
+      if (cum_at(static_cast<int>(j)) > F0) over = true;   // the proof was not honest
+      proven -= j * need;
+      s = static_cast<int>(j);
+    }
+    if (!over && s < G0) hops();
+    // from here every step whose proof runs short re-reads free_count
+    while (!over && s < G0) {
+      int h = step_value(hop, s);
+      if (h == 0) {
+        const int64_t free_rows = F0 + added - cum_at(s);
+        const int64_t want = capacity + need - free_rows;
+        const int64_t selected = plan_div(want + quantum - 1, quantum) * quantum;
+        if (selected > room || selected >= (int64_t{1} << 31)) {
+          stop = s;   // the host grows the slab into larger buffers
+          break;
+        }
+        const int64_t a = selected - capacity;
+        put_seg(nseg, cum_at(s), static_cast<int>(free_rows),
+                static_cast<int>(free_rows + a), static_cast<int>(capacity));
+        ++nseg;
+        ++events;
+        rows_added += a;
+        rows_copied += capacity;
+        added += a;
+        capacity = selected;
+        hops();
+        h = step_value(hop, s);   // >= 1 now
+      }
+      if (s + h >= G0) {
+        // the last read of the launch: the proof left after its steps
+        proven = F0 + added - cum_at(s) - static_cast<int64_t>(G0 - s) * need;
+        s = G0;
+      } else {
+        s += h;
+      }
+    }
+  } else if (cum_g > F0) {
+    over = true;   // no proof: the stack runs out
+  }
+  // LDS of one wave applies in issue order; keep the compiler from moving
+  // the segment reads below above lane 0's writes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // pops that can be given out: all of the planned steps', or the stack's
+  const int vlen = over ? static_cast<int>(F0 + added) : cum_at(stop);
+  int fit = vlen;
+  if (over) {
+    // the pops that fit end at a (step, bank) boundary: the last one at or
+    // below the stack height, found among the banks of the step where the
+    // stack runs out
+    int t_out = 0;   // the last step whose running total is <= vlen
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int t = k * kWave + lane;
+      const uint64_t below = __ballot(t < G0 && cum[k] <= vlen);
+      if (below) t_out = k * kWave + 63 - __builtin_clzll(below);
+    }
+    const int base = cum_at(t_out);
+    int best = base;
+    for (int g = 0; g < B; g += kWave) {
+      const int b = g + lane;
+      uint64_t w;
+      poll_tagged(pb.word(b < B ? b : 0, t_out), b < B, epoch, w, true);
+      const uint32_t v = static_cast<uint32_t>(w);
+      const int end = base + static_cast<int>((v & ~kPrefixDone) >> kPrefixShift) +
+                      __popc(v & 15u);
+      int cand = b < B && (v & kPrefixDone) && end <= vlen ? end : base;
+      for (int o = kWave / 2; o > 0; o >>= 1) {
+        const int y = __shfl_xor(cand, o, kWave);
+        cand = y > cand ? y : cand;
+      }
+      best = cand > best ? cand : best;
+    }
+    fit = best;
+  }
+
+  // ---- running totals for the steps' waves
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int t = k * kWave + lane;
+    if (t < G0) atomic_store_u64(pb.cum + t, tagged(epoch, static_cast<uint32_t>(cum[k])));
+  }
+  if (lane == 0) atomic_store_u64(pb.cum + G0, tagged(epoch, static_cast<uint32_t>(cum_g)));
+
+  // ---- the row each pop takes: segment k pops from its top down.  The
+  // stack entry at position p during segment k is the row the latest growth
+  // j <= k whose positions cover p put there, or the entry the launch found.
+  const int32_t* const found = L.free_rows;
+  auto entry = [&](int p, int k) __attribute__((always_inline)) -> int {
+    for (int j = k; j >= 1; --j) {
+      if (p >= seg_free[j]) return seg_old[j] + (p - seg_free[j]);
+    }
+    return found[p];
+  };
+  // A pop's row is arithmetic unless it comes from the stack the launch
+  // found: those are loaded kPopBatch per lane at once.
+  constexpr int kPopBatch = 8;
+  const int listed = vlen < cum_at(stop) ? vlen : cum_at(stop);
+  for (int k = 0; k < nseg; ++k) {
+    const int q0 = seg_q[k];
+    const int q1 = k + 1 < nseg ? seg_q[k + 1] : listed;
+    const int top = seg_top[k];
+    for (int qb = q0; qb < q1; qb += kWave * kPopBatch) {
+      int row[kPopBatch];
+#pragma unroll
+      for (int i = 0; i < kPopBatch; ++i) {
+        const int q = qb + i * kWave + lane;
+        const int p = top - 1 - (q - q0);
+        int v = -1;   // -1: from the stack the launch found
+        for (int j = k; j >= 1; --j) {
+          if (p >= seg_free[j]) {
+            v = seg_old[j] + (p - seg_free[j]);
+            break;
+          }
+        }
+        // the row, or -2 - p for position p of the found stack
+        row[i] = q >= q1 ? 0 : (v >= 0 ? v : -2 - p);
+      }
+#pragma unroll
+      for (int i = 0; i < kPopBatch; ++i) {
+        if (row[i] <= -2) row[i] = found[-2 - row[i]];
+      }
+#pragma unroll
+      for (int i = 0; i < kPopBatch; ++i) {
+        const int q = qb + i * kWave + lane;
+        if (q < q1) atomic_store_u64(pb.pops + q, tagged(epoch, static_cast<uint32_t>(row[i])));
+      }
+    }
+  }
+  // ---- the stack the launch leaves (rewritten only above the lowest
+  // growth, where no pop read it: segment 0 pops read below every growth's
+  // base, later segments below their own)
+  const int64_t height = F0 + added - fit;
+  if (nseg > 1) {
+    // every entry the launch found was read before the stack changes
+    __builtin_amdgcn_s_waitcnt(0);
+    int lo = seg_free[1];
+    for (int k = 2; k < nseg; ++k) lo = seg_free[k] < lo ? seg_free[k] : lo;
+    // (the layer struct lists free_rows as read-only for the step kernels;
+    // the plan is the one part that rewrites it)
+    int32_t* const stack = const_cast<int32_t*>(L.free_rows);
+    for (int64_t p = lo + lane; p < height; p += kWave) {
+      stack[p] = entry(static_cast<int>(p), nseg - 1);
+    }
+  }
+  if (lane == 0) {
+    *L.free_count = static_cast<int32_t>(height);
+    if (over) {
+      *L.overflow_flag = 1;
+    } else if (nseg > 1) {
+      *L.overflow_flag = 0;   // grow_capacity clears it
+    }
+    control_word(P, layer, COWSDM_CTRL_PROVEN) = over ? 0 : proven;
+    control_word(P, layer, COWSDM_CTRL_CAPACITY) = capacity;
+    control_word(P, layer, COWSDM_CTRL_EVENTS) = events0 + events;
+    control_word(P, layer, COWSDM_CTRL_ADDED) = added0 + rows_added;
+    control_word(P, layer, COWSDM_CTRL_COPIED) = copied0 + rows_copied;
+    control_word(P, layer, COWSDM_CTRL_FREE) = height;
+    control_word(P, layer, COWSDM_CTRL_STEPS) = stop;
+    control_word(P, layer, COWSDM_CTRL_FIT) = vlen;
+    if (stop < G0 && P.trace_status) {
+      __hip_atomic_fetch_or(&P.trace_status[layer], int32_t{COWSDM_TRACE_REFUSED},
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  publish_head(stop, vlen, static_cast<int>(capacity));
+  return true;
+}
+
+// Header part: the steps the layer runs, the pops that fit and the capacity
+// the launch grows to.  False when the header never arrives.
+__device__ inline bool plan_header(const PlanBlock& pb, uint32_t epoch, int& steps, int& fit,
+                                   int& capacity) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  uint64_t w;
+  if (!poll_tagged(pb.head + (lane < 3 ? lane : 0), lane < 3, epoch, w)) return false;
+  const int v = static_cast<int>(static_cast<uint32_t>(w));
+  steps = __builtin_amdgcn_readlane(v, 0);
+  fit = __builtin_amdgcn_readlane(v, 1);
+  capacity = __builtin_amdgcn_readlane(v, 2);
+  return true;
+}
+
+}  // namespace cowsdm_impl

@@ -259,12 +259,14 @@ int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
  * in the reference; for callers that cannot allocate device memory, such as
  * code under HIP graph capture and serving loops that forbid allocation.  It
  * allocates nothing: the plan blocks live in a static device array of
- * COWSDM_STATIC_SCAN_WORDS int64 words on each GPU (8 MiB, held until the
+ * COWSDM_STATIC_SCAN_WORDS int64 words on each GPU (16 MiB, held until the
  * process ends), which limits a call to nlayers *
  * cowsdm_trace_scan_words(banks, W, scan_steps) words (COWSDM_ELIMIT
  * beyond).  Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (other streams, other host threads) race. */
-#define COWSDM_STATIC_SCAN_WORDS (1ll << 20)
+ * overlap on one GPU (other streams, other host threads) race.  A call whose
+ * layout (banks, W, scan_steps, nlayers) differs from the last call's on the
+ * GPU first zeroes the words it uses, with a kernel on `stream`. */
+#define COWSDM_STATIC_SCAN_WORDS (1ll << 21)
 int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nlayers,
                                         const cowsdm_shape_t* shape,
                                         const cowsdm_trace_t* trace, int32_t steps,

@@ -83,7 +83,7 @@ def test_static_trace_refuses_past_its_array(device):
     lib = nat.lib()
     make = _case(device, layers=8, banks=256, slots=64, steps=4, seed=7, quantum=4096)
     tr = make(True)
-    tr.trace.scan_steps = 512          # 8 layers x 256 banks x 512 steps x 5 words / 2
+    tr.trace.scan_steps = 512          # 8 layers x about 5 x 256 x 512 words
     layers = tr.layer_array()
     tr.upload()
     stream = torch.cuda.current_stream().cuda_stream
