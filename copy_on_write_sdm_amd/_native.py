@@ -13,8 +13,10 @@ import ctypes
 import os
 import subprocess
 import threading
+import weakref
 from pathlib import Path
 
+import numpy as np
 import torch
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -56,8 +58,18 @@ CTRL_FREE = 8
 CTRL_STEPS = 9
 CTRL_FIT = 10
 CTRL_WORDS = 12
+# a trace launch's host-mapped report per layer: step counter, status bits,
+# control words (cowsdm_trace_t.report)
+REPORT_STEP = 0
+REPORT_STATUS = 1
+REPORT_CONTROL = 2
+REPORT_WORDS = 2 + CTRL_WORDS
+# cowsdm_trace_run modes
+RUN_PACKED = 0
+RUN_PACKED_STATIC = 1
+RUN_DENSE = 2
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -174,6 +186,7 @@ class Trace(ctypes.Structure):
         ("status", ctypes.c_void_p),
         ("control", ctypes.c_void_p),
         ("control_stride", ctypes.c_int64),
+        ("report", ctypes.c_void_p),
     ]
 
 
@@ -190,6 +203,12 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_trace_scan_words": (_I64, [_I64, _I64, _I32]),
     "cowsdm_trace_persistent": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32]),
+    "cowsdm_host_report_alloc": (
+        _I32, [_I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
+    "cowsdm_host_report_free": (_I32, [_P]),
+    "cowsdm_trace_run": (
+        _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I64,
+               _I32, _I32, _P]),
     "cowsdm_trace_timing": (_I32, [_I32]),
     "cowsdm_trace_timing_read": (
         _I32, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
@@ -269,6 +288,28 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+def _free_host_report(host: int) -> None:
+    lib().cowsdm_host_report_free(host)
+
+
+class HostReport:
+    """Host memory the device writes trace reports into
+    (cowsdm_host_report_alloc): ``array`` is an int64 numpy view
+    [layers, REPORT_WORDS] of it and ``device`` the address kernels write.
+    Freed when the object is collected (left to the process's end at
+    interpreter exit)."""
+
+    def __init__(self, layers: int):
+        host, device = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib().cowsdm_host_report_alloc(layers * REPORT_WORDS, ctypes.byref(host),
+                                             ctypes.byref(device)), "host report")
+        self.device = device.value
+        words = (ctypes.c_int64 * (layers * REPORT_WORDS)).from_address(host.value)
+        self.array = np.frombuffer(words, dtype=np.int64).reshape(layers, REPORT_WORDS)
+        self._free = weakref.finalize(self, _free_host_report, host.value)
+        self._free.atexit = False
+
+
 def check(rc: int, what: str) -> None:
     """Raise RuntimeError on a nonzero C-ABI return code."""
 
@@ -277,9 +318,17 @@ def check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {message}")
 
 
-def stream_handle(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on ``device``."""
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on ``device`` (torch's raw
+    getter where it has one: a tenth of the cost of building the Stream
+    object)."""
+
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

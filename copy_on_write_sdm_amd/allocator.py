@@ -139,6 +139,13 @@ class PackedSDMCopyOnWriteState:
     # (values buffer, free-row buffer) that values and free_rows lead, or None
     slab_buffers: Any = field(default=None, repr=False, compare=False)
 
+    def __setattr__(self, name: str, value: Any) -> None:
+        # every assignment counts in ``_version``: a decode trace that saw
+        # the same version last time knows its device copies of the pointers
+        # and proof words are current
+        object.__setattr__(self, name, value)
+        object.__setattr__(self, "_version", self.__dict__.get("_version", 0) + 1)
+
     # --------------------------------------------------------- creation
 
     @classmethod
@@ -1254,9 +1261,13 @@ class DecodeTrace:
         self._upload_buf = (torch.zeros(nat.CTRL_WORDS, layers, dtype=torch.int64).pin_memory()
                             if not self.dense else None)
         self._uploaded = None   # event after the last upload's copy
-        self._device_signature = None   # control words the device holds (host view)
+        # the states' versions when the device's control words and this
+        # trace's layer structs last matched them, or None (dense tables
+        # have no control words)
+        self._synced_versions = () if self.dense else None
         self._counters_seen = [(0, 0, 0)] * layers
         self._status_clean = False      # every status word is known to be zero
+        self._host_report = None        # nat.HostReport, made by the first run
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
@@ -1292,6 +1303,7 @@ class DecodeTrace:
             self.trace.scan_steps = self.max_steps_per_launch
             self.trace.control_stride = layers
         self._layers = None
+        self._layers_versions = None     # the states' versions the layer structs match
         self._positions = [0] * layers   # host copy of step_index, None when unknown
 
     # ------------------------------------------------------------ set-up
@@ -1316,6 +1328,7 @@ class DecodeTrace:
                      t.scratch.data_ptr() if t.scratch is not None else 0)
                     for t in self.tables)
         capacities = tuple(0 if self.dense else t.capacity_rows for t in self.tables)
+        self._layers_versions = self._versions()
         if self._layers is not None and self._layers[0] == key:
             layers = self._layers[1]
             if self._layers[2] != capacities:
@@ -1370,23 +1383,29 @@ class DecodeTrace:
                  st.growth_quantum_rows, need if st.growth_quantum_rows > 0 else 0)
                 for st in self.tables]
 
+    def _versions(self) -> tuple:
+        """The states' assignment counters (packed state), or () for dense
+        tables, whose pointers never change."""
+
+        return () if self.dense else tuple(st._version for st in self.tables)
+
     def upload(self, *, force: bool = True) -> None:
         """Write the packed layers' control words from their states and zero
         the growth counters the launches add to.  With ``force`` false the
-        copy is skipped when the device already holds these words (it does
-        after a launch whose words were read back, unless a state changed on
-        the host since)."""
+        copy is skipped when no state changed since the device's words last
+        matched them (after an upload, or a run or ``sync`` that read them
+        back)."""
 
         if self.dense:
             return
-        signature = self._signature()
-        if not force and signature == self._device_signature:
+        versions = self._versions()
+        if not force and versions == self._synced_versions:
             return
         buf = self._upload_buf
         if self._uploaded is not None:
             self._uploaded.synchronize()   # the last upload has left the pinned buffer
         buf.zero_()
-        for l, words in enumerate(signature):
+        for l, words in enumerate(self._signature()):
             for k, value in zip((nat.CTRL_PROVEN, nat.CTRL_CAPACITY, nat.CTRL_ROOM,
                                  nat.CTRL_QUANTUM, nat.CTRL_NEED), words):
                 buf[k, l] = value
@@ -1394,37 +1413,39 @@ class DecodeTrace:
         if self._uploaded is None:
             self._uploaded = torch.cuda.Event()
         self._uploaded.record()
-        self._device_signature = signature
         self._counters_seen = [(0, 0, 0)] * len(self.tables)
+        self._synced_versions = versions
 
-    def _absorb(self, control_rows) -> None:
-        """Take the control words read back after launches (host lists, row
-        k = word k of each layer) into the states: proof counter, capacity
-        (grown within the buffers) and the growth the launches added since
-        the last read (the device counters run from the last upload)."""
+    def _absorb(self, per_layer) -> None:
+        """Take the control words read back after launches (per layer, word
+        k of layer l at per_layer[l][k]) into the states: proof counter,
+        capacity (grown within the buffers) and the growth the launches added
+        since the last read (the device counters run from the last upload)."""
 
-        for l, st in enumerate(self.tables):
-            st.proven_maximum_additional_allocations = int(control_rows[nat.CTRL_PROVEN][l])
-            capacity = int(control_rows[nat.CTRL_CAPACITY][l])
-            if capacity != st.capacity_rows:
+        before = self._versions()
+        moved = False
+        for l, (st, words) in enumerate(zip(self.tables, per_layer)):
+            st.proven_maximum_additional_allocations = words[nat.CTRL_PROVEN]
+            capacity = words[nat.CTRL_CAPACITY]
+            if capacity != st.values.shape[0]:
                 vbuf, fbuf = st.slab_buffers
                 st.values, st.free_rows = vbuf[:capacity], fbuf[:capacity]
-            counters = (int(control_rows[nat.CTRL_EVENTS][l]),
-                        int(control_rows[nat.CTRL_ADDED][l]),
-                        int(control_rows[nat.CTRL_COPIED][l]))
+                moved = True
+            counters = (words[nat.CTRL_EVENTS], words[nat.CTRL_ADDED], words[nat.CTRL_COPIED])
             seen = self._counters_seen[l]
-            st.growth_events += counters[0] - seen[0]
-            st.growth_rows_added += counters[1] - seen[1]
-            st.growth_rows_copied += counters[2] - seen[2]
-            self._counters_seen[l] = counters
-            if st.growth_quantum_rows > 0:
+            if counters != seen:
+                st.growth_events += counters[0] - seen[0]
+                st.growth_rows_added += counters[1] - seen[1]
+                st.growth_rows_copied += counters[2] - seen[2]
+                self._counters_seen[l] = counters
+            if st.growth_quantum_rows > 0 and not st.capacity_is_proven:
                 st.capacity_is_proven = True
-        # the launches change only the proof counter and the capacity
-        previous = self._device_signature
-        self._device_signature = (
-            self._signature() if previous is None else
-            [(st.proven_maximum_additional_allocations, st.capacity_rows) + tuple(old[2:])
-             for st, old in zip(self.tables, previous)])
+        # what matched the states before still matches them, except the
+        # layer structs after a capacity grew
+        after = self._versions()
+        if not moved and self._layers_versions == before:
+            self._layers_versions = after
+        self._synced_versions = after if self._synced_versions == before else None
 
     def sync(self) -> None:
         """Read the control words back into the states after ``launch``
@@ -1432,7 +1453,7 @@ class DecodeTrace:
 
         if self.dense or not self.planned:
             return
-        self._absorb(self.control.tolist())
+        self._absorb([list(words) for words in zip(*self.control.tolist())])
         self._positions = None
 
     def reserve_steps(self, steps: int) -> None:
@@ -1536,15 +1557,17 @@ class DecodeTrace:
         if steps <= 0:
             return {"launches": 0, "growth_rounds": 0}
         positions = self._positions if self._positions is not None else self.step_index.tolist()
-        if len(set(positions)) != 1:
-            raise ValueError("decode trace layers stand at different steps")
         start = positions[0]
+        if any(p != start for p in positions):
+            raise ValueError("decode trace layers stand at different steps")
         target = start + steps
         if target > self.steps:
             raise ValueError("trace run passes the recorded steps")
         launch_steps = self.max_steps_per_launch if launch_steps is None else launch_steps
         launch_steps = max(1, min(int(launch_steps), self.max_steps_per_launch))
-        layers = self.layer_array()
+        versions = self._versions()
+        fresh = versions == self._synced_versions and versions == self._layers_versions
+        layers = self._layers[1] if fresh else self.layer_array()
         if not self.dense and not self.planned:
             return self._run_stepwise(start, steps, timing)
         saved = self.trace.steps_recorded
@@ -1554,34 +1577,58 @@ class DecodeTrace:
         if not self._status_clean:
             self.status.zero_()
         self._status_clean = False
-        self.upload(force=False)
+        if not fresh:
+            self.upload(force=False)
         stream = nat.stream_handle(self.device)
+        native = timing is None and (self.dense or self.planned) and self.persistent
+        if native and self._host_report is None:
+            self._host_report = nat.HostReport(len(self.tables))
+        mode = (nat.RUN_DENSE if self.dense else
+                nat.RUN_PACKED_STATIC if self.static_scan else nat.RUN_PACKED)
         launches = rounds = 0
         remaining = steps
         self._positions = None
         try:
             while True:
-                for _ in range(-(-remaining // launch_steps)):
-                    if timing is not None:
-                        e0 = torch.cuda.Event(enable_timing=True)
-                        e1 = torch.cuda.Event(enable_timing=True)
-                        e0.record()
-                        self._call(layers, launch_steps, stream)
-                        e1.record()
-                        timing.append((e0, e1))
-                    else:
-                        self._call(layers, launch_steps, stream)
-                    launches += 1
-                report = self._read_report()      # counters, status, control words
-                positions = report[0]
-                if not self.dense:
-                    self._absorb(report[2:])
-                words = report[1]   # int32 status word l is half l % 2 of word l // 2
-                status = [(words[l // 2] >> (32 * (l % 2))) & 0xFFFFFFFF
-                          for l in range(len(self.tables))]
-                faults = [l for l, s in enumerate(status) if s & nat.TRACE_FAULT]
-                if faults:
-                    self._fault(faults)
+                count = -(-remaining // launch_steps)
+                if native:
+                    # launches, then the layers' reports straight from host
+                    # memory the last wave of each layer wrote
+                    self.trace.report = self._host_report.device
+                    try:
+                        nat.check(nat.lib().cowsdm_trace_run(
+                            layers, len(self.tables), self.shape, self.trace, remaining,
+                            launch_steps, mode, stream), "decode trace run")
+                    finally:
+                        self.trace.report = None
+                    report = self._host_report.array
+                    positions = report[:, nat.REPORT_STEP].tolist()
+                    status = report[:, nat.REPORT_STATUS].tolist()
+                    control = None if self.dense else report[:, nat.REPORT_CONTROL:].tolist()
+                else:
+                    for _ in range(count):
+                        if timing is not None:
+                            e0 = torch.cuda.Event(enable_timing=True)
+                            e1 = torch.cuda.Event(enable_timing=True)
+                            e0.record()
+                            self._call(layers, launch_steps, stream)
+                            e1.record()
+                            timing.append((e0, e1))
+                        else:
+                            self._call(layers, launch_steps, stream)
+                    rows = self._read_report()      # counters, status, control words
+                    positions = rows[0]
+                    words = rows[1]   # int32 status word l is half l % 2 of word l // 2
+                    status = [(words[l // 2] >> (32 * (l % 2))) & 0xFFFFFFFF
+                              for l in range(len(self.tables))]
+                    control = None if self.dense else [list(w) for w in zip(*rows[2:])]
+                launches += count
+                if control is not None:
+                    self._absorb(control)
+                if any(status):
+                    faults = [l for l, s in enumerate(status) if s & nat.TRACE_FAULT]
+                    if faults:
+                        self._fault(faults)
                 behind = [l for l, p in enumerate(positions) if p < target]
                 if not behind:
                     self._status_clean = not any(status)
@@ -1597,7 +1644,7 @@ class DecodeTrace:
                 grown = [self.tables[l] for l in refused]
                 PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
                     grown, self.need(),
-                    free_counts=[report[2 + nat.CTRL_FREE][l] for l in refused])
+                    free_counts=[control[l][nat.CTRL_FREE] for l in refused])
                 for st in grown:
                     st.proven_maximum_additional_allocations += self.need()
                 self.status.zero_()

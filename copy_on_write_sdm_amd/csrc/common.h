@@ -81,6 +81,7 @@ struct StepParams {
   int64_t scan_words;            // words per layer in `scan`
   int64_t* control;              // packed persistent launches: COWSDM_CTRL_* words
   int64_t control_stride;        // word k of layer l at control[k * stride + l]
+  int64_t* report;               // host-mapped COWSDM_REPORT_WORDS per layer, or null
   int32_t plan_steps;            // steps per launch a plan block holds
   int32_t count_table;           // count pass: LDS hash entries per bank (N > kTraceMapSlots)
   int32_t steps;                 // persistent launches: steps per launch
@@ -204,6 +205,30 @@ __device__ __forceinline__ bool tag_is(uint64_t w, uint32_t epoch) {
 }
 __device__ __forceinline__ int64_t& control_word(const StepParams& P, int layer, int k) {
   return P.control[static_cast<int64_t>(k) * P.control_stride + layer];
+}
+
+// A layer's report in host memory, lane k of the calling wave writing word
+// k: the step counter `step`, the status bits (with `extra` set) and the
+// control words.  Called by one wave once no other wave of the layer
+// changes them.
+__device__ __forceinline__ void write_report(const StepParams& P, int layer, int64_t step,
+                                             int32_t extra) {
+  const int k = static_cast<int>(threadIdx.x) & (kWave - 1);
+  if (k >= COWSDM_REPORT_WORDS) return;
+  int64_t v = 0;
+  if (k == 0) {
+    v = step;
+  } else if (k == 1) {
+    const int32_t status = P.trace_status ? __hip_atomic_load(&P.trace_status[layer],
+                                                              __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT)
+                                          : 0;
+    v = static_cast<uint32_t>(status | extra);
+  } else if (P.control) {
+    v = static_cast<int64_t>(atomic_load_u64(&control_word(P, layer, k - 2)));
+  }
+  __hip_atomic_store(P.report + static_cast<int64_t>(layer) * COWSDM_REPORT_WORDS + k, v,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // The steps a trace launch runs for a layer: its first step (from the

@@ -34,8 +34,10 @@
 #include <stdarg.h>
 
 #include <mutex>
+#include <unordered_map>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 
 #include "common.h"
 #include "cowsdm.h"
@@ -767,6 +769,9 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   int vec = row_vec(layers, nlayers, shape, dense, trace);
   if (trace) {
     if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
+    if (trace->report && !trace->step_index) {
+      return fail(COWSDM_EARG, "trace: a report needs the device step counters");
+    }
     if (trace->first_step < 0) return fail(COWSDM_EARG, "trace: negative first step");
     if (trace->steps_recorded <= 0) return fail(COWSDM_EARG, "trace: no recorded steps");
     if (!trace->step_index && trace->first_step + steps > trace->steps_recorded) {
@@ -815,6 +820,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   P.control = planned ? trace->control : nullptr;
   P.control_stride = planned ? trace->control_stride : 0;
   P.plan_steps = planned ? trace->scan_steps : 0;
+  P.report = persistent ? trace->report : nullptr;
   P.count_table = 0;
   P.steps = steps;
   for (int k = 0; k < 9; ++k) P.trace_stride[k] = trace ? trace->stride_bytes[k] : 0;
@@ -953,6 +959,19 @@ int32_t static_scan(int64_t** out, const StaticLayout& layout, int64_t words,
   return 0;
 }
 
+// ---- host-mapped trace reports: the device address of each allocation
+// (what trace->report holds) to its host address
+namespace {
+std::mutex g_report_lock;
+std::unordered_map<const int64_t*, int64_t*> g_report_host;
+}  // namespace
+
+int64_t* report_host(const int64_t* device) {
+  std::lock_guard<std::mutex> hold(g_report_lock);
+  auto it = g_report_host.find(device);
+  return it == g_report_host.end() ? nullptr : it->second;
+}
+
 }  // namespace cowsdm_impl
 
 using namespace cowsdm_impl;
@@ -983,6 +1002,49 @@ int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
   // epoch and header, plan words [steps][banks], step totals, running totals
   // and the launch's pops (at most banks * W per step), int64 each
   return kPlanHead + kPlanHeadWords + banks * steps + steps + (steps + 1) + banks * steps * writes;
+}
+
+int32_t cowsdm_host_report_alloc(int64_t words, int64_t** host, int64_t** device) {
+  if (!host || !device || words <= 0) return fail(COWSDM_EARG, "host report: bad arguments");
+  void* h = nullptr;
+  hipError_t e = hipHostMalloc(&h, static_cast<size_t>(words) * sizeof(int64_t),
+                               hipHostMallocMapped | hipHostMallocCoherent);
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "host report: hipHostMalloc: %s", hipGetErrorString(e));
+  }
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, h, 0);
+  if (e != hipSuccess || !d) {
+    (void)hipHostFree(h);
+    return fail(e != hipSuccess ? static_cast<int32_t>(e) : COWSDM_EARG,
+                "host report: hipHostGetDevicePointer: %s", hipGetErrorString(e));
+  }
+  memset(h, 0, static_cast<size_t>(words) * sizeof(int64_t));
+  {
+    std::lock_guard<std::mutex> hold(g_report_lock);
+    g_report_host[static_cast<int64_t*>(d)] = static_cast<int64_t*>(h);
+  }
+  *host = static_cast<int64_t*>(h);
+  *device = static_cast<int64_t*>(d);
+  return 0;
+}
+
+int32_t cowsdm_host_report_free(int64_t* host) {
+  if (!host) return 0;
+  {
+    std::lock_guard<std::mutex> hold(g_report_lock);
+    for (auto it = g_report_host.begin(); it != g_report_host.end(); ++it) {
+      if (it->second == host) {
+        g_report_host.erase(it);
+        break;
+      }
+    }
+  }
+  const hipError_t e = hipHostFree(host);
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "host report: hipHostFree: %s", hipGetErrorString(e));
+  }
+  return 0;
 }
 
 int32_t cowsdm_trace_timing(int32_t enable) {
@@ -1079,6 +1141,64 @@ int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nl
     t.scan_words = per_layer;
   }
   return run_step(layers, nlayers, shape, false, as_stream(stream), &t, steps);
+}
+
+int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
+                         const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                         int64_t steps, int32_t launch_steps, int32_t mode, void* stream) {
+  if (!trace || !trace->report || !trace->step_index || !trace->status) {
+    return fail(COWSDM_EARG, "trace run: needs the step counters, status words and a report");
+  }
+  if (mode < 0 || mode > 2 || launch_steps <= 0 || steps < 0 || nlayers <= 0 ||
+      nlayers > kMaxLayers) {
+    return fail(COWSDM_EARG, "trace run: bad mode, layer count or step counts");
+  }
+  int64_t* const host = report_host(trace->report);
+  if (!host) return fail(COWSDM_EARG, "trace run: the report is not from cowsdm_host_report_alloc");
+  for (int32_t l = 0; l < nlayers; ++l) host[l * COWSDM_REPORT_WORDS] = -1;   // not written yet
+  hipStream_t s = as_stream(stream);
+  for (int64_t done = 0; done < steps; done += launch_steps) {
+    const int32_t n = static_cast<int32_t>(steps - done < launch_steps ? steps - done : launch_steps);
+    const int32_t rc =
+        mode == 0 ? cowsdm_packed_step_trace(layers, nlayers, shape, trace, n, stream)
+        : mode == 1 ? cowsdm_packed_step_trace_static(layers, nlayers, shape, trace, n, stream)
+                    : cowsdm_dense_step_trace(layers, nlayers, shape, trace, n, stream);
+    if (rc != 0) return rc;
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "trace run: %s", hipGetErrorString(e));
+  }
+  bool written = true;
+  for (int32_t l = 0; l < nlayers; ++l) written = written && host[l * COWSDM_REPORT_WORDS] >= 0;
+  if (written) return 0;
+  // launches of one step each (no persistent kernel fits) write no report:
+  // read the words from the device
+  int64_t counters[kMaxLayers];
+  int32_t status[kMaxLayers];
+  e = hipMemcpy(counters, trace->step_index, sizeof(int64_t) * nlayers, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) {
+    e = hipMemcpy(status, trace->status, sizeof(int32_t) * nlayers, hipMemcpyDeviceToHost);
+  }
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "trace run: report: %s", hipGetErrorString(e));
+  }
+  for (int32_t l = 0; l < nlayers; ++l) {
+    int64_t* const col = host + l * COWSDM_REPORT_WORDS;
+    col[0] = counters[l];
+    col[1] = static_cast<uint32_t>(status[l]);
+    for (int k = 0; k < COWSDM_CTRL_WORDS; ++k) {
+      col[2 + k] = 0;
+      if (trace->control && mode != 2) {
+        e = hipMemcpy(&col[2 + k], trace->control + k * trace->control_stride + l,
+                      sizeof(int64_t), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) {
+          return fail(static_cast<int32_t>(e), "trace run: report: %s", hipGetErrorString(e));
+        }
+      }
+    }
+  }
+  return 0;
 }
 
 int32_t cowsdm_dense_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,

@@ -266,6 +266,9 @@ void sdm_trace_kernel(StepParams P) {
                               __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    if (P.report && threadIdx.x < kWave && blockIdx.x % P.blocks_per_layer == 0) {
+      write_report(P, layer_id, first, COWSDM_TRACE_ENDED);
+    }
     return;  // whole workgroup
   }
   const int N = P.slots;
@@ -627,7 +630,10 @@ void sdm_trace_kernel(StepParams P) {
       if (w & kPlanReady) {
         const int planned = static_cast<int>(w & ~kPlanReady);
         G = planned < G ? planned : G;
-        if (G <= 0) return;
+        if (G <= 0) {
+          if (lane == 0) sync_store(&sync[1], kNoStop);   // finished (see below)
+          return;
+        }
       } else {
         go = false;
       }
@@ -681,8 +687,13 @@ void sdm_trace_kernel(StepParams P) {
         __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      sync_store(&sync[1], kNoStop);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);   // the bits have reached the coherent point
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
+    // finished: the control wave waits for this before it reports the layer
+    // (and no later step of the launch waits on this wave)
+    if (lane == 0) sync_store(&sync[1], kNoStop);
     return;
   }
 
@@ -1541,18 +1552,44 @@ void sdm_trace_kernel(StepParams P) {
   // counter and (packed) the plan's epoch.  Every wave of the layer read both
   // before taking its ticket.  The data waves' row stores need no ordering
   // here: the next launch on the stream starts after this one has ended.
+  // With a report to write, each control wave first waits for its data wave
+  // to finish, so that the last ticket follows every status bit of the layer.
   if (!DENSE || P.trace_step) {
+    if (P.report) {
+      bool finished = false;
+      for (int spins = 0; spins < 64 * kSpinLimit && !finished; ++spins) {
+        finished = sync_load(&sync[1]) == kNoStop;
+        if (!finished) __builtin_amdgcn_s_sleep(1);
+      }
+      if (!finished && lane == 0 && P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // The status bits and control words are device-scope atomics, which
+    // every wave performs at the same coherent point: once this wave's have
+    // completed (the wait), a wave that takes a later ticket and then loads
+    // them sees them.  No release fence: on this chip it writes back the
+    // whole L2 of the wave's XCD.
+    if (P.report) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    }
     int64_t done = 0;
     if (lane == 0) {
       int64_t* const ticket = P.trace_ticket + 1 + layer_id;
       done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1 && lane == 0) {
-      atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
-      if (P.trace_step) {
-        atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
+      if (lane == 0) {
+        atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
+        if (P.trace_step) {
+          atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(first + done_steps));
+        }
+        if constexpr (!DENSE) atomic_store_u64(pb.epoch, static_cast<uint64_t>(epoch));
       }
-      if constexpr (!DENSE) atomic_store_u64(pb.epoch, static_cast<uint64_t>(epoch));
+      if (P.report) write_report(P, layer_id, first + done_steps, 0);
     }
   }
 }
@@ -1676,6 +1713,7 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
     if (P0.trace_ticket) Q.trace_ticket = P0.trace_ticket + l0;  // word 1 + layer
     if (P0.trace_status) Q.trace_status = P0.trace_status + l0;
     if (P0.control) Q.control = P0.control + l0;
+    if (P0.report) Q.report = P0.report + static_cast<int64_t>(l0) * COWSDM_REPORT_WORDS;
     if (P0.scan) Q.scan = P0.scan + static_cast<int64_t>(l0) * P0.scan_words;
     launch(&Q, Q.blocks_per_layer * Q.nlayers, l0 + per_launch >= P0.nlayers);
   }

@@ -231,7 +231,7 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
   if (F0 < 0 || F0 > C0) {
     // a corrupt free count: the layer runs nothing
     if (lane == 0) {
-      control_word(P, layer, COWSDM_CTRL_STEPS) = 0;
+      atomic_store_u64(&control_word(P, layer, COWSDM_CTRL_STEPS), 0);
       __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                             static_cast<int64_t>(COWSDM_ERR_CORRUPT), __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
@@ -431,14 +431,20 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
     } else if (nseg > 1) {
       *L.overflow_flag = 0;   // grow_capacity clears it
     }
-    control_word(P, layer, COWSDM_CTRL_PROVEN) = over ? 0 : proven;
-    control_word(P, layer, COWSDM_CTRL_CAPACITY) = capacity;
-    control_word(P, layer, COWSDM_CTRL_EVENTS) = events0 + events;
-    control_word(P, layer, COWSDM_CTRL_ADDED) = added0 + rows_added;
-    control_word(P, layer, COWSDM_CTRL_COPIED) = copied0 + rows_copied;
-    control_word(P, layer, COWSDM_CTRL_FREE) = height;
-    control_word(P, layer, COWSDM_CTRL_STEPS) = stop;
-    control_word(P, layer, COWSDM_CTRL_FIT) = vlen;
+    // device-scope stores: the layer's report reads them back during the
+    // launch, possibly from another XCD, whose L2 does not see this one's
+    // dirty lines
+    auto put = [&](int k, int64_t v) __attribute__((always_inline)) {
+      atomic_store_u64(&control_word(P, layer, k), static_cast<uint64_t>(v));
+    };
+    put(COWSDM_CTRL_PROVEN, over ? 0 : proven);
+    put(COWSDM_CTRL_CAPACITY, capacity);
+    put(COWSDM_CTRL_EVENTS, events0 + events);
+    put(COWSDM_CTRL_ADDED, added0 + rows_added);
+    put(COWSDM_CTRL_COPIED, copied0 + rows_copied);
+    put(COWSDM_CTRL_FREE, height);
+    put(COWSDM_CTRL_STEPS, stop);
+    put(COWSDM_CTRL_FIT, vlen);
     if (stop < G0 && P.trace_status) {
       __hip_atomic_fetch_or(&P.trace_status[layer], int32_t{COWSDM_TRACE_REFUSED},
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 5
+#define COWSDM_ABI_VERSION 6
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -158,6 +158,7 @@ typedef struct cowsdm_trace {
   int32_t* status;          /* per-layer COWSDM_TRACE_* bits, or null */
   int64_t* control;         /* packed persistent launches, see above */
   int64_t control_stride;
+  int64_t* report;          /* host-mapped report (COWSDM_REPORT_WORDS per layer), or null */
 } cowsdm_trace_t;
 
 /* Control words of one layer of a packed decode trace (int64, word k of
@@ -186,6 +187,17 @@ typedef struct cowsdm_trace {
 #define COWSDM_CTRL_STEPS 9
 #define COWSDM_CTRL_FIT 10
 #define COWSDM_CTRL_WORDS 12
+
+/* The report a trace launch writes when trace->report is set: word k of
+ * layer l at report[l * COWSDM_REPORT_WORDS + k], written by the layer's
+ * last wave once every wave of the layer is done with the launch, into
+ * host memory the device can write (cowsdm_host_report_alloc):
+ *   0      the layer's step counter after the launch
+ *   1      its status bits (COWSDM_TRACE_*)
+ *   2 + k  control word k (packed persistent launches; 0 otherwise)
+ * A host that waits for the launch's stream reads the layer's state there
+ * without a device-to-host copy. */
+#define COWSDM_REPORT_WORDS (2 + COWSDM_CTRL_WORDS)
 
 /* Bits of a decode trace's per-layer status word (sticky: the kernels only
  * set them). */
@@ -220,6 +232,12 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
  * the summed launch time (first kernel's start to the decode kernel's end)
  * and the summed decode-kernel time in milliseconds and the number of
  * launches, and forgets them.  cowsdm_trace_timing(0) stops recording. */
+/* Host memory the device can write, for trace reports: `words` int64
+ * words, zeroed; *host is the host's address of it, *device the device's.
+ * Free with cowsdm_host_report_free(host) once no launch writes it. */
+int32_t cowsdm_host_report_alloc(int64_t words, int64_t** host, int64_t** device);
+int32_t cowsdm_host_report_free(int64_t* host);
+
 int32_t cowsdm_trace_timing(int32_t enable);
 int32_t cowsdm_trace_timing_read(double* launch_ms, double* kernel_ms, int32_t* launches);
 /* Bytes of lifecycle workspace for a ranking over `entries` map entries
@@ -271,6 +289,18 @@ int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nl
                                         const cowsdm_shape_t* shape,
                                         const cowsdm_trace_t* trace, int32_t steps,
                                         void* stream);
+
+/* The decode loop's launches for `steps` steps of every layer from their
+ * device counters, `launch_steps` steps per launch (mode 0:
+ * cowsdm_packed_step_trace, 1: cowsdm_packed_step_trace_static, 2:
+ * cowsdm_dense_step_trace), then a wait for the stream.  trace->step_index
+ * and trace->report must be set: on return each layer's report holds its
+ * step counter, status and control words after its last launch.  No
+ * counterpart in the reference; its decode loop (inference.py:538-566)
+ * calls one step at a time. */
+int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
+                         const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
+                         int64_t steps, int32_t launch_steps, int32_t mode, void* stream);
 
 /* Dense-table control step on values = memory [B, N, D].
  * Replaces _dense_sdm_sparse_step_triton, allocator.py:1322-1378 (kernel

@@ -38,7 +38,7 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 5
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 6
     # epoch and header, plan words [steps][banks], step and running totals,
     # at most banks * W pops per step, int64 each
     assert lib.cowsdm_trace_scan_words(64, 4, 512) == 16 + 64 * 512 + 512 + 513 + 64 * 512 * 4
@@ -74,6 +74,31 @@ def test_argument_errors_return_codes_without_launching():
                                        ctypes.byref(trace), 0) == 0
 
 
+def test_trace_run_argument_errors_without_launching():
+    lib = nat.lib()
+    shape = nat.Shape(banks=4, slots=16, width=8, writes=4, reads=4, templates=1,
+                      index_dtype=0)
+    layer = nat.Layer()
+    trace = nat.Trace()
+    # no report, no step counters: refused before any launch
+    assert lib.cowsdm_trace_run(ctypes.byref(layer), 1, ctypes.byref(shape),
+                                ctypes.byref(trace), 4, 4, nat.RUN_PACKED, None) == -1
+    assert b"report" in lib.cowsdm_last_error_string()
+    words = (ctypes.c_int64 * 64)()
+    trace.step_index = trace.status = trace.report = ctypes.addressof(words)
+    assert lib.cowsdm_trace_run(ctypes.byref(layer), 1, ctypes.byref(shape),
+                                ctypes.byref(trace), 4, 0, nat.RUN_PACKED, None) == -1
+    assert lib.cowsdm_trace_run(ctypes.byref(layer), 1, ctypes.byref(shape),
+                                ctypes.byref(trace), 4, 4, 7, None) == -1
+    # a report the library did not allocate
+    assert lib.cowsdm_trace_run(ctypes.byref(layer), 1, ctypes.byref(shape),
+                                ctypes.byref(trace), 4, 4, nat.RUN_PACKED, None) == -1
+    assert b"cowsdm_host_report_alloc" in lib.cowsdm_last_error_string()
+    host, device = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.cowsdm_host_report_alloc(0, ctypes.byref(host), ctypes.byref(device)) == -1
+    assert lib.cowsdm_host_report_free(None) == 0
+
+
 def test_trace_timing_without_launches():
     lib = nat.lib()
     assert lib.cowsdm_trace_timing(1) == 0
@@ -89,7 +114,8 @@ def test_structure_layout_matches_header():
     # 21 pointer-sized fields and one int64 in cowsdm_layer_t
     assert ctypes.sizeof(nat.Layer) == 21 * 8
     assert ctypes.sizeof(nat.Shape) == 7 * 8
-    assert ctypes.sizeof(nat.Trace) == 19 * 8
+    assert ctypes.sizeof(nat.Trace) == 20 * 8
+    assert nat.REPORT_WORDS == 2 + nat.CTRL_WORDS == 14
 
 
 @pytest.mark.parametrize("name", ["cowsdm_packed_step", "cowsdm_dense_step",

@@ -8,6 +8,8 @@ the CPU oracle (oracle/state.py restating allocator.py:506-1095) exactly.
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -267,7 +269,7 @@ def test_invariant_violations_are_reported(device):
     st, _, _ = _pair(device, steps=4)
     live = st.logical_to_physical[st.logical_to_physical >= 0]
     # two owners of one row
-    bad = cow.PackedSDMCopyOnWriteState(**{**st.__dict__})
+    bad = dataclasses.replace(st)
     bad.logical_to_physical = st.logical_to_physical.clone()
     flat = bad.logical_to_physical.view(-1)
     owners = (flat >= 0).nonzero().flatten()
@@ -275,19 +277,19 @@ def test_invariant_violations_are_reported(device):
     with pytest.raises(AssertionError, match="multiple logical owners"):
         bad.validate_invariants()
     # free stack duplicate
-    bad = cow.PackedSDMCopyOnWriteState(**{**st.__dict__})
+    bad = dataclasses.replace(st)
     bad.free_rows = st.free_rows.clone()
     if int(st.free_count) >= 2:
         bad.free_rows[1] = bad.free_rows[0]
         with pytest.raises(AssertionError, match="free SDM row stack contains duplicates"):
             bad.validate_invariants()
     # coverage
-    bad = cow.PackedSDMCopyOnWriteState(**{**st.__dict__})
+    bad = dataclasses.replace(st)
     bad.free_count = st.free_count.clone() - 1
     with pytest.raises(AssertionError, match="do not cover capacity"):
         bad.validate_invariants()
     # overflow flag
-    bad = cow.PackedSDMCopyOnWriteState(**{**st.__dict__})
+    bad = dataclasses.replace(st)
     bad.overflow_flag = torch.ones((), dtype=torch.int32, device=device)
     with pytest.raises(AssertionError, match="recorded a slab overflow"):
         bad.validate_invariants()
