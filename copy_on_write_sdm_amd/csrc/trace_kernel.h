@@ -1261,6 +1261,8 @@ void sdm_trace_kernel(StepParams P) {
   // ---- the launch's plan (packed; trace_plan.h), before any step
   if constexpr (!DENSE) {
     bool ok = true;
+    PlanControl pc{};
+    if (bank == 0) pc = plan_control(P, layer_id);
     if constexpr (MAPLDS) {
       // count part: this bank's first touches, step by step.  A slot is
       // first-touched by the launch's first step that writes it, unless it
@@ -1274,8 +1276,9 @@ void sdm_trace_kernel(StepParams P) {
       uint32_t mapped[KC];
       int err_step = (base_err & COWSDM_ERR_TEMPLATE) ? 0 : G0;
       int err_bits[KC];
-      // the slots of chunk c + 1 load while chunk c is checked
-      IDX sbuf[2][kIdxRow];
+      // the slots of chunks c + 1 .. c + kAhead load while chunk c is checked
+      constexpr int kAhead = sizeof(IDX) == 4 ? 2 : 1;
+      IDX sbuf[kAhead + 1][kIdxRow];
       auto load_slots = [&](int c, IDX (&dst)[kIdxRow]) __attribute__((always_inline)) {
         const int t = c * kWave + lane;
         const int tc = t < G0 ? t : G0 - 1;
@@ -1306,7 +1309,10 @@ void sdm_trace_kernel(StepParams P) {
           }
         }
       };
-      load_slots(0, sbuf[0]);
+#pragma unroll
+      for (int c = 0; c < kAhead; ++c) {
+        if (c * kWave < G0) load_slots(c, sbuf[c]);
+      }
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const int t = c * kWave + lane;
@@ -1315,8 +1321,8 @@ void sdm_trace_kernel(StepParams P) {
 #pragma unroll
         for (int j = 0; j < kTraceMaxWrites; ++j) wsl[c][j] = -1;
         if (c * kWave >= G0) continue;
-        if ((c + 1) * kWave < G0) load_slots(c + 1, sbuf[(c + 1) & 1]);
-        const IDX (&cur)[kIdxRow] = sbuf[c & 1];
+        if ((c + kAhead) * kWave < G0) load_slots(c + kAhead, sbuf[(c + kAhead) % (kAhead + 1)]);
+        const IDX (&cur)[kIdxRow] = sbuf[c % (kAhead + 1)];
         int e = 0;
 #pragma unroll
         for (int j = 0; j < kTraceMaxWrites; ++j) {
@@ -1335,7 +1341,7 @@ void sdm_trace_kernel(StepParams P) {
             const int64_t v = static_cast<int64_t>(cur[kTraceMaxWrites + i]);
             if (v < 0 || v >= N) {
               e |= COWSDM_ERR_READ_INDEX;
-            } else if (lds_map[v] >= C0) {
+            } else if (any_bad && lds_map[v] >= C0) {
               e |= COWSDM_ERR_CORRUPT;
             }
           }
@@ -1394,10 +1400,17 @@ void sdm_trace_kernel(StepParams P) {
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    // prefix part (steps bank, bank + B, ...), the layer part (bank 0), the
-    // header
-    ok = plan_prefix(pb, bank, B, G0, epoch);
-    if (bank == 0) ok = plan_layer(P, layer_id, pb, B, G0, epoch, &lds_idx[0][0][0][0]) && ok;
+    // prefix part (a contiguous share of the steps per bank), the layer part
+    // (bank 0), the header
+    {
+      const int per = (G0 + B - 1) / B;
+      const int t0 = bank * per < G0 ? bank * per : G0;
+      ok = plan_prefix(pb, B, epoch, t0, t0 + per < G0 ? t0 + per : G0);
+    }
+    if (bank == 0) {
+      ok = plan_layer(P, layer_id, pb, B, G0, epoch, &lds_idx[0][0][0][0], &lds_plan[pair][0],
+                      pc) && ok;
+    }
     int steps = 0, fit = 0, capacity = C0;
     ok = plan_header(pb, epoch, steps, fit, capacity) && ok;
     if (!ok) {

@@ -19,9 +19,9 @@
 //   the bank's first step with an invalid route, after which the bank takes
 //   no step, as count words;
 //
-//   prefix (every control wave, steps bank, bank + B, ...): for each of its
-//   steps, the first touches of the lower banks at that step (a scan across
-//   the banks' count words) and the step's total;
+//   prefix (every control wave, a contiguous share of the steps): for each
+//   of its steps, the first touches of the lower banks at that step (a scan
+//   across the banks' count words) and the step's total;
 //
 //   layer (the control wave of bank 0): the running totals over the steps,
 //   the decode loop's proof step by step from the control words (growing
@@ -44,14 +44,17 @@
 
 namespace cowsdm_impl {
 
-// Wave-inclusive sum over lanes (lane order).
+// Wave-inclusive sum over lanes (lane order), in DPP moves: shifts by 1, 2,
+// 4 and 8 lanes within each row of 16, then row 0's and row 1's last lanes
+// broadcast into the rows after them (a lane shifted in from outside its
+// row, or a row the mask leaves out, adds the identity 0).
 __device__ __forceinline__ int wave_inclusive(int v) {
-  const int lane = static_cast<int>(threadIdx.x) % kWave;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(v, o, kWave);
-    if (lane >= o) v += y;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2 and 3
   return v;
 }
 
@@ -88,18 +91,15 @@ __device__ __forceinline__ int64_t plan_div(int64_t a, int64_t b) {
   return a / b;
 }
 
-// Prefix part: this wave's range of steps (a contiguous share of the G0
-// steps), each against every bank (lane = bank): waits for the banks' count
-// words of the step, replaces each with its prefix word and publishes the
-// step's total.  A bank's words of consecutive steps are contiguous, so a
-// lane loads kBatch steps at once.  False when a count never arrives.
-__device__ inline bool plan_prefix(const PlanBlock& pb, int bank, int B, int G0,
-                                   uint32_t epoch) {
+// Prefix part over steps [t_begin, t_end), each against every bank (lane =
+// bank): waits for the banks' count words of the step, replaces each with
+// its prefix word and publishes the step's total.  A bank's words of
+// consecutive steps are contiguous, so a lane loads kBatch steps at once,
+// and the batch is polled together.  False when a count never arrives.
+__device__ inline bool plan_prefix(const PlanBlock& pb, int B, uint32_t epoch, int t_begin,
+                                   int t_end) {
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   constexpr int kBatch = 8;
-  const int per = (G0 + B - 1) / B;
-  const int t_begin = bank * per;
-  const int t_end = t_begin + per < G0 ? t_begin + per : G0;
   for (int tb = t_begin; tb < t_end; tb += kBatch) {
     int carry[kBatch];
 #pragma unroll
@@ -112,17 +112,27 @@ __device__ inline bool plan_prefix(const PlanBlock& pb, int bank, int B, int G0,
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int t = tb + i < t_end ? tb + i : t_end - 1;
-        w[i] = atomic_load_u64(row + t);
+        w[i] = in ? atomic_load_u64(row + t) : tagged(epoch, 0);
+      }
+      // each round reloads only the words still missing, so the batch waits
+      // one round trip past its last count rather than one per step
+      for (int spins = 0;; ++spins) {
+        bool missing = false;
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) missing |= tb + i < t_end && !tag_is(w[i], epoch);
+        if (__ballot(missing) == 0) break;
+        if (spins >= kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+          if (tb + i < t_end && !tag_is(w[i], epoch)) w[i] = atomic_load_u64(row + tb + i);
+        }
       }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int t = tb + i;
         if (t >= t_end) break;
-        uint64_t x = in ? w[i] : tagged(epoch, 0);
-        if (__ballot(in && !tag_is(x, epoch)) != 0 && !poll_tagged(row + t, in, epoch, x)) {
-          return false;
-        }
-        const uint32_t v = static_cast<uint32_t>(x) & (kCountStop | 15u);
+        const uint32_t v = static_cast<uint32_t>(w[i]) & (kCountStop | 15u);
         const int c = __popc(v & 15u);
         const int incl = wave_inclusive(c);
         if (in) {
@@ -144,12 +154,36 @@ __device__ inline bool plan_prefix(const PlanBlock& pb, int bank, int B, int G0,
   return true;
 }
 
-// Layer part, by one wave (the control wave of bank 0).  `seg` is LDS of
-// 4 * kPlanSegments ints: the launch's growth segments.  Publishes the running totals, the pops and the
-// header (last); false when a step total never arrives (the header then
-// says the layer runs no step).
+// The words the layer part starts from: the control words and the free
+// count the launch found.  Loaded by the layer part's wave at its start, so
+// that their latency hides behind the count and prefix parts.
+struct PlanControl {
+  int64_t capacity, proven, room, quantum, need, events, added, copied;
+  int32_t free_count;
+};
+__device__ __forceinline__ PlanControl plan_control(const StepParams& P, int layer) {
+  PlanControl c;
+  c.capacity = control_word(P, layer, COWSDM_CTRL_CAPACITY);
+  c.proven = control_word(P, layer, COWSDM_CTRL_PROVEN);
+  c.room = control_word(P, layer, COWSDM_CTRL_ROOM);
+  c.quantum = control_word(P, layer, COWSDM_CTRL_QUANTUM);
+  c.need = control_word(P, layer, COWSDM_CTRL_NEED);
+  c.events = control_word(P, layer, COWSDM_CTRL_EVENTS);
+  c.added = control_word(P, layer, COWSDM_CTRL_ADDED);
+  c.copied = control_word(P, layer, COWSDM_CTRL_COPIED);
+  c.free_count = *P.layer[layer].free_count;
+  return c;
+}
+
+// Layer part, by one wave (the control wave of bank 0), from the control
+// words `pc` it loaded at the launch's start.  `seg` is LDS of
+// 4 * kPlanSegments ints: the launch's growth segments; `jump` LDS of
+// kTraceMaxSteps ints for the proof's jump table.  Publishes the running
+// totals, the pops and the header (last); false when a step total never
+// arrives (the header then says the layer runs no step).
 __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBlock& pb, int B,
-                                  int G0, uint32_t epoch, int* seg) {
+                                  int G0, uint32_t epoch, int* seg, int* jump,
+                                  const PlanControl& pc) {
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const cowsdm_layer_t& L = P.layer[layer];
   constexpr int K = kTraceMaxSteps / kWave;
@@ -171,17 +205,15 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
     }
   };
 
-  // the launch's control words and free count, loaded first so that their
-  // latency overlaps the wait for the step totals
-  const int64_t C0 = uniform64(control_word(P, layer, COWSDM_CTRL_CAPACITY));
-  int64_t proven = uniform64(control_word(P, layer, COWSDM_CTRL_PROVEN));
-  const int64_t room = uniform64(control_word(P, layer, COWSDM_CTRL_ROOM));
-  const int64_t quantum = uniform64(control_word(P, layer, COWSDM_CTRL_QUANTUM));
-  const int64_t need = uniform64(control_word(P, layer, COWSDM_CTRL_NEED));
-  const int64_t events0 = uniform64(control_word(P, layer, COWSDM_CTRL_EVENTS));
-  const int64_t added0 = uniform64(control_word(P, layer, COWSDM_CTRL_ADDED));
-  const int64_t copied0 = uniform64(control_word(P, layer, COWSDM_CTRL_COPIED));
-  const int F0 = __builtin_amdgcn_readfirstlane(*L.free_count);
+  const int64_t C0 = uniform64(pc.capacity);
+  int64_t proven = uniform64(pc.proven);
+  const int64_t room = uniform64(pc.room);
+  const int64_t quantum = uniform64(pc.quantum);
+  const int64_t need = uniform64(pc.need);
+  const int64_t events0 = uniform64(pc.events);
+  const int64_t added0 = uniform64(pc.added);
+  const int64_t copied0 = uniform64(pc.copied);
+  const int F0 = __builtin_amdgcn_readfirstlane(pc.free_count);
 
   // ---- running totals: lane l holds the first touches before steps l,
   // l + 64, ... (exclusive), cum_g all of them
@@ -221,7 +253,8 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
   // lane l's value for step s = 64k + l of a per-lane array (s wave-uniform:
   // a register picked by index, then one lane read)
   auto step_value = [&](const int (&v)[K], int s) __attribute__((always_inline)) -> int {
-    return __builtin_amdgcn_readlane(v[s >> 6], s & (kWave - 1));
+    return G0 <= kWave ? __builtin_amdgcn_readlane(v[0], s)
+                       : __builtin_amdgcn_readlane(v[s >> 6], s & (kWave - 1));
   };
   // first touches before step s (s in [0, G0]), wave-uniform
   auto cum_at = [&](int s) __attribute__((always_inline)) -> int {
@@ -273,6 +306,39 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
         hop[k] = static_cast<int>(j < G0 - t ? j : G0 - t);
       }
     };
+    // A long run of reads without a growth is walked through a jump table
+    // (LDS): from each step, the step 2^R reads later, or the first step
+    // that grows or the last read before it when one comes first (pointer
+    // doubling over the hops, R rounds).
+    auto build_jumps = [&](int rounds) __attribute__((always_inline)) {
+      int cur[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int t = k * kWave + lane;
+        cur[k] = t < G0 && hop[k] > 0 && t + hop[k] < G0 ? t + hop[k] : t;
+        if (t < G0) jump[t] = cur[k];
+      }
+      for (int r = 0; r < rounds; ++r) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        int nxt[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int t = k * kWave + lane;
+          nxt[k] = k * kWave < G0 && t < G0 ? jump[cur[k]] : t;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int t = k * kWave + lane;
+          cur[k] = nxt[k];
+          if (t < G0) jump[t] = cur[k];
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     int s = 0;
     if (proven >= need) {
       // steps still covered by the proof the launch starts with
@@ -284,9 +350,19 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
     }
     if (!over && s < G0) hops();
     // from here every step whose proof runs short re-reads free_count
+    bool jumps = false;   // the table matches the hops
+    int walked = 0;       // reads walked one by one since the hops last changed
     while (!over && s < G0) {
+      if (jumps) {
+        for (int n = __builtin_amdgcn_readfirstlane(jump[s]); n != s;
+             n = __builtin_amdgcn_readfirstlane(jump[s])) {
+          s = n;
+        }
+      }
       int h = step_value(hop, s);
       if (h == 0) {
+        jumps = false;
+        walked = 0;
         const int64_t free_rows = F0 + added - cum_at(s);
         const int64_t want = capacity + need - free_rows;
         const int64_t selected = plan_div(want + quantum - 1, quantum) * quantum;
@@ -312,6 +388,14 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
         s = G0;
       } else {
         s += h;
+        if (!jumps && ++walked >= 8 && G0 - s > 16) {
+          // reads keep coming without a growth: enough rounds to cross the
+          // rest of the launch in a few jumps
+          int rounds = 1;
+          while (rounds < 9 && (1 << rounds) < G0 - s) ++rounds;
+          build_jumps(rounds);
+          jumps = true;
+        }
       }
     }
   } else if (cum_g > F0) {
