@@ -587,6 +587,16 @@ __global__ void materialize_kernel(const float* m0, int64_t templates, const int
 
 // Partition check: counts[row] += 1 per live owner and += 1<<16 per free
 // stack entry; stats as documented in cowsdm.h.
+// Adds every lane's v into *target with one atomic per wave (a wave sum
+// first): counters every thread of a grid feeds would otherwise take one
+// same-address atomic per thread.  Every lane of the wave calls it.
+__device__ __forceinline__ void wave_add_stat(int64_t* target, unsigned long long v) {
+  const int64_t sum = wave_sum64(static_cast<int64_t>(v));
+  if ((threadIdx.x & (kWave - 1)) == 0 && sum != 0) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(target), static_cast<unsigned long long>(sum));
+  }
+}
+
 __global__ void own_map_kernel(const int32_t* map, int64_t entries,
                                int64_t capacity, int32_t* counts,
                                int64_t* stats) {
@@ -600,8 +610,8 @@ __global__ void own_map_kernel(const int32_t* map, int64_t entries,
     if (p >= capacity) { ++outside; continue; }
     atomicAdd(&counts[p], 1);
   }
-  if (live) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[0]), live);
-  if (outside) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), outside);
+  wave_add_stat(&stats[0], live);
+  wave_add_stat(&stats[5], outside);
 }
 
 __global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_count,
@@ -617,7 +627,7 @@ __global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_co
     if (p < 0 || p >= capacity) { ++outside; continue; }
     atomicAdd(&counts[p], 1 << 16);
   }
-  if (outside) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[5]), outside);
+  wave_add_stat(&stats[5], outside);
   if (t0 == 0) stats[1] = f;
 }
 
@@ -635,9 +645,9 @@ __global__ void own_eval_kernel(const int32_t* counts, int64_t capacity,
     if (frees > 1) ++dup_free;
     if (owners + frees != 1) ++not_once;
   }
-  if (dup_live) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[2]), dup_live);
-  if (dup_free) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[3]), dup_free);
-  if (not_once) atomicAdd(reinterpret_cast<unsigned long long*>(&stats[4]), not_once);
+  wave_add_stat(&stats[2], dup_live);
+  wave_add_stat(&stats[3], dup_free);
+  wave_add_stat(&stats[4], not_once);
   if (t0 == 0) {
     stats[6] = *overflow;
     stats[7] = scratch ? scratch[COWSDM_SCRATCH_ERRORS] : 0;
