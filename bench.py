@@ -436,6 +436,39 @@ def main() -> int:
         torch.cuda.synchronize()
         eager = B * (n - 2) / (time.perf_counter() - t0)
 
+    # ---- the same per-token loop as one captured graph launch per token:
+    # each replay is one step of every layer with the decode loop's proof and
+    # growth decided on the device (DecodeTrace.capture(1)), no host work
+    graph_step = None
+    if eager_steps:
+        n = min(max(eager_steps, 2 * K), total_steps)
+        gtrace = cow.DecodeTrace(states=states, max_steps_per_launch=1, **inputs)
+        gtrace.reserve_steps(n)
+        gtrace.set_step(0)
+        graph = gtrace.capture(1)
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        g0.record()
+        for _ in range(n - 2):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gtrace.sync()
+        if gtrace.step_index.tolist() != [n] * LAYERS or any(gtrace.status.tolist()):
+            raise AssertionError("captured single-step decode did not run every step")
+        graph_step = {
+            "tokens_per_s": round(B * (n - 2) / wall, 1),
+            "us_per_step": round(1e6 * wall / (n - 2), 3),
+            "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / (n - 2), 3),
+            "steps": n - 2,
+            "what": "hipGraph of one planned launch (all layers, one step) replayed per token",
+        }
+        del graph
+
     # roofline of the dominant kernel, the persistent decode kernel: the
     # algorithmic bytes of the steps the timed launches ran over its mean
     # duration (HIP events at its own start and end); the count and plan
@@ -516,6 +549,7 @@ def main() -> int:
         },
         "allocator": allocator,
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
+        "graph_step": graph_step,
     }
     if not args.no_cpu_baseline and args.config == 2:
         result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)

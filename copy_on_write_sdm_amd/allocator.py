@@ -1478,6 +1478,35 @@ class DecodeTrace:
 
     # ---------------------------------------------------------- launches
 
+    def capture(self, steps: int = 1) -> "torch.cuda.CUDAGraph":
+        """A hipGraph of ``launch(steps)``: each replay runs the next
+        ``steps`` steps of every layer from the device counters, the decode
+        loop's proof and growth within the slab buffers included (packed
+        state), with no host work and no synchronisation.  With one step per
+        replay this is the reference's per-token loop (inference.py:538-566)
+        as one graph launch per token.  Uploads the control words first; call
+        ``sync()`` after the replays, and ``reserve_steps`` beforehand for
+        room to grow (a layer whose growth would pass its buffers stops with
+        COWSDM_TRACE_REFUSED in its status word).  Replays share this trace's
+        plan blocks (or the library's static ones with ``static_scan``), so
+        replays of graphs of one trace must not overlap.  No counterpart in
+        the reference."""
+
+        if steps < 1:
+            raise ValueError("a captured launch runs at least one step")
+        layers = self.layer_array()
+        if not self.dense and not self.planned:
+            raise RuntimeError("packed state needs persistent launches to decide its proof "
+                               "on the device")
+        self.upload()
+        self.status.zero_()
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=torch.cuda.Stream(self.device)):
+            self.launch(steps, layers)
+        self._positions = None
+        return graph
+
     def launch(self, steps: int, layers=None, *, start: int | None = None) -> None:
         """Run ``steps`` consecutive steps of every layer: steps
         start..start+steps-1 (packed state: the decode loop ``run``), or,

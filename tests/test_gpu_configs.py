@@ -253,3 +253,45 @@ def test_config5_full_size(device):
     1,024 Zipf steps with the growth quantum of 4 steps."""
 
     _config5(device, layers=7, steps=1024, seed=71)
+
+
+@pytest.mark.parametrize("static_scan", [False, True])
+def test_captured_single_step_decode_matches_reference_loop(device, static_scan):
+    """Config 2's shape (L=7, B=64, N=256, D=128) after a 256-token handoff,
+    decoded as one hipGraph replay per token (``DecodeTrace.capture(1)``:
+    every replay is one step of all layers with the capacity proof and the
+    growth decided on the device), equals the reference's per-token loop
+    (``decode_sdm_layer``: prepare_step_capacity(B * W), then the step) in
+    readings, maps, physical rows, free stacks, capacities, growth counters
+    and proofs.  With ``static_scan`` the replays allocate nothing."""
+
+    layers, banks, slots, prefix, steps = 7, 64, 256, 256, 40
+    quantum = banks * W * 4
+    print(f"captured single steps static_scan={static_scan}", flush=True)
+    m0 = synthetic.make_initial_memory(layers, 1, slots, D, seed=41, device=device)
+    make_states, _ = _handoff(device, m0, layers=layers, banks=banks, slots=slots,
+                              prefix=prefix, quantum=quantum, seed=42)
+    batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=43)
+    traced, host = make_states(), make_states()
+    outputs = torch.empty(steps, layers, banks, D, device=device)
+    tr = cow.DecodeTrace(states=traced, outputs=outputs, max_steps_per_launch=1,
+                         static_scan=static_scan, **kw)
+    tr.reserve_steps(steps)
+    tr.set_step(0)
+    graph = tr.capture(1)
+    for k in range(steps):
+        graph.replay()
+        if k % 7 == 3:
+            torch.cuda.synchronize()   # eager work between replays
+            assert tr.step_index.tolist() == [k + 1] * layers
+    torch.cuda.synchronize()
+    assert tr.step_index.tolist() == [steps] * layers
+    assert tr.status.tolist() == [0] * layers
+    tr.sync()
+    want = _reference_loop(host, batch, steps=steps, layers=layers)
+    torch.cuda.synchronize()
+    assert torch.equal(outputs, want)
+    assert sum(st.growth_events for st in host) > 0
+    for a, b in zip(traced, host):
+        assert_states_identical(a, b)
+        a.validate_invariants()
