@@ -12,8 +12,9 @@ requests.
 Decode loop: the reference's (inference.py:538-566: prepare_step_capacity
 (B*W) before every step of every layer, then the fused step), run as
 persistent launches of up to 512 steps for every (layer, bank), each planned
-on the device first (count and plan passes: the per-step capacity proof,
-growth within the slab's buffers, the row of every first touch).  The slab
+on the device first, inside the decode kernel (first-touch counts, the
+per-step capacity proof, growth within the slab's buffers, the row of every
+first touch).  The slab
 buffers are sized for the run before timing, so growth happens inside the
 launches; the growth counters still follow the reference's formula.
 --config 3 (2,048-token prefill, packed handoff timed) and --config 5
@@ -23,7 +24,10 @@ other single-GPU configurations; --batch sets B (1/16/64).
 Timing, as the reference's benchmark (5 warmup and 20 timed steps, median of
 5 repetitions, experiments/benchmark_serving.py:1002-1066): W untimed warmup
 steps, then 5 repetitions of exactly K steps, each between synchronisations;
-the median repetition is reported.  The dense-table control runs the same
+the median repetition is reported (0.1 s of untimed dense-control launches
+on scratch tables warm the GPU first).  The same per-token loop is also
+timed as the reference's call pattern on the per-layer kernel (eager) and as
+one captured graph replay per token (graph_step).  The dense-table control runs the same
 routes the same way from the same packed state; both end states must be
 equal.  The CPU baseline is the torch restatement of the reference's
 dense-table step on the host cores (all cores and one

@@ -129,15 +129,17 @@ typedef struct cowsdm_layer {
  * resident; layers whose workgroups do not all fit at once run as groups of
  * layers, one launch after another), else one launch per step.
  *
- * Packed persistent launches plan each launch before running it: a count
- * pass finds every (step, bank)'s first touches, and a plan pass, one
- * workgroup per layer, replays the decode loop's capacity proof
+ * Packed persistent launches plan each launch before running its steps,
+ * inside the decode kernel: every bank's control wave counts its
+ * (step, bank) first touches (a separate count kernel first when the slot
+ * map does not fit in LDS) and scans a share of the steps across banks, and
+ * one wave per layer replays the decode loop's capacity proof
  * (prepare_step_capacity(need) before every step, allocator.py:745-773,
  * inference.py:551-552), grows the slab within its buffer as grow_capacity
  * would (allocator.py:691-743), and lists the rows every first touch pops in
  * the order of single-step launches (step-major, bank-major within a step,
  * allocator.py:1471-1481), writing the free stack and free_count the launch
- * leaves.  The launch then takes its rows from that list.  Readings, maps,
+ * leaves.  The steps then take their rows from that list.  Readings, maps,
  * slab rows, free stacks and growth counters equal those of the loop of
  * single steps.  The proof state lives on the device in `control`
  * (COWSDM_CTRL_WORDS words per layer, word k of layer l at
@@ -223,21 +225,23 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
                                 const struct cowsdm_shape* shape,
                                 const struct cowsdm_trace* trace, int32_t dense);
 
-/* Kernel timing of persistent trace launches, for measurement (no
- * reference counterpart; one host thread): after cowsdm_trace_timing(1)
- * each persistent trace launch (up to 1,024) records HIP events on its
- * stream at the start of its first kernel (a packed launch's count pass), at
- * the start of its decode kernel and at the decode kernel's end
- * (hipExtLaunchKernel).  cowsdm_trace_timing_read waits for them, returns
- * the summed launch time (first kernel's start to the decode kernel's end)
- * and the summed decode-kernel time in milliseconds and the number of
- * launches, and forgets them.  cowsdm_trace_timing(0) stops recording. */
 /* Host memory the device can write, for trace reports: `words` int64
  * words, zeroed; *host is the host's address of it, *device the device's.
- * Free with cowsdm_host_report_free(host) once no launch writes it. */
+ * Free with cowsdm_host_report_free(host) once no launch writes it.  No
+ * counterpart in the reference. */
 int32_t cowsdm_host_report_alloc(int64_t words, int64_t** host, int64_t** device);
 int32_t cowsdm_host_report_free(int64_t* host);
 
+/* Kernel timing of persistent trace launches, for measurement (no
+ * reference counterpart; one host thread): after cowsdm_trace_timing(1)
+ * each persistent trace launch (up to 1,024) records HIP events on its
+ * stream at the start of its first kernel (the count kernel of a packed
+ * launch whose slot map stays in HBM, else the decode kernel), at the start
+ * of its decode kernel and at the decode kernel's end (hipExtLaunchKernel).
+ * cowsdm_trace_timing_read waits for them, returns the summed launch time
+ * (first kernel's start to the decode kernel's end) and the summed
+ * decode-kernel time in milliseconds and the number of launches, and
+ * forgets them.  cowsdm_trace_timing(0) stops recording. */
 int32_t cowsdm_trace_timing(int32_t enable);
 int32_t cowsdm_trace_timing_read(double* launch_ms, double* kernel_ms, int32_t* launches);
 /* Bytes of lifecycle workspace for a ranking over `entries` map entries
