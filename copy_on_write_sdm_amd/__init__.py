@@ -24,20 +24,34 @@ from .inference import (
     pack_prefill_layer,
 )
 from .routing import product_key_routes
+from .controller import (
+    ControllerStep,
+    SDMController,
+    decode_sdm_layer_controller,
+    decode_sdm_layer_controller_dense,
+    finish_sdm_step,
+    prepare_sdm_step,
+)
 
 __all__ = [
+    "ControllerStep",
     "DecodeTrace",
+    "SDMController",
     "FaithfulSDMDecodeState",
     "PackedSDMCopyOnWriteState",
     "SDMCopyOnWriteStep",
     "SDMStepInputs",
     "decode_sdm_layer",
+    "decode_sdm_layer_controller",
+    "decode_sdm_layer_controller_dense",
     "decode_sdm_layer_dense",
     "dense_sdm_sparse_step",
     "dense_sdm_sparse_step_layers",
+    "finish_sdm_step",
     "mark_written",
     "pack_prefill_layer",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
+    "prepare_sdm_step",
     "product_key_routes",
 ]

@@ -24,7 +24,7 @@ REPO_DIR = PACKAGE_DIR.parent
 SOURCE_DIR = PACKAGE_DIR / "csrc"
 # one translation unit per step-kernel family so hipcc can run in parallel
 SOURCES = ("cowsdm.hip", "step_i32_packed.hip", "step_i32_dense.hip", "step_i64_packed.hip",
-           "step_i64_dense.hip", "trace_plan.hip", "routes.hip")
+           "step_i64_dense.hip", "trace_plan.hip", "routes.hip", "controller.hip")
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
@@ -190,6 +190,30 @@ class Trace(ctypes.Structure):
     ]
 
 
+class Controller(ctypes.Structure):
+    """cowsdm_controller_t."""
+
+    _fields_ = [
+        ("width", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("slots", ctypes.c_int64),
+        ("norm_weight", ctypes.c_void_p),
+        ("norm_bias", ctypes.c_void_p),
+        ("proj_weight_t", ctypes.c_void_p),
+        ("proj_bias", ctypes.c_void_p),
+        ("a_log", ctypes.c_void_p),
+        ("dt_bias", ctypes.c_void_p),
+        ("gate_weight_t", ctypes.c_void_p),
+        ("gate_bias", ctypes.c_void_p),
+        ("out_weight_t", ctypes.c_void_p),
+        ("out_bias", ctypes.c_void_p),
+        ("read_norm_weight", ctypes.c_void_p),
+        ("read_norm_bias", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
+        ("read_norm_eps", ctypes.c_float),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -203,6 +227,10 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_trace_scan_words": (_I64, [_I64, _I64, _I32]),
     "cowsdm_trace_persistent": (
         _I32, [ctypes.POINTER(Layer), _I32, ctypes.POINTER(Shape), ctypes.POINTER(Trace), _I32]),
+    "cowsdm_controller_rows": (_I64, [_I64, _I64, _I64]),
+    "cowsdm_controller_prepare": (
+        _I32, [ctypes.POINTER(Controller), _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "cowsdm_controller_finish": (_I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P]),
     "cowsdm_host_report_alloc": (
         _I32, [_I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "cowsdm_host_report_free": (_I32, [_P]),

@@ -1,0 +1,255 @@
+// The SDM controller's per-token work around the copy-on-write step
+// (copy_on_write_sdm/inference.py:459-535): before the step, the input
+// LayerNorm, the read / write key, value, forget and input projections and
+// the gates; after it, the readings LayerNorm, the sigmoid output gate and
+// the output projection.  Routes are selected from the keys by
+// cowsdm_product_key_routes (routes.hip).
+//
+// A workgroup takes kCtlTokens tokens.  Each token's normalised input stays
+// in LDS, and thread j computes output row j of every projection for all of
+// the workgroup's tokens: the weights are stored transposed ([width, rows]),
+// so the lanes of a wave read consecutive floats of one input column, and
+// each weight is loaded once per workgroup and used for every token.
+// Products are accumulated with fused multiply-adds in input order.
+
+#include "common.h"
+
+namespace cowsdm_impl {
+
+constexpr int kCtlTokens = 4;        // tokens per workgroup
+constexpr int kCtlThreads = 256;
+constexpr int kCtlWaves = kCtlThreads / kWave;
+constexpr int kCtlMaxWidth = 1024;         // LDS: 3 x 4 tokens x width floats
+
+struct CtlParams {
+  cowsdm_controller_t c;
+  int64_t batch;
+  const float* tokens;        // prepare: [batch, width]
+  const float* normalized;    // finish: [batch, width]
+  const float* reading;       // finish: [batch * heads, head_width]
+  float* out_normalized;      // prepare
+  float* read_keys;           // prepare: [batch * heads, key_width]
+  float* write_keys;
+  float* values;              // prepare: [batch * heads, head_width]
+  float* input_gate;          // prepare: [batch * heads]
+  float* forget_log_gate;
+  float* out;                 // finish: [batch, width]
+  int width, heads, head_width, key_width, rows;
+};
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// LayerNorm of n floats (LDS) by one wave, as torch's layer_norm: the mean,
+// the biased variance, then (x - mean) / sqrt(var + eps) * w + b.
+__device__ void wave_layer_norm(const float* src, float* dst, int n, const float* w,
+                                const float* b, float eps) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  float s = 0.0f;
+  for (int i = lane; i < n; i += kWave) s += src[i];
+  const float mean = wave_sum_f(s) / static_cast<float>(n);
+  float v = 0.0f;
+  for (int i = lane; i < n; i += kWave) {
+    const float d = src[i] - mean;
+    v = __builtin_fmaf(d, d, v);
+  }
+  const float var = wave_sum_f(v) / static_cast<float>(n);
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (int i = lane; i < n; i += kWave) dst[i] = (src[i] - mean) * rstd * w[i] + b[i];
+}
+
+// torch.nn.functional.softplus with beta 1 and threshold 20
+__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// acc[t] = sum_k x[t][k] * wt[k * rows + j] over the workgroup's tokens
+__device__ __forceinline__ void project(const float* x, int width, const float* wt, int rows,
+                                        int j, float (&acc)[kCtlTokens]) {
+#pragma unroll
+  for (int t = 0; t < kCtlTokens; ++t) acc[t] = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < width; ++k) {
+    const float w = wt[static_cast<int64_t>(k) * rows + j];
+#pragma unroll
+    for (int t = 0; t < kCtlTokens; ++t) acc[t] = __builtin_fmaf(x[t * width + k], w, acc[t]);
+  }
+}
+
+__global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlParams P) {
+  extern __shared__ float lds[];
+  const int W = P.width, H = P.heads, HW = P.head_width, KW = P.key_width;
+  float* const x = lds;                        // [kCtlTokens][W]
+  float* const xn = lds + kCtlTokens * W;      // [kCtlTokens][W]
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
+  const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
+  const int tid = static_cast<int>(threadIdx.x);
+  for (int i = tid; i < kCtlTokens * W; i += kCtlThreads) {
+    x[i] = i < T * W ? P.tokens[b0 * W + i] : 0.0f;
+  }
+  __syncthreads();
+  const int wave = tid / kWave;
+  for (int t = wave; t < kCtlTokens; t += kCtlWaves) {
+    if (t < T) {
+      wave_layer_norm(x + t * W, xn + t * W, W, P.c.norm_weight, P.c.norm_bias, P.c.norm_eps);
+    } else {
+      for (int i = tid % kWave; i < W; i += kWave) xn[t * W + i] = 0.0f;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < T * W; i += kCtlThreads) P.out_normalized[b0 * W + i] = xn[i];
+  // rows: read keys (H x KW), write keys (H x KW), values (W), forget (H), input (H)
+  for (int j = tid; j < P.rows; j += kCtlThreads) {
+    float acc[kCtlTokens];
+    project(xn, W, P.c.proj_weight_t, P.rows, j, acc);
+    const float bias = P.c.proj_bias[j];
+    for (int t = 0; t < T; ++t) {
+      const int64_t b = b0 + t;
+      const float y = acc[t] + bias;
+      int r = j;
+      if (r < H * KW) {
+        const int h = r / KW;
+        P.read_keys[(b * H + h) * KW + (r - h * KW)] = y;
+      } else if ((r -= H * KW) < H * KW) {
+        const int h = r / KW;
+        P.write_keys[(b * H + h) * KW + (r - h * KW)] = y;
+      } else if ((r -= H * KW) < W) {
+        const int h = r / HW;
+        P.values[(b * H + h) * HW + (r - h * HW)] = y;
+      } else if ((r -= W) < H) {
+        P.forget_log_gate[b * H + r] = -expf(P.c.a_log[r]) * softplus(y + P.c.dt_bias[r]);
+      } else {
+        r -= H;
+        P.input_gate[b * H + r] = sigmoid(y);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParams P) {
+  extern __shared__ float lds[];
+  const int W = P.width, HW = P.head_width;
+  float* const nrm = lds;                       // normalized inputs
+  float* const rd = lds + kCtlTokens * W;       // readings, then gate * normalised readings
+  float* const rn = lds + 2 * kCtlTokens * W;   // normalised readings
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
+  const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
+  const int tid = static_cast<int>(threadIdx.x);
+  // a token's readings [heads, head_width] are its `width` contiguous floats
+  for (int i = tid; i < kCtlTokens * W; i += kCtlThreads) {
+    nrm[i] = i < T * W ? P.normalized[b0 * W + i] : 0.0f;
+    rd[i] = i < T * W ? P.reading[b0 * W + i] : 0.0f;
+  }
+  __syncthreads();
+  const int wave = tid / kWave;
+  const int segments = kCtlTokens * P.heads;
+  for (int g = wave; g < segments; g += kCtlWaves) {
+    wave_layer_norm(rd + g * HW, rn + g * HW, HW, P.c.read_norm_weight, P.c.read_norm_bias,
+                    P.c.read_norm_eps);
+  }
+  __syncthreads();
+  for (int j = tid; j < W; j += kCtlThreads) {
+    float acc[kCtlTokens];
+    project(nrm, W, P.c.gate_weight_t, W, j, acc);
+    const float bias = P.c.gate_bias[j];
+#pragma unroll
+    for (int t = 0; t < kCtlTokens; ++t) rd[t * W + j] = sigmoid(acc[t] + bias) * rn[t * W + j];
+  }
+  __syncthreads();
+  for (int j = tid; j < W; j += kCtlThreads) {
+    float acc[kCtlTokens];
+    project(rd, W, P.c.out_weight_t, W, j, acc);
+    const float bias = P.c.out_bias[j];
+    for (int t = 0; t < T; ++t) P.out[(b0 + t) * W + j] = acc[t] + bias;
+  }
+}
+
+namespace {
+
+int32_t check_controller(const cowsdm_controller_t* c, int64_t batch, CtlParams& P) {
+  if (!c) return fail(COWSDM_EARG, "controller: null controller");
+  if (batch < 0) return fail(COWSDM_EARG, "controller: negative batch");
+  if (c->width <= 0 || c->heads <= 0 || c->width % c->heads != 0) {
+    return fail(COWSDM_EARG, "width must be divisible by memory_heads");
+  }
+  if (c->width > kCtlMaxWidth) {
+    return fail(COWSDM_ELIMIT, "controller: width <= %d on the HIP path (got %lld)",
+                kCtlMaxWidth, static_cast<long long>(c->width));
+  }
+  int64_t root = 0;
+  while ((root + 1) * (root + 1) <= c->slots) ++root;
+  if (c->slots < 1 || root * root != c->slots) {
+    return fail(COWSDM_EARG, "faithful SDM slots must be a perfect square");
+  }
+  P.c = *c;
+  P.batch = batch;
+  P.width = static_cast<int>(c->width);
+  P.heads = static_cast<int>(c->heads);
+  P.head_width = static_cast<int>(c->width / c->heads);
+  P.key_width = static_cast<int>(2 * root);
+  const int64_t rows = 2 * c->heads * 2 * root + c->width + 2 * c->heads;
+  if (rows > (int64_t{1} << 24)) return fail(COWSDM_ELIMIT, "controller: too many projection rows");
+  P.rows = static_cast<int>(rows);
+  return 0;
+}
+
+}  // namespace
+}  // namespace cowsdm_impl
+
+using namespace cowsdm_impl;
+
+extern "C" int64_t cowsdm_controller_rows(int64_t width, int64_t heads, int64_t slots) {
+  int64_t root = 0;
+  while ((root + 1) * (root + 1) <= slots) ++root;
+  if (width <= 0 || heads <= 0 || slots < 1 || root * root != slots) return -1;
+  return 2 * heads * 2 * root + width + 2 * heads;
+}
+
+extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const float* tokens,
+                                             int64_t batch, float* normalized, float* read_keys,
+                                             float* write_keys, float* values, float* input_gate,
+                                             float* forget_log_gate, void* stream) {
+  CtlParams P{};
+  if (int32_t e = check_controller(c, batch, P)) return e;
+  if (batch == 0) return 0;
+  if (!tokens || !normalized || !read_keys || !write_keys || !values || !input_gate ||
+      !forget_log_gate || !c->norm_weight || !c->norm_bias || !c->proj_weight_t ||
+      !c->proj_bias || !c->a_log || !c->dt_bias) {
+    return fail(COWSDM_EARG, "controller prepare: null pointer argument");
+  }
+  P.tokens = tokens;
+  P.out_normalized = normalized;
+  P.read_keys = read_keys;
+  P.write_keys = write_keys;
+  P.values = values;
+  P.input_gate = input_gate;
+  P.forget_log_gate = forget_log_gate;
+  const int64_t groups = (batch + kCtlTokens - 1) / kCtlTokens;
+  if (groups > (int64_t{1} << 31) - 1) return fail(COWSDM_ELIMIT, "controller: batch too large");
+  const size_t lds = sizeof(float) * 2 * kCtlTokens * P.width;
+  hipLaunchKernelGGL(controller_prepare_kernel, dim3(static_cast<unsigned>(groups)),
+                     dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
+  return launch_status("controller prepare");
+}
+
+extern "C" int32_t cowsdm_controller_finish(const cowsdm_controller_t* c,
+                                            const float* normalized, const float* reading,
+                                            int64_t batch, float* out, void* stream) {
+  CtlParams P{};
+  if (int32_t e = check_controller(c, batch, P)) return e;
+  if (batch == 0) return 0;
+  if (!normalized || !reading || !out || !c->gate_weight_t || !c->gate_bias ||
+      !c->out_weight_t || !c->out_bias || !c->read_norm_weight || !c->read_norm_bias) {
+    return fail(COWSDM_EARG, "controller finish: null pointer argument");
+  }
+  P.normalized = normalized;
+  P.reading = reading;
+  P.out = out;
+  const int64_t groups = (batch + kCtlTokens - 1) / kCtlTokens;
+  if (groups > (int64_t{1} << 31) - 1) return fail(COWSDM_ELIMIT, "controller: batch too large");
+  const size_t lds = sizeof(float) * 3 * kCtlTokens * P.width;
+  hipLaunchKernelGGL(controller_finish_kernel, dim3(static_cast<unsigned>(groups)),
+                     dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
+  return launch_status("controller finish");
+}

@@ -487,6 +487,59 @@ int32_t cowsdm_product_key_routes(const float* projected, int64_t rows,
                                   float* weights, int64_t* indices,
                                   void* stream);
 
+/* ----------------------------------------------------- controller step */
+
+/* Weights of one SDM layer's controller (float32, device; SparseDeltaMemory,
+ * sdm.py:998-1052).  Projection weights are stored transposed, [in, out]:
+ * proj_weight_t [width, rows] holds, in this order, the read keys
+ * (heads x 2*sqrt(slots)), the write keys (the same), the values (width),
+ * the forget gates (heads) and the input gates (heads) of read_projection,
+ * write_projection, value_projection, forget_projection and
+ * input_projection (rows = cowsdm_controller_rows(width, heads, slots)). */
+typedef struct cowsdm_controller {
+  int64_t width;            /* model width, heads * head_width       */
+  int64_t heads;            /* memory heads                          */
+  int64_t slots;            /* N, a perfect square                   */
+  const float* norm_weight; /* input_norm (LayerNorm(width))         */
+  const float* norm_bias;
+  const float* proj_weight_t;   /* [width, rows]                     */
+  const float* proj_bias;       /* [rows]                            */
+  const float* a_log;           /* [heads]                           */
+  const float* dt_bias;         /* [heads]                           */
+  const float* gate_weight_t;   /* output_gate, [width, width]       */
+  const float* gate_bias;
+  const float* out_weight_t;    /* output_projection, [width, width] */
+  const float* out_bias;
+  const float* read_norm_weight;  /* readings_norm (LayerNorm(head_width)) */
+  const float* read_norm_bias;
+  float norm_eps;
+  float read_norm_eps;
+} cowsdm_controller_t;
+
+/* Rows of the fused controller projection, or -1 for invalid sizes. */
+int64_t cowsdm_controller_rows(int64_t width, int64_t heads, int64_t slots);
+
+/* The position-parallel part of _prepare_faithful_sdm_step
+ * (inference.py:459-519) for `batch` tokens [batch, width]: normalized
+ * [batch, width] = input_norm(tokens); read and write keys
+ * [batch * heads, 2*sqrt(slots)]; values [batch * heads, head_width];
+ * input_gate = sigmoid(input_projection) and forget_log_gate =
+ * -exp(A_log) * softplus(forget_projection + dt_bias), [batch * heads];
+ * row b * heads + h for token b and head h.  Routes come from the keys
+ * through cowsdm_product_key_routes.  width <= 1024. */
+int32_t cowsdm_controller_prepare(const cowsdm_controller_t* controller, const float* tokens,
+                                  int64_t batch, float* normalized, float* read_keys,
+                                  float* write_keys, float* values, float* input_gate,
+                                  float* forget_log_gate, void* stream);
+
+/* _finish_faithful_sdm_step (inference.py:522-535): out [batch, width] =
+ * output_projection(sigmoid(output_gate(normalized)) *
+ * readings_norm(reading)), the reading [batch * heads, head_width]
+ * normalised per head. */
+int32_t cowsdm_controller_finish(const cowsdm_controller_t* controller,
+                                 const float* normalized, const float* reading,
+                                 int64_t batch, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

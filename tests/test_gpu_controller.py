@@ -1,0 +1,143 @@
+"""GPU parity of the controller kernels (csrc/controller.hip) against
+oracle/controller.py, and of the controller-driven layer decode
+(``decode_sdm_layer_controller``, inference.py:538-598) against the oracle's
+step.
+
+Tolerances (float32 kernels against a float64 oracle on the same float32
+weights): the normalised tokens within rtol 1e-5 / atol 1e-5, the keys,
+values, gates and outputs within rtol 1e-4 / atol 2e-5 (a projection sums
+`width` products with fused multiply-adds).  Routes are compared exactly
+with the oracle's routes of the kernel's own keys (a near-tie in keys that
+differ by a rounding could otherwise flip a selection), and the state step
+is compared bit for bit with the oracle's step on the kernel's own step
+inputs."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import copy_on_write_sdm_amd as cow
+from copy_on_write_sdm_amd import controller as ctl
+from controller_cases import make_layer, params_of, tokens
+from gpu_helpers import assert_state_equal
+from oracle import controller as octl
+from oracle import routes as oroutes
+from oracle import state as ref
+
+pytestmark = pytest.mark.gpu
+
+# (width, slots, heads, reads, writes, batch): config 2's controller, config
+# 5's (4 heads of 128, N = 65,536), an odd one (batch not a multiple of the
+# kernel's 4 tokens per workgroup, two heads), the widest supported
+SHAPES = [(128, 256, 1, 16, 4, 64), (512, 65536, 4, 16, 4, 16), (96, 64, 2, 8, 3, 5),
+          (1024, 1024, 8, 8, 2, 3)]
+
+
+def _setup(device, width, slots, heads, reads, writes, batch, seed):
+    layer = make_layer(width, slots=slots, reads=reads, writes=writes, heads=heads,
+                       seed=seed, dtype=torch.float32)
+    controller = ctl.SDMController.from_module(layer, device=device)
+    x = tokens(batch, width, seed=seed + 1, dtype=torch.float32)
+    return layer, controller, x
+
+
+@pytest.mark.parametrize("width,slots,heads,reads,writes,batch", SHAPES)
+def test_prepare_matches_oracle(device, width, slots, heads, reads, writes, batch):
+    print(f"controller prepare width={width} N={slots} H={heads} B={batch}", flush=True)
+    layer, controller, x = _setup(device, width, slots, heads, reads, writes, batch, seed=width)
+    step = ctl.prepare_sdm_step(controller, x.to(device))
+    want = octl.prepare(params_of(layer), x.numpy())
+    got = step.inputs
+    np.testing.assert_allclose(step.normalized.cpu().numpy(), want["normalized"],
+                               rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(got.values.cpu().numpy(), want["values"], rtol=1e-4, atol=2e-5)
+    np.testing.assert_allclose(got.input_gate.cpu().numpy(), want["input_gate"],
+                               rtol=1e-4, atol=2e-5)
+    np.testing.assert_allclose(got.forget_log_gate.cpu().numpy(), want["forget_log_gate"],
+                               rtol=1e-4, atol=2e-5)
+    # the keys, read back from a second launch's outputs
+    keys = {}
+    for name in ("read_keys", "write_keys"):
+        keys[name] = torch.empty(batch * heads, 1, 2 * int(np.sqrt(slots)), device=device)
+    normalized = torch.empty(batch, 1, width, device=device)
+    scratch = [torch.empty(batch * heads, width // heads, device=device)] + \
+              [torch.empty(batch * heads, device=device) for _ in range(2)]
+    from copy_on_write_sdm_amd import _native as nat
+    nat.check(nat.lib().cowsdm_controller_prepare(
+        controller.c_struct(), x.to(device).data_ptr(), batch, normalized.data_ptr(),
+        keys["read_keys"].data_ptr(), keys["write_keys"].data_ptr(), scratch[0].data_ptr(),
+        scratch[1].data_ptr(), scratch[2].data_ptr(), nat.stream_handle(device)), "prepare")
+    for name in keys:
+        np.testing.assert_allclose(keys[name].cpu().numpy(), want[name], rtol=1e-4, atol=2e-5)
+    # routes: exactly the oracle's routes of the kernel's keys
+    for name, k, idx, w in (("read_keys", reads, got.read_indices, got.read_weights),
+                            ("write_keys", writes, got.write_indices, got.write_weights)):
+        ew, ei = oroutes.product_key_routes(keys[name].cpu().numpy(), slots, k)
+        np.testing.assert_array_equal(idx.cpu().numpy(), ei[:, 0])
+        np.testing.assert_allclose(w.cpu().numpy(), ew[:, 0], rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("width,slots,heads,reads,writes,batch", SHAPES)
+def test_finish_matches_oracle(device, width, slots, heads, reads, writes, batch):
+    print(f"controller finish width={width} H={heads} B={batch}", flush=True)
+    layer, controller, x = _setup(device, width, slots, heads, reads, writes, batch,
+                                  seed=3 * width)
+    step = ctl.prepare_sdm_step(controller, x.to(device))
+    reading = tokens(batch * heads, width // heads, seed=77, dtype=torch.float32)[:, 0]
+    out = ctl.finish_sdm_step(controller, step, reading.to(device))
+    want = octl.finish(params_of(layer), step.normalized.cpu().numpy().astype(np.float64),
+                       reading.numpy())
+    assert out.shape == (batch, 1, width)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+
+
+def test_argument_errors(device):
+    layer, controller, x = _setup(device, 64, 16, 2, 4, 2, 3, seed=5)
+    with pytest.raises(ValueError, match="faithful SDM decode requires one token"):
+        ctl.prepare_sdm_step(controller, x.to(device)[:, 0])
+    with pytest.raises(TypeError, match="float32"):
+        ctl.prepare_sdm_step(controller, x.to(device).double())
+    step = ctl.prepare_sdm_step(controller, x.to(device))
+    with pytest.raises(ValueError, match="reading does not match"):
+        ctl.finish_sdm_step(controller, step, torch.zeros(5, 32, device=device))
+    with pytest.raises(ValueError, match="perfect square"):
+        ctl.SDMController.random(64, slots=15, reads=2, writes=2, device=device)
+    with pytest.raises(ValueError, match="divisible"):
+        ctl.SDMController.random(63, slots=16, reads=2, writes=2, memory_heads=2, device=device)
+
+
+@pytest.mark.parametrize("heads", [1, 2])
+def test_controller_layer_decode_matches_oracle_step(device, heads):
+    """Tokens through decode_sdm_layer_controller on packed state, against
+    the oracle's capacity proof and step on the kernel's own step inputs
+    (state bit for bit), the dense twin (readings bit for bit) and the
+    oracle's finish (tolerance)."""
+
+    width, slots, batch, steps = 128, 256, 16, 6
+    print(f"controller layer decode H={heads}", flush=True)
+    layer, controller, _ = _setup(device, width, slots, heads, 16, 4, batch, seed=21 + heads)
+    banks = batch * heads
+    m0 = torch.randn(1, slots, width // heads, generator=torch.Generator().manual_seed(3))
+    state = cow.PackedSDMCopyOnWriteState.allocate(m0.to(device), banks=banks,
+                                                   capacity_rows=32, growth_quantum_rows=64)
+    memory = m0.expand(banks, -1, -1).clone(memory_format=torch.contiguous_format).to(device)
+    orc = ref.allocate(m0.numpy(), banks=banks, capacity_rows=32, growth_quantum_rows=64)
+    p = params_of(layer)
+    for s in range(steps):
+        x = tokens(batch, width, seed=100 + s, dtype=torch.float32).to(device)
+        out = ctl.decode_sdm_layer_controller(controller, x, state)
+        dense_out = ctl.decode_sdm_layer_controller_dense(controller, x, memory)
+        assert torch.equal(out, dense_out)
+        step = ctl.prepare_sdm_step(controller, x)     # the same inputs, again
+        xi = {k: getattr(step.inputs, k).cpu().numpy()
+              for k in ("write_indices", "write_weights", "values", "input_gate",
+                        "forget_log_gate", "read_indices", "read_weights")}
+        ref.prepare_step_capacity(orc, banks * 4)
+        reading, _ = ref.packed_step(orc, **xi, validate_routes=False)
+        want = octl.finish(p, step.normalized.cpu().numpy().astype(np.float64), reading)
+        np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-4, atol=2e-5)
+    assert_state_equal(state, orc)
+    assert state.growth_events > 0
+    state.validate_invariants()
