@@ -473,6 +473,39 @@ def main() -> int:
         }
         del graph
 
+    # ---- the reference's per-token call pattern with the controller on the
+    # device (decode_sdm_layer_controller: input norm, projections and gates,
+    # routes, the capacity proof, the packed step, the output gate and
+    # projection) for every layer, random controller weights of the
+    # configuration's shape and random tokens
+    controller_leg = None
+    if eager_steps:
+        n = min(eager_steps, 16)
+        width_model = HEADS * WIDTH
+        ctls = [cow.SDMController.random(width_model, slots=SLOTS, reads=READS, writes=WRITES,
+                                         memory_heads=HEADS, seed=500 + l, device=dev)
+                for l in range(LAYERS)]
+        toks = torch.randn(n + 2, B, 1, width_model, device=dev,
+                           generator=torch.Generator(device=dev).manual_seed(args.seed))
+
+        def controller_token(s):
+            for l in range(LAYERS):
+                cow.decode_sdm_layer_controller(ctls[l], toks[s], states[l])
+
+        for s in range(2):
+            controller_token(s)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(2, n + 2):
+            controller_token(s)
+        torch.cuda.synchronize()
+        controller_leg = {
+            "tokens_per_s": round(B * n / (time.perf_counter() - t0), 1),
+            "steps": n,
+            "what": "per token and layer: controller prepare, two route selections, "
+                    "prepare_step_capacity, packed step, controller finish (eager)",
+        }
+
     # roofline of the dominant kernel, the persistent decode kernel: the
     # algorithmic bytes of the steps the timed launches ran over its mean
     # duration (HIP events at its own start and end); the count and plan
@@ -554,6 +587,7 @@ def main() -> int:
         "allocator": allocator,
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
         "graph_step": graph_step,
+        "controller_decode": controller_leg,
     }
     if not args.no_cpu_baseline and args.config == 2:
         result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)
