@@ -857,7 +857,13 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
         int table = 64;
         while (table < 2 * P.steps * P.writes) table *= 2;
         P.count_table = table;
-        if (dense) {
+        if (planned && P.steps == 1) {
+          // one step: the step kernel makes the step's proof itself (its
+          // planned mode), with no plan of many steps to wait for
+          if (i64) launch_step_w<int64_t, false>(P, blocks, vec, stream);
+          else launch_step_w<int32_t, false>(P, blocks, vec, stream);
+          rc = 0;
+        } else if (dense) {
           rc = i64 ? launch_trace<int64_t, true>(P, trace_vec, stream)
                    : launch_trace<int32_t, true>(P, trace_vec, stream);
         } else {

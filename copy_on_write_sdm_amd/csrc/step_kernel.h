@@ -35,6 +35,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
                               __HIP_MEMORY_SCOPE_AGENT);
       }
     }
+    if (P.report && bank == P.banks - 1) write_report(P, layer_id, trace_s, COWSDM_TRACE_ENDED);
     return;
   }
   auto step_ptr = [&](const void* base, int k) __attribute__((always_inline)) -> const char* {
@@ -54,8 +55,18 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   const int D = P.width;
   const int W = P.writes;
   const int R = P.reads;
-  const int64_t C = L.capacity_rows;
+  int64_t C = L.capacity_rows;
   const int64_t b = bank;
+  // Planned single step of a decode trace (packed state with control
+  // words): the decode loop's proof for this step, prepare_step_capacity
+  // (need) (allocator.py:745-773), made identically by every wave from the
+  // control words and free_count.  A growth within the slab's buffers puts
+  // row ids C0 .. C0 + added - 1 on top of the found stack (grow_capacity,
+  // allocator.py:691-743), so pop q from the top takes C0 + added - 1 - q
+  // while q < added and the found stack's entry q - added after.
+  const bool planned = !DENSE && P.control != nullptr;
+  int64_t grown = 0;        // rows added on top of the found stack
+  int64_t proven_after = 0;
 
   int lane_err = 0;
 
@@ -77,6 +88,57 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
   if constexpr (!DENSE) {
     old_free = *L.free_count;
     epoch = static_cast<uint32_t>(L.scratch[COWSDM_SCRATCH_EPOCH]);
+    if (planned) {
+      auto word = [&](int k) __attribute__((always_inline)) -> int64_t {
+        const uint64_t v = static_cast<uint64_t>(control_word(P, layer_id, k));
+        return static_cast<int64_t>(
+            (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32))) << 32) |
+            __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+      };
+      C = word(COWSDM_CTRL_CAPACITY);
+      int64_t proven = word(COWSDM_CTRL_PROVEN);
+      const int64_t room = word(COWSDM_CTRL_ROOM);
+      const int64_t quantum = word(COWSDM_CTRL_QUANTUM);
+      const int64_t need = word(COWSDM_CTRL_NEED);
+      bool refused = false;
+      if (need > 0 && quantum > 0) {
+        if (proven < need) {
+          int64_t free_rows = old_free;
+          if (free_rows < need) {
+            const int64_t want = C + need - free_rows;
+            const int64_t selected = (want + quantum - 1) / quantum * quantum;
+            if (selected > room || selected >= (int64_t{1} << 31)) {
+              refused = true;   // the host grows the slab into larger buffers
+            } else {
+              grown = selected - C;
+              free_rows += grown;
+            }
+          }
+          proven = free_rows;
+        }
+        proven_after = proven - need;
+      } else {
+        proven_after = proven;
+      }
+      if (refused) {
+        // the layer takes no step: every wave of it stops here, before any
+        // slot is published; the closing bank reports the refusal
+        if (bank == P.banks - 1) {
+          if (lane == 0) {
+            atomic_store_u64(&control_word(P, layer_id, COWSDM_CTRL_FREE),
+                             static_cast<uint64_t>(old_free));
+            atomic_store_u64(&control_word(P, layer_id, COWSDM_CTRL_STEPS), 0);
+            atomic_store_u64(&control_word(P, layer_id, COWSDM_CTRL_FIT), 0);
+            if (P.trace_status) {
+              __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_REFUSED},
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+          if (P.report) write_report(P, layer_id, trace_s, COWSDM_TRACE_REFUSED);
+        }
+        return;
+      }
+    }
     if (old_free < 0 || old_free > C) lane_err |= COWSDM_ERR_CORRUPT;
 #pragma unroll
     for (int k = 0; k < kFreeWindow / kWave; ++k) {
@@ -246,19 +308,21 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
     if constexpr (!DENSE) {
       int64_t* slots = L.scratch + COWSDM_SCRATCH_SLOTS;
       prefix = bank_prefix(slots, bank, epoch, count, lane, &poisoned);
-      fits = ok && !poisoned && (count == 0 || prefix + count <= old_free);
+      fits = ok && !poisoned && (count == 0 || prefix + count <= old_free + grown);
       int bad_row = 0;
       const int64_t from_top = prefix + rank;  // pop position counted from the top
-      const int src_lane = static_cast<int>(from_top % kWave);
+      const int64_t found = from_top - grown;  // ... and from the found stack's top
+      const int src_lane = static_cast<int>((found < 0 ? 0 : found) % kWave);
       int window_row = -1;
 #pragma unroll
       for (int k = 0; k < kFreeWindow / kWave; ++k) {
         const int v = __shfl(free_top[k], src_lane, kWave);
-        if (from_top / kWave == k) window_row = v;
+        if (found >= 0 && found / kWave == k) window_row = v;
       }
       if (fits && first) {
-        new_row = from_top < kFreeWindow ? window_row : L.free_rows[old_free - 1 - from_top];
-        if (new_row < 0 || new_row >= C) bad_row = 1;
+        new_row = found < 0 ? static_cast<int>(C + grown - 1 - from_top)
+                : found < kFreeWindow ? window_row : L.free_rows[old_free - 1 - found];
+        if (new_row < 0 || new_row >= C + grown) bad_row = 1;
       }
       if (__ballot(bad_row) != 0) {
         fits = false;
@@ -269,7 +333,8 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
         }
       }
       if (lane == 0) {
-        if (ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
+        // (planned steps: the closing bank writes the flag)
+        if (!planned && ok && !fits && count > 0 && !poisoned) *L.overflow_flag = 1;
         if (poisoned) {
           __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
                                 static_cast<int64_t>(COWSDM_ERR_LOOKBACK),
@@ -409,19 +474,45 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
     // largest inclusive prefix that fits, read from the other banks' slots.
     if (bank == P.banks - 1) {
       closed_layer = true;
+      const int64_t top = old_free + grown;
       int64_t served = prefix + count;
-      if (poisoned || served > old_free) {
-        served = fitting_prefix(L.scratch + COWSDM_SCRATCH_SLOTS, P.banks, epoch, old_free,
-                                lane);
+      const bool short_rows = poisoned || served > top;
+      if (short_rows) {
+        served = fitting_prefix(L.scratch + COWSDM_SCRATCH_SLOTS, P.banks, epoch, top, lane);
+      }
+      const int64_t now_free = top - served;
+      if (planned && now_free > old_free) {
+        // the grown rows no pop took stay on the stack, above the found ones
+        int32_t* const stack = const_cast<int32_t*>(L.free_rows);
+        for (int64_t p = old_free + lane; p < now_free; p += kWave) {
+          stack[p] = static_cast<int32_t>(C + (p - old_free));
+        }
       }
       if (lane == 0) {
-        const int64_t now_free = old_free - served;
         *L.free_count = static_cast<int32_t>(now_free);
         if (L.allocated_rows_out) {
-          *L.allocated_rows_out = static_cast<int32_t>(C - now_free);
+          *L.allocated_rows_out = static_cast<int32_t>(C + grown - now_free);
         }
         atomic_store_u64(&L.scratch[COWSDM_SCRATCH_EPOCH],
                          static_cast<uint64_t>(epoch + 1u));
+        if (planned) {
+          if (grown > 0) *L.overflow_flag = 0;   // grow_capacity clears it
+          if (short_rows) *L.overflow_flag = 1;
+          auto put = [&](int k, int64_t v) __attribute__((always_inline)) {
+            atomic_store_u64(&control_word(P, layer_id, k), static_cast<uint64_t>(v));
+          };
+          const int64_t events = control_word(P, layer_id, COWSDM_CTRL_EVENTS);
+          const int64_t added = control_word(P, layer_id, COWSDM_CTRL_ADDED);
+          const int64_t copied = control_word(P, layer_id, COWSDM_CTRL_COPIED);
+          put(COWSDM_CTRL_PROVEN, short_rows ? 0 : proven_after);
+          put(COWSDM_CTRL_CAPACITY, C + grown);
+          put(COWSDM_CTRL_EVENTS, events + (grown > 0 ? 1 : 0));
+          put(COWSDM_CTRL_ADDED, added + grown);
+          put(COWSDM_CTRL_COPIED, copied + (grown > 0 ? C : 0));
+          put(COWSDM_CTRL_FREE, now_free);
+          put(COWSDM_CTRL_STEPS, 1);
+          put(COWSDM_CTRL_FIT, served);
+        }
       }
     }
   } else {
@@ -446,6 +537,7 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_kernel(StepParams P) {
       atomic_store_u64(&P.trace_step[layer_id], static_cast<uint64_t>(trace_s + 1));
     }
   }
+  if (!DENSE && P.report && closed_layer) write_report(P, layer_id, trace_s + 1, 0);
 }
 
 template <typename IDX, int MAXW, int VEC, bool DENSE>

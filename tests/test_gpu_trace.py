@@ -300,6 +300,7 @@ def test_device_counter_graph_replay(device, persistent):
     (8, 24, 16),     # launches shorter than a growth's reach
     (7, 40, 48),     # odd launch length, quantum above a step's need
     (64, 512, 16),   # never short: one proof covers the run
+    (1, 24, 16),     # one step per launch (the step kernel's own proof), host growth
 ])
 def test_decode_loop_matches_reference_loop(device, launch_steps, capacity, quantum):
     """run() against the reference's per-step loop on the oracle: the proof
@@ -360,10 +361,12 @@ def _decode_loop_case(device, launch_steps, *, layers, banks, slots, width, step
     return states
 
 
-def test_decode_loop_grows_on_device_with_reserved_room(device):
+@pytest.mark.parametrize("launch_steps", [512, 1])
+def test_decode_loop_grows_on_device_with_reserved_room(device, launch_steps):
     """With the slab's buffers reserved for the run, every growth happens
-    inside the persistent launches (no host round) and still equals the
-    reference loop."""
+    inside the launches (no host round) and still equals the reference loop:
+    persistent launches, and launches of one step each (the step kernel
+    makes the step's proof and growth itself)."""
 
     layers, banks, slots, steps = 2, 16, 64, 60
     m0 = synthetic.make_initial_memory(layers, 1, slots, 128, seed=5, device=device)
@@ -381,8 +384,8 @@ def test_decode_loop_grows_on_device_with_reserved_room(device):
     outputs = torch.empty(steps, layers, banks, 128, device=device)
     tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
     tr.reserve_steps(steps)
-    report = tr.run(steps)
-    assert report == {"launches": 1, "growth_rounds": 0}
+    report = tr.run(steps, launch_steps=launch_steps)
+    assert report == {"launches": -(-steps // launch_steps), "growth_rounds": 0}
     want = oracle_decode_loop(oracles, routes, steps, need=banks * 4)
     assert np.array_equal(outputs.cpu().numpy(), want)
     for st, orc in zip(states, oracles):
