@@ -163,7 +163,8 @@ __device__ __forceinline__ uint64_t slot_word(uint32_t epoch, uint32_t status,
 // A packed decode trace layer's plan block (int64 words; S = plan_steps,
 // B = banks, W = writes): the epoch, the header, the plan words [B][S]
 // (bank-major: a bank's words of consecutive steps are contiguous), the step
-// totals [S], the running totals [S + 1] and the pops [S * B * W].
+// totals [S], the running totals [S + 1], the pops [S * B * W] and the
+// growth segments [S + 1][4].
 struct PlanBlock {
   int64_t* epoch;
   int64_t* head;
@@ -171,6 +172,7 @@ struct PlanBlock {
   int64_t* totals;
   int64_t* cum;
   int64_t* pops;
+  int64_t* segs;   // [S + 1][4]: the growth segments (plan_layer)
   int64_t steps;   // S
   __device__ int64_t* word(int bank, int t) const {
     return words + static_cast<int64_t>(bank) * steps + t;
@@ -186,6 +188,7 @@ __device__ __forceinline__ PlanBlock plan_block(const StepParams& P, int layer) 
   pb.totals = pb.words + S * P.banks;
   pb.cum = pb.totals + S;
   pb.pops = pb.cum + S + 1;
+  pb.segs = pb.pops + S * P.banks * P.writes;
   pb.steps = S;
   return pb;
 }

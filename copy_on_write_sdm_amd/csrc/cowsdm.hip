@@ -1015,9 +1015,11 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
 
 int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
   if (banks < 0 || writes < 0 || steps < 0) return -1;
-  // epoch and header, plan words [steps][banks], step totals, running totals
-  // and the launch's pops (at most banks * W per step), int64 each
-  return kPlanHead + kPlanHeadWords + banks * steps + steps + (steps + 1) + banks * steps * writes;
+  // epoch and header, plan words [banks][steps], step totals, running
+  // totals, the launch's pops (at most banks * W per step) and its growth
+  // segments (4 words each, at most one per step and the first), int64 each
+  return kPlanHead + kPlanHeadWords + banks * steps + steps + (steps + 1) + banks * steps * writes +
+         4 * (static_cast<int64_t>(steps) + 1);
 }
 
 int32_t cowsdm_host_report_alloc(int64_t words, int64_t** host, int64_t** device) {

@@ -201,6 +201,84 @@ __device__ __forceinline__ int plane_code(uint32_t w, int lo, int hi) {
 // FEW: at most 64 banks per layer (the compiler may then give a wave every
 // register; a grid of more banks needs two workgroups per CU).
 // MAPLDS: packed, the bank's slot map staged in dynamic LDS (N ints per bank).
+// A bank's pops when its launch's plan is in: the row of every first touch
+// of its steps (plan words in LDS, `plan`) into the plan's pop list, from the
+// launch's growth segments when it grows, else the found stack's entry
+// found - 1 - pop.  Lane = step, 64 steps a round; every round's stack
+// entries are loaded before the first is used, so the listing waits for one
+// load's latency, not one per round.  False when a segment never arrives.
+__device__ __forceinline__ bool list_bank_pops(const PlanBlock& pb, uint32_t epoch, int segments,
+                                               int found, int G, int fit, const int* plan,
+                                               int* seg, const int32_t* stack) {
+  constexpr int kRounds = kTraceMaxSteps / kWave;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  bool ok = true;
+  if (segments > 1) ok = plan_segments(pb, epoch, segments, seg);
+  // row[c][r]: the row of pop r of step c * 64 + lane, or -2 - p for the
+  // found stack's entry at position p
+  int row[kRounds][kTraceMaxWrites];
+  int base[kRounds], n[kRounds];
+#pragma unroll
+  for (int c = 0; c < kRounds; ++c) {
+    const int t = c * kWave + lane;
+    const uint32_t w = t < G ? static_cast<uint32_t>(plan[t]) : 0u;
+    base[c] = static_cast<int>(w & kPlanBaseMask);
+    n[c] = __popc((w >> kPlanMaskShift) & 15u);
+#pragma unroll
+    for (int r = 0; r < kTraceMaxWrites; ++r) {
+      const int q = base[c] + r;
+      row[c][r] = 0;
+      if (r < n[c] && q < fit) {
+        if (segments > 1) {
+          const int k = segment_of(seg, segments, q);
+          const int pos = seg[2 * kPlanSegments + k] - 1 - (q - seg[k]);
+          const int v = segment_entry(seg, pos, k);
+          row[c][r] = v >= 0 ? v : -2 - pos;
+        } else {
+          row[c][r] = -2 - (found - 1 - q);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kRounds; ++c) {
+#pragma unroll
+    for (int r = 0; r < kTraceMaxWrites; ++r) {
+      if (row[c][r] <= -2) row[c][r] = stack[-2 - row[c][r]];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kRounds; ++c) {
+#pragma unroll
+    for (int r = 0; r < kTraceMaxWrites; ++r) {
+      if (r < n[c] && base[c] + r < fit) {
+        atomic_store_u64(pb.pops + base[c] + r, tagged(epoch, static_cast<uint32_t>(row[c][r])));
+      }
+    }
+  }
+  return ok;
+}
+
+// The free stack a growing launch leaves (segments staged in `seg`, the
+// capacity it grows to, the pops that fit), by one wave once every control
+// wave of the layer has listed its pops: every position above the lowest
+// growth that a growth covers holds the row the latest such growth put
+// there.
+__device__ __forceinline__ void rewrite_stack(const int* seg, int segments, int capacity, int fit,
+                                              int32_t* stack) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  int lo = seg[kPlanSegments + 1];
+  for (int k = 2; k < segments; ++k) {
+    lo = seg[kPlanSegments + k] < lo ? seg[kPlanSegments + k] : lo;
+  }
+  // segment 0 holds the stack height and the capacity the launch found
+  const int top = seg[kPlanSegments] + (capacity - seg[3 * kPlanSegments]) - fit;
+  for (int p = lo + lane; p < top; p += kWave) {
+    const int v = segment_entry(seg, p, segments - 1);
+    if (v >= 0) stack[p] = v;
+  }
+}
+
 template <typename IDX, int VEC, bool DENSE, bool FULL, bool FEW, bool MAPLDS>
 __global__ __launch_bounds__(kTraceThreads)
 __attribute__((amdgpu_waves_per_eu(1, FEW ? 1 : 2)))
@@ -228,6 +306,10 @@ void sdm_trace_kernel(StepParams P) {
   // control wave (packed): the plan words of two 64-step chunks, staged from
   // registers a chunk ahead
   __shared__ int lds_plan[DENSE ? 1 : NB][DENSE ? 1 : kTraceMaxSteps];
+  // packed, slot maps in global memory: the launch's growth segments (the
+  // planner's, then every bank's copy when it lists its pops; the same values
+  // in every workgroup)
+  __shared__ int lds_seg[DENSE || MAPLDS ? 1 : 4 * kPlanSegments];
   // map in LDS (dynamic, 2 banks x 2 x N ints): each bank's slot map, then
   // each bank's first step of the launch writing each slot (the count part
   // of the launch's plan)
@@ -724,6 +806,8 @@ void sdm_trace_kernel(StepParams P) {
   PlanBlock pb{};
   uint32_t epoch = 0;
   int fit_rows = 0;
+  int found_top = 0;      // the stack height the launch found
+  int plan_segs = 1;      // growth segments of the launch (1: none)
   if constexpr (!DENSE) {
     pb = plan_block(P, layer_id);
     // the epoch word changes only when the layer's last control wave ends
@@ -779,6 +863,34 @@ void sdm_trace_kernel(StepParams P) {
     if constexpr (DENSE) return 0u;
     const int t = c * kWave + lane;
     return (static_cast<uint32_t>(lds_plan[DENSE ? 0 : pair][t < G ? t : G - 1]) >> kPlanMaskShift) & 15u;
+  };
+
+  // ---- this bank's pops, before its first step.  In a launch that grows,
+  // the layer's last control wave to list its pops then rewrites the free
+  // stack above the lowest growth: every entry the launch found there has
+  // been read by then (each wave's stack loads have returned before its
+  // ticket, which the high half of the layer's ticket word counts; the
+  // launch's last wave to finish clears the word).
+  auto list_pops = [&](bool ok) __attribute__((always_inline)) -> bool {
+    if constexpr (DENSE || MAPLDS) {
+      return ok;   // dense, or the planner listed them
+    } else {
+      if (ok) {
+        ok = list_bank_pops(pb, epoch, plan_segs, found_top, G, fit_rows, &lds_plan[pair][0],
+                            lds_seg, L.free_rows);
+      }
+      if (plan_segs > 1) {
+        int64_t listed = 0;
+        if (lane == 0) {
+          listed = __hip_atomic_fetch_add(P.trace_ticket + 1 + layer_id, int64_t{1} << 32,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (__builtin_amdgcn_readfirstlane(static_cast<int>(listed >> 32)) == B - 1 && ok) {
+          rewrite_stack(lds_seg, plan_segs, C, fit_rows, const_cast<int32_t*>(L.free_rows));
+        }
+      }
+      return ok;
+    }
   };
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
@@ -1408,11 +1520,16 @@ void sdm_trace_kernel(StepParams P) {
       ok = plan_prefix(pb, B, epoch, t0, t0 + per < G0 ? t0 + per : G0);
     }
     if (bank == 0) {
-      ok = plan_layer(P, layer_id, pb, B, G0, epoch, &lds_idx[0][0][0][0], &lds_plan[pair][0],
-                      pc) && ok;
+      // slot maps in LDS: the planner lists the pops (its segments in the
+      // chunk slots' LDS, unused until the steps start); else every bank
+      // lists its own
+      ok = plan_layer<!MAPLDS>(P, layer_id, pb, B, G0, epoch,
+                               MAPLDS ? &lds_idx[0][0][0][0] : &lds_seg[0], &lds_plan[pair][0],
+                               pc) && ok;
     }
-    int steps = 0, fit = 0, capacity = C0;
-    ok = plan_header(pb, epoch, steps, fit, capacity) && ok;
+    PlanHeader head{0, 0, C0, 0, 1};
+    ok = plan_header<!MAPLDS>(pb, epoch, head) && ok;
+    int steps = head.steps, fit = head.fit, capacity = head.capacity;
     if (!ok) {
       if (lane == 0) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
@@ -1427,6 +1544,8 @@ void sdm_trace_kernel(StepParams P) {
     }
     G = steps < G0 ? steps : G0;
     fit_rows = fit;
+    plan_segs = ok ? head.segments : 1;
+    found_top = head.found;
     C = pin(capacity);
     if (lane == 0) sync_store(&sync[2], kPlanReady | static_cast<uint32_t>(G));
   }
@@ -1442,7 +1561,7 @@ void sdm_trace_kernel(StepParams P) {
   q.widx = 0; q.ridx = 0; q.base = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1;
   q.rank = 0; q.u = 0; q.fwd = 0; q.rawm = 0;
   if constexpr (DENSE || MAPLDS) load_chunk(0);
-  const bool plan_ok = stage_plan();
+  bool plan_ok = list_pops(stage_plan());
   if constexpr (DENSE || MAPLDS) {
     write_chunk(0, chunk_fm(0));
     if (G > kWave) load_chunk(1);  // written before step 64 is read
@@ -1559,7 +1678,9 @@ void sdm_trace_kernel(StepParams P) {
     sync_store(&sync[0], (static_cast<uint32_t>(done_steps) << 16) | kNoStop);
   }
   if (!plan_ok) lost();   // a plan word never arrived: its steps took no rows
-  }  // G > 0
+  } else {
+    list_pops(true);        // no steps: the count of control waves that listed
+  }
 
   // ---- the layer's last control wave to finish advances the layer's device
   // counter and (packed) the plan's epoch.  Every wave of the layer read both
@@ -1594,6 +1715,7 @@ void sdm_trace_kernel(StepParams P) {
       int64_t* const ticket = P.trace_ticket + 1 + layer_id;
       done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // the low half counts the waves done with the launch
     if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
       if (lane == 0) {
         atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);

@@ -26,11 +26,16 @@
 //   layer (the control wave of bank 0): the running totals over the steps,
 //   the decode loop's proof step by step from the control words (growing
 //   the capacity within the slab's buffers, or stopping the layer before a
-//   growth that would not fit), the row every pop takes, the free stack,
-//   free_count and overflow flag the launch leaves, and a header with the
-//   steps the layer runs, the pops that fit and the capacity;
+//   growth that would not fit), free_count and the overflow flag the launch
+//   leaves, and a header with the steps the layer runs, the pops that fit
+//   and the capacity.  With slot maps in LDS (few first touches per launch)
+//   it also lists the row every pop takes and rewrites the free stack; else
+//   it publishes the launch's growth segments (the first pop, stack heights
+//   and capacity of each growth) for the banks to list from;
 //
-//   header (every control wave): waits for the header.
+//   header (every control wave): waits for the header; with slot maps in
+//   global memory each control wave then lists its own bank's pops, and the
+//   layer's last one to finish listing rewrites the free stack.
 //
 // Waves of different workgroups (on different XCDs) exchange only tagged
 // words (common.h): a word is read with device-scope atomic loads until it
@@ -175,12 +180,43 @@ __device__ __forceinline__ PlanControl plan_control(const StepParams& P, int lay
   return c;
 }
 
+// The stack entry at position p after growth segment k: the row the latest
+// growth j <= k whose positions cover p put there, or -1 for the entry the
+// launch found there.
+__device__ __forceinline__ int segment_entry(const int* seg, int p, int k) {
+  const int* const seg_free = seg + kPlanSegments;
+  const int* const seg_old = seg + 3 * kPlanSegments;
+  for (int j = k; j >= 1; --j) {
+    if (p >= seg_free[j]) return seg_old[j] + (p - seg_free[j]);
+  }
+  return -1;
+}
+
+// The growth segment of pop q: the last one whose first pop is at or below q.
+__device__ __forceinline__ int segment_of(const int* seg, int segments, int q) {
+  int lo = 0, hi = segments - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seg[mid] <= q) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 // Layer part, by one wave (the control wave of bank 0), from the control
 // words `pc` it loaded at the launch's start.  `seg` is LDS of
 // 4 * kPlanSegments ints: the launch's growth segments; `jump` LDS of
 // kTraceMaxSteps ints for the proof's jump table.  Publishes the running
 // totals, the pops and the header (last); false when a step total never
 // arrives (the header then says the layer runs no step).
+//
+// Who lists the pops: with BANKS_LIST false this wave lists every pop of the
+// launch and rewrites the free stack before the header (few pops: slot maps
+// that fit in LDS are small, and their slots are mostly mapped after the
+// first steps); with BANKS_LIST true it publishes the growth segments and
+// every control wave lists its own bank's pops after the header (a large
+// address space: a pop for almost every write, more than one wave lists
+// while the banks step).
+template <bool BANKS_LIST>
 __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBlock& pb, int B,
                                   int G0, uint32_t epoch, int* seg, int* jump,
                                   const PlanControl& pc) {
@@ -192,8 +228,18 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
   int* const seg_top = seg + 2 * kPlanSegments;  // stack height after its growth
   int* const seg_old = seg + 3 * kPlanSegments;  // capacity before its growth
 
-  auto publish_head = [&](int steps, int fit, int capacity) __attribute__((always_inline)) {
-    if (lane < 3) {
+  // header: the steps the layer runs, the pops that fit, the capacity, and
+  // when the banks list their pops the stack height the launch found and
+  // its growth segments
+  auto publish_head = [&](int steps, int fit, int capacity, int found = 0, int segments = 1)
+      __attribute__((always_inline)) {
+    if constexpr (BANKS_LIST) {
+      if (lane < 5) {
+        const int v = lane == 0 ? steps : lane == 1 ? fit : lane == 2 ? capacity
+                    : lane == 3 ? found : segments;
+        atomic_store_u64(pb.head + lane, tagged(epoch, static_cast<uint32_t>(v)));
+      }
+    } else if (lane < 3) {
       const int v = lane == 0 ? steps : (lane == 1 ? fit : capacity);
       atomic_store_u64(pb.head + lane, tagged(epoch, static_cast<uint32_t>(v)));
     }
@@ -447,65 +493,81 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
   }
   if (lane == 0) atomic_store_u64(pb.cum + G0, tagged(epoch, static_cast<uint32_t>(cum_g)));
 
-  // ---- the row each pop takes: segment k pops from its top down.  The
-  // stack entry at position p during segment k is the row the latest growth
-  // j <= k whose positions cover p put there, or the entry the launch found.
-  const int32_t* const found = L.free_rows;
-  auto entry = [&](int p, int k) __attribute__((always_inline)) -> int {
-    for (int j = k; j >= 1; --j) {
-      if (p >= seg_free[j]) return seg_old[j] + (p - seg_free[j]);
-    }
-    return found[p];
-  };
-  // A pop's row is arithmetic unless it comes from the stack the launch
-  // found: those are loaded kPopBatch per lane at once.
-  constexpr int kPopBatch = 8;
-  const int listed = vlen < cum_at(stop) ? vlen : cum_at(stop);
-  for (int k = 0; k < nseg; ++k) {
-    const int q0 = seg_q[k];
-    const int q1 = k + 1 < nseg ? seg_q[k + 1] : listed;
-    const int top = seg_top[k];
-    for (int qb = q0; qb < q1; qb += kWave * kPopBatch) {
-      int row[kPopBatch];
-#pragma unroll
-      for (int i = 0; i < kPopBatch; ++i) {
-        const int q = qb + i * kWave + lane;
-        const int p = top - 1 - (q - q0);
-        int v = -1;   // -1: from the stack the launch found
-        for (int j = k; j >= 1; --j) {
-          if (p >= seg_free[j]) {
-            v = seg_old[j] + (p - seg_free[j]);
-            break;
-          }
-        }
-        // the row, or -2 - p for position p of the found stack
-        row[i] = q >= q1 ? 0 : (v >= 0 ? v : -2 - p);
-      }
-#pragma unroll
-      for (int i = 0; i < kPopBatch; ++i) {
-        if (row[i] <= -2) row[i] = found[-2 - row[i]];
-      }
-#pragma unroll
-      for (int i = 0; i < kPopBatch; ++i) {
-        const int q = qb + i * kWave + lane;
-        if (q < q1) atomic_store_u64(pb.pops + q, tagged(epoch, static_cast<uint32_t>(row[i])));
-      }
-    }
-  }
-  // ---- the stack the launch leaves (rewritten only above the lowest
-  // growth, where no pop read it: segment 0 pops read below every growth's
-  // base, later segments below their own)
   const int64_t height = F0 + added - fit;
-  if (nseg > 1) {
-    // every entry the launch found was read before the stack changes
-    __builtin_amdgcn_s_waitcnt(0);
-    int lo = seg_free[1];
-    for (int k = 2; k < nseg; ++k) lo = seg_free[k] < lo ? seg_free[k] : lo;
-    // (the layer struct lists free_rows as read-only for the step kernels;
-    // the plan is the one part that rewrites it)
-    int32_t* const stack = const_cast<int32_t*>(L.free_rows);
-    for (int64_t p = lo + lane; p < height; p += kWave) {
-      stack[p] = entry(static_cast<int>(p), nseg - 1);
+  if constexpr (BANKS_LIST) {
+    // ---- the growth segments, for every bank to list its own pops (when
+    // the launch does not grow, a pop q is the found stack's entry
+    // F0 - 1 - q); the layer's last control wave to list rewrites the stack
+    if (nseg > 1) {
+      for (int k = lane; k < nseg; k += kWave) {
+        int64_t* const w = pb.segs + 4 * static_cast<int64_t>(k);
+        atomic_store_u64(w, tagged(epoch, static_cast<uint32_t>(seg_q[k])));
+        atomic_store_u64(w + 1, tagged(epoch, static_cast<uint32_t>(seg_free[k])));
+        atomic_store_u64(w + 2, tagged(epoch, static_cast<uint32_t>(seg_top[k])));
+        atomic_store_u64(w + 3, tagged(epoch, static_cast<uint32_t>(seg_old[k])));
+      }
+    }
+  } else {
+    // ---- the row each pop takes: segment k pops from its top down.  The
+    // stack entry at position p during segment k is the row the latest
+    // growth j <= k whose positions cover p put there, or the entry the
+    // launch found.
+    const int32_t* const found = L.free_rows;
+    auto entry = [&](int p, int k) __attribute__((always_inline)) -> int {
+      for (int j = k; j >= 1; --j) {
+        if (p >= seg_free[j]) return seg_old[j] + (p - seg_free[j]);
+      }
+      return found[p];
+    };
+    // A pop's row is arithmetic unless it comes from the stack the launch
+    // found: those are loaded kPopBatch per lane at once.
+    constexpr int kPopBatch = 8;
+    const int listed = vlen < cum_at(stop) ? vlen : cum_at(stop);
+    for (int k = 0; k < nseg; ++k) {
+      const int q0 = seg_q[k];
+      const int q1 = k + 1 < nseg ? seg_q[k + 1] : listed;
+      const int top = seg_top[k];
+      for (int qb = q0; qb < q1; qb += kWave * kPopBatch) {
+        int row[kPopBatch];
+#pragma unroll
+        for (int i = 0; i < kPopBatch; ++i) {
+          const int q = qb + i * kWave + lane;
+          const int p = top - 1 - (q - q0);
+          int v = -1;   // -1: from the stack the launch found
+          for (int j = k; j >= 1; --j) {
+            if (p >= seg_free[j]) {
+              v = seg_old[j] + (p - seg_free[j]);
+              break;
+            }
+          }
+          // the row, or -2 - p for position p of the found stack
+          row[i] = q >= q1 ? 0 : (v >= 0 ? v : -2 - p);
+        }
+#pragma unroll
+        for (int i = 0; i < kPopBatch; ++i) {
+          if (row[i] <= -2) row[i] = found[-2 - row[i]];
+        }
+#pragma unroll
+        for (int i = 0; i < kPopBatch; ++i) {
+          const int q = qb + i * kWave + lane;
+          if (q < q1) atomic_store_u64(pb.pops + q, tagged(epoch, static_cast<uint32_t>(row[i])));
+        }
+      }
+    }
+    // ---- the stack the launch leaves (rewritten only above the lowest
+    // growth, where no pop read it: segment 0 pops read below every
+    // growth's base, later segments below their own)
+    if (nseg > 1) {
+      // every entry the launch found was read before the stack changes
+      __builtin_amdgcn_s_waitcnt(0);
+      int lo = seg_free[1];
+      for (int k = 2; k < nseg; ++k) lo = seg_free[k] < lo ? seg_free[k] : lo;
+      // (the layer struct lists free_rows as read-only for the step
+      // kernels; the plan is the one part that rewrites it)
+      int32_t* const stack = const_cast<int32_t*>(L.free_rows);
+      for (int64_t p = lo + lane; p < height; p += kWave) {
+        stack[p] = entry(static_cast<int>(p), nseg - 1);
+      }
     }
   }
   if (lane == 0) {
@@ -534,22 +596,55 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  publish_head(stop, vlen, static_cast<int>(capacity));
+  publish_head(stop, vlen, static_cast<int>(capacity), F0, nseg);
   return true;
 }
 
-// Header part: the steps the layer runs, the pops that fit and the capacity
-// the launch grows to.  False when the header never arrives.
-__device__ inline bool plan_header(const PlanBlock& pb, uint32_t epoch, int& steps, int& fit,
-                                   int& capacity) {
+// Header part: the steps the layer runs, the pops that fit, the capacity
+// the launch grows to, and with BANKS_LIST the stack height it found and its
+// growth segments (else left as they are).  False when the header never
+// arrives.
+struct PlanHeader {
+  int steps, fit, capacity, found, segments;
+};
+template <bool BANKS_LIST>
+__device__ inline bool plan_header(const PlanBlock& pb, uint32_t epoch, PlanHeader& h) {
   const int lane = static_cast<int>(threadIdx.x) % kWave;
+  constexpr int kWords = BANKS_LIST ? 5 : 3;
   uint64_t w;
-  if (!poll_tagged(pb.head + (lane < 3 ? lane : 0), lane < 3, epoch, w)) return false;
+  if (!poll_tagged(pb.head + (lane < kWords ? lane : 0), lane < kWords, epoch, w)) return false;
   const int v = static_cast<int>(static_cast<uint32_t>(w));
-  steps = __builtin_amdgcn_readlane(v, 0);
-  fit = __builtin_amdgcn_readlane(v, 1);
-  capacity = __builtin_amdgcn_readlane(v, 2);
+  h.steps = __builtin_amdgcn_readlane(v, 0);
+  h.fit = __builtin_amdgcn_readlane(v, 1);
+  h.capacity = __builtin_amdgcn_readlane(v, 2);
+  if constexpr (BANKS_LIST) {
+    h.found = __builtin_amdgcn_readlane(v, 3);
+    h.segments = __builtin_amdgcn_readlane(v, 4);
+  }
   return true;
+}
+
+// A launch's growth segments (plan_layer), staged into `seg` (LDS of
+// 4 * kPlanSegments ints: first pops, stack heights before and after each
+// growth, capacities before it) by one wave.  False when one never arrives.
+__device__ inline bool plan_segments(const PlanBlock& pb, uint32_t epoch, int segments,
+                                     int* seg) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  bool ok = true;
+  for (int k0 = 0; k0 < segments; k0 += kWave) {
+    const int k = k0 + lane;
+    const bool in = k < segments;
+    const int64_t* const w = pb.segs + 4 * static_cast<int64_t>(in ? k : 0);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      uint64_t x;
+      ok = poll_tagged(w + f, in, epoch, x) && ok;
+      if (in) seg[f * kPlanSegments + k] = static_cast<int>(static_cast<uint32_t>(x));
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return ok;
 }
 
 }  // namespace cowsdm_impl

@@ -313,6 +313,18 @@ def test_decode_loop_matches_reference_loop(device, launch_steps, capacity, quan
                       steps=37, capacity=capacity, quantum=quantum)
 
 
+@pytest.mark.parametrize("launch_steps,reserve", [(64, 50), (7, 50), (64, 0)])
+def test_decode_loop_banks_list_their_pops(device, launch_steps, reserve):
+    """Slot maps in global memory (N above the 4,096 that fit in LDS): every
+    bank lists its own pops from the launch's growth segments and the layer's
+    last control wave to list rewrites the free stack.  Almost every write is
+    a first touch, so a launch grows at nearly every step (growth inside the
+    reserved slab buffers, or past them on the host without a reserve)."""
+
+    _decode_loop_case(device, launch_steps, layers=2, banks=8, slots=4500, width=64,
+                      steps=50, capacity=24, quantum=16, reserve=reserve)
+
+
 def test_decode_loop_long_launch(device):
     """One launch of 400 steps over 4,096 slots with room for every slot."""
 
