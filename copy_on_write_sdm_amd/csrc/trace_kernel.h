@@ -48,6 +48,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <atomic>
+
 #include "common.h"
 #include "trace_plan.h"
 
@@ -1736,13 +1738,16 @@ int32_t launch_trace_count(const StepParams& P, hipStream_t stream, hipEvent_t s
 extern template int32_t launch_trace_count<int32_t>(const StepParams&, hipStream_t, hipEvent_t);
 extern template int32_t launch_trace_count<int64_t>(const StepParams&, hipStream_t, hipEvent_t);
 
-// Residency of one persistent kernel variant on one device: how many of its
-// workgroups the device holds at once for a given slot-map size.
-struct TraceResidency {
-  int device = -1;
-  int slots = -1;
-  int blocks = 0;
-};
+// Residency of one persistent kernel variant: how many of its workgroups a
+// device holds at once for a given slot-map size, cached as one word
+// (device + 1 in bits 48-63, the slot-map key in bits 24-47, the workgroups
+// in bits 0-23; 0: nothing cached) so that a reader never pairs one query's
+// key with another's count.
+__host__ inline uint64_t residency_word(int device, int key, int blocks) {
+  return (static_cast<uint64_t>(device + 1) << 48) |
+         ((static_cast<uint64_t>(key) & 0xFFFFFFu) << 24) |
+         (static_cast<uint64_t>(blocks) & 0xFFFFFFu);
+}
 
 // Workgroups of a persistent launch wait on one another, so every one of them
 // must be resident at once.  Returns 0 when launched, 1 (nothing launched)
@@ -1785,9 +1790,9 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
        reinterpret_cast<const void*>(&sdm_trace_kernel<IDX, 4, DENSE, true, true, MAPLDS>)}};
   // Residency depends on the device and on the LDS map's size: cached per
   // kernel variant for the last (device, slot count) it was asked for.  The
-  // cache is process-wide; a library call made from several host threads at
-  // once may query the occupancy twice, which is harmless.
-  static TraceResidency resident[4][3];
+  // cache is process-wide and each entry one atomic word; host threads
+  // calling at once may each query the occupancy, which is harmless.
+  static std::atomic<uint64_t> resident[4][3];
   const int which = vec == 4 ? 2 : (vec == 2 ? 1 : 0);
   const void* kernel = kernels[variant][which];
   // map in LDS: per bank the slot map
@@ -1800,25 +1805,28 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
     (void)hipGetLastError();
     return 1;
   }
-  TraceResidency& cached = resident[variant][which];
-  if (cached.device != device || cached.slots != key) {
+  int resident_blocks = 0;
+  const uint64_t cached = resident[variant][which].load(std::memory_order_relaxed);
+  if (cached != 0 && (cached >> 24) == (residency_word(device, key, 0) >> 24)) {
+    resident_blocks = static_cast<int>(cached & 0xFFFFFFu);
+  } else {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kTraceThreads, lds_bytes) !=
             hipSuccess) {
       (void)hipGetLastError();
-      cached.blocks = 0;
+      resident_blocks = 0;
     } else {
-      cached.blocks = cus * per_cu;
+      resident_blocks = cus * per_cu;
     }
-    cached.device = device;
-    cached.slots = key;
+    resident[variant][which].store(residency_word(device, key, resident_blocks),
+                                   std::memory_order_relaxed);
   }
   // Layers are independent within a launch: when the whole grid cannot be
   // resident, launch groups of layers that can, one after another on the
   // stream, each with its per-layer words offset to its first layer.
-  const int per_launch = cached.blocks / P.blocks_per_layer;
+  const int per_launch = resident_blocks / P.blocks_per_layer;
   if (per_launch <= 0) return 1;
   // With timing on, events at the launch's first kernel's start (the count
   // pass of packed state), at the decode kernel's start and at its end.
@@ -1836,7 +1844,7 @@ int32_t launch_trace_kernels(const StepParams& P0, int vec, hipStream_t stream) 
                              start, last ? stop : nullptr, 0);
     start = nullptr;
   };
-  if (blocks <= cached.blocks) {
+  if (blocks <= resident_blocks) {
     launch(&P, blocks, true);
     return 0;  // a failed launch is reported by the caller's launch_status()
   }
