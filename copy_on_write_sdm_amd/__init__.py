@@ -24,6 +24,7 @@ from .inference import (
     pack_prefill_layer,
 )
 from .routing import product_key_routes
+from .recurrence import dense_sparse_routes, gated_delta_recurrence, sdm_recurrence
 from .controller import (
     ControllerStep,
     SDMController,
@@ -47,11 +48,14 @@ __all__ = [
     "decode_sdm_layer_dense",
     "dense_sdm_sparse_step",
     "dense_sdm_sparse_step_layers",
+    "dense_sparse_routes",
     "finish_sdm_step",
+    "gated_delta_recurrence",
     "mark_written",
     "pack_prefill_layer",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
     "prepare_sdm_step",
     "product_key_routes",
+    "sdm_recurrence",
 ]

@@ -24,7 +24,8 @@ REPO_DIR = PACKAGE_DIR.parent
 SOURCE_DIR = PACKAGE_DIR / "csrc"
 # one translation unit per step-kernel family so hipcc can run in parallel
 SOURCES = ("cowsdm.hip", "step_i32_packed.hip", "step_i32_dense.hip", "step_i64_packed.hip",
-           "step_i64_dense.hip", "trace_plan.hip", "routes.hip", "controller.hip")
+           "step_i64_dense.hip", "trace_plan.hip", "routes.hip", "controller.hip",
+           "recurrence.hip")
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libcowsdm.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
@@ -69,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -214,6 +215,27 @@ class Controller(ctypes.Structure):
     ]
 
 
+class Recurrence(ctypes.Structure):
+    """cowsdm_recurrence_t."""
+
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("time", ctypes.c_int64),
+        ("slots", ctypes.c_int64),
+        ("width", ctypes.c_int64),
+        ("initial_memory", ctypes.c_void_p),
+        ("write_routes", ctypes.c_void_p),
+        ("values", ctypes.c_void_p),
+        ("input_gate", ctypes.c_void_p),
+        ("erase_gate", ctypes.c_void_p),
+        ("forget_log_gate", ctypes.c_void_p),
+        ("read_routes", ctypes.c_void_p),
+        ("readings", ctypes.c_void_p),
+        ("states", ctypes.c_void_p),
+        ("final_memory", ctypes.c_void_p),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -231,6 +253,8 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_controller_prepare": (
         _I32, [ctypes.POINTER(Controller), _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "cowsdm_controller_finish": (_I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P]),
+    "cowsdm_recurrence_forward": (_I32, [ctypes.POINTER(Recurrence), _P]),
+    "cowsdm_dense_routes": (_I32, [_P, _P, _I32, _I64, _I64, _I64, _P, _P, _P]),
     "cowsdm_host_report_alloc": (
         _I32, [_I64, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "cowsdm_host_report_free": (_I32, [_P]),

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 6
+#define COWSDM_ABI_VERSION 7
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -539,6 +539,46 @@ int32_t cowsdm_controller_prepare(const cowsdm_controller_t* controller, const f
 int32_t cowsdm_controller_finish(const cowsdm_controller_t* controller,
                                  const float* normalized, const float* reading,
                                  int64_t batch, float* out, void* stream);
+
+/* ------------------------------------------ dense recurrence (prefill) */
+
+/* One SDM layer's token-serial recurrence over dense route vectors
+ * (float32, device, contiguous).  Replaces _native_sdm_forward_kernel
+ * (sdm.py:534-607) as _NativeSDMRecurrence.forward launches it
+ * (sdm.py:779-861; gated_delta_recurrence, sdm.py:962-995).  Per batch row b
+ * and token t: memory rows with a nonzero write route decay by
+ * exp(forget_log_gate[b, t]); retrieved = sum_n write_routes * memory;
+ * memory += write_routes * (input_gate * values - erase_gate * retrieved);
+ * readings[b, t] = sum_n read_routes * memory. */
+typedef struct cowsdm_recurrence {
+  int64_t batch;                /* B                                   */
+  int64_t time;                 /* T                                   */
+  int64_t slots;                /* N <= 1024                           */
+  int64_t width;                /* D                                   */
+  const float* initial_memory;  /* [B, N, D]                           */
+  const float* write_routes;    /* [B, T, N]                           */
+  const float* values;          /* [B, T, D]                           */
+  const float* input_gate;      /* [B, T]                              */
+  const float* erase_gate;      /* [B, T]                              */
+  const float* forget_log_gate; /* [B, T]                              */
+  const float* read_routes;     /* [B, T, N]                           */
+  float* readings;              /* [B, T, D]                           */
+  float* states;                /* [B, T, N, D] per-token memory, or null */
+  float* final_memory;          /* [B, N, D], or null                  */
+} cowsdm_recurrence_t;
+
+/* Runs the recurrence of cowsdm_recurrence_t; COWSDM_ELIMIT for N > 1024
+ * (the reference's "at most 1,024 slots"). */
+int32_t cowsdm_recurrence_forward(const cowsdm_recurrence_t* recurrence, void* stream);
+
+/* Dense route vectors from sparse routes, sdm.py:162-172
+ * (dense_sparse_routes): dense [rows, slots] = 0 except
+ * dense[row, indices[row, k]] = weights[row, k] (the last k wins for a
+ * repeated index).  An index outside [0, slots) sets bit 0x1 of *bad
+ * (device int32, not cleared here; may be null). */
+int32_t cowsdm_dense_routes(const float* weights, const void* indices, int32_t index_dtype,
+                            int64_t rows, int64_t per_row, int64_t slots, float* dense,
+                            int32_t* bad, void* stream);
 
 #ifdef __cplusplus
 }

@@ -38,7 +38,7 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 6
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 7
     # epoch and header, plan words [banks][steps], step and running totals,
     # at most banks * W pops per step and 4 words per growth segment, int64 each
     assert lib.cowsdm_trace_scan_words(64, 4, 512) == (16 + 64 * 512 + 512 + 513 + 64 * 512 * 4
@@ -116,7 +116,30 @@ def test_structure_layout_matches_header():
     assert ctypes.sizeof(nat.Layer) == 21 * 8
     assert ctypes.sizeof(nat.Shape) == 7 * 8
     assert ctypes.sizeof(nat.Trace) == 20 * 8
+    assert ctypes.sizeof(nat.Recurrence) == 14 * 8
+    assert ctypes.sizeof(nat.Controller) == 15 * 8 + 2 * 4
     assert nat.REPORT_WORDS == 2 + nat.CTRL_WORDS == 14
+
+
+def test_recurrence_argument_errors():
+    """Rejected before any launch, so no GPU is needed."""
+
+    lib = nat.lib()
+    assert lib.cowsdm_recurrence_forward(None, None) == -1
+    r = nat.Recurrence()
+    r.batch, r.time, r.slots, r.width = 2, 3, 1025, 8
+    assert lib.cowsdm_recurrence_forward(r, None) == -2
+    assert b"at most 1024 slots" in lib.cowsdm_last_error_string()
+    r.slots = 0
+    assert lib.cowsdm_recurrence_forward(r, None) == -1
+    r.slots, r.batch = 16, 0
+    assert lib.cowsdm_recurrence_forward(r, None) == 0       # nothing to run
+    r.batch = 1
+    assert lib.cowsdm_recurrence_forward(r, None) == -1      # null tensors
+    assert lib.cowsdm_dense_routes(None, None, 0, 4, 2, 0, None, None, None) == -1
+    assert lib.cowsdm_dense_routes(None, None, 7, 4, 2, 16, None, None, None) == -1
+    assert lib.cowsdm_dense_routes(None, None, 0, 0, 2, 16, None, None, None) == 0
+    assert lib.cowsdm_dense_routes(None, None, 0, 4, 2, 16, None, None, None) == -1
 
 
 @pytest.mark.parametrize("name", ["cowsdm_packed_step", "cowsdm_dense_step",
