@@ -294,6 +294,7 @@ def main() -> int:
     # handoff itself
     m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=args.seed, device=dev)
     handoff_ms = None
+    prefill_info = None
     if PREFIX:
         prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=banks, slots=SLOTS,
                                       width=WIDTH, writes=WRITES, reads=READS,
@@ -306,8 +307,42 @@ def main() -> int:
                                   forget_log_gate=prefix.forget_log_gate,
                                   read_indices=prefix.read_indices,
                                   read_weights=prefix.read_weights)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         prefill.launch(PREFIX, start=0)
+        e1.record()
         torch.cuda.synchronize()
+        prefill_info = {"trace_ms": round(e0.elapsed_time(e1), 3)}
+        # the same prefill through the dense-route recurrence (the reference's
+        # prefill kernel): route scatter and recurrence per layer, timed
+        # together, and its final memory against the trace's tables
+        def per_bank(t):
+            return t.transpose(0, 1).contiguous()
+
+        rec_finals, diff = [], 0.0
+        e0.record()
+        for l in range(LAYERS):
+            wr = cow.dense_sparse_routes(per_bank(prefix.write_weights[:, l]),
+                                         per_bank(prefix.write_indices[:, l]), SLOTS)
+            rr = cow.dense_sparse_routes(per_bank(prefix.read_weights[:, l]),
+                                         per_bank(prefix.read_indices[:, l]), SLOTS)
+            rec_finals.append(cow.gated_delta_recurrence(
+                m0[l][templates].contiguous(), wr, per_bank(prefix.values[:, l]),
+                per_bank(prefix.input_gate[:, l]), per_bank(prefix.forget_log_gate[:, l]),
+                rr)[1])
+        e1.record()
+        torch.cuda.synchronize()
+        diff = max(float((f - t).abs().max()) for f, t in zip(rec_finals, tables))
+        del rec_finals, wr, rr
+        rec_ms = e0.elapsed_time(e1)
+        prefill_info.update({
+            "recurrence_ms": round(rec_ms, 3),
+            "trace_tokens_per_s": round(B * PREFIX / (prefill_info["trace_ms"] / 1e3), 1),
+            "recurrence_tokens_per_s": round(B * PREFIX / (rec_ms / 1e3), 1),
+            "recurrence_vs_trace_max_abs_diff": diff,
+            "what": "prefill of all layers: the sparse decode kernel (one launch over the "
+                    "prefix) against dense_sparse_routes + the dense-route recurrence per layer "
+                    "(different summation orders: a float tolerance, not bit equality)"})
         t0 = time.perf_counter()
         states = []
         for l in range(LAYERS):
@@ -408,6 +443,11 @@ def main() -> int:
         raise AssertionError("packed decode did not consume the trace")
     allocator = {
         "handoff_ms": None if handoff_ms is None else round(handoff_ms, 3),
+        # the handoff reads every live row from the dense table and writes it
+        # into the slab (2 x 4 B x D per row)
+        "handoff_gbps": (None if not handoff_ms else
+                         round(2 * 4 * WIDTH * sum(handoff_rows) / (handoff_ms / 1e3) / 1e9, 1)),
+        "prefill": prefill_info,
         "handoff_live_rows": sum(handoff_rows),
         "handoff_capacity_rows": sum(handoff_capacity),
         "live_rows_after": sum(int(st.allocated_rows_tensor()) for st in states),
