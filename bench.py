@@ -25,7 +25,10 @@ Timing, as the reference's benchmark (5 warmup and 20 timed steps, median of
 5 repetitions, experiments/benchmark_serving.py:1002-1066): W untimed warmup
 steps, then 5 repetitions of exactly K steps, each between synchronisations;
 the median repetition is reported (0.1 s of untimed dense-control launches
-on scratch tables warm the GPU first).  The same per-token loop is also
+on scratch tables warm the GPU first).  Five more repetitions of the next K
+steps each record HIP events at the decode kernel's own start and end for
+the roofline; the wall-clock repetitions run without them (they add about
+20 us of host time per launch).  The same per-token loop is also
 timed as the reference's call pattern on the per-layer kernel (eager) and as
 one captured graph replay per token (graph_step).  The dense-table control runs the same
 routes the same way from the same packed state; both end states must be
@@ -287,7 +290,7 @@ def main() -> int:
         torch.empty_like(src).copy_(src)
         torch.cuda.synchronize()
         del src
-    total_steps = Wm + repeats * K
+    total_steps = Wm + 2 * repeats * K      # wall-clock and kernel-timing repetitions
     quantum = max(16, banks * WRITES * 4)
 
     # ---- prefill (dense kernel) and copy-on-write handoff, untimed except the
@@ -392,27 +395,40 @@ def main() -> int:
         return 0 if trace.dense else sum(int(st.allocated_rows_tensor()) for st in trace.tables)
 
     def measure(trace):
+        """`repeats` wall-clock repetitions of K steps with the library's
+        launch events off (they cost the host about 20 us per launch), then
+        `repeats` more of the next K steps each with HIP events at every
+        decode kernel's own start and end on the launch stream."""
+
+        def growths() -> int:
+            return 0 if trace.dense else sum(st.growth_events for st in trace.tables)
+
         trace.set_step(0)
-        # the warmup takes the same host path as the timed runs, timing included
-        lib.cowsdm_trace_timing(1)
-        trace.run(Wm, launch_steps=args.launch_steps)
+        lib.cowsdm_trace_timing(0)
+        trace.run(Wm, launch_steps=args.launch_steps)   # warmup: the timed runs' host path
         torch.cuda.synchronize()
-        launch_times()
         reps = []
         for _ in range(repeats):
-            rows0 = live_rows(trace)
-            grow0 = 0 if trace.dense else sum(st.growth_events for st in trace.tables)
+            rows0, grow0 = live_rows(trace), growths()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             report = trace.run(K, launch_steps=args.launch_steps)
             torch.cuda.synchronize()
             seconds = time.perf_counter() - t0
+            reps.append(dict(seconds=seconds, new_rows=live_rows(trace) - rows0,
+                             growths=growths() - grow0, **report))
+        lib.cowsdm_trace_timing(1)
+        launch_times()
+        for rep in reps:
+            rows0, grow0 = live_rows(trace), growths()
+            torch.cuda.synchronize()
+            report = trace.run(K, launch_steps=args.launch_steps)
+            torch.cuda.synchronize()
             span_ms, kernel_ms, launches = launch_times()
-            reps.append(dict(
-                seconds=seconds, span_ms=span_ms, kernel_ms=kernel_ms, timed_launches=launches,
-                new_rows=live_rows(trace) - rows0,
-                growths=(0 if trace.dense else
-                         sum(st.growth_events for st in trace.tables) - grow0), **report))
+            rep.update(span_ms=span_ms, kernel_ms=kernel_ms, timed_launches=launches,
+                       kernel_new_rows=live_rows(trace) - rows0,
+                       kernel_growths=growths() - grow0,
+                       kernel_growth_rounds=report["growth_rounds"])
         lib.cowsdm_trace_timing(0)
         return reps
 
@@ -554,7 +570,7 @@ def main() -> int:
     timed_steps = repeats * K
     kernel_us = 1000.0 * sum(r["kernel_ms"] for r in p_reps) / launches
     span_us = 1000.0 * sum(r["span_ms"] for r in p_reps) / launches
-    new_rows = sum(r["new_rows"] for r in p_reps)
+    new_rows = sum(r["kernel_new_rows"] for r in p_reps)
     bytes_per_launch = (algorithmic_bytes(banks, LAYERS) * timed_steps + 8 * new_rows) / launches
     achieved = bytes_per_launch / (kernel_us * 1e-6) / 1e9
     d_launches = sum(r["timed_launches"] for r in d_reps)
@@ -587,6 +603,10 @@ def main() -> int:
         "repeat_kernel_us": [round(1000.0 * r["kernel_ms"] / max(1, r["timed_launches"]), 3)
                              for r in p_reps],
         "repeat_growths": [r["growths"] for r in p_reps],
+        "timing": ("value and repeat_tokens_per_s: wall clock of repetitions with the "
+                   "library's launch events off; kernel_us and repeat_kernel_us: HIP events "
+                   "at the decode kernel's own start and end in the next repetitions of K "
+                   "steps (the events add about 20 us of host time per launch)"),
         "config": {
             "workload": (f"config {args.config}: {cfg['text']}; L={LAYERS} H={HEADS} "
                          f"N={SLOTS} D={WIDTH} top-{WRITES} write / top-{READS} read "
