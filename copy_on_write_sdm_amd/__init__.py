@@ -25,6 +25,7 @@ from .inference import (
 )
 from .routing import product_key_routes
 from .recurrence import dense_sparse_routes, gated_delta_recurrence, sdm_recurrence
+from .prefill import SDMPrefill, prefill_sdm_layer
 from .controller import (
     ControllerStep,
     SDMController,
@@ -38,6 +39,7 @@ __all__ = [
     "ControllerStep",
     "DecodeTrace",
     "SDMController",
+    "SDMPrefill",
     "FaithfulSDMDecodeState",
     "PackedSDMCopyOnWriteState",
     "SDMCopyOnWriteStep",
@@ -55,6 +57,7 @@ __all__ = [
     "pack_prefill_layer",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
+    "prefill_sdm_layer",
     "prepare_sdm_step",
     "product_key_routes",
     "sdm_recurrence",
