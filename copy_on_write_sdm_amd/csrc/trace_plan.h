@@ -577,24 +577,25 @@ __device__ inline bool plan_layer(const StepParams& P, int layer, const PlanBloc
     } else if (nseg > 1) {
       *L.overflow_flag = 0;   // grow_capacity clears it
     }
-    // device-scope stores: the layer's report reads them back during the
-    // launch, possibly from another XCD, whose L2 does not see this one's
-    // dirty lines
-    auto put = [&](int k, int64_t v) __attribute__((always_inline)) {
-      atomic_store_u64(&control_word(P, layer, k), static_cast<uint64_t>(v));
-    };
-    put(COWSDM_CTRL_PROVEN, over ? 0 : proven);
-    put(COWSDM_CTRL_CAPACITY, capacity);
-    put(COWSDM_CTRL_EVENTS, events0 + events);
-    put(COWSDM_CTRL_ADDED, added0 + rows_added);
-    put(COWSDM_CTRL_COPIED, copied0 + rows_copied);
-    put(COWSDM_CTRL_FREE, height);
-    put(COWSDM_CTRL_STEPS, stop);
-    put(COWSDM_CTRL_FIT, vlen);
     if (stop < G0 && P.trace_status) {
       __hip_atomic_fetch_or(&P.trace_status[layer], int32_t{COWSDM_TRACE_REFUSED},
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  // the control words the launch leaves, one lane each: device-scope
+  // stores, since the layer's report reads them back during the launch,
+  // possibly from another XCD, whose L2 does not see this one's dirty lines
+  if (lane < 8) {
+    int k = COWSDM_CTRL_PROVEN;
+    int64_t v = over ? 0 : proven;
+    if (lane == 1) { k = COWSDM_CTRL_CAPACITY; v = capacity; }
+    if (lane == 2) { k = COWSDM_CTRL_EVENTS; v = events0 + events; }
+    if (lane == 3) { k = COWSDM_CTRL_ADDED; v = added0 + rows_added; }
+    if (lane == 4) { k = COWSDM_CTRL_COPIED; v = copied0 + rows_copied; }
+    if (lane == 5) { k = COWSDM_CTRL_FREE; v = height; }
+    if (lane == 6) { k = COWSDM_CTRL_STEPS; v = stop; }
+    if (lane == 7) { k = COWSDM_CTRL_FIT; v = vlen; }
+    atomic_store_u64(&control_word(P, layer, k), static_cast<uint64_t>(v));
   }
   publish_head(stop, vlen, static_cast<int>(capacity), F0, nseg);
   return true;
