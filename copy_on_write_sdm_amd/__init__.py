@@ -25,7 +25,12 @@ from .inference import (
 )
 from .routing import product_key_routes
 from .recurrence import dense_sparse_routes, gated_delta_recurrence, sdm_recurrence
-from .prefill import SDMPrefill, prefill_sdm_layer
+from .prefill import (
+    SDMPrefill,
+    allocate_dense_cache,
+    prefill_faithful_sdm_stack,
+    prefill_sdm_layer,
+)
 from .controller import (
     ControllerStep,
     SDMController,
@@ -44,6 +49,7 @@ __all__ = [
     "PackedSDMCopyOnWriteState",
     "SDMCopyOnWriteStep",
     "SDMStepInputs",
+    "allocate_dense_cache",
     "decode_sdm_layer",
     "decode_sdm_layer_controller",
     "decode_sdm_layer_controller_dense",
@@ -57,6 +63,7 @@ __all__ = [
     "pack_prefill_layer",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
+    "prefill_faithful_sdm_stack",
     "prefill_sdm_layer",
     "prepare_sdm_step",
     "product_key_routes",

@@ -18,10 +18,12 @@ projection).  Float32; there is no CPU path.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import Callable, Sequence
 
 import torch
 
 from .controller import SDMController, finish_sdm_step, prepare_sdm_step
+from .inference import FaithfulSDMDecodeState, pack_prefill_layer
 from .recurrence import dense_sparse_routes, gated_delta_recurrence
 
 
@@ -95,3 +97,108 @@ def prefill_sdm_layer(controller: SDMController, initial_memory: torch.Tensor,
         write_indices=routed(x.write_indices), write_weights=routed(x.write_weights),
         forget_log_gate=routed(x.forget_log_gate), input_gate=routed(x.input_gate),
         values=routed(x.values), final_memory=final.reshape(batch, heads, slots, head_width))
+
+
+def allocate_dense_cache(key: torch.Tensor, value: torch.Tensor,
+                         capacity: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """An attention layer's K/V cache for ``capacity`` positions holding the
+    prefix's keys and values [B, heads, T, head_width] in its first T
+    positions (inference.py:293-306)."""
+
+    batch, heads, time, head_width = key.shape
+    if value.shape != key.shape or capacity < time:
+        raise ValueError("dense prefill cache capacity is invalid")
+    shape = (batch, heads, capacity, head_width)
+    key_cache = torch.empty(shape, device=key.device, dtype=key.dtype)
+    value_cache = torch.empty(shape, device=value.device, dtype=value.dtype)
+    key_cache[:, :, :time].copy_(key)
+    value_cache[:, :, :time].copy_(value)
+    return key_cache, value_cache
+
+
+AttentionBlock = Callable[[int, torch.Tensor], tuple[torch.Tensor, torch.Tensor, torch.Tensor]]
+SDMBlockTail = Callable[[int, torch.Tensor], torch.Tensor]
+
+
+@torch.no_grad()
+def prefill_faithful_sdm_stack(
+    layout: str,
+    sdm_layers: Sequence[tuple[SDMController, torch.Tensor]],
+    tokens: torch.Tensor,
+    *,
+    attention_block: AttentionBlock | None = None,
+    sdm_tail: SDMBlockTail | None = None,
+    capacity: int | None = None,
+    sdm_capacity_rows: int | Sequence[int] | None = None,
+    sdm_growth_quantum_rows: int = 0,
+) -> tuple[torch.Tensor, FaithfulSDMDecodeState]:
+    """``prefill_faithful_sdm_stack`` (inference.py:369-456) with the SDM
+    layers on the device: every "B" layer of ``layout`` runs
+    ``prefill_sdm_layer`` on the tokens entering it, adds its output and
+    hands its final memory to copy-on-write state (``pack_prefill_layer``);
+    the model's other parts stay the caller's:
+
+    * ``attention_block(layer, tokens) -> (tokens, key, value)`` for an "A"
+      layer: the block's residual stream after it, and the prefix's keys and
+      values [B, heads, T, head_width] (the reference's
+      ``attention.prefill_with_cache`` plus its MLP);
+    * ``sdm_tail(layer, tokens) -> tokens`` after an SDM layer's residual
+      add (the reference's SDM MLP; identity when omitted).
+
+    ``sdm_layers`` holds each "B" layer's controller and initial memory
+    [H, N, head_width] in layout order.  Returns the final tokens and the
+    decode state, with the attention layers' K/V caches for ``capacity``
+    positions."""
+
+    if tokens.ndim != 3:
+        raise ValueError("tokens must be [B,T,width]")
+    batch, time, _ = tokens.shape
+    if time <= 0:
+        raise ValueError("prefill requires at least one token")
+    selected_capacity = time if capacity is None else capacity
+    if selected_capacity < time:
+        raise ValueError("prefill capacity is shorter than the prefix")
+    if sdm_growth_quantum_rows < 0:
+        raise ValueError("SDM growth quantum cannot be negative")
+    layer_positions = tuple(i for i, kind in enumerate(layout) if kind == "B")
+    if len(sdm_layers) != len(layer_positions):
+        raise ValueError("one controller and initial memory per B layer")
+    if isinstance(sdm_capacity_rows, Sequence) and not isinstance(sdm_capacity_rows,
+                                                                   (str, bytes)):
+        per_layer = tuple(int(v) for v in sdm_capacity_rows)
+        if len(per_layer) != len(layer_positions):
+            raise ValueError("SDM capacities must contain one value per B layer")
+    else:
+        per_layer = (sdm_capacity_rows,) * len(layer_positions)
+    if any(kind not in "AB" for kind in layout):
+        raise ValueError("layout holds A (attention) and B (SDM) layers only")
+    if "A" in layout and attention_block is None:
+        raise ValueError("an attention layer needs attention_block")
+
+    keys: list[torch.Tensor] = []
+    values: list[torch.Tensor] = []
+    states = []
+    sdm_index = 0
+    for layer, kind in enumerate(layout):
+        if kind == "A":
+            tokens, key, value = attention_block(layer, tokens)
+            key_cache, value_cache = allocate_dense_cache(key, value, selected_capacity)
+            keys.append(key_cache)
+            values.append(value_cache)
+            continue
+        controller, initial_memory = sdm_layers[sdm_index]
+        pre = prefill_sdm_layer(controller, initial_memory, tokens)
+        tokens = tokens + pre.output
+        if sdm_tail is not None:
+            tokens = sdm_tail(layer, tokens)
+        states.append(pack_prefill_layer(
+            initial_memory, pre.final_memory, pre.write_indices,
+            capacity_rows=per_layer[sdm_index], decode_capacity=selected_capacity,
+            growth_quantum_rows=sdm_growth_quantum_rows))
+        del pre
+        sdm_index += 1
+    return tokens, FaithfulSDMDecodeState(
+        layout=layout, position=time, capacity=selected_capacity, activation_dtype=tokens.dtype,
+        active_sequences=torch.ones(batch, device=tokens.device, dtype=torch.bool),
+        sdm_layer_positions=layer_positions, sdm_states=tuple(states),
+        dense_keys=tuple(keys), dense_values=tuple(values))

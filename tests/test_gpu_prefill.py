@@ -96,3 +96,72 @@ def test_prefill_argument_errors(device):
         cow.prefill_sdm_layer(controller, m0, torch.zeros(2, 0, 32, device=device))
     with pytest.raises(ValueError, match="initial memory"):
         cow.prefill_sdm_layer(controller, m0[:1], torch.zeros(2, 3, 32, device=device))
+
+
+def test_stack_prefill_and_admission(device):
+    """prefill_faithful_sdm_stack (inference.py:369-456) over a "BAB"
+    layout with the model's attention block and SDM tail supplied as
+    callables: its tokens equal the same composition of prefill_sdm_layer
+    calls bit for bit, every SDM layer's state materialises to that layer's
+    final memory, the attention caches hold the prefix's keys and values;
+    then a second prefilled cohort is admitted (inference.py:161-206): every
+    SDM layer holds both cohorts' memories and the caches are stacked."""
+
+    width, slots, heads, batch, time = 64, 64, 2, 3, 7
+    g = torch.Generator().manual_seed(17)
+    layers = [make_layer(width, slots=slots, reads=8, writes=4, heads=heads, seed=s,
+                         dtype=torch.float32) for s in (5, 6)]
+    ctrls = [cow.SDMController.from_module(layer, device=device) for layer in layers]
+    m0s = [(torch.randn(heads, slots, width // heads, generator=g) * 0.5).to(device)
+           for _ in layers]
+    wq = (torch.randn(width, width, generator=g) * width ** -0.5).to(device)
+
+    def attention(layer, tokens):
+        b, t, _ = tokens.shape
+        key = (tokens @ wq).reshape(b, t, 4, width // 4).transpose(1, 2).contiguous()
+        return tokens + torch.tanh(tokens @ wq), key, key * 0.5
+
+    def tail(layer, tokens):
+        return tokens * 0.9
+
+    quantum = batch * heads * 4 * 2
+    kw = dict(attention_block=attention, sdm_tail=tail, capacity=time + 6,
+              sdm_growth_quantum_rows=quantum)
+    x = torch.randn(batch, time, width, generator=g).to(device)
+    out, state = cow.prefill_faithful_sdm_stack("BAB", list(zip(ctrls, m0s)), x, **kw)
+    pre0 = cow.prefill_sdm_layer(ctrls[0], m0s[0], x)
+    t = tail(0, x + pre0.output)
+    t, key, value = attention(1, t)
+    pre1 = cow.prefill_sdm_layer(ctrls[1], m0s[1], t)
+    t = tail(2, t + pre1.output)
+    assert torch.equal(out, t)
+    assert state.sdm_layer_positions == (0, 2)
+    assert (state.position, state.capacity, state.batch) == (time, time + 6, batch)
+    for st, pre in zip(state.sdm_states, (pre0, pre1)):
+        assert torch.equal(st.materialize_dense(),
+                           pre.final_memory.reshape(batch * heads, slots, width // heads))
+        st.validate_invariants()
+    assert state.dense_keys[0].shape == (batch, 4, time + 6, width // 4)
+    assert torch.equal(state.dense_keys[0][:, :, :time], key)
+    assert torch.equal(state.dense_values[0][:, :, :time], value)
+
+    x2 = torch.randn(2, time, width, generator=g).to(device)
+    _, incoming = cow.prefill_faithful_sdm_stack("BAB", list(zip(ctrls, m0s)), x2, **kw)
+    expect = [torch.cat((a.materialize_dense(), b.materialize_dense()))
+              for a, b in zip(state.sdm_states, incoming.sdm_states)]
+    keys = torch.cat((state.dense_keys[0], incoming.dense_keys[0]))
+    assert state.admit(incoming) == 2
+    assert state.batch == batch + 2
+    for st, want in zip(state.sdm_states, expect):
+        assert torch.equal(st.materialize_dense(), want)
+        st.validate_invariants()
+    assert torch.equal(state.dense_keys[0], keys)
+
+    with pytest.raises(ValueError, match="shorter than the prefix"):
+        cow.prefill_faithful_sdm_stack("BAB", list(zip(ctrls, m0s)), x, **{**kw, "capacity": 3})
+    with pytest.raises(ValueError, match="one value per B layer"):
+        cow.prefill_faithful_sdm_stack("BAB", list(zip(ctrls, m0s)), x,
+                                       **{**kw, "sdm_capacity_rows": [4096]})
+    with pytest.raises(ValueError, match="attention_block"):
+        cow.prefill_faithful_sdm_stack("BAB", list(zip(ctrls, m0s)), x,
+                                       **{**kw, "attention_block": None})
