@@ -172,8 +172,10 @@ __global__ __launch_bounds__(kRecThreads) void recurrence_kernel(RecParams P) {
   };
   if (T > 0) fetch_gates(0, 0);
   if (T > kWave) fetch_gates(1, 1);
+  if (T > 0) {
 #pragma unroll
-  for (int j = 0; j < PF; ++j) fetch(j, j < T ? j : T - 1);
+    for (int j = 0; j < PF; ++j) fetch(j, j < T ? j : T - 1);
+  }
   for (int64_t t0 = 0; t0 < T; t0 += PF) {
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
