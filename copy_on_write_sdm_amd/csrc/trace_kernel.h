@@ -796,11 +796,23 @@ void sdm_trace_kernel(StepParams P) {
   int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
   bool any_bad = false;  // a map entry outside the slab (checked per chunk only then)
   if constexpr (MAPLDS) {
+    // the bank's slot map into LDS, 4 loads in flight per lane (one memory
+    // round trip for N <= 256)
+    constexpr int kStage = 4;
     uint64_t bad = 0;
-    for (int b = 0; b < N; b += kWave) {
-      const int v = b + lane < N ? map_bank[b + lane] : -1;
-      if (b + lane < N) lds_map[b + lane] = v;
-      bad |= __ballot(v >= C);
+    for (int b = 0; b < N; b += kStage * kWave) {
+      int v[kStage];
+#pragma unroll
+      for (int i = 0; i < kStage; ++i) {
+        const int x = b + i * kWave + lane;
+        v[i] = x < N ? map_bank[x] : -1;
+      }
+#pragma unroll
+      for (int i = 0; i < kStage; ++i) {
+        const int x = b + i * kWave + lane;
+        if (x < N) lds_map[x] = v[i];
+        bad |= __ballot(v[i] >= C);
+      }
     }
     any_bad = bad != 0;
   }
