@@ -1304,6 +1304,7 @@ class DecodeTrace:
             self.trace.control_stride = layers
         self._layers = None
         self._layers_versions = None     # the states' versions the layer structs match
+        self._capacities = None          # the slab lengths the layer structs were built from
         self._positions = [0] * layers   # host copy of step_index, None when unknown
 
     # ------------------------------------------------------------ set-up
@@ -1329,6 +1330,7 @@ class DecodeTrace:
                     for t in self.tables)
         capacities = tuple(0 if self.dense else t.capacity_rows for t in self.tables)
         self._layers_versions = self._versions()
+        self._capacities = list(capacities)
         if self._layers is not None and self._layers[0] == key:
             layers = self._layers[1]
             if self._layers[2] != capacities:
@@ -1424,21 +1426,26 @@ class DecodeTrace:
 
         before = self._versions()
         moved = False
+        proven_k, capacity_k = nat.CTRL_PROVEN, nat.CTRL_CAPACITY
+        events_k, added_k, copied_k = nat.CTRL_EVENTS, nat.CTRL_ADDED, nat.CTRL_COPIED
+        # the slab lengths the layer structs were built from, while no state
+        # changed since (a tensor's shape costs more than the whole check)
+        known = self._capacities if self._layers_versions == before else None
+        seen_all = self._counters_seen
         for l, (st, words) in enumerate(zip(self.tables, per_layer)):
-            st.proven_maximum_additional_allocations = words[nat.CTRL_PROVEN]
-            capacity = words[nat.CTRL_CAPACITY]
-            if capacity != st.values.shape[0]:
+            st.proven_maximum_additional_allocations = words[proven_k]
+            capacity = words[capacity_k]
+            if capacity != (known[l] if known is not None else st.values.shape[0]):
                 vbuf, fbuf = st.slab_buffers
                 st.values, st.free_rows = vbuf[:capacity], fbuf[:capacity]
                 moved = True
-            counters = (words[nat.CTRL_EVENTS], words[nat.CTRL_ADDED], words[nat.CTRL_COPIED])
-            seen = self._counters_seen[l]
-            if counters != seen:
-                st.growth_events += counters[0] - seen[0]
-                st.growth_rows_added += counters[1] - seen[1]
-                st.growth_rows_copied += counters[2] - seen[2]
-                self._counters_seen[l] = counters
-            if st.growth_quantum_rows > 0 and not st.capacity_is_proven:
+            seen = seen_all[l]
+            if words[events_k] != seen[0] or words[added_k] != seen[1] or words[copied_k] != seen[2]:
+                st.growth_events += words[events_k] - seen[0]
+                st.growth_rows_added += words[added_k] - seen[1]
+                st.growth_rows_copied += words[copied_k] - seen[2]
+                seen_all[l] = (words[events_k], words[added_k], words[copied_k])
+            if not st.capacity_is_proven and st.growth_quantum_rows > 0:
                 st.capacity_is_proven = True
         # what matched the states before still matches them, except the
         # layer structs after a capacity grew
