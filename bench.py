@@ -296,7 +296,7 @@ def main() -> int:
     # ---- prefill (dense kernel) and copy-on-write handoff, untimed except the
     # handoff itself
     m0 = synthetic.make_initial_memory(LAYERS, HEADS, SLOTS, WIDTH, seed=args.seed, device=dev)
-    handoff_ms = None
+    handoff_ms = handoff_first_ms = None
     prefill_info = None
     if PREFIX:
         prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=banks, slots=SLOTS,
@@ -346,16 +346,26 @@ def main() -> int:
             "what": "prefill of all layers: the sparse decode kernel (one launch over the "
                     "prefix) against dense_sparse_routes + the dense-route recurrence per layer "
                     "(different summation orders: a float tolerance, not bit equality)"})
-        t0 = time.perf_counter()
-        states = []
-        for l in range(LAYERS):
-            active = torch.zeros(banks, SLOTS, dtype=torch.bool, device=dev)
-            cow.mark_written(active, prefix.write_indices[:, l].permute(1, 0, 2).reshape(banks, -1))
-            states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
-                m0[l], tables[l], active, template_indices=templates,
-                growth_quantum_rows=quantum))
-        torch.cuda.synchronize()
-        handoff_ms = 1000.0 * (time.perf_counter() - t0)
+        # the handoff twice: the first in the process also loads its kernels
+        # and grows the allocator's pools (handoff_first_ms); the second is
+        # the steady state of a serving process (handoff_ms), and its states
+        # decode
+        handoff_first_ms = None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            states = []
+            for l in range(LAYERS):
+                active = torch.zeros(banks, SLOTS, dtype=torch.bool, device=dev)
+                cow.mark_written(active,
+                                 prefix.write_indices[:, l].permute(1, 0, 2).reshape(banks, -1))
+                states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
+                    m0[l], tables[l], active, template_indices=templates,
+                    growth_quantum_rows=quantum))
+            torch.cuda.synchronize()
+            handoff_ms = 1000.0 * (time.perf_counter() - t0)
+            if handoff_first_ms is None:
+                handoff_first_ms = handoff_ms
+                del states
         del prefill, prefix, tables
     else:
         states = [cow.PackedSDMCopyOnWriteState.allocate(
@@ -459,6 +469,7 @@ def main() -> int:
         raise AssertionError("packed decode did not consume the trace")
     allocator = {
         "handoff_ms": None if handoff_ms is None else round(handoff_ms, 3),
+        "handoff_first_ms": None if handoff_first_ms is None else round(handoff_first_ms, 3),
         # the handoff reads every live row from the dense table and writes it
         # into the slab (2 x 4 B x D per row)
         "handoff_gbps": (None if not handoff_ms else
