@@ -639,6 +639,13 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": None if traffic is None else traffic["bytes_per_launch"],
             "traffic_source": None if traffic is None else traffic["source"],
+            # the measured HBM bytes over the same kernel time: how busy HBM
+            # actually is (rows a bank rereads and M0 hit in L2 and MALL)
+            "traffic_gbps": (None if traffic is None else
+                             round(traffic["bytes_per_launch"] / (kernel_us * 1e-6) / 1e9, 1)),
+            "traffic_frac": (None if traffic is None else
+                             round(traffic["bytes_per_launch"] / (kernel_us * 1e-6) / 1e9
+                                   / PEAK_HBM_GBPS, 4)),
             "kernel": f"{kernel} (packed, {LAYERS} layers x {banks} banks)",
             "kernel_us": round(kernel_us, 3),
             "steps_per_launch": round(steps_per_launch, 3),
