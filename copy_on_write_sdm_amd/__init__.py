@@ -31,6 +31,7 @@ from .prefill import (
     prefill_faithful_sdm_stack,
     prefill_sdm_layer,
 )
+from .stack_decode import decode_faithful_sdm_stack, write_dense_cache
 from .controller import (
     ControllerStep,
     SDMController,
@@ -50,6 +51,7 @@ __all__ = [
     "SDMCopyOnWriteStep",
     "SDMStepInputs",
     "allocate_dense_cache",
+    "decode_faithful_sdm_stack",
     "decode_sdm_layer",
     "decode_sdm_layer_controller",
     "decode_sdm_layer_controller_dense",
@@ -68,4 +70,5 @@ __all__ = [
     "prepare_sdm_step",
     "product_key_routes",
     "sdm_recurrence",
+    "write_dense_cache",
 ]

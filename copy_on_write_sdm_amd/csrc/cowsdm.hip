@@ -940,14 +940,24 @@ struct StaticLayout {
   }
 };
 StaticLayout g_static_layout[kStaticDevices];
+bool g_static_captured[kStaticDevices] = {};   // per device: a call was recorded into a graph
 }  // namespace
 
 // The array's address on the current device, looked up once per device.
 // When the call's layout differs from the last call's on this device, the
 // words it will use are zeroed first (a fill kernel on `stream`): words left
 // by another layout could otherwise pass for this one's epoch words.
+//
+// Zeroed words are a valid start for every layout (epoch 0, no word tagged
+// with the next epoch), so a launch whose words were all zeroed first is
+// always right.  A call recorded into a hipGraph (`capturing`) runs whenever
+// the graph is replayed, out of sight of this host-side record, so it always
+// clears its words before its launch; and once a graph has been recorded on
+// a device, the record no longer tells what the array holds (a replay may
+// have written another layout's words over part of it), so from then on
+// every call there clears its words first.
 int32_t static_scan(int64_t** out, const StaticLayout& layout, int64_t words,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool capturing) {
   int device = 0;
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return fail(static_cast<int32_t>(e), "static scan: %s", hipGetErrorString(e));
@@ -966,12 +976,25 @@ int32_t static_scan(int64_t** out, const StaticLayout& layout, int64_t words,
     g_static_scan[device] = static_cast<int64_t*>(ptr);
   }
   *out = g_static_scan[device];
-  if (!(g_static_layout[device] == layout)) {
+  if (capturing) g_static_captured[device] = true;
+  if (g_static_captured[device] || !(g_static_layout[device] == layout)) {
     hipLaunchKernelGGL(zero_i64_kernel, dim3(grid_for(words, 256)), dim3(256), 0, stream,
                        *out, words);
     if (int32_t e = launch_status("static scan clear")) return e;
     g_static_layout[device] = layout;
   }
+  return 0;
+}
+
+// True when `stream` is recording a hipGraph (see static_scan).
+int32_t stream_capturing(hipStream_t stream, bool* capturing) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(stream, &status);
+  if (e != hipSuccess) {
+    return fail(static_cast<int32_t>(e), "static scan: hipStreamIsCapturing: %s",
+                hipGetErrorString(e));
+  }
+  *capturing = status == hipStreamCaptureStatusActive;
   return 0;
 }
 
@@ -1155,7 +1178,12 @@ int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nl
     layout.writes = shape->writes;
     layout.steps = t.scan_steps;
     layout.layers = nlayers;
-    if (int32_t e = static_scan(&t.scan, layout, per_layer * nlayers, as_stream(stream))) return e;
+    bool capturing = false;
+    if (int32_t e = stream_capturing(as_stream(stream), &capturing)) return e;
+    if (int32_t e = static_scan(&t.scan, layout, per_layer * nlayers, as_stream(stream),
+                                capturing)) {
+      return e;
+    }
     t.scan_words = per_layer;
   }
   return run_step(layers, nlayers, shape, false, as_stream(stream), &t, steps);

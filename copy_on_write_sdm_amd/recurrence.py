@@ -49,7 +49,11 @@ def dense_sparse_routes(weights: torch.Tensor, indices: torch.Tensor,
         raise ValueError("route weights and indices must be on one device")
     device = weights.device
     per_row = weights.shape[-1] if weights.ndim else 1
-    rows = weights.numel() // per_row if per_row else 0
+    if per_row == 0:
+        # no routes in a row: every slot of its dense vector stays zero, as
+        # the reference's scatter into zeros leaves it
+        return torch.zeros(*weights.shape[:-1], slots, device=device, dtype=torch.float32)
+    rows = weights.numel() // per_row
     out = torch.empty(*weights.shape[:-1], slots, device=device, dtype=torch.float32)
     if out.numel() == 0:
         return out

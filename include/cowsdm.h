@@ -287,7 +287,11 @@ int32_t cowsdm_packed_step_trace(const cowsdm_layer_t* layers, int32_t nlayers,
  * beyond).  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other host threads) race.  A call whose
  * layout (banks, W, scan_steps, nlayers) differs from the last call's on the
- * GPU first zeroes the words it uses, with a kernel on `stream`. */
+ * GPU first zeroes the words it uses, with a kernel on `stream`.  A call
+ * recorded into a hipGraph records that zeroing too (a fill kernel, no
+ * memset node), and once one has been recorded on a GPU every later call
+ * there zeroes its words first: a replay may have left another layout's
+ * words in the array. */
 #define COWSDM_STATIC_SCAN_WORDS (1ll << 21)
 int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nlayers,
                                         const cowsdm_shape_t* shape,

@@ -169,6 +169,14 @@ def test_dense_sparse_routes_match_numpy(device, index_dtype):
     with pytest.raises(ValueError, match="must align"):
         cow.dense_sparse_routes(torch.from_numpy(w).to(device),
                                 torch.from_numpy(idx[..., :3]).to(device, index_dtype), slots)
+    # rows with no routes scatter nothing: all-zero dense vectors, even
+    # where the output memory held other values before
+    filler = torch.full((5, 8, slots), 7.0, device=device)
+    del filler
+    empty = cow.dense_sparse_routes(torch.zeros(5, 8, 0, device=device),
+                                    torch.zeros(5, 8, 0, device=device, dtype=index_dtype), slots)
+    assert empty.shape == (5, 8, slots)
+    assert not empty.any()
 
 
 def test_argument_errors(device):

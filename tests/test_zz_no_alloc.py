@@ -94,3 +94,43 @@ def test_static_trace_refuses_past_its_array(device):
         b"plan words" in lib.cowsdm_last_error_string()
     torch.cuda.synchronize()
     assert tr.step_index.tolist() == [0] * 8
+
+
+def test_captured_static_launches_of_two_layouts(device):
+    """Graphs of multi-step static launches of two layouts (64 banks over
+    256 slots, 16 banks over 64 slots), replayed in turn and between eager
+    static runs of a third layout, equal the allocated-plan path bit for
+    bit: a replay must never take plan words another layout left in the
+    shared array for its own."""
+
+    cases = {"a": dict(layers=3, banks=64, slots=256, steps=24, seed=11, quantum=1024),
+             "b": dict(layers=2, banks=16, slots=64, steps=24, seed=13, quantum=64),
+             "c": dict(layers=2, banks=32, slots=128, steps=18, seed=17, quantum=256)}
+    static, allocated = {}, {}
+    for name, case in cases.items():
+        make = _case(device, **case)
+        static[name], allocated[name] = make(True), make(False)
+        static[name].set_step(0)
+    print("static capture: graphs of layouts a and b", flush=True)
+    graphs = {name: static[name].capture(4) for name in ("a", "b")}
+    for round_ in range(6):
+        graphs["a"].replay()
+        static["c"].run(2)          # eager static calls of a third layout
+        graphs["b"].replay()
+        if round_ % 2:
+            torch.cuda.synchronize()
+            static["c"].run(2)
+    torch.cuda.synchronize()
+    for name, tr in static.items():
+        steps = cases[name]["steps"]
+        tr.sync()
+        assert tr.step_index.tolist() == [steps] * len(tr.tables), name
+        assert tr.status.tolist() == [0] * len(tr.tables), name
+        want = allocated[name]
+        want.set_step(0)
+        want.run(steps)
+        torch.cuda.synchronize()
+        assert torch.equal(tr.outputs, want.outputs), name
+        for a, b in zip(tr.tables, want.tables):
+            assert_states_identical(a, b)
+            a.validate_invariants()
