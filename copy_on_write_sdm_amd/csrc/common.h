@@ -18,7 +18,6 @@ constexpr int kMaxLayers = 8;               // layers per step launch
 constexpr int kReadBatch = 16;              // read rows in flight per batch
 constexpr int kMaxReadSlots = 4;            // R <= 256 = 4 * 64
 constexpr int kSpinLimit = 1 << 16;         // bounded look-back wait
-constexpr int kFreeWindow = 256;            // prefetched free-stack entries
 constexpr int kTile = 2048;                 // ranking tile (entries)
 constexpr int kTileThreads = 256;
 constexpr int kPerThread = kTile / kTileThreads;
@@ -103,6 +102,20 @@ __device__ __forceinline__ int rl(int x, int lane) {
 
 __device__ __forceinline__ float rlf(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Wave-inclusive sum over lanes (lane order), in DPP moves: shifts by 1, 2,
+// 4 and 8 lanes within each row of 16, then row 0's and row 1's last lanes
+// broadcast into the rows after them (a lane shifted in from outside its
+// row, or a row the mask leaves out, adds the identity 0).
+__device__ __forceinline__ int wave_inclusive(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2 and 3
+  return v;
 }
 
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {

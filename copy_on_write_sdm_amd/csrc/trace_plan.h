@@ -49,20 +49,6 @@
 
 namespace cowsdm_impl {
 
-// Wave-inclusive sum over lanes (lane order), in DPP moves: shifts by 1, 2,
-// 4 and 8 lanes within each row of 16, then row 0's and row 1's last lanes
-// broadcast into the rows after them (a lane shifted in from outside its
-// row, or a row the mask leaves out, adds the identity 0).
-__device__ __forceinline__ int wave_inclusive(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1 and 3
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2 and 3
-  return v;
-}
-
 // Loads *p (lanes with `want`) until every wanted word carries `epoch` (and,
 // with `prefix`, is a prefix word); false when some never does (bounded).
 __device__ __forceinline__ bool poll_tagged(const int64_t* p, bool want, uint32_t epoch,

@@ -58,9 +58,12 @@ extern "C" {
 
 /* Word offsets inside the per-layer step scratch (int64 words). */
 /* EPOCH retires the previous launch's scan slots (the layer's last wave
- * advances it); ERRORS is the sticky COWSDM_ERR_* word; SLOTS[b] is bank b's
- * scan slot.  Words 1, 2 and 4-7 are reserved. */
+ * advances it); TICKET counts the waves of one-step launches that built
+ * the layer's first-touch table themselves (every such launch adds the
+ * bank count; a zeroed word starts it); ERRORS is the sticky COWSDM_ERR_*
+ * word; SLOTS[b] is bank b's scan slot.  Words 2 and 4-7 are reserved. */
 #define COWSDM_SCRATCH_EPOCH 0
+#define COWSDM_SCRATCH_TICKET 1
 #define COWSDM_SCRATCH_ERRORS 3
 #define COWSDM_SCRATCH_SLOTS 8
 
