@@ -486,6 +486,32 @@ def main() -> int:
         "timed_host_growth_rounds": sum(r["growth_rounds"] for r in p_reps),
         "slab_buffer_rows": sum(packed._room(st) for st in states),
     }
+    # the reference's serving-memory result (experiments/benchmark_serving.py:
+    # 889-966, README.md:94-96) for the decoded state: live and allocated
+    # rows over the logical rows, packed private bytes (live, and reserved
+    # with this build's slab headroom) over the dense tables' bytes
+    serving = cow.FaithfulSDMDecodeState(
+        layout="B" * LAYERS, position=PREFIX + total_steps, capacity=PREFIX + total_steps,
+        activation_dtype=torch.float32,
+        active_sequences=torch.ones(B, dtype=torch.bool, device=dev),
+        sdm_layer_positions=tuple(range(LAYERS)), sdm_states=tuple(states))
+    packed_storage = serving.storage_bytes()
+    dense_bytes = sum(4 * t.numel() for t in dense_tables)
+    logical_rows = sum(st.banks * st.slots for st in states)
+    memory = {
+        "logical_rows": logical_rows,
+        "live_row_fraction": round(allocator["live_rows_after"] / logical_rows, 4),
+        "physical_capacity_fraction": round(allocator["capacity_rows_after"] / logical_rows, 4),
+        "packed_over_dense_live_bytes": round(
+            packed_storage["per_user_live_total_excluding_shared"] / dense_bytes, 4),
+        "packed_over_dense_reserved_bytes": round(
+            packed_storage["total_reserved_excluding_shared"] / dense_bytes, 4),
+        "slab_headroom_bytes": sum(st.storage_bytes()["slab_headroom"] for st in states),
+        "dense_sdm_bytes": dense_bytes,
+        "what": ("the reference's memory figures (benchmark_serving.py:889-966) after the "
+                 "timed decode: packed storage_bytes() (reserved includes the slab buffers' "
+                 "growth headroom that reserve_steps gave every layer) over the dense tables"),
+    }
 
     # ---- per-layer Python drop-in path (exact reference call pattern), on
     # the decoded packed states once every check on them is done
@@ -517,13 +543,16 @@ def main() -> int:
         gtrace.reserve_steps(n)
         gtrace.set_step(0)
         graph = gtrace.capture(1)
-        for _ in range(2):
+        # untimed replays first: the first replays of a graph run slower
+        # (tens of microseconds) than the steady state
+        warm = min(16, n // 4)
+        for _ in range(warm):
             graph.replay()
         torch.cuda.synchronize()
         g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         g0.record()
-        for _ in range(n - 2):
+        for _ in range(n - warm):
             graph.replay()
         g1.record()
         torch.cuda.synchronize()
@@ -532,10 +561,11 @@ def main() -> int:
         if gtrace.step_index.tolist() != [n] * LAYERS or any(gtrace.status.tolist()):
             raise AssertionError("captured single-step decode did not run every step")
         graph_step = {
-            "tokens_per_s": round(B * (n - 2) / wall, 1),
-            "us_per_step": round(1e6 * wall / (n - 2), 3),
-            "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / (n - 2), 3),
-            "steps": n - 2,
+            "tokens_per_s": round(B * (n - warm) / wall, 1),
+            "us_per_step": round(1e6 * wall / (n - warm), 3),
+            "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / (n - warm), 3),
+            "steps": n - warm,
+            "warmup_replays": warm,
             "what": "hipGraph of one planned launch (all layers, one step) replayed per token",
         }
         del graph
@@ -572,6 +602,44 @@ def main() -> int:
             "what": "per token and layer: controller prepare, two route selections, "
                     "prepare_step_capacity, packed step, controller finish (eager)",
         }
+
+    # ---- the same per-token decode with the controller on the device,
+    # captured once and replayed per token (ControllerDecodeGraph: per layer
+    # prepare, two route selections, the proof and growth on the device, the
+    # packed step, the finish, the residual add)
+    controller_graph = None
+    if eager_steps:
+        n = max(eager_steps, 2 * K)
+        dec = cow.ControllerDecodeGraph(ctls, states, B)
+        dec.reserve_tokens(n + 2)
+        dec.capture()
+        toks = torch.randn(n + 2, B, 1, width_model, device=dev,
+                           generator=torch.Generator(device=dev).manual_seed(args.seed + 7))
+        for s in range(2):
+            dec(toks[s])
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        g0.record()
+        for s in range(2, n + 2):
+            dec(toks[s])
+        g1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        dec.check()
+        dec.sync()
+        for st in states:
+            st.validate_invariants()
+        controller_graph = {
+            "tokens_per_s": round(B * n / wall, 1),
+            "us_per_step": round(1e6 * wall / n, 3),
+            "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / n, 3),
+            "steps": n,
+            "what": "hipGraph per token of every layer's controller prepare, two route "
+                    "selections, capacity proof and growth on the device, packed step, "
+                    "controller finish and residual add (ControllerDecodeGraph)",
+        }
+        del dec
 
     # roofline of the dominant kernel, the persistent decode kernel: the
     # algorithmic bytes of the steps the timed launches ran over its mean
@@ -629,6 +697,12 @@ def main() -> int:
             "capacity_proof": ("the reference's prepare_step_capacity(B*W) before every "
                                "step, planned on the device per launch"),
             "launch": "persistent launches over all layers and banks",
+            "mode": ("teacher-forced: the routes of every step are resident before the "
+                     "launches (synthetic routes, as the reference's benchmark pre-generates "
+                     "them), so one launch runs up to max_steps_per_launch steps; a decode "
+                     "whose routes depend on the previous token runs one step per launch: "
+                     "graph_step (synthetic routes) and controller_graph (routes from the "
+                     "device controller) give that per-token rate"),
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -663,9 +737,11 @@ def main() -> int:
             "state_max_abs_diff": state_diff,
         },
         "allocator": allocator,
+        "memory": memory,
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
         "graph_step": graph_step,
         "controller_decode": controller_leg,
+        "controller_graph": controller_graph,
     }
     if not args.no_cpu_baseline and args.config == 2:
         result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)

@@ -33,6 +33,7 @@ from .prefill import (
 )
 from .stack_decode import decode_faithful_sdm_stack, write_dense_cache
 from .controller import (
+    ControllerDecodeGraph,
     ControllerStep,
     SDMController,
     decode_sdm_layer_controller,
@@ -42,6 +43,7 @@ from .controller import (
 )
 
 __all__ = [
+    "ControllerDecodeGraph",
     "ControllerStep",
     "DecodeTrace",
     "SDMController",

@@ -1209,8 +1209,12 @@ class DecodeTrace:
     after the last (and give the slabs room with ``reserve_steps``).
     ``outputs`` is [S, L, B, D] (one reading per step) or [L, B, D] (every
     step overwrites the same buffer).  ``memories`` given instead of
-    ``states`` runs the dense-table control.  No counterpart in the
-    reference.
+    ``states`` runs the dense-table control.  With ``repeat`` the inputs are
+    [1, L, B, ...] buffers that the caller (or kernels captured before the
+    launch) refills before every step: every launch reads them, the device
+    counters count steps without bound, and only ``launch``/``capture`` of
+    device-counted steps run (the decode of routes made token by token).  No
+    counterpart in the reference.
     """
 
     _INPUTS = ("write_indices", "write_weights", "values", "input_gate", "erase_gate",
@@ -1219,7 +1223,7 @@ class DecodeTrace:
     def __init__(self, *, states=None, memories=None, write_indices, write_weights, values,
                  input_gate, forget_log_gate, read_indices, read_weights, erase_gate=None,
                  outputs=None, persistent: bool = True, max_steps_per_launch: int = 512,
-                 static_scan: bool = False):
+                 static_scan: bool = False, repeat: bool = False):
         if (states is None) == (memories is None):
             raise ValueError("give exactly one of states or memories")
         self.dense = memories is not None
@@ -1287,6 +1291,13 @@ class DecodeTrace:
         self.max_steps_per_launch = max(1, min(512, int(max_steps_per_launch)))
         self.trace.persistent = int(persistent)
         self.trace.steps_recorded = steps
+        self.repeat = bool(repeat)
+        if self.repeat:
+            if steps != 1:
+                raise ValueError("a repeating decode trace takes [1, L, B, ...] input buffers")
+            for k in range(9):
+                self.trace.stride_bytes[k] = 0
+            self.trace.steps_recorded = 1 << 62
         self.scan = None
         self.planned = False
         # static_scan: packed launches take their plan blocks from the
@@ -1521,6 +1532,8 @@ class DecodeTrace:
         device counter on the current stream."""
 
         if start is not None:
+            if self.repeat:
+                raise ValueError("a repeating decode trace runs device-counted launches only")
             if start < 0 or start + steps > self.steps:
                 raise ValueError("trace launch runs past the recorded steps")
             if not self.dense:
@@ -1590,6 +1603,8 @@ class DecodeTrace:
         on the stream and is appended to it.  Returns the number of launches
         and of host growth rounds."""
 
+        if self.repeat:
+            raise ValueError("a repeating decode trace runs device-counted launches only")
         if steps <= 0:
             return {"launches": 0, "growth_rounds": 0}
         positions = self._positions if self._positions is not None else self.step_index.tolist()

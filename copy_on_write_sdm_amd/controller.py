@@ -317,3 +317,156 @@ _prepare_faithful_sdm_step = prepare_sdm_step
 _finish_faithful_sdm_step = finish_sdm_step
 _decode_faithful_sdm_layer = decode_sdm_layer_controller
 _decode_faithful_sdm_layer_dense = decode_sdm_layer_controller_dense
+
+
+class ControllerDecodeGraph:
+    """The per-token decode of a stack of SDM layers with the controller on
+    the device, captured once as a hipGraph and replayed per token.  A replay
+    runs, layer after layer, what ``decode_sdm_layer_controller`` runs
+    (``_decode_faithful_sdm_layer``, inference.py:538-566): the controller's
+    prepare kernel (input norm, projections, gates), the read and write
+    product-key route selections (sdm.py:96-159), the decode loop's capacity
+    proof (prepare_step_capacity(B * H * W), allocator.py:745-773) with the
+    slab's growth decided on the device, the packed step and the
+    controller's finish; each layer's output joins the residual stream
+    (``tokens + mixed``, then ``tail(layer, tokens)`` when given, as the
+    stack decode's SDM tail).  No host work and no synchronisation per
+    token.
+
+    ``reserve_tokens(n)`` gives every slab buffer room to grow for n more
+    tokens; a layer whose growth would pass its buffers refuses its step on
+    the device, and ``check()`` raises then.  ``sync()`` reads the proof
+    counters, capacities and growth counters back into the states before
+    they are used eagerly again.  The output tensor ``__call__`` returns is
+    rewritten by the next replay.  No counterpart in the reference.
+    """
+
+    def __init__(self, controllers: list[SDMController],
+                 states: list[PackedSDMCopyOnWriteState], batch: int, *, tail=None):
+        from .allocator import DecodeTrace
+
+        if not controllers or len(controllers) != len(states):
+            raise ValueError("one packed state per controller")
+        c0 = controllers[0]
+        if any(c.width != c0.width or c.device != c0.device for c in controllers):
+            raise ValueError("the controllers of one stack share its width and device")
+        self.controllers = list(controllers)
+        self.states = list(states)
+        self.batch = batch
+        self.tail = tail
+        self.device = c0.device
+        self.tokens = torch.zeros(batch, 1, c0.width, device=self.device)
+        self.output = None
+        self.graph = None
+        self.layers = []
+        for c, st in zip(controllers, states):
+            banks = batch * c.memory_heads
+            if st.banks != banks or st.width != c.head_width or st.slots != c.slots:
+                raise ValueError("packed SDM state does not match batch and controller")
+            root = math.isqrt(c.slots)
+            reads = min(c.reads, min(c.reads, root) ** 2)
+            writes = min(c.writes, min(c.writes, root) ** 2)
+            f32 = dict(device=self.device, dtype=torch.float32)
+            i64 = dict(device=self.device, dtype=torch.int64)
+            buf = {
+                "normalized": torch.empty(batch, 1, c.width, **f32),
+                "read_keys": torch.empty(banks, 1, c.key_width_per_head, **f32),
+                "write_keys": torch.empty(banks, 1, c.key_width_per_head, **f32),
+                "values": torch.empty(banks, c.head_width, **f32),
+                "input_gate": torch.empty(banks, **f32),
+                "forget": torch.empty(banks, **f32),
+                "read_weights": torch.empty(banks, 1, reads, **f32),
+                "read_indices": torch.empty(banks, 1, reads, **i64),
+                "write_weights": torch.empty(banks, 1, writes, **f32),
+                "write_indices": torch.empty(banks, 1, writes, **i64),
+                "reading": torch.empty(1, banks, c.head_width, **f32),
+                "out": torch.empty(batch, 1, c.width, **f32),
+            }
+            trace = DecodeTrace(
+                states=[st], repeat=True, max_steps_per_launch=1, outputs=buf["reading"],
+                write_indices=buf["write_indices"].view(1, 1, banks, writes),
+                write_weights=buf["write_weights"].view(1, 1, banks, writes),
+                values=buf["values"].view(1, 1, banks, c.head_width),
+                input_gate=buf["input_gate"].view(1, 1, banks),
+                forget_log_gate=buf["forget"].view(1, 1, banks),
+                read_indices=buf["read_indices"].view(1, 1, banks, reads),
+                read_weights=buf["read_weights"].view(1, 1, banks, reads))
+            self.layers.append((c, buf, trace))
+
+    def reserve_tokens(self, tokens: int) -> None:
+        """Room in every slab's buffers for ``tokens`` more tokens of growth."""
+
+        for _, _, trace in self.layers:
+            trace.reserve_steps(tokens)
+
+    def _record(self, stream: int, structs) -> torch.Tensor:
+        lib = nat.lib()
+        x = self.tokens
+        for index, ((c, buf, trace), layer) in enumerate(zip(self.layers, structs)):
+            nat.check(lib.cowsdm_controller_prepare(
+                c.c_struct(), x.data_ptr(), self.batch, buf["normalized"].data_ptr(),
+                buf["read_keys"].data_ptr(), buf["write_keys"].data_ptr(),
+                buf["values"].data_ptr(), buf["input_gate"].data_ptr(), buf["forget"].data_ptr(),
+                stream), "cowsdm_controller_prepare")
+            product_key_routes(buf["read_keys"], slots=c.slots, selected=c.reads,
+                               out=(buf["read_weights"], buf["read_indices"]))
+            product_key_routes(buf["write_keys"], slots=c.slots, selected=c.writes,
+                               out=(buf["write_weights"], buf["write_indices"]))
+            trace.launch(1, layer)
+            nat.check(lib.cowsdm_controller_finish(
+                c.c_struct(), buf["normalized"].data_ptr(), buf["reading"].data_ptr(), self.batch,
+                buf["out"].data_ptr(), stream), "cowsdm_controller_finish")
+            x = x + buf["out"]
+            if self.tail is not None:
+                x = self.tail(index, x)
+        return x
+
+    def capture(self) -> "torch.cuda.CUDAGraph":
+        """Record the per-token decode of every layer (the control words are
+        uploaded from the states first)."""
+
+        structs = []
+        for _, _, trace in self.layers:
+            structs.append(trace.layer_array())
+            if not trace.planned:
+                raise RuntimeError("packed state needs the planned one-step kernel (W <= 4, "
+                                   "R <= 16, D <= 256, banks <= 256) to prove on the device")
+            trace.upload()
+            trace.status.zero_()
+            trace.set_step(0)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=torch.cuda.Stream(self.device)):
+            self.output = self._record(nat.stream_handle(self.device), structs)
+        for _, _, trace in self.layers:
+            trace._positions = None
+        self.graph = graph
+        return graph
+
+    @torch.no_grad()
+    def __call__(self, tokens: torch.Tensor) -> torch.Tensor:
+        """One token [B, 1, width] through every layer: its input copied into
+        the graph's buffer, one replay."""
+
+        if self.graph is None:
+            self.capture()
+        self.tokens.copy_(tokens)
+        self.graph.replay()
+        return self.output
+
+    def sync(self) -> None:
+        """Read the device's proof counters, capacities and growth back into
+        the states."""
+
+        for _, _, trace in self.layers:
+            trace.sync()
+
+    def check(self) -> None:
+        """Raise when a replay refused a layer's step (its growth would pass
+        the slab's buffers) or stopped on a fault."""
+
+        for index, (_, _, trace) in enumerate(self.layers):
+            status = int(trace.status[0])
+            if status:
+                raise RuntimeError(f"captured decode layer {index} stopped with status "
+                                   f"{status:#x} (reserve_tokens before capturing)")

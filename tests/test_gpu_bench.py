@@ -46,3 +46,8 @@ def test_driver_command_bench_line():
     assert r["traffic"] is None or r["traffic"] > 0
     assert len(d["repeat_kernel_us"]) == 5 and all(x > 0 for x in d["repeat_kernel_us"])
     assert d["dense_control"]["state_max_abs_diff"] == 0.0
+    # the reference's memory figures for the decoded state
+    m = d["memory"]
+    assert 0 < m["live_row_fraction"] <= m["physical_capacity_fraction"]
+    assert 0 < m["packed_over_dense_live_bytes"] <= m["packed_over_dense_reserved_bytes"]
+    assert m["logical_rows"] == 7 * 64 * 256
