@@ -14,8 +14,9 @@ decode (``DecodeTrace.run``) equals
 
 and keeps the allocator invariants.
 
-Config 2: L=7, N=256, D=128, 256-token prefill handed off, B = 1, 16, 64.
-Config 3: B=64, 2,048-token prefill handed off.  Config 5 (4 heads x 64
+Config 2: L=7, N=256, D=128, 256-token prefill handed off, B = 1, 16, 64
+(at B=64 its 512 decode steps as one persistent launch).
+Config 3: B=64, 2,048-token prefill handed off, its 256 decode steps.  Config 5 (4 heads x 64
 requests = 256 banks, N=65,536, Zipf(1.1) routes) decoded from an empty slab
 that grows every few steps: one layer, and all 7 layers for 1,024 steps.
 """
@@ -137,15 +138,16 @@ def test_config1_end_to_end_matches_oracle(device):
     traced[0].validate_invariants()
 
 
-@pytest.mark.parametrize("batch_size,prefix,steps", [
-    (64, 256, 128),    # config 2
-    (16, 256, 96),     # config 2, B=16
-    (1, 256, 96),      # config 2, B=1
-    (64, 2048, 64),    # config 3
+@pytest.mark.parametrize("batch_size,prefix,steps,split", [
+    (64, 256, 512, False),   # config 2: its 512 decode steps as one launch
+    (64, 256, 128, True),    # config 2, a short run then the rest
+    (16, 256, 96, True),     # config 2, B=16
+    (1, 256, 96, True),      # config 2, B=1
+    (64, 2048, 256, True),   # config 3: all 256 decode steps
 ])
-def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, steps):
+def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, steps, split):
     layers, banks, slots = 7, batch_size, 256
-    print(f"config handoff B={banks} prefix={prefix} decode={steps}", flush=True)
+    print(f"config handoff B={banks} prefix={prefix} decode={steps} split={split}", flush=True)
     quantum = max(16, banks * W * 4)
     m0 = synthetic.make_initial_memory(layers, 1, slots, D, seed=31, device=device)
     make_states, _ = _handoff(device, m0, layers=layers, banks=banks, slots=slots,
@@ -155,10 +157,16 @@ def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, ste
     dense = [st.materialize_dense() for st in traced]
     dense_steps = [t.clone() for t in dense]
     outputs = torch.empty(steps, layers, banks, D, device=device)
-    # two runs, the first of an odd length, as a warmup then a timed run would
     tr = cow.DecodeTrace(states=traced, outputs=outputs, **kw)
-    tr.run(5)
-    tr.run(steps - 5)
+    if split:
+        # two runs, the first of an odd length, as a warmup then a timed run would
+        tr.run(5)
+        tr.run(steps - 5)
+    else:
+        # the bench's kernel configuration: slab buffers sized for the run,
+        # then one persistent launch whose plan grows the slabs on the device
+        tr.reserve_steps(steps)
+        assert tr.run(steps) == {"launches": 1, "growth_rounds": 0}
     dense_out = torch.empty_like(outputs)
     cow.DecodeTrace(memories=dense, outputs=dense_out, **kw).launch(steps, start=0)
     want = _reference_loop(host, batch, steps=steps, layers=layers)

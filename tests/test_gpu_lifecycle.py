@@ -312,15 +312,18 @@ def _decode_both(states, oracles, dense, seq, device):
 
 
 def test_continuous_batching_config4(device):
-    """Continuous batching (experiments/benchmark_serving.py:472-613 pattern):
-    4 requests decode, requests 0 and 2 are released, survivors compacted
-    and the pools trimmed, 2 new requests with 128-token prefixes admitted,
-    decode continues at mixed positions.  Packed state must equal the dense
+    """Continuous batching (experiments/benchmark_serving.py:472-613 pattern)
+    at config 4's shape (B=4, L=7, N=256, D=128): 4 requests decode 16
+    steps, requests 0 and 2 are released, survivors compacted and the pools
+    trimmed, 2 new requests with 128-token prefixes admitted, decode
+    continues 16 steps at mixed positions.  Packed state must equal the dense
     control and the oracle throughout; released rows must equal the rows
     those requests held."""
 
-    layers, batch, slots, width, writes, reads = 3, 4, 256, 128, 4, 16
+    layers, batch, slots, width, writes, reads = 7, 4, 256, 128, 4, 16
     quantum = 16
+    before, after = 16, 16      # decode steps around the lifecycle events
+    layout = "B" * layers
     m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=21)
 
     def prefill(requests, time, seed):
@@ -347,14 +350,14 @@ def test_continuous_batching_config4(device):
 
     states, oracles = prefill(batch, 16, seed=30)
     serving = cow.FaithfulSDMDecodeState(
-        layout="BBB", position=16, capacity=160, activation_dtype=torch.float32,
+        layout=layout, position=16, capacity=160, activation_dtype=torch.float32,
         active_sequences=torch.ones(batch, dtype=torch.bool, device=device),
-        sdm_layer_positions=(0, 1, 2), sdm_states=tuple(states))
+        sdm_layer_positions=tuple(range(layers)), sdm_states=tuple(states))
     dense = [st.materialize_dense() for st in states]
-    steps = synthetic.make_steps(steps=2, layers=layers, banks=batch, slots=slots, width=width,
-                                 writes=writes, reads=reads, seed=31)
+    steps = synthetic.make_steps(steps=before, layers=layers, banks=batch, slots=slots,
+                                 width=width, writes=writes, reads=reads, seed=31)
     _decode_both(states, oracles, dense,
-                 [[steps.step(s, l) for l in range(layers)] for s in range(2)], device)
+                 [[steps.step(s, l) for l in range(layers)] for s in range(before)], device)
 
     held = sum(int((st.logical_to_physical[[0, 2]] >= 0).sum()) for st in states)
     released = serving.release_and_compact([0, 2], trim=True, trim_headroom_rows=16)
@@ -370,12 +373,12 @@ def test_continuous_batching_config4(device):
 
     new_states, new_oracles = prefill(2, 128, seed=40)
     incoming = cow.FaithfulSDMDecodeState(
-        layout="BBB", position=128, capacity=160, activation_dtype=torch.float32,
+        layout=layout, position=128, capacity=160, activation_dtype=torch.float32,
         active_sequences=torch.ones(2, dtype=torch.bool, device=device),
-        sdm_layer_positions=(0, 1, 2), sdm_states=tuple(new_states))
-    serving.position = 18
+        sdm_layer_positions=tuple(range(layers)), sdm_states=tuple(new_states))
+    serving.position = 16 + before
     assert serving.admit(incoming) == 2
-    assert serving.current_positions().tolist() == [18, 18, 128, 128]
+    assert serving.current_positions().tolist() == [16 + before] * 2 + [128, 128]
     for o, n in zip(oracles, new_oracles):
         n.shared_initial_memory = o.shared_initial_memory
         ref.append_banks_from(o, n)
@@ -384,15 +387,15 @@ def test_continuous_batching_config4(device):
         st.validate_invariants()
 
     dense = [st.materialize_dense() for st in serving.sdm_states]
-    more = synthetic.make_steps(steps=2, layers=layers, banks=4, slots=slots, width=width,
+    more = synthetic.make_steps(steps=after, layers=layers, banks=4, slots=slots, width=width,
                                 writes=writes, reads=reads, seed=41)
     _decode_both(list(serving.sdm_states), oracles, dense,
-                 [[more.step(s, l) for l in range(layers)] for s in range(2)], device)
+                 [[more.step(s, l) for l in range(layers)] for s in range(after)], device)
     for st, tab, o in zip(serving.sdm_states, dense, oracles):
         assert torch.equal(st.materialize_dense(), tab)
         assert_state_equal(st, o)
     usage = serving.storage_bytes()
-    assert usage["sdm_logical_dense_fp32"] == 3 * 4 * slots * width * 4
+    assert usage["sdm_logical_dense_fp32"] == layers * 4 * slots * width * 4
     live = sum(int(st.allocated_rows_tensor()) for st in serving.sdm_states)
     assert serving.release() == live
     for st in serving.sdm_states:
