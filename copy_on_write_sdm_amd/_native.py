@@ -70,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -168,6 +168,13 @@ class Layer(ctypes.Structure):
         ("first_touches_out", ctypes.c_void_p),
         ("repeated_writes_out", ctypes.c_void_p),
         ("allocated_rows_out", ctypes.c_void_p),
+        # paged slot map (map_page_shift > 0)
+        ("map_directory", ctypes.c_void_p),
+        ("map_pages", ctypes.c_void_p),
+        ("map_page_count", ctypes.c_void_p),
+        ("map_page_capacity", ctypes.c_int64),
+        ("map_page_shift", ctypes.c_int32),
+        ("map_reserved", ctypes.c_int32),
     ]
 
 
@@ -286,6 +293,9 @@ SIGNATURES: dict[str, tuple] = {
         _I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P]),
     "cowsdm_grow": (_I32, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "cowsdm_count_active": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_paged_count": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P, _P]),
+    "cowsdm_paged_compress": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P, _P, _I64, _P, _P]),
+    "cowsdm_paged_expand": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _P, _P]),
     "cowsdm_pack_overlay": (
         _I32, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P]),
     "cowsdm_trim_repack": (

@@ -24,6 +24,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass, field
 from typing import Any, Sequence
 
@@ -100,6 +101,143 @@ def _scratch(banks: int, device: torch.device) -> torch.Tensor:
     return torch.zeros(words, dtype=torch.int64, device=device)
 
 
+def _map_placeholder(banks: int, slots: int) -> torch.Tensor:
+    """The ``logical_to_physical`` of a state whose map is paged: the direct
+    map's shape on the meta device, holding no data (its pointer is null, so
+    a kernel handed it fails its argument check, and reading it raises)."""
+
+    return torch.empty((banks, slots), device="meta", dtype=torch.int32)
+
+
+@dataclass
+class PagedSlotMap:
+    """A compressed logical-to-physical map for large address spaces: the
+    direct map's entries in pages of P slots, only the pages holding a mapped
+    slot stored.  The reference leaves this map as future work
+    (README.md:123-130; allocator.py:485-489: "a later compressed map can
+    replace it without changing SDM").
+
+    ``directory`` int32 [B, N / P]: the page of each (bank, page of slots),
+    -1 when none of its slots is mapped.  ``pages`` int32 [capacity, P]:
+    rows 0 .. ``page_count`` - 1 in use; a decode step takes new pages from
+    ``page_count`` up.  ``pages_bound`` is the host's upper bound on the
+    pages in use (the page proof, ``prove``).  No counterpart in the
+    reference."""
+
+    directory: torch.Tensor
+    pages: torch.Tensor
+    page_count: torch.Tensor
+    page_shift: int
+    pages_bound: int = 0
+
+    @property
+    def page_slots(self) -> int:
+        return 1 << self.page_shift
+
+    @property
+    def banks(self) -> int:
+        return self.directory.shape[0]
+
+    @property
+    def slots(self) -> int:
+        return self.directory.shape[1] << self.page_shift
+
+    @property
+    def capacity(self) -> int:
+        return self.pages.shape[0]
+
+    @staticmethod
+    def _shift(page_slots: int, slots: int) -> int:
+        shift = int(page_slots).bit_length() - 1
+        if page_slots < 2 or page_slots > 64 or (1 << shift) != page_slots or slots % page_slots:
+            raise ValueError("SDM map pages hold a power of two of 2 to 64 slots dividing N")
+        return shift
+
+    @classmethod
+    def empty(cls, banks: int, slots: int, page_slots: int, device,
+              capacity: int | None = None) -> "PagedSlotMap":
+        """A map with no slot mapped."""
+
+        shift = cls._shift(page_slots, slots)
+        capacity = max(64, banks) if capacity is None else max(1, int(capacity))
+        return cls(
+            directory=torch.full((banks, slots >> shift), -1, device=device, dtype=torch.int32),
+            pages=torch.empty(capacity, 1 << shift, device=device, dtype=torch.int32),
+            page_count=torch.zeros((), device=device, dtype=torch.int32),
+            page_shift=shift)
+
+    @classmethod
+    @torch.no_grad()
+    def compress(cls, mapping: torch.Tensor, page_slots: int) -> "PagedSlotMap":
+        """The paged form of a direct map [B, N]: its pages holding a mapped
+        slot, numbered in row-major (bank, page) order."""
+
+        banks, slots = mapping.shape
+        shift = cls._shift(page_slots, slots)
+        device = mapping.device
+        per_bank = slots >> shift
+        entries = banks * per_bank
+        flags = torch.empty(max(entries, 1), device=device, dtype=torch.uint8)
+        workspace = _workspace(entries, 0, device)
+        total = torch.empty(1, device=device, dtype=torch.int64)
+        stream = nat.stream_handle(device)
+        direct = mapping.contiguous()
+        nat.check(nat.lib().cowsdm_paged_count(
+            direct.data_ptr(), banks, slots, shift, flags.data_ptr(), workspace.data_ptr(),
+            total.data_ptr(), stream), "cowsdm_paged_count")
+        used = int(total.item())
+        out = cls.empty(banks, slots, 1 << shift, device, capacity=max(used, 64))
+        nat.check(nat.lib().cowsdm_paged_compress(
+            direct.data_ptr(), banks, slots, shift, flags.data_ptr(), workspace.data_ptr(),
+            out.directory.data_ptr(), out.pages.data_ptr(), out.capacity,
+            out.page_count.data_ptr(), stream), "cowsdm_paged_compress")
+        out.pages_bound = used
+        return out
+
+    @torch.no_grad()
+    def expand(self) -> torch.Tensor:
+        """The direct map [B, N]."""
+
+        mapping = torch.empty(self.banks, self.slots, device=self.directory.device,
+                              dtype=torch.int32)
+        nat.check(nat.lib().cowsdm_paged_expand(
+            self.directory.data_ptr(), self.pages.data_ptr(), self.capacity, self.banks,
+            self.slots, self.page_shift, mapping.data_ptr(),
+            nat.stream_handle(self.directory.device)), "cowsdm_paged_expand")
+        return mapping
+
+    @torch.no_grad()
+    def prove(self, maximum_new_pages: int) -> None:
+        """Room for ``maximum_new_pages`` more pages before a step (a step
+        takes at most one per write route): the page count is read only when
+        the host's bound runs short, and the pool grows (doubling) when the
+        pages in use leave too little room."""
+
+        if self.pages_bound + maximum_new_pages > self.capacity:
+            used = int(self.page_count.item())
+            self.pages_bound = used
+            if used + maximum_new_pages > self.capacity:
+                grown = max(2 * self.capacity, used + maximum_new_pages)
+                if grown >= 2**31:
+                    raise ValueError("SDM map pages cannot pass 2^31")
+                pages = torch.empty(grown, self.page_slots, device=self.pages.device,
+                                    dtype=torch.int32)
+                pages[:self.capacity].copy_(self.pages)
+                self.pages = pages
+        self.pages_bound += maximum_new_pages
+
+    def storage_bytes(self) -> int:
+        return (_tensor_bytes(self.directory) + _tensor_bytes(self.pages)
+                + _tensor_bytes(self.page_count))
+
+    def used_bytes(self) -> int:
+        """Directory plus the pages in use (reads the page count)."""
+
+        return (_tensor_bytes(self.directory)
+                + int(self.page_count.item()) * self.page_slots * 4
+                + _tensor_bytes(self.page_count))
+
+
 @dataclass(frozen=True)
 class SDMCopyOnWriteStep:
     """Diagnostics for one packed SDM decode step (allocator.py:467-473)."""
@@ -138,6 +276,9 @@ class PackedSDMCopyOnWriteState:
     scratch: torch.Tensor | None = None
     # (values buffer, free-row buffer) that values and free_rows lead, or None
     slab_buffers: Any = field(default=None, repr=False, compare=False)
+    # the paged form of the map, or None; when set, logical_to_physical is a
+    # data-less placeholder of the direct map's shape
+    paged_map: PagedSlotMap | None = field(default=None, repr=False, compare=False)
 
     def __setattr__(self, name: str, value: Any) -> None:
         # every assignment counts in ``_version``: a decode trace that saw
@@ -158,8 +299,11 @@ class PackedSDMCopyOnWriteState:
         template_indices: torch.Tensor | None = None,
         state_dtype: torch.dtype = torch.float32,
         growth_quantum_rows: int = 0,
+        map_page_slots: int | None = None,
     ) -> "PackedSDMCopyOnWriteState":
-        """Allocate an empty shared slab (allocator.py:506-585)."""
+        """Allocate an empty shared slab (allocator.py:506-585).  With
+        ``map_page_slots`` (not in the reference) the map is paged
+        (``PagedSlotMap``) with that many slots per page."""
 
         if shared_initial_memory.ndim == 2:
             shared_initial_memory = shared_initial_memory.unsqueeze(0)
@@ -218,6 +362,9 @@ class PackedSDMCopyOnWriteState:
         )
         if int(result.item()) & nat.ERR_TEMPLATE:
             raise ValueError("template index lies outside shared initial memory")
+        if map_page_slots is not None:
+            state.paged_map = PagedSlotMap.empty(banks, slots, map_page_slots, device)
+            state.logical_to_physical = _map_placeholder(banks, slots)
         return state
 
     @classmethod
@@ -233,9 +380,11 @@ class PackedSDMCopyOnWriteState:
         state_dtype: torch.dtype = torch.float32,
         maximum_future_allocations: int | None = None,
         growth_quantum_rows: int = 0,
+        map_page_slots: int | None = None,
     ) -> "PackedSDMCopyOnWriteState":
         """Pack an exact full-prefix state into a first-write overlay
-        (allocator.py:587-689)."""
+        (allocator.py:587-689).  With ``map_page_slots`` (not in the
+        reference) the packed map is paged (``PagedSlotMap``)."""
 
         if shared_initial_memory.ndim == 2:
             shared_initial_memory = shared_initial_memory.unsqueeze(0)
@@ -298,7 +447,59 @@ class PackedSDMCopyOnWriteState:
         state.capacity_is_proven = maximum_future_allocations is not None
         state.proven_maximum_additional_allocations = possible
         state.validate_invariants()
+        if map_page_slots is not None:
+            state.to_paged_map(map_page_slots)
         return state
+
+    # ------------------------------------------------------- map forms
+
+    @torch.no_grad()
+    def to_paged_map(self, page_slots: int) -> None:
+        """Keep the map paged, ``page_slots`` slots per page (a power of two
+        from 2 to 64 dividing N): only pages holding a mapped slot are
+        stored.  No counterpart in the reference."""
+
+        mapping = self.direct_map()
+        self.paged_map = PagedSlotMap.compress(mapping, page_slots)
+        self.logical_to_physical = _map_placeholder(*mapping.shape)
+
+    @torch.no_grad()
+    def to_direct_map(self) -> None:
+        """Keep the map as the direct [B, N] table again."""
+
+        if self.paged_map is not None:
+            mapping = self.paged_map.expand()
+            self.paged_map = None
+            self.logical_to_physical = mapping
+
+    def direct_map(self) -> torch.Tensor:
+        """The direct map [B, N] int32 (-1 = shared M0), built from the pages
+        when the map is paged."""
+
+        return self.logical_to_physical if self.paged_map is None else self.paged_map.expand()
+
+    @contextmanager
+    def _direct_form(self, *, keep: bool = True):
+        """A lifecycle operation on a paged state runs on the direct map:
+        expanded for it, then (``keep``: the operation changes the map)
+        packed back into pages, renumbered in row-major order."""
+
+        paged = self.paged_map
+        if paged is None:
+            yield
+            return
+        mapping = paged.expand()
+        self.paged_map = None
+        self.logical_to_physical = mapping
+        try:
+            yield
+        finally:
+            if keep:
+                mapping = self.logical_to_physical
+                self.paged_map = PagedSlotMap.compress(mapping, paged.page_slots)
+            else:
+                self.paged_map = paged
+            self.logical_to_physical = _map_placeholder(*mapping.shape)
 
     # ------------------------------------------------------------ growth
 
@@ -464,6 +665,9 @@ class PackedSDMCopyOnWriteState:
     def trim_capacity(self, *, headroom_rows: int = 0) -> int:
         """Repack live rows and return unused slab rows (allocator.py:775-839)."""
 
+        if self.paged_map is not None:
+            with self._direct_form():
+                return self.trim_capacity(headroom_rows=headroom_rows)
         if headroom_rows < 0:
             raise ValueError("SDM trim headroom cannot be negative")
         quantum = self.growth_quantum_rows
@@ -504,6 +708,9 @@ class PackedSDMCopyOnWriteState:
         Only live rows are copied, into rows popped from the top of this free
         stack in the other map's row-major order."""
 
+        if self.paged_map is not None or other.paged_map is not None:
+            with self._direct_form(), other._direct_form(keep=False):
+                return self.append_banks_from(other)
         if (
             other.slots != self.slots
             or other.width != self.width
@@ -576,6 +783,9 @@ class PackedSDMCopyOnWriteState:
         """Compact already-released banks; values never move
         (allocator.py:916-942)."""
 
+        if self.paged_map is not None:
+            with self._direct_form():
+                return self.retain_banks(bank_indices)
         bank_list = self._bank_list(bank_indices, "retained")
         flags = self._check_banks(bank_list, discarded_active=True)
         if flags & 1:
@@ -602,6 +812,9 @@ class PackedSDMCopyOnWriteState:
         """Release whole banks and push their rows on the free stack
         (allocator.py:1018-1067).  Returns the released row count (0-d)."""
 
+        if self.paged_map is not None:
+            with self._direct_form():
+                return self.release(bank_indices)
         bank_list = self._bank_list(bank_indices, "released")
         if bank_list.numel() == 0:
             return self.free_count.new_zeros(())
@@ -651,9 +864,12 @@ class PackedSDMCopyOnWriteState:
         ``slab_headroom`` (growth room beyond the capacity rows) are this
         build's extras."""
 
+        paged = self.paged_map
         private = {
             "value_slab_reserved": _tensor_bytes(self.values),
-            "logical_to_physical": _tensor_bytes(self.logical_to_physical),
+            # a paged map: its directory and page pool
+            "logical_to_physical": (_tensor_bytes(self.logical_to_physical) if paged is None
+                                    else paged.storage_bytes()),
             "free_row_stack": _tensor_bytes(self.free_rows),
             "free_count": _tensor_bytes(self.free_count),
             "overflow_flag": _tensor_bytes(self.overflow_flag),
@@ -677,7 +893,8 @@ class PackedSDMCopyOnWriteState:
         allocated = int(self.allocated_rows_tensor().item())
         live_values = allocated * self.width * self.values.element_size()
         metadata = (
-            _tensor_bytes(self.logical_to_physical)
+            (_tensor_bytes(self.logical_to_physical) if self.paged_map is None
+             else self.paged_map.used_bytes())
             + _tensor_bytes(self.free_rows)
             + _tensor_bytes(self.free_count)
             + _tensor_bytes(self.overflow_flag)
@@ -695,6 +912,9 @@ class PackedSDMCopyOnWriteState:
     def materialize_dense(self) -> torch.Tensor:
         """Effective [B,N,D] table for validation (allocator.py:1003-1016)."""
 
+        if self.paged_map is not None:
+            with self._direct_form(keep=False):
+                return self.materialize_dense()
         device = self.values.device
         dense = torch.empty(self.banks, self.slots, self.width, device=device,
                             dtype=self.values.dtype)
@@ -715,6 +935,9 @@ class PackedSDMCopyOnWriteState:
         (allocator.py:1069-1095); also surfaces the kernels' sticky error
         word."""
 
+        if self.paged_map is not None:
+            with self._direct_form(keep=False):
+                return self.validate_invariants()
         device = self.values.device
         workspace = _workspace(self.banks * self.slots, self.capacity_rows, device)
         stats = torch.empty(8, device=device, dtype=torch.int64)
@@ -865,7 +1088,15 @@ def _step_layer(
         layer.shared_initial_memory = state.shared_initial_memory.data_ptr()
         layer.template_indices = state.template_indices.data_ptr()
         layer.values = state.values.data_ptr()
-        layer.logical_to_physical = state.logical_to_physical.data_ptr()
+        paged = state.paged_map
+        if paged is None:
+            layer.logical_to_physical = state.logical_to_physical.data_ptr()
+        else:
+            layer.map_directory = paged.directory.data_ptr()
+            layer.map_pages = paged.pages.data_ptr()
+            layer.map_page_count = paged.page_count.data_ptr()
+            layer.map_page_capacity = paged.capacity
+            layer.map_page_shift = paged.page_shift
         layer.free_rows = state.free_rows.data_ptr()
         layer.free_count = state.free_count.data_ptr()
         layer.overflow_flag = state.overflow_flag.data_ptr()
@@ -965,6 +1196,8 @@ def packed_sdm_cow_step(
         first = torch.empty(banks, device=device, dtype=torch.int64)
         repeated = torch.empty(banks, device=device, dtype=torch.int64)
         allocated = torch.empty((), device=device, dtype=torch.int32)
+    if state.paged_map is not None and banks:
+        state.paged_map.prove(banks * write_indices.shape[1])
     layer = _step_layer(state, None, write_indices, write_weights, values, input_gate,
                         effective_erase, forget_log_gate, read_indices, read_weights, output,
                         first, repeated, allocated)
@@ -1087,6 +1320,8 @@ def packed_sdm_cow_step_layers(
         code = _index_code(wi[i], ri[i])
         out = outs[i] if outs[i] is not None else torch.empty_like(vv[i])
         results.append(out)
+        if state.paged_map is not None and state.banks:
+            state.paged_map.prove(state.banks * wi[i].shape[1])
         layers[i] = _step_layer(state, None, wi[i], ww[i], vv[i], ig[i], effective_erase,
                                 fg[i], ri[i], rw[i], out, None, None, None)
         this_shape = _shape(state.banks, state.slots, state.width, wi[i].shape[1],
@@ -1335,7 +1570,9 @@ class DecodeTrace:
 
         key = tuple((t.data_ptr(),) if self.dense else
                     (t.values.data_ptr(), t.free_rows.data_ptr(), t.free_count.data_ptr(),
-                     t.overflow_flag.data_ptr(), t.logical_to_physical.data_ptr(),
+                     t.overflow_flag.data_ptr(),
+                     t.logical_to_physical.data_ptr() if t.paged_map is None else
+                     (t.paged_map.directory.data_ptr(), t.paged_map.pages.data_ptr()),
                      t.template_indices.data_ptr(), t.shared_initial_memory.data_ptr(),
                      t.scratch.data_ptr() if t.scratch is not None else 0)
                     for t in self.tables)

@@ -18,6 +18,7 @@ constexpr int kMaxLayers = 8;               // layers per step launch
 constexpr int kReadBatch = 16;              // read rows in flight per batch
 constexpr int kMaxReadSlots = 4;            // R <= 256 = 4 * 64
 constexpr int kSpinLimit = 1 << 16;         // bounded look-back wait
+constexpr int kMaxPageShift = 6;            // paged slot maps: at most 64 slots per page
 constexpr int kTile = 2048;                 // ranking tile (entries)
 constexpr int kTileThreads = 256;
 constexpr int kPerThread = kTile / kTileThreads;
@@ -126,6 +127,24 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
 __device__ __forceinline__ int wave_or(int v) {
   for (int o = kWave / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, kWave);
   return v;
+}
+
+// Map entry of bank `bank`'s slot `slot` (N slots per bank): the direct
+// map's, or through the paged map's directory (*dir_out: the directory
+// entry, -1 when the page does not exist; the direct map gives 0).
+__device__ __forceinline__ int map_entry(const cowsdm_layer_t& L, int64_t bank, int N, int slot,
+                                         int* dir_out = nullptr) {
+  const int shift = L.map_page_shift;
+  if (shift == 0) {
+    if (dir_out) *dir_out = 0;
+    return L.logical_to_physical[bank * N + slot];
+  }
+  const int d = L.map_directory[bank * (N >> shift) + (slot >> shift)];
+  if (dir_out) *dir_out = d;
+  if (d < 0) return -1;
+  // a directory entry past the pages is corrupt: an entry past every slab
+  if (d >= L.map_page_capacity) return 0x7fffffff;
+  return L.map_pages[(static_cast<int64_t>(d) << shift) + (slot & ((1 << shift) - 1))];
 }
 
 template <typename IDX>

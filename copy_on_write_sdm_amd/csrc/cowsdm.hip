@@ -150,7 +150,7 @@ __global__ __launch_bounds__(1024) void precheck_kernel(
       }
     }
     if (check_capacity && !dense) {
-      const int p = L.logical_to_physical[b * slots + x];
+      const int p = map_entry(L, b, slots, static_cast<int>(x));
       if (p < 0) ++first;
       else if (p >= C) flags |= COWSDM_ERR_CORRUPT;
     }
@@ -367,6 +367,7 @@ enum RankOp : int32_t {
   kOpTrim = 1,     // trim_capacity
   kOpAppend = 2,   // append_banks_from
   kOpRelease = 3,  // release
+  kOpPages = 4,    // paged map compression: entries are (bank, page) pairs
 };
 
 struct RankApply {
@@ -382,6 +383,9 @@ struct RankApply {
   int64_t list_rows;         // entries list_a / list_b can hold
   int64_t src_capacity;      // trim/append: rows of the slab read from
   int32_t* map_clear;        // release: map whose listed rows become -1
+  const int32_t* page_src;   // pages: the direct map the pages copy
+  int32_t* pages_out;        // pages: page rows, list_rows of them
+  int32_t page_shift;        // pages: log2 of the slots per page
 };
 
 // Rank each active entry in ranked order and apply the operation.
@@ -449,6 +453,16 @@ __global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
         a.map_out[a.map_row_offset * s.slots + e] = dst;
         break;
       }
+      case kOpPages: {
+        // entry e is page e % (N / P) of bank e / (N / P): its slots are the
+        // direct map's entries e * P .. e * P + P - 1
+        a.map_out[e] = act[k] && rank < a.list_rows ? static_cast<int32_t>(rank) : -1;
+        if (act[k] && rank < a.list_rows) {
+          const int64_t P = int64_t{1} << a.page_shift;
+          for (int64_t i = 0; i < P; ++i) a.pages_out[rank * P + i] = a.page_src[e * P + i];
+        }
+        break;
+      }
       case kOpRelease:
         if (row < 0) break;
         if (act[k]) {
@@ -462,6 +476,37 @@ __global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
     }
     if (act[k]) ++rank;
   }
+}
+
+// Paged maps: page g of bank b holds a mapped slot (flags over [B * N / P]).
+__global__ void page_flags_kernel(const int32_t* map, int64_t pages, int32_t shift,
+                                  uint8_t* flags) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t P = int64_t{1} << shift;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < pages;
+       e += stride) {
+    uint8_t any = 0;
+    for (int64_t i = 0; i < P; ++i) any |= map[e * P + i] >= 0 ? 1 : 0;
+    flags[e] = any;
+  }
+}
+
+// The direct map of a paged one: entry (b, x) through the directory.
+__global__ void page_expand_kernel(const int32_t* directory, const int32_t* pages,
+                                   int64_t page_capacity, int64_t entries, int32_t shift,
+                                   int32_t* map) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t mask = (int64_t{1} << shift) - 1;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < entries;
+       e += stride) {
+    const int32_t d = directory[e >> shift];
+    // (a directory entry past the pages is corrupt: an entry past every slab)
+    map[e] = d < 0 ? -1 : d >= page_capacity ? 0x7fffffff : pages[(int64_t{d} << shift) + (e & mask)];
+  }
+}
+
+__global__ void store_count_kernel(const int64_t* total, int32_t* count) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *count = static_cast<int32_t>(*total);
 }
 
 // free_rows[i] = A + i for i < capacity - A; free_count = capacity - A.
@@ -709,10 +754,17 @@ int32_t check_layer(const cowsdm_layer_t& L, bool dense) {
     return fail(COWSDM_EARG, "null tensor pointer in step layer");
   }
   if (!dense) {
+    const bool paged = L.map_page_shift != 0;
     if (!L.shared_initial_memory || !L.template_indices ||
-        !L.logical_to_physical || !L.free_rows || !L.free_count ||
-        !L.overflow_flag || !L.scratch) {
+        (paged ? (!L.map_directory || !L.map_pages || !L.map_page_count)
+               : !L.logical_to_physical) ||
+        !L.free_rows || !L.free_count || !L.overflow_flag || !L.scratch) {
       return fail(COWSDM_EARG, "null state pointer in packed step layer");
+    }
+    if (paged && (L.map_page_shift < 0 || L.map_page_shift > kMaxPageShift ||
+                  L.map_page_capacity <= 0 || L.map_page_capacity >= (1ll << 31))) {
+      return fail(COWSDM_EARG, "paged map: page shift in [1, %d] and a positive page capacity",
+                  kMaxPageShift);
     }
     if (L.capacity_rows <= 0 || L.capacity_rows >= (1ll << 31)) {
       return fail(COWSDM_EARG, "capacity_rows must be in [1, 2^31)");
@@ -749,8 +801,8 @@ int row_vec(const cowsdm_layer_t* layers, int32_t nlayers, const cowsdm_shape_t*
 // Float lanes of a persistent trace launch (a row of D <= 64 floats takes
 // one per lane, <= 128 two, <= 256 four), or 0 when the shape, the alignment
 // or the strides rule one out.
-int persistent_vec(int vec, const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
-                   int32_t nlayers, bool dense) {
+int persistent_vec(int vec, const cowsdm_layer_t* layers, const cowsdm_shape_t* shape,
+                   const cowsdm_trace_t* trace, int32_t nlayers, bool dense) {
   const int64_t D = shape->width;
   int tv = D <= kWave ? 1 : (D <= 2 * kWave ? 2 : (D <= 4 * kWave ? 4 : 0));
   if (tv && D % tv != 0) tv = 0;
@@ -760,6 +812,10 @@ int persistent_vec(int vec, const cowsdm_shape_t* shape, const cowsdm_trace_t* t
     if (trace->stride_bytes[k] < 0 || trace->stride_bytes[k] >= (1ll << 32)) tv = 0;
   }
   if (shape->writes > kTraceMaxWrites || shape->reads > kTraceMaxReads || nlayers > kMaxLayers) tv = 0;
+  // (persistent launches keep the direct map)
+  for (int32_t i = 0; i < nlayers && !dense; ++i) {
+    if (layers[i].map_page_shift != 0) tv = 0;
+  }
   if (!dense && shape->banks > kTraceMaxBanks) tv = 0;
   return tv;
 }
@@ -777,6 +833,22 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
     return fail(COWSDM_EARG, "templates must be positive");
   }
   int vec = row_vec(layers, nlayers, shape, dense, trace);
+  if (!dense) {
+    // paged slot maps run the small one-step kernel only
+    for (int32_t i = 0; i < nlayers; ++i) {
+      const int shift = layers[i].map_page_shift;
+      if (shift == 0) continue;
+      if (shape->slots % (int64_t{1} << shift) != 0) {
+        return fail(COWSDM_EARG, "paged map: %lld slots are not whole pages of %d",
+                    static_cast<long long>(shape->slots), 1 << shift);
+      }
+      if (shape->writes > 4 || shape->reads > 16 || shape->width > kWave * vec ||
+          shape->banks > 256) {
+        return fail(COWSDM_ELIMIT, "paged map: steps need W <= 4, R <= 16, one row pass "
+                                   "(D <= %d here) and at most 256 banks", kWave * vec);
+      }
+    }
+  }
   if (trace) {
     if (trace->step_index && !trace->ticket) return fail(COWSDM_EARG, "trace: null ticket");
     if (trace->report && !trace->step_index) {
@@ -799,7 +871,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   }
   if (steps < 0) return fail(COWSDM_EARG, "steps must be non-negative");
   // persistent multi-step launches: up to scan_steps steps per launch
-  const int trace_vec = trace ? persistent_vec(vec, shape, trace, nlayers, dense) : 0;
+  const int trace_vec = trace ? persistent_vec(vec, layers, shape, trace, nlayers, dense) : 0;
   // packed persistent launches are planned: they need the control words and
   // scan blocks of enough steps
   const bool planned = !dense && trace && trace->control;
@@ -1033,7 +1105,7 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
   if (!layers || !shape || !trace || nlayers <= 0) return 0;
   if (check_shape(shape) != 0) return 0;
   const int vec = row_vec(layers, nlayers, shape, dense != 0, trace);
-  return persistent_vec(vec, shape, trace, nlayers, dense != 0) > 0 ? 1 : 0;
+  return persistent_vec(vec, layers, shape, trace, nlayers, dense != 0) > 0 ? 1 : 0;
 }
 
 int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
@@ -1263,7 +1335,8 @@ int32_t cowsdm_step_precheck(const cowsdm_layer_t* layer, const cowsdm_shape_t* 
     return fail(COWSDM_EARG, "precheck: null route indices");
   }
   if (check_capacity && !dense &&
-      (!layer->logical_to_physical || !layer->free_count)) {
+      ((layer->map_page_shift == 0 ? !layer->logical_to_physical : !layer->map_directory) ||
+       !layer->free_count)) {
     return fail(COWSDM_EARG, "precheck: capacity check needs map and free_count");
   }
   const hipStream_t s = as_stream(stream);
@@ -1537,6 +1610,67 @@ int32_t cowsdm_retain_banks(const int32_t* map, const int64_t* tmpl, int64_t ban
                      map, tmpl, banks, slots, bank_list, nsel, new_map, new_tmpl,
                      static_cast<const int64_t*>(nullptr), int64_t{0});
   return launch_status("retain_banks");
+}
+
+int32_t cowsdm_paged_count(const int32_t* map, int64_t banks, int64_t slots, int32_t page_shift,
+                           uint8_t* flags, void* workspace, int64_t* total, void* stream) {
+  if (!map || !flags || !workspace || !total || banks < 0 || slots <= 0 ||
+      page_shift < 1 || page_shift > kMaxPageShift || slots % (int64_t{1} << page_shift) != 0) {
+    return fail(COWSDM_EARG, "paged_count: invalid arguments (page shift in [1, %d], whole pages)",
+                kMaxPageShift);
+  }
+  const int64_t pages = banks * (slots >> page_shift);
+  if (pages >= (1ll << 31)) return fail(COWSDM_ELIMIT, "paged_count: too many pages");
+  const hipStream_t s = as_stream(stream);
+  if (pages > 0) {
+    hipLaunchKernelGGL(page_flags_kernel, dim3(grid_for(pages, 256)), dim3(256), 0, s, map,
+                       pages, page_shift, flags);
+    if (int32_t e = launch_status("page flags")) return e;
+  }
+  return cowsdm_count_active(nullptr, banks, slots >> page_shift, nullptr, banks, flags,
+                             workspace, total, stream);
+}
+
+int32_t cowsdm_paged_compress(const int32_t* map, int64_t banks, int64_t slots,
+                              int32_t page_shift, const uint8_t* flags, void* workspace,
+                              int32_t* directory, int32_t* pages, int64_t page_capacity,
+                              int32_t* page_count, void* stream) {
+  if (!map || !flags || !workspace || !directory || !page_count || banks < 0 || slots <= 0 ||
+      page_shift < 1 || page_shift > kMaxPageShift || slots % (int64_t{1} << page_shift) != 0 ||
+      page_capacity < 0 || (page_capacity > 0 && !pages)) {
+    return fail(COWSDM_EARG, "paged_compress: invalid arguments");
+  }
+  const hipStream_t s = as_stream(stream);
+  const int64_t per_bank = slots >> page_shift;
+  const int64_t entries = banks * per_bank;
+  Workspace ws = carve(workspace, entries, 0);
+  RankSource src{nullptr, nullptr, flags, per_bank, entries, banks};
+  RankApply a{};
+  a.op = kOpPages;
+  a.map_out = directory;
+  a.list_rows = page_capacity;
+  a.page_src = map;
+  a.pages_out = pages;
+  a.page_shift = page_shift;
+  if (int32_t e = rank_apply(src, ws, a, s)) return e;
+  hipLaunchKernelGGL(store_count_kernel, dim3(1), dim3(64), 0, s,
+                     static_cast<const int64_t*>(ws.total), page_count);
+  return launch_status("paged compress");
+}
+
+int32_t cowsdm_paged_expand(const int32_t* directory, const int32_t* pages,
+                            int64_t page_capacity, int64_t banks, int64_t slots,
+                            int32_t page_shift, int32_t* map, void* stream) {
+  if (!directory || !map || banks < 0 || slots <= 0 || page_shift < 1 ||
+      page_shift > kMaxPageShift || slots % (int64_t{1} << page_shift) != 0 ||
+      page_capacity < 0 || (page_capacity > 0 && !pages)) {
+    return fail(COWSDM_EARG, "paged_expand: invalid arguments");
+  }
+  const int64_t entries = banks * slots;
+  if (entries == 0) return 0;
+  hipLaunchKernelGGL(page_expand_kernel, dim3(grid_for(entries, 256)), dim3(256), 0,
+                     as_stream(stream), directory, pages, page_capacity, entries, page_shift, map);
+  return launch_status("paged expand");
 }
 
 int32_t cowsdm_materialize_dense(const float* m0, int64_t templates, const int64_t* tmpl,

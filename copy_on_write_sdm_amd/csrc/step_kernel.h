@@ -196,7 +196,7 @@ struct FirstTouchTable {
         int mapped[kLocalTableWrites];
 #pragma unroll
         for (int j = 0; j < kLocalTableWrites; ++j) {
-          mapped[j] = j < W ? L.logical_to_physical[static_cast<int64_t>(tb) * N + slot[k][j]] : 0;
+          mapped[j] = j < W ? map_entry(L, tb, N, slot[k][j]) : 0;
         }
         int c = 0;
 #pragma unroll
@@ -380,6 +380,56 @@ __device__ __forceinline__ void record_errors(const cowsdm_layer_t& L, int lane,
   }
 }
 
+// First-touch map entries of one bank in a paged map (lanes w < W hold the
+// write routes; `first` marks first touches, `dir` their directory entry,
+// `row` their popped row).  A first touch in a page the bank already has is
+// one store; the first touches in pages it lacks take one new page per
+// distinct page, in lane order from the layer's page counter, and the
+// wave writes each such page whole (-1 but for those first touches) and
+// then its directory entry.  Called once every table of the launch is
+// built (no wave reads this bank's pages after that).
+__device__ __forceinline__ void store_paged(const cowsdm_layer_t& L, int64_t bank, int N,
+                                            int slot, bool first, int dir, int row, int lane) {
+  const int shift = L.map_page_shift;
+  const int pmask = (1 << shift) - 1;
+  if (first && dir >= 0) {
+    L.map_pages[(static_cast<int64_t>(dir) << shift) + (slot & pmask)] = row;
+  }
+  const bool need = first && dir < 0;
+  const int page = need ? (slot >> shift) : -1;
+  // the lowest lane needing the same page takes it
+  bool leads = need;
+#pragma unroll
+  for (int j = 0; j < kLocalTableWrites; ++j) {
+    if (need && j < lane && rl(page, j) == page) leads = false;
+  }
+  const uint64_t leaders = __ballot(leads);
+  if (leaders == 0) return;
+  int base = 0;
+  if (lane == 0) {
+    base = __hip_atomic_fetch_add(L.map_page_count, __popcll(leaders), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  }
+  base = rl(base, 0);
+  if (base + __popcll(leaders) > L.map_page_capacity) {
+    // the host's page proof rules this out: flag the state, write nothing
+    record_errors(L, lane, COWSDM_ERR_CORRUPT);
+    return;
+  }
+  for (uint64_t left = leaders; left != 0; left &= left - 1) {
+    const int k = __ffsll(static_cast<long long>(left)) - 1;
+    const int kpage = rl(page, k);
+    const int id = base + __popcll(leaders & ((1ull << k) - 1));
+    int entry = -1;
+#pragma unroll
+    for (int j = 0; j < kLocalTableWrites; ++j) {
+      if (rl(page, j) == kpage && (rl(slot, j) & pmask) == lane) entry = rl(row, j);
+    }
+    if (lane <= pmask) L.map_pages[(static_cast<int64_t>(id) << shift) + lane] = entry;
+    if (lane == 0) L.map_directory[bank * (N >> shift) + kpage] = id;
+  }
+}
+
 // ------------------------------------------------- the small decode step
 
 // One wave = one bank of one layer, for W <= 4, R <= 16 and a row that one
@@ -474,9 +524,10 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_small_kernel(StepParams
 
   // ---- map lookups (packed), then the table's
   int phys = -1;
+  int dir = -1;   // paged map: the slot's directory entry
   if constexpr (!DENSE) {
     if ((is_w || is_r) && !((werr | rerr) & (COWSDM_ERR_WRITE_INDEX | COWSDM_ERR_READ_INDEX))) {
-      phys = L.logical_to_physical[b * N + slot];
+      phys = map_entry(L, b, N, slot, &dir);
       if (phys >= C) {
         if (is_w) werr |= COWSDM_ERR_CORRUPT;
         else rerr |= COWSDM_ERR_CORRUPT;
@@ -663,7 +714,11 @@ __global__ __launch_bounds__(kStepThreads) void sdm_step_small_kernel(StepParams
   bool closed_layer = false;
   if constexpr (!DENSE) {
     const bool stored_ok = wait_tickets(L, ticket, B, lane);
-    if (commit && first && stored_ok) L.logical_to_physical[b * N + slot] = new_row;
+    if (L.map_page_shift == 0) {
+      if (commit && first && stored_ok) L.logical_to_physical[b * N + slot] = new_row;
+    } else if (commit && stored_ok) {
+      store_paged(L, b, N, slot, first, dir, new_row, lane);
+    }
     if (lane == 0) {
       if (L.first_touches_out) L.first_touches_out[b] = commit ? count : 0;
       if (L.repeated_writes_out) L.repeated_writes_out[b] = wok ? W - count : W;

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 7
+#define COWSDM_ABI_VERSION 8
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -106,6 +106,22 @@ typedef struct cowsdm_layer {
   int64_t* first_touches_out;   /* [B] or null */
   int64_t* repeated_writes_out; /* [B] or null */
   int32_t* allocated_rows_out;  /* scalar or null */
+  /* Paged slot map (map_page_shift > 0; 0 keeps the direct map
+   * logical_to_physical).  With P = 1 << map_page_shift slots per page,
+   * bank b's slot x is mapped at
+   *   map_pages[(map_directory[b * (N / P) + x / P] << map_page_shift) + x % P]
+   * and a directory entry of -1 means no slot of that page is mapped.  Pages
+   * in use are map_pages rows 0 .. *map_page_count - 1; a step takes new ones
+   * from *map_page_count up (never more than map_page_capacity), at most one
+   * per write route.  logical_to_physical is ignored (may be null).  Paged
+   * layers run the one-step kernel only: W <= 4, R <= 16, D <= 256, B <= 256
+   * (COWSDM_ELIMIT otherwise), and no persistent launches. */
+  int32_t* map_directory;       /* [B, N / P] */
+  int32_t* map_pages;           /* [map_page_capacity, P] */
+  int32_t* map_page_count;      /* scalar */
+  int64_t map_page_capacity;
+  int32_t map_page_shift;
+  int32_t map_reserved;
 } cowsdm_layer_t;
 
 /* Consecutive steps over device-resident inputs of many decode steps;
@@ -443,6 +459,39 @@ int32_t cowsdm_retain_banks(const int32_t* logical_to_physical,
                             const int64_t* bank_list, int64_t nsel,
                             int32_t* new_logical_to_physical,
                             int64_t* new_template_indices, void* stream);
+
+/* ---- paged slot maps (the compressed map the reference leaves for large
+ * address spaces, README.md:123-130; allocator.py:485-489 reserves the
+ * place: "a later compressed map can replace it without changing SDM").
+ * A paged map holds the same entries as the direct map [B, N], in pages of
+ * P = 1 << page_shift slots (P divides N); only pages with a mapped slot
+ * exist (see cowsdm_layer_t).  Lifecycle operations run on the direct form:
+ * cowsdm_paged_expand rebuilds it, cowsdm_paged_count + _compress pack it
+ * back, pages numbered in row-major (bank, page) order. */
+
+/* The pages holding a mapped slot: flags[b * (N / P) + g] = 1 when page g
+ * of bank b holds one (uint8 [B * N / P]), and *total their count.  Leaves
+ * the ranks cowsdm_paged_compress uses in `workspace`
+ * (cowsdm_workspace_bytes(B * N / P, 0) bytes).  No counterpart in the
+ * reference. */
+int32_t cowsdm_paged_count(const int32_t* logical_to_physical, int64_t banks, int64_t slots,
+                           int32_t page_shift, uint8_t* flags, void* workspace,
+                           int64_t* total, void* stream);
+
+/* After cowsdm_paged_count with the same arguments: directory[b, g] = the
+ * page's rank among flagged pages (row-major), or -1; pages[rank] = the
+ * map's P entries; *page_count = the flagged pages.  Size `pages` from the
+ * count's total: pages ranked at or past page_capacity are not written.
+ * No counterpart in the reference. */
+int32_t cowsdm_paged_compress(const int32_t* logical_to_physical, int64_t banks,
+                              int64_t slots, int32_t page_shift, const uint8_t* flags,
+                              void* workspace, int32_t* directory, int32_t* pages,
+                              int64_t page_capacity, int32_t* page_count, void* stream);
+
+/* The direct map [B, N] of a paged one.  No counterpart in the reference. */
+int32_t cowsdm_paged_expand(const int32_t* directory, const int32_t* pages,
+                            int64_t page_capacity, int64_t banks, int64_t slots,
+                            int32_t page_shift, int32_t* logical_to_physical, void* stream);
 
 /* dense[b, n] = map[b, n] >= 0 ? values[map[b, n]] : M0[template[b], n].
  * Replaces materialize_dense, allocator.py:1003-1016. */

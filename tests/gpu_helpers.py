@@ -21,7 +21,7 @@ def snapshot(state) -> dict:
     """Exact host copy of a product state's allocator-visible tensors."""
 
     free = int(state.free_count.item())
-    mapping = state.logical_to_physical.cpu().numpy()
+    mapping = state.direct_map().cpu().numpy()
     values = state.values.cpu().numpy()
     live = mapping[mapping >= 0]
     return {

@@ -38,7 +38,7 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 7
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 8
     # epoch and header, plan words [banks][steps], step and running totals,
     # at most banks * W pops per step and 4 words per growth segment, int64 each
     assert lib.cowsdm_trace_scan_words(64, 4, 512) == (16 + 64 * 512 + 512 + 513 + 64 * 512 * 4
@@ -112,13 +112,34 @@ def test_trace_timing_without_launches():
 
 
 def test_structure_layout_matches_header():
-    # 21 pointer-sized fields and one int64 in cowsdm_layer_t
-    assert ctypes.sizeof(nat.Layer) == 21 * 8
+    # 21 pointer-sized fields and one int64 in cowsdm_layer_t, then the
+    # paged map: 3 pointers, an int64 and two int32
+    assert ctypes.sizeof(nat.Layer) == 21 * 8 + 3 * 8 + 8 + 2 * 4
+    assert nat.Layer.map_directory.offset == 21 * 8
     assert ctypes.sizeof(nat.Shape) == 7 * 8
     assert ctypes.sizeof(nat.Trace) == 20 * 8
     assert ctypes.sizeof(nat.Recurrence) == 14 * 8
     assert ctypes.sizeof(nat.Controller) == 15 * 8 + 2 * 4
     assert nat.REPORT_WORDS == 2 + nat.CTRL_WORDS == 14
+
+
+def test_paged_map_argument_errors():
+    """Rejected before any launch: page shifts outside [1, 6], slots that
+    are not whole pages, null tensors."""
+
+    lib = nat.lib()
+    buf = ctypes.c_int64(0)
+    p = ctypes.byref(buf)
+    assert lib.cowsdm_paged_count(p, 4, 64, 0, p, p, p, None) == -1
+    assert lib.cowsdm_paged_count(p, 4, 64, 7, p, p, p, None) == -1
+    assert b"page shift" in lib.cowsdm_last_error_string()
+    assert lib.cowsdm_paged_count(p, 4, 60, 4, p, p, p, None) == -1
+    assert lib.cowsdm_paged_count(None, 4, 64, 4, p, p, p, None) == -1
+    assert lib.cowsdm_paged_compress(p, 4, 60, 4, p, p, p, p, 8, p, None) == -1
+    assert lib.cowsdm_paged_compress(p, 4, 64, 4, p, p, p, None, 8, p, None) == -1
+    assert lib.cowsdm_paged_expand(p, p, 8, 4, 60, 4, p, None) == -1
+    assert lib.cowsdm_paged_expand(None, p, 8, 4, 64, 4, p, None) == -1
+    assert lib.cowsdm_paged_expand(p, p, 8, 0, 64, 4, p, None) == 0     # nothing to run
 
 
 def test_recurrence_argument_errors():

@@ -1,0 +1,147 @@
+"""GPU parity of the paged slot map (PagedSlotMap: the compressed map the
+reference leaves as future work for large address spaces, README.md:123-130,
+allocator.py:485-489).  A state whose map is paged must behave exactly like
+the same state with the direct map: equal readings, maps (physical rows
+included), free stacks, live rows, capacities and growth counters, bit for
+bit, through
+
+* the reference's decode loop (decode_sdm_layer: prepare_step_capacity then
+  the packed step) at config 5's shape (4 heads x 64 requests = 256 banks,
+  N = 65,536, Zipf(1.1) routes, an empty slab growing every few steps), with
+  pages taken inside the step and the page pool growing;
+* the handoff of a dense prefix (from_dense_overlay), release, retain
+  (compaction), trim and admission (append_banks_from of a paged cohort),
+  with decode steps between them;
+
+while storing fewer map bytes than the direct map."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import copy_on_write_sdm_amd as cow
+from copy_on_write_sdm_amd import synthetic
+from copy_on_write_sdm_amd.inference import SDMStepInputs, decode_sdm_layer
+from gpu_helpers import assert_states_identical
+
+pytestmark = pytest.mark.gpu
+
+W, R, D = 4, 16, 128
+
+
+def _decode(states, batch, steps, start=0):
+    """decode_sdm_layer step by step on each state; readings [steps, S, B, D]."""
+
+    out = []
+    for s in range(start, start + steps):
+        out.append(torch.stack([decode_sdm_layer(st, SDMStepInputs(**batch.step(s, 0)))
+                                for st in states]))
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("page_slots", [16, 64])
+def test_paged_decode_matches_direct_config5(device, page_slots):
+    heads, requests, slots, steps = 4, 64, 65536, 48
+    banks = heads * requests
+    quantum = banks * W * 4
+    print(f"paged decode config 5 P={page_slots}", flush=True)
+    m0 = synthetic.make_initial_memory(1, heads, slots, D, seed=61, device=device)[0]
+    templates = torch.arange(heads, device=device).repeat(requests)
+    batch = synthetic.make_steps(steps=steps, layers=1, banks=banks, slots=slots, width=D,
+                                 writes=W, reads=R, seed=62, device=device,
+                                 distribution="zipf", heads=heads)
+    kw = dict(banks=banks, capacity_rows=quantum, template_indices=templates,
+              growth_quantum_rows=quantum)
+    direct = cow.PackedSDMCopyOnWriteState.allocate(m0, **kw)
+    paged = cow.PackedSDMCopyOnWriteState.allocate(m0, map_page_slots=page_slots, **kw)
+    assert paged.paged_map is not None and paged.paged_map.capacity == banks
+    want = _decode([direct], batch, steps)
+    got = _decode([paged], batch, steps)
+    assert torch.equal(got, want)
+    assert_states_identical(paged, direct)
+    assert paged.growth_events > 0
+    # the page pool grew inside the decode (it started at one page per bank)
+    assert paged.paged_map.capacity > banks
+    paged.validate_invariants()
+    used = int(paged.paged_map.page_count)
+    assert used == int((paged.paged_map.directory >= 0).sum())
+    stored = paged.storage_bytes()["logical_to_physical"]
+    assert stored < direct.storage_bytes()["logical_to_physical"]
+    print(f"map bytes: direct {direct.storage_bytes()['logical_to_physical']} "
+          f"paged {stored} ({used} pages in use)", flush=True)
+    # a decode trace over a paged state runs one launch per step and equals
+    # the loop too
+    more = synthetic.make_steps(steps=8, layers=1, banks=banks, slots=slots, width=D,
+                                writes=W, reads=R, seed=63, device=device,
+                                distribution="zipf", heads=heads)
+    kw_more = dict(write_indices=more.write_indices, write_weights=more.write_weights,
+                   values=more.values, input_gate=more.input_gate,
+                   forget_log_gate=more.forget_log_gate, read_indices=more.read_indices,
+                   read_weights=more.read_weights)
+    out = torch.empty(8, 1, banks, D, device=device)
+    tr = cow.DecodeTrace(states=[paged], outputs=out, **kw_more)
+    tr.run(8)
+    assert not tr.planned
+    want = _decode([direct], more, 8)
+    assert torch.equal(out, want)
+    assert_states_identical(paged, direct)
+
+
+def test_paged_lifecycle_matches_direct(device):
+    """Handoff, decode, release, retain, trim, admission, decode: the paged
+    state equals the direct one after every operation."""
+
+    banks, slots, prefix, page_slots = 8, 1024, 24, 16
+    quantum = banks * W * 2
+    m0 = synthetic.make_initial_memory(1, 1, slots, D, seed=71, device=device)[0]
+    g = torch.Generator().manual_seed(72)
+
+    def cohort(n, seed):
+        table = m0[0].expand(n, -1, -1).clone(memory_format=torch.contiguous_format)
+        table += (torch.randn(n, slots, D, generator=g) * 0.1).to(device)
+        active = torch.zeros(n, slots, dtype=torch.bool)
+        for b in range(n):
+            active[b, torch.randperm(slots, generator=g)[:prefix * W // 2]] = True
+        active = active.to(device)
+        tmpl = torch.zeros(n, dtype=torch.int64, device=device)
+        make = lambda p: cow.PackedSDMCopyOnWriteState.from_dense_overlay(  # noqa: E731
+            m0, table, active, template_indices=tmpl, growth_quantum_rows=quantum,
+            map_page_slots=p)
+        return make(None), make(page_slots)
+
+    direct, paged = cohort(banks, 1)
+    assert_states_identical(paged, direct)
+    assert torch.equal(paged.materialize_dense(), direct.materialize_dense())
+
+    def decode(n, seed):
+        batch = synthetic.make_steps(steps=n, layers=1, banks=direct.banks, slots=slots,
+                                     width=D, writes=W, reads=R, seed=seed, device=device)
+        assert torch.equal(_decode([paged], batch, n), _decode([direct], batch, n))
+        assert_states_identical(paged, direct)
+
+    decode(6, 80)
+    gone = torch.tensor([1, 4, 6], device=device)
+    assert int(paged.release(gone)) == int(direct.release(gone)) > 0
+    assert_states_identical(paged, direct)
+    keep = torch.tensor([0, 2, 3, 5, 7], device=device)
+    paged.retain_banks(keep)
+    direct.retain_banks(keep)
+    assert_states_identical(paged, direct)
+    assert paged.trim_capacity(headroom_rows=8) == direct.trim_capacity(headroom_rows=8) > 0
+    assert_states_identical(paged, direct)
+    decode(4, 81)
+    other_direct, other_paged = cohort(3, 2)
+    assert paged.append_banks_from(other_paged) == direct.append_banks_from(other_direct)
+    assert_states_identical(paged, direct)
+    assert_states_identical(other_paged, other_direct)   # the source is unchanged
+    decode(6, 82)
+    for st in (paged, direct):
+        st.validate_invariants()
+    assert torch.equal(paged.materialize_dense(), direct.materialize_dense())
+    with pytest.raises(ValueError, match="retained bank index is invalid"):
+        paged.retain_banks(torch.tensor([0, 0], device=device))
+    assert_states_identical(paged, direct)
+    paged.to_direct_map()
+    assert paged.paged_map is None
+    assert torch.equal(paged.logical_to_physical, direct.logical_to_physical)

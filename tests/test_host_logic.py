@@ -168,3 +168,16 @@ def test_lifecycle_argument_errors():
     with pytest.raises(ValueError, match="retained bank indices must be integer"):
         state.retain_banks(torch.zeros(2))
     assert int(state.release(torch.zeros(0, dtype=torch.int64))) == 0
+
+
+def test_paged_map_page_sizes():
+    """Pages hold a power of two of 2 to 64 slots dividing N."""
+
+    from copy_on_write_sdm_amd.allocator import PagedSlotMap
+
+    assert PagedSlotMap._shift(16, 65536) == 4
+    assert PagedSlotMap._shift(2, 4) == 1
+    assert PagedSlotMap._shift(64, 128) == 6
+    for bad, slots in ((1, 64), (3, 63), (128, 1024), (16, 40), (0, 16)):
+        with pytest.raises(ValueError, match="power of two"):
+            PagedSlotMap._shift(bad, slots)
