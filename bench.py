@@ -83,6 +83,9 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="run one 256 MiB device copy first, so that counter passes "
                         "(FETCH_SIZE, WRITE_SIZE) can be scaled by a kernel of known traffic")
+    p.add_argument("--map-page-slots", type=int, default=None,
+                   help="after the run, report the paged slot map with this many slots per "
+                        "page (default: 16 for config 5, none otherwise)")
     p.add_argument("--eager-steps", type=int, default=None,
                    help="steps of the per-layer Python drop-in path to time (0: skip; "
                         "default 32 for config 2, else 0)")
@@ -283,6 +286,8 @@ def main() -> int:
         print("--steps must be positive and --warmup non-negative", file=sys.stderr)
         return 2
     eager_steps = (32 if args.config == 2 else 0) if args.eager_steps is None else args.eager_steps
+    if args.map_page_slots is None and args.config == 5:
+        args.map_page_slots = 16
     banks = B * HEADS                       # bank = request * H + head
     templates = torch.arange(HEADS, dtype=torch.int64, device=dev).repeat(B)
     if args.copy_calibration:
@@ -641,6 +646,71 @@ def main() -> int:
         }
         del dec
 
+    # ---- the paged slot map (large address spaces, config 5): map bytes of
+    # the decoded states, direct and paged; then fresh states of both forms
+    # decoded 64 steps from an empty slab (one launch of all layers per step
+    # with the host proof: paged maps have no persistent launches), outputs
+    # compared, both timed, and their map bytes
+    paged_leg = None
+    if args.map_page_slots:
+        P = args.map_page_slots
+        direct_bytes = sum(st.storage_bytes()["logical_to_physical"] for st in states)
+        end_paged = sum(cow.PagedSlotMap.compress(st.logical_to_physical, P).used_bytes()
+                        for st in states)
+        fresh_steps = 64
+        fresh = synthetic.make_steps(steps=fresh_steps, layers=LAYERS, banks=banks, slots=SLOTS,
+                                     width=WIDTH, writes=WRITES, reads=READS,
+                                     seed=args.seed + 9, device=dev,
+                                     distribution=cfg["distribution"], heads=HEADS)
+        keys = ("write_indices", "write_weights", "values", "input_gate", "forget_log_gate",
+                "read_indices", "read_weights")
+
+        def fresh_decode(page_slots):
+            sts = [cow.PackedSDMCopyOnWriteState.allocate(
+                m0[l], banks=banks, capacity_rows=quantum, template_indices=templates,
+                growth_quantum_rows=quantum, map_page_slots=page_slots) for l in range(LAYERS)]
+            outs = torch.empty(fresh_steps, LAYERS, banks, WIDTH, device=dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for s in range(fresh_steps):
+                cow.PackedSDMCopyOnWriteState.prepare_step_capacity_layers(sts, banks * WRITES)
+                cow.packed_sdm_cow_step_layers(sts, *[getattr(fresh, k)[s] for k in keys],
+                                               outputs=list(outs[s]))
+            torch.cuda.synchronize()
+            return sts, outs, B * fresh_steps / (time.perf_counter() - t0)
+
+        d_states, d_out, d_rate = fresh_decode(None)
+        p_states, p_out, p_rate = fresh_decode(P)
+        if not torch.equal(d_out, p_out) or not all(
+                torch.equal(a.direct_map(), b.logical_to_physical)
+                for a, b in zip(p_states, d_states)):
+            raise AssertionError("paged and direct maps decoded differently")
+        fresh_direct = sum(st.storage_bytes()["logical_to_physical"] for st in d_states)
+        fresh_paged = sum(st.paged_map.used_bytes() for st in p_states)
+        live = sum(int(st.allocated_rows_tensor()) for st in p_states)
+        paged_leg = {
+            "page_slots": P,
+            "direct_map_bytes_per_layer": direct_bytes // LAYERS,
+            "after_run": {
+                "live_slot_fraction": memory["live_row_fraction"],
+                "paged_map_bytes_per_layer": round(end_paged / LAYERS),
+                "paged_over_direct_map_bytes": round(end_paged / direct_bytes, 4),
+            },
+            f"after_{fresh_steps}_steps": {
+                "live_slot_fraction": round(live / (LAYERS * banks * SLOTS), 4),
+                "paged_map_bytes_per_layer": round(fresh_paged / LAYERS),
+                "paged_over_direct_map_bytes": round(fresh_paged / fresh_direct, 4),
+                "stepwise_tokens_per_s_direct": round(d_rate, 1),
+                "stepwise_tokens_per_s_paged": round(p_rate, 1),
+                "outputs_equal": True,
+            },
+            "what": ("map bytes (paged: directory plus the pages in use) after the timed run, "
+                     "and of fresh states after 64 steps decoded in both forms, one launch of "
+                     "all layers per step with the host proof; the pages pay while few slots "
+                     "of a page are live (the synthetic Zipf routes scatter hot slots over N)"),
+        }
+        del d_states, p_states, d_out, p_out
+
     # roofline of the dominant kernel, the persistent decode kernel: the
     # algorithmic bytes of the steps the timed launches ran over its mean
     # duration (HIP events at its own start and end); the count and plan
@@ -743,6 +813,8 @@ def main() -> int:
         "controller_decode": controller_leg,
         "controller_graph": controller_graph,
     }
+    if paged_leg is not None:
+        result["paged_map"] = paged_leg
     if not args.no_cpu_baseline and args.config == 2:
         result["cpu_baseline"] = cpu_baseline(B, args.cpu_seconds, args.seed)
     print(json.dumps(result))

@@ -9,6 +9,7 @@ kernels for gfx950 in libcowsdm.so (C ABI: include/cowsdm.h).
 from .allocator import (
     DecodeTrace,
     PackedSDMCopyOnWriteState,
+    PagedSlotMap,
     SDMCopyOnWriteStep,
     dense_sdm_sparse_step,
     dense_sdm_sparse_step_layers,
@@ -50,6 +51,7 @@ __all__ = [
     "SDMPrefill",
     "FaithfulSDMDecodeState",
     "PackedSDMCopyOnWriteState",
+    "PagedSlotMap",
     "SDMCopyOnWriteStep",
     "SDMStepInputs",
     "allocate_dense_cache",
