@@ -358,14 +358,18 @@ def main() -> int:
         handoff_first_ms = None
         for _ in range(2):
             t0 = time.perf_counter()
-            states = []
+            masks = []
             for l in range(LAYERS):
                 active = torch.zeros(banks, SLOTS, dtype=torch.bool, device=dev)
                 cow.mark_written(active,
                                  prefix.write_indices[:, l].permute(1, 0, 2).reshape(banks, -1))
-                states.append(cow.PackedSDMCopyOnWriteState.from_dense_overlay(
-                    m0[l], tables[l], active, template_indices=templates,
-                    growth_quantum_rows=quantum))
+                masks.append(active)
+            # every layer's handoff at once: one read of the active counts and
+            # one of the invariant checks for all layers
+            states = cow.PackedSDMCopyOnWriteState.from_dense_overlay_layers(
+                [m0[l] for l in range(LAYERS)], tables, masks, template_indices=templates,
+                growth_quantum_rows=quantum)
+            del masks
             torch.cuda.synchronize()
             handoff_ms = 1000.0 * (time.perf_counter() - t0)
             if handoff_first_ms is None:

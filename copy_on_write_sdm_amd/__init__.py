@@ -23,6 +23,7 @@ from .inference import (
     decode_sdm_layer,
     decode_sdm_layer_dense,
     pack_prefill_layer,
+    pack_prefill_layers,
 )
 from .routing import product_key_routes
 from .recurrence import dense_sparse_routes, gated_delta_recurrence, sdm_recurrence
@@ -67,6 +68,7 @@ __all__ = [
     "gated_delta_recurrence",
     "mark_written",
     "pack_prefill_layer",
+    "pack_prefill_layers",
     "packed_sdm_cow_step",
     "packed_sdm_cow_step_layers",
     "prefill_faithful_sdm_stack",

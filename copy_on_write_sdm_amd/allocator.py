@@ -305,6 +305,21 @@ class PackedSDMCopyOnWriteState:
         ``map_page_slots`` (not in the reference) the map is paged
         (``PagedSlotMap``) with that many slots per page."""
 
+        state, result = cls._allocate_state(
+            shared_initial_memory, banks=banks, capacity_rows=capacity_rows,
+            template_indices=template_indices, state_dtype=state_dtype,
+            growth_quantum_rows=growth_quantum_rows, map_page_slots=map_page_slots)
+        if int(result.item()) & nat.ERR_TEMPLATE:
+            raise ValueError("template index lies outside shared initial memory")
+        return state
+
+    @classmethod
+    def _allocate_state(cls, shared_initial_memory, *, banks, capacity_rows,
+                        template_indices=None, state_dtype=torch.float32,
+                        growth_quantum_rows=0, map_page_slots=None, result=None):
+        """``allocate`` with the template check's result word left on the
+        device (``result``, int64, or a new one): the caller reads it."""
+
         if shared_initial_memory.ndim == 2:
             shared_initial_memory = shared_initial_memory.unsqueeze(0)
         if shared_initial_memory.ndim != 3:
@@ -350,7 +365,8 @@ class PackedSDMCopyOnWriteState:
                 int(nat.lib().cowsdm_step_scratch_words(banks)), device=device,
                 dtype=torch.int64),
         )
-        result = torch.empty(1, device=device, dtype=torch.int64)
+        if result is None:
+            result = torch.empty(1, device=device, dtype=torch.int64)
         nat.check(
             nat.lib().cowsdm_init_state(
                 state.logical_to_physical.data_ptr(), banks, slots,
@@ -360,12 +376,10 @@ class PackedSDMCopyOnWriteState:
                 result.data_ptr(), nat.stream_handle(device)),
             "cowsdm_init_state",
         )
-        if int(result.item()) & nat.ERR_TEMPLATE:
-            raise ValueError("template index lies outside shared initial memory")
         if map_page_slots is not None:
             state.paged_map = PagedSlotMap.empty(banks, slots, map_page_slots, device)
             state.logical_to_physical = _map_placeholder(banks, slots)
-        return state
+        return state, result
 
     @classmethod
     @torch.no_grad()
@@ -386,70 +400,131 @@ class PackedSDMCopyOnWriteState:
         (allocator.py:587-689).  With ``map_page_slots`` (not in the
         reference) the packed map is paged (``PagedSlotMap``)."""
 
-        if shared_initial_memory.ndim == 2:
-            shared_initial_memory = shared_initial_memory.unsqueeze(0)
-        if shared_initial_memory.ndim != 3 or dense_memory.ndim != 3:
-            raise ValueError("SDM handoff memory must be [H,N,D] and [B,N,D]")
-        banks, slots, width = dense_memory.shape
-        if (
-            active_slots.shape != (banks, slots)
-            or active_slots.dtype != torch.bool
-            or active_slots.device != dense_memory.device
-            or shared_initial_memory.device != dense_memory.device
-            or shared_initial_memory.shape[1:] != (slots, width)
-        ):
-            raise ValueError("SDM handoff state and active-slot mask do not align")
-        if (
-            template_indices.shape != (banks,)
-            or template_indices.device != dense_memory.device
-        ):
-            raise ValueError("SDM handoff template indices must be [B] on device")
-        _require_device(dense_memory, "SDM handoff memory")
-        device = dense_memory.device
-        dense = dense_memory.to(torch.float32).contiguous()
-        mask = active_slots.contiguous()
-        workspace = _workspace(banks * slots, 0, device)
-        total = torch.empty(1, device=device, dtype=torch.int64)
+        return cls.from_dense_overlay_layers(
+            [shared_initial_memory], [dense_memory], [active_slots],
+            template_indices=template_indices, capacity_rows=capacity_rows,
+            state_dtype=state_dtype, maximum_future_allocations=maximum_future_allocations,
+            growth_quantum_rows=growth_quantum_rows, map_page_slots=map_page_slots)[0]
+
+    @classmethod
+    @torch.no_grad()
+    def from_dense_overlay_layers(
+        cls,
+        shared_initial_memories: Sequence[torch.Tensor],
+        dense_memories: Sequence[torch.Tensor],
+        active_slots: Sequence[torch.Tensor],
+        *,
+        template_indices: torch.Tensor,
+        capacity_rows: int | None | Sequence[int | None] = None,
+        state_dtype: torch.dtype = torch.float32,
+        maximum_future_allocations: int | None = None,
+        growth_quantum_rows: int = 0,
+        map_page_slots: int | None = None,
+    ) -> list["PackedSDMCopyOnWriteState"]:
+        """``from_dense_overlay`` of several layers at once: the same states,
+        checks and errors, with one host read of every layer's active count
+        (which sizes the slabs) and one of every layer's invariant check
+        (allocator.py:639, 687), instead of two reads per layer.  The
+        arguments after the per-layer sequences apply to every layer
+        (``capacity_rows`` may also give one per layer).  No counterpart in
+        the reference."""
+
+        layers = len(dense_memories)
+        if isinstance(capacity_rows, (list, tuple)):
+            if len(capacity_rows) != layers:
+                raise ValueError("SDM capacities must contain one value per layer")
+            capacities = list(capacity_rows)
+        else:
+            capacities = [capacity_rows] * layers
+        if len(shared_initial_memories) != layers or len(active_slots) != layers:
+            raise ValueError("one initial memory, dense memory and active mask per layer")
+        prepared = []
+        for m0, dense_memory, active in zip(shared_initial_memories, dense_memories,
+                                           active_slots):
+            if m0.ndim == 2:
+                m0 = m0.unsqueeze(0)
+            if m0.ndim != 3 or dense_memory.ndim != 3:
+                raise ValueError("SDM handoff memory must be [H,N,D] and [B,N,D]")
+            banks, slots, width = dense_memory.shape
+            if (
+                active.shape != (banks, slots)
+                or active.dtype != torch.bool
+                or active.device != dense_memory.device
+                or m0.device != dense_memory.device
+                or m0.shape[1:] != (slots, width)
+            ):
+                raise ValueError("SDM handoff state and active-slot mask do not align")
+            if (
+                template_indices.shape != (banks,)
+                or template_indices.device != dense_memory.device
+            ):
+                raise ValueError("SDM handoff template indices must be [B] on device")
+            _require_device(dense_memory, "SDM handoff memory")
+            prepared.append((m0, dense_memory.to(torch.float32).contiguous(),
+                             active.contiguous()))
+        if not prepared:
+            return []
+        device = prepared[0][1].device
         stream = nat.stream_handle(device)
-        nat.check(
-            nat.lib().cowsdm_count_active(
-                None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
-                total.data_ptr(), stream),
-            "cowsdm_count_active",
-        )
-        active_count = int(total.item())
-        selected, possible = handoff_capacity(
-            active_count, banks, slots, capacity_rows, growth_quantum_rows,
-            maximum_future_allocations)
-        state = cls.allocate(
-            shared_initial_memory,
-            banks=banks,
-            capacity_rows=selected,
-            template_indices=template_indices,
-            state_dtype=state_dtype,
-            growth_quantum_rows=growth_quantum_rows,
-        )
-        workspace = _workspace(banks * slots, selected, device)
-        nat.check(
-            nat.lib().cowsdm_count_active(
-                None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
-                total.data_ptr(), stream),
-            "cowsdm_count_active",
-        )
-        nat.check(
-            nat.lib().cowsdm_pack_overlay(
-                dense.data_ptr(), mask.data_ptr(), banks, slots, width,
-                state.logical_to_physical.data_ptr(), state.values.data_ptr(),
-                state.free_rows.data_ptr(), selected, state.free_count.data_ptr(),
-                workspace.data_ptr(), stream),
-            "cowsdm_pack_overlay",
-        )
-        state.capacity_is_proven = maximum_future_allocations is not None
-        state.proven_maximum_additional_allocations = possible
-        state.validate_invariants()
+        # every layer's active count, read once; each workspace keeps the ranks
+        # its count leaves for the pack, with room for a slab of every slot
+        totals = torch.empty(layers, device=device, dtype=torch.int64)
+        workspaces = []
+        for (m0, dense, mask), total in zip(prepared, totals):
+            banks, slots, _ = dense.shape
+            rows = max(banks * slots, max((c for c in capacities if c is not None), default=0))
+            workspace = _workspace(banks * slots, rows, device)
+            workspaces.append((workspace, rows))
+            nat.check(
+                nat.lib().cowsdm_count_active(
+                    None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
+                    total.data_ptr(), stream),
+                "cowsdm_count_active",
+            )
+        counts = totals.tolist()
+        states = []
+        checks = torch.empty(layers, 9, device=device, dtype=torch.int64)
+        for l, ((m0, dense, mask), active_count) in enumerate(zip(prepared, counts)):
+            banks, slots, width = dense.shape
+            selected, possible = handoff_capacity(
+                active_count, banks, slots, capacities[l], growth_quantum_rows,
+                maximum_future_allocations)
+            state, _ = cls._allocate_state(
+                m0, banks=banks, capacity_rows=selected, template_indices=template_indices,
+                state_dtype=state_dtype, growth_quantum_rows=growth_quantum_rows,
+                result=checks[l, 8:])
+            workspace, rows = workspaces[l]
+            if rows < selected:
+                # a slab larger than the workspace's lists: count again into one
+                workspace = _workspace(banks * slots, selected, device)
+                total = torch.empty(1, device=device, dtype=torch.int64)
+                nat.check(
+                    nat.lib().cowsdm_count_active(
+                        None, banks, slots, None, banks, mask.data_ptr(),
+                        workspace.data_ptr(), total.data_ptr(), stream),
+                    "cowsdm_count_active",
+                )
+            nat.check(
+                nat.lib().cowsdm_pack_overlay(
+                    dense.data_ptr(), mask.data_ptr(), banks, slots, width,
+                    state.logical_to_physical.data_ptr(), state.values.data_ptr(),
+                    state.free_rows.data_ptr(), selected, state.free_count.data_ptr(),
+                    workspace.data_ptr(), stream),
+                "cowsdm_pack_overlay",
+            )
+            state.capacity_is_proven = maximum_future_allocations is not None
+            state.proven_maximum_additional_allocations = possible
+            state._launch_invariants(checks[l, :8])
+            states.append(state)
+        # the template checks and every layer's invariants, read once
+        for state, words in zip(states, checks.tolist()):
+            if words[8] & nat.ERR_TEMPLATE:
+                raise ValueError("template index lies outside shared initial memory")
+            state._judge_invariants(words[:8])
         if map_page_slots is not None:
-            state.to_paged_map(map_page_slots)
-        return state
+            for state in states:
+                state.to_paged_map(map_page_slots)
+        return states
 
     # ------------------------------------------------------- map forms
 
@@ -594,7 +669,7 @@ class PackedSDMCopyOnWriteState:
                 raise ValueError("SDM COW capacity has no decode proof")
             return 0
         if self.proven_maximum_additional_allocations < maximum_new_rows:
-            free_rows = int(self.free_count.item())
+            free_rows = self._read_free_count()
             if free_rows < maximum_new_rows:
                 self.grow_capacity(self.capacity_rows + maximum_new_rows - free_rows)
                 free_rows = int(self.free_count.item())
@@ -628,7 +703,13 @@ class PackedSDMCopyOnWriteState:
             if free_counts is not None:
                 frees = [int(free_counts[i]) for i in picks]
             else:
-                frees = torch.stack([st.free_count for st in short]).tolist()
+                # the free counts and the kernels' error words in one read
+                words = torch.stack([st.free_count.to(torch.int64) for st in short]
+                                    + [st.ensure_scratch()[nat.SCRATCH_ERRORS] for st in short])
+                words = words.tolist()
+                frees = words[:len(short)]
+                for st, errors in zip(short, words[len(short):]):
+                    st._raise_on_fault(errors)
             for st, free_rows in zip(short, frees):
                 if free_rows < maximum_new_rows:
                     free_rows += st.grow_capacity(
@@ -645,6 +726,23 @@ class PackedSDMCopyOnWriteState:
             st.capacity_is_proven = True
             capacities.append(st.capacity_rows)
         return capacities
+
+    def _read_free_count(self) -> int:
+        """free_count, read with the kernels' sticky error word (one
+        transfer); raises when a step stopped on a fault."""
+
+        words = torch.stack([self.free_count.to(torch.int64),
+                             self.ensure_scratch()[nat.SCRATCH_ERRORS]]).tolist()
+        self._raise_on_fault(words[1])
+        return int(words[0])
+
+    @staticmethod
+    def _raise_on_fault(errors: int) -> None:
+        # a bounded wait that gave up, or state found outside the slab: the
+        # step left the state inconsistent (the bits latch until cleared)
+        if errors & (nat.ERR_LOOKBACK | nat.ERR_CORRUPT):
+            raise RuntimeError(f"an SDM COW step stopped on a fault (error word {errors:#x}): "
+                               "a bounded wait timed out or the state is corrupt")
 
     # -------------------------------------------------------- lifecycle
 
@@ -935,12 +1033,31 @@ class PackedSDMCopyOnWriteState:
         (allocator.py:1069-1095); also surfaces the kernels' sticky error
         word."""
 
+        stats = torch.empty(8, device=self.values.device, dtype=torch.int64)
+        self._launch_invariants(stats)
+        return self._judge_invariants(stats.tolist())
+
+    @staticmethod
+    @torch.no_grad()
+    def validate_invariants_layers(states: Sequence["PackedSDMCopyOnWriteState"]) -> list[dict]:
+        """``validate_invariants`` of every state with one device-to-host
+        read for all of them.  No counterpart in the reference."""
+
+        if not states:
+            return []
+        stats = torch.empty(len(states), 8, device=states[0].values.device, dtype=torch.int64)
+        for st, row in zip(states, stats):
+            st._launch_invariants(row)
+        return [st._judge_invariants(row) for st, row in zip(states, stats.tolist())]
+
+    def _launch_invariants(self, stats: torch.Tensor) -> None:
+        """Enqueue the invariant counts (8 int64 words) into ``stats``."""
+
         if self.paged_map is not None:
             with self._direct_form(keep=False):
-                return self.validate_invariants()
+                return self._launch_invariants(stats)
         device = self.values.device
         workspace = _workspace(self.banks * self.slots, self.capacity_rows, device)
-        stats = torch.empty(8, device=device, dtype=torch.int64)
         nat.check(
             nat.lib().cowsdm_check_invariants(
                 self.logical_to_physical.data_ptr(), self.banks, self.slots,
@@ -949,8 +1066,12 @@ class PackedSDMCopyOnWriteState:
                 workspace.data_ptr(), stats.data_ptr(), nat.stream_handle(device)),
             "cowsdm_check_invariants",
         )
+
+    def _judge_invariants(self, stats: Sequence[int]) -> dict[str, Any]:
+        """The reference's assertions (allocator.py:1077-1089) on the counts."""
+
         (live, free, dup_live, dup_free, not_once, outside, overflow, errors) = (
-            int(x) for x in stats.tolist())
+            int(x) for x in stats)
         if overflow != 0:
             raise AssertionError("SDM COW allocator recorded a slab overflow")
         if errors != 0:

@@ -308,6 +308,51 @@ def pack_prefill_layer(
 
 
 @torch.no_grad()
+def pack_prefill_layers(
+    initial_memories: Sequence[torch.Tensor],
+    final_memories: Sequence[torch.Tensor],
+    write_indices: Sequence[torch.Tensor],
+    *,
+    capacity_rows: int | None | Sequence[int | None],
+    decode_capacity: int,
+    growth_quantum_rows: int,
+) -> list[PackedSDMCopyOnWriteState]:
+    """``pack_prefill_layer`` for every SDM layer of a stack at once: the
+    same states, with the host reads of the handoff made once for all
+    layers (``from_dense_overlay_layers``).  No counterpart in the
+    reference (which packs layer by layer, inference.py:314-366)."""
+
+    masks, finals, templates, shapes = [], [], None, None
+    for initial_memory, final_memory, indices in zip(initial_memories, final_memories,
+                                                     write_indices):
+        batch, time, heads, writes = indices.shape
+        if initial_memory.ndim != 3 or final_memory.shape != (
+                batch, heads, initial_memory.shape[1], initial_memory.shape[2]):
+            raise ValueError("SDM prefill routing does not match its controller")
+        slots = initial_memory.shape[1]
+        active = torch.zeros(batch * heads, slots, device=indices.device, dtype=torch.bool)
+        mark_written(active, indices.permute(0, 2, 1, 3).reshape(batch * heads,
+                                                                 time * writes))
+        masks.append(active)
+        finals.append(final_memory.flatten(0, 1))
+        if shapes is None:
+            shapes = (batch, time, heads, writes)
+            templates = torch.arange(heads, device=active.device,
+                                     dtype=torch.int64).repeat(batch)
+        elif shapes != (batch, time, heads, writes):
+            raise ValueError("the SDM layers of one stack share batch, prefix and heads")
+    if shapes is None:
+        return []
+    batch, time, heads, writes = shapes
+    return PackedSDMCopyOnWriteState.from_dense_overlay_layers(
+        list(initial_memories), finals, masks, template_indices=templates,
+        capacity_rows=capacity_rows, state_dtype=torch.float32,
+        maximum_future_allocations=(
+            None if growth_quantum_rows else batch * heads * writes * (decode_capacity - time)),
+        growth_quantum_rows=growth_quantum_rows)
+
+
+@torch.no_grad()
 def decode_sdm_layer(state: PackedSDMCopyOnWriteState, step: SDMStepInputs, *,
                      backend: str = "auto") -> torch.Tensor:
     """Packed decode of one SDM layer for one token (inference.py:538-566):

@@ -23,7 +23,7 @@ from typing import Callable, Sequence
 import torch
 
 from .controller import SDMController, finish_sdm_step, prepare_sdm_step
-from .inference import FaithfulSDMDecodeState, pack_prefill_layer
+from .inference import FaithfulSDMDecodeState, pack_prefill_layers
 from .recurrence import dense_sparse_routes, gated_delta_recurrence
 
 
@@ -134,9 +134,11 @@ def prefill_faithful_sdm_stack(
 ) -> tuple[torch.Tensor, FaithfulSDMDecodeState]:
     """``prefill_faithful_sdm_stack`` (inference.py:369-456) with the SDM
     layers on the device: every "B" layer of ``layout`` runs
-    ``prefill_sdm_layer`` on the tokens entering it, adds its output and
-    hands its final memory to copy-on-write state (``pack_prefill_layer``);
-    the model's other parts stay the caller's:
+    ``prefill_sdm_layer`` on the tokens entering it and adds its output;
+    every layer's final memory is then handed to copy-on-write state
+    (``pack_prefill_layers``: the reference's per-layer handoff with the
+    host reads made once for all layers); the model's other parts stay the
+    caller's:
 
     * ``attention_block(layer, tokens) -> (tokens, key, value)`` for an "A"
       layer: the block's residual stream after it, and the prefix's keys and
@@ -177,7 +179,7 @@ def prefill_faithful_sdm_stack(
 
     keys: list[torch.Tensor] = []
     values: list[torch.Tensor] = []
-    states = []
+    handoffs = []   # (initial memory, final memory, write routes) per SDM layer
     sdm_index = 0
     for layer, kind in enumerate(layout):
         if kind == "A":
@@ -191,12 +193,16 @@ def prefill_faithful_sdm_stack(
         tokens = tokens + pre.output
         if sdm_tail is not None:
             tokens = sdm_tail(layer, tokens)
-        states.append(pack_prefill_layer(
-            initial_memory, pre.final_memory, pre.write_indices,
-            capacity_rows=per_layer[sdm_index], decode_capacity=selected_capacity,
-            growth_quantum_rows=sdm_growth_quantum_rows))
+        handoffs.append((initial_memory, pre.final_memory, pre.write_indices))
         del pre
         sdm_index += 1
+    # every SDM layer's handoff (_pack_prefill_layer, inference.py:314-366)
+    # at once: the handoff's host reads are made once for all layers
+    states = pack_prefill_layers(
+        [h[0] for h in handoffs], [h[1] for h in handoffs], [h[2] for h in handoffs],
+        capacity_rows=list(per_layer), decode_capacity=selected_capacity,
+        growth_quantum_rows=sdm_growth_quantum_rows)
+    del handoffs
     return tokens, FaithfulSDMDecodeState(
         layout=layout, position=time, capacity=selected_capacity, activation_dtype=tokens.dtype,
         active_sequences=torch.ones(batch, device=tokens.device, dtype=torch.bool),

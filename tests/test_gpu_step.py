@@ -13,6 +13,7 @@ import pytest
 import torch
 
 import copy_on_write_sdm_amd as cow
+from copy_on_write_sdm_amd import _native as nat
 import reference_cases as rc
 from gpu_helpers import assert_state_equal, make_case, to_device, to_numpy
 from oracle import state as ref
@@ -264,3 +265,26 @@ def test_zipf_routes_large_address_space(device):
 
     _trace(device, banks=8, slots=65536, width=128, writes=4, reads=16, steps=8, seed=77,
            distribution="zipf", capacity=1024)
+
+
+def test_fault_bits_raise_at_the_proofs_read(device):
+    """A step whose bounded wait gave up (or that found the state corrupt)
+    latches COWSDM_ERR_LOOKBACK / _CORRUPT; the next read the decode loop
+    makes anyway (the proof's free-count read, single and batched) raises.
+    The fault is set from the host: no kernel is made to stop."""
+
+    initial, _ = rc.reference_case(1)
+    state = cow.PackedSDMCopyOnWriteState.allocate(initial.to(device), banks=rc.BANKS,
+                                                   capacity_rows=8, growth_quantum_rows=8)
+    state.prepare_step_capacity(4)       # a clean word: the proof reads and passes
+    for bit in (nat.ERR_LOOKBACK, nat.ERR_CORRUPT):
+        state.ensure_scratch()[nat.SCRATCH_ERRORS] = bit
+        state.proven_maximum_additional_allocations = 0
+        with pytest.raises(RuntimeError, match="stopped on a fault"):
+            state.prepare_step_capacity(4)
+        with pytest.raises(RuntimeError, match="stopped on a fault"):
+            cow.PackedSDMCopyOnWriteState.prepare_step_capacity_layers([state], 4)
+    # a route error alone (the bank was skipped) does not stop the loop
+    state.ensure_scratch()[nat.SCRATCH_ERRORS] = nat.ERR_WRITE_INDEX
+    state.proven_maximum_additional_allocations = 0
+    state.prepare_step_capacity(4)
