@@ -547,14 +547,16 @@ def main() -> int:
     # growth decided on the device (DecodeTrace.capture(1)), no host work
     graph_step = None
     if eager_steps:
-        n = min(max(eager_steps, 2 * K), total_steps)
+        # untimed replays first (as many as the recorded routes leave after
+        # the timed ones, at most 64): the first replays of a graph run
+        # slower (tens of microseconds) than the steady state
+        timed = min(max(eager_steps, 2 * K), total_steps // 2)
+        warm = min(64, total_steps - timed)
+        n = warm + timed
         gtrace = cow.DecodeTrace(states=states, max_steps_per_launch=1, **inputs)
         gtrace.reserve_steps(n)
         gtrace.set_step(0)
         graph = gtrace.capture(1)
-        # untimed replays first: the first replays of a graph run slower
-        # (tens of microseconds) than the steady state
-        warm = min(16, n // 4)
         for _ in range(warm):
             graph.replay()
         torch.cuda.synchronize()
@@ -619,18 +621,19 @@ def main() -> int:
     controller_graph = None
     if eager_steps:
         n = max(eager_steps, 2 * K)
+        warm = 16       # untimed replays, as for graph_step
         dec = cow.ControllerDecodeGraph(ctls, states, B)
-        dec.reserve_tokens(n + 2)
+        dec.reserve_tokens(n + warm)
         dec.capture()
-        toks = torch.randn(n + 2, B, 1, width_model, device=dev,
+        toks = torch.randn(n + warm, B, 1, width_model, device=dev,
                            generator=torch.Generator(device=dev).manual_seed(args.seed + 7))
-        for s in range(2):
+        for s in range(warm):
             dec(toks[s])
         torch.cuda.synchronize()
         g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         g0.record()
-        for s in range(2, n + 2):
+        for s in range(warm, n + warm):
             dec(toks[s])
         g1.record()
         torch.cuda.synchronize()
@@ -644,6 +647,7 @@ def main() -> int:
             "us_per_step": round(1e6 * wall / n, 3),
             "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / n, 3),
             "steps": n,
+            "warmup_replays": warm,
             "what": "hipGraph per token of every layer's controller prepare, two route "
                     "selections, capacity proof and growth on the device, packed step, "
                     "controller finish and residual add (ControllerDecodeGraph)",
