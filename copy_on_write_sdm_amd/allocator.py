@@ -1871,6 +1871,9 @@ class DecodeTrace:
         if steps < 1:
             raise ValueError("a captured launch runs at least one step")
         layers = self.layer_array()
+        if not self.dense and any(t.paged_map is not None for t in self.tables):
+            raise RuntimeError("a paged slot map takes its page proof on the host: decode it "
+                               "with run(), not captured launches")
         if not self.dense and not self.planned:
             raise RuntimeError("packed state needs persistent launches to decide its proof "
                                "on the device")
@@ -1913,6 +1916,9 @@ class DecodeTrace:
                 self.trace.step_index = self.step_index.data_ptr()
                 self.trace.first_step = 0
             return
+        if not self.dense and any(t.paged_map is not None for t in self.tables):
+            raise RuntimeError("a paged slot map takes its page proof on the host: decode it "
+                               "with run(), not device-counted launches")
         layers = self.layer_array() if layers is None else layers
         stream = nat.stream_handle(self.device)
         self._positions = None

@@ -86,6 +86,12 @@ def test_paged_decode_matches_direct_config5(device, page_slots):
     want = _decode([direct], more, 8)
     assert torch.equal(out, want)
     assert_states_identical(paged, direct)
+    # device-counted launches would skip the host's page proof: refused
+    tr.set_step(0)
+    with pytest.raises(RuntimeError, match="page proof"):
+        tr.launch(1)
+    with pytest.raises(RuntimeError, match="page proof"):
+        tr.capture(1)
 
 
 def test_paged_lifecycle_matches_direct(device):
