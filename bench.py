@@ -411,7 +411,14 @@ def main() -> int:
         return span.value, kernel.value, count.value
 
     def live_rows(trace) -> int:
-        return 0 if trace.dense else sum(int(st.allocated_rows_tensor()) for st in trace.tables)
+        # between repetitions from the last run's report in host memory: a
+        # device read here would put copies on the stream before the next
+        # timed launch
+        if trace.dense:
+            return 0
+        rows = trace.reported_live_rows()
+        return rows if rows is not None else sum(int(st.allocated_rows_tensor())
+                                                 for st in trace.tables)
 
     def measure(trace):
         """`repeats` wall-clock repetitions of K steps with the library's

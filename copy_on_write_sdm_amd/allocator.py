@@ -1628,6 +1628,8 @@ class DecodeTrace:
         self._counters_seen = [(0, 0, 0)] * layers
         self._status_clean = False      # every status word is known to be zero
         self._host_report = None        # nat.HostReport, made by the first run
+        self._report_versions = None    # the states' versions the host report matches
+        self._step_index_ptr = self.step_index.data_ptr()
         self.ticket = torch.zeros(1 + layers, dtype=torch.int64, device=device)
         self.banks, self.writes = banks, write_indices.shape[3]
         self.trace = nat.Trace()
@@ -1787,41 +1789,79 @@ class DecodeTrace:
         self._counters_seen = [(0, 0, 0)] * len(self.tables)
         self._synced_versions = versions
 
-    def _absorb(self, per_layer) -> None:
+    def _absorb(self, per_layer, offset: int = 0, before: tuple | None = None) -> None:
         """Take the control words read back after launches (per layer, word
-        k of layer l at per_layer[l][k]) into the states: proof counter,
-        capacity (grown within the buffers) and the growth the launches added
-        since the last read (the device counters run from the last upload)."""
+        k of layer l at per_layer[l][offset + k]) into the states: proof
+        counter, capacity (grown within the buffers) and the growth the
+        launches added since the last read (the device counters run from the
+        last upload).  ``before``: the states' versions, when the caller has
+        them."""
 
-        before = self._versions()
+        tables = self.tables
+        if before is None:
+            before = self._versions()
         moved = False
-        proven_k, capacity_k = nat.CTRL_PROVEN, nat.CTRL_CAPACITY
-        events_k, added_k, copied_k = nat.CTRL_EVENTS, nat.CTRL_ADDED, nat.CTRL_COPIED
+        proven_k, capacity_k = offset + nat.CTRL_PROVEN, offset + nat.CTRL_CAPACITY
+        events_k, added_k = offset + nat.CTRL_EVENTS, offset + nat.CTRL_ADDED
+        copied_k = offset + nat.CTRL_COPIED
         # the slab lengths the layer structs were built from, while no state
         # changed since (a tensor's shape costs more than the whole check)
         known = self._capacities if self._layers_versions == before else None
         seen_all = self._counters_seen
-        for l, (st, words) in enumerate(zip(self.tables, per_layer)):
-            st.proven_maximum_additional_allocations = words[proven_k]
+        after = []
+        for l, st in enumerate(tables):
+            words = per_layer[l]
+            d = st.__dict__
+            proven = words[proven_k]
+            if d["proven_maximum_additional_allocations"] != proven:
+                # the assignment with its version count (__setattr__), inline
+                d["proven_maximum_additional_allocations"] = proven
+                d["_version"] = d["_version"] + 1
             capacity = words[capacity_k]
             if capacity != (known[l] if known is not None else st.values.shape[0]):
                 vbuf, fbuf = st.slab_buffers
                 st.values, st.free_rows = vbuf[:capacity], fbuf[:capacity]
-                moved = True
+                struct = self._layers[1][l] if known is not None else None
+                if (struct is not None and struct.values == vbuf.data_ptr()
+                        and struct.free_rows == fbuf.data_ptr()):
+                    # grown within the buffers the layer struct points at:
+                    # only its length changes
+                    struct.capacity_rows = capacity
+                    known[l] = capacity
+                else:
+                    moved = True
             seen = seen_all[l]
             if words[events_k] != seen[0] or words[added_k] != seen[1] or words[copied_k] != seen[2]:
                 st.growth_events += words[events_k] - seen[0]
                 st.growth_rows_added += words[added_k] - seen[1]
                 st.growth_rows_copied += words[copied_k] - seen[2]
                 seen_all[l] = (words[events_k], words[added_k], words[copied_k])
-            if not st.capacity_is_proven and st.growth_quantum_rows > 0:
+            if not d["capacity_is_proven"] and d["growth_quantum_rows"] > 0:
                 st.capacity_is_proven = True
+            after.append(d["_version"])
         # what matched the states before still matches them, except the
         # layer structs after a capacity grew
-        after = self._versions()
+        after = tuple(after)
         if not moved and self._layers_versions == before:
             self._layers_versions = after
+            key, structs, _ = self._layers
+            self._layers = (key, structs, tuple(self._capacities))
         self._synced_versions = after if self._synced_versions == before else None
+
+    def reported_live_rows(self) -> int | None:
+        """The packed layers' live physical rows (capacity minus free count,
+        allocator.py:960-963, summed) as the last ``run`` of this trace left
+        them, from its report in host memory (no device read); None when
+        there is no such report or this trace's states changed since.  Work
+        enqueued on the states by other means (another trace's launches, a
+        lifecycle call) after the run is not seen."""
+
+        if (self.dense or self._report_versions is None or self._positions is None
+                or self._report_versions != self._versions()):
+            return None
+        a = self._host_report.array
+        base = nat.REPORT_CONTROL
+        return int((a[:, base + nat.CTRL_CAPACITY] - a[:, base + nat.CTRL_FREE]).sum())
 
     def sync(self) -> None:
         """Read the control words back into the states after ``launch``
@@ -1973,7 +2013,7 @@ class DecodeTrace:
             return {"launches": 0, "growth_rounds": 0}
         positions = self._positions if self._positions is not None else self.step_index.tolist()
         start = positions[0]
-        if any(p != start for p in positions):
+        if positions.count(start) != len(positions):
             raise ValueError("decode trace layers stand at different steps")
         target = start + steps
         if target > self.steps:
@@ -1985,15 +2025,17 @@ class DecodeTrace:
         layers = self._layers[1] if fresh else self.layer_array()
         if not self.dense and not self.planned:
             return self._run_stepwise(start, steps, timing)
-        saved = self.trace.steps_recorded
-        self.trace.steps_recorded = target
-        self.trace.step_index = self.step_index.data_ptr()
-        self.trace.first_step = 0
+        trace = self.trace
+        saved = trace.steps_recorded
+        trace.steps_recorded = target
+        trace.step_index = self._step_index_ptr
+        trace.first_step = 0
         if not self._status_clean:
             self.status.zero_()
         self._status_clean = False
         if not fresh:
             self.upload(force=False)
+            versions = self._versions()
         stream = nat.stream_handle(self.device)
         native = timing is None and (self.dense or self.planned) and self.persistent
         if native and self._host_report is None:
@@ -2003,23 +2045,27 @@ class DecodeTrace:
         launches = rounds = 0
         remaining = steps
         self._positions = None
+        self._report_versions = None
         try:
             while True:
                 count = -(-remaining // launch_steps)
                 if native:
                     # launches, then the layers' reports straight from host
                     # memory the last wave of each layer wrote
-                    self.trace.report = self._host_report.device
+                    trace.report = self._host_report.device
                     try:
-                        nat.check(nat.lib().cowsdm_trace_run(
-                            layers, len(self.tables), self.shape, self.trace, remaining,
-                            launch_steps, mode, stream), "decode trace run")
+                        rc = nat.lib().cowsdm_trace_run(
+                            layers, len(self.tables), self.shape, trace, remaining,
+                            launch_steps, mode, stream)
                     finally:
-                        self.trace.report = None
-                    report = self._host_report.array
-                    positions = report[:, nat.REPORT_STEP].tolist()
-                    status = report[:, nat.REPORT_STATUS].tolist()
-                    control = None if self.dense else report[:, nat.REPORT_CONTROL:].tolist()
+                        trace.report = None
+                    if rc:
+                        nat.check(rc, "decode trace run")
+                    rows = self._host_report.array.tolist()
+                    positions = [r[nat.REPORT_STEP] for r in rows]
+                    status = [r[nat.REPORT_STATUS] for r in rows]
+                    control = None if self.dense else rows
+                    offset = nat.REPORT_CONTROL
                 else:
                     for _ in range(count):
                         if timing is not None:
@@ -2037,9 +2083,10 @@ class DecodeTrace:
                     status = [(words[l // 2] >> (32 * (l % 2))) & 0xFFFFFFFF
                               for l in range(len(self.tables))]
                     control = None if self.dense else [list(w) for w in zip(*rows[2:])]
+                    offset = 0
                 launches += count
                 if control is not None:
-                    self._absorb(control)
+                    self._absorb(control, offset, versions if rounds == 0 else None)
                 if any(status):
                     faults = [l for l, s in enumerate(status) if s & nat.TRACE_FAULT]
                     if faults:
@@ -2059,7 +2106,7 @@ class DecodeTrace:
                 grown = [self.tables[l] for l in refused]
                 PackedSDMCopyOnWriteState.prepare_step_capacity_layers(
                     grown, self.need(),
-                    free_counts=[control[l][nat.CTRL_FREE] for l in refused])
+                    free_counts=[control[l][offset + nat.CTRL_FREE] for l in refused])
                 for st in grown:
                     st.proven_maximum_additional_allocations += self.need()
                 self.status.zero_()
@@ -2068,8 +2115,10 @@ class DecodeTrace:
                 remaining = target - min(positions)
                 rounds += 1
         finally:
-            self.trace.steps_recorded = saved
+            trace.steps_recorded = saved
         self._positions = [target] * len(self.tables)
+        if native and rounds == 0 and not self.dense:
+            self._report_versions = self._synced_versions
         return {"launches": launches, "growth_rounds": rounds}
 
     def _run_stepwise(self, start: int, steps: int, timing: list | None) -> dict:

@@ -398,12 +398,17 @@ def test_decode_loop_grows_on_device_with_reserved_room(device, launch_steps):
     tr.reserve_steps(steps)
     report = tr.run(steps, launch_steps=launch_steps)
     assert report == {"launches": -(-steps // launch_steps), "growth_rounds": 0}
+    # the live rows of the run's host report equal the device's
+    assert tr.reported_live_rows() == sum(int(st.allocated_rows_tensor()) for st in states)
     want = oracle_decode_loop(oracles, routes, steps, need=banks * 4)
     assert np.array_equal(outputs.cpu().numpy(), want)
     for st, orc in zip(states, oracles):
         assert st.growth_events > 3
         assert_state_equal(st, orc)
         st.validate_invariants()
+    # an assignment to a state since the run: the report no longer speaks for it
+    states[0].capacity_is_proven = states[0].capacity_is_proven
+    assert tr.reported_live_rows() is None
 
 
 def test_graph_replay_grows_on_device(device):
