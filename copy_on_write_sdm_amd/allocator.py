@@ -12,8 +12,14 @@ Differences from the reference, all deliberate:
 * Physical rows for first touches are popped in bank-major order on every
   backend, so the map, slab and free stack match the reference's torch path
   (allocator.py:1471-1481) exactly instead of up to a permutation.
-* ``backend`` accepts "auto" and "hip".  "triton" raises the reference's
-  unavailable-backend error; "torch" raises too: no CPU path ships.
+* ``backend`` accepts "auto", "hip" and "torch"; all three run the HIP
+  kernels on device tensors (no CPU path ships, so CPU tensors raise).
+  "torch" asks for the reference torch path's semantics: its results
+  (bank-major pops, the same rows and counts; float sums within 1e-6 of
+  torch's reduction order) and its exhaustion check before every step, which
+  the reference asserts on the device (allocator.py:1474) and this build
+  raises as ValueError after one synchronisation.  "triton" raises the
+  reference's unavailable-backend error.
 * Value state, route weights, values and gates are float32.
 * The state carries one more tensor, ``scratch`` (int64 [8 + B]), holding the
   bank-order scan slots, a ticket counter and a sticky error word.
@@ -1125,20 +1131,19 @@ def _validate_gates(input_gate, erase_gate, forget_log_gate, *, banks: int) -> N
         raise ValueError("SDM input, erase, and forget gates must align")
 
 
-def _select_backend(backend: str, *, tensor: torch.Tensor, writes: int, reads: int) -> None:
-    """Backend dispatch (allocator.py:1158-1176): only the HIP kernels ship."""
+def _select_backend(backend: str, *, tensor: torch.Tensor, writes: int, reads: int) -> bool:
+    """Backend dispatch (allocator.py:1158-1176): the HIP kernels run every
+    backend but "triton"; True for "torch", whose exhaustion check runs
+    before every step (allocator.py:1474)."""
 
     if backend not in ("auto", "torch", "triton", "hip"):
         raise ValueError("allocator backend must be auto, hip, torch, or triton")
     if backend == "triton":
         raise RuntimeError("the requested Triton SDM COW backend is unavailable")
-    if backend == "torch":
-        raise RuntimeError(
-            "the torch SDM COW backend is not shipped: the HIP kernels are the "
-            "only implementation")
     _require_device(tensor, "SDM COW step tensors")
     if writes > 64 or reads > 256:
         raise ValueError("HIP SDM COW step supports at most 64 writes and 256 reads")
+    return backend == "torch"
 
 
 def _check_float_tensors(tensors: Sequence[torch.Tensor]) -> None:
@@ -1306,8 +1311,8 @@ def packed_sdm_cow_step(
     effective_erase = _check_step_inputs(
         banks, slots, width, device, write_indices, write_weights, values, input_gate,
         forget_log_gate, read_indices, read_weights, erase_gate, dense=False)
-    _select_backend(backend, tensor=state.values, writes=write_indices.shape[1],
-                    reads=read_indices.shape[1])
+    torch_checks = _select_backend(backend, tensor=state.values,
+                                   writes=write_indices.shape[1], reads=read_indices.shape[1])
     _check_float_tensors((write_weights, values, input_gate, effective_erase,
                           forget_log_gate, read_weights))
     index_code = _index_code(write_indices, read_indices)
@@ -1324,9 +1329,9 @@ def packed_sdm_cow_step(
                         first, repeated, allocated)
     shape = _shape(banks, slots, width, write_indices.shape[1], read_indices.shape[1],
                    state.shared_initial_memory.shape[0], index_code)
-    if banks and (validate_routes or not state.capacity_is_proven):
+    if banks and (validate_routes or torch_checks or not state.capacity_is_proven):
         _run_precheck(layer, shape, dense=False, unique=validate_routes,
-                      capacity=not state.capacity_is_proven, device=device)
+                      capacity=torch_checks or not state.capacity_is_proven, device=device)
     if banks:
         nat.check(nat.lib().cowsdm_packed_step(layer, shape, nat.stream_handle(device)),
                   "cowsdm_packed_step")

@@ -794,6 +794,54 @@ void sdm_trace_kernel(StepParams P) {
       DENSE ? nullptr : L.shared_initial_memory + tmpl * static_cast<int64_t>(N) * D;
   int32_t* const map_bank = DENSE ? nullptr : L.logical_to_physical + static_cast<int64_t>(bank) * N;
   int* const lds_map = MAPLDS ? lds_map_all + pair * N : nullptr;
+  const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
+  const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
+  const uint32_t st_wi = pin(static_cast<uint32_t>(P.trace_stride[0]));
+  const uint32_t st_ri = pin(static_cast<uint32_t>(P.trace_stride[6]));
+  const char* const wbase = first_step(L.write_indices, 0) + static_cast<int64_t>(bank) * W * sizeof(IDX);
+  const char* const rbase = first_step(L.read_indices, 6) + static_cast<int64_t>(bank) * R * sizeof(IDX);
+  // packed, slot map in LDS: the slots of the launch's first chunks, for the
+  // plan's count part, are loaded before anything else (their round trip
+  // overlaps the slot map's); chunk 0's then serve the steps too.  The
+  // slots of chunks c + 1 .. c + kAhead load while chunk c is counted.
+  constexpr int kAhead = sizeof(IDX) == 4 ? 2 : 1;
+  IDX sbuf[kAhead + 1][kIdxRow];
+  auto load_slots = [&](int c, IDX (&dst)[kIdxRow]) __attribute__((always_inline)) {
+    const int t = c * kWave + lane;
+    const int tc = t < G0 ? t : G0 - 1;
+    const char* const w = at(wbase, st_wi, tc);
+    const char* const r = at(rbase, st_ri, tc);
+    if constexpr (FULL && sizeof(IDX) == 4) {
+      // a step's 4 write and 16 read slots are 16 and 64 contiguous,
+      // 16-byte aligned bytes: five vector loads per lane
+      const i32x4_t a = *(const __attribute__((address_space(1))) i32x4_t*)(w);
+      dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
+#pragma unroll
+      for (int k = 0; k < kTraceMaxReads / 4; ++k) {
+        const i32x4_t b = *(const __attribute__((address_space(1))) i32x4_t*)(r + 16 * k);
+        dst[kTraceMaxWrites + 4 * k] = b.x;
+        dst[kTraceMaxWrites + 4 * k + 1] = b.y;
+        dst[kTraceMaxWrites + 4 * k + 2] = b.z;
+        dst[kTraceMaxWrites + 4 * k + 3] = b.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kTraceMaxWrites; ++j) {
+        dst[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : W - 1) * sizeof(IDX));
+      }
+#pragma unroll
+      for (int i = 0; i < kTraceMaxReads; ++i) {
+        dst[kTraceMaxWrites + i] =
+            *(const __attribute__((address_space(1))) IDX*)(r + (i < R ? i : R - 1) * sizeof(IDX));
+      }
+    }
+  };
+  if constexpr (!DENSE && MAPLDS) {
+#pragma unroll
+    for (int c = 0; c < kAhead; ++c) {
+      if (c * kWave < G0) load_slots(c, sbuf[c]);
+    }
+  }
   bool any_bad = false;  // a map entry outside the slab (checked per chunk only then)
   if constexpr (MAPLDS) {
     // the bank's slot map into LDS, 4 loads in flight per lane (one memory
@@ -822,6 +870,11 @@ void sdm_trace_kernel(StepParams P) {
   int fit_rows = 0;
   int found_top = 0;      // the stack height the launch found
   int plan_segs = 1;      // growth segments of the launch (1: none)
+  // the launch's plan was made by this wave alone (plan_local): its plan
+  // words are in LDS, its pops come straight from the found stack, and the
+  // layer's last control wave writes what the launch leaves
+  bool local_plan = false;
+  int64_t local_proven = 0;
   if constexpr (!DENSE) {
     pb = plan_block(P, layer_id);
     // the epoch word changes only when the layer's last control wave ends
@@ -835,6 +888,7 @@ void sdm_trace_kernel(StepParams P) {
   auto stage_plan = [&]() __attribute__((always_inline)) -> bool {
     bool ok = true;
     if constexpr (!DENSE) {
+      if (local_plan) return true;   // staged by the local plan
       constexpr int KC = kTraceMaxSteps / kWave;
       uint64_t w[KC], c[KC];
 #pragma unroll
@@ -908,10 +962,6 @@ void sdm_trace_kernel(StepParams P) {
   };
 
   // ---- this lane's slots at the launch's first step; step t adds t * stride
-  const char* const wi_l = first_step(L.write_indices, 0) + (static_cast<int64_t>(bank) * W + wl) * sizeof(IDX);
-  const char* const ri_l = first_step(L.read_indices, 6) + (static_cast<int64_t>(bank) * R + rl_) * sizeof(IDX);
-  const uint32_t st_wi = pin(static_cast<uint32_t>(P.trace_stride[0]));
-  const uint32_t st_ri = pin(static_cast<uint32_t>(P.trace_stride[6]));
 
   // ---- stages
   auto load_idx = [&](int t, TraceIdx& m) __attribute__((always_inline)) {
@@ -931,8 +981,6 @@ void sdm_trace_kernel(StepParams P) {
   // vector memory is waited on once per 64 steps instead of every step (it
   // completes in order, so a per-step wait would also wait for every claim
   // and device-scope store issued before it).
-  const char* const wbase = first_step(L.write_indices, 0) + static_cast<int64_t>(bank) * W * sizeof(IDX);
-  const char* const rbase = first_step(L.read_indices, 6) + static_cast<int64_t>(bank) * R * sizeof(IDX);
   IDX chunk[kIdxRow];
 #pragma unroll
   for (int k = 0; k < kIdxRow; ++k) chunk[k] = 0;
@@ -1303,13 +1351,19 @@ void sdm_trace_kernel(StepParams P) {
   // the step is classified, and the row is used two iterations later, when
   // the step resolves.  A step whose pops reach past the rows the plan could
   // give out (a capacity proof that was missing or not honest) overflows: it
-  // takes none, and the bank stops.
+  // takes none, and the bank stops.  After a local plan (no growth) pop q is
+  // the found stack's entry found_top - 1 - q, loaded from the stack itself.
   auto claim = [&](const TraceRoute& rt, uint64_t& home) __attribute__((always_inline)) {
     if constexpr (!DENSE) {
       const int count = route_count(rt.u);
       if (count > 0 && route_ok(rt.u) && rt.base + count <= fit_rows) {
         const bool first = lane < kTraceMaxWrites && ((route_fmask(rt.u) >> lane) & 1u);
-        if (first) home = atomic_load_u64(pb.pops + rt.base + rt.rank);
+        if (first) {
+          home = local_plan
+                     ? static_cast<uint64_t>(static_cast<uint32_t>(
+                           L.free_rows[found_top - 1 - (rt.base + rt.rank)]))
+                     : atomic_load_u64(pb.pops + rt.base + rt.rank);
+        }
       }
     }
   };
@@ -1325,7 +1379,7 @@ void sdm_trace_kernel(StepParams P) {
       bool fits = rt.base + count <= fit_rows;
       if (fits) {
         const bool first = lane < kTraceMaxWrites && ((fmask >> lane) & 1u);
-        if (__ballot(first && !tag_is(home, epoch)) != 0) {
+        if (!local_plan && __ballot(first && !tag_is(home, epoch)) != 0) {
           // rare: the pop was loaded before it arrived
           if (!poll_tagged(pb.pops + rt.base + rt.rank, first, epoch, home)) {
             if (lane == 0) {
@@ -1388,7 +1442,11 @@ void sdm_trace_kernel(StepParams P) {
   if constexpr (!DENSE) {
     bool ok = true;
     PlanControl pc{};
-    if (bank == 0) pc = plan_control(P, layer_id);
+    // a short launch tries the local plan first: every control wave needs
+    // the control words and the free count then
+    const bool local_try = MAPLDS && G0 <= kLocalPlanSteps && B <= kWave &&
+                           G0 + local_words(G0) <= pb.steps;
+    if (bank == 0 || local_try) pc = plan_control(P, layer_id);
     if constexpr (MAPLDS) {
       // count part: this bank's first touches, step by step.  A slot is
       // first-touched by the launch's first step that writes it, unless it
@@ -1402,43 +1460,6 @@ void sdm_trace_kernel(StepParams P) {
       uint32_t mapped[KC];
       int err_step = (base_err & COWSDM_ERR_TEMPLATE) ? 0 : G0;
       int err_bits[KC];
-      // the slots of chunks c + 1 .. c + kAhead load while chunk c is checked
-      constexpr int kAhead = sizeof(IDX) == 4 ? 2 : 1;
-      IDX sbuf[kAhead + 1][kIdxRow];
-      auto load_slots = [&](int c, IDX (&dst)[kIdxRow]) __attribute__((always_inline)) {
-        const int t = c * kWave + lane;
-        const int tc = t < G0 ? t : G0 - 1;
-        const char* const w = at(wbase, st_wi, tc);
-        const char* const r = at(rbase, st_ri, tc);
-        if constexpr (FULL && sizeof(IDX) == 4) {
-          // a step's 4 write and 16 read slots are 16 and 64 contiguous,
-          // 16-byte aligned bytes: five vector loads per lane
-          const i32x4_t a = *(const __attribute__((address_space(1))) i32x4_t*)(w);
-          dst[0] = a.x; dst[1] = a.y; dst[2] = a.z; dst[3] = a.w;
-#pragma unroll
-          for (int k = 0; k < kTraceMaxReads / 4; ++k) {
-            const i32x4_t b = *(const __attribute__((address_space(1))) i32x4_t*)(r + 16 * k);
-            dst[kTraceMaxWrites + 4 * k] = b.x;
-            dst[kTraceMaxWrites + 4 * k + 1] = b.y;
-            dst[kTraceMaxWrites + 4 * k + 2] = b.z;
-            dst[kTraceMaxWrites + 4 * k + 3] = b.w;
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < kTraceMaxWrites; ++j) {
-            dst[j] = *(const __attribute__((address_space(1))) IDX*)(w + (j < W ? j : W - 1) * sizeof(IDX));
-          }
-#pragma unroll
-          for (int i = 0; i < kTraceMaxReads; ++i) {
-            dst[kTraceMaxWrites + i] =
-                *(const __attribute__((address_space(1))) IDX*)(r + (i < R ? i : R - 1) * sizeof(IDX));
-          }
-        }
-      };
-#pragma unroll
-      for (int c = 0; c < kAhead; ++c) {
-        if (c * kWave < G0) load_slots(c, sbuf[c]);
-      }
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const int t = c * kWave + lane;
@@ -1493,6 +1514,11 @@ void sdm_trace_kernel(StepParams P) {
           err_bits[c] = e;
           err_step = t < err_step ? t : err_step;
         }
+        if (c == 0) {
+          // chunk 0's slots serve the steps too (the prologue's chunk)
+#pragma unroll
+          for (int k = 0; k < kIdxRow; ++k) chunk[k] = cur[k];
+        }
       }
       // the bank's first invalid step and its errors
       for (int o = kWave / 2; o > 0; o >>= 1) {
@@ -1506,6 +1532,7 @@ void sdm_trace_kernel(StepParams P) {
       // one wave's LDS accesses apply in issue order: keep the reads after
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint32_t count0 = 0;   // lane t < 64: step t's count word
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         const int t = c * kWave + lane;
@@ -1518,31 +1545,69 @@ void sdm_trace_kernel(StepParams P) {
             if (x >= 0 && !((mapped[c] >> j) & 1u) && first_write[x] == t) mask |= 1u << j;
           }
         }
-        atomic_store_u64(pb.word(bank, t),
-                         tagged(epoch, mask | (t >= err_step ? kCountStop : 0u)));
+        const uint32_t word = mask | (t >= err_step ? kCountStop : 0u);
+        if (c == 0) count0 = word;
+        atomic_store_u64(pb.word(bank, t), tagged(epoch, word));
+      }
+      if (local_try) {
+        // the same words packed for the local plan, kLocalStepsPerWord steps
+        // per word, at the end of the bank's row
+        uint32_t packed = 0;
+#pragma unroll
+        for (int k = 0; k < kLocalWords; ++k) {
+          uint32_t v = 0;
+#pragma unroll
+          for (int i = 0; i < kLocalStepsPerWord; ++i) {
+            const int t = k * kLocalStepsPerWord + i;
+            if (t < kLocalPlanSteps && t < G0) {
+              v |= static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(count0), t))
+                   << (kLocalBits * i);
+            }
+          }
+          if (lane == k) packed = v;
+        }
+        if (lane < local_words(G0)) {
+          atomic_store_u64(local_word(pb, bank, lane), tagged(epoch, packed));
+        }
       }
       if (lane == 0 && bits != 0) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(bits),
                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    // prefix part (a contiguous share of the steps per bank), the layer part
-    // (bank 0), the header
-    {
-      const int per = (G0 + B - 1) / B;
-      const int t0 = bank * per < G0 ? bank * per : G0;
-      ok = plan_prefix(pb, B, epoch, t0, t0 + per < G0 ? t0 + per : G0);
-    }
-    if (bank == 0) {
-      // slot maps in LDS: the planner lists the pops (its segments in the
-      // chunk slots' LDS, unused until the steps start); else every bank
-      // lists its own
-      ok = plan_layer<!MAPLDS>(P, layer_id, pb, B, G0, epoch,
-                               MAPLDS ? &lds_idx[0][0][0][0] : &lds_seg[0], &lds_plan[pair][0],
-                               pc) && ok;
-    }
     PlanHeader head{0, 0, C0, 0, 1};
-    ok = plan_header<!MAPLDS>(pb, epoch, head) && ok;
+    int local = 0;
+    if constexpr (MAPLDS) {
+      LocalPlan lp{};
+      if (local_try) local = plan_local(pb, B, G0, epoch, bank, pc, &lds_plan[pair][0], lp);
+      if (local > 0) {
+        head.steps = G0;
+        head.fit = lp.fit;
+        head.found = lp.found;
+        local_plan = true;
+        local_proven = lp.proven;
+      } else if (local < 0) {
+        ok = false;
+      }
+    }
+    if (local == 0) {
+      // the central plan: prefix part (a contiguous share of the steps per
+      // bank), the layer part (bank 0), the header
+      {
+        const int per = (G0 + B - 1) / B;
+        const int t0 = bank * per < G0 ? bank * per : G0;
+        ok = plan_prefix(pb, B, epoch, t0, t0 + per < G0 ? t0 + per : G0);
+      }
+      if (bank == 0) {
+        // slot maps in LDS: the planner lists the pops (its segments in the
+        // chunk slots' LDS, unused until the steps start); else every bank
+        // lists its own
+        ok = plan_layer<!MAPLDS>(P, layer_id, pb, B, G0, epoch,
+                                 MAPLDS ? &lds_idx[0][0][0][0] : &lds_seg[0], &lds_plan[pair][0],
+                                 pc) && ok;
+      }
+      ok = plan_header<!MAPLDS>(pb, epoch, head) && ok;
+    }
     int steps = head.steps, fit = head.fit, capacity = head.capacity;
     if (!ok) {
       if (lane == 0) {
@@ -1559,7 +1624,7 @@ void sdm_trace_kernel(StepParams P) {
     G = steps < G0 ? steps : G0;
     fit_rows = fit;
     plan_segs = ok ? head.segments : 1;
-    found_top = head.found;
+    found_top = head.found;   // BANKS_LIST, or a local plan
     C = pin(capacity);
     if (lane == 0) sync_store(&sync[2], kPlanReady | static_cast<uint32_t>(G));
   }
@@ -1574,7 +1639,8 @@ void sdm_trace_kernel(StepParams P) {
   TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
   q.widx = 0; q.ridx = 0; q.base = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1;
   q.rank = 0; q.u = 0; q.fwd = 0; q.rawm = 0;
-  if constexpr (DENSE || MAPLDS) load_chunk(0);
+  // (packed with the map in LDS: chunk 0 was loaded for the plan's count)
+  if constexpr (DENSE) load_chunk(0);
   bool plan_ok = list_pops(stage_plan());
   if constexpr (DENSE || MAPLDS) {
     write_chunk(0, chunk_fm(0));
@@ -1731,6 +1797,24 @@ void sdm_trace_kernel(StepParams P) {
     }
     // the low half counts the waves done with the launch
     if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
+      if constexpr (!DENSE) {
+        if (local_plan) {
+          // what a local plan leaves (the central plan's layer part writes
+          // these before the steps; here every wave has read the free count
+          // and control words by now): the stack's new height and the proof
+          if (lane == 0) *L.free_count = static_cast<int32_t>(found_top - fit_rows);
+          if (lane < 4) {
+            int k = COWSDM_CTRL_PROVEN;
+            int64_t v = local_proven;
+            if (lane == 1) { k = COWSDM_CTRL_FREE; v = found_top - fit_rows; }
+            if (lane == 2) { k = COWSDM_CTRL_STEPS; v = G0; }
+            if (lane == 3) { k = COWSDM_CTRL_FIT; v = fit_rows; }
+            atomic_store_u64(&control_word(P, layer_id, k), static_cast<uint64_t>(v));
+          }
+          // the report below reads the control words back
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+      }
       if (lane == 0) {
         atomic_store_u64(P.trace_ticket + 1 + layer_id, 0);
         if (P.trace_step) {

@@ -166,6 +166,172 @@ __device__ __forceinline__ PlanControl plan_control(const StepParams& P, int lay
   return c;
 }
 
+// ---- the local plan of a short launch
+//
+// A launch of at most kLocalPlanSteps steps over at most kWave banks, with
+// slot maps in LDS, first tries a plan that every control wave makes by
+// itself.  Each bank's count part also publishes its count words packed,
+// kLocalStepsPerWord steps to a tagged word, at the end of its row of plan
+// words (past the launch's steps).  Every control wave reads all banks'
+// packed words (lane = bank), takes each step's first touches of the lower
+// banks and its total from ballots of the banks' first-touch lanes, adds
+// the totals up into running totals, and walks the decode loop's proof from
+// the control words.  When the launch neither grows the slab nor overflows
+// it, that is the whole plan: the bank's first touches pop the found
+// stack's entries free_count - 1 - (running total + prefix + rank)
+// directly, with no prefix, layer or header part and no pop list, and the
+// layer's last control wave to finish writes the free count and control
+// words the launch leaves.  A launch that grows, overflows, or finds a
+// corrupt free count takes the central plan instead: every wave decides so
+// from the same words, so all of them do.
+constexpr int kLocalPlanSteps = 32;
+constexpr int kLocalBits = 5;   // a count word: 4 first-touch lanes and the stop bit
+constexpr int kLocalStepsPerWord = 32 / kLocalBits;
+constexpr int kLocalWords = (kLocalPlanSteps + kLocalStepsPerWord - 1) / kLocalStepsPerWord;
+
+__host__ __device__ constexpr int local_words(int steps) {
+  return (steps + kLocalStepsPerWord - 1) / kLocalStepsPerWord;
+}
+// packed word k of a bank: the row's last words, which a launch of at most
+// steps - kLocalWords steps does not use
+__device__ __forceinline__ int64_t* local_word(const PlanBlock& pb, int bank, int k) {
+  return pb.word(bank, static_cast<int>(pb.steps) - 1 - k);
+}
+
+struct LocalPlan {
+  int fit;          // the pops the launch gives: all of its first touches
+  int found;        // the stack height the launch found
+  int64_t proven;   // the proof counter the launch leaves
+};
+
+// 1: planned (this bank's plan words are in plan_words[0, G0)); 0: the
+// launch needs the central plan; -1: a count word never arrived (bounded).
+__device__ inline int plan_local(const PlanBlock& pb, int B, int G0, uint32_t epoch, int bank,
+                                 const PlanControl& pc, int* plan_words, LocalPlan& out) {
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const bool in = lane < B;
+  const int nw = local_words(G0);
+  // every bank's packed count words, lane = bank
+  uint64_t w[kLocalWords];
+#pragma unroll
+  for (int k = 0; k < kLocalWords; ++k) {
+    w[k] = k < nw && in ? atomic_load_u64(local_word(pb, lane, k)) : tagged(epoch, 0);
+  }
+  for (int spins = 0;; ++spins) {
+    bool missing = false;
+#pragma unroll
+    for (int k = 0; k < kLocalWords; ++k) missing |= !tag_is(w[k], epoch);
+    if (__ballot(missing) == 0) break;
+    if (spins >= kSpinLimit) return -1;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < kLocalWords; ++k) {
+      if (k < nw && in && !tag_is(w[k], epoch)) w[k] = atomic_load_u64(local_word(pb, lane, k));
+    }
+  }
+  // the first touches of the lower banks and each step's total: the banks'
+  // counts (lane = bank) packed kSumSteps steps to an int in 9-bit fields
+  // (a sum over 64 banks of at most 4 each fits), so one scan across the
+  // wave serves kSumSteps steps; then step by step (wave-uniform), lane t
+  // keeping step t's running total and this bank's plan word
+  constexpr int kSumBits = 9;
+  constexpr int kSumSteps = 3;
+  constexpr int kSums = (kLocalPlanSteps + kSumSteps - 1) / kSumSteps;
+  auto count_word = [&](int t) __attribute__((always_inline)) -> uint32_t {
+    return (static_cast<uint32_t>(w[t / kLocalStepsPerWord]) >>
+            (kLocalBits * (t % kLocalStepsPerWord))) & ((1u << kLocalBits) - 1);
+  };
+  uint32_t own_words[kLocalWords];   // this bank's packed count words
+#pragma unroll
+  for (int k = 0; k < kLocalWords; ++k) {
+    own_words[k] = k < nw ? static_cast<uint32_t>(__builtin_amdgcn_readlane(
+                                static_cast<int>(static_cast<uint32_t>(w[k])), bank))
+                          : 0u;
+  }
+  int cum = 0;
+  int cum_l = 0;
+  uint32_t word_l = 0;
+#pragma unroll
+  for (int g = 0; g < kSums; ++g) {
+    if (g * kSumSteps < G0) {
+      int packed = 0;
+#pragma unroll
+      for (int i = 0; i < kSumSteps; ++i) {
+        const int t = g * kSumSteps + i;
+        if (t < kLocalPlanSteps && t < G0) {
+          packed += __popc(count_word(t) & 15u) << (kSumBits * i);
+        }
+      }
+      const int incl = wave_inclusive(packed);
+      const uint32_t lower = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - packed, bank));
+      const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl, kWave - 1));
+#pragma unroll
+      for (int i = 0; i < kSumSteps; ++i) {
+        const int t = g * kSumSteps + i;
+        if (t < kLocalPlanSteps && t < G0) {
+          const int pre = static_cast<int>((lower >> (kSumBits * i)) & ((1u << kSumBits) - 1));
+          const int tot = static_cast<int>((total >> (kSumBits * i)) & ((1u << kSumBits) - 1));
+          const uint32_t own = (own_words[t / kLocalStepsPerWord] >>
+                                (kLocalBits * (t % kLocalStepsPerWord))) & ((1u << kLocalBits) - 1);
+          const uint32_t base = static_cast<uint32_t>(cum + pre);
+          const uint32_t word = (base & kPlanBaseMask) | ((own & 15u) << kPlanMaskShift) |
+                                ((own & kCountStop) ? 1u << kPlanStopBit : 0u);
+          if (lane == t) {
+            cum_l = cum;
+            word_l = word;
+          }
+          cum += tot;
+        }
+      }
+    }
+  }
+  const int cum_g = cum;
+  auto cum_at = [&](int s) __attribute__((always_inline)) -> int {
+    return s >= G0 ? cum_g : __builtin_amdgcn_readlane(cum_l, s);
+  };
+
+  // the decode loop's proof (plan_layer's walk, with no growth)
+  const int64_t C0 = uniform64(pc.capacity);
+  int64_t proven = uniform64(pc.proven);
+  const int64_t quantum = uniform64(pc.quantum);
+  const int64_t need = uniform64(pc.need);
+  const int F0 = __builtin_amdgcn_readfirstlane(pc.free_count);
+  if (F0 < 0 || F0 > C0) return 0;
+  if (need > 0 && quantum > 0) {
+    int s = 0;
+    if (proven >= need) {
+      int64_t j = plan_div(proven, need);
+      if (j > G0) j = G0;
+      if (cum_at(static_cast<int>(j)) > F0) return 0;   // not honest: it overflows
+      proven -= j * need;
+      s = static_cast<int>(j);
+    }
+    while (s < G0) {
+      const int64_t free_rows = F0 - cum_at(s);
+      if (free_rows < need) return 0;   // the slab grows at step s
+      const int64_t h = plan_div(free_rows, need);
+      if (s + h >= G0) {
+        proven = free_rows - static_cast<int64_t>(G0 - s) * need;
+        s = G0;
+      } else {
+        s += static_cast<int>(h);
+      }
+    }
+  }
+  // no proof (or a proof for less than the steps' first touches) and the
+  // stack runs out: the central plan overflows.  Below, every pop lies in
+  // the found stack: found_top - 1 - q >= 0.
+  if (cum_g > F0) return 0;
+
+  if (lane < G0) plan_words[lane] = static_cast<int>(word_l);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  out.fit = cum_g;
+  out.found = F0;
+  out.proven = proven;
+  return 1;
+}
+
 // The stack entry at position p after growth segment k: the row the latest
 // growth j <= k whose positions cover p put there, or -1 for the entry the
 // launch found there.

@@ -58,8 +58,11 @@ def _trace(device, *, banks, slots, width, writes, reads, steps, seed,
     return state, oracle
 
 
-def test_reference_known_answers(device):
-    """tests/test_allocator.py:65-82 on the GPU path."""
+@pytest.mark.parametrize("backend", ["auto", "torch"])
+def test_reference_known_answers(device, backend):
+    """tests/test_allocator.py:65-82 on the GPU path, also with the backend
+    the reference's test names ("torch": the same kernels, with the torch
+    path's exhaustion check before every step)."""
 
     initial, steps = rc.reference_case(2)
     packed = cow.PackedSDMCopyOnWriteState.allocate(
@@ -69,8 +72,8 @@ def test_reference_known_answers(device):
     firsts = []
     for inputs in steps:
         gpu = to_device(inputs, device)
-        dense_read = cow.dense_sdm_sparse_step(dense, **gpu)
-        packed_read, diag = cow.packed_sdm_cow_step(packed, **gpu)
+        dense_read = cow.dense_sdm_sparse_step(dense, **gpu, backend=backend)
+        packed_read, diag = cow.packed_sdm_cow_step(packed, **gpu, backend=backend)
         want, _ = ref.packed_step(oracle, **to_numpy(inputs))
         assert torch.equal(dense_read, packed_read)
         assert torch.equal(dense, packed.materialize_dense())
@@ -199,6 +202,24 @@ def test_unproven_exhaustion_raises_without_mutation(device):
         cow.packed_sdm_cow_step(state, **to_device(steps[0], device))
     assert torch.equal(state.logical_to_physical, before)
     assert int(state.free_count) == 5
+
+
+def test_torch_backend_checks_exhaustion_on_proven_state(device):
+    """The reference's torch path asserts the free stack covers the step's
+    first touches whether or not a proof exists (allocator.py:1474): with
+    backend="torch" a proven state too small for the step raises before
+    anything changes."""
+
+    initial, steps = rc.reference_case(1)
+    state = cow.PackedSDMCopyOnWriteState.allocate(initial.to(device), banks=rc.BANKS,
+                                                   capacity_rows=5)
+    state.capacity_is_proven = True
+    before = state.logical_to_physical.clone()
+    with pytest.raises(ValueError, match="physical slab is exhausted"):
+        cow.packed_sdm_cow_step(state, **to_device(steps[0], device), validate_routes=False,
+                                backend="torch")
+    assert torch.equal(state.logical_to_physical, before)
+    assert int(state.free_count) == 5 and int(state.overflow_flag) == 0
 
 
 def test_proven_overflow_latches_and_spares_later_banks(device):

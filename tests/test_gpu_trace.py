@@ -481,3 +481,62 @@ def test_persistent_overflow_sets_flag_and_keeps_partition(device):
     free = st[0].free_rows[: int(st[0].free_count)].cpu()
     rows = torch.cat((live, free)).sort().values
     assert torch.equal(rows, torch.arange(60, dtype=rows.dtype))
+
+
+@pytest.mark.parametrize("banks,launch_steps", [(16, 20), (64, 32), (5, 3)])
+def test_short_launches_plan_locally(device, banks, launch_steps):
+    """Launches of at most 32 steps over at most 64 banks with slot maps in
+    LDS make their plan in every control wave, with no header: while the
+    slab does not grow, a launch leaves the header words of an earlier epoch
+    and its pops come straight from the found stack; a launch that grows
+    takes the central plan, whose header carries the launch's epoch.  Both
+    equal the reference's decode loop, rows and stacks included."""
+
+    layers, slots, width, writes, reads = 2, 64, 64, 4, 8
+    steps = 3 * launch_steps + 1
+    m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=41, device=device)
+    routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
+                                  width=width, writes=writes, reads=reads, seed=42, device=device)
+    kw = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+              values=routes.values, input_gate=routes.input_gate,
+              forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+              read_weights=routes.read_weights)
+
+    def case(capacity, quantum):
+        states = [cow.PackedSDMCopyOnWriteState.allocate(
+            m0[l], banks=banks, capacity_rows=capacity, growth_quantum_rows=quantum)
+            for l in range(layers)]
+        oracles = [ref.allocate(m0[l].cpu().numpy(), banks=banks, capacity_rows=capacity,
+                                growth_quantum_rows=quantum) for l in range(layers)]
+        outputs = torch.empty(steps, layers, banks, width, device=device)
+        tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
+        tr.reserve_steps(steps)
+        headers = []
+        done = 0
+        while done < steps:
+            n = min(launch_steps, steps - done)
+            tr.run(n, launch_steps=launch_steps)
+            scan = tr.scan.cpu()
+            # the launch's epoch (its last control wave stores it) against
+            # the epoch of the header words
+            headers.append([int(scan[l, 8]) >> 32 == int(scan[l, 0]) & 0xFFFFFFFF
+                            for l in range(layers)])
+            done += n
+        want = oracle_decode_loop(oracles, routes, steps, need=banks * writes)
+        torch.cuda.synchronize()
+        assert np.array_equal(outputs.cpu().numpy(), want)
+        for st, orc in zip(states, oracles):
+            assert_state_equal(st, orc)
+            st.validate_invariants()
+        return states, headers
+
+    # room for every slot twice over: the proof re-reads the free count every
+    # few launches but never grows the slab, so every plan is local
+    states, headers = case(2 * banks * slots, banks * writes)
+    assert not any(any(h) for h in headers)
+    assert all(st.growth_events == 0 for st in states)
+    assert int(states[0].allocated_rows_tensor()) > banks * 4
+    # a slab that grows in the first launch: that launch plans centrally
+    states, headers = case(banks * writes, banks * writes)
+    assert all(headers[0])
+    assert all(st.growth_events > 0 for st in states)
