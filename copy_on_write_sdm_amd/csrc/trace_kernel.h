@@ -299,6 +299,9 @@ void sdm_trace_kernel(StepParams P) {
   // [1]: data -> control, steps computed; [2]: control -> data, packed:
   // kPlanReady | the steps the launch's plan lets the bank run
   __shared__ uint32_t lds_sync[NB][3];
+  // the workgroup's control waves done with the launch (the last of them
+  // takes the layer's tickets for all)
+  __shared__ uint32_t lds_done;
   // control wave: the slots of two 64-step chunks, per step W write slots
   // then R read slots (-1: outside [0, N)) and the step's four class words,
   // staged from registers a chunk ahead (map in LDS, or dense)
@@ -381,6 +384,7 @@ void sdm_trace_kernel(StepParams P) {
     lds_sync[pair][1] = 0;
     lds_sync[pair][2] = 0;
   }
+  if (threadIdx.x == 0) lds_done = 0;
   __syncthreads();
   if (bank >= B) return;  // both waves of the bank
 
@@ -1790,13 +1794,31 @@ void sdm_trace_kernel(StepParams P) {
       __builtin_amdgcn_s_waitcnt(0);
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-    int64_t done = 0;
-    if (lane == 0) {
+    // The workgroup's control waves combine their tickets in LDS: the last
+    // of them to finish takes one for each (fewer atomics on the layer's
+    // word, which serialise), the others are done.  Their status bits have
+    // completed before their LDS add (the wait above), and so before it.
+    const int members = __builtin_amdgcn_readfirstlane(
+        B - (bank - pair) < NB ? B - (bank - pair) : NB);
+    int take = 1;
+    bool last_here = true;
+    if (members > 1) {
+      uint32_t before = 0;
+      if (lane == 0) {
+        before = __hip_atomic_fetch_add(&lds_done, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      last_here = __builtin_amdgcn_readfirstlane(static_cast<int>(before)) + 1 == members;
+      take = members;
+    }
+    int64_t done = -1;
+    if (last_here && lane == 0) {
       int64_t* const ticket = P.trace_ticket + 1 + layer_id;
-      done = __hip_atomic_fetch_add(ticket, int64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      done = __hip_atomic_fetch_add(ticket, int64_t{take}, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
     }
     // the low half counts the waves done with the launch
-    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done)) == B - 1) {
+    if (last_here && __builtin_amdgcn_readfirstlane(static_cast<int>(done)) + take == B) {
       if constexpr (!DENSE) {
         if (local_plan) {
           // what a local plan leaves (the central plan's layer part writes
