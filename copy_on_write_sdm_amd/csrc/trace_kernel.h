@@ -297,8 +297,11 @@ void sdm_trace_kernel(StepParams P) {
   // [0]: control -> data, (stop step << 16) | steps whose row addresses are
   // published (the masks and store rows of all but the last of them);
   // [1]: data -> control, steps computed; [2]: control -> data, packed:
-  // kPlanReady | the steps the launch's plan lets the bank run
-  __shared__ uint32_t lds_sync[NB][3];
+  // kPlanReady | the steps the launch's plan lets the bank run; [3]: data ->
+  // control, packed short launch: 2 + the local plan's result (plan_local)
+  __shared__ uint32_t lds_sync[NB][4];
+  // data -> control: the local plan's pops, found stack height and proof
+  __shared__ int64_t lds_local[NB][3];
   // the workgroup's control waves done with the launch (the last of them
   // takes the layer's tickets for all)
   __shared__ uint32_t lds_done;
@@ -383,6 +386,7 @@ void sdm_trace_kernel(StepParams P) {
     lds_sync[pair][0] = kNoStop << 16;
     lds_sync[pair][1] = 0;
     lds_sync[pair][2] = 0;
+    lds_sync[pair][3] = 0;
   }
   if (threadIdx.x == 0) lds_done = 0;
   __syncthreads();
@@ -705,6 +709,25 @@ void sdm_trace_kernel(StepParams P) {
     auto need = [&](int t) __attribute__((always_inline)) -> uint32_t {
       return static_cast<uint32_t>(t + 3 < G + 1 ? t + 3 : G + 1);
     };
+    // packed short launch, slot map in LDS: the local plan (trace_plan.h)
+    // is made here while the control wave classifies the launch's first
+    // chunk; the control wave takes the result from LDS
+    if constexpr (!DENSE && MAPLDS) {
+      const PlanBlock pbd = plan_block(P, layer_id);
+      if (local_plan_fits(G0, B, pbd)) {
+        const uint32_t ep = static_cast<uint32_t>(
+            __builtin_amdgcn_readfirstlane(static_cast<int>(launch_epoch(pbd))));
+        const PlanControl pcd = plan_control(P, layer_id);
+        LocalPlan lp{};
+        const int r = plan_local(pbd, B, G0, ep, bank, pcd, &lds_plan[pair][0], lp);
+        if (lane == 0) {
+          lds_local[pair][0] = lp.fit;
+          lds_local[pair][1] = lp.found;
+          lds_local[pair][2] = lp.proven;
+          sync_store(&sync[3], static_cast<uint32_t>(2 + r));
+        }
+      }
+    }
     // packed: the steps the launch's plan lets this bank run, from the
     // control wave before it publishes any step (bounded wait)
     bool go = true;
@@ -879,6 +902,7 @@ void sdm_trace_kernel(StepParams P) {
   // layer's last control wave writes what the launch leaves
   bool local_plan = false;
   int64_t local_proven = 0;
+  bool chunk0_classified = false;   // chunk 0's class words are in LDS
   if constexpr (!DENSE) {
     pb = plan_block(P, layer_id);
     // the epoch word changes only when the layer's last control wave ends
@@ -1446,11 +1470,9 @@ void sdm_trace_kernel(StepParams P) {
   if constexpr (!DENSE) {
     bool ok = true;
     PlanControl pc{};
-    // a short launch tries the local plan first: every control wave needs
-    // the control words and the free count then
-    const bool local_try = MAPLDS && G0 <= kLocalPlanSteps && B <= kWave &&
-                           G0 + local_words(G0) <= pb.steps;
-    if (bank == 0 || local_try) pc = plan_control(P, layer_id);
+    // a short launch tries the local plan first (the data wave makes it)
+    const bool local_try = MAPLDS && local_plan_fits(G0, B, pb);
+    if (bank == 0) pc = plan_control(P, layer_id);
     if constexpr (MAPLDS) {
       // count part: this bank's first touches, step by step.  A slot is
       // first-touched by the launch's first step that writes it, unless it
@@ -1524,15 +1546,29 @@ void sdm_trace_kernel(StepParams P) {
           for (int k = 0; k < kIdxRow; ++k) chunk[k] = cur[k];
         }
       }
-      // the bank's first invalid step and its errors
-      for (int o = kWave / 2; o > 0; o >>= 1) {
-        const int y = __shfl_xor(err_step, o, kWave);
-        err_step = y < err_step ? y : err_step;
+      // the bank's first invalid step (a ballot per chunk: lane = step) and
+      // its errors
+      {
+        int first_bad = (base_err & COWSDM_ERR_TEMPLATE) ? 0 : G0;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          if (c * kWave < G0) {
+            const uint64_t m = __ballot(err_bits[c] != 0);
+            if (m != 0) {
+              const int t = c * kWave + static_cast<int>(__builtin_ctzll(m));
+              first_bad = t < first_bad ? t : first_bad;
+            }
+          }
+        }
+        err_step = first_bad;
       }
       int bits = 0;
 #pragma unroll
-      for (int c = 0; c < KC; ++c) bits |= c * kWave + lane == err_step ? err_bits[c] : 0;
-      bits = wave_or(bits);
+      for (int c = 0; c < KC; ++c) {
+        if (c * kWave < G0 && err_step < G0 && (err_step >> 6) == c) {
+          bits = __builtin_amdgcn_readlane(err_bits[c], err_step & (kWave - 1));
+        }
+      }
       // one wave's LDS accesses apply in issue order: keep the reads after
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1573,6 +1609,11 @@ void sdm_trace_kernel(StepParams P) {
         if (lane < local_words(G0)) {
           atomic_store_u64(local_word(pb, bank, lane), tagged(epoch, packed));
         }
+        // chunk 0's class words while the data wave makes the local plan:
+        // the first-touch lanes are this bank's own count words' (the plan
+        // adds only where the rows come from)
+        write_chunk(0, count0 & 15u);
+        chunk0_classified = true;
       }
       if (lane == 0 && bits != 0) {
         __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS], static_cast<int64_t>(bits),
@@ -1582,16 +1623,23 @@ void sdm_trace_kernel(StepParams P) {
     PlanHeader head{0, 0, C0, 0, 1};
     int local = 0;
     if constexpr (MAPLDS) {
-      LocalPlan lp{};
-      if (local_try) local = plan_local(pb, B, G0, epoch, bank, pc, &lds_plan[pair][0], lp);
-      if (local > 0) {
-        head.steps = G0;
-        head.fit = lp.fit;
-        head.found = lp.found;
-        local_plan = true;
-        local_proven = lp.proven;
-      } else if (local < 0) {
-        ok = false;
+      if (local_try) {
+        // the data wave's local plan (bounded wait)
+        uint32_t r = 0;
+        for (int spins = 0; spins < 64 * kSpinLimit && r == 0; ++spins) {
+          r = sync_load(&sync[3]);
+          if (r == 0) __builtin_amdgcn_s_sleep(1);
+        }
+        local = r == 0 ? -1 : static_cast<int>(r) - 2;
+        if (local > 0) {
+          head.steps = G0;
+          head.fit = static_cast<int>(lds_local[pair][0]);
+          head.found = static_cast<int>(lds_local[pair][1]);
+          local_plan = true;
+          local_proven = lds_local[pair][2];
+        } else if (local < 0) {
+          ok = false;
+        }
       }
     }
     if (local == 0) {
@@ -1643,11 +1691,16 @@ void sdm_trace_kernel(StepParams P) {
   TraceRoute q, rA, rB;            // steps s and s+1 at the start of iteration s
   q.widx = 0; q.ridx = 0; q.base = 0; q.wrow = -1; q.wsrc = -1; q.rsrc = -1; q.rraw = -1;
   q.rank = 0; q.u = 0; q.fwd = 0; q.rawm = 0;
-  // (packed with the map in LDS: chunk 0 was loaded for the plan's count)
+  // (packed with the map in LDS: chunk 0 was loaded for the plan's count,
+  // and for a short launch classified beside the local plan: again here
+  // after a central plan whose planner used this LDS, or whose growth
+  // changed the capacity the class words check map entries against)
   if constexpr (DENSE) load_chunk(0);
   bool plan_ok = list_pops(stage_plan());
   if constexpr (DENSE || MAPLDS) {
-    write_chunk(0, chunk_fm(0));
+    if (!chunk0_classified || (!local_plan && (bank == 0 || C != C0))) {
+      write_chunk(0, chunk_fm(0));
+    }
     if (G > kWave) load_chunk(1);  // written before step 64 is read
   }
   {

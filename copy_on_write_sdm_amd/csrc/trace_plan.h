@@ -198,6 +198,12 @@ __device__ __forceinline__ int64_t* local_word(const PlanBlock& pb, int bank, in
   return pb.word(bank, static_cast<int>(pb.steps) - 1 - k);
 }
 
+// Whether a launch of G0 steps over B banks takes the local plan first (its
+// packed words fit past its steps in each bank's row of plan words).
+__device__ __forceinline__ bool local_plan_fits(int G0, int B, const PlanBlock& pb) {
+  return G0 <= kLocalPlanSteps && B <= kWave && G0 + local_words(G0) <= pb.steps;
+}
+
 struct LocalPlan {
   int fit;          // the pops the launch gives: all of its first touches
   int found;        // the stack height the launch found
