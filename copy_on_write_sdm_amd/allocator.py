@@ -20,7 +20,10 @@ Differences from the reference, all deliberate:
   the reference asserts on the device (allocator.py:1474) and this build
   raises as ValueError after one synchronisation.  "triton" raises the
   reference's unavailable-backend error.
-* Value state, route weights, values and gates are float32.
+* Value state is float32 (the reference's serving path and benchmark use
+  float32 state, inference.py:359); route weights, values and gates may be
+  float16 or bfloat16: they compute in float32, as in both reference
+  backends, and the reading comes back in the values' dtype.
 * The state carries one more tensor, ``scratch`` (int64 [8 + B]), holding the
   bank-order scan slots, a ticket counter and a sticky error word.
 * Route validation (``validate_routes=True``) and steps on a state without a
@@ -1146,6 +1149,18 @@ def _select_backend(backend: str, *, tensor: torch.Tensor, writes: int, reads: i
     return backend == "torch"
 
 
+_NARROW_FLOATS = (torch.float16, torch.bfloat16)
+
+
+def _widen(tensor: torch.Tensor) -> torch.Tensor:
+    """A 16-bit float route weight, value or gate tensor widened to float32 on
+    the device (exact), as both reference backends take them: the Triton
+    kernels load and convert to float32 (allocator.py:74-229), the torch path
+    calls .float() (allocator.py:1136-1139, 1490-1498)."""
+
+    return tensor.float() if tensor.dtype in _NARROW_FLOATS else tensor
+
+
 def _check_float_tensors(tensors: Sequence[torch.Tensor]) -> None:
     for tensor in tensors:
         if tensor.dtype != torch.float32:
@@ -1313,6 +1328,12 @@ def packed_sdm_cow_step(
         forget_log_gate, read_indices, read_weights, erase_gate, dense=False)
     torch_checks = _select_backend(backend, tensor=state.values,
                                    writes=write_indices.shape[1], reads=read_indices.shape[1])
+    # float16/bfloat16 weights, values and gates compute in float32; the
+    # reading comes back in the values' dtype (allocator.py:1521)
+    reading_dtype = values.dtype
+    write_weights, values, input_gate, effective_erase, forget_log_gate, read_weights = (
+        _widen(t) for t in (write_weights, values, input_gate, effective_erase,
+                            forget_log_gate, read_weights))
     _check_float_tensors((write_weights, values, input_gate, effective_erase,
                           forget_log_gate, read_weights))
     index_code = _index_code(write_indices, read_indices)
@@ -1337,6 +1358,8 @@ def packed_sdm_cow_step(
                   "cowsdm_packed_step")
     elif allocated is not None:
         allocated = state.allocated_rows_tensor()
+    if reading_dtype != output.dtype:
+        output = output.to(reading_dtype)
     if not collect_diagnostics:
         return output, None
     return output, SDMCopyOnWriteStep(
@@ -1374,6 +1397,10 @@ def dense_sdm_sparse_step(
         forget_log_gate, read_indices, read_weights, erase_gate, dense=True)
     _select_backend(backend, tensor=memory, writes=write_indices.shape[1],
                     reads=read_indices.shape[1])
+    reading_dtype = values.dtype
+    write_weights, values, input_gate, effective_erase, forget_log_gate, read_weights = (
+        _widen(t) for t in (write_weights, values, input_gate, effective_erase,
+                            forget_log_gate, read_weights))
     _check_float_tensors((memory, write_weights, values, input_gate, effective_erase,
                           forget_log_gate, read_weights))
     index_code = _index_code(write_indices, read_indices)
@@ -1388,7 +1415,7 @@ def dense_sdm_sparse_step(
     if banks:
         nat.check(nat.lib().cowsdm_dense_step(layer, shape, nat.stream_handle(device)),
                   "cowsdm_dense_step")
-    return output
+    return output if reading_dtype == output.dtype else output.to(reading_dtype)
 
 
 def _layer_arrays(count: int, *args):

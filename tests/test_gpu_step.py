@@ -309,3 +309,33 @@ def test_fault_bits_raise_at_the_proofs_read(device):
     state.ensure_scratch()[nat.SCRATCH_ERRORS] = nat.ERR_WRITE_INDEX
     state.proven_maximum_additional_allocations = 0
     state.prepare_step_capacity(4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_precision_inputs(device, dtype):
+    """Route weights, values and gates in float16/bfloat16 (the reference
+    model's activations): both steps compute in float32 from the widened
+    inputs, as both reference backends do (allocator.py:1136-1139, 1490-1521),
+    so the state equals the oracle's step on the widened inputs bit for bit
+    and the reading is that step's reading rounded to the values' dtype."""
+
+    banks, slots, width = 8, 64, 128
+    m0, steps = make_case(banks=banks, slots=slots, width=width, writes=4, reads=16, steps=6,
+                          seed=51)
+    packed = cow.PackedSDMCopyOnWriteState.allocate(m0.to(device), banks=banks,
+                                                    capacity_rows=banks * slots)
+    dense = m0.expand(banks, -1, -1).clone().to(device)
+    oracle = ref.allocate(m0.numpy(), banks=banks, capacity_rows=banks * slots)
+    floats = ("write_weights", "values", "input_gate", "forget_log_gate", "read_weights")
+    for inputs in steps:
+        narrow = {k: (v.to(dtype) if k in floats else v) for k, v in inputs.items()}
+        widened = {k: (v.float() if k in floats else v) for k, v in narrow.items()}
+        got, _ = cow.packed_sdm_cow_step(packed, **to_device(narrow, device))
+        got_dense = cow.dense_sdm_sparse_step(dense, **to_device(narrow, device))
+        assert got.dtype == dtype and got_dense.dtype == dtype
+        want, _ = ref.packed_step(oracle, **to_numpy(widened))
+        want = torch.from_numpy(want).to(dtype)
+        assert torch.equal(got.cpu(), want)
+        assert torch.equal(got_dense.cpu(), want)
+        assert torch.equal(dense, packed.materialize_dense())
+    assert_state_equal(packed, oracle)
