@@ -70,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -195,6 +195,8 @@ class Trace(ctypes.Structure):
         ("control", ctypes.c_void_p),
         ("control_stride", ctypes.c_int64),
         ("report", ctypes.c_void_p),
+        ("first_known", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

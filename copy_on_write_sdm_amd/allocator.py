@@ -2061,7 +2061,10 @@ class DecodeTrace:
         saved = trace.steps_recorded
         trace.steps_recorded = target
         trace.step_index = self._step_index_ptr
-        trace.first_step = 0
+        # every layer's counter stands at `start`: the first launch takes it
+        # from here instead of loading the counter first
+        trace.first_step = start
+        trace.first_known = 1
         if not self._status_clean:
             self.status.zero_()
         self._status_clean = False
@@ -2091,6 +2094,7 @@ class DecodeTrace:
                             launch_steps, mode, stream)
                     finally:
                         trace.report = None
+                    trace.first_known = 0
                     if rc:
                         nat.check(rc, "decode trace run")
                     rows = self._host_report.array.tolist()
@@ -2109,6 +2113,7 @@ class DecodeTrace:
                             timing.append((e0, e1))
                         else:
                             self._call(layers, launch_steps, stream)
+                        trace.first_known = 0
                     rows = self._read_report()      # counters, status, control words
                     positions = rows[0]
                     words = rows[1]   # int32 status word l is half l % 2 of word l // 2
@@ -2148,6 +2153,8 @@ class DecodeTrace:
                 rounds += 1
         finally:
             trace.steps_recorded = saved
+            trace.first_known = 0
+            trace.first_step = 0
         self._positions = [target] * len(self.tables)
         if native and rounds == 0 and not self.dense:
             self._report_versions = self._synced_versions

@@ -50,6 +50,7 @@ constexpr uint32_t kPrefixDone = 1u << 31;
 constexpr int kPlanHead = 8;        // header words (tagged): steps, fit, capacity
 constexpr int kPlanHeadWords = 8;
 constexpr int kPlanSegments = kTraceMaxSteps + 1;   // growth segments of one launch
+constexpr int kPlanLocalWords = 6;  // a short launch's packed count words per bank
 constexpr uint32_t kPlanReady = 1u << 31;            // the plan's steps are in a sync word
 constexpr uint32_t kStatusEmpty = 0;
 constexpr uint32_t kStatusAggregate = 1;
@@ -74,6 +75,7 @@ struct StepParams {
   int64_t* trace_step;           // per-layer device step counters, or null
   int64_t* trace_ticket;         // [1 + layer]: waves of a layer done with the launch
   int64_t trace_first;           // step of this launch when trace_step is null
+  int64_t trace_known;           // every layer's trace_step value when the caller knows it, or -1
   int64_t trace_len;             // steps the trace inputs hold
   int32_t* trace_status;         // per-layer status bits, or null
   int64_t trace_stride[9];
@@ -117,6 +119,18 @@ __device__ __forceinline__ int wave_inclusive(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1 and 3
   v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2 and 3
   return v;
+}
+
+// OR of v over the wave, in every lane (DPP OR scan, lane 63's result)
+__device__ __forceinline__ uint32_t wave_or_all(uint32_t v) {
+  int x = static_cast<int>(v);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(x, kWave - 1));
 }
 
 __device__ __forceinline__ int64_t wave_sum64(int64_t v) {
@@ -205,6 +219,7 @@ struct PlanBlock {
   int64_t* cum;
   int64_t* pops;
   int64_t* segs;   // [S + 1][4]: the growth segments (plan_layer)
+  int64_t* local;  // [kPlanLocalWords][kWave]: short launches' packed count words (k-major)
   int64_t steps;   // S
   __device__ int64_t* word(int bank, int t) const {
     return words + static_cast<int64_t>(bank) * steps + t;
@@ -221,16 +236,25 @@ __device__ __forceinline__ PlanBlock plan_block(const StepParams& P, int layer) 
   pb.cum = pb.totals + S;
   pb.pops = pb.cum + S + 1;
   pb.segs = pb.pops + S * P.banks * P.writes;
+  pb.local = pb.segs + 4 * (S + 1);
   pb.steps = S;
   return pb;
 }
 // The tag of a layer's words in the launch now starting: one past the epoch
 // word, which the layer's last control wave sets to it when the launch ends.
 // Never 0, so that zeroed memory carries no valid word.
-__device__ __forceinline__ uint32_t launch_epoch(const PlanBlock& pb) {
-  const uint32_t e = static_cast<uint32_t>(__hip_atomic_load(
-      const_cast<int64_t*>(pb.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+// the launch's epoch from the layer's epoch word (the last launch's epoch,
+// stored zero-extended: its low half, read on its own, is all of it)
+__device__ __forceinline__ uint32_t epoch_after(uint32_t word) {
+  const uint32_t e = word + 1u;
   return e == 0 ? 1u : e;
+}
+__device__ __forceinline__ uint32_t epoch_word(const PlanBlock& pb) {
+  return __hip_atomic_load(reinterpret_cast<uint32_t*>(pb.epoch), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t launch_epoch(const PlanBlock& pb) {
+  return epoch_after(epoch_word(pb));
 }
 __device__ __forceinline__ uint64_t tagged(uint32_t epoch, uint32_t value) {
   return (static_cast<uint64_t>(epoch) << 32) | value;

@@ -895,6 +895,7 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
   P.trace_step = trace ? trace->step_index : nullptr;
   P.trace_ticket = trace ? trace->ticket : nullptr;
   P.trace_first = trace ? trace->first_step : 0;
+  P.trace_known = trace && trace->step_index && trace->first_known ? trace->first_step : -1;
   P.trace_len = trace ? trace->steps_recorded : 0;
   P.trace_status = trace ? trace->status : nullptr;
   P.scan = planned ? trace->scan : nullptr;
@@ -925,6 +926,10 @@ int32_t run_step(const cowsdm_layer_t* layers, int32_t nlayers,
       for (int32_t done = 0; done < steps; done += launch_steps) {
         P.steps = (steps - done) < launch_steps ? (steps - done) : launch_steps;
         P.trace_first = trace->first_step + done;  // ignored when step_index is set
+        // (a later launch of the call starts where the last one left each
+        // layer's counter, which a refused layer leaves behind)
+        P.trace_known =
+            done == 0 && trace->step_index && trace->first_known ? trace->first_step : -1;
         // count pass: an LDS hash of at least twice the launch's write routes
         int table = 64;
         while (table < 2 * P.steps * P.writes) table *= 2;
@@ -1111,10 +1116,12 @@ int32_t cowsdm_trace_persistent(const cowsdm_layer_t* layers, int32_t nlayers,
 int64_t cowsdm_trace_scan_words(int64_t banks, int64_t writes, int32_t steps) {
   if (banks < 0 || writes < 0 || steps < 0) return -1;
   // epoch and header, plan words [banks][steps], step totals, running
-  // totals, the launch's pops (at most banks * W per step) and its growth
-  // segments (4 words each, at most one per step and the first), int64 each
+  // totals, the launch's pops (at most banks * W per step), its growth
+  // segments (4 words each, at most one per step and the first) and a short
+  // launch's packed count words (kPlanLocalWords rows of one word per bank of
+  // a wave), int64 each
   return kPlanHead + kPlanHeadWords + banks * steps + steps + (steps + 1) + banks * steps * writes +
-         4 * (static_cast<int64_t>(steps) + 1);
+         4 * (static_cast<int64_t>(steps) + 1) + kPlanLocalWords * kWave;
 }
 
 int32_t cowsdm_host_report_alloc(int64_t words, int64_t** host, int64_t** device) {
@@ -1275,12 +1282,16 @@ int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
   if (!host) return fail(COWSDM_EARG, "trace run: the report is not from cowsdm_host_report_alloc");
   for (int32_t l = 0; l < nlayers; ++l) host[l * COWSDM_REPORT_WORDS] = -1;   // not written yet
   hipStream_t s = as_stream(stream);
+  // launches after the first read the counters the one before left
+  cowsdm_trace_t later = *trace;
+  later.first_known = 0;
   for (int64_t done = 0; done < steps; done += launch_steps) {
     const int32_t n = static_cast<int32_t>(steps - done < launch_steps ? steps - done : launch_steps);
+    const cowsdm_trace_t* const t = done == 0 ? trace : &later;
     const int32_t rc =
-        mode == 0 ? cowsdm_packed_step_trace(layers, nlayers, shape, trace, n, stream)
-        : mode == 1 ? cowsdm_packed_step_trace_static(layers, nlayers, shape, trace, n, stream)
-                    : cowsdm_dense_step_trace(layers, nlayers, shape, trace, n, stream);
+        mode == 0 ? cowsdm_packed_step_trace(layers, nlayers, shape, t, n, stream)
+        : mode == 1 ? cowsdm_packed_step_trace_static(layers, nlayers, shape, t, n, stream)
+                    : cowsdm_dense_step_trace(layers, nlayers, shape, t, n, stream);
     if (rc != 0) return rc;
   }
   hipError_t e = hipStreamSynchronize(s);

@@ -333,11 +333,16 @@ void sdm_trace_kernel(StepParams P) {
   const cowsdm_layer_t& L = P.layer[layer_id];
   // Device-counted launches read the layer's first step from its counter
   // (every thread reads the same value: it changes only after all waves of
-  // the layer are done) and run at most the steps recorded after it.
+  // the layer are done), or take it from the caller when it knows where the
+  // counters stand (the control wave of bank 0 then compares the counter
+  // with it once its steps are out, off the critical path), and run at most
+  // the steps recorded after it.
+  const bool known_first = P.trace_step && P.trace_known >= 0;
   int64_t first = P.trace_first;
   int64_t left = P.steps;
   if (P.trace_step) {
-    const uint64_t f = static_cast<uint64_t>(P.trace_step[layer_id]);
+    const uint64_t f = known_first ? static_cast<uint64_t>(P.trace_known)
+                                   : static_cast<uint64_t>(P.trace_step[layer_id]);
     first = static_cast<int64_t>(
         (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(f >> 32))) << 32) |
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(f)));
@@ -1591,7 +1596,7 @@ void sdm_trace_kernel(StepParams P) {
       }
       if (local_try) {
         // the same words packed for the local plan, kLocalStepsPerWord steps
-        // per word, at the end of the bank's row
+        // per word, into the plan block's local rows
         uint32_t packed = 0;
 #pragma unroll
         for (int k = 0; k < kLocalWords; ++k) {
@@ -1826,6 +1831,22 @@ void sdm_trace_kernel(StepParams P) {
   // With a report to write, each control wave first waits for its data wave
   // to finish, so that the last ticket follows every status bit of the layer.
   if (!DENSE || P.trace_step) {
+    // a first step the caller gave that the counter does not hold: the
+    // launch ran the wrong steps (the counter is still the launch's: only
+    // the layer's last wave advances it, after every ticket)
+    if (known_first && bank == 0 && lane == 0 &&
+        __hip_atomic_load(P.trace_step + layer_id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) !=
+            P.trace_known) {
+      if (P.trace_status) {
+        __hip_atomic_fetch_or(&P.trace_status[layer_id], int32_t{COWSDM_TRACE_FAULT},
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if constexpr (!DENSE) {
+        __hip_atomic_fetch_or(&L.scratch[COWSDM_SCRATCH_ERRORS],
+                              static_cast<int64_t>(COWSDM_ERR_TRACE_RANGE), __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     if (P.report) {
       bool finished = false;
       for (int spins = 0; spins < 64 * kSpinLimit && !finished; ++spins) {

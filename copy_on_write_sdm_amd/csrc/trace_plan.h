@@ -188,20 +188,22 @@ constexpr int kLocalPlanSteps = 32;
 constexpr int kLocalBits = 5;   // a count word: 4 first-touch lanes and the stop bit
 constexpr int kLocalStepsPerWord = 32 / kLocalBits;
 constexpr int kLocalWords = (kLocalPlanSteps + kLocalStepsPerWord - 1) / kLocalStepsPerWord;
+static_assert(kLocalWords <= kPlanLocalWords, "the plan block's local rows hold every packed word");
 
 __host__ __device__ constexpr int local_words(int steps) {
   return (steps + kLocalStepsPerWord - 1) / kLocalStepsPerWord;
 }
-// packed word k of a bank: the row's last words, which a launch of at most
-// steps - kLocalWords steps does not use
+// packed word k of a bank: row k of the plan block's local words, one word
+// per bank, so that a wave reading every bank's word k (lane = bank) reads
+// one contiguous row
 __device__ __forceinline__ int64_t* local_word(const PlanBlock& pb, int bank, int k) {
-  return pb.word(bank, static_cast<int>(pb.steps) - 1 - k);
+  return pb.local + k * kWave + bank;
 }
 
-// Whether a launch of G0 steps over B banks takes the local plan first (its
-// packed words fit past its steps in each bank's row of plan words).
+// Whether a launch of G0 steps over B banks takes the local plan first.
 __device__ __forceinline__ bool local_plan_fits(int G0, int B, const PlanBlock& pb) {
-  return G0 <= kLocalPlanSteps && B <= kWave && G0 + local_words(G0) <= pb.steps;
+  (void)pb;
+  return G0 <= kLocalPlanSteps && B <= kWave;
 }
 
 struct LocalPlan {
@@ -235,63 +237,92 @@ __device__ inline int plan_local(const PlanBlock& pb, int B, int G0, uint32_t ep
       if (k < nw && in && !tag_is(w[k], epoch)) w[k] = atomic_load_u64(local_word(pb, lane, k));
     }
   }
-  // the first touches of the lower banks and each step's total: the banks'
-  // counts (lane = bank) packed kSumSteps steps to an int in 9-bit fields
-  // (a sum over 64 banks of at most 4 each fits), so one scan across the
-  // wave serves kSumSteps steps; then step by step (wave-uniform), lane t
-  // keeping step t's running total and this bank's plan word
+  // The first touches of the lower banks at each step (pre) and the step's
+  // total over all banks (tot), word by word (lane = bank): a step that no
+  // bank first-touches adds nothing, so only the word's active steps are
+  // summed, by ballots of their first-touch lanes when they are few, else by
+  // two scans across the wave of three steps each, packed in 9-bit fields
+  // (a sum over 64 banks of at most 4 each fits).  Lane t keeps the running
+  // total before step t (cum_l), the lower banks' first touches at step t
+  // (pre_l) and this bank's count word of step t (own_l).
   constexpr int kSumBits = 9;
   constexpr int kSumSteps = 3;
-  constexpr int kSums = (kLocalPlanSteps + kSumSteps - 1) / kSumSteps;
-  auto count_word = [&](int t) __attribute__((always_inline)) -> uint32_t {
-    return (static_cast<uint32_t>(w[t / kLocalStepsPerWord]) >>
-            (kLocalBits * (t % kLocalStepsPerWord))) & ((1u << kLocalBits) - 1);
+  constexpr int kBallotSteps = 3;   // active steps of a word summed by ballots
+  constexpr uint32_t kField = (1u << kLocalBits) - 1;
+  constexpr uint32_t kTouchFields = [] {
+    uint32_t m = 0;
+    for (int i = 0; i < kLocalStepsPerWord; ++i) m |= 15u << (kLocalBits * i);
+    return m;
+  }();
+  const uint64_t lower = (uint64_t{1} << bank) - 1;   // bank < kWave
+  const int lane_word = lane / kLocalStepsPerWord;
+  const int lane_shift = kLocalBits * (lane % kLocalStepsPerWord);
+  int cum_l = 0;
+  int pre_l = 0;
+  int cum_g = 0;
+  uint32_t own_l = 0;
+  auto add_step = [&](int t, int pre, int tot) __attribute__((always_inline)) {
+    if (lane == t) pre_l = pre;
+    if (lane > t) cum_l += tot;
+    cum_g += tot;
   };
-  uint32_t own_words[kLocalWords];   // this bank's packed count words
 #pragma unroll
   for (int k = 0; k < kLocalWords; ++k) {
-    own_words[k] = k < nw ? static_cast<uint32_t>(__builtin_amdgcn_readlane(
-                                static_cast<int>(static_cast<uint32_t>(w[k])), bank))
-                          : 0u;
-  }
-  int cum = 0;
-  int cum_l = 0;
-  uint32_t word_l = 0;
+    if (k < nw) {
+      const uint32_t lo = static_cast<uint32_t>(w[k]);
+      const uint32_t own = static_cast<uint32_t>(
+          __builtin_amdgcn_readlane(static_cast<int>(lo), bank));
+      if (lane_word == k) own_l = (own >> lane_shift) & kField;
+      const int steps_here = G0 - k * kLocalStepsPerWord;
+      const uint32_t valid =
+          steps_here >= kLocalStepsPerWord ? ~0u : (1u << (kLocalBits * steps_here)) - 1;
+      uint32_t act = wave_or_all(lo) & kTouchFields & valid;
+      // one bit per active field
+      uint32_t fields = 0;
 #pragma unroll
-  for (int g = 0; g < kSums; ++g) {
-    if (g * kSumSteps < G0) {
-      int packed = 0;
-#pragma unroll
-      for (int i = 0; i < kSumSteps; ++i) {
-        const int t = g * kSumSteps + i;
-        if (t < kLocalPlanSteps && t < G0) {
-          packed += __popc(count_word(t) & 15u) << (kSumBits * i);
-        }
+      for (int f = 0; f < kLocalStepsPerWord; ++f) {
+        if ((act >> (kLocalBits * f)) & 15u) fields |= 1u << f;
       }
-      const int incl = wave_inclusive(packed);
-      const uint32_t lower = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - packed, bank));
-      const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl, kWave - 1));
+      if (__popc(fields) <= kBallotSteps) {
+        while (fields != 0) {
+          const int f = __builtin_ctz(fields);
+          fields &= fields - 1;
+          int pre = 0, tot = 0;
 #pragma unroll
-      for (int i = 0; i < kSumSteps; ++i) {
-        const int t = g * kSumSteps + i;
-        if (t < kLocalPlanSteps && t < G0) {
-          const int pre = static_cast<int>((lower >> (kSumBits * i)) & ((1u << kSumBits) - 1));
-          const int tot = static_cast<int>((total >> (kSumBits * i)) & ((1u << kSumBits) - 1));
-          const uint32_t own = (own_words[t / kLocalStepsPerWord] >>
-                                (kLocalBits * (t % kLocalStepsPerWord))) & ((1u << kLocalBits) - 1);
-          const uint32_t base = static_cast<uint32_t>(cum + pre);
-          const uint32_t word = (base & kPlanBaseMask) | ((own & 15u) << kPlanMaskShift) |
-                                ((own & kCountStop) ? 1u << kPlanStopBit : 0u);
-          if (lane == t) {
-            cum_l = cum;
-            word_l = word;
+          for (int j = 0; j < 4; ++j) {
+            const uint64_t m = __ballot((lo >> (kLocalBits * f + j)) & 1u);
+            pre += __popcll(m & lower);
+            tot += __popcll(m);
           }
-          cum += tot;
+          add_step(k * kLocalStepsPerWord + f, pre, tot);
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < kLocalStepsPerWord / kSumSteps; ++h) {
+          int packed = 0;
+#pragma unroll
+          for (int i = 0; i < kSumSteps; ++i) {
+            const int f = h * kSumSteps + i;
+            packed += __popc((lo >> (kLocalBits * f)) & 15u) << (kSumBits * i);
+          }
+          const int incl = wave_inclusive(packed);
+          const uint32_t lw = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl - packed, bank));
+          const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(incl, kWave - 1));
+#pragma unroll
+          for (int i = 0; i < kSumSteps; ++i) {
+            const int t = k * kLocalStepsPerWord + h * kSumSteps + i;
+            if (t < G0) {
+              add_step(t, static_cast<int>((lw >> (kSumBits * i)) & ((1u << kSumBits) - 1)),
+                       static_cast<int>((total >> (kSumBits * i)) & ((1u << kSumBits) - 1)));
+            }
+          }
         }
       }
     }
   }
-  const int cum_g = cum;
+  const uint32_t word_l =
+      (static_cast<uint32_t>(cum_l + pre_l) & kPlanBaseMask) | ((own_l & 15u) << kPlanMaskShift) |
+      ((own_l & kCountStop) ? 1u << kPlanStopBit : 0u);
   auto cum_at = [&](int s) __attribute__((always_inline)) -> int {
     return s >= G0 ? cum_g : __builtin_amdgcn_readlane(cum_l, s);
   };

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 8
+#define COWSDM_ABI_VERSION 9
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -136,7 +136,12 @@ typedef struct cowsdm_layer {
  * Device counters (step_index set, nlayers int64 counters): layer l runs up
  * to `steps` steps from step_index[l], never past steps_recorded, and the
  * kernels advance step_index[l] by the steps it ran, so the call can be
- * captured once in a hipGraph and replayed.  ticket points at 1 + nlayers
+ * captured once in a hipGraph and replayed.  A caller that knows where the
+ * counters stand (every layer's the same) may say so: first_known nonzero
+ * and the value in first_step.  Persistent launches then take their first
+ * step from there rather than waiting for the counter's load before their
+ * first input loads, and still compare it with the counter (a mismatch sets
+ * COWSDM_TRACE_FAULT); a call of several launches does so for its first.  ticket points at 1 + nlayers
  * int64 words that are zero before the first launch and stay zero between
  * launches.  A layer with no step left runs nothing and sets
  * COWSDM_TRACE_ENDED in status[l] (status null, packed state:
@@ -180,6 +185,8 @@ typedef struct cowsdm_trace {
   int64_t* control;         /* packed persistent launches, see above */
   int64_t control_stride;
   int64_t* report;          /* host-mapped report (COWSDM_REPORT_WORDS per layer), or null */
+  int32_t first_known;      /* nonzero: every step_index[l] holds first_step (see above) */
+  int32_t reserved;
 } cowsdm_trace_t;
 
 /* Control words of one layer of a packed decode trace (int64, word k of

@@ -38,11 +38,11 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 8
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 9
     # epoch and header, plan words [banks][steps], step and running totals,
     # at most banks * W pops per step and 4 words per growth segment, int64 each
     assert lib.cowsdm_trace_scan_words(64, 4, 512) == (16 + 64 * 512 + 512 + 513 + 64 * 512 * 4
-                                                       + 4 * 513)
+                                                       + 4 * 513 + 6 * 64)
     assert lib.cowsdm_trace_scan_words(-1, 4, 512) == -1
     assert lib.cowsdm_step_scratch_words(64) == 8 + 64
     assert lib.cowsdm_step_scratch_words(-1) == -1
@@ -117,7 +117,7 @@ def test_structure_layout_matches_header():
     assert ctypes.sizeof(nat.Layer) == 21 * 8 + 3 * 8 + 8 + 2 * 4
     assert nat.Layer.map_directory.offset == 21 * 8
     assert ctypes.sizeof(nat.Shape) == 7 * 8
-    assert ctypes.sizeof(nat.Trace) == 20 * 8
+    assert ctypes.sizeof(nat.Trace) == 21 * 8
     assert ctypes.sizeof(nat.Recurrence) == 14 * 8
     assert ctypes.sizeof(nat.Controller) == 15 * 8 + 2 * 4
     assert nat.REPORT_WORDS == 2 + nat.CTRL_WORDS == 14

@@ -540,3 +540,42 @@ def test_short_launches_plan_locally(device, banks, launch_steps):
     states, headers = case(banks * writes, banks * writes)
     assert all(headers[0])
     assert all(st.growth_events > 0 for st in states)
+
+
+def test_known_first_step_checked_against_counters(device):
+    """run() hands the kernel the step every layer's counter stands at, so
+    that a launch's first loads need not wait for the counter.  The kernel
+    still compares the two: a first step the counters do not hold (here a
+    stale host position) stops the run with a fault instead of passing
+    silently, and a correct one matches the reference loop."""
+
+    layers, banks, slots, width, writes, reads = 2, 8, 32, 64, 4, 8
+    steps = 24
+    m0 = synthetic.make_initial_memory(layers, 1, slots, width, seed=61, device=device)
+    routes = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots,
+                                  width=width, writes=writes, reads=reads, seed=62, device=device)
+    kw = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
+              values=routes.values, input_gate=routes.input_gate,
+              forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
+              read_weights=routes.read_weights)
+    capacity = banks * slots
+    states = [cow.PackedSDMCopyOnWriteState.allocate(
+        m0[l], banks=banks, capacity_rows=capacity, growth_quantum_rows=banks * writes)
+        for l in range(layers)]
+    oracles = [ref.allocate(m0[l].cpu().numpy(), banks=banks, capacity_rows=capacity,
+                            growth_quantum_rows=banks * writes) for l in range(layers)]
+    outputs = torch.empty(steps, layers, banks, width, device=device)
+    tr = cow.DecodeTrace(states=states, outputs=outputs, **kw)
+    tr.reserve_steps(steps)
+    tr.run(8, launch_steps=8)
+    tr.run(8, launch_steps=4)
+    want = oracle_decode_loop(oracles, routes, 16, need=banks * writes)
+    torch.cuda.synchronize()
+    assert np.array_equal(outputs[:16].cpu().numpy(), want)
+    for st, orc in zip(states, oracles):
+        assert_state_equal(st, orc)
+    assert tr.step_index.tolist() == [16] * layers
+    # a stale host position: the counters stand at 16, the host says 18
+    tr._positions = [18] * layers
+    with pytest.raises(RuntimeError, match="fault"):
+        tr.run(4, launch_steps=4)
