@@ -358,18 +358,18 @@ def main() -> int:
         handoff_first_ms = None
         for _ in range(2):
             t0 = time.perf_counter()
-            masks = []
-            for l in range(LAYERS):
-                active = torch.zeros(banks, SLOTS, dtype=torch.bool, device=dev)
-                cow.mark_written(active,
-                                 prefix.write_indices[:, l].permute(1, 0, 2).reshape(banks, -1))
-                masks.append(active)
+            # every layer's written slots in one mask (a layer's rows are its
+            # banks), one launch
+            active = torch.zeros(LAYERS * banks, SLOTS, dtype=torch.bool, device=dev)
+            cow.mark_written(active, prefix.write_indices.permute(1, 2, 0, 3).reshape(
+                LAYERS * banks, -1))
+            masks = list(active.view(LAYERS, banks, SLOTS))
             # every layer's handoff at once: one read of the active counts and
             # one of the invariant checks for all layers
             states = cow.PackedSDMCopyOnWriteState.from_dense_overlay_layers(
                 [m0[l] for l in range(LAYERS)], tables, masks, template_indices=templates,
                 growth_quantum_rows=quantum)
-            del masks
+            del masks, active
             torch.cuda.synchronize()
             handoff_ms = 1000.0 * (time.perf_counter() - t0)
             if handoff_first_ms is None:

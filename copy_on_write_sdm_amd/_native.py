@@ -70,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -245,6 +245,31 @@ class Recurrence(ctypes.Structure):
     ]
 
 
+class HandoffLayer(ctypes.Structure):
+    """cowsdm_handoff_layer_t."""
+
+    _fields_ = [
+        ("dense_memory", ctypes.c_void_p),
+        ("active_mask", ctypes.c_void_p),
+        ("banks", ctypes.c_int64),
+        ("slots", ctypes.c_int64),
+        ("width", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("total", ctypes.c_void_p),
+        ("template_indices", ctypes.c_void_p),
+        ("templates", ctypes.c_int64),
+        ("checks", ctypes.c_void_p),
+        ("logical_to_physical", ctypes.c_void_p),
+        ("values", ctypes.c_void_p),
+        ("free_rows", ctypes.c_void_p),
+        ("capacity_rows", ctypes.c_int64),
+        ("free_count", ctypes.c_void_p),
+        ("overflow_flag", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_words", ctypes.c_int64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I32 = ctypes.c_int32
@@ -295,6 +320,8 @@ SIGNATURES: dict[str, tuple] = {
         _I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P]),
     "cowsdm_grow": (_I32, [_P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "cowsdm_count_active": (_I32, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_handoff_count": (_I32, [_P, _I32, _P]),
+    "cowsdm_handoff_pack": (_I32, [_P, _I32, _P]),
     "cowsdm_paged_count": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P, _P]),
     "cowsdm_paged_compress": (_I32, [_P, _I64, _I64, _I32, _P, _P, _P, _P, _I64, _P, _P]),
     "cowsdm_paged_expand": (_I32, [_P, _P, _I64, _I64, _I64, _I32, _P, _P]),

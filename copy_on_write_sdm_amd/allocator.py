@@ -33,6 +33,7 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
+import ctypes
 from contextlib import contextmanager
 from dataclasses import dataclass, field
 from typing import Any, Sequence
@@ -325,9 +326,12 @@ class PackedSDMCopyOnWriteState:
     @classmethod
     def _allocate_state(cls, shared_initial_memory, *, banks, capacity_rows,
                         template_indices=None, state_dtype=torch.float32,
-                        growth_quantum_rows=0, map_page_slots=None, result=None):
+                        growth_quantum_rows=0, map_page_slots=None, result=None,
+                        initialize=True):
         """``allocate`` with the template check's result word left on the
-        device (``result``, int64, or a new one): the caller reads it."""
+        device (``result``, int64, or a new one): the caller reads it.  With
+        ``initialize`` False the state's tensors are left for the caller's
+        kernels to fill (no template check either)."""
 
         if shared_initial_memory.ndim == 2:
             shared_initial_memory = shared_initial_memory.unsqueeze(0)
@@ -374,6 +378,8 @@ class PackedSDMCopyOnWriteState:
                 int(nat.lib().cowsdm_step_scratch_words(banks)), device=device,
                 dtype=torch.int64),
         )
+        if not initialize:
+            return state, None
         if result is None:
             result = torch.empty(1, device=device, dtype=torch.int64)
         nat.check(
@@ -475,24 +481,39 @@ class PackedSDMCopyOnWriteState:
             return []
         device = prepared[0][1].device
         stream = nat.stream_handle(device)
-        # every layer's active count, read once; each workspace keeps the ranks
-        # its count leaves for the pack, with room for a slab of every slot
-        totals = torch.empty(layers, device=device, dtype=torch.int64)
-        workspaces = []
-        for (m0, dense, mask), total in zip(prepared, totals):
+        # The count part of every layer in two launches (cowsdm_handoff_count),
+        # one read of the active counts, every layer's state allocated, and
+        # the pack, free stack and invariant counts of every layer in five
+        # launches (cowsdm_handoff_pack), then one read of the checks.  Each
+        # layer's workspace (one allocation carved for all) keeps the ranks
+        # its count leaves for the pack, with room for a slab of every slot.
+        lib = nat.lib()
+        entries = (nat.HandoffLayer * layers)()
+        rows = []
+        offsets = [0]
+        for (m0, dense, mask) in prepared:
             banks, slots, _ = dense.shape
-            rows = max(banks * slots, max((c for c in capacities if c is not None), default=0))
-            workspace = _workspace(banks * slots, rows, device)
-            workspaces.append((workspace, rows))
-            nat.check(
-                nat.lib().cowsdm_count_active(
-                    None, banks, slots, None, banks, mask.data_ptr(), workspace.data_ptr(),
-                    total.data_ptr(), stream),
-                "cowsdm_count_active",
-            )
+            r = max(banks * slots, max((c for c in capacities if c is not None), default=0))
+            rows.append(r)
+            offsets.append(offsets[-1] + -(-int(lib.cowsdm_workspace_bytes(banks * slots, r)) // 256) * 256)
+        workspace = torch.empty(max(offsets[-1], 256), dtype=torch.uint8, device=device)
+        totals = torch.empty(layers, device=device, dtype=torch.int64)
+        checks = torch.empty(layers, 9, device=device, dtype=torch.int64)
+        tmpl = template_indices.to(torch.int64).contiguous()
+        keep = [workspace, totals, checks, tmpl]
+        for l, (m0, dense, mask) in enumerate(prepared):
+            e = entries[l]
+            e.dense_memory = dense.data_ptr()
+            e.active_mask = mask.data_ptr()
+            e.banks, e.slots, e.width = dense.shape
+            e.workspace = workspace.data_ptr() + offsets[l]
+            e.total = totals.data_ptr() + 8 * l
+            e.template_indices = tmpl.data_ptr()
+            e.templates = m0.shape[0]
+            e.checks = checks.data_ptr() + 72 * l
+        nat.check(lib.cowsdm_handoff_count(entries, layers, stream), "cowsdm_handoff_count")
         counts = totals.tolist()
         states = []
-        checks = torch.empty(layers, 9, device=device, dtype=torch.int64)
         for l, ((m0, dense, mask), active_count) in enumerate(zip(prepared, counts)):
             banks, slots, width = dense.shape
             selected, possible = handoff_capacity(
@@ -501,35 +522,33 @@ class PackedSDMCopyOnWriteState:
             state, _ = cls._allocate_state(
                 m0, banks=banks, capacity_rows=selected, template_indices=template_indices,
                 state_dtype=state_dtype, growth_quantum_rows=growth_quantum_rows,
-                result=checks[l, 8:])
-            workspace, rows = workspaces[l]
-            if rows < selected:
+                initialize=False)
+            e = entries[l]
+            if rows[l] < selected:
                 # a slab larger than the workspace's lists: count again into one
-                workspace = _workspace(banks * slots, selected, device)
-                total = torch.empty(1, device=device, dtype=torch.int64)
-                nat.check(
-                    nat.lib().cowsdm_count_active(
-                        None, banks, slots, None, banks, mask.data_ptr(),
-                        workspace.data_ptr(), total.data_ptr(), stream),
-                    "cowsdm_count_active",
-                )
-            nat.check(
-                nat.lib().cowsdm_pack_overlay(
-                    dense.data_ptr(), mask.data_ptr(), banks, slots, width,
-                    state.logical_to_physical.data_ptr(), state.values.data_ptr(),
-                    state.free_rows.data_ptr(), selected, state.free_count.data_ptr(),
-                    workspace.data_ptr(), stream),
-                "cowsdm_pack_overlay",
-            )
+                own = _workspace(banks * slots, selected, device)
+                keep.append(own)
+                e.workspace = own.data_ptr()
+                nat.check(lib.cowsdm_handoff_count(ctypes.byref(e), 1, stream),
+                          "cowsdm_handoff_count")
+            e.logical_to_physical = state.logical_to_physical.data_ptr()
+            e.values = state.values.data_ptr()
+            e.free_rows = state.free_rows.data_ptr()
+            e.capacity_rows = selected
+            e.free_count = state.free_count.data_ptr()
+            e.overflow_flag = state.overflow_flag.data_ptr()
+            e.scratch = state.scratch.data_ptr()
+            e.scratch_words = state.scratch.numel()
             state.capacity_is_proven = maximum_future_allocations is not None
             state.proven_maximum_additional_allocations = possible
-            state._launch_invariants(checks[l, :8])
             states.append(state)
+        nat.check(lib.cowsdm_handoff_pack(entries, layers, stream), "cowsdm_handoff_pack")
         # the template checks and every layer's invariants, read once
         for state, words in zip(states, checks.tolist()):
             if words[8] & nat.ERR_TEMPLATE:
                 raise ValueError("template index lies outside shared initial memory")
             state._judge_invariants(words[:8])
+        del keep
         if map_page_slots is not None:
             for state in states:
                 state.to_paged_map(map_page_slots)

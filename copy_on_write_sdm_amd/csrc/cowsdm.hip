@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 #include <stdint.h>
@@ -190,7 +191,7 @@ __global__ void init_state_kernel(int32_t* map, int64_t map_entries,
   }
 }
 
-__global__ __launch_bounds__(256) void check_templates_kernel(
+__device__ __forceinline__ void check_templates_body(
     const int64_t* tmpl, int64_t banks, int64_t templates, int64_t* result) {
   __shared__ int s_bad;
   if (threadIdx.x == 0) s_bad = 0;
@@ -203,10 +204,14 @@ __global__ __launch_bounds__(256) void check_templates_kernel(
   __syncthreads();
   if (threadIdx.x == 0) *result = s_bad ? COWSDM_ERR_TEMPLATE : 0;
 }
+__global__ __launch_bounds__(256) void check_templates_kernel(
+    const int64_t* tmpl, int64_t banks, int64_t templates, int64_t* result) {
+  check_templates_body(tmpl, banks, templates, result);
+}
 
 // Row copy dst[dst_rows[i]] = src[src_rows[i]] for i < *count (null row
 // lists mean identity); float4 when the width allows it.
-__global__ void copy_rows_kernel(float* dst, const int32_t* dst_rows,
+__device__ __forceinline__ void copy_rows_body(float* dst, const int32_t* dst_rows,
                                  const float* src, const int32_t* src_rows,
                                  const int64_t* count_ptr, int64_t count_max,
                                  int64_t width) {
@@ -230,6 +235,12 @@ __global__ void copy_rows_kernel(float* dst, const int32_t* dst_rows,
       dst[d * width + c] = src[s * width + c];
     }
   }
+}
+__global__ void copy_rows_kernel(float* dst, const int32_t* dst_rows,
+                                 const float* src, const int32_t* src_rows,
+                                 const int64_t* count_ptr, int64_t count_max,
+                                 int64_t width) {
+  copy_rows_body(dst, dst_rows, src, src_rows, count_ptr, count_max, width);
 }
 
 __global__ void copy_i64_kernel(int64_t* dst, const int64_t* src, int64_t n) {
@@ -319,7 +330,7 @@ __device__ __forceinline__ bool rank_active(const RankSource& s, int64_t e) {
   return row >= 0 && s.map[row * s.slots + e % s.slots] >= 0;
 }
 
-__global__ __launch_bounds__(kTileThreads) void rank_count_kernel(
+__device__ __forceinline__ void rank_count_body(
     RankSource s, int32_t* tile_count) {
   __shared__ int s_sum;
   if (threadIdx.x == 0) s_sum = 0;
@@ -335,9 +346,13 @@ __global__ __launch_bounds__(kTileThreads) void rank_count_kernel(
   __syncthreads();
   if (threadIdx.x == 0) tile_count[blockIdx.x] = s_sum;
 }
+__global__ __launch_bounds__(kTileThreads) void rank_count_kernel(
+    RankSource s, int32_t* tile_count) {
+  rank_count_body(s, tile_count);
+}
 
 // Exclusive scan of tile counts by one workgroup; writes the total.
-__global__ __launch_bounds__(1024) void rank_scan_kernel(
+__device__ __forceinline__ void rank_scan_body(
     const int32_t* tile_count, int32_t* tile_offset, int64_t ntiles,
     int64_t* total) {
   __shared__ int64_t s_part[1024];
@@ -360,6 +375,11 @@ __global__ __launch_bounds__(1024) void rank_scan_kernel(
     run += tile_count[i];
   }
   if (threadIdx.x == blockDim.x - 1) *total = s_part[threadIdx.x];
+}
+__global__ __launch_bounds__(1024) void rank_scan_kernel(
+    const int32_t* tile_count, int32_t* tile_offset, int64_t ntiles,
+    int64_t* total) {
+  rank_scan_body(tile_count, tile_offset, ntiles, total);
 }
 
 enum RankOp : int32_t {
@@ -389,7 +409,7 @@ struct RankApply {
 };
 
 // Rank each active entry in ranked order and apply the operation.
-__global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
+__device__ __forceinline__ void rank_apply_body(
     RankSource s, const int32_t* tile_offset, RankApply a) {
   __shared__ int s_scan[kTileThreads];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile + threadIdx.x * kPerThread;
@@ -476,6 +496,10 @@ __global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
     }
     if (act[k]) ++rank;
   }
+}
+__global__ __launch_bounds__(kTileThreads) void rank_apply_kernel(
+    RankSource s, const int32_t* tile_offset, RankApply a) {
+  rank_apply_body(s, tile_offset, a);
 }
 
 // Paged maps: page g of bank b holds a mapped slot (flags over [B * N / P]).
@@ -642,7 +666,7 @@ __device__ __forceinline__ void wave_add_stat(int64_t* target, unsigned long lon
   }
 }
 
-__global__ void own_map_kernel(const int32_t* map, int64_t entries,
+__device__ __forceinline__ void own_map_body(const int32_t* map, int64_t entries,
                                int64_t capacity, int32_t* counts,
                                int64_t* stats) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -658,8 +682,13 @@ __global__ void own_map_kernel(const int32_t* map, int64_t entries,
   wave_add_stat(&stats[0], live);
   wave_add_stat(&stats[5], outside);
 }
+__global__ void own_map_kernel(const int32_t* map, int64_t entries,
+                               int64_t capacity, int32_t* counts,
+                               int64_t* stats) {
+  own_map_body(map, entries, capacity, counts, stats);
+}
 
-__global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_count,
+__device__ __forceinline__ void own_free_body(const int32_t* free_rows, const int32_t* free_count,
                                 int64_t capacity, int32_t* counts, int64_t* stats) {
   int64_t f = *free_count;
   if (f < 0) f = 0;
@@ -675,8 +704,12 @@ __global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_co
   wave_add_stat(&stats[5], outside);
   if (t0 == 0) stats[1] = f;
 }
+__global__ void own_free_kernel(const int32_t* free_rows, const int32_t* free_count,
+                                int64_t capacity, int32_t* counts, int64_t* stats) {
+  own_free_body(free_rows, free_count, capacity, counts, stats);
+}
 
-__global__ void own_eval_kernel(const int32_t* counts, int64_t capacity,
+__device__ __forceinline__ void own_eval_body(const int32_t* counts, int64_t capacity,
                                 const int32_t* overflow, const int64_t* scratch,
                                 int64_t* stats) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -697,6 +730,11 @@ __global__ void own_eval_kernel(const int32_t* counts, int64_t capacity,
     stats[6] = *overflow;
     stats[7] = scratch ? scratch[COWSDM_SCRATCH_ERRORS] : 0;
   }
+}
+__global__ void own_eval_kernel(const int32_t* counts, int64_t capacity,
+                                const int32_t* overflow, const int64_t* scratch,
+                                int64_t* stats) {
+  own_eval_body(counts, capacity, overflow, scratch, stats);
 }
 
 template <typename IDX>
@@ -1086,6 +1124,161 @@ int64_t* report_host(const int64_t* device) {
   std::lock_guard<std::mutex> hold(g_report_lock);
   auto it = g_report_host.find(device);
   return it == g_report_host.end() ? nullptr : it->second;
+}
+
+// ---- the handoff of several layers at once (cowsdm_handoff_count/_pack):
+// blockIdx.y is the layer, and each kernel runs the per-layer bodies above
+struct HandoffBatch {
+  cowsdm_handoff_layer_t layer[kMaxLayers];
+  Workspace ws[kMaxLayers];
+  int64_t entries[kMaxLayers];   // B * N
+  int64_t ntiles[kMaxLayers];
+};
+
+__global__ __launch_bounds__(kTileThreads) void handoff_count_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  if (blockIdx.x >= b.ntiles[l]) return;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  const RankSource s{nullptr, nullptr, L.active_mask, L.slots, b.entries[l], L.banks};
+  rank_count_body(s, b.ws[l].tile_count);
+}
+
+// the tile offsets and total of each layer, and its template check
+__global__ __launch_bounds__(1024) void handoff_scan_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  rank_scan_body(b.ws[l].tile_count, b.ws[l].tile_offset, b.ntiles[l], b.ws[l].total);
+  // (the thread that wrote the workspace's total)
+  if (threadIdx.x == blockDim.x - 1) *L.total = *b.ws[l].total;
+  check_templates_body(L.template_indices, L.banks, L.templates, L.checks + 8);
+}
+
+// scratch, overflow flag, invariant words and the invariant counts cleared
+__global__ void handoff_prep_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = t0; i < L.scratch_words; i += stride) L.scratch[i] = 0;
+  for (int64_t i = t0; i < L.capacity_rows; i += stride) b.ws[l].list_b[i] = 0;
+  if (t0 < 8) L.checks[t0] = 0;
+  if (t0 == 0) *L.overflow_flag = 0;
+}
+
+// map entries: active pairs in row-major order get rows 0..A-1
+__global__ __launch_bounds__(kTileThreads) void handoff_apply_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  if (blockIdx.x >= b.ntiles[l]) return;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  const RankSource s{nullptr, nullptr, L.active_mask, L.slots, b.entries[l], L.banks};
+  RankApply a{};
+  a.op = kOpPack;
+  a.map_out = L.logical_to_physical;
+  a.list_a = b.ws[l].list_a;
+  a.list_rows = L.capacity_rows;
+  a.capacity = L.capacity_rows;
+  rank_apply_body(s, b.ws[l].tile_offset, a);
+}
+
+// the rows (values[r] = dense[list_a[r]] for r < A) and the free stack
+// (free_rows[i] = A + i for i < C - A, i after; free_count = C - A)
+__global__ void handoff_rows_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  const Workspace& w = b.ws[l];
+  copy_rows_body(L.values, nullptr, L.dense_memory, w.list_a, w.total, L.capacity_rows, L.width);
+  const int64_t a = *w.total;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = t0; i < L.capacity_rows; i += stride) {
+    L.free_rows[i] = static_cast<int32_t>(i < L.capacity_rows - a ? a + i : i);
+  }
+  if (t0 == 0) *L.free_count = static_cast<int32_t>(L.capacity_rows - a);
+}
+
+// the invariant counts: each row's owners and free-stack entries ...
+__global__ void handoff_own_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  own_map_body(L.logical_to_physical, b.entries[l], L.capacity_rows, b.ws[l].list_b, L.checks);
+  own_free_body(L.free_rows, L.free_count, L.capacity_rows, b.ws[l].list_b, L.checks);
+}
+
+// ... and the checks on them
+__global__ void handoff_eval_kernel(HandoffBatch b) {
+  const int l = blockIdx.y;
+  const cowsdm_handoff_layer_t& L = b.layer[l];
+  own_eval_body(b.ws[l].list_b, L.capacity_rows, L.overflow_flag, L.scratch, L.checks);
+}
+
+int32_t check_handoff_layer(const cowsdm_handoff_layer_t& L, bool pack) {
+  if (!L.dense_memory || !L.active_mask || !L.workspace || !L.total || !L.checks ||
+      (L.banks > 0 && !L.template_indices) || L.banks < 0 || L.slots <= 0 || L.width <= 0 ||
+      L.templates <= 0) {
+    return fail(COWSDM_EARG, "handoff: invalid layer arguments");
+  }
+  if (L.banks * L.slots >= (1ll << 31)) return fail(COWSDM_ELIMIT, "handoff: too many entries");
+  if (pack && (!L.logical_to_physical || !L.values || !L.free_rows || !L.free_count ||
+               !L.overflow_flag || L.capacity_rows <= 0 || L.capacity_rows >= (1ll << 31) ||
+               L.scratch_words < 0 || (L.scratch_words > 0 && !L.scratch))) {
+    return fail(COWSDM_EARG, "handoff: invalid state arguments");
+  }
+  return 0;
+}
+
+// Launches of the count (pack: false) or pack part over groups of up to
+// kMaxLayers layers.
+int32_t run_handoff(const cowsdm_handoff_layer_t* layers, int32_t n, bool pack,
+                    hipStream_t s) {
+  if (!layers || n < 0) return fail(COWSDM_EARG, "handoff: no layers");
+  for (int32_t i = 0; i < n; ++i) {
+    if (int32_t e = check_handoff_layer(layers[i], pack)) return e;
+  }
+  for (int32_t start = 0; start < n; start += kMaxLayers) {
+    const int32_t g = n - start < kMaxLayers ? n - start : kMaxLayers;
+    HandoffBatch b{};
+    int64_t tiles = 1, vecs = 1, work = 1;
+    for (int32_t i = 0; i < g; ++i) {
+      const cowsdm_handoff_layer_t& L = layers[start + i];
+      b.layer[i] = L;
+      b.entries[i] = L.banks * L.slots;
+      b.ntiles[i] = num_tiles(b.entries[i]);
+      // (the count carves no row lists; the pack the capacity's two)
+      b.ws[i] = carve(L.workspace, b.entries[i], pack ? L.capacity_rows : 0);
+      tiles = b.ntiles[i] > tiles ? b.ntiles[i] : tiles;
+      if (pack) {
+        // the row copy's float4s (or floats); every other pass runs over
+        // the entries, the rows or the scratch words
+        const int64_t v = L.capacity_rows * (L.width % 4 == 0 ? L.width / 4 : L.width);
+        vecs = v > vecs ? v : vecs;
+        const int64_t w = std::max({b.entries[i], L.capacity_rows, L.scratch_words});
+        work = w > work ? w : work;
+      }
+    }
+    const dim3 tile_grid(static_cast<unsigned>(tiles), static_cast<unsigned>(g));
+    const dim3 grid(static_cast<unsigned>(grid_for(work, 256)), static_cast<unsigned>(g));
+    const dim3 row_grid(static_cast<unsigned>(grid_for(vecs > work ? vecs : work, 256)),
+                        static_cast<unsigned>(g));
+    if (!pack) {
+      hipLaunchKernelGGL(handoff_count_kernel, tile_grid, dim3(kTileThreads), 0, s, b);
+      if (int32_t e = launch_status("handoff count")) return e;
+      hipLaunchKernelGGL(handoff_scan_kernel, dim3(1, static_cast<unsigned>(g)), dim3(1024), 0, s,
+                         b);
+      if (int32_t e = launch_status("handoff scan")) return e;
+      continue;
+    }
+    hipLaunchKernelGGL(handoff_prep_kernel, grid, dim3(256), 0, s, b);
+    if (int32_t e = launch_status("handoff prep")) return e;
+    hipLaunchKernelGGL(handoff_apply_kernel, tile_grid, dim3(kTileThreads), 0, s, b);
+    if (int32_t e = launch_status("handoff apply")) return e;
+    hipLaunchKernelGGL(handoff_rows_kernel, row_grid, dim3(256), 0, s, b);
+    if (int32_t e = launch_status("handoff rows")) return e;
+    hipLaunchKernelGGL(handoff_own_kernel, grid, dim3(256), 0, s, b);
+    if (int32_t e = launch_status("handoff own")) return e;
+    hipLaunchKernelGGL(handoff_eval_kernel, grid, dim3(256), 0, s, b);
+    if (int32_t e = launch_status("handoff eval")) return e;
+  }
+  return 0;
 }
 
 }  // namespace cowsdm_impl
@@ -1728,6 +1921,16 @@ int32_t cowsdm_check_invariants(const int32_t* map, int64_t banks, int64_t slots
                      static_cast<const int32_t*>(ws.list_a), capacity_rows, overflow_flag,
                      scratch, stats);
   return launch_status("invariants eval");
+}
+
+int32_t cowsdm_handoff_count(const cowsdm_handoff_layer_t* layers, int32_t nlayers,
+                             void* stream) {
+  return run_handoff(layers, nlayers, false, as_stream(stream));
+}
+
+int32_t cowsdm_handoff_pack(const cowsdm_handoff_layer_t* layers, int32_t nlayers,
+                            void* stream) {
+  return run_handoff(layers, nlayers, true, as_stream(stream));
 }
 
 int32_t cowsdm_mark_written(uint8_t* active_mask, int64_t banks, int64_t slots,

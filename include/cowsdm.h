@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 9
+#define COWSDM_ABI_VERSION 10
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -404,6 +404,47 @@ int32_t cowsdm_pack_overlay(const float* dense_memory, const uint8_t* active_mas
                             int32_t* logical_to_physical, float* values,
                             int32_t* free_rows, int64_t capacity_rows,
                             int32_t* free_count, void* workspace, void* stream);
+
+/* The handoff of several layers at once (from_dense_overlay of each,
+ * allocator.py:587-689), in a few launches over all of them instead of
+ * count, pack and invariant launches per layer.  One entry per layer:
+ *   count part: dense_memory [B, N, D] float32, active_mask [B, N],
+ *     workspace (cowsdm_workspace_bytes(B * N, max(B * N, capacity_rows))),
+ *     total (int64: the layer's active entries A), template_indices [B]
+ *     (templates rows of shared initial memory) and checks (9 int64 words:
+ *     word 8 gets COWSDM_ERR_TEMPLATE or 0);
+ *   pack part, after the caller has read the totals and allocated each
+ *     layer's state: logical_to_physical [B, N], values [capacity_rows, D],
+ *     free_rows [capacity_rows], free_count, overflow_flag, scratch
+ *     (scratch_words int64).  The pack leaves the state of
+ *     cowsdm_init_state + cowsdm_pack_overlay (free_rows[i] = A + i for
+ *     i < C - A, i after), and checks words 0-7 get the counts of
+ *     cowsdm_check_invariants.
+ * No counterpart in the reference (its handoff is per layer, with host
+ * reads of each layer's count and invariants). */
+typedef struct cowsdm_handoff_layer {
+  const float* dense_memory;
+  const uint8_t* active_mask;
+  int64_t banks, slots, width;
+  void* workspace;
+  int64_t* total;
+  const int64_t* template_indices;
+  int64_t templates;
+  int64_t* checks;
+  int32_t* logical_to_physical;
+  float* values;
+  int32_t* free_rows;
+  int64_t capacity_rows;
+  int32_t* free_count;
+  int32_t* overflow_flag;
+  int64_t* scratch;
+  int64_t scratch_words;
+} cowsdm_handoff_layer_t;
+
+int32_t cowsdm_handoff_count(const cowsdm_handoff_layer_t* layers, int32_t nlayers,
+                             void* stream);
+int32_t cowsdm_handoff_pack(const cowsdm_handoff_layer_t* layers, int32_t nlayers,
+                            void* stream);
 
 /* Repack live rows into a smaller slab in row-major map order:
  * new_values[:A] = values[live rows], new_map = ranks, new_free_rows =

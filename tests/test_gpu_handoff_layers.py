@@ -73,3 +73,41 @@ def test_pack_prefill_layers_equals_per_layer(device):
         want = cow.pack_prefill_layer(m0[l], finals[l], routes[l], capacity_rows=None, **kw)
         assert_states_identical(got[l], want)
         assert got[l].capacity_is_proven and want.capacity_is_proven
+
+
+def test_single_layer_entry_points_equal_batched(device):
+    """The per-layer C entry points (cowsdm_count_active + cowsdm_pack_overlay
+    after cowsdm_init_state), kept for C callers, leave the state the batched
+    handoff leaves."""
+
+    from copy_on_write_sdm_amd import _native as nat
+
+    m0, dense, masks = _layers(device, layers=1, banks=6, slots=64, width=32, seed=9)
+    tmpl = torch.zeros(6, dtype=torch.int64, device=device)
+    got = cow.PackedSDMCopyOnWriteState.from_dense_overlay_layers(
+        m0, dense, masks, template_indices=tmpl, capacity_rows=[300])[0]
+    lib = nat.lib()
+    stream = nat.stream_handle(device)
+    banks, slots, width = dense[0].shape
+    workspace = torch.empty(int(lib.cowsdm_workspace_bytes(banks * slots, 300)),
+                            dtype=torch.uint8, device=device)
+    total = torch.empty(1, dtype=torch.int64, device=device)
+    state, result = cow.PackedSDMCopyOnWriteState._allocate_state(
+        m0[0], banks=banks, capacity_rows=300, template_indices=tmpl)
+    mask = masks[0].contiguous()
+    nat.check(lib.cowsdm_count_active(None, banks, slots, None, banks, mask.data_ptr(),
+                                      workspace.data_ptr(), total.data_ptr(), stream),
+              "cowsdm_count_active")
+    nat.check(lib.cowsdm_pack_overlay(dense[0].data_ptr(), mask.data_ptr(), banks, slots, width,
+                                      state.logical_to_physical.data_ptr(),
+                                      state.values.data_ptr(), state.free_rows.data_ptr(), 300,
+                                      state.free_count.data_ptr(), workspace.data_ptr(), stream),
+              "cowsdm_pack_overlay")
+    torch.cuda.synchronize()
+    assert int(total.item()) == int(mask.sum())
+    assert int(result.item()) == 0
+    live = int(total.item())
+    assert torch.equal(state.logical_to_physical, got.logical_to_physical)
+    assert torch.equal(state.values[:live], got.values[:live])
+    assert torch.equal(state.free_rows, got.free_rows)
+    assert int(state.free_count.item()) == int(got.free_count.item()) == 300 - live

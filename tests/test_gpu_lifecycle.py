@@ -225,8 +225,11 @@ def test_from_dense_overlay_matches_oracle(device):
     active = torch.rand(banks, slots, generator=gen) < 0.3
     dense[active] = torch.randn(int(active.sum()), width, generator=gen)
     tmpl = torch.zeros(banks, dtype=torch.int64)
+    # (a quantum past B * N: a slab larger than the count's row lists, which
+    # the handoff counts again into a larger workspace)
     for kwargs in (dict(growth_quantum_rows=8), dict(capacity_rows=80),
-                   dict(capacity_rows=160, maximum_future_allocations=100), dict()):
+                   dict(capacity_rows=160, maximum_future_allocations=100), dict(),
+                   dict(growth_quantum_rows=256)):
         st = cow.PackedSDMCopyOnWriteState.from_dense_overlay(
             m0.to(device), dense.to(device), active.to(device),
             template_indices=tmpl.to(device), **kwargs)
