@@ -70,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -287,6 +287,11 @@ SIGNATURES: dict[str, tuple] = {
     "cowsdm_controller_prepare": (
         _I32, [ctypes.POINTER(Controller), _P, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "cowsdm_controller_finish": (_I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P]),
+    "cowsdm_controller_prepare_routes": (
+        _I32, [ctypes.POINTER(Controller), _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P,
+               _P, _P, _P]),
+    "cowsdm_controller_finish_residual": (
+        _I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P, _P, _P]),
     "cowsdm_recurrence_forward": (_I32, [ctypes.POINTER(Recurrence), _P]),
     "cowsdm_dense_routes": (_I32, [_P, _P, _I32, _I64, _I64, _I64, _P, _P, _P]),
     "cowsdm_host_report_alloc": (

@@ -381,6 +381,7 @@ class ControllerDecodeGraph:
                 "write_indices": torch.empty(banks, 1, writes, **i64),
                 "reading": torch.empty(1, banks, c.head_width, **f32),
                 "out": torch.empty(batch, 1, c.width, **f32),
+                "sum": torch.empty(batch, 1, c.width, **f32),
             }
             trace = DecodeTrace(
                 states=[st], repeat=True, max_steps_per_launch=1, outputs=buf["reading"],
@@ -403,20 +404,20 @@ class ControllerDecodeGraph:
         lib = nat.lib()
         x = self.tokens
         for index, ((c, buf, trace), layer) in enumerate(zip(self.layers, structs)):
-            nat.check(lib.cowsdm_controller_prepare(
+            x = x.contiguous()
+            nat.check(lib.cowsdm_controller_prepare_routes(
                 c.c_struct(), x.data_ptr(), self.batch, buf["normalized"].data_ptr(),
                 buf["read_keys"].data_ptr(), buf["write_keys"].data_ptr(),
                 buf["values"].data_ptr(), buf["input_gate"].data_ptr(), buf["forget"].data_ptr(),
-                stream), "cowsdm_controller_prepare")
-            product_key_routes(buf["read_keys"], slots=c.slots, selected=c.reads,
-                               out=(buf["read_weights"], buf["read_indices"]))
-            product_key_routes(buf["write_keys"], slots=c.slots, selected=c.writes,
-                               out=(buf["write_weights"], buf["write_indices"]))
+                c.reads, c.writes, buf["read_weights"].data_ptr(),
+                buf["read_indices"].data_ptr(), buf["write_weights"].data_ptr(),
+                buf["write_indices"].data_ptr(), stream), "cowsdm_controller_prepare_routes")
             trace.launch(1, layer)
-            nat.check(lib.cowsdm_controller_finish(
+            nat.check(lib.cowsdm_controller_finish_residual(
                 c.c_struct(), buf["normalized"].data_ptr(), buf["reading"].data_ptr(), self.batch,
-                buf["out"].data_ptr(), stream), "cowsdm_controller_finish")
-            x = x + buf["out"]
+                buf["out"].data_ptr(), x.data_ptr(), buf["sum"].data_ptr(), stream),
+                "cowsdm_controller_finish_residual")
+            x = buf["sum"]
             if self.tail is not None:
                 x = self.tail(index, x)
         return x

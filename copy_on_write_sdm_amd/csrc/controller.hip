@@ -3,7 +3,9 @@
 // LayerNorm, the read / write key, value, forget and input projections and
 // the gates; after it, the readings LayerNorm, the sigmoid output gate and
 // the output projection.  Routes are selected from the keys by
-// cowsdm_product_key_routes (routes.hip).
+// cowsdm_product_key_routes (routes.hip), or, for sqrt(N) <= 64, by the
+// prepare kernel itself once its tokens' keys are out (one wave per route
+// row, routes.h): cowsdm_controller_prepare_routes.
 //
 // A workgroup takes kCtlTokens tokens.  Each token's normalised input stays
 // in LDS, and thread j computes output row j of every projection for all of
@@ -13,12 +15,17 @@
 // Products are accumulated with fused multiply-adds in input order.
 
 #include "common.h"
+#include "routes.h"
 
 namespace cowsdm_impl {
 
 constexpr int kCtlTokens = 4;        // tokens per workgroup
 constexpr int kCtlThreads = 256;
 constexpr int kCtlWaves = kCtlThreads / kWave;
+// prepare with its routes: a wave for each of a workgroup's 2 x kCtlTokens
+// route rows (one head)
+constexpr int kCtlRouteThreads = 2 * kCtlTokens * kWave;
+constexpr int kCtlRouteWaves = kCtlRouteThreads / kWave;
 constexpr int kCtlMaxWidth = 1024;         // LDS: 3 x 4 tokens x width floats
 
 struct CtlParams {
@@ -34,7 +41,19 @@ struct CtlParams {
   float* input_gate;          // prepare: [batch * heads]
   float* forget_log_gate;
   float* out;                 // finish: [batch, width]
+  const float* residual;      // finish: [batch, width] or null
+  float* out_sum;             // finish: residual + out, when residual is set
   int width, heads, head_width, key_width, rows;
+};
+
+// The routes the prepare kernel selects itself (sqrt(N) <= 64): every
+// token's read and write route rows, one wave per row.
+struct CtlRoutes {
+  int root, read_sub, read_k, write_sub, write_k;
+  float* read_weights;        // [batch * heads, read_k]
+  int64_t* read_indices;
+  float* write_weights;       // [batch * heads, write_k]
+  int64_t* write_indices;
 };
 
 __device__ __forceinline__ float wave_sum_f(float v) {
@@ -77,20 +96,20 @@ __device__ __forceinline__ void project(const float* x, int width, const float* 
   }
 }
 
-__global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlParams P) {
-  extern __shared__ float lds[];
+template <int NT>
+__device__ __forceinline__ void controller_prepare_body(const CtlParams& P, float* lds) {
   const int W = P.width, H = P.heads, HW = P.head_width, KW = P.key_width;
   float* const x = lds;                        // [kCtlTokens][W]
   float* const xn = lds + kCtlTokens * W;      // [kCtlTokens][W]
   const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
   const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
   const int tid = static_cast<int>(threadIdx.x);
-  for (int i = tid; i < kCtlTokens * W; i += kCtlThreads) {
+  for (int i = tid; i < kCtlTokens * W; i += NT) {
     x[i] = i < T * W ? P.tokens[b0 * W + i] : 0.0f;
   }
   __syncthreads();
   const int wave = tid / kWave;
-  for (int t = wave; t < kCtlTokens; t += kCtlWaves) {
+  for (int t = wave; t < kCtlTokens; t += NT / kWave) {
     if (t < T) {
       wave_layer_norm(x + t * W, xn + t * W, W, P.c.norm_weight, P.c.norm_bias, P.c.norm_eps);
     } else {
@@ -98,9 +117,9 @@ __global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlPara
     }
   }
   __syncthreads();
-  for (int i = tid; i < T * W; i += kCtlThreads) P.out_normalized[b0 * W + i] = xn[i];
+  for (int i = tid; i < T * W; i += NT) P.out_normalized[b0 * W + i] = xn[i];
   // rows: read keys (H x KW), write keys (H x KW), values (W), forget (H), input (H)
-  for (int j = tid; j < P.rows; j += kCtlThreads) {
+  for (int j = tid; j < P.rows; j += NT) {
     float acc[kCtlTokens];
     project(xn, W, P.c.proj_weight_t, P.rows, j, acc);
     const float bias = P.c.proj_bias[j];
@@ -123,6 +142,41 @@ __global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlPara
         r -= H;
         P.input_gate[b * H + r] = sigmoid(y);
       }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlParams P) {
+  extern __shared__ float lds[];
+  controller_prepare_body<kCtlThreads>(P, lds);
+}
+
+// prepare, then the routes of the workgroup's tokens from the keys its
+// threads stored (visible to the whole workgroup after the barrier)
+template <int MR, int MW>
+__global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_routes_kernel(
+    CtlParams P, CtlRoutes R) {
+  extern __shared__ float lds[];
+  __shared__ float stage_val[kCtlRouteWaves][kRouteMaxSelected];
+  __shared__ int stage_pos[kCtlRouteWaves][kRouteMaxSelected];
+  __shared__ float pool_val[kCtlRouteWaves][kWave];
+  __shared__ int pool_pos[kCtlRouteWaves][kWave];
+  controller_prepare_body<kCtlRouteThreads>(P, lds);
+  __syncthreads();
+  const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
+  const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
+  const int rows = T * P.heads;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  for (int task = wave; task < 2 * rows; task += kCtlRouteWaves) {
+    if (task < rows) {
+      product_key_route_row<1, MR>(P.read_keys, b0 * P.heads + task, R.root, R.read_sub,
+                                   R.read_k, R.read_weights, R.read_indices, stage_val[wave],
+                                   stage_pos[wave], pool_val[wave], pool_pos[wave]);
+    } else {
+      product_key_route_row<1, MW>(P.write_keys, b0 * P.heads + task - rows, R.root,
+                                   R.write_sub, R.write_k, R.write_weights, R.write_indices,
+                                   stage_val[wave], stage_pos[wave], pool_val[wave],
+                                   pool_pos[wave]);
     }
   }
 }
@@ -161,7 +215,12 @@ __global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParam
     float acc[kCtlTokens];
     project(rd, W, P.c.out_weight_t, W, j, acc);
     const float bias = P.c.out_bias[j];
-    for (int t = 0; t < T; ++t) P.out[(b0 + t) * W + j] = acc[t] + bias;
+    for (int t = 0; t < T; ++t) {
+      const int64_t at = (b0 + t) * W + j;
+      const float y = acc[t] + bias;
+      P.out[at] = y;
+      if (P.residual) P.out_sum[at] = P.residual[at] + y;
+    }
   }
 }
 
@@ -206,11 +265,11 @@ extern "C" int64_t cowsdm_controller_rows(int64_t width, int64_t heads, int64_t 
   return 2 * heads * 2 * root + width + 2 * heads;
 }
 
-extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const float* tokens,
-                                             int64_t batch, float* normalized, float* read_keys,
-                                             float* write_keys, float* values, float* input_gate,
-                                             float* forget_log_gate, void* stream) {
-  CtlParams P{};
+namespace {
+
+int32_t prepare_params(const cowsdm_controller_t* c, const float* tokens, int64_t batch,
+                       float* normalized, float* read_keys, float* write_keys, float* values,
+                       float* input_gate, float* forget_log_gate, CtlParams& P) {
   if (int32_t e = check_controller(c, batch, P)) return e;
   if (batch == 0) return 0;
   if (!tokens || !normalized || !read_keys || !write_keys || !values || !input_gate ||
@@ -225,18 +284,97 @@ extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const
   P.values = values;
   P.input_gate = input_gate;
   P.forget_log_gate = forget_log_gate;
+  if ((batch + kCtlTokens - 1) / kCtlTokens > (int64_t{1} << 31) - 1) {
+    return fail(COWSDM_ELIMIT, "controller: batch too large");
+  }
+  return 0;
+}
+
+template <int MR, int MW>
+void launch_prepare_routes(const CtlParams& P, const CtlRoutes& R, hipStream_t s) {
+  const int64_t groups = (P.batch + kCtlTokens - 1) / kCtlTokens;
+  const size_t lds = sizeof(float) * 2 * kCtlTokens * P.width;
+  hipLaunchKernelGGL((controller_prepare_routes_kernel<MR, MW>),
+                     dim3(static_cast<unsigned>(groups)), dim3(kCtlRouteThreads), lds, s, P, R);
+}
+
+}  // namespace
+
+extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const float* tokens,
+                                             int64_t batch, float* normalized, float* read_keys,
+                                             float* write_keys, float* values, float* input_gate,
+                                             float* forget_log_gate, void* stream) {
+  CtlParams P{};
+  if (int32_t e = prepare_params(c, tokens, batch, normalized, read_keys, write_keys, values,
+                                 input_gate, forget_log_gate, P)) {
+    return e;
+  }
+  if (batch == 0) return 0;
   const int64_t groups = (batch + kCtlTokens - 1) / kCtlTokens;
-  if (groups > (int64_t{1} << 31) - 1) return fail(COWSDM_ELIMIT, "controller: batch too large");
   const size_t lds = sizeof(float) * 2 * kCtlTokens * P.width;
   hipLaunchKernelGGL(controller_prepare_kernel, dim3(static_cast<unsigned>(groups)),
                      dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
   return launch_status("controller prepare");
 }
 
-extern "C" int32_t cowsdm_controller_finish(const cowsdm_controller_t* c,
-                                            const float* normalized, const float* reading,
-                                            int64_t batch, float* out, void* stream) {
+extern "C" int32_t cowsdm_product_key_routes(const float* projected, int64_t rows,
+                                             int64_t slots, int64_t selected,
+                                             float* weights, int64_t* indices, void* stream);
+
+extern "C" int32_t cowsdm_controller_prepare_routes(
+    const cowsdm_controller_t* c, const float* tokens, int64_t batch, float* normalized,
+    float* read_keys, float* write_keys, float* values, float* input_gate,
+    float* forget_log_gate, int64_t reads, int64_t writes, float* read_weights,
+    int64_t* read_indices, float* write_weights, int64_t* write_indices, void* stream) {
   CtlParams P{};
+  if (int32_t e = prepare_params(c, tokens, batch, normalized, read_keys, write_keys, values,
+                                 input_gate, forget_log_gate, P)) {
+    return e;
+  }
+  CtlRoutes R{};
+  if (int32_t e = route_geometry(c->slots, reads, R.root, R.read_sub, R.read_k)) return e;
+  if (int32_t e = route_geometry(c->slots, writes, R.root, R.write_sub, R.write_k)) return e;
+  if (batch == 0) return 0;
+  if (!read_weights || !read_indices || !write_weights || !write_indices) {
+    return fail(COWSDM_EARG, "controller prepare: null route pointer");
+  }
+  R.read_weights = read_weights;
+  R.read_indices = read_indices;
+  R.write_weights = write_weights;
+  R.write_indices = write_indices;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (R.root > kWave) {
+    // a shortlist of more than one entry per lane: the separate launches
+    if (int32_t e = cowsdm_controller_prepare(c, tokens, batch, normalized, read_keys,
+                                              write_keys, values, input_gate, forget_log_gate,
+                                              stream)) {
+      return e;
+    }
+    const int64_t rows = batch * c->heads;
+    if (int32_t e = cowsdm_product_key_routes(read_keys, rows, c->slots, reads, read_weights,
+                                              read_indices, stream)) {
+      return e;
+    }
+    return cowsdm_product_key_routes(write_keys, rows, c->slots, writes, write_weights,
+                                     write_indices, stream);
+  }
+  const int mr = route_pair_m(R.read_sub, R.read_k), mw = route_pair_m(R.write_sub, R.write_k);
+  if (mr == 1 && mw == 1) launch_prepare_routes<1, 1>(P, R, s);
+  else if (mr == 1) launch_prepare_routes<1, 2>(P, R, s);
+  else if (mw == 1) launch_prepare_routes<2, 1>(P, R, s);
+  else launch_prepare_routes<2, 2>(P, R, s);
+  return launch_status("controller prepare routes");
+}
+
+extern "C" int32_t cowsdm_controller_finish_residual(const cowsdm_controller_t* c,
+                                                     const float* normalized,
+                                                     const float* reading, int64_t batch,
+                                                     float* out, const float* residual,
+                                                     float* out_sum, void* stream) {
+  CtlParams P{};
+  if (residual && !out_sum) return fail(COWSDM_EARG, "controller finish: null residual sum");
+  P.residual = residual;
+  P.out_sum = out_sum;
   if (int32_t e = check_controller(c, batch, P)) return e;
   if (batch == 0) return 0;
   if (!normalized || !reading || !out || !c->gate_weight_t || !c->gate_bias ||
@@ -252,4 +390,11 @@ extern "C" int32_t cowsdm_controller_finish(const cowsdm_controller_t* c,
   hipLaunchKernelGGL(controller_finish_kernel, dim3(static_cast<unsigned>(groups)),
                      dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
   return launch_status("controller finish");
+}
+
+extern "C" int32_t cowsdm_controller_finish(const cowsdm_controller_t* c,
+                                            const float* normalized, const float* reading,
+                                            int64_t batch, float* out, void* stream) {
+  return cowsdm_controller_finish_residual(c, normalized, reading, batch, out, nullptr, nullptr,
+                                           stream);
 }

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 10
+#define COWSDM_ABI_VERSION 11
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -643,6 +643,30 @@ int32_t cowsdm_controller_prepare(const cowsdm_controller_t* controller, const f
 int32_t cowsdm_controller_finish(const cowsdm_controller_t* controller,
                                  const float* normalized, const float* reading,
                                  int64_t batch, float* out, void* stream);
+
+/* cowsdm_controller_prepare followed by the product-key routes of every
+ * token's read and write keys (sdm.py:96-159, as
+ * _prepare_faithful_sdm_step calls them, inference.py:479-488), in one
+ * launch when sqrt(slots) <= 64: read_weights/read_indices
+ * [batch * heads, min(reads, min(reads, sqrt N)^2)], the write routes
+ * likewise; larger tables fall back to the three separate launches.  The
+ * routes equal cowsdm_product_key_routes' bit for bit; reads and writes
+ * take its `selected` checks.  No single counterpart in the reference: it
+ * is the fusion of the calls above for a decode step's launch count. */
+int32_t cowsdm_controller_prepare_routes(
+    const cowsdm_controller_t* controller, const float* tokens, int64_t batch,
+    float* normalized, float* read_keys, float* write_keys, float* values, float* input_gate,
+    float* forget_log_gate, int64_t reads, int64_t writes, float* read_weights,
+    int64_t* read_indices, float* write_weights, int64_t* write_indices, void* stream);
+
+/* cowsdm_controller_finish that also writes out_sum = residual + out
+ * [batch, width] (the residual add after the SDM mixer, tokens + mixed,
+ * inference.py:660) when residual is non-null; out is written either
+ * way. */
+int32_t cowsdm_controller_finish_residual(const cowsdm_controller_t* controller,
+                                          const float* normalized, const float* reading,
+                                          int64_t batch, float* out, const float* residual,
+                                          float* out_sum, void* stream);
 
 /* ------------------------------------------ dense recurrence (prefill) */
 

@@ -141,3 +141,76 @@ def test_controller_layer_decode_matches_oracle_step(device, heads):
     assert_state_equal(state, orc)
     assert state.growth_events > 0
     state.validate_invariants()
+
+
+@pytest.mark.parametrize("width,slots,heads,reads,writes,batch", SHAPES)
+def test_fused_prepare_routes_and_residual_finish_equal_separate_launches(
+        device, width, slots, heads, reads, writes, batch):
+    """cowsdm_controller_prepare_routes (one launch for sqrt(N) <= 64, the
+    separate launches above it) writes exactly what prepare and the two
+    route launches write; finish_residual's out equals finish's and its sum
+    is residual + out."""
+    from copy_on_write_sdm_amd import _native as nat
+    from copy_on_write_sdm_amd.routing import product_key_routes
+    print(f"fused controller prepare width={width} N={slots} H={heads} B={batch}", flush=True)
+    layer, controller, x = _setup(device, width, slots, heads, reads, writes, batch,
+                                  seed=5 * width)
+    x = x.to(device)
+    root = int(np.sqrt(slots))
+    kr, kw = min(reads, min(reads, root) ** 2), min(writes, min(writes, root) ** 2)
+    rows, hw = batch * heads, width // heads
+    lib, stream = nat.lib(), nat.stream_handle(device)
+
+    def outputs():
+        f = dict(device=device, dtype=torch.float32)
+        return {"normalized": torch.full((batch, width), 7.0, **f),
+                "read_keys": torch.full((rows, 2 * root), 7.0, **f),
+                "write_keys": torch.full((rows, 2 * root), 7.0, **f),
+                "values": torch.full((rows, hw), 7.0, **f),
+                "input_gate": torch.full((rows,), 7.0, **f),
+                "forget": torch.full((rows,), 7.0, **f),
+                "read_weights": torch.full((rows, kr), 7.0, **f),
+                "read_indices": torch.full((rows, kr), -7, device=device, dtype=torch.int64),
+                "write_weights": torch.full((rows, kw), 7.0, **f),
+                "write_indices": torch.full((rows, kw), -7, device=device, dtype=torch.int64)}
+
+    def prepare_args(o):
+        return (controller.c_struct(), x.data_ptr(), batch, o["normalized"].data_ptr(),
+                o["read_keys"].data_ptr(), o["write_keys"].data_ptr(), o["values"].data_ptr(),
+                o["input_gate"].data_ptr(), o["forget"].data_ptr())
+
+    want = outputs()
+    nat.check(lib.cowsdm_controller_prepare(*prepare_args(want), stream), "prepare")
+    product_key_routes(want["read_keys"].view(rows, 1, -1), slots=slots, selected=reads,
+                       out=(want["read_weights"].view(rows, 1, kr),
+                            want["read_indices"].view(rows, 1, kr)))
+    product_key_routes(want["write_keys"].view(rows, 1, -1), slots=slots, selected=writes,
+                       out=(want["write_weights"].view(rows, 1, kw),
+                            want["write_indices"].view(rows, 1, kw)))
+    got = outputs()
+    nat.check(lib.cowsdm_controller_prepare_routes(
+        *prepare_args(got), reads, writes, got["read_weights"].data_ptr(),
+        got["read_indices"].data_ptr(), got["write_weights"].data_ptr(),
+        got["write_indices"].data_ptr(), stream), "prepare_routes")
+    for name in want:
+        assert torch.equal(got[name], want[name]), name
+
+    reading = tokens(rows, hw, seed=91, dtype=torch.float32)[:, 0].to(device)
+    out_want = torch.empty(batch, width, device=device)
+    nat.check(lib.cowsdm_controller_finish(
+        controller.c_struct(), want["normalized"].data_ptr(), reading.data_ptr(), batch,
+        out_want.data_ptr(), stream), "finish")
+    out, total = torch.empty_like(out_want), torch.empty_like(out_want)
+    nat.check(lib.cowsdm_controller_finish_residual(
+        controller.c_struct(), want["normalized"].data_ptr(), reading.data_ptr(), batch,
+        out.data_ptr(), x.data_ptr(), total.data_ptr(), stream), "finish_residual")
+    assert torch.equal(out, out_want)
+    assert torch.equal(total, x.view(batch, width) + out_want)
+    # argument checks: the route counts take product_key_routes' checks
+    assert lib.cowsdm_controller_prepare_routes(
+        *prepare_args(got), 0, writes, got["read_weights"].data_ptr(),
+        got["read_indices"].data_ptr(), got["write_weights"].data_ptr(),
+        got["write_indices"].data_ptr(), stream) != 0
+    assert lib.cowsdm_controller_finish_residual(
+        controller.c_struct(), want["normalized"].data_ptr(), reading.data_ptr(), batch,
+        out.data_ptr(), x.data_ptr(), None, stream) != 0
