@@ -64,6 +64,12 @@ CONFIGS = {
     5: dict(heads=4, slots=65536, prefix=0, warmup=64, steps=960, distribution="zipf",
             text="large address space: Zipf(1.1) routes, decode from an empty slab"),
 }
+# --skewed (config 3): Zipf routes whose exponent makes the union of a bank's
+# written slots after the 2048-token prefill about 94 of 256 (measured with
+# synthetic.make_steps: 2.40 -> 95.9, 2.45 -> 90.8 over 64 bank-layers), the
+# trained model's occupancy the configuration quotes (about 660 private rows
+# of 1,792 per request); prefill and decode share each layer's hot slots.
+SKEWED_EXPONENT = 2.42
 
 
 def parse():
@@ -89,6 +95,9 @@ def parse():
     p.add_argument("--eager-steps", type=int, default=None,
                    help="steps of the per-layer Python drop-in path to time (0: skip; "
                         "default 32 for config 2, else 0)")
+    p.add_argument("--skewed", action="store_true",
+                   help="config 3 only: calibrated Zipf routes (about 37%% of each layer's "
+                        "slots written by the prefill) instead of uniform ones")
     p.add_argument("--routes", action="store_true",
                    help="time product_key_routes (the route producer) instead of the decode "
                         "step: one JSON line per shape")
@@ -276,7 +285,18 @@ def main() -> int:
     from copy_on_write_sdm_amd import synthetic
 
     dev = torch.device("cuda:0")
-    cfg = CONFIGS[args.config]
+    cfg = dict(CONFIGS[args.config])
+    if args.skewed:
+        if args.config != 3:
+            print("--skewed applies to config 3", file=sys.stderr)
+            return 2
+        cfg.update(distribution="zipf", zipf_exponent=SKEWED_EXPONENT,
+                   text=(f"long-prefix handoff with calibrated Zipf({SKEWED_EXPONENT}) routes "
+                         "(about 37% of slots written by the prefill): 2048-token dense "
+                         "prefill packed, then 256 decode steps"))
+    route_kw = dict(distribution=cfg["distribution"], heads=cfg["heads"],
+                    zipf_exponent=cfg.get("zipf_exponent", 1.1),
+                    zipf_seed=args.seed + 7 if args.skewed else None)
     HEADS, SLOTS, PREFIX = cfg["heads"], cfg["slots"], cfg["prefix"]
     B = args.batch
     K = cfg["steps"] if args.steps is None else args.steps
@@ -306,8 +326,7 @@ def main() -> int:
     if PREFIX:
         prefix = synthetic.make_steps(steps=PREFIX, layers=LAYERS, banks=banks, slots=SLOTS,
                                       width=WIDTH, writes=WRITES, reads=READS,
-                                      seed=args.seed + 1, device=dev,
-                                      distribution=cfg["distribution"], heads=HEADS)
+                                      seed=args.seed + 1, device=dev, **route_kw)
         tables = [m0[l][templates].contiguous() for l in range(LAYERS)]
         prefill = cow.DecodeTrace(memories=tables, write_indices=prefix.write_indices,
                                   write_weights=prefix.write_weights, values=prefix.values,
@@ -386,7 +405,7 @@ def main() -> int:
     # ---- decode routes
     routes = synthetic.make_steps(steps=total_steps, layers=LAYERS, banks=banks, slots=SLOTS,
                                   width=WIDTH, writes=WRITES, reads=READS, seed=args.seed + 2,
-                                  device=dev, distribution=cfg["distribution"], heads=HEADS)
+                                  device=dev, **route_kw)
     inputs = dict(write_indices=routes.write_indices, write_weights=routes.write_weights,
                   values=routes.values, input_gate=routes.input_gate,
                   forget_log_gate=routes.forget_log_gate, read_indices=routes.read_indices,
@@ -516,6 +535,8 @@ def main() -> int:
     logical_rows = sum(st.banks * st.slots for st in states)
     memory = {
         "logical_rows": logical_rows,
+        # the rows the handoff packed (private rows after the prefill)
+        "handoff_live_row_fraction": round(allocator["handoff_live_rows"] / logical_rows, 4),
         "live_row_fraction": round(allocator["live_rows_after"] / logical_rows, 4),
         "physical_capacity_fraction": round(allocator["capacity_rows_after"] / logical_rows, 4),
         "packed_over_dense_live_bytes": round(
@@ -675,8 +696,7 @@ def main() -> int:
         fresh_steps = 64
         fresh = synthetic.make_steps(steps=fresh_steps, layers=LAYERS, banks=banks, slots=SLOTS,
                                      width=WIDTH, writes=WRITES, reads=READS,
-                                     seed=args.seed + 9, device=dev,
-                                     distribution=cfg["distribution"], heads=HEADS)
+                                     seed=args.seed + 9, device=dev, **route_kw)
         keys = ("write_indices", "write_weights", "values", "input_gate", "forget_log_gate",
                 "read_indices", "read_weights")
 
@@ -778,6 +798,7 @@ def main() -> int:
             "batch": B, "heads": HEADS, "banks": banks, "layers": LAYERS, "slots": SLOTS,
             "width": WIDTH, "writes": WRITES, "reads": READS, "prefix": PREFIX,
             "distribution": cfg["distribution"],
+            **({"zipf_exponent": cfg["zipf_exponent"]} if "zipf_exponent" in cfg else {}),
             "growth_quantum_rows": quantum, "max_steps_per_launch": args.launch_steps,
             "capacity_proof": ("the reference's prepare_step_capacity(B*W) before every "
                                "step, planned on the device per launch"),

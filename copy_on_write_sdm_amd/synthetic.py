@@ -9,7 +9,9 @@ it), forget log gate = -U(0, 1) as in tests/test_allocator.py:31-38.
 ``uniform`` draws every slot with equal probability; ``zipf`` draws slot
 ``perm[k]`` with probability proportional to (k + 1)^-s without replacement
 (Gumbel top-k over log-weights), with one fixed random permutation per
-(layer, head).
+(layer, head), drawn from the call's generator or, with ``zipf_seed``, from
+a generator of its own, so that calls with different seeds (a prefill and
+the decode after it) share their hot slots.
 """
 
 from __future__ import annotations
@@ -74,6 +76,7 @@ def make_steps(
     distribution: str = "uniform",
     zipf_exponent: float = 1.1,
     heads: int = 1,
+    zipf_seed: int | None = None,
 ) -> StepBatch:
     """Generate a seeded batch of synthetic step inputs on ``device``."""
 
@@ -87,10 +90,14 @@ def make_steps(
         raise ValueError("banks must be a multiple of heads")
     logw = None
     if distribution == "zipf":
+        perm_gen = gen
+        if zipf_seed is not None:
+            perm_gen = torch.Generator(device=device)
+            perm_gen.manual_seed(zipf_seed)
         logw = torch.stack([
             torch.stack([
                 zipf_log_weights(slots, zipf_exponent,
-                                 torch.randperm(slots, generator=gen, device=device))
+                                 torch.randperm(slots, generator=perm_gen, device=device))
                 for _ in range(heads)])
             for _ in range(layers)])                    # [L, H, N]
         logw = logw.repeat(1, banks // heads, 1)        # bank = seq * H + h

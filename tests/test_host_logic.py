@@ -182,3 +182,33 @@ def test_paged_map_page_sizes():
     for bad, slots in ((1, 64), (3, 63), (128, 1024), (16, 40), (0, 16)):
         with pytest.raises(ValueError, match="power of two"):
             PagedSlotMap._shift(bad, slots)
+
+
+def test_zipf_seed_shares_hot_slots_across_calls():
+    """make_steps(zipf_seed=...) draws the per-(layer, head) Zipf permutation
+    from its own generator: a prefill and a decode drawn with different seeds
+    write the same hot slots, and calls without it keep drawing the
+    permutation from the call's generator."""
+    import torch
+    from copy_on_write_sdm_amd.synthetic import make_steps
+
+    kw = dict(steps=64, layers=2, banks=4, slots=64, width=4, writes=4, reads=8,
+              distribution="zipf", zipf_exponent=2.4, heads=2)
+    a = make_steps(seed=1, zipf_seed=11, **kw).write_indices.long()
+    b = make_steps(seed=2, zipf_seed=11, **kw).write_indices.long()
+    c = make_steps(seed=2, zipf_seed=12, **kw).write_indices.long()
+
+    def hottest(w):
+        counts = torch.zeros(w.shape[1], w.shape[2], kw["slots"], dtype=torch.long)
+        for t in range(w.shape[0]):
+            counts.scatter_add_(2, w[t], torch.ones_like(w[t]))
+        return counts.argmax(dim=2)
+
+    assert torch.equal(hottest(a), hottest(b))
+    assert not torch.equal(hottest(b), hottest(c))
+    # banks of one head share its permutation (bank = request * heads + head)
+    h = hottest(a)
+    assert torch.equal(h[:, 0], h[:, 2]) and torch.equal(h[:, 1], h[:, 3])
+    # without zipf_seed the call's own generator draws it: same seed, same routes
+    d = make_steps(seed=3, **kw).write_indices
+    assert torch.equal(d, make_steps(seed=3, **kw).write_indices)
