@@ -39,22 +39,24 @@ pytestmark = pytest.mark.gpu
 W, R, D = 4, 16, 128
 
 
-def _routes(device, *, steps, layers, banks, slots, seed, distribution="uniform", heads=1):
+def _routes(device, *, steps, layers, banks, slots, seed, distribution="uniform", heads=1,
+            **zipf):
     batch = synthetic.make_steps(steps=steps, layers=layers, banks=banks, slots=slots, width=D,
                                  writes=W, reads=R, seed=seed, device=device,
-                                 distribution=distribution, heads=heads)
+                                 distribution=distribution, heads=heads, **zipf)
     return batch, dict(write_indices=batch.write_indices, write_weights=batch.write_weights,
                        values=batch.values, input_gate=batch.input_gate,
                        forget_log_gate=batch.forget_log_gate,
                        read_indices=batch.read_indices, read_weights=batch.read_weights)
 
 
-def _handoff(device, m0, *, layers, banks, slots, prefix, quantum, seed):
+def _handoff(device, m0, *, layers, banks, slots, prefix, quantum, seed, **routes):
     """Dense prefill of `prefix` tokens, then the copy-on-write handoff of
     every layer (inference.py:314-366).  Returns a factory of fresh states
     and the prefix routes."""
 
-    pre, kw = _routes(device, steps=prefix, layers=layers, banks=banks, slots=slots, seed=seed)
+    pre, kw = _routes(device, steps=prefix, layers=layers, banks=banks, slots=slots, seed=seed,
+                      **routes)
     tables = [m0[l, 0].expand(banks, -1, -1).clone(memory_format=torch.contiguous_format) for l in range(layers)]
     cow.DecodeTrace(memories=tables, **kw).launch(prefix, start=0)
 
@@ -138,22 +140,34 @@ def test_config1_end_to_end_matches_oracle(device):
     traced[0].validate_invariants()
 
 
-@pytest.mark.parametrize("batch_size,prefix,steps,split", [
-    (64, 256, 512, False),   # config 2: its 512 decode steps as one launch
-    (64, 256, 128, True),    # config 2, a short run then the rest
-    (16, 256, 96, True),     # config 2, B=16
-    (1, 256, 96, True),      # config 2, B=1
-    (64, 2048, 256, True),   # config 3: all 256 decode steps
+@pytest.mark.parametrize("batch_size,prefix,steps,split,skewed", [
+    (64, 256, 512, False, False),   # config 2: its 512 decode steps as one launch
+    (64, 256, 128, True, False),    # config 2, a short run then the rest
+    (16, 256, 96, True, False),     # config 2, B=16
+    (1, 256, 96, True, False),      # config 2, B=1
+    (64, 2048, 256, True, False),   # config 3: all 256 decode steps
+    (64, 2048, 256, True, True),    # config 3, bench.py --skewed's routes
 ])
-def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, steps, split):
+def test_config2_and_config3_handoff_then_decode(device, batch_size, prefix, steps, split,
+                                                   skewed):
     layers, banks, slots = 7, batch_size, 256
-    print(f"config handoff B={banks} prefix={prefix} decode={steps} split={split}", flush=True)
+    print(f"config handoff B={banks} prefix={prefix} decode={steps} split={split} "
+          f"skewed={skewed}", flush=True)
     quantum = max(16, banks * W * 4)
+    # skewed: the calibrated Zipf of bench.py --skewed, one set of hot slots
+    # per layer for the prefill and the decode
+    routes = dict(distribution="zipf", zipf_exponent=2.42, zipf_seed=39) if skewed else {}
     m0 = synthetic.make_initial_memory(layers, 1, slots, D, seed=31, device=device)
     make_states, _ = _handoff(device, m0, layers=layers, banks=banks, slots=slots,
-                              prefix=prefix, quantum=quantum, seed=32)
-    batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=33)
+                              prefix=prefix, quantum=quantum, seed=32, **routes)
+    batch, kw = _routes(device, steps=steps, layers=layers, banks=banks, slots=slots, seed=33,
+                        **routes)
     traced, host = make_states(), make_states()
+    if skewed:
+        # the handoff packs about 37 % of the logical rows (the trained
+        # model's occupancy the configuration quotes)
+        live = sum(int(st.allocated_rows_tensor()) for st in traced) / (layers * banks * slots)
+        assert 0.30 < live < 0.45, live
     dense = [st.materialize_dense() for st in traced]
     dense_steps = [t.clone() for t in dense]
     outputs = torch.empty(steps, layers, banks, D, device=device)
