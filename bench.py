@@ -30,7 +30,8 @@ steps each record HIP events at the decode kernel's own start and end for
 the roofline; the wall-clock repetitions run without them (they add about
 20 us of host time per launch).  The same per-token loop is also
 timed as the reference's call pattern on the per-layer kernel (eager) and as
-one captured graph replay per token (graph_step).  The dense-table control runs the same
+one captured graph replay per token (graph_step) and as the same launch enqueued
+directly per token (launch_step).  The dense-table control runs the same
 routes the same way from the same packed state; both end states must be
 equal.  The CPU baseline is the torch restatement of the reference's
 dense-table step on the host cores (all cores and one
@@ -573,7 +574,7 @@ def main() -> int:
     # ---- the same per-token loop as one captured graph launch per token:
     # each replay is one step of every layer with the decode loop's proof and
     # growth decided on the device (DecodeTrace.capture(1)), no host work
-    graph_step = None
+    graph_step = launch_step = None
     if eager_steps:
         # untimed replays first (as many as the recorded routes leave after
         # the timed ones, at most 64): the first replays of a graph run
@@ -608,6 +609,37 @@ def main() -> int:
             "what": "hipGraph of one planned launch (all layers, one step) replayed per token",
         }
         del graph
+        # the same launches enqueued one per token without the graph: the
+        # runtime's graph launch costs about 16 us of host time per replay,
+        # more than the kernel, a device-counted launch about 5 us, so the
+        # stream is never empty and the rate is the kernel's
+        layers_arr = gtrace.layer_array()
+        gtrace.set_step(0)
+        gtrace.upload()
+        gtrace.status.zero_()
+        for _ in range(warm):
+            gtrace.launch(1, layers_arr)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g0.record()
+        for _ in range(n - warm):
+            gtrace.launch(1, layers_arr)
+        g1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gtrace.sync()
+        if gtrace.step_index.tolist() != [n] * LAYERS or any(gtrace.status.tolist()):
+            raise AssertionError("per-token decode launches did not run every step")
+        launch_step = {
+            "tokens_per_s": round(B * (n - warm) / wall, 1),
+            "us_per_step": round(1e6 * wall / (n - warm), 3),
+            "gpu_us_per_step": round(1000.0 * g0.elapsed_time(g1) / (n - warm), 3),
+            "steps": n - warm,
+            "warmup_launches": warm,
+            "what": ("the launches of graph_step enqueued directly, one per token "
+                     "(DecodeTrace.launch(1): device counters, proof and growth on the "
+                     "device, no host synchronisation)"),
+        }
 
     # ---- the reference's per-token call pattern with the controller on the
     # device (decode_sdm_layer_controller: input norm, projections and gates,
@@ -807,8 +839,8 @@ def main() -> int:
                      "launches (synthetic routes, as the reference's benchmark pre-generates "
                      "them), so one launch runs up to max_steps_per_launch steps; a decode "
                      "whose routes depend on the previous token runs one step per launch: "
-                     "graph_step (synthetic routes) and controller_graph (routes from the "
-                     "device controller) give that per-token rate"),
+                     "launch_step and graph_step (synthetic routes) and controller_graph "
+                     "(routes from the device controller) give that per-token rate"),
             "parallelism": "single GPU",
         },
         "roofline": {
@@ -846,6 +878,7 @@ def main() -> int:
         "memory": memory,
         "eager_drop_in_tokens_per_s": None if eager is None else round(eager, 1),
         "graph_step": graph_step,
+        "launch_step": launch_step,
         "controller_decode": controller_leg,
         "controller_graph": controller_graph,
     }
