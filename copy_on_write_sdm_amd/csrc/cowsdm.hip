@@ -1473,7 +1473,11 @@ int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
   }
   int64_t* const host = report_host(trace->report);
   if (!host) return fail(COWSDM_EARG, "trace run: the report is not from cowsdm_host_report_alloc");
-  for (int32_t l = 0; l < nlayers; ++l) host[l * COWSDM_REPORT_WORDS] = -1;   // not written yet
+  // not written yet: no word of a report takes this value (counters,
+  // status bits and control words are never below -1)
+  constexpr int64_t kUnwritten = INT64_MIN + 1;
+  const int64_t words = static_cast<int64_t>(nlayers) * COWSDM_REPORT_WORDS;
+  for (int64_t k = 0; k < words; ++k) __atomic_store_n(&host[k], kUnwritten, __ATOMIC_RELAXED);
   hipStream_t s = as_stream(stream);
   // launches after the first read the counters the one before left
   cowsdm_trace_t later = *trace;
@@ -1487,12 +1491,29 @@ int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
                     : cowsdm_dense_step_trace(layers, nlayers, shape, t, n, stream);
     if (rc != 0) return rc;
   }
+  if (steps > 0 && steps <= launch_steps) {
+    // One launch: its layers' last waves write every report word into host
+    // memory before the kernel's remaining waves exit, so return as soon as
+    // all words are in (each is one 8-byte store: a word that is not
+    // kUnwritten is this launch's).  The caller's work after the return
+    // overlaps the kernel's exit; later work on the stream still waits for
+    // it.  A launch that writes no report (one-step kernels) or fails is
+    // found done by the stream query and takes the path below.
+    for (uint32_t spin = 0;; ++spin) {
+      bool all = true;
+      for (int64_t k = 0; k < words && all; ++k) {
+        all = __atomic_load_n(&host[k], __ATOMIC_ACQUIRE) != kUnwritten;
+      }
+      if (all) return 0;
+      if ((spin & 255u) == 255u && hipStreamQuery(s) != hipErrorNotReady) break;
+    }
+  }
   hipError_t e = hipStreamSynchronize(s);
   if (e != hipSuccess) {
     return fail(static_cast<int32_t>(e), "trace run: %s", hipGetErrorString(e));
   }
   bool written = true;
-  for (int32_t l = 0; l < nlayers; ++l) written = written && host[l * COWSDM_REPORT_WORDS] >= 0;
+  for (int64_t k = 0; k < words; ++k) written = written && host[k] != kUnwritten;
   if (written) return 0;
   // launches of one step each (no persistent kernel fits) write no report:
   // read the words from the device

@@ -327,11 +327,13 @@ int32_t cowsdm_packed_step_trace_static(const cowsdm_layer_t* layers, int32_t nl
 /* The decode loop's launches for `steps` steps of every layer from their
  * device counters, `launch_steps` steps per launch (mode 0:
  * cowsdm_packed_step_trace, 1: cowsdm_packed_step_trace_static, 2:
- * cowsdm_dense_step_trace), then a wait for the stream.  trace->step_index
- * and trace->report must be set: on return each layer's report holds its
- * step counter, status and control words after its last launch.  No
- * counterpart in the reference; its decode loop (inference.py:538-566)
- * calls one step at a time. */
+ * cowsdm_dense_step_trace), then a wait: for a single launch until every
+ * layer's report is in host memory (the kernel's waves may still be
+ * exiting; later work on the stream waits for them), else for the stream.
+ * trace->step_index and trace->report must be set: on return each layer's
+ * report holds its step counter, status and control words after its last
+ * launch.  No counterpart in the reference; its decode loop
+ * (inference.py:538-566) calls one step at a time. */
 int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
                          const cowsdm_shape_t* shape, const cowsdm_trace_t* trace,
                          int64_t steps, int32_t launch_steps, int32_t mode, void* stream);
