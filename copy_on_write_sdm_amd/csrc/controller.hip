@@ -8,11 +8,13 @@
 // row, routes.h): cowsdm_controller_prepare_routes.
 //
 // A workgroup takes kCtlTokens tokens.  Each token's normalised input stays
-// in LDS, and thread j computes output row j of every projection for all of
-// the workgroup's tokens: the weights are stored transposed ([width, rows]),
-// so the lanes of a wave read consecutive floats of one input column, and
-// each weight is loaded once per workgroup and used for every token.
-// Products are accumulated with fused multiply-adds in input order.
+// in LDS, and a wave computes 32 output rows of a projection at a time for
+// all of the workgroup's tokens, lanes l and l + 32 the lower and the upper
+// half of the inputs of row l: the weights are stored transposed ([width,
+// rows]), so a half-wave reads consecutive floats of one input column, and
+// each weight is loaded once per workgroup and used for every token.  Each
+// half accumulates its products with fused multiply-adds in input order,
+// and the row is the lower half's sum plus the upper half's.
 
 #include "common.h"
 #include "routes.h"
@@ -83,16 +85,27 @@ __device__ void wave_layer_norm(const float* src, float* dst, int n, const float
 __device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// acc[t] = sum_k x[t][k] * wt[k * rows + j] over the workgroup's tokens
+// acc[t] = sum_k x[t][k] * wt[k * rows + j] over the workgroup's tokens,
+// row j taken by lanes l and l + 32 of a wave (the inputs below width / 2,
+// then the rest); both lanes end with lower + upper.  Every lane of the wave
+// calls it (the halves meet through a cross-lane exchange).
 __device__ __forceinline__ void project(const float* x, int width, const float* wt, int rows,
                                         int j, float (&acc)[kCtlTokens]) {
+  const bool lower = (threadIdx.x & (kWave - 1)) < kWave / 2;
+  const int k0 = lower ? 0 : width / 2;
+  const int k1 = lower ? width / 2 : width;
 #pragma unroll
   for (int t = 0; t < kCtlTokens; ++t) acc[t] = 0.0f;
 #pragma unroll 8
-  for (int k = 0; k < width; ++k) {
+  for (int k = k0; k < k1; ++k) {
     const float w = wt[static_cast<int64_t>(k) * rows + j];
 #pragma unroll
     for (int t = 0; t < kCtlTokens; ++t) acc[t] = __builtin_fmaf(x[t * width + k], w, acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < kCtlTokens; ++t) {
+    const float other = __shfl_xor(acc[t], kWave / 2, kWave);
+    acc[t] = lower ? acc[t] + other : other + acc[t];
   }
 }
 
@@ -118,10 +131,14 @@ __device__ __forceinline__ void controller_prepare_body(const CtlParams& P, floa
   }
   __syncthreads();
   for (int i = tid; i < T * W; i += NT) P.out_normalized[b0 * W + i] = xn[i];
-  // rows: read keys (H x KW), write keys (H x KW), values (W), forget (H), input (H)
-  for (int j = tid; j < P.rows; j += NT) {
+  // rows: read keys (H x KW), write keys (H x KW), values (W), forget (H), input (H),
+  // 32 a wave at a time (lane l and l + 32: row j0 + l)
+  for (int j0 = wave * (kWave / 2); j0 < P.rows; j0 += (NT / kWave) * (kWave / 2)) {
+    const int j = j0 + (tid & (kWave / 2 - 1));
+    const bool on = j < P.rows;
     float acc[kCtlTokens];
-    project(xn, W, P.c.proj_weight_t, P.rows, j, acc);
+    project(xn, W, P.c.proj_weight_t, P.rows, on ? j : P.rows - 1, acc);
+    if (!on || (tid & (kWave - 1)) >= kWave / 2) continue;
     const float bias = P.c.proj_bias[j];
     for (int t = 0; t < T; ++t) {
       const int64_t b = b0 + t;
@@ -203,17 +220,25 @@ __global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParam
                     P.c.read_norm_eps);
   }
   __syncthreads();
-  for (int j = tid; j < W; j += kCtlThreads) {
+  const int half_lane = tid & (kWave / 2 - 1);
+  const bool writer = (tid & (kWave - 1)) < kWave / 2;
+  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kCtlWaves * (kWave / 2)) {
+    const int j = j0 + half_lane;
+    const bool on = j < W;
     float acc[kCtlTokens];
-    project(nrm, W, P.c.gate_weight_t, W, j, acc);
+    project(nrm, W, P.c.gate_weight_t, W, on ? j : W - 1, acc);
+    if (!on || !writer) continue;
     const float bias = P.c.gate_bias[j];
 #pragma unroll
     for (int t = 0; t < kCtlTokens; ++t) rd[t * W + j] = sigmoid(acc[t] + bias) * rn[t * W + j];
   }
   __syncthreads();
-  for (int j = tid; j < W; j += kCtlThreads) {
+  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kCtlWaves * (kWave / 2)) {
+    const int j = j0 + half_lane;
+    const bool on = j < W;
     float acc[kCtlTokens];
-    project(rd, W, P.c.out_weight_t, W, j, acc);
+    project(rd, W, P.c.out_weight_t, W, on ? j : W - 1, acc);
+    if (!on || !writer) continue;
     const float bias = P.c.out_bias[j];
     for (int t = 0; t < T; ++t) {
       const int64_t at = (b0 + t) * W + j;
