@@ -22,10 +22,11 @@
 namespace cowsdm_impl {
 
 constexpr int kCtlTokens = 4;        // tokens per workgroup
-constexpr int kCtlThreads = 256;
+constexpr int kCtlThreads = 256;     // finish
 constexpr int kCtlWaves = kCtlThreads / kWave;
-// prepare with its routes: a wave for each of a workgroup's 2 x kCtlTokens
-// route rows (one head)
+// prepare (alone and with its routes): 8 waves, so config 2's 194 rows are
+// one pass of 32 rows a wave, and a wave for each of a workgroup's
+// 2 x kCtlTokens route rows (one head)
 constexpr int kCtlRouteThreads = 2 * kCtlTokens * kWave;
 constexpr int kCtlRouteWaves = kCtlRouteThreads / kWave;
 constexpr int kCtlMaxWidth = 1024;         // LDS: 3 x 4 tokens x width floats
@@ -163,9 +164,9 @@ __device__ __forceinline__ void controller_prepare_body(const CtlParams& P, floa
   }
 }
 
-__global__ __launch_bounds__(kCtlThreads) void controller_prepare_kernel(CtlParams P) {
+__global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_kernel(CtlParams P) {
   extern __shared__ float lds[];
-  controller_prepare_body<kCtlThreads>(P, lds);
+  controller_prepare_body<kCtlRouteThreads>(P, lds);
 }
 
 // prepare, then the routes of the workgroup's tokens from the keys its
@@ -338,7 +339,7 @@ extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const
   const int64_t groups = (batch + kCtlTokens - 1) / kCtlTokens;
   const size_t lds = sizeof(float) * 2 * kCtlTokens * P.width;
   hipLaunchKernelGGL(controller_prepare_kernel, dim3(static_cast<unsigned>(groups)),
-                     dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
+                     dim3(kCtlRouteThreads), lds, static_cast<hipStream_t>(stream), P);
   return launch_status("controller prepare");
 }
 
