@@ -70,7 +70,7 @@ RUN_PACKED = 0
 RUN_PACKED_STATIC = 1
 RUN_DENSE = 2
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 STATIC_SCAN_WORDS = 1 << 21   # COWSDM_STATIC_SCAN_WORDS
 
 SCRATCH_EPOCH = 0
@@ -292,6 +292,9 @@ SIGNATURES: dict[str, tuple] = {
                _P, _P, _P]),
     "cowsdm_controller_finish_residual": (
         _I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P, _P, _P]),
+    "cowsdm_controller_finish_prepare_routes": (
+        _I32, [ctypes.POINTER(Controller), _P, _P, _I64, _P, _P, _P, ctypes.POINTER(Controller),
+               _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "cowsdm_recurrence_forward": (_I32, [ctypes.POINTER(Recurrence), _P]),
     "cowsdm_dense_routes": (_I32, [_P, _P, _I32, _I64, _I64, _I64, _P, _P, _P]),
     "cowsdm_host_report_alloc": (

@@ -400,26 +400,47 @@ class ControllerDecodeGraph:
         for _, _, trace in self.layers:
             trace.reserve_steps(tokens)
 
+    @staticmethod
+    def _prepare_args(c, buf) -> tuple:
+        return (buf["normalized"].data_ptr(), buf["read_keys"].data_ptr(),
+                buf["write_keys"].data_ptr(), buf["values"].data_ptr(),
+                buf["input_gate"].data_ptr(), buf["forget"].data_ptr(), c.reads, c.writes,
+                buf["read_weights"].data_ptr(), buf["read_indices"].data_ptr(),
+                buf["write_weights"].data_ptr(), buf["write_indices"].data_ptr())
+
     def _record(self, stream: int, structs) -> torch.Tensor:
+        """Per layer: prepare with the routes, the step, finish with the
+        residual add.  Without a tail between layers a layer's finish and the
+        next layer's prepare are one call (one launch at sqrt(N) <= 64)."""
+
         lib = nat.lib()
-        x = self.tokens
+        x = self.tokens.contiguous()
+        c0, buf0, _ = self.layers[0]
+        nat.check(lib.cowsdm_controller_prepare_routes(
+            c0.c_struct(), x.data_ptr(), self.batch, *self._prepare_args(c0, buf0), stream),
+            "cowsdm_controller_prepare_routes")
+        last = len(self.layers) - 1
         for index, ((c, buf, trace), layer) in enumerate(zip(self.layers, structs)):
-            x = x.contiguous()
-            nat.check(lib.cowsdm_controller_prepare_routes(
-                c.c_struct(), x.data_ptr(), self.batch, buf["normalized"].data_ptr(),
-                buf["read_keys"].data_ptr(), buf["write_keys"].data_ptr(),
-                buf["values"].data_ptr(), buf["input_gate"].data_ptr(), buf["forget"].data_ptr(),
-                c.reads, c.writes, buf["read_weights"].data_ptr(),
-                buf["read_indices"].data_ptr(), buf["write_weights"].data_ptr(),
-                buf["write_indices"].data_ptr(), stream), "cowsdm_controller_prepare_routes")
             trace.launch(1, layer)
-            nat.check(lib.cowsdm_controller_finish_residual(
-                c.c_struct(), buf["normalized"].data_ptr(), buf["reading"].data_ptr(), self.batch,
-                buf["out"].data_ptr(), x.data_ptr(), buf["sum"].data_ptr(), stream),
-                "cowsdm_controller_finish_residual")
+            finish = (c.c_struct(), buf["normalized"].data_ptr(), buf["reading"].data_ptr(),
+                      self.batch, buf["out"].data_ptr(), x.data_ptr(), buf["sum"].data_ptr())
+            if index < last and self.tail is None:
+                cn, bufn, _ = self.layers[index + 1]
+                nat.check(lib.cowsdm_controller_finish_prepare_routes(
+                    *finish, cn.c_struct(), *self._prepare_args(cn, bufn), stream),
+                    "cowsdm_controller_finish_prepare_routes")
+                x = buf["sum"]
+                continue
+            nat.check(lib.cowsdm_controller_finish_residual(*finish, stream),
+                      "cowsdm_controller_finish_residual")
             x = buf["sum"]
             if self.tail is not None:
-                x = self.tail(index, x)
+                x = self.tail(index, x).contiguous()
+            if index < last:
+                cn, bufn, _ = self.layers[index + 1]
+                nat.check(lib.cowsdm_controller_prepare_routes(
+                    cn.c_struct(), x.data_ptr(), self.batch, *self._prepare_args(cn, bufn),
+                    stream), "cowsdm_controller_prepare_routes")
         return x
 
     def capture(self) -> "torch.cuda.CUDAGraph":

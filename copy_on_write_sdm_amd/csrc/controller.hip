@@ -110,7 +110,10 @@ __device__ __forceinline__ void project(const float* x, int width, const float* 
   }
 }
 
-template <int NT>
+// prepare of the workgroup's tokens; with FROM_LDS their inputs are already
+// in lds[0 .. kCtlTokens * W) (zeros past the batch), the previous layer's
+// finish having put them there
+template <int NT, bool FROM_LDS>
 __device__ __forceinline__ void controller_prepare_body(const CtlParams& P, float* lds) {
   const int W = P.width, H = P.heads, HW = P.head_width, KW = P.key_width;
   float* const x = lds;                        // [kCtlTokens][W]
@@ -118,8 +121,10 @@ __device__ __forceinline__ void controller_prepare_body(const CtlParams& P, floa
   const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
   const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
   const int tid = static_cast<int>(threadIdx.x);
-  for (int i = tid; i < kCtlTokens * W; i += NT) {
-    x[i] = i < T * W ? P.tokens[b0 * W + i] : 0.0f;
+  if constexpr (!FROM_LDS) {
+    for (int i = tid; i < kCtlTokens * W; i += NT) {
+      x[i] = i < T * W ? P.tokens[b0 * W + i] : 0.0f;
+    }
   }
   __syncthreads();
   const int wave = tid / kWave;
@@ -166,21 +171,22 @@ __device__ __forceinline__ void controller_prepare_body(const CtlParams& P, floa
 
 __global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_kernel(CtlParams P) {
   extern __shared__ float lds[];
-  controller_prepare_body<kCtlRouteThreads>(P, lds);
+  controller_prepare_body<kCtlRouteThreads, false>(P, lds);
 }
 
-// prepare, then the routes of the workgroup's tokens from the keys its
-// threads stored (visible to the whole workgroup after the barrier)
+// The read and write routes of the workgroup's tokens from the keys its
+// threads stored (visible to the whole workgroup after a barrier), one wave
+// per route row.
+struct RouteStage {
+  float val[kCtlRouteWaves][kRouteMaxSelected];
+  int pos[kCtlRouteWaves][kRouteMaxSelected];
+  float pool_val[kCtlRouteWaves][kWave];
+  int pool_pos[kCtlRouteWaves][kWave];
+};
+
 template <int MR, int MW>
-__global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_routes_kernel(
-    CtlParams P, CtlRoutes R) {
-  extern __shared__ float lds[];
-  __shared__ float stage_val[kCtlRouteWaves][kRouteMaxSelected];
-  __shared__ int stage_pos[kCtlRouteWaves][kRouteMaxSelected];
-  __shared__ float pool_val[kCtlRouteWaves][kWave];
-  __shared__ int pool_pos[kCtlRouteWaves][kWave];
-  controller_prepare_body<kCtlRouteThreads>(P, lds);
-  __syncthreads();
+__device__ __forceinline__ void controller_routes_part(const CtlParams& P, const CtlRoutes& R,
+                                                       RouteStage& st) {
   const int64_t b0 = static_cast<int64_t>(blockIdx.x) * kCtlTokens;
   const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
   const int rows = T * P.heads;
@@ -188,19 +194,34 @@ __global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_routes_ke
   for (int task = wave; task < 2 * rows; task += kCtlRouteWaves) {
     if (task < rows) {
       product_key_route_row<1, MR>(P.read_keys, b0 * P.heads + task, R.root, R.read_sub,
-                                   R.read_k, R.read_weights, R.read_indices, stage_val[wave],
-                                   stage_pos[wave], pool_val[wave], pool_pos[wave]);
+                                   R.read_k, R.read_weights, R.read_indices, st.val[wave],
+                                   st.pos[wave], st.pool_val[wave], st.pool_pos[wave]);
     } else {
       product_key_route_row<1, MW>(P.write_keys, b0 * P.heads + task - rows, R.root,
                                    R.write_sub, R.write_k, R.write_weights, R.write_indices,
-                                   stage_val[wave], stage_pos[wave], pool_val[wave],
-                                   pool_pos[wave]);
+                                   st.val[wave], st.pos[wave], st.pool_val[wave],
+                                   st.pool_pos[wave]);
     }
   }
 }
 
-__global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParams P) {
+// prepare, then the routes of the workgroup's tokens
+template <int MR, int MW>
+__global__ __launch_bounds__(kCtlRouteThreads) void controller_prepare_routes_kernel(
+    CtlParams P, CtlRoutes R) {
   extern __shared__ float lds[];
+  __shared__ RouteStage stage;
+  controller_prepare_body<kCtlRouteThreads, false>(P, lds);
+  __syncthreads();
+  controller_routes_part<MR, MW>(P, R, stage);
+}
+
+// finish of the workgroup's tokens; with TO_LDS the residual sums (the next
+// layer's inputs) also go to lds[0 .. kCtlTokens * W), zeros past the batch
+// (that region holds the normalised inputs, dead once the gate is applied)
+template <int NT, bool TO_LDS>
+__device__ __forceinline__ void controller_finish_body(const CtlParams& P, float* lds) {
+  constexpr int kWaves = NT / kWave;
   const int W = P.width, HW = P.head_width;
   float* const nrm = lds;                       // normalized inputs
   float* const rd = lds + kCtlTokens * W;       // readings, then gate * normalised readings
@@ -209,21 +230,21 @@ __global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParam
   const int T = static_cast<int>(P.batch - b0 < kCtlTokens ? P.batch - b0 : kCtlTokens);
   const int tid = static_cast<int>(threadIdx.x);
   // a token's readings [heads, head_width] are its `width` contiguous floats
-  for (int i = tid; i < kCtlTokens * W; i += kCtlThreads) {
+  for (int i = tid; i < kCtlTokens * W; i += NT) {
     nrm[i] = i < T * W ? P.normalized[b0 * W + i] : 0.0f;
     rd[i] = i < T * W ? P.reading[b0 * W + i] : 0.0f;
   }
   __syncthreads();
   const int wave = tid / kWave;
   const int segments = kCtlTokens * P.heads;
-  for (int g = wave; g < segments; g += kCtlWaves) {
+  for (int g = wave; g < segments; g += kWaves) {
     wave_layer_norm(rd + g * HW, rn + g * HW, HW, P.c.read_norm_weight, P.c.read_norm_bias,
                     P.c.read_norm_eps);
   }
   __syncthreads();
   const int half_lane = tid & (kWave / 2 - 1);
   const bool writer = (tid & (kWave - 1)) < kWave / 2;
-  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kCtlWaves * (kWave / 2)) {
+  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kWaves * (kWave / 2)) {
     const int j = j0 + half_lane;
     const bool on = j < W;
     float acc[kCtlTokens];
@@ -234,7 +255,7 @@ __global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParam
     for (int t = 0; t < kCtlTokens; ++t) rd[t * W + j] = sigmoid(acc[t] + bias) * rn[t * W + j];
   }
   __syncthreads();
-  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kCtlWaves * (kWave / 2)) {
+  for (int j0 = wave * (kWave / 2); j0 < W; j0 += kWaves * (kWave / 2)) {
     const int j = j0 + half_lane;
     const bool on = j < W;
     float acc[kCtlTokens];
@@ -245,9 +266,35 @@ __global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParam
       const int64_t at = (b0 + t) * W + j;
       const float y = acc[t] + bias;
       P.out[at] = y;
-      if (P.residual) P.out_sum[at] = P.residual[at] + y;
+      if (P.residual) {
+        const float next = P.residual[at] + y;
+        P.out_sum[at] = next;
+        if constexpr (TO_LDS) nrm[t * W + j] = next;
+      }
+    }
+    if constexpr (TO_LDS) {
+      for (int t = T; t < kCtlTokens; ++t) nrm[t * W + j] = 0.0f;
     }
   }
+}
+
+__global__ __launch_bounds__(kCtlThreads) void controller_finish_kernel(CtlParams P) {
+  extern __shared__ float lds[];
+  controller_finish_body<kCtlThreads, false>(P, lds);
+}
+
+// one layer's finish with the residual add, then the next layer's prepare
+// and routes on the same tokens, whose inputs the finish left in LDS
+template <int MR, int MW>
+__global__ __launch_bounds__(kCtlRouteThreads) void controller_finish_prepare_routes_kernel(
+    CtlParams F, CtlParams P, CtlRoutes R) {
+  extern __shared__ float lds[];
+  __shared__ RouteStage stage;
+  controller_finish_body<kCtlRouteThreads, true>(F, lds);
+  __syncthreads();
+  controller_prepare_body<kCtlRouteThreads, true>(P, lds);
+  __syncthreads();
+  controller_routes_part<MR, MW>(P, R, stage);
 }
 
 namespace {
@@ -324,6 +371,55 @@ void launch_prepare_routes(const CtlParams& P, const CtlRoutes& R, hipStream_t s
                      dim3(static_cast<unsigned>(groups)), dim3(kCtlRouteThreads), lds, s, P, R);
 }
 
+template <int MR, int MW>
+void launch_finish_prepare_routes(const CtlParams& F, const CtlParams& P, const CtlRoutes& R,
+                                  hipStream_t s) {
+  const int64_t groups = (P.batch + kCtlTokens - 1) / kCtlTokens;
+  const size_t lds = sizeof(float) * 3 * kCtlTokens * P.width;
+  hipLaunchKernelGGL((controller_finish_prepare_routes_kernel<MR, MW>),
+                     dim3(static_cast<unsigned>(groups)), dim3(kCtlRouteThreads), lds, s, F, P,
+                     R);
+}
+
+// The route geometry of `reads` and `writes` selections over c's slots and
+// the four output pointers (checked once batch > 0).
+int32_t route_params(const cowsdm_controller_t* c, int64_t batch, int64_t reads, int64_t writes,
+                     float* read_weights, int64_t* read_indices, float* write_weights,
+                     int64_t* write_indices, CtlRoutes& R) {
+  if (int32_t e = route_geometry(c->slots, reads, R.root, R.read_sub, R.read_k)) return e;
+  if (int32_t e = route_geometry(c->slots, writes, R.root, R.write_sub, R.write_k)) return e;
+  if (batch == 0) return 0;
+  if (!read_weights || !read_indices || !write_weights || !write_indices) {
+    return fail(COWSDM_EARG, "controller prepare: null route pointer");
+  }
+  R.read_weights = read_weights;
+  R.read_indices = read_indices;
+  R.write_weights = write_weights;
+  R.write_indices = write_indices;
+  return 0;
+}
+
+int32_t finish_params(const cowsdm_controller_t* c, const float* normalized,
+                      const float* reading, int64_t batch, float* out, const float* residual,
+                      float* out_sum, CtlParams& P) {
+  if (residual && !out_sum) return fail(COWSDM_EARG, "controller finish: null residual sum");
+  P.residual = residual;
+  P.out_sum = out_sum;
+  if (int32_t e = check_controller(c, batch, P)) return e;
+  if (batch == 0) return 0;
+  if (!normalized || !reading || !out || !c->gate_weight_t || !c->gate_bias ||
+      !c->out_weight_t || !c->out_bias || !c->read_norm_weight || !c->read_norm_bias) {
+    return fail(COWSDM_EARG, "controller finish: null pointer argument");
+  }
+  P.normalized = normalized;
+  P.reading = reading;
+  P.out = out;
+  if ((batch + kCtlTokens - 1) / kCtlTokens > (int64_t{1} << 31) - 1) {
+    return fail(COWSDM_ELIMIT, "controller: batch too large");
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" int32_t cowsdm_controller_prepare(const cowsdm_controller_t* c, const float* tokens,
@@ -358,16 +454,11 @@ extern "C" int32_t cowsdm_controller_prepare_routes(
     return e;
   }
   CtlRoutes R{};
-  if (int32_t e = route_geometry(c->slots, reads, R.root, R.read_sub, R.read_k)) return e;
-  if (int32_t e = route_geometry(c->slots, writes, R.root, R.write_sub, R.write_k)) return e;
-  if (batch == 0) return 0;
-  if (!read_weights || !read_indices || !write_weights || !write_indices) {
-    return fail(COWSDM_EARG, "controller prepare: null route pointer");
+  if (int32_t e = route_params(c, batch, reads, writes, read_weights, read_indices,
+                               write_weights, write_indices, R)) {
+    return e;
   }
-  R.read_weights = read_weights;
-  R.read_indices = read_indices;
-  R.write_weights = write_weights;
-  R.write_indices = write_indices;
+  if (batch == 0) return 0;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (R.root > kWave) {
     // a shortlist of more than one entry per lane: the separate launches
@@ -398,20 +489,11 @@ extern "C" int32_t cowsdm_controller_finish_residual(const cowsdm_controller_t* 
                                                      float* out, const float* residual,
                                                      float* out_sum, void* stream) {
   CtlParams P{};
-  if (residual && !out_sum) return fail(COWSDM_EARG, "controller finish: null residual sum");
-  P.residual = residual;
-  P.out_sum = out_sum;
-  if (int32_t e = check_controller(c, batch, P)) return e;
-  if (batch == 0) return 0;
-  if (!normalized || !reading || !out || !c->gate_weight_t || !c->gate_bias ||
-      !c->out_weight_t || !c->out_bias || !c->read_norm_weight || !c->read_norm_bias) {
-    return fail(COWSDM_EARG, "controller finish: null pointer argument");
+  if (int32_t e = finish_params(c, normalized, reading, batch, out, residual, out_sum, P)) {
+    return e;
   }
-  P.normalized = normalized;
-  P.reading = reading;
-  P.out = out;
+  if (batch == 0) return 0;
   const int64_t groups = (batch + kCtlTokens - 1) / kCtlTokens;
-  if (groups > (int64_t{1} << 31) - 1) return fail(COWSDM_ELIMIT, "controller: batch too large");
   const size_t lds = sizeof(float) * 3 * kCtlTokens * P.width;
   hipLaunchKernelGGL(controller_finish_kernel, dim3(static_cast<unsigned>(groups)),
                      dim3(kCtlThreads), lds, static_cast<hipStream_t>(stream), P);
@@ -423,4 +505,52 @@ extern "C" int32_t cowsdm_controller_finish(const cowsdm_controller_t* c,
                                             int64_t batch, float* out, void* stream) {
   return cowsdm_controller_finish_residual(c, normalized, reading, batch, out, nullptr, nullptr,
                                            stream);
+}
+
+extern "C" int32_t cowsdm_controller_finish_prepare_routes(
+    const cowsdm_controller_t* c, const float* normalized, const float* reading, int64_t batch,
+    float* out, const float* residual, float* out_sum, const cowsdm_controller_t* next,
+    float* next_normalized, float* read_keys, float* write_keys, float* values,
+    float* input_gate, float* forget_log_gate, int64_t reads, int64_t writes,
+    float* read_weights, int64_t* read_indices, float* write_weights, int64_t* write_indices,
+    void* stream) {
+  if (!residual || !out_sum) {
+    return fail(COWSDM_EARG, "controller finish and prepare: null residual or sum");
+  }
+  CtlParams F{};
+  if (int32_t e = finish_params(c, normalized, reading, batch, out, residual, out_sum, F)) {
+    return e;
+  }
+  CtlParams P{};
+  if (int32_t e = prepare_params(next, out_sum, batch, next_normalized, read_keys, write_keys,
+                                 values, input_gate, forget_log_gate, P)) {
+    return e;
+  }
+  if (next->width != c->width) {
+    return fail(COWSDM_EARG, "controller finish and prepare: the layers' widths differ");
+  }
+  CtlRoutes R{};
+  if (int32_t e = route_params(next, batch, reads, writes, read_weights, read_indices,
+                               write_weights, write_indices, R)) {
+    return e;
+  }
+  if (batch == 0) return 0;
+  if (R.root > kWave) {
+    // the next layer's routes take their own launches: finish, then prepare
+    if (int32_t e = cowsdm_controller_finish_residual(c, normalized, reading, batch, out,
+                                                      residual, out_sum, stream)) {
+      return e;
+    }
+    return cowsdm_controller_prepare_routes(next, out_sum, batch, next_normalized, read_keys,
+                                            write_keys, values, input_gate, forget_log_gate,
+                                            reads, writes, read_weights, read_indices,
+                                            write_weights, write_indices, stream);
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mr = route_pair_m(R.read_sub, R.read_k), mw = route_pair_m(R.write_sub, R.write_k);
+  if (mr == 1 && mw == 1) launch_finish_prepare_routes<1, 1>(F, P, R, s);
+  else if (mr == 1) launch_finish_prepare_routes<1, 2>(F, P, R, s);
+  else if (mw == 1) launch_finish_prepare_routes<2, 1>(F, P, R, s);
+  else launch_finish_prepare_routes<2, 2>(F, P, R, s);
+  return launch_status("controller finish and prepare");
 }

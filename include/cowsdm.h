@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define COWSDM_ABI_VERSION 11
+#define COWSDM_ABI_VERSION 12
 
 /* Index dtype codes. */
 #define COWSDM_INDEX_INT32 0
@@ -669,6 +669,23 @@ int32_t cowsdm_controller_finish_residual(const cowsdm_controller_t* controller,
                                           const float* normalized, const float* reading,
                                           int64_t batch, float* out, const float* residual,
                                           float* out_sum, void* stream);
+
+/* One layer's cowsdm_controller_finish_residual (residual and out_sum
+ * required) followed by the next layer's cowsdm_controller_prepare_routes
+ * on out_sum: the layer stack's per-token walk (inference.py:655-661) for
+ * a caller with nothing between the layers (the reference's stack puts an
+ * MLP there, inference.py:661, and takes the two calls), in one launch
+ * when the next layer's
+ * sqrt(slots) <= 64 (its tokens' inputs stay on chip between the two), else
+ * in the two launches.  The layers share their width.  Every output equals
+ * the two calls' bit for bit.  No single counterpart in the reference. */
+int32_t cowsdm_controller_finish_prepare_routes(
+    const cowsdm_controller_t* controller, const float* normalized, const float* reading,
+    int64_t batch, float* out, const float* residual, float* out_sum,
+    const cowsdm_controller_t* next, float* next_normalized, float* read_keys,
+    float* write_keys, float* values, float* input_gate, float* forget_log_gate,
+    int64_t reads, int64_t writes, float* read_weights, int64_t* read_indices,
+    float* write_weights, int64_t* write_indices, void* stream);
 
 /* ------------------------------------------ dense recurrence (prefill) */
 

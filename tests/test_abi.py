@@ -38,7 +38,7 @@ def test_bindings_cover_header():
 
 def test_info_entry_points():
     lib = nat.lib()
-    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 11
+    assert lib.cowsdm_abi_version() == nat.ABI_VERSION == 12
     # epoch and header, plan words [banks][steps], step and running totals,
     # at most banks * W pops per step and 4 words per growth segment, int64 each
     assert lib.cowsdm_trace_scan_words(64, 4, 512) == (16 + 64 * 512 + 512 + 513 + 64 * 512 * 4

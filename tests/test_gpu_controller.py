@@ -214,3 +214,63 @@ def test_fused_prepare_routes_and_residual_finish_equal_separate_launches(
     assert lib.cowsdm_controller_finish_residual(
         controller.c_struct(), want["normalized"].data_ptr(), reading.data_ptr(), batch,
         out.data_ptr(), x.data_ptr(), None, stream) != 0
+
+
+@pytest.mark.parametrize("width,slots,heads,reads,writes,batch", SHAPES)
+def test_finish_then_next_prepare_in_one_call_equals_two(device, width, slots, heads, reads,
+                                                        writes, batch):
+    """cowsdm_controller_finish_prepare_routes (one launch for sqrt(N) <= 64,
+    two above) writes exactly what finish_residual then prepare_routes of
+    the next layer on its sum write."""
+    from copy_on_write_sdm_amd import _native as nat
+    print(f"finish+prepare width={width} N={slots} H={heads} B={batch}", flush=True)
+    layer, c1, x = _setup(device, width, slots, heads, reads, writes, batch, seed=7 * width)
+    _, c2, _ = _setup(device, width, slots, heads, reads, writes, batch, seed=7 * width + 1)
+    x = x.to(device)
+    root = int(np.sqrt(slots))
+    kr, kw = min(reads, min(reads, root) ** 2), min(writes, min(writes, root) ** 2)
+    rows, hw = batch * heads, width // heads
+    lib, stream = nat.lib(), nat.stream_handle(device)
+    step = ctl.prepare_sdm_step(c1, x)
+    normalized = step.normalized.contiguous()
+    reading = tokens(rows, hw, seed=93, dtype=torch.float32)[:, 0].to(device)
+
+    def outputs():
+        f = dict(device=device, dtype=torch.float32)
+        i64 = dict(device=device, dtype=torch.int64)
+        return {"out": torch.full((batch, width), 7.0, **f),
+                "sum": torch.full((batch, width), 7.0, **f),
+                "normalized": torch.full((batch, width), 7.0, **f),
+                "read_keys": torch.full((rows, 2 * root), 7.0, **f),
+                "write_keys": torch.full((rows, 2 * root), 7.0, **f),
+                "values": torch.full((rows, hw), 7.0, **f),
+                "input_gate": torch.full((rows,), 7.0, **f),
+                "forget": torch.full((rows,), 7.0, **f),
+                "read_weights": torch.full((rows, kr), 7.0, **f),
+                "read_indices": torch.full((rows, kr), -7, **i64),
+                "write_weights": torch.full((rows, kw), 7.0, **f),
+                "write_indices": torch.full((rows, kw), -7, **i64)}
+
+    def prepare_args(o):
+        return (o["normalized"].data_ptr(), o["read_keys"].data_ptr(),
+                o["write_keys"].data_ptr(), o["values"].data_ptr(), o["input_gate"].data_ptr(),
+                o["forget"].data_ptr(), reads, writes, o["read_weights"].data_ptr(),
+                o["read_indices"].data_ptr(), o["write_weights"].data_ptr(),
+                o["write_indices"].data_ptr())
+
+    finish = (c1.c_struct(), normalized.data_ptr(), reading.data_ptr(), batch)
+    want = outputs()
+    nat.check(lib.cowsdm_controller_finish_residual(
+        *finish, want["out"].data_ptr(), x.data_ptr(), want["sum"].data_ptr(), stream), "finish")
+    nat.check(lib.cowsdm_controller_prepare_routes(
+        c2.c_struct(), want["sum"].data_ptr(), batch, *prepare_args(want), stream), "prepare")
+    got = outputs()
+    nat.check(lib.cowsdm_controller_finish_prepare_routes(
+        *finish, got["out"].data_ptr(), x.data_ptr(), got["sum"].data_ptr(), c2.c_struct(),
+        *prepare_args(got), stream), "finish_prepare_routes")
+    for name in want:
+        assert torch.equal(got[name], want[name]), name
+    # the residual is required
+    assert lib.cowsdm_controller_finish_prepare_routes(
+        *finish, got["out"].data_ptr(), None, got["sum"].data_ptr(), c2.c_struct(),
+        *prepare_args(got), stream) != 0

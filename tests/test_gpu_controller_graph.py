@@ -54,18 +54,22 @@ def _setup(device, *, layers, batch, heads, width, slots, reads, writes, quantum
     return ctrls, states, tokens
 
 
-@pytest.mark.parametrize("heads,batch,layers", [(1, 64, 3), (2, 6, 2)])
-def test_captured_controller_decode(device, heads, batch, layers):
+@pytest.mark.parametrize("heads,batch,layers,with_tail", [
+    (1, 64, 3, True), (2, 6, 2, True),
+    # no tail: a layer's finish and the next layer's prepare are one launch
+    (1, 64, 3, False), (2, 6, 3, False)])
+def test_captured_controller_decode(device, heads, batch, layers, with_tail):
     width, slots, reads, writes = 128, 256, 16, 4
     quantum = batch * heads * writes * 2
     n = 12
-    print(f"controller graph H={heads} B={batch} L={layers}", flush=True)
+    print(f"controller graph H={heads} B={batch} L={layers} tail={with_tail}", flush=True)
+    tail = _tail if with_tail else (lambda layer, x: x)
     ctrls, make_states, tokens = _setup(device, layers=layers, batch=batch, heads=heads,
                                         width=width, slots=slots, reads=reads, writes=writes,
                                         quantum=quantum, seed=71 + heads)
     graphed, eager = make_states(), make_states()
     oracles = [oracle_of(st) for st in eager]
-    dec = cow.ControllerDecodeGraph(ctrls, graphed, batch, tail=_tail)
+    dec = cow.ControllerDecodeGraph(ctrls, graphed, batch, tail=_tail if with_tail else None)
     dec.reserve_tokens(n)
     dec.capture()
     got = []
@@ -81,7 +85,7 @@ def test_captured_controller_decode(device, heads, batch, layers):
         x = tokens[t]
         x_ref = tokens[t]
         for l, (c, st, orc) in enumerate(zip(ctrls, eager, oracles)):
-            x = _tail(l, x + cow.decode_sdm_layer_controller(c, x, st))
+            x = tail(l, x + cow.decode_sdm_layer_controller(c, x, st))
             # the oracle composition: the same controller kernels, the
             # reference's proof and step on the oracle state
             step = cow.prepare_sdm_step(c, x_ref)
@@ -91,7 +95,7 @@ def test_captured_controller_decode(device, heads, batch, layers):
                                 "forget_log_gate", "read_indices", "read_weights")}
             reading, _ = ref.packed_step(orc, **inputs, validate_routes=False)
             out = cow.finish_sdm_step(c, step, torch.from_numpy(reading).to(device))
-            x_ref = _tail(l, x_ref + out)
+            x_ref = tail(l, x_ref + out)
         assert torch.equal(got[t], x), t
         assert torch.equal(got[t], x_ref), t
     for a, b, orc in zip(graphed, eager, oracles):
