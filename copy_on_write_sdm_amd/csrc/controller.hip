@@ -5,7 +5,9 @@
 // the output projection.  Routes are selected from the keys by
 // cowsdm_product_key_routes (routes.hip), or, for sqrt(N) <= 64, by the
 // prepare kernel itself once its tokens' keys are out (one wave per route
-// row, routes.h): cowsdm_controller_prepare_routes.
+// row, routes.h): cowsdm_controller_prepare_routes; with nothing between two
+// layers, one layer's finish and the next one's prepare and routes share a
+// launch (cowsdm_controller_finish_prepare_routes).
 //
 // A workgroup takes kCtlTokens tokens.  Each token's normalised input stays
 // in LDS, and a wave computes 32 output rows of a projection at a time for
@@ -23,7 +25,6 @@ namespace cowsdm_impl {
 
 constexpr int kCtlTokens = 4;        // tokens per workgroup
 constexpr int kCtlThreads = 256;     // finish
-constexpr int kCtlWaves = kCtlThreads / kWave;
 // prepare (alone and with its routes): 8 waves, so config 2's 194 rows are
 // one pass of 32 rows a wave, and a wave for each of a workgroup's
 // 2 x kCtlTokens route rows (one head)
