@@ -1505,7 +1505,7 @@ int32_t cowsdm_trace_run(const cowsdm_layer_t* layers, int32_t nlayers,
         all = __atomic_load_n(&host[k], __ATOMIC_ACQUIRE) != kUnwritten;
       }
       if (all) return 0;
-      if ((spin & 255u) == 255u && hipStreamQuery(s) != hipErrorNotReady) break;
+      if ((spin & 63u) == 63u && hipStreamQuery(s) != hipErrorNotReady) break;
     }
   }
   hipError_t e = hipStreamSynchronize(s);
