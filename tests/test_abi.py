@@ -170,3 +170,37 @@ def test_header_cites_reference(name):
     block = text[:text.index(name + "(")]
     comment = block[block.rfind("/*"):]
     assert "allocator.py:" in comment
+
+
+def test_fused_controller_argument_errors_without_launching():
+    """The fused controller entry points check their arguments before any
+    launch: the residual is required where the next layer's input is its
+    sum, the layers must share their width, route counts take
+    product_key_routes' checks, and a zero batch launches nothing."""
+    lib = nat.lib()
+    c = nat.Controller()
+    c.width, c.heads, c.slots = 8, 1, 16
+    other = nat.Controller()
+    other.width, other.heads, other.slots = 16, 1, 16
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: every call fails first
+    args = [fake] * 6
+    # no residual
+    assert lib.cowsdm_controller_finish_prepare_routes(
+        ctypes.byref(c), fake, fake, 4, fake, None, fake, ctypes.byref(c), *args,
+        4, 2, fake, fake, fake, fake, None) == -1
+    assert b"residual" in lib.cowsdm_last_error_string()
+    # widths differ (weights null for the finish: the pointer check comes
+    # first, so give the batch 0 path the width check)
+    assert lib.cowsdm_controller_finish_prepare_routes(
+        ctypes.byref(c), fake, fake, 0, fake, fake, fake, ctypes.byref(other), *args,
+        4, 2, fake, fake, fake, fake, None) == -1
+    assert b"widths differ" in lib.cowsdm_last_error_string()
+    # route counts
+    assert lib.cowsdm_controller_prepare_routes(
+        ctypes.byref(c), fake, 0, *args, 0, 2, fake, fake, fake, fake, None) != 0
+    # a zero batch is a no-op
+    assert lib.cowsdm_controller_prepare_routes(
+        ctypes.byref(c), fake, 0, *args, 4, 2, fake, fake, fake, fake, None) == 0
+    assert lib.cowsdm_controller_finish_residual(
+        ctypes.byref(c), fake, fake, 0, fake, fake, None, None) == -1
+    assert b"residual sum" in lib.cowsdm_last_error_string()
