@@ -37,8 +37,10 @@ __device__ __forceinline__ uint64_t route_key(float v, int pos) {
   return (static_cast<uint64_t>(bits) << 32) | static_cast<uint32_t>(~pos);
 }
 
-// rank[j] = number of keys in the wave (J per lane, absent ones 0) above key[j]
-template <int J>
+// rank[j] = number of keys in the wave (J per lane, absent ones 0) above key[j];
+// lanes from LANES on hold absent keys only (every present key is above 0),
+// so only the first LANES are broadcast
+template <int J, int LANES = kWave>
 __device__ __forceinline__ void wave_rank(const uint64_t (&key)[J], int (&rank)[J]) {
 #pragma unroll
   for (int j = 0; j < J; ++j) rank[j] = 0;
@@ -55,9 +57,9 @@ __device__ __forceinline__ void wave_rank(const uint64_t (&key)[J], int (&rank)[
     };
     if constexpr (J <= 4) {
 #pragma unroll
-      for (int u = 0; u < kWave; ++u) count(u);   // lane selects as immediates
+      for (int u = 0; u < LANES; ++u) count(u);   // lane selects as immediates
     } else {
-      for (int u = 0; u < kWave; ++u) count(u);
+      for (int u = 0; u < LANES; ++u) count(u);
     }
   }
 }
@@ -71,7 +73,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Lane t < count ends with the t-th best (value, position) of the wave's
 // candidates (pos < 0: absent).  stage_val/stage_pos hold kRouteMaxSelected
 // entries of this wave.
-template <int J>
+template <int J, int LANES = kWave>
 __device__ __forceinline__ void wave_top(const float (&val)[J], const int (&pos)[J], int count,
                                          int lane, float* stage_val, int* stage_pos,
                                          float& top_val, int& top_pos) {
@@ -79,7 +81,7 @@ __device__ __forceinline__ void wave_top(const float (&val)[J], const int (&pos)
   int rank[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) key[j] = pos[j] >= 0 ? route_key(val[j], pos[j]) : 0;
-  wave_rank<J>(key, rank);
+  wave_rank<J, LANES>(key, rank);
 #pragma unroll
   for (int j = 0; j < J; ++j)
     if (pos[j] >= 0 && rank[j] < count) {
@@ -179,6 +181,13 @@ __device__ __forceinline__ void product_key_route_row(
                        pool_pos, first_val, first_idx);
     wave_top_pruned<J>(sv, sp, sub, lane, stage_val, stage_pos, pool_val,
                        pool_pos, second_val, second_idx);
+  } else if (root <= 16) {
+    // root <= 64: entries only in lanes below root
+    wave_top<J, 16>(fv, fp, sub, lane, stage_val, stage_pos, first_val, first_idx);
+    wave_top<J, 16>(sv, sp, sub, lane, stage_val, stage_pos, second_val, second_idx);
+  } else if (root <= 32) {
+    wave_top<J, 32>(fv, fp, sub, lane, stage_val, stage_pos, first_val, first_idx);
+    wave_top<J, 32>(sv, sp, sub, lane, stage_val, stage_pos, second_val, second_idx);
   } else {
     wave_top<J>(fv, fp, sub, lane, stage_val, stage_pos, first_val, first_idx);
     wave_top<J>(sv, sp, sub, lane, stage_val, stage_pos, second_val, second_idx);
